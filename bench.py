@@ -1,0 +1,208 @@
+"""
+Benchmark: nanoSpeaker MoE block on one MI355X (BASELINE.json's metric and configs).
+
+A step is one forward + backward of the MoE block over one batch of synthetic tokens
+(T = 8192, bf16, train mode, loss = (out * g).sum() + aux_loss):
+router GEMM, the HIP route / dispatch / grouped-expert / combine kernels, and the HIP
+backward producing dX, dW for all 78 experts and the router gradient.  Inputs and
+weights are resident in HBM before the timed region.
+
+Prints ONE JSON line.  `value` is forward+backward tokens/s; the forward-only rate
+(train mode, no_grad) is reported beside it.  `roofline` covers the step's dominant
+kernel, timed live with HIP events recorded by the library on the stream it launches
+on.  `cpu_baseline` times the CPU restatement of the reference's eager bf16 path
+(oracle/moe_ref.py, pinned bit-exact to the reference by tests/golden) on this host's
+cores over a bounded sample.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--tokens", type=int, default=8192)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    return ap.parse_args()
+
+
+def build_block(T: int, seed: int = 0):
+    """BASELINE recipe: seed 0, params in the reference's draw order x 0.02, bf16; then x, g."""
+    from nanospeaker_amd import MoEBlock
+
+    torch.manual_seed(seed)
+    m = MoEBlock(576, 76, d_ff=192, top_k=6, n_shared=2, capacity_factor=None, fused=False)
+    m = m.to(torch.bfloat16).train()
+    x = torch.randn(T, 576).to(torch.bfloat16)
+    g = torch.randn(T, 576).to(torch.bfloat16)
+    return m, x, g
+
+
+def kernel_units(name: str, T: int, k: int, S: int, d: int, H: int, E: int):
+    """(algorithmic units per launch, bound, unit) for the roofline of kernel `name`."""
+    rows = T * k + S * T  # routed pairs + shared rows
+    if name == "expert_fwd":        # GEMM1 + GEMM2 per row
+        return rows * (2 * d * 2 * H + 2 * H * d), "mfma", "TFLOP/s"
+    if name == "expert_bwd":        # G = dout W_out^T, dX = dA1 W_in^T per row
+        return rows * (2 * d * H + 2 * 2 * H * d), "mfma", "TFLOP/s"
+    if name == "expert_fwd_a1":
+        return rows * (2 * d * 2 * H), "mfma", "TFLOP/s"
+    if name == "dw_in":
+        return rows * (2 * d * 2 * H), "mfma", "TFLOP/s"
+    if name == "dw_out":
+        return rows * (2 * H * d), "mfma", "TFLOP/s"
+    if name == "combine":           # read k + S rows, write one, per token (+ inv)
+        return T * ((k + S) * d * 2 + d * 2 + k * 4), "hbm", "GB/s"
+    if name == "route_fwd":         # logits in, probs out, ids + gates out
+        return T * (E * 4 * 2 + k * 8 + k * 2), "hbm", "GB/s"
+    if name == "dispatch":          # ids read twice, sorted ids + inverse written
+        return T * k * (8 * 2 + 4 + 4), "hbm", "GB/s"
+    return None
+
+
+def time_gpu(m, x, g, steps: int, warmup: int):
+    from nanospeaker_amd import _native as nat
+
+    params = [p for p in m.parameters()]
+
+    def step():
+        for p in params:
+            p.grad = None
+        xg = x.detach().requires_grad_(True)
+        out = m(xg)
+        torch.autograd.backward([out, m.aux_loss], [g, torch.ones_like(m.aux_loss)])
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # fwd + bwd, timed
+    nat.timing_enable(64 * steps + 64)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    kernels = {}
+    for name in ("route_fwd", "dispatch", "expert_fwd", "combine", "expert_bwd", "dw_in",
+                 "dw_out", "expert_fwd_a1"):
+        tot, n = nat.timing_read(name)
+        if n:
+            kernels[name] = (tot / n, n // steps)
+    nat.timing_enable(0)
+
+    # forward only (train mode, no autograd)
+    with torch.no_grad():
+        for _ in range(warmup):
+            m(x)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            m(x)
+        torch.cuda.synchronize()
+        fwd_ms = (time.perf_counter() - t0) * 1e3 / steps
+    return ms, fwd_ms, kernels
+
+
+def cpu_baseline(seconds: float):
+    """The reference's eager bf16 CPU path (restated in oracle/moe_ref.py), fwd + bwd."""
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import moe_ref as R
+
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    torch.set_num_threads(cores)
+    c = R.nanospeaker_config()
+    p = R.make_params(0, c["d"], c["E"], c["d_ff"], n_shared=c["n_shared"]).to(dtype=torch.bfloat16)
+    T = 8192
+    x = torch.randn(T, c["d"]).to(torch.bfloat16)
+    g = torch.randn(T, c["d"]).to(torch.bfloat16)
+    R.block(x[:512], p, c["top_k"], grad_out=g[:512])  # warm-up on a slice
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 5 and (time.perf_counter() - t_start) < seconds:
+        t0 = time.perf_counter()
+        R.block(x, p, c["top_k"], grad_out=g)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    return {
+        "value": round(T / med, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
+        "sample": f"{len(times)} fwd+bwd steps of the eager bf16 block at T=8192 "
+                  f"(median {med * 1e3:.0f} ms; oracle/moe_ref.py, torch CPU)",
+    }
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; multi-GPU sharding is "
+                                   "design-only (DESIGN.md), so --gpus must be 1"}))
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        sys.exit(1)
+    T = a.tokens
+    m, x, g = build_block(T)
+    m = m.cuda()
+    x, g = x.cuda(), g.cuda()
+    ms, fwd_ms, kernels = time_gpu(m, x, g, a.steps, a.warmup)
+
+    k, S, d, H, E = 6, 2, 576, 128, 76
+    dom = max(kernels, key=lambda n: kernels[n][0] * kernels[n][1]) if kernels else None
+    roofline = None
+    if dom:
+        units, bound, unit = kernel_units(dom, T, k, S, d, H, E)
+        avg_s = kernels[dom][0] / 1e3
+        if bound == "mfma":
+            achieved, peak = units / avg_s / 1e12, PEAK_BF16_TFLOPS
+        else:
+            achieved, peak = units / avg_s / 1e9, PEAK_HBM_GBS
+        roofline = {"kernel": dom, "bound": bound, "achieved": round(achieved, 2),
+                    "peak": peak, "unit": unit, "frac": round(achieved / peak, 4),
+                    "traffic": None, "avg_launch_us": round(kernels[dom][0] * 1e3, 2),
+                    "algorithmic_per_launch": units}
+    rec = {
+        "metric": "MoE-block tokens/s fwd & fwd+bwd at T=8192 bf16; % of MFMA / HBM peak",
+        "value": round(T / (ms / 1e3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"nanoSpeaker MoE block fwd+bwd, T={T} (BASELINE config 2)",
+                   "n_tokens": T, "d_model": d, "n_experts": E, "n_shared": S, "top_k": k,
+                   "d_hidden": H, "mode": "train, aux_loss 1e-2"},
+        "fwd_tokens_per_s": round(T / (fwd_ms / 1e3), 1),
+        "fwd_ms": round(fwd_ms, 4),
+        "kernels_us": {n: round(v[0] * 1e3, 2) for n, v in kernels.items()},
+        "roofline": roofline,
+    }
+    if not a.no_cpu_baseline:
+        rec["cpu_baseline"] = cpu_baseline(a.cpu_seconds)
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

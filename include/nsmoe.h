@@ -1,0 +1,184 @@
+/*
+ * nsmoe.h -- C ABI of libnsmoe.so, the MI355X (gfx950) HIP implementation of
+ * nanoSpeaker's dropless MoE hot path: router tail, dispatch, grouped SwiGLU experts
+ * (routed + shared), combine and the full backward.
+ *
+ * Conventions
+ *   - Every pointer is a device pointer unless stated; tensors are dense row-major.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the default stream).  Calls only
+ *     enqueue work: no host synchronisation, no device allocation.  Scratch memory is a
+ *     caller-provided `workspace` sized by the matching *_workspace_size query.
+ *   - Return value: 0 on success, non-zero on error; nsmoe_last_error() then holds a
+ *     message (thread-local).  1 = invalid argument, 2 = HIP launch error,
+ *     3 = workspace too small.
+ *   - dtype codes: 0 = bf16, 1 = fp16, 2 = fp32 (NSMOE_BF16 / NSMOE_F16 / NSMOE_F32).
+ *   - activation codes match the reference's KERNEL_ACTIVATIONS
+ *     (src/model/moe_kernel.py:75): 0 silu/swish, 1 gelu (erf), 2 relu, 3 sigmoid,
+ *     4 tanh.
+ *
+ * Each entry point names the reference interface it replaces.
+ */
+#ifndef NSMOE_H_
+#define NSMOE_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NSMOE_BF16 0
+#define NSMOE_F16 1
+#define NSMOE_F32 2
+
+/* ---- library housekeeping ---------------------------------------------------------- */
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* nsmoe_last_error(void);
+
+/* Number of kernels this process has launched through the library (monotonic). */
+uint64_t nsmoe_launch_count(void);
+
+/* ABI version of this header. */
+int32_t nsmoe_abi_version(void);
+
+/* Measurement hooks (no counterpart in the reference; used by bench.py).  When enabled,
+ * the library records a HIP event pair on the launch stream around each launch of its
+ * main kernels ("expert_fwd", "expert_fwd_a1", "combine", "expert_bwd", "dw_in",
+ * "dw_out", "route_fwd", "dispatch") until `capacity` pairs are used.
+ * nsmoe_timing_read waits for the recorded events of one kernel and returns their
+ * summed duration.  capacity 0 disables timing and frees the events. */
+int nsmoe_timing_enable(int32_t capacity);
+int nsmoe_timing_read(const char* kernel_name, double* total_ms, int64_t* launches);
+
+/* ---- router tail ----------------------------------------------------------------------
+ * Replaces the softmax / topk / renormalise / cast tail of TopKRouter.forward
+ * (src/model/router.py:79-98); the logits GEMM `(x @ W).float()` (router.py:69) is the
+ * caller's.
+ *   logits    [n_tokens, n_experts] fp32
+ *   flags     bit 0 NSMOE_ROUTE_PROBS: training branch (router.py:79-81): probs =
+ *             softmax(logits) is written to `probs` [n_tokens, n_experts] fp32 and the
+ *             top-k runs on it; otherwise top-k runs on the logits (router.py:86-92).
+ *             bit 1 NSMOE_ROUTE_NORMALIZE: normalize_weights.
+ *   topk_w    [n_tokens, top_k] in w_dtype; topk_idx [n_tokens, top_k] int64, in the
+ *             order CPU torch.topk returns them, ties included.
+ * Limits: 1 <= top_k <= n_experts <= 128.
+ */
+#define NSMOE_ROUTE_PROBS 1
+#define NSMOE_ROUTE_NORMALIZE 2
+int nsmoe_route_fwd(const float* logits, int64_t n_tokens, int32_t n_experts, int32_t top_k,
+                    int32_t flags, int32_t w_dtype, void* topk_w, int64_t* topk_idx,
+                    float* probs, void* stream);
+
+/* Backward of nsmoe_route_fwd to d(logits) [n_tokens, n_experts] fp32 (torch autograd
+ * through router.py:79-98).  `src` is the probs of the forward when flags has
+ * NSMOE_ROUTE_PROBS, else the logits.  grad_probs (the balance-loss gradient,
+ * router.py:110-111) may be NULL. */
+int nsmoe_route_bwd(const float* src, const int64_t* topk_idx, const void* grad_topk_w,
+                    int32_t w_dtype, const float* grad_probs, int64_t n_tokens,
+                    int32_t n_experts, int32_t top_k, int32_t flags, float* grad_logits,
+                    void* stream);
+
+/* ---- dispatch -------------------------------------------------------------------------
+ * Replaces moe_dispatch (src/model/moe_kernel.py:180-218) with the permutation of
+ * MoEBlock._plan (src/model/moe.py:208-223): pairs p = t * top_k + j are sorted by
+ * expert, stably, so each expert's run is in increasing p.
+ *   topk_idx     [n_pairs] int64 expert ids (ids outside [0, n_experts) are ignored and
+ *                get inv = -1)
+ *   sorted_ids   [l_cap] int32: pair id per slot, sentinel n_pairs in pad slots
+ *   expert_ids   [l_cap / align_m] int32: owner expert of each aligned block (0 past the
+ *                data)
+ *   pad_offsets  [n_experts + 1] int32: run starts, each run padded to align_m slots
+ *   counts       [n_experts] int32: routing counts
+ *   n_post_pad   [1] int32: padded total
+ *   inv          [n_pairs] int32: slot of each pair
+ * l_cap = nsmoe_dispatch_l_cap(n_pairs, n_experts); workspace >=
+ * nsmoe_dispatch_workspace_size(n_pairs, n_experts) bytes.  n_experts <= 1024.
+ */
+int64_t nsmoe_align_m(void);
+int64_t nsmoe_dispatch_l_cap(int64_t n_pairs, int32_t n_experts);
+size_t nsmoe_dispatch_workspace_size(int64_t n_pairs, int32_t n_experts);
+int nsmoe_dispatch(const int64_t* topk_idx, int64_t n_pairs, int32_t n_experts,
+                   int32_t* sorted_ids, int32_t* expert_ids, int32_t* pad_offsets,
+                   int32_t* counts, int32_t* n_post_pad, int32_t* inv, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
+/* ---- experts --------------------------------------------------------------------------
+ * Routed experts (moe_experts, src/model/moe_kernel.py:558-617) plus, when n_shared > 0,
+ * the always-on shared experts (MoEBlock._shared, src/model/moe.py:310-329) folded in
+ * as extra groups over every token at gate 1.
+ *
+ * Row space: routed rows are the dispatch slots [0, l_cap); shared expert s owns rows
+ * l_cap + s * n_tokens + t.  rows_total = l_cap + n_shared * n_tokens.
+ *
+ * Limits: d_hidden <= 256; n_experts + n_shared <= 1024.
+ */
+typedef struct nsmoe_experts_args {
+  int32_t dtype;       /* element type of x, weights, biases, topk_w and outputs */
+  int32_t activation;
+  int64_t n_tokens;    /* T */
+  int32_t d_model;     /* d */
+  int32_t d_hidden;    /* H; w_in is [E, d, 2H] with gate columns [0, H), up [H, 2H) */
+  int32_t n_experts;   /* E (routed) */
+  int32_t n_shared;    /* S */
+  int32_t top_k;       /* k */
+  int32_t reserved0;
+  int64_t l_cap;       /* length of sorted_ids */
+
+  const void* x;        /* [T, d] */
+  const void* w_in;     /* [E, d, 2H] */
+  const void* w_out;    /* [E, H, d] */
+  const void* b_in;     /* [E, 2H] or NULL */
+  const void* b_out;    /* [E, d] or NULL */
+  const void* w_sh_in;  /* [S, d, 2H] (NULL when S == 0) */
+  const void* w_sh_out; /* [S, H, d] */
+  const void* b_sh_in;  /* [S, 2H] or NULL */
+  const void* b_sh_out; /* [S, d] or NULL */
+  const void* topk_w;   /* [T, k] gate weights */
+
+  const int32_t* sorted_ids;  /* dispatch outputs (nsmoe_dispatch) */
+  const int32_t* pad_offsets;
+  const int32_t* counts;
+} nsmoe_experts_args;
+
+/* Forward: out [T, d] = sum_j topk_w[t, j] * expert_{idx[t, j]}(x[t]) + sum_s shared_s(x[t]).
+ *   inv    [T * k] int32 from nsmoe_dispatch.
+ * workspace >= nsmoe_experts_fwd_workspace_size(args) (the per-row expert outputs). */
+size_t nsmoe_experts_fwd_workspace_size(const nsmoe_experts_args* args);
+int nsmoe_experts_fwd(const nsmoe_experts_args* args, const int32_t* inv, void* out,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* Backward (_moe_experts_bwd, src/model/moe_kernel.py:626-739, plus the shared experts).
+ * The gate/up pre-activations are recomputed inside the backward's tiles (fp32, never
+ * stored), as the reference recomputes them (moe_kernel.py:663-672).
+ *   grad_out  [T, d]
+ *   dx        [T, d]; dw_in / dw_out like w_in / w_out; dw_sh_in / dw_sh_out like the
+ *             shared weights (NULL when S == 0); dtopk_w [T, k]
+ *   db_in, db_out, db_sh_in, db_sh_out: bias gradients, each NULL when not wanted.
+ * dtopk_w is the full derivative of (h W_out + b_out) * w with respect to w, so it
+ * includes <grad_out, b_out> when the experts have an output bias.
+ * workspace >= nsmoe_experts_bwd_workspace_size(args). */
+typedef struct nsmoe_experts_grads {
+  void* dx;
+  void* dw_in;
+  void* dw_out;
+  void* dw_sh_in;
+  void* dw_sh_out;
+  void* dtopk_w;
+  void* db_in;
+  void* db_out;
+  void* db_sh_in;
+  void* db_sh_out;
+} nsmoe_experts_grads;
+
+size_t nsmoe_experts_bwd_workspace_size(const nsmoe_experts_args* args);
+int nsmoe_experts_bwd(const nsmoe_experts_args* args, const int32_t* inv,
+                      const void* grad_out, const nsmoe_experts_grads* grads,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NSMOE_H_ */

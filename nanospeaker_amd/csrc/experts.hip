@@ -1,0 +1,1101 @@
+// Grouped SwiGLU experts on gfx950 MFMA: forward, combine and the full backward.
+//
+// Reference: moe_experts / _moe_experts_bwd (src/model/moe_kernel.py:558-739) for the
+// routed experts, MoEBlock._shared (src/model/moe.py:310-329) for the shared ones.  The
+// shared experts are folded in as extra groups: group g < E is routed expert g over its
+// dispatch slots, group E + s is shared expert s over every token at gate 1.
+//
+// Kernels (one workgroup = 4 waves, tiles of 64 rows of one group):
+//   expert_fwd   GEMM1 x[tok] @ W_in[g] with the gate and up halves in two accumulator
+//                sets, bias + act(gate) * up in registers, h kept in LDS (bf16) and fed
+//                straight into GEMM2 h @ W_out[g]; + b_out, * gate weight, stored per row.
+//   combine      out[t] = sum_j y[inv[t, j]] + sum_s y[shared_s, t], in fp32.
+//   expert_bwd   recomputes a1 = x[tok] @ W_in[g] (fp32, in registers) alongside
+//                G = dout[tok] @ W_out[g]^T, runs the GLU backward in the epilogue (dA1,
+//                the hidden h, the gate gradient), then dA1 @ W_in[g]^T from LDS into
+//                per-row dX rows (reduced by `combine`).
+//   dw           dW_in[g] = x^T dA1 and dW_out[g] = h^T (w * dout) over the group's rows,
+//                split into row chunks of DW_RC; groups with several chunks write fp32
+//                partials that dw_reduce sums in chunk order (deterministic, no atomics).
+//   bias_grad    per-group column sums for the optional biases.
+#include <algorithm>
+
+#include "gemm_core.h"
+#include "nsmoe_capi_internal.h"
+#include "../../include/nsmoe.h"
+
+namespace nsmoe {
+
+constexpr int BM = 64;      // rows per tile
+constexpr int NT = 256;     // threads per workgroup
+constexpr int DW_RC = 2048; // rows per dW chunk
+
+struct ExpParams {
+  const void* x;
+  const void* w_in;
+  const void* w_out;
+  const void* b_in;
+  const void* b_out;
+  const void* w_sh_in;
+  const void* w_sh_out;
+  const void* b_sh_in;
+  const void* b_sh_out;
+  const void* topk_w;
+  const int32_t* sorted_ids;
+  const int32_t* offs;
+  const int32_t* counts;
+  int64_t T;
+  int64_t l_cap;
+  int d, H, E, S, k, act;
+  int fast;
+  // forward output rows
+  void* y;
+  // backward
+  const void* dout;
+  void* da1;
+  void* hbuf;
+  void* dxrow;
+  void* dtw;
+  // dW
+  void* dw_a;      // dW_in or dW_out (routed)
+  void* dw_sh;     // shared counterpart
+  float* partial;  // fp32 partials
+  void* db;        // bias grad (routed)
+  void* db_sh;     // bias grad (shared)
+};
+
+__device__ __forceinline__ int rows_of(const ExpParams& p, int g) {
+  return g < p.E ? p.counts[g] : (int)p.T;
+}
+__device__ __forceinline__ int64_t row_start(const ExpParams& p, int g) {
+  return g < p.E ? (int64_t)p.offs[g] : p.l_cap + (int64_t)(g - p.E) * p.T;
+}
+template <class T>
+__device__ __forceinline__ const T* per_group(const void* routed, const void* shared, int g,
+                                              int E, int64_t stride) {
+  return g < E ? (const T*)routed + (int64_t)g * stride
+               : (const T*)shared + (int64_t)(g - E) * stride;
+}
+
+// Token, gate weight and pair id of local row `r` of group g (slot = row_start + r).
+template <int DT>
+__device__ __forceinline__ void row_info(const ExpParams& p, int g, int64_t slot, int r,
+                                         int& tok, float& w, int& pair) {
+  if (g < p.E) {
+    pair = p.sorted_ids[slot];
+    tok = pair / p.k;
+    w = Elem<DT>::to_f(((const typename Elem<DT>::T*)p.topk_w)[pair]);
+  } else {
+    pair = -1;
+    tok = r;
+    w = 1.0f;
+  }
+}
+
+// Copies `rows` rows of an LDS tile out to global rows dst + (slot0 + m) * ld, columns
+// [0, n_a) from LDS columns [0, n_a) and, if n_b > 0, global columns [n_a, n_a + n_b)
+// from LDS columns [lds_b, lds_b + n_b).
+template <int DT>
+__device__ __forceinline__ void copy_out(const char* tile, int pitch, int rows,
+                                         typename Elem<DT>::T* dst, int64_t ld, int64_t col0,
+                                         int n_a, int lds_b, int n_b, bool fast) {
+  using G = Geo<DT>;
+  using T = typename G::T;
+  const int ncols = n_a + n_b;
+  if (fast) {
+    const int vpr = ncols / G::VE;
+    for (int i = threadIdx.x; i < rows * vpr; i += NT) {
+      const int m = i / vpr, c = (i % vpr) * G::VE;
+      const int lc = c < n_a ? c : lds_b + (c - n_a);
+      *(u32x4*)(dst + m * ld + col0 + c) = *(const u32x4*)(tile + m * pitch + lc * G::ES);
+    }
+  } else {
+    for (int i = threadIdx.x; i < rows * ncols; i += NT) {
+      const int m = i / ncols, c = i % ncols;
+      const int lc = c < n_a ? c : lds_b + (c - n_a);
+      dst[m * ld + col0 + c] = *(const T*)(tile + m * pitch + lc * G::ES);
+    }
+  }
+}
+
+// ============================ forward ====================================================
+
+template <int DT, int NBW>
+__global__ void __launch_bounds__(NT) expert_fwd_kernel(ExpParams p) {
+  using G = Geo<DT>;
+  using T = typename G::T;
+  using M = Mma<DT>;
+  constexpr int HPMAX = 64 * NBW;  // gate (and up) columns one tile covers
+  constexpr int SA = BM * G::PITCH;
+  constexpr int SB = 2 * HPMAX * G::PITCH;
+  constexpr int REGION0 = 2 * (SA + SB);
+  constexpr int HP_PITCH = HPMAX * G::ES + 16;
+  constexpr int SB2 = 64 * G::PITCH;
+  constexpr int Y_PITCH = 64 * G::ES + 16;
+  static_assert(2 * SB2 + BM * Y_PITCH <= REGION0, "GEMM2 staging must fit in the region");
+  __shared__ __attribute__((aligned(16))) char s_r0[REGION0];
+  __shared__ __attribute__((aligned(16))) char s_h[BM * HP_PITCH];
+  __shared__ int s_tok[BM];
+  __shared__ float s_w[BM];
+  __shared__ int s_loc[3];
+
+  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  Located loc;
+  if (!locate(tile, p.E + p.S, [&](int g) { return (rows_of(p, g) + BM - 1) / BM; },
+              [](int) { return 0; }, s_loc, loc))
+    return;
+  const int g = loc.g, m0 = loc.local * BM;
+  const int rows = min(BM, rows_of(p, g) - m0);
+  const int64_t slot0 = row_start(p, g) + m0;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lc = lane & 15, lg = lane >> 4;
+  if (tid < BM) {
+    int tok = -1, pair;
+    float w = 0.0f;
+    if (tid < rows) row_info<DT>(p, g, slot0 + tid, m0 + tid, tok, w, pair);
+    s_tok[tid] = tok;
+    s_w[tid] = w;
+  }
+  __syncthreads();
+
+  const int d = p.d, H = p.H, twoH = 2 * p.H;
+  const bool fast = p.fast;
+  const T* X = (const T*)p.x;
+  const T* Win = per_group<T>(p.w_in, p.w_sh_in, g, p.E, (int64_t)d * twoH);
+  auto rowA = [&](int r) -> const T* {
+    const int t = s_tok[r];
+    return t >= 0 ? X + (int64_t)t * d : nullptr;
+  };
+  auto rowB = [&](int k) -> const T* { return Win + (int64_t)k * twoH; };
+  auto sA = [&](int b) { return s_r0 + b * SA; };
+  auto sB = [&](int b) { return s_r0 + 2 * SA + b * SB; };
+
+  // ---- GEMM1: [BM, d] x [d, gate | up] ----
+  DirectStage<DT, BM, NT> stA;
+  TransStage<DT, HPMAX, NT> stG, stU;
+  f32x4 accg[4][NBW], accu[4][NBW];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) accg[i][j] = accu[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int nk = (d + G::KC - 1) / G::KC;
+  stA.load(rowA, 0, d, fast);
+  stG.load(rowB, NoScale{}, 0, d, 0, H, fast);
+  stU.load(rowB, NoScale{}, 0, d, H, twoH, fast);
+  stA.store(sA(0));
+  stG.store(sB(0));
+  stU.store(sB(0) + HPMAX * G::PITCH);
+  __syncthreads();
+  for (int kc = 0; kc < nk; ++kc) {
+    const int cur = kc & 1;
+    const bool more = kc + 1 < nk;
+    if (more) {
+      const int k0 = (kc + 1) * G::KC;
+      stA.load(rowA, k0, d, fast);
+      stG.load(rowB, NoScale{}, k0, d, 0, H, fast);
+      stU.load(rowB, NoScale{}, k0, d, H, twoH, fast);
+    }
+    typename M::Frag af[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) af[i] = frag_at<DT>(sA(cur), G::PITCH, i * 16, 0);
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) {
+      const int jb = (wave * NBW + j) * 16;
+      const typename M::Frag bg = frag_at<DT>(sB(cur), G::PITCH, jb, 0);
+      const typename M::Frag bu = frag_at<DT>(sB(cur), G::PITCH, HPMAX + jb, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        M::run(accg[i][j], af[i], bg);
+        M::run(accu[i][j], af[i], bu);
+      }
+    }
+    if (more) {
+      stA.store(sA(cur ^ 1));
+      stG.store(sB(cur ^ 1));
+      stU.store(sB(cur ^ 1) + HPMAX * G::PITCH);
+    }
+    __syncthreads();
+  }
+
+  // ---- GEMM1 epilogue: bias, h = act(gate) * up into LDS ----
+  const T* bin = (g < p.E ? p.b_in : p.b_sh_in)
+                     ? per_group<T>(p.b_in, p.b_sh_in, g, p.E, twoH) : nullptr;
+#pragma unroll
+  for (int j = 0; j < NBW; ++j) {
+    const int n = (wave * NBW + j) * 16 + lc;
+    const bool nv = n < H;
+    const float bgv = (nv && bin) ? Elem<DT>::to_f(bin[n]) : 0.0f;
+    const float buv = (nv && bin) ? Elem<DT>::to_f(bin[H + n]) : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = i * 16 + lg * 4 + r;
+        const float gv = accg[i][j][r] + bgv, uv = accu[i][j][r] + buv;
+        const float hv = nv ? act_fwd(gv, p.act) * uv : 0.0f;
+        *(T*)(s_h + m * HP_PITCH + n * G::ES) = Elem<DT>::from_f(hv);
+      }
+  }
+  __syncthreads();
+
+  // ---- GEMM2: [BM, H] x [H, d] in column blocks of 64, + b_out, * gate ----
+  const T* Wout = per_group<T>(p.w_out, p.w_sh_out, g, p.E, (int64_t)H * d);
+  const T* bout = (g < p.E ? p.b_out : p.b_sh_out)
+                      ? per_group<T>(p.b_out, p.b_sh_out, g, p.E, d) : nullptr;
+  auto rowW = [&](int k) -> const T* { return Wout + (int64_t)k * d; };
+  auto sB2 = [&](int b) { return s_r0 + b * SB2; };
+  char* sY = s_r0 + 2 * SB2;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int nk2 = (H + G::KC - 1) / G::KC;
+  TransStage<DT, 64, NT> stW;
+  T* Y = (T*)p.y;
+  for (int n0 = 0; n0 < d; n0 += 64) {
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    stW.load(rowW, NoScale{}, 0, H, n0, d, fast);
+    stW.store(sB2(0));
+    __syncthreads();
+    for (int kc = 0; kc < nk2; ++kc) {
+      const int cur = kc & 1;
+      const bool more = kc + 1 < nk2;
+      if (more) stW.load(rowW, NoScale{}, (kc + 1) * G::KC, H, n0, d, fast);
+      typename M::Frag af[2], bf[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        af[i] = frag_at<DT>(s_h, HP_PITCH, wm * 32 + i * 16, kc * G::ROWB);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) bf[j] = frag_at<DT>(sB2(cur), G::PITCH, wn * 32 + j * 16, 0);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) M::run(acc[i][j], af[i], bf[j]);
+      if (more) stW.store(sB2(cur ^ 1));
+      __syncthreads();
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int nl = wn * 32 + j * 16 + lc;
+      const int n = n0 + nl;
+      const float bo = (bout && n < d) ? Elem<DT>::to_f(bout[n]) : 0.0f;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = wm * 32 + i * 16 + lg * 4 + r;
+          *(T*)(sY + m * Y_PITCH + nl * G::ES) = Elem<DT>::from_f((acc[i][j][r] + bo) * s_w[m]);
+        }
+    }
+    __syncthreads();
+    copy_out<DT>(sY, Y_PITCH, rows, Y + slot0 * d, d, n0, min(64, d - n0), 0, 0, fast);
+    __syncthreads();
+  }
+}
+
+// ============================ combine ====================================================
+// out[t] = sum_j rows[inv[t * k + j]] + sum_s rows[l_cap + s * T + t], fp32 accumulation.
+template <int DT>
+__global__ void __launch_bounds__(NT)
+combine_kernel(const typename Elem<DT>::T* __restrict__ rows, const int32_t* __restrict__ inv,
+               int64_t ntok, int d, int k, int S, int64_t l_cap,
+               typename Elem<DT>::T* __restrict__ out, int fast) {
+  using G = Geo<DT>;
+  using TT = typename G::T;
+  if (fast) {
+    const int vpr = d / G::VE;
+    const int64_t n = ntok * vpr;
+    for (int64_t i = (int64_t)blockIdx.x * NT + threadIdx.x; i < n; i += (int64_t)gridDim.x * NT) {
+      const int64_t t = i / vpr;
+      const int c = (int)(i % vpr) * G::VE;
+      float acc[G::VE];
+#pragma unroll
+      for (int e = 0; e < G::VE; ++e) acc[e] = 0.0f;
+      for (int j = 0; j < k; ++j) {
+        const int32_t s = inv[t * k + j];
+        if (s < 0) continue;
+        u32x4 v = *(const u32x4*)(rows + (int64_t)s * d + c);
+        TT tmp[G::VE];
+        __builtin_memcpy(tmp, &v, 16);
+#pragma unroll
+        for (int e = 0; e < G::VE; ++e) acc[e] += Elem<DT>::to_f(tmp[e]);
+      }
+      for (int s = 0; s < S; ++s) {
+        u32x4 v = *(const u32x4*)(rows + (l_cap + (int64_t)s * ntok + t) * d + c);
+        TT tmp[G::VE];
+        __builtin_memcpy(tmp, &v, 16);
+#pragma unroll
+        for (int e = 0; e < G::VE; ++e) acc[e] += Elem<DT>::to_f(tmp[e]);
+      }
+      TT o[G::VE];
+#pragma unroll
+      for (int e = 0; e < G::VE; ++e) o[e] = Elem<DT>::from_f(acc[e]);
+      u32x4 ov;
+      __builtin_memcpy(&ov, o, 16);
+      *(u32x4*)(out + t * d + c) = ov;
+    }
+  } else {
+    const int64_t n = ntok * d;
+    for (int64_t i = (int64_t)blockIdx.x * NT + threadIdx.x; i < n; i += (int64_t)gridDim.x * NT) {
+      const int64_t t = i / d;
+      const int c = (int)(i % d);
+      float acc = 0.0f;
+      for (int j = 0; j < k; ++j) {
+        const int32_t s = inv[t * k + j];
+        if (s >= 0) acc += Elem<DT>::to_f(rows[(int64_t)s * d + c]);
+      }
+      for (int s = 0; s < S; ++s)
+        acc += Elem<DT>::to_f(rows[(l_cap + (int64_t)s * ntok + t) * d + c]);
+      out[t * d + c] = Elem<DT>::from_f(acc);
+    }
+  }
+}
+
+// ============================ backward: recompute, GLU backward, dX rows ==================
+//
+// Phase 1 runs three GEMMs over the same 64 gathered token rows and K = d in one loop:
+//   a1 = x[tok] @ W_in[g]      (gate and up, the forward's pre-activations, recomputed
+//                               in fp32 registers instead of being saved and re-read)
+//   G  = dout[tok] @ W_out[g]^T
+// Wave w owns hidden columns {(w * NBW + j) * 16 ..}: the gate, up and G accumulators of
+// one (row, column) sit in the same lane and register, so the GLU backward is lane-local:
+//   h = act(g) * u,  dtopk_w += G * h,  d_gate = w G u act'(g),  d_up = w G act(g).
+// dA1 = [d_gate | d_up] goes to LDS (bf16) for phase 3 and to HBM for dW_in; h goes to
+// HBM for dW_out.  The gate gradient also takes <dout[tok], b_out[g]> when the expert
+// has an output bias (the derivative of (h W_out + b_out) * w with respect to w).
+// Phase 3: dX rows = dA1 @ W_in[g]^T, reduced per token by `combine`.
+template <int DT, int NBW>
+struct BwdCfg {
+  using G = Geo<DT>;
+  static constexpr int HPMAX = 64 * NBW;
+  static constexpr int SX = BM * G::PITCH;           // x chunk
+  static constexpr int SD = BM * G::PITCH;           // dout chunk
+  static constexpr int SWI = 2 * HPMAX * G::PITCH;   // W_in^T chunk (gate | up)
+  static constexpr int SWO = HPMAX * G::PITCH;       // W_out chunk
+  static constexpr int STAGE = SX + SD + SWI + SWO;
+  static constexpr int DA_PITCH = 2 * HPMAX * G::ES + 16;
+  static constexpr int SDA = BM * DA_PITCH;
+  static constexpr bool DB = 2 * STAGE + SDA <= 150 * 1024;  // double-buffer if it fits
+  static constexpr int REGION0 = (DB ? 2 : 1) * STAGE;
+  static constexpr int SB3 = 64 * G::PITCH;
+  static constexpr int Y_PITCH = 64 * G::ES + 16;
+  static_assert(2 * SB3 + BM * Y_PITCH <= REGION0, "dX staging must fit in the region");
+};
+
+template <int DT, int NBW>
+__global__ void __launch_bounds__(NT) expert_bwd_kernel(ExpParams p) {
+  using G = Geo<DT>;
+  using T = typename G::T;
+  using M = Mma<DT>;
+  using C = BwdCfg<DT, NBW>;
+  constexpr int HPMAX = C::HPMAX;
+  __shared__ __attribute__((aligned(16))) char s_r0[C::REGION0];
+  __shared__ __attribute__((aligned(16))) char s_da[C::SDA];
+  __shared__ int s_tok[BM];
+  __shared__ int s_pair[BM];
+  __shared__ float s_w[BM];
+  __shared__ float s_dtw[5][BM];
+  __shared__ int s_loc[3];
+
+  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  Located loc;
+  if (!locate(tile, p.E + p.S, [&](int g) { return (rows_of(p, g) + BM - 1) / BM; },
+              [](int) { return 0; }, s_loc, loc))
+    return;
+  const int g = loc.g, m0 = loc.local * BM;
+  const int rows = min(BM, rows_of(p, g) - m0);
+  const int64_t slot0 = row_start(p, g) + m0;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lc = lane & 15, lg = lane >> 4;
+  if (tid < BM) {
+    int tok = -1, pair = -1;
+    float w = 0.0f;
+    if (tid < rows) row_info<DT>(p, g, slot0 + tid, m0 + tid, tok, w, pair);
+    s_tok[tid] = tok;
+    s_pair[tid] = pair;
+    s_w[tid] = w;
+    s_dtw[4][tid] = 0.0f;
+  }
+  __syncthreads();
+
+  const int d = p.d, H = p.H, twoH = 2 * p.H;
+  const bool fast = p.fast;
+  const T* X = (const T*)p.x;
+  const T* DO = (const T*)p.dout;
+  const T* Win = per_group<T>(p.w_in, p.w_sh_in, g, p.E, (int64_t)d * twoH);
+  const T* Wout = per_group<T>(p.w_out, p.w_sh_out, g, p.E, (int64_t)H * d);
+  auto rowX = [&](int r) -> const T* {
+    const int t = s_tok[r];
+    return t >= 0 ? X + (int64_t)t * d : nullptr;
+  };
+  auto rowD = [&](int r) -> const T* {
+    const int t = s_tok[r];
+    return t >= 0 ? DO + (int64_t)t * d : nullptr;
+  };
+  auto rowWi = [&](int k) -> const T* { return Win + (int64_t)k * twoH; };
+  auto rowWo = [&](int n) -> const T* { return n < H ? Wout + (int64_t)n * d : nullptr; };
+  auto stage = [&](int b) { return s_r0 + (C::DB ? b : 0) * C::STAGE; };
+  auto sX = [&](int b) { return stage(b); };
+  auto sD = [&](int b) { return stage(b) + C::SX; };
+  auto sWi = [&](int b) { return stage(b) + C::SX + C::SD; };
+  auto sWo = [&](int b) { return stage(b) + C::SX + C::SD + C::SWI; };
+
+  // ---- phase 1: a1 = x W_in, G = dout W_out^T ----
+  DirectStage<DT, BM, NT> stX, stD;
+  TransStage<DT, HPMAX, NT> stG, stU;
+  DirectStage<DT, HPMAX, NT> stO;
+  f32x4 accg[4][NBW], accu[4][NBW], accG[4][NBW];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < NBW; ++j)
+      accg[i][j] = accu[i][j] = accG[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto load = [&](int k0) {
+    stX.load(rowX, k0, d, fast);
+    stD.load(rowD, k0, d, fast);
+    stG.load(rowWi, NoScale{}, k0, d, 0, H, fast);
+    stU.load(rowWi, NoScale{}, k0, d, H, twoH, fast);
+    stO.load(rowWo, k0, d, fast);
+  };
+  auto store = [&](int b) {
+    stX.store(sX(b));
+    stD.store(sD(b));
+    stG.store(sWi(b));
+    stU.store(sWi(b) + HPMAX * G::PITCH);
+    stO.store(sWo(b));
+  };
+  auto compute = [&](int b) {
+    typename M::Frag ax[4], ad[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      ax[i] = frag_at<DT>(sX(b), G::PITCH, i * 16, 0);
+      ad[i] = frag_at<DT>(sD(b), G::PITCH, i * 16, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) {
+      const int jb = (wave * NBW + j) * 16;
+      const typename M::Frag bg = frag_at<DT>(sWi(b), G::PITCH, jb, 0);
+      const typename M::Frag bu = frag_at<DT>(sWi(b), G::PITCH, HPMAX + jb, 0);
+      const typename M::Frag bo = frag_at<DT>(sWo(b), G::PITCH, jb, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        M::run(accg[i][j], ax[i], bg);
+        M::run(accu[i][j], ax[i], bu);
+        M::run(accG[i][j], ad[i], bo);
+      }
+    }
+  };
+
+  const int nk = (d + G::KC - 1) / G::KC;
+  if constexpr (C::DB) {
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int kc = 0; kc < nk; ++kc) {
+      const int cur = kc & 1;
+      const bool more = kc + 1 < nk;
+      if (more) load((kc + 1) * G::KC);
+      compute(cur);
+      if (more) store(cur ^ 1);
+      __syncthreads();
+    }
+  } else {
+    load(0);
+    for (int kc = 0; kc < nk; ++kc) {
+      store(0);
+      __syncthreads();
+      if (kc + 1 < nk) load((kc + 1) * G::KC);
+      compute(0);
+      __syncthreads();
+    }
+  }
+
+  // ---- phase 2: GLU backward, lane-local ----
+  const T* bin = (g < p.E ? p.b_in : p.b_sh_in)
+                     ? per_group<T>(p.b_in, p.b_sh_in, g, p.E, twoH) : nullptr;
+  T* HB = (T*)p.hbuf;
+  float part[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) part[i][r] = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NBW; ++j) {
+    const int n = (wave * NBW + j) * 16 + lc;
+    const bool nv = n < H;
+    const float bgv = (nv && bin) ? Elem<DT>::to_f(bin[n]) : 0.0f;
+    const float buv = (nv && bin) ? Elem<DT>::to_f(bin[H + n]) : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = i * 16 + lg * 4 + r;
+        const bool v = m < rows && nv;
+        float dg = 0.0f, du = 0.0f;
+        if (v) {
+          const float gg = accg[i][j][r] + bgv, uu = accu[i][j][r] + buv;
+          const float Gv = accG[i][j][r];
+          const float a = act_fwd(gg, p.act);
+          const float hv = a * uu;
+          part[i][r] += Gv * hv;
+          const float dh = s_w[m] * Gv;
+          dg = dh * uu * act_bwd(gg, p.act);
+          du = dh * a;
+          HB[(slot0 + m) * H + n] = Elem<DT>::from_f(hv);
+        }
+        *(T*)(s_da + m * C::DA_PITCH + n * G::ES) = Elem<DT>::from_f(dg);
+        *(T*)(s_da + m * C::DA_PITCH + (HPMAX + n) * G::ES) = Elem<DT>::from_f(du);
+      }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v = part[i][r];
+      v += __shfl_xor(v, 1, 64);
+      v += __shfl_xor(v, 2, 64);
+      v += __shfl_xor(v, 4, 64);
+      v += __shfl_xor(v, 8, 64);
+      if (lc == 0) s_dtw[wave][i * 16 + lg * 4 + r] = v;
+    }
+  // <dout[tok], b_out[g]>: four lanes per row, strided over d.
+  if (g < p.E && p.b_out) {
+    const T* bo = (const T*)p.b_out + (int64_t)g * d;
+    const int m = tid >> 2, q = tid & 3;
+    float v = 0.0f;
+    if (m < rows) {
+      const T* dr = DO + (int64_t)s_tok[m] * d;
+      for (int c = q; c < d; c += 4) v += Elem<DT>::to_f(dr[c]) * Elem<DT>::to_f(bo[c]);
+    }
+    v += __shfl_xor(v, 1, 64);
+    v += __shfl_xor(v, 2, 64);
+    if (q == 0 && m < rows) s_dtw[4][m] = v;
+  }
+  __syncthreads();
+  if (g < p.E && tid < rows) {
+    const float s = s_dtw[0][tid] + s_dtw[1][tid] + s_dtw[2][tid] + s_dtw[3][tid] + s_dtw[4][tid];
+    ((T*)p.dtw)[s_pair[tid]] = Elem<DT>::from_f(s);
+  }
+  copy_out<DT>(s_da, C::DA_PITCH, rows, (T*)p.da1 + slot0 * twoH, twoH, 0, H, HPMAX, H, fast);
+
+  // ---- phase 3: dX rows = dA1 @ W_in[g]^T, in column blocks of 64 ----
+  const int nkh = (H + G::KC - 1) / G::KC;  // chunks per half
+  const int nk3 = 2 * nkh;
+  auto sB3 = [&](int b) { return s_r0 + b * C::SB3; };
+  char* sY = s_r0 + 2 * C::SB3;
+  const int wm = wave >> 1, wn = wave & 1;
+  DirectStage<DT, 64, NT> stW;
+  T* DX = (T*)p.dxrow;
+  for (int n0 = 0; n0 < d; n0 += 64) {
+    auto rowW = [&](int n) -> const T* {
+      return n0 + n < d ? Win + (int64_t)(n0 + n) * twoH : nullptr;
+    };
+    f32x4 acc2[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc2[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // chunk q: half = q / nkh (0 gate, 1 up), source columns half * H + (q % nkh) * 32
+    __syncthreads();  // sB3 / sY are free (phase 1 or the previous block is done)
+    stW.load(rowW, 0, H, fast);
+    stW.store(sB3(0));
+    __syncthreads();
+    for (int q = 0; q < nk3; ++q) {
+      const int cur = q & 1;
+      const bool more = q + 1 < nk3;
+      if (more) {
+        const int qn = q + 1, half = qn / nkh, kk = (qn % nkh) * G::KC;
+        stW.load(rowW, half * H + kk, half * H + H, fast);
+      }
+      const int half = q / nkh, kk = (q % nkh) * G::KC;
+      const int kbyte = (half * HPMAX + kk) * G::ES;
+      typename M::Frag af[2], bf[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        af[i] = frag_at<DT>(s_da, C::DA_PITCH, wm * 32 + i * 16, kbyte);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) bf[j] = frag_at<DT>(sB3(cur), G::PITCH, wn * 32 + j * 16, 0);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) M::run(acc2[i][j], af[i], bf[j]);
+      if (more) stW.store(sB3(cur ^ 1));
+      __syncthreads();
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int nl = wn * 32 + j * 16 + lc;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = wm * 32 + i * 16 + lg * 4 + r;
+          *(T*)(sY + m * C::Y_PITCH + nl * G::ES) = Elem<DT>::from_f(acc2[i][j][r]);
+        }
+    }
+    __syncthreads();
+    copy_out<DT>(sY, C::Y_PITCH, rows, DX + slot0 * d, d, n0, min(64, d - n0), 0, 0, fast);
+  }
+}
+
+// ============================ backward: dW ===============================================
+// MODE 0: dW_in[g]  [d, 2H] = sum_r x[tok_r]^T dA1[slot_r]
+// MODE 1: dW_out[g] [H, d]  = sum_r h[slot_r]^T (w_r * dout[tok_r])
+__device__ __forceinline__ int dw_chunks(int rows) {
+  const int c = (rows + DW_RC - 1) / DW_RC;
+  return c < 1 ? 1 : c;  // an empty group still owns one (all-zero) chunk
+}
+
+template <int DT, int MODE>
+__global__ void __launch_bounds__(NT) dw_kernel(ExpParams p) {
+  using G = Geo<DT>;
+  using T = typename G::T;
+  using Mm = Mma<DT>;
+  constexpr int S1 = 64 * G::PITCH;
+  __shared__ __attribute__((aligned(16))) char s_a[2][S1];
+  __shared__ __attribute__((aligned(16))) char s_b[2][S1];
+  __shared__ int s_loc[3];
+
+  const int d = p.d, H = p.H, twoH = 2 * p.H;
+  const int Md = MODE == 0 ? d : H;
+  const int Nd = MODE == 0 ? twoH : d;
+  const int tn = (Nd + 63) / 64, ntiles = ((Md + 63) / 64) * tn;
+  const int item = xcd_remap(blockIdx.x, gridDim.x);
+  Located loc;
+  if (!locate(item, p.E + p.S, [&](int g) { return dw_chunks(rows_of(p, g)) * ntiles; },
+              [&](int g) {
+                const int c = dw_chunks(rows_of(p, g));
+                return c > 1 ? c : 0;
+              },
+              s_loc, loc))
+    return;
+  const int g = loc.g;
+  const int rows_g = rows_of(p, g);
+  const int nch = dw_chunks(rows_g);
+  const int chunk = loc.local / ntiles, t = loc.local % ntiles;
+  const int mt = t / tn, nt = t % tn;
+  const int m0 = mt * 64, n0 = nt * 64;
+  const int r0 = chunk * DW_RC, r1 = min(rows_g, r0 + DW_RC);
+  const int64_t rs = row_start(p, g);
+  const bool fast = p.fast;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lc = lane & 15, lg = lane >> 4;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  const T* X = (const T*)p.x;
+  const T* DA = (const T*)p.da1;
+  const T* HB = (const T*)p.hbuf;
+  const T* DO = (const T*)p.dout;
+  auto tok_of = [&](int r) -> int {
+    if (g < p.E) return p.sorted_ids[rs + r] / p.k;
+    return r;
+  };
+  auto rowA = [&](int r) -> const T* {
+    if (MODE == 0) return X + (int64_t)tok_of(r) * d;
+    return HB + (rs + r) * H;
+  };
+  auto rowB = [&](int r) -> const T* {
+    if (MODE == 0) return DA + (rs + r) * twoH;
+    return DO + (int64_t)tok_of(r) * d;
+  };
+  auto scaleB = [&](int r) -> float {
+    if (MODE == 0 || g >= p.E) return 1.0f;
+    return Elem<DT>::to_f(((const T*)p.topk_w)[p.sorted_ids[rs + r]]);
+  };
+
+  TransStage<DT, 64, NT> stA, stB;
+  f32x4 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int nk = (r1 - r0 + G::KC - 1) / G::KC;
+  if (nk > 0) {
+    stA.load(rowA, NoScale{}, r0, r1, m0, Md, fast);
+    stB.load(rowB, scaleB, r0, r1, n0, Nd, fast);
+    stA.store(s_a[0]);
+    stB.store(s_b[0]);
+    __syncthreads();
+    for (int kc = 0; kc < nk; ++kc) {
+      const int cur = kc & 1;
+      const bool more = kc + 1 < nk;
+      if (more) {
+        const int k0 = r0 + (kc + 1) * G::KC;
+        stA.load(rowA, NoScale{}, k0, r1, m0, Md, fast);
+        stB.load(rowB, scaleB, k0, r1, n0, Nd, fast);
+      }
+      typename Mm::Frag af[2], bf[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) af[i] = frag_at<DT>(s_a[cur], G::PITCH, wm * 32 + i * 16, 0);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) bf[j] = frag_at<DT>(s_b[cur], G::PITCH, wn * 32 + j * 16, 0);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) Mm::run(acc[i][j], af[i], bf[j]);
+      if (more) {
+        stA.store(s_a[cur ^ 1]);
+        stB.store(s_b[cur ^ 1]);
+      }
+      __syncthreads();
+    }
+  }
+  const int64_t mn = (int64_t)Md * Nd;
+  T* dst = nullptr;
+  float* pdst = nullptr;
+  if (nch == 1) {
+    dst = g < p.E ? (T*)p.dw_a + (int64_t)g * mn : (T*)p.dw_sh + (int64_t)(g - p.E) * mn;
+  } else {
+    pdst = p.partial + (int64_t)(loc.aux + chunk) * mn;
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + wm * 32 + i * 16 + lg * 4 + r;
+        const int n = n0 + wn * 32 + j * 16 + lc;
+        if (m < Md && n < Nd) {
+          if (dst) dst[(int64_t)m * Nd + n] = Elem<DT>::from_f(acc[i][j][r]);
+          else pdst[(int64_t)m * Nd + n] = acc[i][j][r];
+        }
+      }
+}
+
+// Sums the fp32 partials of multi-chunk groups in chunk order.  grid.y = group.
+template <int DT, int MODE>
+__global__ void __launch_bounds__(NT) dw_reduce_kernel(ExpParams p) {
+  using T = typename Elem<DT>::T;
+  const int g = blockIdx.y;
+  const int nch = dw_chunks(rows_of(p, g));
+  if (nch <= 1) return;
+  __shared__ int s_base;
+  if (threadIdx.x == 0) {
+    int base = 0;
+    for (int q = 0; q < g; ++q) {
+      const int c = dw_chunks(rows_of(p, q));
+      if (c > 1) base += c;
+    }
+    s_base = base;
+  }
+  __syncthreads();
+  const int d = p.d, H = p.H;
+  const int64_t mn = MODE == 0 ? (int64_t)d * 2 * H : (int64_t)H * d;
+  T* dst = g < p.E ? (T*)p.dw_a + (int64_t)g * mn : (T*)p.dw_sh + (int64_t)(g - p.E) * mn;
+  const float* src = p.partial + (int64_t)s_base * mn;
+  for (int64_t i = (int64_t)blockIdx.x * NT + threadIdx.x; i < mn; i += (int64_t)gridDim.x * NT) {
+    float s = 0.0f;
+    for (int c = 0; c < nch; ++c) s += src[(int64_t)c * mn + i];
+    dst[i] = Elem<DT>::from_f(s);
+  }
+}
+
+// Bias gradients: WHICH 0 -> db_in[g] = sum_r dA1[slot_r]; 1 -> db_out[g] = sum_r w_r dout[tok_r].
+template <int DT, int WHICH>
+__global__ void __launch_bounds__(NT) bias_grad_kernel(ExpParams p) {
+  using T = typename Elem<DT>::T;
+  const int g = blockIdx.y;
+  T* dst = g < p.E ? (T*)p.db : (T*)p.db_sh;
+  if (!dst) return;
+  const int ncols = WHICH == 0 ? 2 * p.H : p.d;
+  const int col = blockIdx.x * NT + threadIdx.x;
+  if (col >= ncols) return;
+  const int rows = rows_of(p, g);
+  const int64_t rs = row_start(p, g);
+  float s = 0.0f;
+  for (int r = 0; r < rows; ++r) {
+    if (WHICH == 0) {
+      s += Elem<DT>::to_f(((const T*)p.da1)[(rs + r) * ncols + col]);
+    } else {
+      int tok, pair;
+      float w;
+      row_info<DT>(p, g, rs + r, r, tok, w, pair);
+      s += w * Elem<DT>::to_f(((const T*)p.dout)[(int64_t)tok * p.d + col]);
+    }
+  }
+  dst[(int64_t)(g < p.E ? g : g - p.E) * ncols + col] = Elem<DT>::from_f(s);
+}
+
+// ============================ host side ==================================================
+
+static int elem_size(int dt) { return dt == DT_F32 ? 4 : 2; }
+
+static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+static int64_t rows_total(const nsmoe_experts_args* a) {
+  return a->l_cap + (int64_t)a->n_shared * a->n_tokens;
+}
+
+static int nbw_for(const nsmoe_experts_args* a) {
+  const int hp = (a->d_hidden + 15) / 16 * 16;
+  if (hp <= 64) return 1;
+  if (hp <= 128) return 2;
+  return 4;
+}
+
+static int validate(const nsmoe_experts_args* a) {
+  NSMOE_REQUIRE(a, "experts: NULL args");
+  NSMOE_REQUIRE(a->dtype == DT_BF16 || a->dtype == DT_F16 || a->dtype == DT_F32,
+                "experts: unknown dtype %d", a->dtype);
+  NSMOE_REQUIRE(a->activation >= 0 && a->activation <= 4, "experts: unknown activation %d",
+                a->activation);
+  NSMOE_REQUIRE(a->n_tokens >= 0 && a->d_model >= 1 && a->d_hidden >= 1 && a->n_experts >= 1 &&
+                    a->n_shared >= 0 && a->top_k >= 1 && a->top_k <= a->n_experts,
+                "experts: bad dimensions");
+  NSMOE_REQUIRE(a->d_hidden <= (a->dtype == DT_F32 ? 128 : 256),
+                "experts: d_hidden %d above the kernel limit", a->d_hidden);
+  NSMOE_REQUIRE(a->n_experts + a->n_shared <= 1024, "experts: too many groups");
+  NSMOE_REQUIRE(a->n_tokens * a->top_k < (int64_t)INT32_MAX / 2 &&
+                    rows_total(a) < (int64_t)INT32_MAX / 2,
+                "experts: too many rows");
+  NSMOE_REQUIRE(a->n_shared == 0 || (a->w_sh_in && a->w_sh_out),
+                "experts: shared weights missing");
+  return NSMOE_OK;
+}
+
+static bool aligned16(const void* q) { return ((uintptr_t)q & 15u) == 0; }
+
+static ExpParams make_params(const nsmoe_experts_args* a) {
+  ExpParams p{};
+  p.x = a->x;
+  p.w_in = a->w_in;
+  p.w_out = a->w_out;
+  p.b_in = a->b_in;
+  p.b_out = a->b_out;
+  p.w_sh_in = a->w_sh_in;
+  p.w_sh_out = a->w_sh_out;
+  p.b_sh_in = a->b_sh_in;
+  p.b_sh_out = a->b_sh_out;
+  p.topk_w = a->topk_w;
+  p.sorted_ids = a->sorted_ids;
+  p.offs = a->pad_offsets;
+  p.counts = a->counts;
+  p.T = a->n_tokens;
+  p.l_cap = a->l_cap;
+  p.d = a->d_model;
+  p.H = a->d_hidden;
+  p.E = a->n_experts;
+  p.S = a->n_shared;
+  p.k = a->top_k;
+  p.act = a->activation;
+  const int ve = 16 / elem_size(a->dtype);
+  p.fast = (a->d_model % ve == 0) && (a->d_hidden % ve == 0) && aligned16(a->x) &&
+           aligned16(a->w_in) && aligned16(a->w_out) &&
+           (a->n_shared == 0 || (aligned16(a->w_sh_in) && aligned16(a->w_sh_out)));
+  return p;
+}
+
+static int64_t fwd_grid(const nsmoe_experts_args* a) {
+  const int64_t M = a->n_tokens * a->top_k;
+  const int64_t nonempty = M < a->n_experts ? M : a->n_experts;
+  return cdiv(M, BM) + nonempty + (int64_t)a->n_shared * cdiv(a->n_tokens, BM);
+}
+
+static int64_t dw_groups_chunks(const nsmoe_experts_args* a) {
+  const int64_t M = a->n_tokens * a->top_k;
+  return a->n_experts + cdiv(M, DW_RC) + (int64_t)a->n_shared * (cdiv(a->n_tokens, DW_RC) + 1);
+}
+
+static int64_t dw_partial_chunks(const nsmoe_experts_args* a) {
+  const int64_t M = a->n_tokens * a->top_k;
+  return 2 * cdiv(M, DW_RC) + 1 + (int64_t)a->n_shared * (cdiv(a->n_tokens, DW_RC) + 1);
+}
+
+template <int DT>
+static int launch_fwd_tiles(const ExpParams& p, int nbw, int64_t grid, hipStream_t s) {
+  if (grid <= 0) return NSMOE_OK;
+  KernelTimer timer("expert_fwd", s);
+  if (nbw == 1) expert_fwd_kernel<DT, 1><<<(unsigned)grid, NT, 0, s>>>(p);
+  else if (nbw == 2) expert_fwd_kernel<DT, 2><<<(unsigned)grid, NT, 0, s>>>(p);
+  else if constexpr (DT != DT_F32) expert_fwd_kernel<DT, 4><<<(unsigned)grid, NT, 0, s>>>(p);
+  timer.stop();
+  return check_launch("expert_fwd_kernel");
+}
+
+template <int DT>
+static int launch_combine(const void* rows, const int32_t* inv, int64_t T, int d, int k, int S,
+                          int64_t l_cap, void* out, bool fast, hipStream_t s) {
+  using TT = typename Elem<DT>::T;
+  if (T <= 0) return NSMOE_OK;
+  const int ve = 16 / (int)sizeof(TT);
+  const int64_t work = fast ? T * (d / ve) : T * d;
+  int64_t blocks = cdiv(work, NT);
+  if (blocks > 65535) blocks = 65535;
+  KernelTimer timer("combine", s);
+  combine_kernel<DT><<<(unsigned)blocks, NT, 0, s>>>((const TT*)rows, inv, T, d, k, S, l_cap,
+                                                      (TT*)out, fast ? 1 : 0);
+  timer.stop();
+  return check_launch("combine_kernel");
+}
+
+template <int DT>
+static int experts_fwd_impl(const nsmoe_experts_args* a, const int32_t* inv, void* out, void* ws,
+                            hipStream_t s) {
+  ExpParams p = make_params(a);
+  p.y = ws;
+  const bool fast = p.fast && aligned16(out);
+  NSMOE_TRY(launch_fwd_tiles<DT>(p, nbw_for(a), fwd_grid(a), s));
+  return launch_combine<DT>(ws, inv, a->n_tokens, a->d_model, a->top_k, a->n_shared, a->l_cap,
+                            out, fast, s);
+}
+
+struct BwdLayout {
+  size_t da1, hbuf, dxrow, p_in, p_out, total;
+};
+
+static BwdLayout bwd_layout(const nsmoe_experts_args* a) {
+  const size_t es = elem_size(a->dtype);
+  const size_t rt = (size_t)rows_total(a);
+  const size_t d = a->d_model, H = a->d_hidden;
+  const size_t pc = (size_t)dw_partial_chunks(a);
+  BwdLayout L;
+  size_t off = 0;
+  L.da1 = off;
+  off += align256(rt * 2 * H * es);
+  L.hbuf = off;
+  off += align256(rt * H * es);
+  L.dxrow = off;
+  off += align256(rt * d * es);
+  L.p_in = off;
+  off += align256(pc * d * 2 * H * 4);
+  L.p_out = off;
+  off += align256(pc * H * d * 4);
+  L.total = off;
+  return L;
+}
+
+template <int DT>
+static int experts_bwd_impl(const nsmoe_experts_args* a, const int32_t* inv, const void* dout,
+                            const nsmoe_experts_grads* gr, char* ws, hipStream_t s) {
+  const BwdLayout L = bwd_layout(a);
+  ExpParams p = make_params(a);
+  const int nbw = nbw_for(a);
+  const int64_t grid = fwd_grid(a);
+  const int G = a->n_experts + a->n_shared;
+  p.dout = dout;
+  p.da1 = ws + L.da1;
+  p.hbuf = ws + L.hbuf;
+  p.dxrow = ws + L.dxrow;
+  p.dtw = gr->dtopk_w;
+  p.fast = p.fast && aligned16(dout);
+  if (grid > 0) {
+    KernelTimer timer("expert_bwd", s);
+    if (nbw == 1) expert_bwd_kernel<DT, 1><<<(unsigned)grid, NT, 0, s>>>(p);
+    else if (nbw == 2) expert_bwd_kernel<DT, 2><<<(unsigned)grid, NT, 0, s>>>(p);
+    else if constexpr (DT != DT_F32) expert_bwd_kernel<DT, 4><<<(unsigned)grid, NT, 0, s>>>(p);
+    timer.stop();
+    NSMOE_TRY(check_launch("expert_bwd_kernel"));
+  }
+  NSMOE_TRY(launch_combine<DT>(ws + L.dxrow, inv, a->n_tokens, a->d_model, a->top_k,
+                               a->n_shared, a->l_cap, gr->dx, p.fast && aligned16(gr->dx), s));
+
+  const int d = a->d_model, H = a->d_hidden;
+  const int64_t gc = dw_groups_chunks(a);
+  {  // dW_in
+    ExpParams q = p;
+    q.dw_a = gr->dw_in;
+    q.dw_sh = gr->dw_sh_in;
+    q.partial = (float*)(ws + L.p_in);
+    const int64_t ntiles = cdiv(d, 64) * cdiv(2 * H, 64);
+    KernelTimer timer("dw_in", s);
+    dw_kernel<DT, 0><<<(unsigned)(gc * ntiles), NT, 0, s>>>(q);
+    timer.stop();
+    NSMOE_TRY(check_launch("dw_kernel<in>"));
+    dim3 rg((unsigned)std::min<int64_t>(cdiv((int64_t)d * 2 * H, NT), 1024), (unsigned)G);
+    dw_reduce_kernel<DT, 0><<<rg, NT, 0, s>>>(q);
+    NSMOE_TRY(check_launch("dw_reduce_kernel<in>"));
+  }
+  {  // dW_out
+    ExpParams q = p;
+    q.dw_a = gr->dw_out;
+    q.dw_sh = gr->dw_sh_out;
+    q.partial = (float*)(ws + L.p_out);
+    const int64_t ntiles = cdiv(H, 64) * cdiv(d, 64);
+    KernelTimer timer("dw_out", s);
+    dw_kernel<DT, 1><<<(unsigned)(gc * ntiles), NT, 0, s>>>(q);
+    timer.stop();
+    NSMOE_TRY(check_launch("dw_kernel<out>"));
+    dim3 rg((unsigned)std::min<int64_t>(cdiv((int64_t)H * d, NT), 1024), (unsigned)G);
+    dw_reduce_kernel<DT, 1><<<rg, NT, 0, s>>>(q);
+    NSMOE_TRY(check_launch("dw_reduce_kernel<out>"));
+  }
+  if (gr->db_in || gr->db_sh_in) {
+    ExpParams q = p;
+    q.db = gr->db_in;
+    q.db_sh = gr->db_sh_in;
+    dim3 bg((unsigned)cdiv(2 * H, NT), (unsigned)G);
+    bias_grad_kernel<DT, 0><<<bg, NT, 0, s>>>(q);
+    NSMOE_TRY(check_launch("bias_grad_kernel<in>"));
+  }
+  if (gr->db_out || gr->db_sh_out) {
+    ExpParams q = p;
+    q.db = gr->db_out;
+    q.db_sh = gr->db_sh_out;
+    dim3 bg((unsigned)cdiv(d, NT), (unsigned)G);
+    bias_grad_kernel<DT, 1><<<bg, NT, 0, s>>>(q);
+    NSMOE_TRY(check_launch("bias_grad_kernel<out>"));
+  }
+  return NSMOE_OK;
+}
+
+}  // namespace nsmoe
+
+using namespace nsmoe;
+
+extern "C" size_t nsmoe_experts_fwd_workspace_size(const nsmoe_experts_args* a) {
+  if (!a) return 0;
+  return align256((size_t)rows_total(a) * a->d_model * elem_size(a->dtype));
+}
+
+extern "C" int nsmoe_experts_fwd(const nsmoe_experts_args* a, const int32_t* inv, void* out,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+  NSMOE_TRY(validate(a));
+  if (a->n_tokens == 0) return NSMOE_OK;
+  NSMOE_REQUIRE(a->x && a->w_in && a->w_out && a->topk_w && a->sorted_ids && a->pad_offsets &&
+                    a->counts && inv && out, "experts_fwd: NULL pointer");
+  const size_t need = nsmoe_experts_fwd_workspace_size(a);
+  if (workspace_bytes < need || !workspace) {
+    set_error("experts_fwd: workspace %zu B < %zu B", workspace_bytes, need);
+    return NSMOE_EWORKSPACE;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  switch (a->dtype) {
+    case DT_BF16: return experts_fwd_impl<DT_BF16>(a, inv, out, workspace, s);
+    case DT_F16: return experts_fwd_impl<DT_F16>(a, inv, out, workspace, s);
+    default: return experts_fwd_impl<DT_F32>(a, inv, out, workspace, s);
+  }
+}
+
+extern "C" size_t nsmoe_experts_bwd_workspace_size(const nsmoe_experts_args* a) {
+  if (!a) return 0;
+  return bwd_layout(a).total;
+}
+
+extern "C" int nsmoe_experts_bwd(const nsmoe_experts_args* a, const int32_t* inv,
+                                 const void* grad_out, const nsmoe_experts_grads* grads,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+  NSMOE_TRY(validate(a));
+  NSMOE_REQUIRE(grads, "experts_bwd: NULL grads");
+  if (a->n_tokens == 0) return NSMOE_OK;
+  NSMOE_REQUIRE(a->x && a->w_in && a->w_out && a->topk_w && a->sorted_ids && a->pad_offsets &&
+                    a->counts && inv && grad_out && grads->dx && grads->dw_in &&
+                    grads->dw_out && grads->dtopk_w,
+                "experts_bwd: NULL pointer");
+  NSMOE_REQUIRE(a->n_shared == 0 || (grads->dw_sh_in && grads->dw_sh_out),
+                "experts_bwd: shared weight gradients missing");
+  const size_t need = bwd_layout(a).total;
+  if (workspace_bytes < need || !workspace) {
+    set_error("experts_bwd: workspace %zu B < %zu B", workspace_bytes, need);
+    return NSMOE_EWORKSPACE;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  switch (a->dtype) {
+    case DT_BF16:
+      return experts_bwd_impl<DT_BF16>(a, inv, grad_out, grads, (char*)workspace, s);
+    case DT_F16:
+      return experts_bwd_impl<DT_F16>(a, inv, grad_out, grads, (char*)workspace, s);
+    default:
+      return experts_bwd_impl<DT_F32>(a, inv, grad_out, grads, (char*)workspace, s);
+  }
+}

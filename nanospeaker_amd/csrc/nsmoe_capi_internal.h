@@ -1,0 +1,67 @@
+// Host-side plumbing shared by the C-ABI entry points: error strings, launch checks and
+// a launch counter the tests read to prove the HIP path ran.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include <atomic>
+#include <string>
+
+namespace nsmoe {
+
+enum Status : int { NSMOE_OK = 0, NSMOE_EINVAL = 1, NSMOE_EHIP = 2, NSMOE_EWORKSPACE = 3 };
+
+void set_error(const char* fmt, ...);
+void note_launch();
+
+// Checks the launch that was just enqueued; records an error string on failure.
+inline int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("%s: %s", what, hipGetErrorString(e));
+    return NSMOE_EHIP;
+  }
+  note_launch();
+  return NSMOE_OK;
+}
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace nsmoe
+
+#define NSMOE_REQUIRE(cond, ...)          \
+  do {                                    \
+    if (!(cond)) {                        \
+      ::nsmoe::set_error(__VA_ARGS__);    \
+      return ::nsmoe::NSMOE_EINVAL;       \
+    }                                     \
+  } while (0)
+
+#define NSMOE_TRY(expr)                   \
+  do {                                    \
+    int _rc = (expr);                     \
+    if (_rc != 0) return _rc;             \
+  } while (0)
+
+namespace nsmoe {
+// dst[0, n) = value, as a kernel (graph-capture safe, unlike hipMemsetAsync).
+int fill_i32(int32_t* dst, int64_t n, int32_t value, hipStream_t stream);
+}  // namespace nsmoe
+
+namespace nsmoe {
+// Optional per-kernel timing with HIP events recorded on the launch stream (enabled by
+// nsmoe_timing_enable; used by the benchmark to time its dominant kernel live).
+// KernelTimer brackets one launch: construct before the launch, stop() after it.
+class KernelTimer {
+ public:
+  KernelTimer(const char* name, hipStream_t stream);
+  void stop();
+
+ private:
+  int slot_;
+  hipStream_t stream_;
+};
+}  // namespace nsmoe

@@ -1,0 +1,491 @@
+"""
+HIP (gfx950) dispatch for MoEBlock's dropless path: the drop-in for the reference's
+Triton module src/model/moe_kernel.py.
+
+Same public surface as the reference module -- `ALIGN_M`, `KERNEL_ACTIVATIONS`,
+`KERNEL_DTYPES`, `kernel_supported`, `fused_moe_forward`, and the custom ops
+`moe_dispatch`, `moe_experts` (with its autograd) and `moe_experts_bwd` with the
+reference's schemas (moe_kernel.py:180-218, 558-780, 785-803) -- plus the ops this build
+adds around them:
+
+  * `route` / `route_bwd`: the softmax / top-k / renormalise tail of TopKRouter.forward
+    (src/model/router.py:79-98) and its backward, with CPU torch.topk's tie order;
+  * `moe_block` / `moe_block_bwd`: routed *and* shared experts (MoEBlock._shared,
+    src/model/moe.py:310-329) in one grouped launch.
+
+Every op enqueues on torch's current stream through the C ABI in include/nsmoe.h
+(`_native`); buffers come from torch's caching allocator; nothing syncs with the host.
+There is no fallback: on a GPU tensor a missing library raises.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+from torch import Tensor
+
+from . import _native as nat
+
+# Each expert's run of dispatch slots is padded to a multiple of ALIGN_M.  The grouped
+# GEMMs schedule 64-row tiles per expert on device, so the alignment only has to keep
+# the padding small (decode-sized batches would waste most of a 128-row alignment).
+ALIGN_M = 16
+
+# Gate activations the kernels implement (ids as in the reference, moe_kernel.py:75).
+KERNEL_ACTIVATIONS = {"silu": 0, "swish": 0, "gelu": 1, "relu": 2, "sigmoid": 3, "tanh": 4}
+
+# MFMA input types on gfx950 (bf16 / fp16 16x16x32, fp32 16x16x4); fp64 stays eager.
+KERNEL_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
+
+# Shape limits of the HIP kernels (include/nsmoe.h).
+ROUTE_MAX_EXPERTS = 128
+DISPATCH_MAX_EXPERTS = 1024
+MAX_GROUPS = 1024
+
+_DT = {torch.bfloat16: nat.BF16, torch.float16: nat.F16, torch.float32: nat.F32}
+
+
+def kernel_supported(t: Tensor) -> bool:
+    """
+    Whether the fused path takes tensors like this one (device and dtype).  On a GPU
+    tensor of a supported dtype the native library must load: a missing build raises
+    instead of quietly handing the block to a slower path (moe_kernel.py:81-90 is the
+    reference predicate).
+    """
+    if not (t.is_cuda and t.dtype in KERNEL_DTYPES):
+        return False
+    nat.lib()
+    return True
+
+
+def shape_supported(n_experts: int, n_shared: int, d_hidden: int, dtype: torch.dtype) -> bool:
+    """Whether a block of this shape fits the kernels' limits."""
+    max_hidden = 128 if dtype == torch.float32 else 256
+    return (n_experts <= DISPATCH_MAX_EXPERTS and n_experts + n_shared <= MAX_GROUPS
+            and d_hidden <= max_hidden)
+
+
+def _l_cap(m: int, n_experts: int) -> int:
+    """Host worst case for the padded slot count (reference: moe_kernel.py:100-108)."""
+    if m <= 0:
+        return 0
+    return -(-(m + min(n_experts, m) * (ALIGN_M - 1)) // ALIGN_M) * ALIGN_M
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _p(t: Optional[Tensor]) -> Optional[int]:
+    return None if t is None or t.numel() == 0 else t.data_ptr()
+
+
+def _ws(nbytes: int, device) -> Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+# ---------------------------------------------------------------------------------------
+# router tail
+# ---------------------------------------------------------------------------------------
+
+def _route_flags(want_probs: bool, normalize: bool) -> int:
+    return (nat.ROUTE_PROBS if want_probs else 0) | (nat.ROUTE_NORMALIZE if normalize else 0)
+
+
+@torch.library.custom_op("nsmoe::route", mutates_args=())
+def route(logits: Tensor, top_k: int, want_probs: bool, normalize: bool,
+          w_dtype: int) -> tuple[Tensor, Tensor, Tensor]:
+    """
+    fp32 logits [T, E] -> (topk_w [T, k] in the dtype coded by w_dtype, topk_idx [T, k]
+    int64, probs [T, E] fp32 -- or an empty tensor when want_probs is False).
+    """
+    logits = logits.contiguous()
+    n, e = logits.shape
+    dtype = {v: k for k, v in _DT.items()}[w_dtype]
+    w = torch.empty((n, top_k), dtype=dtype, device=logits.device)
+    idx = torch.empty((n, top_k), dtype=torch.int64, device=logits.device)
+    probs = torch.empty((n, e) if want_probs else (0,), dtype=torch.float32, device=logits.device)
+    if n:
+        nat.check(nat.lib().nsmoe_route_fwd(
+            logits.data_ptr(), n, e, top_k, _route_flags(want_probs, normalize), w_dtype,
+            w.data_ptr(), idx.data_ptr(), _p(probs), _stream()), "nsmoe_route_fwd")
+    return w, idx, probs
+
+
+@route.register_fake
+def _(logits, top_k, want_probs, normalize, w_dtype):
+    n, e = logits.shape
+    dtype = {v: k for k, v in _DT.items()}[w_dtype]
+    return (logits.new_empty((n, top_k), dtype=dtype),
+            logits.new_empty((n, top_k), dtype=torch.int64),
+            logits.new_empty((n, e) if want_probs else (0,), dtype=torch.float32))
+
+
+@torch.library.custom_op("nsmoe::route_bwd", mutates_args=())
+def route_bwd(src: Tensor, topk_idx: Tensor, grad_w: Tensor, grad_probs: Optional[Tensor],
+              want_probs: bool, normalize: bool) -> Tensor:
+    """d(logits) [T, E] fp32; `src` is the forward's probs (train branch) or logits."""
+    src = src.contiguous()
+    n, e = src.shape
+    k = topk_idx.shape[1]
+    grad_w = grad_w.contiguous()
+    gp = grad_probs.contiguous() if grad_probs is not None else None
+    out = torch.empty((n, e), dtype=torch.float32, device=src.device)
+    if n:
+        nat.check(nat.lib().nsmoe_route_bwd(
+            src.data_ptr(), topk_idx.contiguous().data_ptr(), grad_w.data_ptr(),
+            _DT[grad_w.dtype], _p(gp), n, e, k, _route_flags(want_probs, normalize),
+            out.data_ptr(), _stream()), "nsmoe_route_bwd")
+    return out
+
+
+@route_bwd.register_fake
+def _(src, topk_idx, grad_w, grad_probs, want_probs, normalize):
+    return torch.empty_like(src, dtype=torch.float32)
+
+
+def _route_setup(ctx, inputs, output):
+    logits, top_k, want_probs, normalize, w_dtype = inputs
+    w, idx, probs = output
+    ctx.want_probs, ctx.normalize = want_probs, normalize
+    ctx.w_dtype = w.dtype
+    ctx.mark_non_differentiable(idx)
+    ctx.save_for_backward(probs if want_probs else logits, idx)
+
+
+def _route_backward(ctx, grad_w, grad_idx, grad_probs):
+    src, idx = ctx.saved_tensors
+    if grad_w is None and grad_probs is None:
+        return None, None, None, None, None
+    if grad_w is None:
+        grad_w = torch.zeros(idx.shape, dtype=ctx.w_dtype, device=idx.device)
+    if not ctx.want_probs:
+        grad_probs = None
+    dl = route_bwd(src, idx, grad_w.to(ctx.w_dtype), grad_probs, ctx.want_probs, ctx.normalize)
+    return dl, None, None, None, None
+
+
+route.register_autograd(_route_backward, setup_context=_route_setup)
+
+
+def route_dtype_code(dtype: torch.dtype) -> int:
+    return _DT[dtype]
+
+
+# ---------------------------------------------------------------------------------------
+# dispatch (reference schema: moe_kernel.py:180-218)
+# ---------------------------------------------------------------------------------------
+
+@torch.library.custom_op("nsmoe::moe_dispatch", mutates_args=())
+def moe_dispatch(topk_idx: Tensor, n_experts: int) -> tuple[
+        Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """
+    Stable counting sort of the (token, expert) pairs into ALIGN_M-padded expert runs.
+
+    Returns int32 tensors: sorted pair ids [l_cap] (sentinel M in pad slots),
+    aligned-block -> expert map [l_cap / ALIGN_M], run offsets [E + 1], routing counts
+    [E], the padded total [1] and the inverse pair -> slot [M].  Inside each run the
+    pairs are in increasing pair id -- the order of `topk_idx.flatten().sort(stable=True)`
+    (moe.py:220) -- so the permutation is deterministic and bit-exact.
+    """
+    flat = topk_idx.reshape(-1).contiguous().to(torch.int64)
+    m = flat.numel()
+    dev, i32 = topk_idx.device, torch.int32
+    l_cap = _l_cap(m, n_experts)
+    sids = torch.empty(l_cap, dtype=i32, device=dev)
+    eids = torch.empty(l_cap // ALIGN_M, dtype=i32, device=dev)
+    offs = torch.empty(n_experts + 1, dtype=i32, device=dev)
+    counts = torch.empty(n_experts, dtype=i32, device=dev)
+    npp = torch.empty(1, dtype=i32, device=dev)
+    inv = torch.empty(m, dtype=i32, device=dev)
+    lib = nat.lib()
+    ws = _ws(lib.nsmoe_dispatch_workspace_size(m, n_experts), dev)
+    nat.check(lib.nsmoe_dispatch(
+        _p(flat), m, n_experts, _p(sids), _p(eids), offs.data_ptr(), counts.data_ptr(),
+        npp.data_ptr(), _p(inv), ws.data_ptr(), ws.numel(), _stream()), "nsmoe_dispatch")
+    return sids, eids, offs, counts, npp, inv
+
+
+@moe_dispatch.register_fake
+def _(topk_idx, n_experts):
+    l_cap = _l_cap(topk_idx.numel(), n_experts)
+    mk = lambda n: topk_idx.new_empty((n,), dtype=torch.int32)
+    return (mk(l_cap), mk(l_cap // ALIGN_M), mk(n_experts + 1), mk(n_experts), mk(1),
+            mk(topk_idx.numel()))
+
+
+# ---------------------------------------------------------------------------------------
+# experts
+# ---------------------------------------------------------------------------------------
+
+def _args(x, w_in, w_out, topk_w, b_in, b_out, w_sh_in, w_sh_out, b_sh_in, b_sh_out,
+          sorted_ids, pad_offsets, counts, activation) -> nat.ExpertsArgs:
+    n, d = x.shape
+    return nat.ExpertsArgs(
+        dtype=_DT[x.dtype], activation=KERNEL_ACTIVATIONS[activation], n_tokens=n,
+        d_model=d, d_hidden=w_in.shape[2] // 2, n_experts=w_in.shape[0],
+        n_shared=0 if w_sh_in is None else w_sh_in.shape[0], top_k=topk_w.shape[-1],
+        reserved0=0, l_cap=sorted_ids.numel(),
+        x=_p(x), w_in=_p(w_in), w_out=_p(w_out), b_in=_p(b_in), b_out=_p(b_out),
+        w_sh_in=_p(w_sh_in), w_sh_out=_p(w_sh_out), b_sh_in=_p(b_sh_in), b_sh_out=_p(b_sh_out),
+        topk_w=_p(topk_w), sorted_ids=_p(sorted_ids), pad_offsets=_p(pad_offsets),
+        counts=_p(counts))
+
+
+def _c(t: Optional[Tensor]) -> Optional[Tensor]:
+    return None if t is None else t.contiguous()
+
+
+def _check_activation(activation: str) -> None:
+    if activation not in KERNEL_ACTIVATIONS:
+        raise ValueError(
+            f"activation {activation!r} has no kernel; use one of "
+            f"{sorted(set(KERNEL_ACTIVATIONS))} or fall back to the eager path.")
+
+
+def _experts_forward(x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out,
+                     topk_w, sorted_ids, pad_offsets, counts, inv_ids, activation):
+    x, w_in, w_out = x.contiguous(), w_in.contiguous(), w_out.contiguous()
+    w_sh_in, w_sh_out = _c(w_sh_in), _c(w_sh_out)
+    b_in, b_out, b_sh_in, b_sh_out = _c(b_in), _c(b_out), _c(b_sh_in), _c(b_sh_out)
+    topk_w = topk_w.reshape(x.shape[0], -1).contiguous()
+    n, d = x.shape
+    out = torch.empty((n, d), dtype=x.dtype, device=x.device)
+    if n == 0:
+        return out
+    args = _args(x, w_in, w_out, topk_w, b_in, b_out, w_sh_in, w_sh_out, b_sh_in, b_sh_out,
+                 sorted_ids, pad_offsets, counts, activation)
+    lib = nat.lib()
+    ws = _ws(lib.nsmoe_experts_fwd_workspace_size(args), x.device)
+    nat.check(lib.nsmoe_experts_fwd(args, _p(inv_ids), out.data_ptr(), ws.data_ptr(),
+                                    ws.numel(), _stream()), "nsmoe_experts_fwd")
+    return out
+
+
+def _experts_backward(grad_out, x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in,
+                      topk_w, sorted_ids, pad_offsets, counts, inv_ids, activation,
+                      need_db_in, need_db_out, need_db_sh_in, need_db_sh_out):
+    grad_out = grad_out.to(x.dtype).contiguous()
+    x, w_in, w_out = x.contiguous(), w_in.contiguous(), w_out.contiguous()
+    w_sh_in, w_sh_out = _c(w_sh_in), _c(w_sh_out)
+    b_in, b_out, b_sh_in = _c(b_in), _c(b_out), _c(b_sh_in)
+    tw = topk_w.reshape(x.shape[0], -1).contiguous()
+    n, d = x.shape
+    e, _, h2 = w_in.shape
+    s = 0 if w_sh_in is None else w_sh_in.shape[0]
+    dev, dt = x.device, x.dtype
+    dx = torch.empty_like(x)
+    dw_in, dw_out = torch.empty_like(w_in), torch.empty_like(w_out)
+    dw_sh_in = torch.empty_like(w_sh_in) if s else x.new_empty(0)
+    dw_sh_out = torch.empty_like(w_sh_out) if s else x.new_empty(0)
+    dtw = torch.empty(topk_w.shape, dtype=tw.dtype, device=dev)
+    db_in = torch.empty((e, h2), dtype=dt, device=dev) if need_db_in else x.new_empty(0)
+    db_out = torch.empty((e, d), dtype=dt, device=dev) if need_db_out else x.new_empty(0)
+    db_sh_in = torch.empty((s, h2), dtype=dt, device=dev) if need_db_sh_in else x.new_empty(0)
+    db_sh_out = torch.empty((s, d), dtype=dt, device=dev) if need_db_sh_out else x.new_empty(0)
+    if n == 0:
+        dw_in.zero_(), dw_out.zero_(), dtw.zero_()
+        for t in (dw_sh_in, dw_sh_out, db_in, db_out, db_sh_in, db_sh_out):
+            t.zero_()
+        return dx, dw_in, dw_out, dw_sh_in, dw_sh_out, dtw, db_in, db_out, db_sh_in, db_sh_out
+    args = _args(x, w_in, w_out, tw, b_in, b_out, w_sh_in, w_sh_out, b_sh_in, None,
+                 sorted_ids, pad_offsets, counts, activation)
+    grads = nat.ExpertsGrads(
+        dx=_p(dx), dw_in=_p(dw_in), dw_out=_p(dw_out), dw_sh_in=_p(dw_sh_in),
+        dw_sh_out=_p(dw_sh_out), dtopk_w=_p(dtw), db_in=_p(db_in), db_out=_p(db_out),
+        db_sh_in=_p(db_sh_in), db_sh_out=_p(db_sh_out))
+    lib = nat.lib()
+    ws = _ws(lib.nsmoe_experts_bwd_workspace_size(args), dev)
+    nat.check(lib.nsmoe_experts_bwd(args, _p(inv_ids), grad_out.data_ptr(), grads,
+                                    ws.data_ptr(), ws.numel(), _stream()), "nsmoe_experts_bwd")
+    return dx, dw_in, dw_out, dw_sh_in, dw_sh_out, dtw, db_in, db_out, db_sh_in, db_sh_out
+
+
+# ---- reference schema: routed experts only (moe_kernel.py:558-780) ----------------------
+
+@torch.library.custom_op("nsmoe::moe_experts", mutates_args=())
+def moe_experts(x: Tensor, w_in: Tensor, w_out: Tensor, topk_w: Tensor,
+                b_in: Optional[Tensor], b_out: Optional[Tensor], sorted_ids: Tensor,
+                expert_ids: Tensor, pad_offsets: Tensor, counts: Tensor, n_post_pad: Tensor,
+                inv_ids: Tensor, activation: str) -> Tensor:
+    """The routed experts on pre-dispatched pairs: out[t] = sum_j w * expert_j(x[t])."""
+    return _experts_forward(x, w_in, w_out, None, None, b_in, b_out, None, None, topk_w,
+                            sorted_ids, pad_offsets, counts, inv_ids, activation)
+
+
+@moe_experts.register_fake
+def _(x, w_in, w_out, topk_w, b_in, b_out, sorted_ids, expert_ids, pad_offsets, counts,
+      n_post_pad, inv_ids, activation):
+    return x.new_empty(x.shape)
+
+
+@torch.library.custom_op("nsmoe::moe_experts_bwd", mutates_args=())
+def moe_experts_bwd(grad_out: Tensor, x: Tensor, w_in: Tensor, w_out: Tensor, topk_w: Tensor,
+                    b_in: Optional[Tensor], sorted_ids: Tensor, expert_ids: Tensor,
+                    pad_offsets: Tensor, counts: Tensor, n_post_pad: Tensor, inv_ids: Tensor,
+                    activation: str, need_db_in: bool, need_db_out: bool,
+                    b_out: Optional[Tensor] = None
+                    ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """
+    (dx, dW_in, dW_out, dtopk_w, db_in, db_out); unneeded bias grads come back empty.
+    The reference schema plus a trailing optional b_out: dtopk_w then includes the
+    <grad_out, b_out> term of d((h W_out + b_out) * w) / dw.
+    """
+    r = _experts_backward(grad_out, x, w_in, w_out, None, None, b_in, b_out, None, topk_w,
+                          sorted_ids, pad_offsets, counts, inv_ids, activation,
+                          need_db_in, need_db_out, False, False)
+    dx, dw_in, dw_out, _, _, dtw, db_in, db_out, _, _ = r
+    return dx, dw_in, dw_out, dtw, db_in, db_out
+
+
+@moe_experts_bwd.register_fake
+def _(grad_out, x, w_in, w_out, topk_w, b_in, sorted_ids, expert_ids, pad_offsets, counts,
+      n_post_pad, inv_ids, activation, need_db_in, need_db_out, b_out=None):
+    e_n, _, h2 = w_in.shape
+    return (torch.empty_like(x), torch.empty_like(w_in), torch.empty_like(w_out),
+            torch.empty_like(topk_w),
+            x.new_empty((e_n, h2)) if need_db_in else x.new_empty(0),
+            x.new_empty((e_n, x.shape[1])) if need_db_out else x.new_empty(0))
+
+
+def _moe_experts_setup(ctx, inputs, output):
+    (x, w_in, w_out, topk_w, b_in, b_out, sorted_ids, expert_ids, pad_offsets,
+     counts, n_post_pad, inv_ids, activation) = inputs
+    saved = [x, w_in, w_out, topk_w, sorted_ids, expert_ids, pad_offsets, counts,
+             n_post_pad, inv_ids]
+    saved += [t for t in (b_in, b_out) if t is not None]
+    ctx.save_for_backward(*saved)
+    ctx.has_b_in, ctx.has_b_out = b_in is not None, b_out is not None
+    ctx.activation = activation
+
+
+def _moe_experts_backward(ctx, grad_out):
+    (x, w_in, w_out, topk_w, sorted_ids, expert_ids, pad_offsets, counts,
+     n_post_pad, inv_ids, *rest) = ctx.saved_tensors
+    it = iter(rest)
+    b_in = next(it) if ctx.has_b_in else None
+    b_out = next(it) if ctx.has_b_out else None
+    dx, dw_in, dw_out, dtw, db_in, db_out = moe_experts_bwd(
+        grad_out, x, w_in, w_out, topk_w, b_in, sorted_ids, expert_ids, pad_offsets,
+        counts, n_post_pad, inv_ids, ctx.activation, ctx.has_b_in, ctx.has_b_out, b_out)
+    return (dx, dw_in, dw_out, dtw, db_in if ctx.has_b_in else None,
+            db_out if ctx.has_b_out else None, None, None, None, None, None, None, None)
+
+
+moe_experts.register_autograd(_moe_experts_backward, setup_context=_moe_experts_setup)
+
+
+# ---- routed + shared experts in one grouped launch ----------------------------------------
+
+@torch.library.custom_op("nsmoe::moe_block", mutates_args=())
+def moe_block(x: Tensor, w_in: Tensor, w_out: Tensor, w_sh_in: Optional[Tensor],
+              w_sh_out: Optional[Tensor], b_in: Optional[Tensor], b_out: Optional[Tensor],
+              b_sh_in: Optional[Tensor], b_sh_out: Optional[Tensor], topk_w: Tensor,
+              sorted_ids: Tensor, pad_offsets: Tensor, counts: Tensor, inv_ids: Tensor,
+              activation: str) -> Tensor:
+    """Routed plus shared experts: out[t] = sum_j w_tj * expert_j(x[t]) + sum_s shared_s(x[t])."""
+    return _experts_forward(x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in,
+                            b_sh_out, topk_w, sorted_ids, pad_offsets, counts, inv_ids,
+                            activation)
+
+
+@moe_block.register_fake
+def _(x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out, topk_w, sorted_ids,
+      pad_offsets, counts, inv_ids, activation):
+    return x.new_empty(x.shape)
+
+
+@torch.library.custom_op("nsmoe::moe_block_bwd", mutates_args=())
+def moe_block_bwd(grad_out: Tensor, x: Tensor, w_in: Tensor, w_out: Tensor,
+                  w_sh_in: Optional[Tensor], w_sh_out: Optional[Tensor],
+                  b_in: Optional[Tensor], b_out: Optional[Tensor], b_sh_in: Optional[Tensor],
+                  topk_w: Tensor, sorted_ids: Tensor, pad_offsets: Tensor, counts: Tensor,
+                  inv_ids: Tensor, activation: str, need_db_in: bool, need_db_out: bool,
+                  need_db_sh_in: bool, need_db_sh_out: bool) -> tuple[
+                      Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor,
+                      Tensor]:
+    """(dx, dW_in, dW_out, dW_sh_in, dW_sh_out, dtopk_w, db_in, db_out, db_sh_in, db_sh_out)."""
+    return _experts_backward(grad_out, x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in,
+                             topk_w, sorted_ids, pad_offsets, counts, inv_ids, activation,
+                             need_db_in, need_db_out, need_db_sh_in, need_db_sh_out)
+
+
+@moe_block_bwd.register_fake
+def _(grad_out, x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, topk_w, sorted_ids,
+      pad_offsets, counts, inv_ids, activation, need_db_in, need_db_out, need_db_sh_in,
+      need_db_sh_out):
+    e, d, h2 = w_in.shape
+    s = 0 if w_sh_in is None else w_sh_in.shape[0]
+    emp = x.new_empty(0)
+    return (torch.empty_like(x), torch.empty_like(w_in), torch.empty_like(w_out),
+            torch.empty_like(w_sh_in) if s else emp, torch.empty_like(w_sh_out) if s else emp,
+            torch.empty_like(topk_w),
+            x.new_empty((e, h2)) if need_db_in else emp,
+            x.new_empty((e, d)) if need_db_out else emp,
+            x.new_empty((s, h2)) if need_db_sh_in else emp,
+            x.new_empty((s, d)) if need_db_sh_out else emp)
+
+
+def _moe_block_setup(ctx, inputs, output):
+    (x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out, topk_w, sorted_ids,
+     pad_offsets, counts, inv_ids, activation) = inputs
+    ctx.has = [t is not None for t in (w_sh_in, b_in, b_out, b_sh_in, b_sh_out)]
+    opt = [t for t in (w_sh_in, w_sh_out, b_in, b_out, b_sh_in) if t is not None]
+    ctx.save_for_backward(x, w_in, w_out, topk_w, sorted_ids, pad_offsets, counts, inv_ids,
+                          *opt)
+    ctx.activation = activation
+
+
+def _moe_block_backward(ctx, grad_out):
+    (x, w_in, w_out, topk_w, sorted_ids, pad_offsets, counts, inv_ids, *opt) = ctx.saved_tensors
+    has_sh, has_b_in, has_b_out, has_b_sh_in, has_b_sh_out = ctx.has
+    it = iter(opt)
+    w_sh_in = next(it) if has_sh else None
+    w_sh_out = next(it) if has_sh else None
+    b_in = next(it) if has_b_in else None
+    b_out = next(it) if has_b_out else None
+    b_sh_in = next(it) if has_b_sh_in else None
+    (dx, dw_in, dw_out, dw_sh_in, dw_sh_out, dtw, db_in, db_out, db_sh_in,
+     db_sh_out) = moe_block_bwd(grad_out, x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out,
+                                b_sh_in, topk_w, sorted_ids, pad_offsets, counts, inv_ids,
+                                ctx.activation, has_b_in, has_b_out, has_b_sh_in,
+                                has_b_sh_out)
+    return (dx, dw_in, dw_out,
+            dw_sh_in if has_sh else None, dw_sh_out if has_sh else None,
+            db_in if has_b_in else None, db_out if has_b_out else None,
+            db_sh_in if has_b_sh_in else None, db_sh_out if has_b_sh_out else None,
+            dtw, None, None, None, None, None)
+
+
+moe_block.register_autograd(_moe_block_backward, setup_context=_moe_block_setup)
+
+
+# ---------------------------------------------------------------------------------------
+# entry points for MoEBlock
+# ---------------------------------------------------------------------------------------
+
+def fused_moe_forward(x, w_in, w_out, topk_w, topk_idx, b_in, b_out, activation):
+    """
+    Dispatch + routed experts; returns (out [N, d_model], counts [n_experts] int32), as
+    the reference's entry point (moe_kernel.py:785-803).  Params are cast to x's dtype,
+    as autocast would run the eager matmuls.
+    """
+    _check_activation(activation)
+    sids, eids, offs, counts, npp, inv = moe_dispatch(topk_idx, w_in.shape[0])
+    cast = lambda t: None if t is None else t.to(x.dtype)
+    out = moe_experts(x, cast(w_in), cast(w_out), topk_w.to(x.dtype), cast(b_in),
+                      cast(b_out), sids, eids, offs, counts, npp, inv, activation)
+    return out, counts
+
+
+def fused_moe_block_forward(x, w_in, w_out, topk_w, topk_idx, b_in, b_out, w_sh_in,
+                            w_sh_out, b_sh_in, b_sh_out, activation):
+    """fused_moe_forward with the shared experts folded into the same grouped launch."""
+    _check_activation(activation)
+    sids, eids, offs, counts, npp, inv = moe_dispatch(topk_idx, w_in.shape[0])
+    cast = lambda t: None if t is None else t.to(x.dtype)
+    out = moe_block(x, cast(w_in), cast(w_out), cast(w_sh_in), cast(w_sh_out), cast(b_in),
+                    cast(b_out), cast(b_sh_in), cast(b_sh_out), topk_w.to(x.dtype), sids,
+                    offs, counts, inv, activation)
+    return out, counts

@@ -1,0 +1,121 @@
+"""
+The C-ABI boundary without a GPU: libnsmoe.so loads, exports every function that
+include/nsmoe.h declares, agrees with the Python mirror on the layout of its argument
+structs and on the dispatch size formulas, and rejects bad arguments with an error
+string before launching anything.
+"""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from nanospeaker_amd import _native as nat
+from nanospeaker_amd import moe_kernel as mk
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "nsmoe.h"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(nsmoe_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = nat.lib()
+    names = declared_functions()
+    assert len(names) >= 14
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in nsmoe.h but not exported"
+        assert name in nat.SIGNATURES, f"{name} has no ctypes signature"
+
+
+def test_struct_layouts_match_the_header():
+    # nsmoe_experts_args: 2 x i32, i64, 6 x i32, i64, then 13 pointers
+    assert ctypes.sizeof(nat.ExpertsArgs) == 4 * 2 + 8 + 4 * 6 + 8 + 8 * 13
+    assert nat.ExpertsArgs.x.offset == 48
+    assert ctypes.sizeof(nat.ExpertsGrads) == 8 * 10
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    body = text[text.index("typedef struct nsmoe_experts_args"):text.index("} nsmoe_experts_args")]
+    fields = re.findall(r"\b(\w+);", body)
+    assert fields == [f for f, _ in nat.ExpertsArgs._fields_]
+
+
+def test_abi_version_and_alignment():
+    assert nat.lib().nsmoe_abi_version() == 1
+    assert nat.lib().nsmoe_align_m() == mk.ALIGN_M
+
+
+@pytest.mark.parametrize("m,e", [(0, 8), (1, 8), (49152, 76), (384, 76), (100, 1000), (15, 8)])
+def test_l_cap_matches_python(m, e):
+    assert nat.lib().nsmoe_dispatch_l_cap(m, e) == mk._l_cap(m, e)
+
+
+def test_workspace_sizes_are_positive_and_grow():
+    a = nat.ExpertsArgs(dtype=0, activation=0, n_tokens=8192, d_model=576, d_hidden=128,
+                        n_experts=76, n_shared=2, top_k=6, l_cap=mk._l_cap(49152, 76))
+    fwd = nat.lib().nsmoe_experts_fwd_workspace_size(a)
+    bwd = nat.lib().nsmoe_experts_bwd_workspace_size(a)
+    assert fwd >= (49152 + 2 * 8192) * 576 * 2
+    assert bwd > fwd
+    assert nat.lib().nsmoe_dispatch_workspace_size(49152, 76) == 192 * 76 * 4
+
+
+@pytest.mark.parametrize("call,needle", [
+    (lambda L: L.nsmoe_route_fwd(None, 4, 0, 1, 0, 0, None, None, None, None), "n_experts"),
+    (lambda L: L.nsmoe_route_fwd(None, 4, 300, 1, 0, 0, None, None, None, None), "n_experts"),
+    (lambda L: L.nsmoe_route_fwd(None, 4, 8, 9, 0, 0, None, None, None, None), "top_k"),
+    (lambda L: L.nsmoe_route_fwd(None, 4, 8, 2, 1, 0, None, None, None, None), "probs"),
+    (lambda L: L.nsmoe_route_bwd(None, None, None, 0, None, 4, 8, 0, 0, None, None), "top_k"),
+    (lambda L: L.nsmoe_dispatch(None, -1, 8, None, None, None, None, None, None, None, 0, None),
+     "n_pairs"),
+    (lambda L: L.nsmoe_dispatch(None, 10, 0, None, None, None, None, None, None, None, 0, None),
+     "n_experts"),
+])
+def test_bad_arguments_are_rejected_with_a_message(call, needle):
+    lib = nat.lib()
+    rc = call(lib)
+    assert rc == 1
+    assert needle in lib.nsmoe_last_error().decode()
+
+
+def test_dispatch_workspace_too_small_is_an_error():
+    lib = nat.lib()
+    rc = lib.nsmoe_dispatch(1, 100, 8, 1, 1, 1, 1, 1, 1, 1, 4, None)
+    assert rc == 3 and "workspace" in lib.nsmoe_last_error().decode()
+
+
+def test_experts_argument_validation():
+    lib = nat.lib()
+    bad = nat.ExpertsArgs(dtype=7, activation=0, n_tokens=1, d_model=8, d_hidden=8,
+                          n_experts=2, n_shared=0, top_k=1, l_cap=16)
+    assert lib.nsmoe_experts_fwd(bad, None, None, None, 0, None) == 1
+    assert "dtype" in lib.nsmoe_last_error().decode()
+    big = nat.ExpertsArgs(dtype=2, activation=0, n_tokens=1, d_model=8, d_hidden=200,
+                          n_experts=2, n_shared=0, top_k=1, l_cap=16)
+    assert lib.nsmoe_experts_fwd(big, None, None, None, 0, None) == 1
+    assert "d_hidden" in lib.nsmoe_last_error().decode()
+    empty = nat.ExpertsArgs(dtype=0, activation=0, n_tokens=0, d_model=8, d_hidden=8,
+                            n_experts=2, n_shared=0, top_k=1, l_cap=0)
+    assert lib.nsmoe_experts_fwd(empty, None, None, None, 0, None) == 0
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(nat, "_LIB", None)
+    monkeypatch.setattr(nat, "LIB_PATH", tmp_path / "missing.so")
+    with pytest.raises(nat.NativeLibraryError):
+        nat.lib()
+    assert not nat.available()
+
+
+def test_kernel_supported_raises_on_a_gpu_tensor_without_the_library(monkeypatch, tmp_path):
+    """A GPU tensor never silently falls back: the missing build is an error."""
+    class FakeCuda:
+        is_cuda = True
+        dtype = __import__("torch").bfloat16
+
+    monkeypatch.setattr(nat, "_LIB", None)
+    monkeypatch.setattr(nat, "LIB_PATH", tmp_path / "missing.so")
+    with pytest.raises(nat.NativeLibraryError):
+        mk.kernel_supported(FakeCuda())
