@@ -45,8 +45,8 @@ int32_t nsmoe_abi_version(void);
 
 /* Measurement hooks (no counterpart in the reference; used by bench.py).  When enabled,
  * the library records a HIP event pair on the launch stream around each launch of its
- * main kernels ("expert_fwd", "expert_fwd_a1", "combine", "expert_bwd", "dw_in",
- * "dw_out", "route_fwd", "dispatch") until `capacity` pairs are used.
+ * main kernels ("pack", "route_fwd", "dispatch", "expert_fwd", "combine",
+ * "expert_bwd", "dw_in", "dw_out") until `capacity` pairs are used.
  * nsmoe_timing_read waits for the recorded events of one kernel and returns their
  * summed duration.  capacity 0 disables timing and frees the events. */
 int nsmoe_timing_enable(int32_t capacity);
@@ -140,7 +140,20 @@ typedef struct nsmoe_experts_args {
   const int32_t* sorted_ids;  /* dispatch outputs (nsmoe_dispatch) */
   const int32_t* pad_offsets;
   const int32_t* counts;
+
+  const void* w_in_packed;   /* nsmoe_pack_weights outputs: required by the forward */
+  const void* w_out_packed;  /* (both) and the backward (w_in_packed) */
 } nsmoe_experts_args;
+
+/* Weight repacking (no counterpart in the reference: the layout its Triton kernels read
+ * through tl.dot is the plain stack).  Rewrites w_in / w_sh_in and w_out / w_sh_out into
+ * MFMA fragment order so the grouped GEMMs load each 16 x 32 weight fragment with one
+ * coalesced load.  Run once per weight update (every forward in training); the backward
+ * reuses the forward's w_in_packed.  w_out_packed may be NULL to pack W_in only.
+ * nsmoe_pack_sizes reports the two buffer sizes in bytes. */
+int nsmoe_pack_sizes(const nsmoe_experts_args* args, size_t* w_in_bytes, size_t* w_out_bytes);
+int nsmoe_pack_weights(const nsmoe_experts_args* args, void* w_in_packed, void* w_out_packed,
+                       void* stream);
 
 /* Forward: out [T, d] = sum_j topk_w[t, j] * expert_{idx[t, j]}(x[t]) + sum_s shared_s(x[t]).
  *   inv    [T * k] int32 from nsmoe_dispatch.

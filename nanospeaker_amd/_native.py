@@ -30,6 +30,7 @@ class ExpertsArgs(ctypes.Structure):
         ("x", _vp), ("w_in", _vp), ("w_out", _vp), ("b_in", _vp), ("b_out", _vp),
         ("w_sh_in", _vp), ("w_sh_out", _vp), ("b_sh_in", _vp), ("b_sh_out", _vp),
         ("topk_w", _vp), ("sorted_ids", _vp), ("pad_offsets", _vp), ("counts", _vp),
+        ("w_in_packed", _vp), ("w_out_packed", _vp),
     ]
 
 
@@ -54,6 +55,9 @@ SIGNATURES = {
     "nsmoe_dispatch_l_cap": (_i64, [_i64, _i32]),
     "nsmoe_dispatch_workspace_size": (_sz, [_i64, _i32]),
     "nsmoe_dispatch": (ctypes.c_int, [_vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "nsmoe_pack_sizes": (ctypes.c_int, [ctypes.POINTER(ExpertsArgs), ctypes.POINTER(_sz),
+                                        ctypes.POINTER(_sz)]),
+    "nsmoe_pack_weights": (ctypes.c_int, [ctypes.POINTER(ExpertsArgs), _vp, _vp, _vp]),
     "nsmoe_experts_fwd_workspace_size": (_sz, [ctypes.POINTER(ExpertsArgs)]),
     "nsmoe_experts_fwd": (ctypes.c_int, [ctypes.POINTER(ExpertsArgs), _vp, _vp, _vp, _sz, _vp]),
     "nsmoe_experts_bwd_workspace_size": (_sz, [ctypes.POINTER(ExpertsArgs)]),

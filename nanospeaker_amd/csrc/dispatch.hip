@@ -10,9 +10,12 @@
 // The reference scatters with an atomic cursor, so its order inside a run is arbitrary
 // (moe_kernel.py:35-36).  Here the order is the stable sort's, bit for bit, with no
 // global atomics deciding it:
-//   1. hist:    one workgroup per chunk of 256 pairs counts its experts in LDS;
-//   2. scan:    one workgroup turns the [chunks, E] counts into per-chunk run bases,
-//               the padded run offsets, the block -> expert map and the pad sentinels;
+//   1. hist:    one workgroup per chunk of pairs (1024, or 256 for E > 256) counts its
+//               experts in LDS;
+//   2. scan:    one workgroup turns the [chunks, E] counts into per-chunk run bases (a
+//               segmented scan down each expert's column: every thread owns one
+//               segment, so the loads of a column are issued together, not one by
+//               one), the padded run offsets, the block -> expert map and the sentinels;
 //   3. scatter: each chunk ranks its pairs inside each expert.  Every lane sets its bit
 //               in a per-wave 64-bit LDS mask for its expert (ds_or_b64, order-free);
 //               the rank is then popcount(mask & lanes-below) plus the popcounts of the
@@ -22,25 +25,27 @@
 
 namespace nsmoe {
 
-constexpr int DISPATCH_CHUNK = 256;          // pairs per chunk = threads per workgroup
-constexpr int DISPATCH_WAVES = DISPATCH_CHUNK / 64;
 constexpr int ALIGN_M = 16;                  // run alignment (slots)
 constexpr int DISPATCH_MAX_EXPERTS = 1024;
 
-__global__ void __launch_bounds__(DISPATCH_CHUNK)
+// Pairs per chunk = threads per workgroup of the hist and scatter kernels.  The scatter
+// keeps one 64-bit mask per (wave, expert) in LDS, so wide chunks need few experts.
+static inline int dispatch_chunk(int E) { return E <= 256 ? 1024 : 256; }
+
+__global__ void __launch_bounds__(1024)
 dispatch_hist_kernel(const int64_t* __restrict__ topk_idx, int64_t M, int E,
                      int32_t* __restrict__ hist) {
   extern __shared__ int32_t s_cnt[];
-  for (int e = threadIdx.x; e < E; e += DISPATCH_CHUNK) s_cnt[e] = 0;
+  for (int e = threadIdx.x; e < E; e += blockDim.x) s_cnt[e] = 0;
   __syncthreads();
-  const int64_t p = (int64_t)blockIdx.x * DISPATCH_CHUNK + threadIdx.x;
+  const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (p < M) {
     int64_t e = topk_idx[p];
     if (e >= 0 && e < E) atomicAdd(&s_cnt[e], 1);
   }
   __syncthreads();
   int32_t* row = hist + (int64_t)blockIdx.x * E;
-  for (int e = threadIdx.x; e < E; e += DISPATCH_CHUNK) row[e] = s_cnt[e];
+  for (int e = threadIdx.x; e < E; e += blockDim.x) row[e] = s_cnt[e];
 }
 
 // One workgroup.  hist is rewritten in place into exclusive per-chunk bases.
@@ -54,18 +59,36 @@ dispatch_scan_kernel(int32_t* __restrict__ hist, int64_t n_chunks, int E, int64_
   __shared__ int32_t s_wave[16];
   const int tid = threadIdx.x;
 
-  // Per-expert running sums down the chunk column (coalesced across experts).
-  for (int e = tid; e < E; e += blockDim.x) {
-    int32_t run = 0;
-    for (int64_t c = 0; c < n_chunks; ++c) {
-      int32_t v = hist[c * E + e];
-      hist[c * E + e] = run;
-      run += v;
+  // Per-expert exclusive sums down the chunk column.  Thread (e, seg) owns chunks
+  // [seg * L, (seg + 1) * L) of expert e's column: it sums them (independent loads),
+  // the segment totals are scanned in LDS, then it rewrites its chunks as bases.
+  __shared__ int32_t s_seg[1024];
+  const int nseg = E <= (int)blockDim.x ? (int)blockDim.x / E : 1;
+  const int64_t L = (n_chunks + nseg - 1) / nseg;
+  for (int base_e = 0; base_e < E; base_e += (int)blockDim.x / nseg) {
+    const int e = base_e + tid / nseg, seg = tid % nseg;
+    const bool own = tid / nseg < (int)blockDim.x / nseg && e < E;
+    const int64_t c0 = seg * L, c1 = c0 + L < n_chunks ? c0 + L : n_chunks;
+    int32_t sum = 0;
+    if (own)
+      for (int64_t c = c0; c < c1; ++c) sum += hist[c * E + e];
+    s_seg[tid] = own ? sum : 0;
+    __syncthreads();
+    if (own) {
+      int32_t run = 0;
+      for (int q = 0; q < seg; ++q) run += s_seg[tid - seg + q];
+      for (int64_t c = c0; c < c1; ++c) {
+        const int32_t v = hist[c * E + e];
+        hist[c * E + e] = run;
+        run += v;
+      }
+      if (seg == nseg - 1) {
+        s_cnt[e] = run;
+        counts[e] = run;
+      }
     }
-    s_cnt[e] = run;
-    counts[e] = run;
+    __syncthreads();
   }
-  __syncthreads();
 
   // Exclusive scan of the ALIGN_M-padded counts (E <= 1024: one pass per thread chunk).
   const int per = (E + blockDim.x - 1) / blockDim.x;
@@ -128,16 +151,17 @@ dispatch_scan_kernel(int32_t* __restrict__ hist, int64_t n_chunks, int E, int64_
   for (int64_t s = total + tid; s < l_cap; s += blockDim.x) sorted_ids[s] = (int32_t)M;
 }
 
-__global__ void __launch_bounds__(DISPATCH_CHUNK)
+__global__ void __launch_bounds__(1024)
 dispatch_scatter_kernel(const int64_t* __restrict__ topk_idx, int64_t M, int E,
                         const int32_t* __restrict__ chunk_base,
                         const int32_t* __restrict__ offs, int32_t* __restrict__ sorted_ids,
                         int32_t* __restrict__ inv) {
-  extern __shared__ unsigned long long s_mask[];  // [DISPATCH_WAVES][E]
-  for (int i = threadIdx.x; i < DISPATCH_WAVES * E; i += DISPATCH_CHUNK) s_mask[i] = 0ull;
+  extern __shared__ unsigned long long s_mask[];  // [waves][E]
+  const int waves = blockDim.x >> 6;
+  for (int i = threadIdx.x; i < waves * E; i += blockDim.x) s_mask[i] = 0ull;
   __syncthreads();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t p = (int64_t)blockIdx.x * DISPATCH_CHUNK + threadIdx.x;
+  const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   int e = -1;
   if (p < M) {
     int64_t v = topk_idx[p];
@@ -174,8 +198,8 @@ extern "C" int64_t nsmoe_dispatch_l_cap(int64_t n_pairs, int32_t n_experts) {
 }
 
 extern "C" size_t nsmoe_dispatch_workspace_size(int64_t n_pairs, int32_t n_experts) {
-  if (n_pairs <= 0) return 0;
-  return (size_t)cdiv(n_pairs, DISPATCH_CHUNK) * (size_t)n_experts * sizeof(int32_t);
+  if (n_pairs <= 0 || n_experts <= 0) return 0;
+  return (size_t)cdiv(n_pairs, dispatch_chunk(n_experts)) * (size_t)n_experts * sizeof(int32_t);
 }
 
 extern "C" int nsmoe_dispatch(const int64_t* topk_idx, int64_t n_pairs, int32_t n_experts,
@@ -203,20 +227,21 @@ extern "C" int nsmoe_dispatch(const int64_t* topk_idx, int64_t n_pairs, int32_t 
     set_error("dispatch: workspace %zu B < %zu B", workspace_bytes, need);
     return NSMOE_EWORKSPACE;
   }
-  const int64_t n_chunks = cdiv(n_pairs, DISPATCH_CHUNK);
+  const int chunk = dispatch_chunk(n_experts);
+  const int64_t n_chunks = cdiv(n_pairs, chunk);
   const int64_t l_cap = nsmoe_dispatch_l_cap(n_pairs, n_experts);
   int32_t* hist = (int32_t*)workspace;
 
   KernelTimer timer("dispatch", s);
-  dispatch_hist_kernel<<<(unsigned)n_chunks, DISPATCH_CHUNK, n_experts * sizeof(int32_t), s>>>(
+  dispatch_hist_kernel<<<(unsigned)n_chunks, chunk, n_experts * sizeof(int32_t), s>>>(
       topk_idx, n_pairs, n_experts, hist);
   NSMOE_TRY(check_launch("dispatch_hist_kernel"));
   dispatch_scan_kernel<<<1, 1024, 0, s>>>(hist, n_chunks, n_experts, n_pairs, l_cap,
                                           sorted_ids, expert_ids, pad_offsets, counts,
                                           n_post_pad);
   NSMOE_TRY(check_launch("dispatch_scan_kernel"));
-  dispatch_scatter_kernel<<<(unsigned)n_chunks, DISPATCH_CHUNK,
-                            DISPATCH_WAVES * n_experts * sizeof(unsigned long long), s>>>(
+  dispatch_scatter_kernel<<<(unsigned)n_chunks, chunk,
+                            (chunk / 64) * n_experts * sizeof(unsigned long long), s>>>(
       topk_idx, n_pairs, n_experts, hist, pad_offsets, sorted_ids, inv);
   timer.stop();
   return check_launch("dispatch_scatter_kernel");

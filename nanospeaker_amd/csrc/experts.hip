@@ -22,6 +22,7 @@
 
 #include "gemm_core.h"
 #include "nsmoe_capi_internal.h"
+#include "pack.h"
 #include "../../include/nsmoe.h"
 
 namespace nsmoe {
@@ -48,6 +49,10 @@ struct ExpParams {
   int64_t l_cap;
   int d, H, E, S, k, act;
   int fast;
+  // fragment-order weight packs (pack.hip): W_in for GEMM1, W_out for GEMM2
+  const char* p_in;
+  const char* p_out;
+  int in_kb, in_nb, out_kb, out_nb;
   // forward output rows
   void* y;
   // backward
@@ -119,22 +124,29 @@ __device__ __forceinline__ void copy_out(const char* tile, int pitch, int rows,
 }
 
 // ============================ forward ====================================================
+//
+// One workgroup = 4 waves = one 64-row tile of one group.  GEMM1 [64, d] x [d, gate|up]:
+// the gathered token rows go through swizzled LDS (shared by the waves), the packed W_in
+// fragments come straight from L2 into registers one k-step ahead.  Wave w owns gate
+// column blocks [w * NBW, +NBW) and the up blocks at the same columns, so act(gate) * up
+// is lane-local.  h (rounded to the element type, as the reference stores it) stays in
+// LDS and feeds GEMM2 [64, H] x [H, d] against packed W_out in 192-column passes
+// (48 columns per wave); + b_out, * gate weight, then the rows go out through LDS.
+constexpr int NP2 = 192;  // output columns per pass of the second GEMMs
 
 template <int DT, int NBW>
 __global__ void __launch_bounds__(NT) expert_fwd_kernel(ExpParams p) {
   using G = Geo<DT>;
   using T = typename G::T;
   using M = Mma<DT>;
-  constexpr int HPMAX = 64 * NBW;  // gate (and up) columns one tile covers
-  constexpr int SA = BM * G::PITCH;
-  constexpr int SB = 2 * HPMAX * G::PITCH;
-  constexpr int REGION0 = 2 * (SA + SB);
+  using Frag = typename M::Frag;
+  constexpr int HPMAX = 64 * NBW;
+  constexpr int SA = BM * G::ROWB;
   constexpr int HP_PITCH = HPMAX * G::ES + 16;
-  constexpr int SB2 = 64 * G::PITCH;
-  constexpr int Y_PITCH = 64 * G::ES + 16;
-  static_assert(2 * SB2 + BM * Y_PITCH <= REGION0, "GEMM2 staging must fit in the region");
-  __shared__ __attribute__((aligned(16))) char s_r0[REGION0];
+  constexpr int Y_PITCH = NP2 * G::ES + 16;
+  __shared__ __attribute__((aligned(16))) char s_a[2][SA];
   __shared__ __attribute__((aligned(16))) char s_h[BM * HP_PITCH];
+  __shared__ __attribute__((aligned(16))) char s_y[BM * Y_PITCH];
   __shared__ int s_tok[BM];
   __shared__ float s_w[BM];
   __shared__ int s_loc[3];
@@ -160,61 +172,55 @@ __global__ void __launch_bounds__(NT) expert_fwd_kernel(ExpParams p) {
   const int d = p.d, H = p.H, twoH = 2 * p.H;
   const bool fast = p.fast;
   const T* X = (const T*)p.x;
-  const T* Win = per_group<T>(p.w_in, p.w_sh_in, g, p.E, (int64_t)d * twoH);
   auto rowA = [&](int r) -> const T* {
     const int t = s_tok[r];
     return t >= 0 ? X + (int64_t)t * d : nullptr;
   };
-  auto rowB = [&](int k) -> const T* { return Win + (int64_t)k * twoH; };
-  auto sA = [&](int b) { return s_r0 + b * SA; };
-  auto sB = [&](int b) { return s_r0 + 2 * SA + b * SB; };
+  const char* P1 = p.p_in + (int64_t)g * p.in_nb * p.in_kb * G::PKB;
 
-  // ---- GEMM1: [BM, d] x [d, gate | up] ----
+  // ---- GEMM1 ----
   DirectStage<DT, BM, NT> stA;
-  TransStage<DT, HPMAX, NT> stG, stU;
   f32x4 accg[4][NBW], accu[4][NBW];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < NBW; ++j) accg[i][j] = accu[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  const int nk = (d + G::KC - 1) / G::KC;
-  stA.load(rowA, 0, d, fast);
-  stG.load(rowB, NoScale{}, 0, d, 0, H, fast);
-  stU.load(rowB, NoScale{}, 0, d, H, twoH, fast);
-  stA.store(sA(0));
-  stG.store(sB(0));
-  stU.store(sB(0) + HPMAX * G::PITCH);
-  __syncthreads();
-  for (int kc = 0; kc < nk; ++kc) {
-    const int cur = kc & 1;
-    const bool more = kc + 1 < nk;
-    if (more) {
-      const int k0 = (kc + 1) * G::KC;
-      stA.load(rowA, k0, d, fast);
-      stG.load(rowB, NoScale{}, k0, d, 0, H, fast);
-      stU.load(rowB, NoScale{}, k0, d, H, twoH, fast);
-    }
-    typename M::Frag af[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) af[i] = frag_at<DT>(sA(cur), G::PITCH, i * 16, 0);
+  Frag b0[2 * NBW], b1[2 * NBW];
+  auto loadB = [&](Frag* b, int kb) {
 #pragma unroll
     for (int j = 0; j < NBW; ++j) {
-      const int jb = (wave * NBW + j) * 16;
-      const typename M::Frag bg = frag_at<DT>(sB(cur), G::PITCH, jb, 0);
-      const typename M::Frag bu = frag_at<DT>(sB(cur), G::PITCH, HPMAX + jb, 0);
+      const int jb = wave * NBW + j;
+      b[j] = frag_pk<DT>(P1, jb, kb, p.in_kb);
+      b[NBW + j] = frag_pk<DT>(P1, HPMAX / 16 + jb, kb, p.in_kb);
+    }
+  };
+  const int nk = p.in_kb;
+  auto step = [&](int kc, const Frag* use, Frag* nxt) {
+    const bool more = kc + 1 < nk;
+    if (more) {
+      stA.load(rowA, (kc + 1) * G::KC, d, fast);
+      loadB(nxt, kc + 1);
+    }
+    Frag af[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) af[i] = frag_sw<DT>(s_a[kc & 1], i * 16);
+#pragma unroll
+    for (int j = 0; j < NBW; ++j)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        M::run(accg[i][j], af[i], bg);
-        M::run(accu[i][j], af[i], bu);
+        M::run(accg[i][j], af[i], use[j]);
+        M::run(accu[i][j], af[i], use[NBW + j]);
       }
-    }
-    if (more) {
-      stA.store(sA(cur ^ 1));
-      stG.store(sB(cur ^ 1));
-      stU.store(sB(cur ^ 1) + HPMAX * G::PITCH);
-    }
+    if (more) stA.store(s_a[(kc + 1) & 1]);
     __syncthreads();
+  };
+  stA.load(rowA, 0, d, fast);
+  loadB(b0, 0);
+  stA.store(s_a[0]);
+  __syncthreads();
+  for (int kc = 0; kc < nk; kc += 2) {
+    step(kc, b0, b1);
+    if (kc + 1 < nk) step(kc + 1, b1, b0);
   }
 
   // ---- GEMM1 epilogue: bias, h = act(gate) * up into LDS ----
@@ -238,58 +244,53 @@ __global__ void __launch_bounds__(NT) expert_fwd_kernel(ExpParams p) {
   }
   __syncthreads();
 
-  // ---- GEMM2: [BM, H] x [H, d] in column blocks of 64, + b_out, * gate ----
-  const T* Wout = per_group<T>(p.w_out, p.w_sh_out, g, p.E, (int64_t)H * d);
+  // ---- GEMM2: [BM, H] x [H, d] in passes of NP2 columns, + b_out, * gate ----
+  const char* P4 = p.p_out + (int64_t)g * p.out_nb * p.out_kb * G::PKB;
   const T* bout = (g < p.E ? p.b_out : p.b_sh_out)
                       ? per_group<T>(p.b_out, p.b_sh_out, g, p.E, d) : nullptr;
-  auto rowW = [&](int k) -> const T* { return Wout + (int64_t)k * d; };
-  auto sB2 = [&](int b) { return s_r0 + b * SB2; };
-  char* sY = s_r0 + 2 * SB2;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int nk2 = (H + G::KC - 1) / G::KC;
-  TransStage<DT, 64, NT> stW;
+  const int nk2 = p.out_kb;
   T* Y = (T*)p.y;
-  for (int n0 = 0; n0 < d; n0 += 64) {
-    f32x4 acc[2][2];
+  for (int n0 = 0; n0 < d; n0 += NP2) {
+    f32x4 acc[4][3];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    stW.load(rowW, NoScale{}, 0, H, n0, d, fast);
-    stW.store(sB2(0));
-    __syncthreads();
-    for (int kc = 0; kc < nk2; ++kc) {
-      const int cur = kc & 1;
-      const bool more = kc + 1 < nk2;
-      if (more) stW.load(rowW, NoScale{}, (kc + 1) * G::KC, H, n0, d, fast);
-      typename M::Frag af[2], bf[2];
+      for (int j = 0; j < 3; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int nbase = n0 / 16 + wave * 3;
+    auto loadB2 = [&](Frag* b, int kb) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
-        af[i] = frag_at<DT>(s_h, HP_PITCH, wm * 32 + i * 16, kc * G::ROWB);
+      for (int j = 0; j < 3; ++j)
+        b[j] = nbase + j < p.out_nb ? frag_pk<DT>(P4, nbase + j, kb, p.out_kb) : M::zero();
+    };
+    Frag c0[3], c1[3];
+    loadB2(c0, 0);
+    for (int kk = 0; kk < nk2; ++kk) {
+      Frag* use = (kk & 1) ? c1 : c0;
+      Frag* nxt = (kk & 1) ? c0 : c1;
+      if (kk + 1 < nk2) loadB2(nxt, kk + 1);
+      Frag af[4];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) bf[j] = frag_at<DT>(sB2(cur), G::PITCH, wn * 32 + j * 16, 0);
+      for (int i = 0; i < 4; ++i) af[i] = frag_at<DT>(s_h, HP_PITCH, i * 16, kk * G::ROWB);
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int j = 0; j < 3; ++j)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) M::run(acc[i][j], af[i], bf[j]);
-      if (more) stW.store(sB2(cur ^ 1));
-      __syncthreads();
+        for (int i = 0; i < 4; ++i) M::run(acc[i][j], af[i], use[j]);
     }
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int nl = wn * 32 + j * 16 + lc;
+    for (int j = 0; j < 3; ++j) {
+      const int nl = wave * 48 + j * 16 + lc;
       const int n = n0 + nl;
       const float bo = (bout && n < d) ? Elem<DT>::to_f(bout[n]) : 0.0f;
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int m = wm * 32 + i * 16 + lg * 4 + r;
-          *(T*)(sY + m * Y_PITCH + nl * G::ES) = Elem<DT>::from_f((acc[i][j][r] + bo) * s_w[m]);
+          const int m = i * 16 + lg * 4 + r;
+          *(T*)(s_y + m * Y_PITCH + nl * G::ES) = Elem<DT>::from_f((acc[i][j][r] + bo) * s_w[m]);
         }
     }
     __syncthreads();
-    copy_out<DT>(sY, Y_PITCH, rows, Y + slot0 * d, d, n0, min(64, d - n0), 0, 0, fast);
+    copy_out<DT>(s_y, Y_PITCH, rows, Y + slot0 * d, d, n0, min(NP2, d - n0), 0, 0, fast);
     __syncthreads();
   }
 }
@@ -358,40 +359,30 @@ combine_kernel(const typename Elem<DT>::T* __restrict__ rows, const int32_t* __r
 //   a1 = x[tok] @ W_in[g]      (gate and up, the forward's pre-activations, recomputed
 //                               in fp32 registers instead of being saved and re-read)
 //   G  = dout[tok] @ W_out[g]^T
-// Wave w owns hidden columns {(w * NBW + j) * 16 ..}: the gate, up and G accumulators of
-// one (row, column) sit in the same lane and register, so the GLU backward is lane-local:
+// x and dout rows go through swizzled LDS; packed W_in fragments and the rows of W_out
+// (contiguous along d, the contraction index) come straight from L2.  Wave w owns hidden
+// columns {(w * NBW + j) * 16 ..}: the gate, up and G accumulators of one (row, column)
+// sit in the same lane and register, so the GLU backward is lane-local:
 //   h = act(g) * u,  dtopk_w += G * h,  d_gate = w G u act'(g),  d_up = w G act(g).
-// dA1 = [d_gate | d_up] goes to LDS (bf16) for phase 3 and to HBM for dW_in; h goes to
-// HBM for dW_out.  The gate gradient also takes <dout[tok], b_out[g]> when the expert
+// dA1 = [d_gate | d_up] goes to LDS (bf16) for phase 3 and to HBM for dW_in; w * h goes
+// to HBM for dW_out (= sum (w h)^T dout).  The gate gradient also takes <dout[tok], b_out[g]> when the expert
 // has an output bias (the derivative of (h W_out + b_out) * w with respect to w).
-// Phase 3: dX rows = dA1 @ W_in[g]^T, reduced per token by `combine`.
-template <int DT, int NBW>
-struct BwdCfg {
-  using G = Geo<DT>;
-  static constexpr int HPMAX = 64 * NBW;
-  static constexpr int SX = BM * G::PITCH;           // x chunk
-  static constexpr int SD = BM * G::PITCH;           // dout chunk
-  static constexpr int SWI = 2 * HPMAX * G::PITCH;   // W_in^T chunk (gate | up)
-  static constexpr int SWO = HPMAX * G::PITCH;       // W_out chunk
-  static constexpr int STAGE = SX + SD + SWI + SWO;
-  static constexpr int DA_PITCH = 2 * HPMAX * G::ES + 16;
-  static constexpr int SDA = BM * DA_PITCH;
-  static constexpr bool DB = 2 * STAGE + SDA <= 150 * 1024;  // double-buffer if it fits
-  static constexpr int REGION0 = (DB ? 2 : 1) * STAGE;
-  static constexpr int SB3 = 64 * G::PITCH;
-  static constexpr int Y_PITCH = 64 * G::ES + 16;
-  static_assert(2 * SB3 + BM * Y_PITCH <= REGION0, "dX staging must fit in the region");
-};
-
+// Phase 3: dX rows = dA1 @ W_in[g]^T (W_in's rows are contiguous along 2H, the
+// contraction index), in passes of NP2 columns; reduced per token by `combine`.
 template <int DT, int NBW>
 __global__ void __launch_bounds__(NT) expert_bwd_kernel(ExpParams p) {
   using G = Geo<DT>;
   using T = typename G::T;
   using M = Mma<DT>;
-  using C = BwdCfg<DT, NBW>;
-  constexpr int HPMAX = C::HPMAX;
-  __shared__ __attribute__((aligned(16))) char s_r0[C::REGION0];
-  __shared__ __attribute__((aligned(16))) char s_da[C::SDA];
+  using Frag = typename M::Frag;
+  constexpr int HPMAX = 64 * NBW;
+  constexpr int SA = BM * G::ROWB;
+  constexpr int DA_PITCH = 2 * HPMAX * G::ES + 16;
+  constexpr int Y_PITCH = NP2 * G::ES + 16;
+  __shared__ __attribute__((aligned(16))) char s_ax[2][SA];
+  __shared__ __attribute__((aligned(16))) char s_ad[2][SA];
+  __shared__ __attribute__((aligned(16))) char s_da[BM * DA_PITCH];
+  __shared__ __attribute__((aligned(16))) char s_y[BM * Y_PITCH];
   __shared__ int s_tok[BM];
   __shared__ int s_pair[BM];
   __shared__ float s_w[BM];
@@ -424,6 +415,7 @@ __global__ void __launch_bounds__(NT) expert_bwd_kernel(ExpParams p) {
   const T* DO = (const T*)p.dout;
   const T* Win = per_group<T>(p.w_in, p.w_sh_in, g, p.E, (int64_t)d * twoH);
   const T* Wout = per_group<T>(p.w_out, p.w_sh_out, g, p.E, (int64_t)H * d);
+  const char* P1 = p.p_in + (int64_t)g * p.in_nb * p.in_kb * G::PKB;
   auto rowX = [&](int r) -> const T* {
     const int t = s_tok[r];
     return t >= 0 ? X + (int64_t)t * d : nullptr;
@@ -432,83 +424,63 @@ __global__ void __launch_bounds__(NT) expert_bwd_kernel(ExpParams p) {
     const int t = s_tok[r];
     return t >= 0 ? DO + (int64_t)t * d : nullptr;
   };
-  auto rowWi = [&](int k) -> const T* { return Win + (int64_t)k * twoH; };
   auto rowWo = [&](int n) -> const T* { return n < H ? Wout + (int64_t)n * d : nullptr; };
-  auto stage = [&](int b) { return s_r0 + (C::DB ? b : 0) * C::STAGE; };
-  auto sX = [&](int b) { return stage(b); };
-  auto sD = [&](int b) { return stage(b) + C::SX; };
-  auto sWi = [&](int b) { return stage(b) + C::SX + C::SD; };
-  auto sWo = [&](int b) { return stage(b) + C::SX + C::SD + C::SWI; };
 
   // ---- phase 1: a1 = x W_in, G = dout W_out^T ----
   DirectStage<DT, BM, NT> stX, stD;
-  TransStage<DT, HPMAX, NT> stG, stU;
-  DirectStage<DT, HPMAX, NT> stO;
   f32x4 accg[4][NBW], accu[4][NBW], accG[4][NBW];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < NBW; ++j)
       accg[i][j] = accu[i][j] = accG[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  auto load = [&](int k0) {
-    stX.load(rowX, k0, d, fast);
-    stD.load(rowD, k0, d, fast);
-    stG.load(rowWi, NoScale{}, k0, d, 0, H, fast);
-    stU.load(rowWi, NoScale{}, k0, d, H, twoH, fast);
-    stO.load(rowWo, k0, d, fast);
-  };
-  auto store = [&](int b) {
-    stX.store(sX(b));
-    stD.store(sD(b));
-    stG.store(sWi(b));
-    stU.store(sWi(b) + HPMAX * G::PITCH);
-    stO.store(sWo(b));
-  };
-  auto compute = [&](int b) {
-    typename M::Frag ax[4], ad[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      ax[i] = frag_at<DT>(sX(b), G::PITCH, i * 16, 0);
-      ad[i] = frag_at<DT>(sD(b), G::PITCH, i * 16, 0);
-    }
+  Frag b0[3 * NBW], b1[3 * NBW];
+  auto loadB = [&](Frag* b, int kb) {
 #pragma unroll
     for (int j = 0; j < NBW; ++j) {
-      const int jb = (wave * NBW + j) * 16;
-      const typename M::Frag bg = frag_at<DT>(sWi(b), G::PITCH, jb, 0);
-      const typename M::Frag bu = frag_at<DT>(sWi(b), G::PITCH, HPMAX + jb, 0);
-      const typename M::Frag bo = frag_at<DT>(sWo(b), G::PITCH, jb, 0);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        M::run(accg[i][j], ax[i], bg);
-        M::run(accu[i][j], ax[i], bu);
-        M::run(accG[i][j], ad[i], bo);
-      }
+      const int jb = wave * NBW + j;
+      b[j] = frag_pk<DT>(P1, jb, kb, p.in_kb);
+      b[NBW + j] = frag_pk<DT>(P1, HPMAX / 16 + jb, kb, p.in_kb);
+      b[2 * NBW + j] = frag_rows<DT>(rowWo, jb * 16, kb * G::KC, d, fast);
     }
   };
-
-  const int nk = (d + G::KC - 1) / G::KC;
-  if constexpr (C::DB) {
-    load(0);
-    store(0);
+  const int nk = p.in_kb;
+  auto step = [&](int kc, const Frag* use, Frag* nxt) {
+    const bool more = kc + 1 < nk;
+    if (more) {
+      stX.load(rowX, (kc + 1) * G::KC, d, fast);
+      stD.load(rowD, (kc + 1) * G::KC, d, fast);
+      loadB(nxt, kc + 1);
+    }
+    Frag ax[4], ad[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      ax[i] = frag_sw<DT>(s_ax[kc & 1], i * 16);
+      ad[i] = frag_sw<DT>(s_ad[kc & 1], i * 16);
+    }
+#pragma unroll
+    for (int j = 0; j < NBW; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        M::run(accg[i][j], ax[i], use[j]);
+        M::run(accu[i][j], ax[i], use[NBW + j]);
+        M::run(accG[i][j], ad[i], use[2 * NBW + j]);
+      }
+    if (more) {
+      stX.store(s_ax[(kc + 1) & 1]);
+      stD.store(s_ad[(kc + 1) & 1]);
+    }
     __syncthreads();
-    for (int kc = 0; kc < nk; ++kc) {
-      const int cur = kc & 1;
-      const bool more = kc + 1 < nk;
-      if (more) load((kc + 1) * G::KC);
-      compute(cur);
-      if (more) store(cur ^ 1);
-      __syncthreads();
-    }
-  } else {
-    load(0);
-    for (int kc = 0; kc < nk; ++kc) {
-      store(0);
-      __syncthreads();
-      if (kc + 1 < nk) load((kc + 1) * G::KC);
-      compute(0);
-      __syncthreads();
-    }
+  };
+  stX.load(rowX, 0, d, fast);
+  stD.load(rowD, 0, d, fast);
+  loadB(b0, 0);
+  stX.store(s_ax[0]);
+  stD.store(s_ad[0]);
+  __syncthreads();
+  for (int kc = 0; kc < nk; kc += 2) {
+    step(kc, b0, b1);
+    if (kc + 1 < nk) step(kc + 1, b1, b0);
   }
 
   // ---- phase 2: GLU backward, lane-local ----
@@ -542,10 +514,10 @@ __global__ void __launch_bounds__(NT) expert_bwd_kernel(ExpParams p) {
           const float dh = s_w[m] * Gv;
           dg = dh * uu * act_bwd(gg, p.act);
           du = dh * a;
-          HB[(slot0 + m) * H + n] = Elem<DT>::from_f(hv);
+          HB[(slot0 + m) * H + n] = Elem<DT>::from_f(s_w[m] * hv);
         }
-        *(T*)(s_da + m * C::DA_PITCH + n * G::ES) = Elem<DT>::from_f(dg);
-        *(T*)(s_da + m * C::DA_PITCH + (HPMAX + n) * G::ES) = Elem<DT>::from_f(du);
+        *(T*)(s_da + m * DA_PITCH + n * G::ES) = Elem<DT>::from_f(dg);
+        *(T*)(s_da + m * DA_PITCH + (HPMAX + n) * G::ES) = Elem<DT>::from_f(du);
       }
   }
 #pragma unroll
@@ -577,90 +549,193 @@ __global__ void __launch_bounds__(NT) expert_bwd_kernel(ExpParams p) {
     const float s = s_dtw[0][tid] + s_dtw[1][tid] + s_dtw[2][tid] + s_dtw[3][tid] + s_dtw[4][tid];
     ((T*)p.dtw)[s_pair[tid]] = Elem<DT>::from_f(s);
   }
-  copy_out<DT>(s_da, C::DA_PITCH, rows, (T*)p.da1 + slot0 * twoH, twoH, 0, H, HPMAX, H, fast);
+  copy_out<DT>(s_da, DA_PITCH, rows, (T*)p.da1 + slot0 * twoH, twoH, 0, H, HPMAX, H, fast);
 
-  // ---- phase 3: dX rows = dA1 @ W_in[g]^T, in column blocks of 64 ----
-  const int nkh = (H + G::KC - 1) / G::KC;  // chunks per half
+  // ---- phase 3: dX rows = dA1 @ W_in[g]^T in passes of NP2 columns ----
+  // k chunk q: half = q / nkh (0 gate, 1 up); LDS columns half * HPMAX + kk, source
+  // columns half * H + kk of W_in's rows.
+  const int nkh = (H + G::KC - 1) / G::KC;
   const int nk3 = 2 * nkh;
-  auto sB3 = [&](int b) { return s_r0 + b * C::SB3; };
-  char* sY = s_r0 + 2 * C::SB3;
-  const int wm = wave >> 1, wn = wave & 1;
-  DirectStage<DT, 64, NT> stW;
+  auto rowWi = [&](int n) -> const T* { return n < d ? Win + (int64_t)n * twoH : nullptr; };
   T* DX = (T*)p.dxrow;
-  for (int n0 = 0; n0 < d; n0 += 64) {
-    auto rowW = [&](int n) -> const T* {
-      return n0 + n < d ? Win + (int64_t)(n0 + n) * twoH : nullptr;
+  for (int n0 = 0; n0 < d; n0 += NP2) {
+    f32x4 acc[4][3];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 3; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int nw = n0 + wave * 48;
+    auto loadB3 = [&](Frag* b, int q) {
+      const int half = q / nkh, kk = (q % nkh) * G::KC;
+#pragma unroll
+      for (int j = 0; j < 3; ++j)
+        b[j] = frag_rows<DT>(rowWi, nw + j * 16, half * H + kk, half * H + H, fast);
     };
-    f32x4 acc2[2][2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) acc2[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // chunk q: half = q / nkh (0 gate, 1 up), source columns half * H + (q % nkh) * 32
-    __syncthreads();  // sB3 / sY are free (phase 1 or the previous block is done)
-    stW.load(rowW, 0, H, fast);
-    stW.store(sB3(0));
-    __syncthreads();
+    Frag c0[3], c1[3];
+    loadB3(c0, 0);
     for (int q = 0; q < nk3; ++q) {
-      const int cur = q & 1;
-      const bool more = q + 1 < nk3;
-      if (more) {
-        const int qn = q + 1, half = qn / nkh, kk = (qn % nkh) * G::KC;
-        stW.load(rowW, half * H + kk, half * H + H, fast);
-      }
+      Frag* use = (q & 1) ? c1 : c0;
+      Frag* nxt = (q & 1) ? c0 : c1;
+      if (q + 1 < nk3) loadB3(nxt, q + 1);
       const int half = q / nkh, kk = (q % nkh) * G::KC;
       const int kbyte = (half * HPMAX + kk) * G::ES;
-      typename M::Frag af[2], bf[2];
+      Frag af[4];
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
-        af[i] = frag_at<DT>(s_da, C::DA_PITCH, wm * 32 + i * 16, kbyte);
+      for (int i = 0; i < 4; ++i) af[i] = frag_at<DT>(s_da, DA_PITCH, i * 16, kbyte);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) bf[j] = frag_at<DT>(sB3(cur), G::PITCH, wn * 32 + j * 16, 0);
+      for (int j = 0; j < 3; ++j)
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) M::run(acc2[i][j], af[i], bf[j]);
-      if (more) stW.store(sB3(cur ^ 1));
-      __syncthreads();
+        for (int i = 0; i < 4; ++i) M::run(acc[i][j], af[i], use[j]);
     }
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int nl = wn * 32 + j * 16 + lc;
+    for (int j = 0; j < 3; ++j) {
+      const int nl = wave * 48 + j * 16 + lc;
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int m = wm * 32 + i * 16 + lg * 4 + r;
-          *(T*)(sY + m * C::Y_PITCH + nl * G::ES) = Elem<DT>::from_f(acc2[i][j][r]);
+          const int m = i * 16 + lg * 4 + r;
+          *(T*)(s_y + m * Y_PITCH + nl * G::ES) = Elem<DT>::from_f(acc[i][j][r]);
         }
     }
     __syncthreads();
-    copy_out<DT>(sY, C::Y_PITCH, rows, DX + slot0 * d, d, n0, min(64, d - n0), 0, 0, fast);
+    copy_out<DT>(s_y, Y_PITCH, rows, DX + slot0 * d, d, n0, min(NP2, d - n0), 0, 0, fast);
+    __syncthreads();
   }
 }
 
 // ============================ backward: dW ===============================================
 // MODE 0: dW_in[g]  [d, 2H] = sum_r x[tok_r]^T dA1[slot_r]
-// MODE 1: dW_out[g] [H, d]  = sum_r h[slot_r]^T (w_r * dout[tok_r])
+// MODE 1: dW_out[g] [H, d]  = sum_r (w_r h[slot_r])^T dout[tok_r]   (the backward stores
+//                                                                     w * h per row)
+// The contraction runs over the group's rows, which are contiguous along the output
+// index in memory, so both operands are staged transposed (TransStage) into swizzled
+// LDS: KCH chunks of 32 rows per barrier, the A and B chunks of a stage staged by
+// disjoint thread ranges so every wave shares the transposes.  The row -> token lookups
+// of the work item's rows are read once into LDS.  Tile BMo x BNo =
+// (WGM * TM * 16) x (WGN * TN * 16).
 __device__ __forceinline__ int dw_chunks(int rows) {
   const int c = (rows + DW_RC - 1) / DW_RC;
   return c < 1 ? 1 : c;  // an empty group still owns one (all-zero) chunk
 }
+
+template <int MODE> struct DwShape;
+template <> struct DwShape<0> {  // dW_in: 64 x 128 tiles, waves side by side along N
+  static constexpr int WGM = 1, WGN = 4, TM = 4, TN = 2;
+};
+template <> struct DwShape<1> {  // dW_out: 128 x 64 tiles, waves stacked along M
+  static constexpr int WGM = 4, WGN = 1, TM = 2, TN = 4;
+};
+
+// Transposed staging of one dW stage: KCH chunks of the A tile (BMA columns) and of the
+// B tile (BNB columns), VE x VE blocks spread over the workgroup's threads (a thread keeps
+// registers for its own PER blocks only).  Same transpose, rotation and swizzle as
+// TransStage.
+template <int DT, int BMA, int BNB, int KCH>
+struct DwStager {
+  using G = Geo<DT>;
+  using T = typename G::T;
+  static constexpr int VE = G::VE;
+  static constexpr int KB = G::KC / VE;
+  static constexpr int NBA = KB * (BMA / VE), NBB = KB * (BNB / VE);
+  static constexpr int TOT = KCH * (NBA + NBB);
+  static constexpr int PER = (TOT + NT - 1) / NT;
+  static constexpr int TA = BMA * G::ROWB, TB = BNB * G::ROWB;
+  u32x4 v[PER][VE];
+
+  struct Role {
+    bool on, is_a;
+    int q, kb, nb;
+  };
+  __device__ __forceinline__ static Role role(int i) {
+    const int b = (int)threadIdx.x + i * NT;
+    Role r{b < TOT, false, 0, 0, 0};
+    if (!r.on) return r;
+    int blk;
+    if (b < KCH * NBA) {
+      r.is_a = true;
+      r.q = b / NBA;
+      blk = b % NBA;
+    } else {
+      const int b2 = b - KCH * NBA;
+      r.q = b2 / NBB;
+      blk = b2 % NBB;
+    }
+    r.kb = blk % KB;
+    r.nb = blk / KB;
+    return r;
+  }
+
+  template <class RowA, class RowB>
+  __device__ __forceinline__ void load(RowA rowA, RowB rowB, int k0, int klim, int m0, int Md,
+                                       int n0, int Nd, bool fast) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const Role ro = role(i);
+      const int col = (ro.is_a ? m0 : n0) + ro.nb * VE;
+      const int lim = ro.is_a ? Md : Nd;
+#pragma unroll
+      for (int r = 0; r < VE; ++r) {
+        v[i][r] = u32x4{0u, 0u, 0u, 0u};
+        const int k = k0 + ro.q * G::KC + ro.kb * VE + r;
+        if (!ro.on || k >= klim) continue;
+        const T* src = ro.is_a ? rowA(k) : rowB(k);
+        T tmp[VE];
+        if (fast) {
+          if (col < lim) {
+            u32x4 raw = *(const u32x4*)(src + col);
+            __builtin_memcpy(tmp, &raw, 16);
+          } else {
+#pragma unroll
+            for (int e = 0; e < VE; ++e) tmp[e] = T(0);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < VE; ++e) tmp[e] = (col + e < lim) ? src[col + e] : T(0);
+        }
+        __builtin_memcpy(&v[i][r], tmp, 16);
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(char* stage) const {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const Role ro = role(i);
+      if (!ro.on) continue;
+      char* tile = stage + (ro.is_a ? ro.q * TA : KCH * TA + ro.q * TB);
+      if constexpr (G::ES == 2) {
+        store_trans8<DT>(v[i], tile, ro.nb, ro.kb);
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          u32x4 o{v[i][0][c], v[i][1][c], v[i][2][c], v[i][3][c]};
+          *(u32x4*)(tile + sw_off<DT>(ro.nb * 4 + c, ro.kb)) = o;
+        }
+      }
+    }
+  }
+};
 
 template <int DT, int MODE>
 __global__ void __launch_bounds__(NT) dw_kernel(ExpParams p) {
   using G = Geo<DT>;
   using T = typename G::T;
   using Mm = Mma<DT>;
-  constexpr int S1 = 64 * G::PITCH;
-  __shared__ __attribute__((aligned(16))) char s_a[2][S1];
-  __shared__ __attribute__((aligned(16))) char s_b[2][S1];
+  using S = DwShape<MODE>;
+  constexpr int BMo = S::WGM * S::TM * 16, BNo = S::WGN * S::TN * 16;
+  constexpr int KCH = 2;  // 32-row chunks per stage
+  using Stager = DwStager<DT, BMo, BNo, KCH>;
+  constexpr int TA = Stager::TA, TB = Stager::TB;
+  constexpr int STAGE = KCH * (TA + TB);
+  __shared__ __attribute__((aligned(16))) char s_stage[2][STAGE];
+  __shared__ int s_tok[DW_RC];
   __shared__ int s_loc[3];
 
   const int d = p.d, H = p.H, twoH = 2 * p.H;
   const int Md = MODE == 0 ? d : H;
   const int Nd = MODE == 0 ? twoH : d;
-  const int tn = (Nd + 63) / 64, ntiles = ((Md + 63) / 64) * tn;
+  const int tn = (Nd + BNo - 1) / BNo, ntiles = ((Md + BMo - 1) / BMo) * tn;
   const int item = xcd_remap(blockIdx.x, gridDim.x);
   Located loc;
   if (!locate(item, p.E + p.S, [&](int g) { return dw_chunks(rows_of(p, g)) * ntiles; },
@@ -674,69 +749,63 @@ __global__ void __launch_bounds__(NT) dw_kernel(ExpParams p) {
   const int rows_g = rows_of(p, g);
   const int nch = dw_chunks(rows_g);
   const int chunk = loc.local / ntiles, t = loc.local % ntiles;
-  const int mt = t / tn, nt = t % tn;
-  const int m0 = mt * 64, n0 = nt * 64;
+  const int m0 = (t / tn) * BMo, n0 = (t % tn) * BNo;
   const int r0 = chunk * DW_RC, r1 = min(rows_g, r0 + DW_RC);
   const int64_t rs = row_start(p, g);
   const bool fast = p.fast;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lc = lane & 15, lg = lane >> 4;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / S::WGN, wn = wave % S::WGN;
+
+  for (int r = r0 + tid; r < r1; r += NT)
+    s_tok[r - r0] = g < p.E ? p.sorted_ids[rs + r] / p.k : r;
+  __syncthreads();
 
   const T* X = (const T*)p.x;
   const T* DA = (const T*)p.da1;
   const T* HB = (const T*)p.hbuf;
   const T* DO = (const T*)p.dout;
-  auto tok_of = [&](int r) -> int {
-    if (g < p.E) return p.sorted_ids[rs + r] / p.k;
-    return r;
-  };
   auto rowA = [&](int r) -> const T* {
-    if (MODE == 0) return X + (int64_t)tok_of(r) * d;
+    if (MODE == 0) return X + (int64_t)s_tok[r - r0] * d;
     return HB + (rs + r) * H;
   };
   auto rowB = [&](int r) -> const T* {
     if (MODE == 0) return DA + (rs + r) * twoH;
-    return DO + (int64_t)tok_of(r) * d;
-  };
-  auto scaleB = [&](int r) -> float {
-    if (MODE == 0 || g >= p.E) return 1.0f;
-    return Elem<DT>::to_f(((const T*)p.topk_w)[p.sorted_ids[rs + r]]);
+    return DO + (int64_t)s_tok[r - r0] * d;
   };
 
-  TransStage<DT, 64, NT> stA, stB;
-  f32x4 acc[2][2];
+  Stager stg;
+  auto load = [&](int k0) { stg.load(rowA, rowB, k0, r1, m0, Md, n0, Nd, fast); };
+  auto store = [&](int b) { stg.store(s_stage[b]); };
+  f32x4 acc[S::TM][S::TN];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < S::TM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const int nk = (r1 - r0 + G::KC - 1) / G::KC;
-  if (nk > 0) {
-    stA.load(rowA, NoScale{}, r0, r1, m0, Md, fast);
-    stB.load(rowB, scaleB, r0, r1, n0, Nd, fast);
-    stA.store(s_a[0]);
-    stB.store(s_b[0]);
+    for (int j = 0; j < S::TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int KS = KCH * G::KC;
+  const int ns = (r1 - r0 + KS - 1) / KS;
+  if (ns > 0) {
+    load(r0);
+    store(0);
     __syncthreads();
-    for (int kc = 0; kc < nk; ++kc) {
-      const int cur = kc & 1;
-      const bool more = kc + 1 < nk;
-      if (more) {
-        const int k0 = r0 + (kc + 1) * G::KC;
-        stA.load(rowA, NoScale{}, k0, r1, m0, Md, fast);
-        stB.load(rowB, scaleB, k0, r1, n0, Nd, fast);
+    for (int st = 0; st < ns; ++st) {
+      const int cur = st & 1;
+      const bool more = st + 1 < ns;
+      if (more) load(r0 + (st + 1) * KS);
+#pragma unroll
+      for (int q = 0; q < KCH; ++q) {
+        const char* ta = s_stage[cur] + q * TA;
+        const char* tb = s_stage[cur] + KCH * TA + q * TB;
+        typename Mm::Frag af[S::TM], bf[S::TN];
+#pragma unroll
+        for (int i = 0; i < S::TM; ++i) af[i] = frag_sw<DT>(ta, (wm * S::TM + i) * 16);
+#pragma unroll
+        for (int j = 0; j < S::TN; ++j) bf[j] = frag_sw<DT>(tb, (wn * S::TN + j) * 16);
+#pragma unroll
+        for (int i = 0; i < S::TM; ++i)
+#pragma unroll
+          for (int j = 0; j < S::TN; ++j) Mm::run(acc[i][j], af[i], bf[j]);
       }
-      typename Mm::Frag af[2], bf[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) af[i] = frag_at<DT>(s_a[cur], G::PITCH, wm * 32 + i * 16, 0);
-#pragma unroll
-      for (int j = 0; j < 2; ++j) bf[j] = frag_at<DT>(s_b[cur], G::PITCH, wn * 32 + j * 16, 0);
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) Mm::run(acc[i][j], af[i], bf[j]);
-      if (more) {
-        stA.store(s_a[cur ^ 1]);
-        stB.store(s_b[cur ^ 1]);
-      }
+      if (more) store(cur ^ 1);
       __syncthreads();
     }
   }
@@ -749,13 +818,13 @@ __global__ void __launch_bounds__(NT) dw_kernel(ExpParams p) {
     pdst = p.partial + (int64_t)(loc.aux + chunk) * mn;
   }
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < S::TM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < S::TN; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wm * 32 + i * 16 + lg * 4 + r;
-        const int n = n0 + wn * 32 + j * 16 + lc;
+        const int m = m0 + (wm * S::TM + i) * 16 + lg * 4 + r;
+        const int n = n0 + (wn * S::TN + j) * 16 + lc;
         if (m < Md && n < Nd) {
           if (dst) dst[(int64_t)m * Nd + n] = Elem<DT>::from_f(acc[i][j][r]);
           else pdst[(int64_t)m * Nd + n] = acc[i][j][r];
@@ -834,7 +903,7 @@ static int nbw_for(const nsmoe_experts_args* a) {
   return 4;
 }
 
-static int validate(const nsmoe_experts_args* a) {
+static int validate_dims(const nsmoe_experts_args* a) {
   NSMOE_REQUIRE(a, "experts: NULL args");
   NSMOE_REQUIRE(a->dtype == DT_BF16 || a->dtype == DT_F16 || a->dtype == DT_F32,
                 "experts: unknown dtype %d", a->dtype);
@@ -849,6 +918,11 @@ static int validate(const nsmoe_experts_args* a) {
   NSMOE_REQUIRE(a->n_tokens * a->top_k < (int64_t)INT32_MAX / 2 &&
                     rows_total(a) < (int64_t)INT32_MAX / 2,
                 "experts: too many rows");
+  return NSMOE_OK;
+}
+
+static int validate(const nsmoe_experts_args* a) {
+  NSMOE_TRY(validate_dims(a));
   NSMOE_REQUIRE(a->n_shared == 0 || (a->w_sh_in && a->w_sh_out),
                 "experts: shared weights missing");
   return NSMOE_OK;
@@ -871,6 +945,13 @@ static ExpParams make_params(const nsmoe_experts_args* a) {
   p.sorted_ids = a->sorted_ids;
   p.offs = a->pad_offsets;
   p.counts = a->counts;
+  p.p_in = (const char*)a->w_in_packed;
+  p.p_out = (const char*)a->w_out_packed;
+  const PackGeom pg = pack_geom(a->dtype, a->d_model, a->d_hidden, a->n_experts, a->n_shared);
+  p.in_kb = pg.in_kb;
+  p.in_nb = pg.in_nb;
+  p.out_kb = pg.out_kb;
+  p.out_nb = pg.out_nb;
   p.T = a->n_tokens;
   p.l_cap = a->l_cap;
   p.d = a->d_model;
@@ -879,8 +960,9 @@ static ExpParams make_params(const nsmoe_experts_args* a) {
   p.S = a->n_shared;
   p.k = a->top_k;
   p.act = a->activation;
-  const int ve = 16 / elem_size(a->dtype);
-  p.fast = (a->d_model % ve == 0) && (a->d_hidden % ve == 0) && aligned16(a->x) &&
+  // Weight fragments and staged rows read 8 (2-byte types) or 4..8 (fp32) contiguous
+  // elements per lane: the vector paths need d and H to be multiples of 8.
+  p.fast = (a->d_model % 8 == 0) && (a->d_hidden % 8 == 0) && aligned16(a->x) &&
            aligned16(a->w_in) && aligned16(a->w_out) &&
            (a->n_shared == 0 || (aligned16(a->w_sh_in) && aligned16(a->w_sh_out)));
   return p;
@@ -997,7 +1079,7 @@ static int experts_bwd_impl(const nsmoe_experts_args* a, const int32_t* inv, con
     q.dw_a = gr->dw_in;
     q.dw_sh = gr->dw_sh_in;
     q.partial = (float*)(ws + L.p_in);
-    const int64_t ntiles = cdiv(d, 64) * cdiv(2 * H, 64);
+    const int64_t ntiles = cdiv(d, 64) * cdiv(2 * H, 128);
     KernelTimer timer("dw_in", s);
     dw_kernel<DT, 0><<<(unsigned)(gc * ntiles), NT, 0, s>>>(q);
     timer.stop();
@@ -1011,7 +1093,7 @@ static int experts_bwd_impl(const nsmoe_experts_args* a, const int32_t* inv, con
     q.dw_a = gr->dw_out;
     q.dw_sh = gr->dw_sh_out;
     q.partial = (float*)(ws + L.p_out);
-    const int64_t ntiles = cdiv(H, 64) * cdiv(d, 64);
+    const int64_t ntiles = cdiv(H, 128) * cdiv(d, 64);
     KernelTimer timer("dw_out", s);
     dw_kernel<DT, 1><<<(unsigned)(gc * ntiles), NT, 0, s>>>(q);
     timer.stop();
@@ -1054,6 +1136,8 @@ extern "C" int nsmoe_experts_fwd(const nsmoe_experts_args* a, const int32_t* inv
   if (a->n_tokens == 0) return NSMOE_OK;
   NSMOE_REQUIRE(a->x && a->w_in && a->w_out && a->topk_w && a->sorted_ids && a->pad_offsets &&
                     a->counts && inv && out, "experts_fwd: NULL pointer");
+  NSMOE_REQUIRE(a->w_in_packed && a->w_out_packed,
+                "experts_fwd: packed weights missing (nsmoe_pack_weights)");
   const size_t need = nsmoe_experts_fwd_workspace_size(a);
   if (workspace_bytes < need || !workspace) {
     set_error("experts_fwd: workspace %zu B < %zu B", workspace_bytes, need);
@@ -1084,6 +1168,7 @@ extern "C" int nsmoe_experts_bwd(const nsmoe_experts_args* a, const int32_t* inv
                 "experts_bwd: NULL pointer");
   NSMOE_REQUIRE(a->n_shared == 0 || (grads->dw_sh_in && grads->dw_sh_out),
                 "experts_bwd: shared weight gradients missing");
+  NSMOE_REQUIRE(a->w_in_packed, "experts_bwd: packed W_in missing (nsmoe_pack_weights)");
   const size_t need = bwd_layout(a).total;
   if (workspace_bytes < need || !workspace) {
     set_error("experts_bwd: workspace %zu B < %zu B", workspace_bytes, need);
@@ -1098,4 +1183,26 @@ extern "C" int nsmoe_experts_bwd(const nsmoe_experts_args* a, const int32_t* inv
     default:
       return experts_bwd_impl<DT_F32>(a, inv, grad_out, grads, (char*)workspace, s);
   }
+}
+
+extern "C" int nsmoe_pack_sizes(const nsmoe_experts_args* a, size_t* w_in_bytes,
+                                size_t* w_out_bytes) {
+  NSMOE_TRY(validate_dims(a));
+  NSMOE_REQUIRE(w_in_bytes && w_out_bytes, "pack_sizes: NULL output");
+  const PackGeom pg = pack_geom(a->dtype, a->d_model, a->d_hidden, a->n_experts, a->n_shared);
+  *w_in_bytes = pg.in_bytes;
+  *w_out_bytes = pg.out_bytes;
+  return NSMOE_OK;
+}
+
+extern "C" int nsmoe_pack_weights(const nsmoe_experts_args* a, void* w_in_packed,
+                                  void* w_out_packed, void* stream) {
+  NSMOE_TRY(validate(a));
+  NSMOE_REQUIRE(a->w_in && w_in_packed, "pack_weights: NULL W_in or destination");
+  NSMOE_REQUIRE(!w_out_packed || a->w_out, "pack_weights: NULL W_out");
+  NSMOE_REQUIRE(a->n_shared == 0 || (a->w_sh_in && (!w_out_packed || a->w_sh_out)),
+                "pack_weights: shared weights missing");
+  return pack_weights(a->dtype, a->w_in, w_out_packed ? a->w_out : nullptr, a->w_sh_in,
+                      a->w_sh_out, a->n_experts, a->n_shared, a->d_model, a->d_hidden,
+                      w_in_packed, w_out_packed, (hipStream_t)stream);
 }

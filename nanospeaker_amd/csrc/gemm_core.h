@@ -1,9 +1,5 @@
 // MFMA building blocks for the grouped expert GEMMs on gfx950.
 //
-// Operand tiles live in LDS "k-major": one row per output row (A) or output column (B),
-// 32 contraction elements per row -- exactly one MFMA k-step -- padded by 16 bytes so
-// the 16 lanes that read one 16x16 block's fragments hit distinct banks.
-//
 // MFMA contract used everywhere (v_mfma_f32_16x16x32_{bf16,f16}; fp32 issues eight
 // v_mfma_f32_16x16x4_f32 over the same 32 elements):
 //   A fragment: lane l supplies row (l % 16), k elements [8 * (l / 16), +8)
@@ -11,6 +7,16 @@
 //   D:          lane l holds rows 4 * (l / 16) + {0..3} of column (l % 16)
 // A and B always draw their k elements through the same (lane, slot) assignment, so the
 // contraction does not depend on how the hardware orders k inside an instruction.
+//
+// Operand placement:
+//   * Weights reach the MFMAs straight from global memory (L2-resident).  Those whose
+//     contraction index is not contiguous in memory (W_in for GEMM1, W_out for GEMM2)
+//     are first repacked into "fragment order" (pack.hip): the 64 lanes' 16-byte pieces
+//     of one 16 x 32 fragment are one contiguous 1 KiB block, so a fragment is a single
+//     fully coalesced load.
+//   * Token rows (the gathered A operand, shared by all waves of a workgroup) are staged
+//     through LDS in 32-element rows with an XOR swizzle of the 16-byte chunks, so both
+//     the staging stores and the 16-lane fragment reads touch distinct banks.
 #pragma once
 
 #include "nsmoe_common.h"
@@ -24,10 +30,10 @@ template <int DT> struct Geo {
   static constexpr int ES = (int)sizeof(T);  // element bytes: 2 or 4
   static constexpr int VE = 16 / ES;         // elements per 16-byte vector
   static constexpr int KC = 32;              // contraction elements per LDS row
-  static constexpr int ROWB = KC * ES;       // 64 or 128 bytes
-  static constexpr int PITCH = ROWB + 16;    // LDS row pitch (bytes)
-  static constexpr int VPR = ROWB / 16;      // 16-byte vectors per LDS row
+  static constexpr int ROWB = KC * ES;       // 64 or 128 bytes per LDS row
+  static constexpr int VPR = ROWB / 16;      // 16-byte chunks per LDS row
   static constexpr int FRAGB = 8 * ES;       // bytes one lane reads per fragment
+  static constexpr int PKB = 64 * FRAGB;     // bytes of one packed fragment
 };
 
 template <int DT> struct Mma;
@@ -35,6 +41,7 @@ template <int DT> struct Mma;
 template <> struct Mma<DT_BF16> {
   struct Frag { u32x4 v; };
   __device__ static Frag load(const char* p) { return Frag{*(const u32x4*)p}; }
+  __device__ static Frag zero() { return Frag{u32x4{0u, 0u, 0u, 0u}}; }
   __device__ static void run(f32x4& acc, const Frag& a, const Frag& b) {
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a.v),
                                                   __builtin_bit_cast(bf16x8, b.v), acc, 0, 0, 0);
@@ -44,6 +51,7 @@ template <> struct Mma<DT_BF16> {
 template <> struct Mma<DT_F16> {
   struct Frag { u32x4 v; };
   __device__ static Frag load(const char* p) { return Frag{*(const u32x4*)p}; }
+  __device__ static Frag zero() { return Frag{u32x4{0u, 0u, 0u, 0u}}; }
   __device__ static void run(f32x4& acc, const Frag& a, const Frag& b) {
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a.v),
                                                  __builtin_bit_cast(f16x8, b.v), acc, 0, 0, 0);
@@ -55,6 +63,7 @@ template <> struct Mma<DT_F32> {
   __device__ static Frag load(const char* p) {
     return Frag{*(const u32x4*)p, *(const u32x4*)(p + 16)};
   }
+  __device__ static Frag zero() { return Frag{u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}}; }
   __device__ static void run(f32x4& acc, const Frag& a, const Frag& b) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -67,7 +76,39 @@ template <> struct Mma<DT_F32> {
   }
 };
 
-// Fragment of the 16-row block starting at `row0` of a k-major LDS tile.
+// ---- swizzled 32-element LDS rows ---------------------------------------------------------
+//
+// Chunk c (16 bytes) of row r lives at r * ROWB + ((c ^ swz(r)) * 16).  For 64-byte rows
+// (2-byte types) swz mixes bits 1..3 of the row: any 8 consecutive rows then cover the
+// 8 (row parity, chunk) slots of a 128-byte bank line exactly once, and any 16 rows the
+// 16 slots of a 256-byte line.  For 128-byte rows (fp32) swz = (r ^ r >> 3) & 7.
+template <int DT>
+__device__ __forceinline__ int swz(int r) {
+  if constexpr (Geo<DT>::VPR == 4) return ((r >> 1) ^ (r >> 3)) & 3;
+  else return (r ^ (r >> 3)) & 7;
+}
+
+template <int DT>
+__device__ __forceinline__ int sw_off(int r, int c) {
+  return r * Geo<DT>::ROWB + ((c ^ swz<DT>(r)) << 4);
+}
+
+// Fragment of rows [row0, row0 + 16) of a swizzled tile (row0 a multiple of 16).
+template <int DT>
+__device__ __forceinline__ typename Mma<DT>::Frag frag_sw(const char* tile, int row0) {
+  const int l = lane_id();
+  const int r = row0 + (l & 15);
+  if constexpr (Geo<DT>::VPR == 4) {
+    return Mma<DT>::load(tile + sw_off<DT>(r, l >> 4));
+  } else {
+    typename Mma<DT>::Frag f;
+    f.lo = *(const u32x4*)(tile + sw_off<DT>(r, 2 * (l >> 4)));
+    f.hi = *(const u32x4*)(tile + sw_off<DT>(r, 2 * (l >> 4) + 1));
+    return f;
+  }
+}
+
+// Fragment of a padded (unswizzled) k-major LDS tile: rows [row0, +16), k bytes from kbyte0.
 template <int DT>
 __device__ __forceinline__ typename Mma<DT>::Frag frag_at(const char* tile, int pitch,
                                                           int row0, int kbyte0) {
@@ -75,12 +116,61 @@ __device__ __forceinline__ typename Mma<DT>::Frag frag_at(const char* tile, int 
   return Mma<DT>::load(tile + (row0 + (l & 15)) * pitch + kbyte0 + (l >> 4) * Geo<DT>::FRAGB);
 }
 
-__device__ __forceinline__ uint32_t lane_half(const u32x4& v, int c) {
-  uint32_t d = v[c >> 1];
-  return (c & 1) ? (d >> 16) : (d & 0xffffu);
+// Packed weight fragment (nb, kb) of a [n_blocks][k_blocks] fragment-order array.
+template <int DT>
+__device__ __forceinline__ typename Mma<DT>::Frag frag_pk(const char* pk, int nb, int kb,
+                                                          int k_blocks) {
+  return Mma<DT>::load(pk + ((int64_t)nb * k_blocks + kb) * Geo<DT>::PKB +
+                       lane_id() * Geo<DT>::FRAGB);
 }
 
-// ---- staging: global -> registers -> LDS ---------------------------------------------
+// Fragment of a row-major source whose rows are the fragment's 16 columns and whose k
+// index is contiguous: column (n0 + l % 16) is row `row(n)` (nullptr = zero), k elements
+// [k0 + 8 * (l / 16), +8) valid below klim.  `fast`: rows and k0 are 16-byte aligned and
+// klim is a multiple of 8.
+template <int DT, class RowPtr>
+__device__ __forceinline__ typename Mma<DT>::Frag frag_rows(RowPtr row, int n0, int k0,
+                                                            int klim, bool fast) {
+  using T = typename Elem<DT>::T;
+  const int l = lane_id();
+  const T* src = row(n0 + (l & 15));
+  const int k = k0 + (l >> 4) * 8;
+  typename Mma<DT>::Frag f = Mma<DT>::zero();
+  if (!src) return f;
+  if (fast) {
+    if (k < klim) f = Mma<DT>::load((const char*)(src + k));
+  } else {
+    T tmp[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) tmp[e] = (k + e < klim) ? src[k + e] : T(0);
+    __builtin_memcpy(&f, tmp, sizeof(tmp));
+  }
+  return f;
+}
+
+// Transposed store of one 8 x 8 block of 16-bit elements: v[r] holds source row r (8
+// elements), LDS row nb * 8 + c of chunk kb receives element c of every v[r].  Odd n
+// blocks write their rows in the order c ^ 1, so the two n blocks sharing an 8-lane group
+// write rows of opposite parity (distinct halves of a bank line).  The parity only
+// changes v_perm_b32's byte selector (halves 0/1 of each dword) and the row address, so
+// the register operands stay static.
+template <int DT>
+__device__ __forceinline__ void store_trans8(const u32x4 (&v)[8], char* tile, int nb, int kb) {
+  const int odd = nb & 1;
+  constexpr uint32_t kLow = 0x05040100u, kHigh = 0x07060302u;  // low / high halves
+  const uint32_t s_even = odd ? kHigh : kLow, s_odd = odd ? kLow : kHigh;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const uint32_t sel = (c & 1) ? s_odd : s_even;
+    u32x4 o;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      o[q] = __builtin_amdgcn_perm(v[2 * q + 1][c >> 1], v[2 * q][c >> 1], sel);
+    *(u32x4*)(tile + sw_off<DT>(nb * 8 + (c ^ odd), kb)) = o;
+  }
+}
+
+// ---- staging: global -> registers -> swizzled LDS -------------------------------------
 //
 // DirectStage copies NROWS rows of 32 contraction elements whose source is contiguous in
 // k (row r, element k at rowptr(r)[k]).  TransStage builds the same k-major tile from a
@@ -128,39 +218,46 @@ struct DirectStage {
       const int idx = threadIdx.x + i * NT;
       if (NV % NT == 0 || idx < NV) {
         const int r = idx / G::VPR, c = idx % G::VPR;
-        *(u32x4*)(tile + r * G::PITCH + c * 16) = v[i];
+        *(u32x4*)(tile + sw_off<DT>(r, c)) = v[i];
       }
     }
   }
 };
 
-template <int DT, int NCOLS, int NT>
+// T0 is the first thread that takes part: staging several tiles on disjoint thread
+// ranges spreads the work over all waves when one tile has fewer blocks than threads.
+template <int DT, int NCOLS, int NT, int T0 = 0>
 struct TransStage {
   using G = Geo<DT>;
   using T = typename G::T;
-  static constexpr int KB = G::KC / G::VE;  // k blocks per chunk
+  static constexpr int KB = G::KC / G::VE;  // k blocks per chunk (= chunks per LDS row)
   static constexpr int NB = NCOLS / G::VE;  // n blocks per tile
   static constexpr int NBLK = KB * NB;
   static constexpr int PER = (NBLK + NT - 1) / NT;
   u32x4 v[PER][G::VE];
+  __device__ __forceinline__ static int block(int i) { return (int)threadIdx.x - T0 + i * NT; }
+  __device__ __forceinline__ static bool live(int blk) {
+    return blk >= 0 && ((NBLK % NT == 0 && T0 == 0) || blk < NBLK);
+  }
 
   // Source rows k in [k0, k0 + 32) (valid below klim), columns [n0, n0 + NCOLS) (valid
   // below nlim).  scale(k) multiplies the row in fp32 before it is re-rounded; rows
-  // whose rowptr is null load as zero.
+  // whose rowptr is null load as zero.  Block blk covers k block (blk % KB) and n block
+  // (blk / KB): the KB threads of one n block write the KB chunks of the same LDS rows.
   template <class RowPtr, class Scale>
   __device__ __forceinline__ void load(RowPtr rowptr, Scale scale, int k0, int klim, int n0,
                                        int nlim, bool fast) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      const int blk = threadIdx.x + i * NT;
-      const bool live = (NBLK % NT == 0) || blk < NBLK;
-      const int kb = blk / NB, nb = blk % NB;
+      const int blk = block(i);
+      const bool on = live(blk);
+      const int kb = blk % KB, nb = blk / KB;
       const int col = n0 + nb * G::VE;
 #pragma unroll
       for (int r = 0; r < G::VE; ++r) {
         v[i][r] = u32x4{0u, 0u, 0u, 0u};
         const int k = k0 + kb * G::VE + r;
-        if (!live || k >= klim) continue;
+        if (!on || k >= klim) continue;
         const T* src = rowptr(k);
         if (!src) continue;
         T tmp[G::VE];
@@ -189,24 +286,16 @@ struct TransStage {
   __device__ __forceinline__ void store(char* tile) const {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      const int blk = threadIdx.x + i * NT;
-      if (!((NBLK % NT == 0) || blk < NBLK)) continue;
-      const int kb = blk / NB, nb = blk % NB;
-      char* dst = tile + (nb * G::VE) * G::PITCH + kb * G::VE * G::ES;
+      const int blk = block(i);
+      if (!live(blk)) continue;
+      const int kb = blk % KB, nb = blk / KB;
       if constexpr (G::ES == 2) {
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          u32x4 o;
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            o[q] = lane_half(v[i][2 * q], c) | (lane_half(v[i][2 * q + 1], c) << 16);
-          *(u32x4*)(dst + c * G::PITCH) = o;
-        }
+        store_trans8<DT>(v[i], tile, nb, kb);
       } else {
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           u32x4 o{v[i][0][c], v[i][1][c], v[i][2][c], v[i][3][c]};
-          *(u32x4*)(dst + c * G::PITCH) = o;
+          *(u32x4*)(tile + sw_off<DT>(nb * 4 + c, kb)) = o;
         }
       }
     }

@@ -5,27 +5,29 @@
 // `(x @ W).float()` (router.py:69) and the optional exploration noise (router.py:76-77)
 // stay in torch; this file takes the fp32 logits from there.
 //
-// Layout: one token row per lane, 64 rows per workgroup.  The workgroup's [64, E]
-// logit slab is read with coalesced loads into LDS, lane-interleaved (element e of
-// lane l at [e * 64 + l]) so the per-lane passes over a row are bank-conflict free.
-// Each LDS element is a 64-bit (key bits << 32 | expert id) pair, so a swap in the
-// selection is one 64-bit move.
+// Layout: one token row per wavefront, four rows per workgroup.  The wave's lanes load
+// the row (coalesced), reduce max / sum for the softmax and write probs; the row's
+// (key, expert id) pairs are staged in LDS as 64-bit words (key bits << 32 | id) so a
+// swap in the selection is one 64-bit move.  The selection itself is sequential (lane 0
+// of the wave): with one row per wave no lane waits on another row's control flow, and
+// T rows give T independent waves to hide the LDS latency of the sequential passes.
 //
 // Selection has to reproduce torch's CPU topk bit for bit, ties included: the order of
 // equal keys is whatever libstdc++'s nth_element / sort / partial_sort leave (see
-// ATen/native/TopKImpl.h:44-94).  The per-lane routines below restate those published
+// ATen/native/TopKImpl.h:44-94).  The routines below restate those published
 // algorithms (introselect with median-of-three, unguarded Hoare partition, heap select,
-// insertion sort, introsort) on the lane's LDS row.
+// insertion sort, introsort) on the row in LDS.
 #include "nsmoe_capi_internal.h"
 #include "nsmoe_common.h"
 
 namespace nsmoe {
 
-constexpr int ROUTE_ROWS = 64;  // rows per workgroup = lanes per wave
+constexpr int ROUTE_WAVES = 4;  // rows (waves) per workgroup
+constexpr int ROUTE_THREADS = 64 * ROUTE_WAVES;
 
 struct LaneRow {
-  uint64_t* base;  // element i at base[i * ROUTE_ROWS]
-  __device__ __forceinline__ uint64_t& operator[](int i) const { return base[i * ROUTE_ROWS]; }
+  uint64_t* base;  // the row's element i
+  __device__ __forceinline__ uint64_t& operator[](int i) const { return base[i]; }
 };
 
 __device__ __forceinline__ float key_of(uint64_t e) { return __uint_as_float((uint32_t)(e >> 32)); }
@@ -226,6 +228,20 @@ __device__ void topk_select(const LaneRow& a, int n, int k) {
   }
 }
 
+// ---- wave reductions ---------------------------------------------------------------------
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
 // ---- forward ---------------------------------------------------------------------------
 //
 // flags bit 0 (want_probs): training branch, probs = softmax(logits) and the selection
@@ -234,189 +250,184 @@ __device__ void topk_select(const LaneRow& a, int n, int k) {
 // Without want_probs the selection runs on the logits and the gates are
 // softmax(topk logits) (normalize) or softmax(logits)[idx] (router.py:83-92).
 // With want_probs and normalize and k > 1 the gates are p / sum(p) (router.py:96-97).
+// E <= 128: each lane holds row elements lane and lane + 64.
 template <int DT>
-__global__ void __launch_bounds__(ROUTE_ROWS)
+__global__ void __launch_bounds__(ROUTE_THREADS)
 route_fwd_kernel(const float* __restrict__ logits, int64_t T, int E, int k, int flags,
                  typename Elem<DT>::T* __restrict__ topk_w, int64_t* __restrict__ topk_idx,
                  float* __restrict__ probs) {
-  extern __shared__ uint64_t lds_q[];
-  const int lane = threadIdx.x;
-  const int64_t row0 = (int64_t)blockIdx.x * ROUTE_ROWS;
-  const int rows = (int)min((int64_t)ROUTE_ROWS, T - row0);
+  extern __shared__ uint64_t lds_q[];  // [ROUTE_WAVES][E]
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * ROUTE_WAVES + wave;
+  const bool active = row < T;
   const bool want_probs = flags & 1;
   const bool normalize = flags & 2;
+  uint64_t* q = lds_q + wave * E;
+  const bool has0 = lane < E, has1 = lane + 64 < E;
 
-  // Coalesced slab load: element (r, e) of the slab lands at [e * 64 + r].
-  const float* slab = logits + row0 * E;
-  for (int i = lane; i < rows * E; i += ROUTE_ROWS) {
-    int r = i / E, e = i - r * E;
-    lds_q[e * ROUTE_ROWS + r] = pack(slab[i], e);
+  float v0 = -INFINITY, v1 = -INFINITY;
+  if (active) {
+    const float* lrow = logits + row * E;
+    if (has0) v0 = lrow[lane];
+    if (has1) v1 = lrow[lane + 64];
+  }
+  // Row max (NaN-propagating, like torch's softmax) and sum of exp.
+  const bool nan_here = (has0 && __builtin_isnan(v0)) || (has1 && __builtin_isnan(v1));
+  const bool any_nan = __ballot(nan_here) != 0ull;
+  float m = wave_max(fmaxf(v0, v1));
+  if (any_nan) m = __uint_as_float(0x7fc00000u);
+  float row_inv_sum = 0.0f;
+  float k0 = v0, k1 = v1;
+  if (want_probs || !normalize) {
+    const float e0 = has0 ? expf(v0 - m) : 0.0f;
+    const float e1 = has1 ? expf(v1 - m) : 0.0f;
+    row_inv_sum = 1.0f / wave_sum(e0 + e1);
+    if (want_probs) {
+      k0 = e0 * row_inv_sum;
+      k1 = e1 * row_inv_sum;
+      if (active) {
+        float* prow = probs + row * E;
+        if (has0) prow[lane] = k0;
+        if (has1) prow[lane + 64] = k1;
+      }
+    }
+  }
+  if (active) {
+    if (has0) q[lane] = pack(k0, lane);
+    if (has1) q[lane + 64] = pack(k1, lane + 64);
   }
   __syncthreads();
-
-  LaneRow a{lds_q + lane};
-  const bool active = lane < rows;
-  float row_max = 0.0f, row_inv_sum = 0.0f;
-  if (active) {
-    // max / sum over the full row: needed for probs (train) and for the eval
-    // normalize=False branch.
-    if (want_probs || !normalize) {
-      float m = -INFINITY;
-      bool any_nan = false;
-      for (int e = 0; e < E; ++e) {
-        float v = key_of(a[e]);
-        any_nan |= __builtin_isnan(v);
-        m = fmaxf(m, v);
-      }
-      if (any_nan) m = __uint_as_float(0x7fc00000u);
-      float s = 0.0f;
-      for (int e = 0; e < E; ++e) s += expf(key_of(a[e]) - m);
-      row_max = m;
-      row_inv_sum = 1.0f / s;
-      if (want_probs) {
-        for (int e = 0; e < E; ++e) a[e] = pack(expf(key_of(a[e]) - m) * row_inv_sum, e);
-      }
-    }
-  }
-  if (want_probs) {
-    __syncthreads();
-    float* prow = probs + row0 * E;
-    for (int i = lane; i < rows * E; i += ROUTE_ROWS) {
-      int r = i / E, e = i - r * E;
-      prow[i] = key_of(lds_q[e * ROUTE_ROWS + r]);
-    }
-    __syncthreads();
-  }
+  if (active && lane == 0) topk_select(LaneRow{q}, E, k);
+  __syncthreads();
   if (!active) return;
 
-  topk_select(a, E, k);
-
+  // Lane j < k handles output j (and j + 64 when k > 64).
   using OutT = typename Elem<DT>::T;
-  const int64_t row = row0 + lane;
   int64_t* idx_out = topk_idx + row * k;
   OutT* w_out = topk_w + row * k;
-  for (int j = 0; j < k; ++j) idx_out[j] = id_of(a[j]);
-
+  const bool o0 = lane < k, o1 = lane + 64 < k;
+  const float s0 = o0 ? key_of(q[lane]) : 0.0f, s1 = o1 ? key_of(q[lane + 64]) : 0.0f;
+  if (o0) idx_out[lane] = id_of(q[lane]);
+  if (o1) idx_out[lane + 64] = id_of(q[lane + 64]);
+  float w0 = s0, w1 = s1;
   if (want_probs) {
     if (normalize && k > 1) {
-      float s = 0.0f;
-      for (int j = 0; j < k; ++j) s += key_of(a[j]);
-      for (int j = 0; j < k; ++j) w_out[j] = Elem<DT>::from_f(key_of(a[j]) / s);
-    } else {
-      for (int j = 0; j < k; ++j) w_out[j] = Elem<DT>::from_f(key_of(a[j]));
+      const float S = wave_sum(s0 + s1);
+      w0 = s0 / S;
+      w1 = s1 / S;
     }
   } else if (normalize) {
-    float m = -INFINITY;
-    for (int j = 0; j < k; ++j) m = fmaxf(m, key_of(a[j]));
-    float s = 0.0f;
-    for (int j = 0; j < k; ++j) s += expf(key_of(a[j]) - m);
-    float inv = 1.0f / s;
-    for (int j = 0; j < k; ++j) w_out[j] = Elem<DT>::from_f(expf(key_of(a[j]) - m) * inv);
+    const float mk = wave_max(fmaxf(o0 ? s0 : -INFINITY, o1 ? s1 : -INFINITY));
+    const float e0 = o0 ? expf(s0 - mk) : 0.0f, e1 = o1 ? expf(s1 - mk) : 0.0f;
+    const float inv = 1.0f / wave_sum(e0 + e1);
+    w0 = e0 * inv;
+    w1 = e1 * inv;
   } else {
-    for (int j = 0; j < k; ++j)
-      w_out[j] = Elem<DT>::from_f(expf(key_of(a[j]) - row_max) * row_inv_sum);
+    w0 = expf(s0 - m) * row_inv_sum;
+    w1 = expf(s1 - m) * row_inv_sum;
   }
+  if (o0) w_out[lane] = Elem<DT>::from_f(w0);
+  if (o1) w_out[lane + 64] = Elem<DT>::from_f(w1);
 }
 
 // ---- backward --------------------------------------------------------------------------
 //
-// d(logits) for the same three branches, in fp32:
+// d(logits) for the same three branches, in fp32, one row per wave:
 //   train: w = p_sel / S (normalize, k > 1)  ->  dp_j = (dw_j - sum_i dw_i w_i) / S
 //          dprobs = grad_probs (aux loss, may be absent) + scatter(dp)
 //          dlogits = p * (dprobs - sum_e p_e dprobs_e)
 //   eval normalize:   w = softmax(l_sel) -> dl_sel = w * (dw - sum w dw)
 //   eval !normalize:  w = softmax(l)[idx] -> softmax backward of scatter(dw)
-// `src` holds probs for the train branch and logits otherwise.
+// `src` holds probs for the train branch and logits otherwise.  Ids outside [0, E)
+// (not produced by route_fwd) give the row a zero gradient.
 template <int DT>
-__global__ void __launch_bounds__(ROUTE_ROWS)
+__global__ void __launch_bounds__(ROUTE_THREADS)
 route_bwd_kernel(const float* __restrict__ src, const int64_t* __restrict__ topk_idx,
                  const typename Elem<DT>::T* __restrict__ grad_w,
                  const float* __restrict__ grad_probs, int64_t T, int E, int k, int flags,
                  float* __restrict__ grad_logits) {
   extern __shared__ float lds_f[];
-  float* s_src = lds_f;                       // [E][64]
-  float* s_g = lds_f + E * ROUTE_ROWS;        // [E][64] running d(probs) / d(logits)
-  const int lane = threadIdx.x;
-  const int64_t row0 = (int64_t)blockIdx.x * ROUTE_ROWS;
-  const int rows = (int)min((int64_t)ROUTE_ROWS, T - row0);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * ROUTE_WAVES + wave;
+  if (row >= T) return;  // no workgroup barriers below: each wave works alone
   const bool want_probs = flags & 1;
   const bool normalize = flags & 2;
+  float* sv = lds_f + wave * 2 * E;  // the row's src values
+  float* sg = sv + E;                // running d(probs) or d(logits) row
+  const bool has0 = lane < E, has1 = lane + 64 < E;
+  const float* srow = src + row * E;
+  const float x0 = has0 ? srow[lane] : 0.0f, x1 = has1 ? srow[lane + 64] : 0.0f;
+  float g0 = 0.0f, g1 = 0.0f;
+  if (grad_probs && want_probs) {
+    const float* gp = grad_probs + row * E;
+    if (has0) g0 = gp[lane];
+    if (has1) g1 = gp[lane + 64];
+  }
+  if (has0) { sv[lane] = x0; sg[lane] = want_probs ? g0 : 0.0f; }
+  if (has1) { sv[lane + 64] = x1; sg[lane + 64] = want_probs ? g1 : 0.0f; }
+  const bool o0 = lane < k, o1 = lane + 64 < k;
+  int64_t i0 = o0 ? topk_idx[row * k + lane] : 0, i1 = o1 ? topk_idx[row * k + lane + 64] : 0;
+  const bool bad = (o0 && (i0 < 0 || i0 >= E)) || (o1 && (i1 < 0 || i1 >= E));
+  float* drow = grad_logits + row * E;
+  if (__ballot(bad) != 0ull) {
+    if (has0) drow[lane] = 0.0f;
+    if (has1) drow[lane + 64] = 0.0f;
+    return;
+  }
+  const float d0 = o0 ? Elem<DT>::to_f(grad_w[row * k + lane]) : 0.0f;
+  const float d1 = o1 ? Elem<DT>::to_f(grad_w[row * k + lane + 64]) : 0.0f;
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  const float s_0 = o0 ? sv[i0] : 0.0f, s_1 = o1 ? sv[i1] : 0.0f;  // selected src values
 
-  for (int i = lane; i < rows * E; i += ROUTE_ROWS) {
-    int r = i / E, e = i - r * E;
-    s_src[e * ROUTE_ROWS + r] = src[row0 * E + i];
-    s_g[e * ROUTE_ROWS + r] = grad_probs ? grad_probs[row0 * E + i] : 0.0f;
-  }
-  __syncthreads();
-
-  bool ids_ok = true;
-  if (lane < rows) {
-    const int64_t* idx = topk_idx + (row0 + lane) * k;
-    for (int j = 0; j < k; ++j) ids_ok &= idx[j] >= 0 && idx[j] < E;
-  }
-  if (lane < rows && !ids_ok) {  // ids not from route_fwd: no gradient, no stray access
-    float* sg = s_g + lane;
-    for (int e = 0; e < E; ++e) sg[e * ROUTE_ROWS] = 0.0f;
-  }
-  if (lane < rows && ids_ok) {
-    const int64_t row = row0 + lane;
-    const int64_t* idx = topk_idx + row * k;
-    const typename Elem<DT>::T* dw = grad_w + row * k;
-    float* sv = s_src + lane;
-    float* sg = s_g + lane;
-    if (want_probs) {
-      float S = 0.0f, dot = 0.0f;
-      const bool renorm = normalize && k > 1;
-      if (renorm) {
-        for (int j = 0; j < k; ++j) S += sv[idx[j] * ROUTE_ROWS];
-        for (int j = 0; j < k; ++j)
-          dot += Elem<DT>::to_f(dw[j]) * (sv[idx[j] * ROUTE_ROWS] / S);
-      }
-      for (int j = 0; j < k; ++j) {
-        float d = Elem<DT>::to_f(dw[j]);
-        sg[idx[j] * ROUTE_ROWS] += renorm ? (d - dot) / S : d;
-      }
-      float pd = 0.0f;
-      for (int e = 0; e < E; ++e) pd += sv[e * ROUTE_ROWS] * sg[e * ROUTE_ROWS];
-      for (int e = 0; e < E; ++e)
-        sg[e * ROUTE_ROWS] = sv[e * ROUTE_ROWS] * (sg[e * ROUTE_ROWS] - pd);
-    } else if (normalize) {
-      float m = -INFINITY;
-      for (int j = 0; j < k; ++j) m = fmaxf(m, sv[idx[j] * ROUTE_ROWS]);
-      float s = 0.0f;
-      for (int j = 0; j < k; ++j) s += expf(sv[idx[j] * ROUTE_ROWS] - m);
-      float dot = 0.0f;
-      for (int j = 0; j < k; ++j)
-        dot += expf(sv[idx[j] * ROUTE_ROWS] - m) / s * Elem<DT>::to_f(dw[j]);
-      for (int e = 0; e < E; ++e) sg[e * ROUTE_ROWS] = 0.0f;
-      for (int j = 0; j < k; ++j) {
-        float w = expf(sv[idx[j] * ROUTE_ROWS] - m) / s;
-        sg[idx[j] * ROUTE_ROWS] += w * (Elem<DT>::to_f(dw[j]) - dot);
-      }
-    } else {
-      float m = -INFINITY;
-      for (int e = 0; e < E; ++e) m = fmaxf(m, sv[e * ROUTE_ROWS]);
-      float s = 0.0f;
-      for (int e = 0; e < E; ++e) s += expf(sv[e * ROUTE_ROWS] - m);
-      float inv = 1.0f / s;
-      for (int e = 0; e < E; ++e) sg[e * ROUTE_ROWS] = 0.0f;
-      for (int j = 0; j < k; ++j) sg[idx[j] * ROUTE_ROWS] += Elem<DT>::to_f(dw[j]);
-      float pd = 0.0f;
-      for (int e = 0; e < E; ++e) pd += expf(sv[e * ROUTE_ROWS] - m) * inv * sg[e * ROUTE_ROWS];
-      for (int e = 0; e < E; ++e) {
-        float p = expf(sv[e * ROUTE_ROWS] - m) * inv;
-        sg[e * ROUTE_ROWS] = p * (sg[e * ROUTE_ROWS] - pd);
-      }
+  float p0, p1;  // softmax probabilities of this lane's row elements
+  if (want_probs) {
+    const bool renorm = normalize && k > 1;
+    float a0 = d0, a1 = d1;
+    if (renorm) {
+      const float S = wave_sum(s_0 + s_1);
+      const float dot = wave_sum(d0 * (s_0 / S) + d1 * (s_1 / S));
+      a0 = (d0 - dot) / S;
+      a1 = (d1 - dot) / S;
     }
+    __builtin_amdgcn_wave_barrier();
+    if (o0) sg[i0] += a0;  // ids in a row are distinct: no two lanes hit one slot
+    if (o1) sg[i1] += a1;
+    p0 = x0;
+    p1 = x1;
+  } else if (normalize) {
+    const float mk = wave_max(fmaxf(o0 ? s_0 : -INFINITY, o1 ? s_1 : -INFINITY));
+    const float e0 = o0 ? expf(s_0 - mk) : 0.0f, e1 = o1 ? expf(s_1 - mk) : 0.0f;
+    const float inv = 1.0f / wave_sum(e0 + e1);
+    const float w0 = e0 * inv, w1 = e1 * inv;
+    const float dot = wave_sum(w0 * d0 + w1 * d1);
+    __builtin_amdgcn_wave_barrier();
+    if (o0) sg[i0] = w0 * (d0 - dot);
+    if (o1) sg[i1] = w1 * (d1 - dot);
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    if (has0) drow[lane] = sg[lane];
+    if (has1) drow[lane + 64] = sg[lane + 64];
+    return;
+  } else {
+    const float m = wave_max(fmaxf(has0 ? x0 : -INFINITY, has1 ? x1 : -INFINITY));
+    const float e0 = has0 ? expf(x0 - m) : 0.0f, e1 = has1 ? expf(x1 - m) : 0.0f;
+    const float inv = 1.0f / wave_sum(e0 + e1);
+    p0 = e0 * inv;
+    p1 = e1 * inv;
+    __builtin_amdgcn_wave_barrier();
+    if (o0) sg[i0] += d0;
+    if (o1) sg[i1] += d1;
   }
-  __syncthreads();
-  for (int i = lane; i < rows * E; i += ROUTE_ROWS) {
-    int r = i / E, e = i - r * E;
-    grad_logits[row0 * E + i] = s_g[e * ROUTE_ROWS + r];
-  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  const float q0 = has0 ? sg[lane] : 0.0f, q1 = has1 ? sg[lane + 64] : 0.0f;
+  const float pd = wave_sum((has0 ? p0 * q0 : 0.0f) + (has1 ? p1 * q1 : 0.0f));
+  if (has0) drow[lane] = p0 * (q0 - pd);
+  if (has1) drow[lane + 64] = p1 * (q1 - pd);
 }
 
-constexpr int ROUTE_MAX_EXPERTS = 128;  // 64 rows x 128 x 8 B = 64 KiB of LDS
+constexpr int ROUTE_MAX_EXPERTS = 128;  // two row elements per lane
 
 }  // namespace nsmoe
 
@@ -433,8 +444,8 @@ extern "C" int nsmoe_route_fwd(const float* logits, int64_t n_tokens, int32_t n_
   NSMOE_REQUIRE(!(flags & 1) || probs, "route_fwd: probs requested but NULL");
   if (n_tokens == 0) return NSMOE_OK;
   NSMOE_REQUIRE(logits && topk_w && topk_idx, "route_fwd: NULL pointer");
-  dim3 grid((unsigned)cdiv(n_tokens, ROUTE_ROWS)), block(ROUTE_ROWS);
-  size_t lds = (size_t)n_experts * ROUTE_ROWS * sizeof(uint64_t);
+  dim3 grid((unsigned)cdiv(n_tokens, ROUTE_WAVES)), block(ROUTE_THREADS);
+  size_t lds = (size_t)n_experts * ROUTE_WAVES * sizeof(uint64_t);
   hipStream_t s = (hipStream_t)stream;
   KernelTimer timer("route_fwd", s);
   switch (w_dtype) {
@@ -467,8 +478,8 @@ extern "C" int nsmoe_route_bwd(const float* src, const int64_t* topk_idx, const 
   NSMOE_REQUIRE(top_k >= 1 && top_k <= n_experts, "route_bwd: bad top_k %d", top_k);
   if (n_tokens == 0) return NSMOE_OK;
   NSMOE_REQUIRE(src && topk_idx && grad_w && grad_logits, "route_bwd: NULL pointer");
-  dim3 grid((unsigned)cdiv(n_tokens, ROUTE_ROWS)), block(ROUTE_ROWS);
-  size_t lds = (size_t)n_experts * ROUTE_ROWS * sizeof(float) * 2;
+  dim3 grid((unsigned)cdiv(n_tokens, ROUTE_WAVES)), block(ROUTE_THREADS);
+  size_t lds = (size_t)n_experts * ROUTE_WAVES * sizeof(float) * 2;
   hipStream_t s = (hipStream_t)stream;
   switch (w_dtype) {
     case DT_BF16:

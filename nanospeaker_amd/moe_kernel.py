@@ -20,6 +20,7 @@ There is no fallback: on a GPU tensor a missing library raises.
 
 from __future__ import annotations
 
+import ctypes
 from typing import Optional
 
 import torch
@@ -237,6 +238,20 @@ def _c(t: Optional[Tensor]) -> Optional[Tensor]:
     return None if t is None else t.contiguous()
 
 
+def _pack(args: nat.ExpertsArgs, device, with_out: bool = True):
+    """Weights in MFMA fragment order (nsmoe_pack_weights): (packed W_in, packed W_out)."""
+    lib = nat.lib()
+    nb_in, nb_out = ctypes.c_size_t(), ctypes.c_size_t()
+    nat.check(lib.nsmoe_pack_sizes(args, ctypes.byref(nb_in), ctypes.byref(nb_out)),
+              "nsmoe_pack_sizes")
+    p_in = torch.empty(nb_in.value, dtype=torch.uint8, device=device)
+    p_out = torch.empty(nb_out.value if with_out else 0, dtype=torch.uint8, device=device)
+    nat.check(lib.nsmoe_pack_weights(args, p_in.data_ptr(), _p(p_out), _stream()),
+              "nsmoe_pack_weights")
+    args.w_in_packed, args.w_out_packed = p_in.data_ptr(), _p(p_out)
+    return p_in, p_out
+
+
 def _check_activation(activation: str) -> None:
     if activation not in KERNEL_ACTIVATIONS:
         raise ValueError(
@@ -246,6 +261,7 @@ def _check_activation(activation: str) -> None:
 
 def _experts_forward(x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out,
                      topk_w, sorted_ids, pad_offsets, counts, inv_ids, activation):
+    """(out, packed W_in); the packed W_in is what the backward needs again."""
     x, w_in, w_out = x.contiguous(), w_in.contiguous(), w_out.contiguous()
     w_sh_in, w_sh_out = _c(w_sh_in), _c(w_sh_out)
     b_in, b_out, b_sh_in, b_sh_out = _c(b_in), _c(b_out), _c(b_sh_in), _c(b_sh_out)
@@ -253,19 +269,21 @@ def _experts_forward(x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_
     n, d = x.shape
     out = torch.empty((n, d), dtype=x.dtype, device=x.device)
     if n == 0:
-        return out
+        return out, x.new_empty(0, dtype=torch.uint8)
     args = _args(x, w_in, w_out, topk_w, b_in, b_out, w_sh_in, w_sh_out, b_sh_in, b_sh_out,
                  sorted_ids, pad_offsets, counts, activation)
+    p_in, p_out = _pack(args, x.device)
     lib = nat.lib()
     ws = _ws(lib.nsmoe_experts_fwd_workspace_size(args), x.device)
     nat.check(lib.nsmoe_experts_fwd(args, _p(inv_ids), out.data_ptr(), ws.data_ptr(),
                                     ws.numel(), _stream()), "nsmoe_experts_fwd")
-    return out
+    return out, p_in
 
 
 def _experts_backward(grad_out, x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in,
                       topk_w, sorted_ids, pad_offsets, counts, inv_ids, activation,
-                      need_db_in, need_db_out, need_db_sh_in, need_db_sh_out):
+                      need_db_in, need_db_out, need_db_sh_in, need_db_sh_out,
+                      w_in_packed: Optional[Tensor] = None):
     grad_out = grad_out.to(x.dtype).contiguous()
     x, w_in, w_out = x.contiguous(), w_in.contiguous(), w_out.contiguous()
     w_sh_in, w_sh_out = _c(w_sh_in), _c(w_sh_out)
@@ -295,6 +313,10 @@ def _experts_backward(grad_out, x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, 
         dx=_p(dx), dw_in=_p(dw_in), dw_out=_p(dw_out), dw_sh_in=_p(dw_sh_in),
         dw_sh_out=_p(dw_sh_out), dtopk_w=_p(dtw), db_in=_p(db_in), db_out=_p(db_out),
         db_sh_in=_p(db_sh_in), db_sh_out=_p(db_sh_out))
+    if w_in_packed is not None and w_in_packed.numel():
+        args.w_in_packed = w_in_packed.data_ptr()
+    else:
+        w_in_packed, _ = _pack(args, dev, with_out=False)
     lib = nat.lib()
     ws = _ws(lib.nsmoe_experts_bwd_workspace_size(args), dev)
     nat.check(lib.nsmoe_experts_bwd(args, _p(inv_ids), grad_out.data_ptr(), grads,
@@ -310,8 +332,9 @@ def moe_experts(x: Tensor, w_in: Tensor, w_out: Tensor, topk_w: Tensor,
                 expert_ids: Tensor, pad_offsets: Tensor, counts: Tensor, n_post_pad: Tensor,
                 inv_ids: Tensor, activation: str) -> Tensor:
     """The routed experts on pre-dispatched pairs: out[t] = sum_j w * expert_j(x[t])."""
-    return _experts_forward(x, w_in, w_out, None, None, b_in, b_out, None, None, topk_w,
-                            sorted_ids, pad_offsets, counts, inv_ids, activation)
+    out, _ = _experts_forward(x, w_in, w_out, None, None, b_in, b_out, None, None, topk_w,
+                              sorted_ids, pad_offsets, counts, inv_ids, activation)
+    return out
 
 
 @moe_experts.register_fake
@@ -383,17 +406,32 @@ def moe_block(x: Tensor, w_in: Tensor, w_out: Tensor, w_sh_in: Optional[Tensor],
               w_sh_out: Optional[Tensor], b_in: Optional[Tensor], b_out: Optional[Tensor],
               b_sh_in: Optional[Tensor], b_sh_out: Optional[Tensor], topk_w: Tensor,
               sorted_ids: Tensor, pad_offsets: Tensor, counts: Tensor, inv_ids: Tensor,
-              activation: str) -> Tensor:
-    """Routed plus shared experts: out[t] = sum_j w_tj * expert_j(x[t]) + sum_s shared_s(x[t])."""
+              activation: str) -> tuple[Tensor, Tensor]:
+    """
+    Routed plus shared experts: out[t] = sum_j w_tj * expert_j(x[t]) + sum_s shared_s(x[t]).
+    Returns (out, W_in packed in fragment order); the second output only carries the
+    packed weights to the backward.
+    """
     return _experts_forward(x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in,
                             b_sh_out, topk_w, sorted_ids, pad_offsets, counts, inv_ids,
                             activation)
 
 
+def _packed_in_bytes(x, w_in, w_sh_in) -> int:
+    e, d, h2 = w_in.shape
+    h = h2 // 2
+    hp16 = -(-h // 16) * 16
+    hp = 64 if hp16 <= 64 else 128 if hp16 <= 128 else 256
+    groups = e + (0 if w_sh_in is None else w_sh_in.shape[0])
+    es = 4 if x.dtype == torch.float32 else 2
+    return groups * (2 * hp // 16) * (-(-d // 32)) * 64 * 8 * es
+
+
 @moe_block.register_fake
 def _(x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out, topk_w, sorted_ids,
       pad_offsets, counts, inv_ids, activation):
-    return x.new_empty(x.shape)
+    n = _packed_in_bytes(x, w_in, w_sh_in) if x.shape[0] else 0
+    return x.new_empty(x.shape), x.new_empty((n,), dtype=torch.uint8)
 
 
 @torch.library.custom_op("nsmoe::moe_block_bwd", mutates_args=())
@@ -402,19 +440,21 @@ def moe_block_bwd(grad_out: Tensor, x: Tensor, w_in: Tensor, w_out: Tensor,
                   b_in: Optional[Tensor], b_out: Optional[Tensor], b_sh_in: Optional[Tensor],
                   topk_w: Tensor, sorted_ids: Tensor, pad_offsets: Tensor, counts: Tensor,
                   inv_ids: Tensor, activation: str, need_db_in: bool, need_db_out: bool,
-                  need_db_sh_in: bool, need_db_sh_out: bool) -> tuple[
+                  need_db_sh_in: bool, need_db_sh_out: bool,
+                  w_in_packed: Optional[Tensor] = None) -> tuple[
                       Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor,
                       Tensor]:
     """(dx, dW_in, dW_out, dW_sh_in, dW_sh_out, dtopk_w, db_in, db_out, db_sh_in, db_sh_out)."""
     return _experts_backward(grad_out, x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in,
                              topk_w, sorted_ids, pad_offsets, counts, inv_ids, activation,
-                             need_db_in, need_db_out, need_db_sh_in, need_db_sh_out)
+                             need_db_in, need_db_out, need_db_sh_in, need_db_sh_out,
+                             w_in_packed)
 
 
 @moe_block_bwd.register_fake
 def _(grad_out, x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, topk_w, sorted_ids,
       pad_offsets, counts, inv_ids, activation, need_db_in, need_db_out, need_db_sh_in,
-      need_db_sh_out):
+      need_db_sh_out, w_in_packed=None):
     e, d, h2 = w_in.shape
     s = 0 if w_sh_in is None else w_sh_in.shape[0]
     emp = x.new_empty(0)
@@ -430,15 +470,18 @@ def _(grad_out, x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, topk_w,
 def _moe_block_setup(ctx, inputs, output):
     (x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out, topk_w, sorted_ids,
      pad_offsets, counts, inv_ids, activation) = inputs
+    out, w_in_packed = output
+    ctx.mark_non_differentiable(w_in_packed)
     ctx.has = [t is not None for t in (w_sh_in, b_in, b_out, b_sh_in, b_sh_out)]
     opt = [t for t in (w_sh_in, w_sh_out, b_in, b_out, b_sh_in) if t is not None]
     ctx.save_for_backward(x, w_in, w_out, topk_w, sorted_ids, pad_offsets, counts, inv_ids,
-                          *opt)
+                          w_in_packed, *opt)
     ctx.activation = activation
 
 
-def _moe_block_backward(ctx, grad_out):
-    (x, w_in, w_out, topk_w, sorted_ids, pad_offsets, counts, inv_ids, *opt) = ctx.saved_tensors
+def _moe_block_backward(ctx, grad_out, grad_packed):
+    (x, w_in, w_out, topk_w, sorted_ids, pad_offsets, counts, inv_ids, w_in_packed,
+     *opt) = ctx.saved_tensors
     has_sh, has_b_in, has_b_out, has_b_sh_in, has_b_sh_out = ctx.has
     it = iter(opt)
     w_sh_in = next(it) if has_sh else None
@@ -450,7 +493,7 @@ def _moe_block_backward(ctx, grad_out):
      db_sh_out) = moe_block_bwd(grad_out, x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out,
                                 b_sh_in, topk_w, sorted_ids, pad_offsets, counts, inv_ids,
                                 ctx.activation, has_b_in, has_b_out, has_b_sh_in,
-                                has_b_sh_out)
+                                has_b_sh_out, w_in_packed)
     return (dx, dw_in, dw_out,
             dw_sh_in if has_sh else None, dw_sh_out if has_sh else None,
             db_in if has_b_in else None, db_out if has_b_out else None,
@@ -485,7 +528,7 @@ def fused_moe_block_forward(x, w_in, w_out, topk_w, topk_idx, b_in, b_out, w_sh_
     _check_activation(activation)
     sids, eids, offs, counts, npp, inv = moe_dispatch(topk_idx, w_in.shape[0])
     cast = lambda t: None if t is None else t.to(x.dtype)
-    out = moe_block(x, cast(w_in), cast(w_out), cast(w_sh_in), cast(w_sh_out), cast(b_in),
-                    cast(b_out), cast(b_sh_in), cast(b_sh_out), topk_w.to(x.dtype), sids,
-                    offs, counts, inv, activation)
+    out, _ = moe_block(x, cast(w_in), cast(w_out), cast(w_sh_in), cast(w_sh_out), cast(b_in),
+                       cast(b_out), cast(b_sh_in), cast(b_sh_out), topk_w.to(x.dtype), sids,
+                       offs, counts, inv, activation)
     return out, counts

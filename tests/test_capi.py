@@ -25,15 +25,15 @@ def declared_functions():
 def test_library_loads_and_exports_every_declared_symbol():
     lib = nat.lib()
     names = declared_functions()
-    assert len(names) >= 14
+    assert len(names) >= 16
     for name in names:
         assert hasattr(lib, name), f"{name} declared in nsmoe.h but not exported"
         assert name in nat.SIGNATURES, f"{name} has no ctypes signature"
 
 
 def test_struct_layouts_match_the_header():
-    # nsmoe_experts_args: 2 x i32, i64, 6 x i32, i64, then 13 pointers
-    assert ctypes.sizeof(nat.ExpertsArgs) == 4 * 2 + 8 + 4 * 6 + 8 + 8 * 13
+    # nsmoe_experts_args: 2 x i32, i64, 6 x i32, i64, then 15 pointers
+    assert ctypes.sizeof(nat.ExpertsArgs) == 4 * 2 + 8 + 4 * 6 + 8 + 8 * 15
     assert nat.ExpertsArgs.x.offset == 48
     assert ctypes.sizeof(nat.ExpertsGrads) == 8 * 10
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
@@ -59,7 +59,25 @@ def test_workspace_sizes_are_positive_and_grow():
     bwd = nat.lib().nsmoe_experts_bwd_workspace_size(a)
     assert fwd >= (49152 + 2 * 8192) * 576 * 2
     assert bwd > fwd
-    assert nat.lib().nsmoe_dispatch_workspace_size(49152, 76) == 192 * 76 * 4
+    # [chunks, E] int32 histograms; chunks of 1024 pairs while E <= 256, else 256
+    assert nat.lib().nsmoe_dispatch_workspace_size(49152, 76) == 48 * 76 * 4
+    assert nat.lib().nsmoe_dispatch_workspace_size(49152, 1000) == 192 * 1000 * 4
+
+
+def test_pack_sizes_match_the_fragment_layout():
+    a = nat.ExpertsArgs(dtype=0, activation=0, n_tokens=8192, d_model=576, d_hidden=128,
+                        n_experts=76, n_shared=2, top_k=6, l_cap=mk._l_cap(49152, 76))
+    nin, nout = ctypes.c_size_t(), ctypes.c_size_t()
+    assert nat.lib().nsmoe_pack_sizes(a, ctypes.byref(nin), ctypes.byref(nout)) == 0
+    frag = 64 * 8 * 2                      # one 16 x 32 bf16 fragment
+    assert nin.value == 78 * 16 * 18 * frag  # 2 * 128 / 16 column blocks, 576 / 32 k blocks
+    assert nout.value == 78 * 36 * 4 * frag  # 576 / 16 column blocks, 128 / 32 k blocks
+    w_sh = torch_empty = None
+    import torch
+    x = torch.empty(8192, 576, dtype=torch.bfloat16)
+    w_in = torch.empty(76, 576, 256, dtype=torch.bfloat16)
+    w_sh_in = torch.empty(2, 576, 256, dtype=torch.bfloat16)
+    assert mk._packed_in_bytes(x, w_in, w_sh_in) == nin.value
 
 
 @pytest.mark.parametrize("call,needle", [

@@ -57,8 +57,9 @@ def gpu_fwd_bwd(p, x, gout, topk_w, topk_idx, act, with_grad=True):
     xg, twg = dev(x), dev(topk_w)
     P = {n: dev(getattr(p, n)) for n in ("W_in", "W_out") + GRAD_NAMES[2:]}
     sids, eids, offs, counts, npp, inv = mk.moe_dispatch(topk_idx.to(DEV), p.W_in.shape[0])
-    out = mk.moe_block(xg, P["W_in"], P["W_out"], P["W_sh_in"], P["W_sh_out"], P["b_in"],
-                       P["b_out"], P["b_sh_in"], P["b_sh_out"], twg, sids, offs, counts, inv, act)
+    out, _ = mk.moe_block(xg, P["W_in"], P["W_out"], P["W_sh_in"], P["W_sh_out"], P["b_in"],
+                          P["b_out"], P["b_sh_in"], P["b_sh_out"], twg, sids, offs, counts, inv,
+                          act)
     grads = {}
     if with_grad:
         (out.float() * gout.to(DEV).float()).sum().backward()
