@@ -1,8 +1,8 @@
 """
-Benchmark: nanoSpeaker MoE block on one MI355X (BASELINE.json's metric and configs).
+Benchmark: nanoSpeaker MoE block on one MI355X (tokens/s, fwd and fwd+bwd, at T = 8192 bf16).
 
 A step is one forward + backward of the MoE block over one batch of synthetic tokens
-(T = 8192, bf16, train mode, loss = (out * g).sum() + aux_loss):
+(the training-shape workload: T = 8192, bf16, train mode, loss = (out * g).sum() + aux_loss):
 router GEMM, the HIP route / dispatch / grouped-expert / combine kernels, and the HIP
 backward producing dX, dW for all 78 experts and the router gradient.  Inputs and
 weights are resident in HBM before the timed region.
@@ -43,7 +43,7 @@ def parse():
 
 
 def build_block(T: int, seed: int = 0):
-    """BASELINE recipe: seed 0, params in the reference's draw order x 0.02, bf16; then x, g."""
+    """Seed 0, params in the reference's draw order x 0.02 (moe.py:131-165), bf16; then x, g."""
     from nanospeaker_amd import MoEBlock
 
     torch.manual_seed(seed)
@@ -153,7 +153,7 @@ def main():
     a = parse()
     if a.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; multi-GPU sharding is "
-                                   "design-only (DESIGN.md), so --gpus must be 1"}))
+                                   "design-only, so --gpus must be 1"}))
         sys.exit(2)
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU visible"}))
@@ -191,7 +191,7 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": f"nanoSpeaker MoE block fwd+bwd, T={T} (BASELINE config 2)",
+        "config": {"workload": f"nanoSpeaker MoE block fwd+bwd, T={T} (training shape)",
                    "n_tokens": T, "d_model": d, "n_experts": E, "n_shared": S, "top_k": k,
                    "d_hidden": H, "mode": "train, aux_loss 1e-2"},
         "fwd_tokens_per_s": round(T / (fwd_ms / 1e3), 1),

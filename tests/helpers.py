@@ -58,7 +58,7 @@ def golden_inputs(info: dict):
 
 
 def nanospeaker_inputs(T: int, seed: int = 0, dtype=torch.bfloat16):
-    """BASELINE.json's recipe: seed, params in the reference's order (x0.02, bf16), x, g."""
+    """Benchmark recipe: seed, params in the reference's order (x0.02, bf16), x, g."""
     c = R.nanospeaker_config()
     p = R.make_params(seed, c["d"], c["E"], c["d_ff"], n_shared=c["n_shared"]).to(dtype=dtype)
     x = torch.randn(T, c["d"]).to(dtype)
