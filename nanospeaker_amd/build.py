@@ -25,7 +25,7 @@ ARCH = "gfx950"
 # wrong results on these boxes); hipcc's host pass warns that it does not know the
 # feature, which is harmless.
 COMMON = [
-    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    f"--offload-arch={ARCH}", "-O3", "-std=c++20", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-result",
 ]

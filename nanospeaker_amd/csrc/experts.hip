@@ -20,108 +20,11 @@
 //   bias_grad    per-group column sums for the optional biases.
 #include <algorithm>
 
-#include "gemm_core.h"
-#include "nsmoe_capi_internal.h"
+#include "experts_common.h"
 #include "pack.h"
 #include "../../include/nsmoe.h"
 
 namespace nsmoe {
-
-constexpr int BM = 64;      // rows per tile
-constexpr int NT = 256;     // threads per workgroup
-constexpr int DW_RC = 2048; // rows per dW chunk
-
-struct ExpParams {
-  const void* x;
-  const void* w_in;
-  const void* w_out;
-  const void* b_in;
-  const void* b_out;
-  const void* w_sh_in;
-  const void* w_sh_out;
-  const void* b_sh_in;
-  const void* b_sh_out;
-  const void* topk_w;
-  const int32_t* sorted_ids;
-  const int32_t* offs;
-  const int32_t* counts;
-  int64_t T;
-  int64_t l_cap;
-  int d, H, E, S, k, act;
-  int fast;
-  // fragment-order weight packs (pack.hip): W_in for GEMM1, W_out for GEMM2
-  const char* p_in;
-  const char* p_out;
-  int in_kb, in_nb, out_kb, out_nb;
-  // forward output rows
-  void* y;
-  // backward
-  const void* dout;
-  void* da1;
-  void* hbuf;
-  void* dxrow;
-  void* dtw;
-  // dW
-  void* dw_a;      // dW_in or dW_out (routed)
-  void* dw_sh;     // shared counterpart
-  float* partial;  // fp32 partials
-  void* db;        // bias grad (routed)
-  void* db_sh;     // bias grad (shared)
-};
-
-__device__ __forceinline__ int rows_of(const ExpParams& p, int g) {
-  return g < p.E ? p.counts[g] : (int)p.T;
-}
-__device__ __forceinline__ int64_t row_start(const ExpParams& p, int g) {
-  return g < p.E ? (int64_t)p.offs[g] : p.l_cap + (int64_t)(g - p.E) * p.T;
-}
-template <class T>
-__device__ __forceinline__ const T* per_group(const void* routed, const void* shared, int g,
-                                              int E, int64_t stride) {
-  return g < E ? (const T*)routed + (int64_t)g * stride
-               : (const T*)shared + (int64_t)(g - E) * stride;
-}
-
-// Token, gate weight and pair id of local row `r` of group g (slot = row_start + r).
-template <int DT>
-__device__ __forceinline__ void row_info(const ExpParams& p, int g, int64_t slot, int r,
-                                         int& tok, float& w, int& pair) {
-  if (g < p.E) {
-    pair = p.sorted_ids[slot];
-    tok = pair / p.k;
-    w = Elem<DT>::to_f(((const typename Elem<DT>::T*)p.topk_w)[pair]);
-  } else {
-    pair = -1;
-    tok = r;
-    w = 1.0f;
-  }
-}
-
-// Copies `rows` rows of an LDS tile out to global rows dst + (slot0 + m) * ld, columns
-// [0, n_a) from LDS columns [0, n_a) and, if n_b > 0, global columns [n_a, n_a + n_b)
-// from LDS columns [lds_b, lds_b + n_b).
-template <int DT>
-__device__ __forceinline__ void copy_out(const char* tile, int pitch, int rows,
-                                         typename Elem<DT>::T* dst, int64_t ld, int64_t col0,
-                                         int n_a, int lds_b, int n_b, bool fast) {
-  using G = Geo<DT>;
-  using T = typename G::T;
-  const int ncols = n_a + n_b;
-  if (fast) {
-    const int vpr = ncols / G::VE;
-    for (int i = threadIdx.x; i < rows * vpr; i += NT) {
-      const int m = i / vpr, c = (i % vpr) * G::VE;
-      const int lc = c < n_a ? c : lds_b + (c - n_a);
-      *(u32x4*)(dst + m * ld + col0 + c) = *(const u32x4*)(tile + m * pitch + lc * G::ES);
-    }
-  } else {
-    for (int i = threadIdx.x; i < rows * ncols; i += NT) {
-      const int m = i / ncols, c = i % ncols;
-      const int lc = c < n_a ? c : lds_b + (c - n_a);
-      dst[m * ld + col0 + c] = *(const T*)(tile + m * pitch + lc * G::ES);
-    }
-  }
-}
 
 // ============================ forward ====================================================
 //
@@ -132,7 +35,6 @@ __device__ __forceinline__ void copy_out(const char* tile, int pitch, int rows,
 // is lane-local.  h (rounded to the element type, as the reference stores it) stays in
 // LDS and feeds GEMM2 [64, H] x [H, d] against packed W_out in 192-column passes
 // (48 columns per wave); + b_out, * gate weight, then the rows go out through LDS.
-constexpr int NP2 = 192;  // output columns per pass of the second GEMMs
 
 template <int DT, int NBW>
 __global__ void __launch_bounds__(NT) expert_fwd_kernel(ExpParams p) {
@@ -987,6 +889,8 @@ static int64_t dw_partial_chunks(const nsmoe_experts_args* a) {
 template <int DT>
 static int launch_fwd_tiles(const ExpParams& p, int nbw, int64_t grid, hipStream_t s) {
   if (grid <= 0) return NSMOE_OK;
+  const int rc = launch_fwd_async(DT, p, nbw, grid, s);
+  if (rc != -1) return rc;
   KernelTimer timer("expert_fwd", s);
   if (nbw == 1) expert_fwd_kernel<DT, 1><<<(unsigned)grid, NT, 0, s>>>(p);
   else if (nbw == 2) expert_fwd_kernel<DT, 2><<<(unsigned)grid, NT, 0, s>>>(p);

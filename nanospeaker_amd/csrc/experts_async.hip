@@ -1,0 +1,268 @@
+// Grouped SwiGLU experts with an asynchronous operand pipeline (gfx950, 16-bit types).
+//
+// Same arithmetic, tiles and outputs as the register-staged kernels in experts.hip
+// (reference: moe_experts, src/model/moe_kernel.py:558-623, and MoEBlock._shared,
+// src/model/moe.py:310-329); what changes is how operands reach LDS.  Every k-step's
+// operands -- the 64 gathered token rows (32 elements each) and each wave's packed weight
+// fragments -- are copied global -> LDS by global_load_lds_dwordx4 into an S-stage ring,
+// S - 1 steps ahead of the MFMAs, so a workgroup keeps S - 1 steps of loads in flight
+// without holding them in registers.  One barrier per step: it publishes the step's
+// copies and frees the ring slot the next issue overwrites.
+//
+// Taken for bf16 / fp16 when d and H are multiples of 8, the operands are 16-byte aligned
+// and H <= 128 (the ring and the h tile fit one workgroup's LDS); other shapes use the
+// register-staged kernels.
+#include "experts_common.h"
+
+namespace nsmoe {
+
+namespace {
+
+// Loads per lane that step s issues, and the vmcnt wait that leaves exactly the steps
+// after s in flight: s + 1 .. s + S - 2 (the issue for s + S - 1 comes after the wait).
+template <int S, class LoadsOf>
+__device__ __forceinline__ void wait_step(int s, int nsteps, LoadsOf loads_of) {
+  int n = 0;
+#pragma unroll
+  for (int u = 1; u <= S - 2; ++u)
+    if (s + u < nsteps) n += loads_of(s + u);
+  wait_vmcnt_dyn(n);
+}
+
+}  // namespace
+
+// ============================ forward ====================================================
+//
+// One workgroup = 4 waves = one 64-row tile of one group.
+//   steps [0, nk1):              GEMM1 k-block s: B = token rows (ring), A = packed W_in
+//                                gate and up fragments of the wave's hidden columns (ring)
+//   steps [nk1, nk1 + npass*nk2): GEMM2 pass q / nk2, k-block q % nk2: B = h (LDS),
+//                                A = 3 packed W_out fragments per wave (ring)
+// GEMM2's first fragments are already in flight while GEMM1 finishes.
+//
+// Both GEMMs run transposed (weights as the MFMA's A operand, token rows as B), so each
+// lane ends with 4 consecutive output columns of one row: h reaches LDS with one 8-byte
+// store per 16 x 16 block and y reaches HBM with one 8-byte store per block, no staging.
+template <int DT, int NBW, int S>
+__global__ void __launch_bounds__(NT, 2) expert_fwd_async_kernel(ExpParams p) {
+  using G = Geo<DT>;
+  using T = typename G::T;
+  using M = Mma<DT>;
+  using Frag = typename M::Frag;
+  static_assert(G::ES == 2, "16-bit types only");
+  constexpr int HPMAX = 64 * NBW;
+  constexpr int A_BYTES = BM * G::ROWB;  // 64 rows x 32 elements = 4 KiB = one copy per lane
+  constexpr int NB1 = 2 * NBW;           // GEMM1 fragments per wave per step
+  constexpr int NB2 = 3;                 // GEMM2 fragments per wave per step
+  constexpr int NBMAX = NB1 > NB2 ? NB1 : NB2;
+  constexpr int WB = NBMAX * G::PKB;     // one wave's fragment area
+  constexpr int STAGE = A_BYTES + 4 * WB;
+  // 4 dwords of skew per row: the 8-byte h stores of 32 lanes (16 rows x 2 column groups)
+  // and the 16-byte fragment reads of 16 rows each hit distinct banks.
+  constexpr int HP_PITCH = HPMAX * G::ES + 16;
+  __shared__ __attribute__((aligned(1024))) char s_ring[S][STAGE];
+  __shared__ __attribute__((aligned(16))) char s_h[BM * HP_PITCH];
+  __shared__ int s_tok[BM];
+  __shared__ float s_w[BM];
+  __shared__ int s_loc[3];
+
+  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  Located loc;
+  if (!locate(tile, p.E + p.S, [&](int g) { return (rows_of(p, g) + BM - 1) / BM; },
+              [](int) { return 0; }, s_loc, loc))
+    return;
+  const int g = loc.g, m0 = loc.local * BM;
+  const int rows = min(BM, rows_of(p, g) - m0);
+  const int64_t slot0 = row_start(p, g) + m0;
+  const int tid = threadIdx.x, lane = tid & 63, lc = lane & 15, lg = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  if (tid < BM) {
+    int tok = -1, pair;
+    float w = 0.0f;
+    if (tid < rows) row_info<DT>(p, g, slot0 + tid, m0 + tid, tok, w, pair);
+    s_tok[tid] = tok;
+    s_w[tid] = w;
+  }
+  __syncthreads();
+
+  const int d = p.d, H = p.H, twoH = 2 * p.H;
+  // This lane's share of a step's token tile: LDS chunk tid = row ar, slot (tid & 3),
+  // which holds the row's global chunk ac (the swizzle applied on the source side).
+  const int ar = tid >> 2, ac = (tid & 3) ^ swz<DT>(ar);
+  const int atok = s_tok[ar];
+  const T* arow = atok >= 0 ? (const T*)p.x + (int64_t)atok * d + ac * G::VE : nullptr;
+  const char* zero = (const char*)g_zero_kib + lane * 16;
+  const char* P1 = p.p_in + (int64_t)g * p.in_nb * p.in_kb * G::PKB + lane * G::FRAGB;
+  const char* P4 = p.p_out + (int64_t)g * p.out_nb * p.out_kb * G::PKB + lane * G::FRAGB;
+  const int nk1 = p.in_kb, nk2 = p.out_kb;
+  const int npass = (d + NP2 - 1) / NP2;
+  const int nsteps = nk1 + npass * nk2;
+
+  auto loads_of = [&](int s) { return s < nk1 ? 1 + NB1 : NB2; };
+  auto issue = [&](int s) {
+    char* st = s_ring[s % S];
+    char* bw = st + A_BYTES + wave * WB;
+    if (s < nk1) {
+      const int k0 = s * G::KC;
+      const bool av = arow && k0 + ac * G::VE < d;
+      async_copy16(av ? (const void*)(arow + k0) : (const void*)zero, st + wave * 1024);
+#pragma unroll
+      for (int j = 0; j < NBW; ++j) {
+        const int jb = wave * NBW + j;
+        async_copy16(P1 + ((int64_t)jb * nk1 + s) * G::PKB, bw + j * G::PKB);
+        async_copy16(P1 + ((int64_t)(HPMAX / 16 + jb) * nk1 + s) * G::PKB,
+                     bw + (NBW + j) * G::PKB);
+      }
+    } else {
+      const int q = s - nk1, pass = q / nk2, kb = q - pass * nk2;
+      const int nbase = pass * (NP2 / 16) + wave * 3;
+#pragma unroll
+      for (int j = 0; j < NB2; ++j) {
+        const int nb = nbase + j;
+        const char* src = nb < p.out_nb ? P4 + ((int64_t)nb * nk2 + kb) * G::PKB : zero;
+        async_copy16(src, bw + j * G::PKB);
+      }
+    }
+  };
+  // vmcnt wait that completes step s (steps s + 1 .. s + S - 2 stay in flight).
+  auto wait_for = [&](int s) {
+    if (s + S - 2 < nk1) wait_vmcnt<(S - 2) * (1 + NB1)>();
+    else if (s >= nk1 && s + S - 2 < nsteps) wait_vmcnt<(S - 2) * NB2>();
+    else wait_step<S>(s, nsteps, loads_of);
+  };
+
+  for (int s = 0; s < S - 1 && s < nsteps; ++s) issue(s);
+
+  // ---- GEMM1 (transposed): acc[i][j] = W_in[:, cols of block j]^T x[rows of block i]^T ----
+  f32x4 accg[4][NBW], accu[4][NBW];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) accg[i][j] = accu[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < nk1; ++s) {
+    wait_for(s);
+    barrier_lds();
+    if (s + S - 1 < nsteps) issue(s + S - 1);
+    const char* st = s_ring[s % S];
+    const char* bw = st + A_BYTES + wave * WB + lane * G::FRAGB;
+    Frag xf[4], wg[NBW], wu[NBW];
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) {
+      wg[j] = M::load(bw + j * G::PKB);
+      wu[j] = M::load(bw + (NBW + j) * G::PKB);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xf[i] = frag_sw<DT>(st, i * 16);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < NBW; ++j) {
+        M::run(accg[i][j], wg[j], xf[i]);
+        M::run(accu[i][j], wu[j], xf[i]);
+      }
+  }
+
+  // ---- GEMM1 epilogue: bias, h = act(gate) * up -> LDS (published by the next barrier) ----
+  // Lane (lc, lg) of block (i, j) holds row m = i*16 + lc, hidden columns n0 .. n0 + 3.
+  const T* bin = (g < p.E ? p.b_in : p.b_sh_in)
+                     ? per_group<T>(p.b_in, p.b_sh_in, g, p.E, twoH) : nullptr;
+  with_act(p.act, [&]<int ACT>() {
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) {
+      const int n0 = (wave * NBW + j) * 16 + lg * 4;
+      float bg[4] = {0.f, 0.f, 0.f, 0.f}, bu[4] = {0.f, 0.f, 0.f, 0.f};
+      if (bin) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if (n0 + r < H) {
+            bg[r] = Elem<DT>::to_f(bin[n0 + r]);
+            bu[r] = Elem<DT>::to_f(bin[H + n0 + r]);
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float hv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          hv[r] = n0 + r < H ? act_fwd_t<ACT>(accg[i][j][r] + bg[r]) * (accu[i][j][r] + bu[r])
+                             : 0.0f;
+        const uint32_t lo = pack2<DT>(hv[0], hv[1]), hi = pack2<DT>(hv[2], hv[3]);
+        *(uint2*)(s_h + (i * 16 + lc) * HP_PITCH + n0 * G::ES) = make_uint2(lo, hi);
+      }
+    }
+  });
+
+  // ---- GEMM2 (transposed): y^T = W_out^T h^T, + b_out, * gate, 8-byte row stores ----
+  const T* bout = (g < p.E ? p.b_out : p.b_sh_out)
+                      ? per_group<T>(p.b_out, p.b_sh_out, g, p.E, d) : nullptr;
+  float wrow[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) wrow[i] = s_w[i * 16 + lc];
+  T* Y = (T*)p.y + slot0 * d;
+  for (int pass = 0; pass < npass; ++pass) {
+    f32x4 acc[4][3];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 3; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int kb = 0; kb < nk2; ++kb) {
+      const int s = nk1 + pass * nk2 + kb;
+      wait_for(s);
+      barrier_lds();
+      if (s + S - 1 < nsteps) issue(s + S - 1);
+      const char* bw = s_ring[s % S] + A_BYTES + wave * WB + lane * G::FRAGB;
+      Frag hf[4], wf[3];
+#pragma unroll
+      for (int j = 0; j < 3; ++j) wf[j] = M::load(bw + j * G::PKB);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) hf[i] = frag_at<DT>(s_h, HP_PITCH, i * 16, kb * G::ROWB);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) M::run(acc[i][j], wf[j], hf[i]);
+    }
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const int n0 = (pass * (NP2 / 16) + wave * 3 + j) * 16 + lg * 4;
+      if (n0 >= d) continue;
+      float bo[4] = {0.f, 0.f, 0.f, 0.f};
+      if (bout) {
+        const uint2 b = *(const uint2*)(bout + n0);
+        bo[0] = unpack2<DT>(b.x, 0);
+        bo[1] = unpack2<DT>(b.x, 1);
+        bo[2] = unpack2<DT>(b.y, 0);
+        bo[3] = unpack2<DT>(b.y, 1);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = i * 16 + lc;
+        if (m < rows) {
+          const float w = wrow[i];
+          const uint32_t lo = pack2<DT>((acc[i][j][0] + bo[0]) * w, (acc[i][j][1] + bo[1]) * w);
+          const uint32_t hi = pack2<DT>((acc[i][j][2] + bo[2]) * w, (acc[i][j][3] + bo[3]) * w);
+          *(uint2*)(Y + (int64_t)m * d + n0) = make_uint2(lo, hi);
+        }
+      }
+    }
+  }
+  wait_vmcnt<0>();  // nothing may be in flight when the workgroup retires
+}
+
+int launch_fwd_async(int dtype, const ExpParams& p, int nbw, int64_t grid, hipStream_t s) {
+  if (!p.fast || nbw > 2 || (dtype != DT_BF16 && dtype != DT_F16)) return -1;
+  if (grid <= 0) return NSMOE_OK;
+  constexpr int S = 3;
+  KernelTimer timer("expert_fwd", s);
+  if (dtype == DT_BF16) {
+    if (nbw == 1) expert_fwd_async_kernel<DT_BF16, 1, S><<<(unsigned)grid, NT, 0, s>>>(p);
+    else expert_fwd_async_kernel<DT_BF16, 2, S><<<(unsigned)grid, NT, 0, s>>>(p);
+  } else {
+    if (nbw == 1) expert_fwd_async_kernel<DT_F16, 1, S><<<(unsigned)grid, NT, 0, s>>>(p);
+    else expert_fwd_async_kernel<DT_F16, 2, S><<<(unsigned)grid, NT, 0, s>>>(p);
+  }
+  timer.stop();
+  return check_launch("expert_fwd_async_kernel");
+}
+
+}  // namespace nsmoe

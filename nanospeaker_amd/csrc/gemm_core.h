@@ -170,6 +170,72 @@ __device__ __forceinline__ void store_trans8(const u32x4 (&v)[8], char* tile, in
   }
 }
 
+// ---- asynchronous staging: global -> LDS without registers ---------------------------------
+//
+// gfx950's global_load_lds_dwordx4 copies 16 bytes per lane from the lane's own global
+// address to LDS at M0 (wave-uniform base) + lane * 16, and counts against vmcnt like any
+// vector load.  A wave waits for its own copies with s_waitcnt vmcnt(n); a workgroup
+// barrier afterwards makes every wave's copies visible.  A tile whose LDS layout is not
+// lane-linear (the swizzled row tiles) is filled by permuting which global chunk each
+// lane fetches instead of where it lands.
+//
+// The copy is issued from inline asm on purpose: the compiler then neither waits for all
+// outstanding copies before every LDS read it cannot prove disjoint from them, nor at
+// every barrier, and the explicit vmcnt waits below are the only synchronisation.  In
+// exchange every kernel that issues copies must wait for all of them (wait_vmcnt<0>)
+// before it reads the data or exits.  M0 is saved and restored around the copy because
+// the compiler reserves it and does not expect asm to change it.
+
+// 1 KiB of zeros (never written): the source of zero fill for rows or chunks outside the
+// valid range, so every lane always issues its copy.  One copy per translation unit.
+static __device__ __attribute__((aligned(1024))) uint32_t g_zero_kib[256] = {0};
+
+__device__ __forceinline__ void async_copy16(const void* gsrc, char* lds_wave_base) {
+  const uint32_t lds = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds_wave_base);
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(gsrc), "s"(lds)
+      : "memory");
+}
+
+// Workgroup barrier that orders LDS accesses only: outstanding vector-memory loads (the
+// asynchronous copies of later steps) stay in flight across it.
+__device__ __forceinline__ void barrier_lds() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// s_waitcnt vmcnt(n), every other counter left alone (GFX9 encoding: vmcnt bits [3:0] and
+// [15:14], expcnt [6:4], lgkmcnt [11:8]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// vmcnt(n) for a wave-uniform run-time n; n above 31 waits down to 31 outstanding, which
+// is stricter than needed and therefore safe.
+__device__ __forceinline__ void wait_vmcnt_dyn(int n) {
+  switch (n) {
+#define NSMOE_VM(i) case i: wait_vmcnt<i>(); break;
+    NSMOE_VM(0) NSMOE_VM(1) NSMOE_VM(2) NSMOE_VM(3) NSMOE_VM(4) NSMOE_VM(5) NSMOE_VM(6)
+    NSMOE_VM(7) NSMOE_VM(8) NSMOE_VM(9) NSMOE_VM(10) NSMOE_VM(11) NSMOE_VM(12) NSMOE_VM(13)
+    NSMOE_VM(14) NSMOE_VM(15) NSMOE_VM(16) NSMOE_VM(17) NSMOE_VM(18) NSMOE_VM(19)
+    NSMOE_VM(20) NSMOE_VM(21) NSMOE_VM(22) NSMOE_VM(23) NSMOE_VM(24) NSMOE_VM(25)
+    NSMOE_VM(26) NSMOE_VM(27) NSMOE_VM(28) NSMOE_VM(29) NSMOE_VM(30)
+#undef NSMOE_VM
+    default: wait_vmcnt<31>(); break;
+  }
+}
+
 // ---- staging: global -> registers -> swizzled LDS -------------------------------------
 //
 // DirectStage copies NROWS rows of 32 contraction elements whose source is contiguous in

@@ -99,6 +99,91 @@ __device__ __forceinline__ float act_bwd(float g, int act) {
   }
 }
 
+// ---- compile-time activations for the expert epilogues ----------------------------------
+//
+// Same closed forms as act_fwd / act_bwd (moe_kernel.py:223-250), selected at compile time
+// so an epilogue carries no per-element dispatch.  The logistic function uses the
+// hardware exp2 and reciprocal (a few ulp in fp32), far inside the bf16 / fp16 output
+// rounding and the fp32 kernels' 1e-5 tolerance; erf and its derivative keep the accurate
+// library forms.
+__device__ __forceinline__ float fast_sigmoid(float g) {
+  return __builtin_amdgcn_rcpf(1.0f + __expf(-g));
+}
+
+template <int ACT>
+__device__ __forceinline__ float act_fwd_t(float g) {
+  if constexpr (ACT == ACT_SILU) return g * fast_sigmoid(g);
+  else if constexpr (ACT == ACT_GELU) return 0.5f * g * (1.0f + erff(g * 0.7071067811865476f));
+  else if constexpr (ACT == ACT_RELU) return g > 0.0f ? g : 0.0f;
+  else if constexpr (ACT == ACT_SIGMOID) return fast_sigmoid(g);
+  else return 2.0f * fast_sigmoid(2.0f * g) - 1.0f;  // tanh g = 2 sigma(2g) - 1
+}
+
+// act(g) and act'(g) together (they share the logistic term).
+template <int ACT>
+__device__ __forceinline__ void act_both_t(float g, float& a, float& da) {
+  if constexpr (ACT == ACT_SILU) {
+    const float s = fast_sigmoid(g);
+    a = g * s;
+    da = s * (1.0f + g * (1.0f - s));
+  } else if constexpr (ACT == ACT_GELU) {
+    const float c = 0.5f * (1.0f + erff(g * 0.7071067811865476f));
+    a = g * c;
+    da = c + g * 0.3989422804014327f * __expf(-0.5f * g * g);
+  } else if constexpr (ACT == ACT_RELU) {
+    a = g > 0.0f ? g : 0.0f;
+    da = g > 0.0f ? 1.0f : 0.0f;
+  } else if constexpr (ACT == ACT_SIGMOID) {
+    const float s = fast_sigmoid(g);
+    a = s;
+    da = s * (1.0f - s);
+  } else {
+    const float t = 2.0f * fast_sigmoid(2.0f * g) - 1.0f;
+    a = t;
+    da = 1.0f - t * t;
+  }
+}
+
+// Calls f.template operator()<ACT>() with the run-time activation id as a constant.
+template <class F>
+__device__ __forceinline__ void with_act(int act, F&& f) {
+  switch (act) {
+    case ACT_SILU: f.template operator()<ACT_SILU>(); break;
+    case ACT_GELU: f.template operator()<ACT_GELU>(); break;
+    case ACT_RELU: f.template operator()<ACT_RELU>(); break;
+    case ACT_SIGMOID: f.template operator()<ACT_SIGMOID>(); break;
+    default: f.template operator()<ACT_TANH>(); break;
+  }
+}
+
+// ---- packed conversions (hardware round-to-nearest-even) --------------------------------
+
+typedef __attribute__((ext_vector_type(2))) float f32x2;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+typedef __attribute__((ext_vector_type(2))) _Float16 f16x2_t;
+
+// Two fp32 values as two 16-bit elements of type DT in one dword (low half = lo).
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  uint32_t u;
+  if constexpr (DT == DT_BF16) {
+    const bf16x2_t b = __builtin_convertvector(f32x2{lo, hi}, bf16x2_t);
+    __builtin_memcpy(&u, &b, 4);
+  } else {
+    const f16x2_t h = __builtin_convertvector(f32x2{lo, hi}, f16x2_t);
+    __builtin_memcpy(&u, &h, 4);
+  }
+  return u;
+}
+
+// Element e (0 or 1) of a dword holding two 16-bit elements, as fp32.
+template <int DT>
+__device__ __forceinline__ float unpack2(uint32_t u, int e) {
+  const uint16_t v = (uint16_t)(e ? (u >> 16) : (u & 0xffffu));
+  if constexpr (DT == DT_BF16) return bf16_to_f(v);
+  else return f16_to_f(v);
+}
+
 // ---- wave helpers ---------------------------------------------------------------------
 
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
