@@ -59,10 +59,10 @@ def kernel_units(name: str, T: int, k: int, S: int, d: int, H: int, E: int):
     rows = T * k + S * T  # routed pairs + shared rows
     if name == "expert_fwd":        # GEMM1 + GEMM2 per row
         return rows * (2 * d * 2 * H + 2 * H * d), "mfma", "TFLOP/s"
-    if name == "expert_bwd":        # G = dout W_out^T, dX = dA1 W_in^T per row
-        return rows * (2 * d * H + 2 * 2 * H * d), "mfma", "TFLOP/s"
-    if name == "expert_fwd_a1":
-        return rows * (2 * d * 2 * H), "mfma", "TFLOP/s"
+    if name == "expert_bwd":        # G = dout W_out^T per row (the a1 recompute not counted)
+        return rows * (2 * d * H), "mfma", "TFLOP/s"
+    if name == "expert_dx":         # dX rows = dA1 W_in^T
+        return rows * (2 * 2 * H * d), "mfma", "TFLOP/s"
     if name == "dw_in":
         return rows * (2 * d * 2 * H), "mfma", "TFLOP/s"
     if name == "dw_out":
@@ -73,6 +73,8 @@ def kernel_units(name: str, T: int, k: int, S: int, d: int, H: int, E: int):
         return T * (E * 4 * 2 + k * 8 + k * 2), "hbm", "GB/s"
     if name == "dispatch":          # ids read twice, sorted ids + inverse written
         return T * k * (8 * 2 + 4 + 4), "hbm", "GB/s"
+    if name == "pack":              # W_in (routed + shared) read once and written once
+        return (E + S) * d * 2 * H * 2 * 2, "hbm", "GB/s"
     return None
 
 
@@ -101,8 +103,8 @@ def time_gpu(m, x, g, steps: int, warmup: int):
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / steps
     kernels = {}
-    for name in ("route_fwd", "dispatch", "expert_fwd", "combine", "expert_bwd", "dw_in",
-                 "dw_out", "expert_fwd_a1"):
+    for name in ("route_fwd", "dispatch", "pack", "expert_fwd", "combine", "expert_bwd",
+                 "expert_dx", "dw_in", "dw_out"):
         tot, n = nat.timing_read(name)
         if n:
             kernels[name] = (tot / n, n // steps)

@@ -965,7 +965,10 @@ static int experts_bwd_impl(const nsmoe_experts_args* a, const int32_t* inv, con
   p.dxrow = ws + L.dxrow;
   p.dtw = gr->dtopk_w;
   p.fast = p.fast && aligned16(dout);
-  if (grid > 0) {
+  const int arc = launch_bwd_async(DT, p, nbw, grid, s);
+  if (arc != -1) {
+    NSMOE_TRY(arc);
+  } else if (grid > 0) {
     KernelTimer timer("expert_bwd", s);
     if (nbw == 1) expert_bwd_kernel<DT, 1><<<(unsigned)grid, NT, 0, s>>>(p);
     else if (nbw == 2) expert_bwd_kernel<DT, 2><<<(unsigned)grid, NT, 0, s>>>(p);

@@ -249,6 +249,334 @@ __global__ void __launch_bounds__(NT, 2) expert_fwd_async_kernel(ExpParams p) {
   wait_vmcnt<0>();  // nothing may be in flight when the workgroup retires
 }
 
+// ============================ backward ===================================================
+//
+// expert_bwd_async: one workgroup = one 64-row tile of one group; per k-step of d:
+//   a1^T = W_in^T x[tok]^T   (gate and up, recomputed in fp32)   A = packed W_in (ring)
+//   G^T  = W_out dout[tok]^T                                     A = W_out rows (ring)
+// both token tiles (x and dout rows) arrive through the ring as B operands.  The GLU
+// backward is lane-local (gate, up and G of one (row, column) share lane and register):
+//   h = act(g) u,  dtopk_w += G h,  d_gate = w G u act'(g),  d_up = w G act(g),
+// and dA1 = [d_gate | d_up] and w h leave as 8-byte row stores (for dX and both dW).
+// The gate gradient also takes <dout[tok], b_out[g]> when the expert has an output bias.
+template <int DT, int NBW, int S>
+__global__ void __launch_bounds__(NT, 2) expert_bwd_async_kernel(ExpParams p) {
+  using G = Geo<DT>;
+  using T = typename G::T;
+  using M = Mma<DT>;
+  using Frag = typename M::Frag;
+  static_assert(G::ES == 2, "16-bit types only");
+  constexpr int HPMAX = 64 * NBW;
+  constexpr int A_BYTES = BM * G::ROWB;  // one token tile (x or dout): 4 KiB
+  constexpr int NBF = 3 * NBW;           // gate, up and G fragments per wave per step
+  constexpr int WB = NBF * G::PKB;
+  constexpr int STAGE = 2 * A_BYTES + 4 * WB;
+  constexpr int LOADS = 2 + NBF;         // copies per lane per step
+  __shared__ __attribute__((aligned(1024))) char s_ring[S][STAGE];
+  __shared__ int s_tok[BM];
+  __shared__ int s_pair[BM];
+  __shared__ float s_w[BM];
+  __shared__ float s_dtw[5][BM];
+  __shared__ int s_loc[3];
+
+  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  Located loc;
+  if (!locate(tile, p.E + p.S, [&](int g) { return (rows_of(p, g) + BM - 1) / BM; },
+              [](int) { return 0; }, s_loc, loc))
+    return;
+  const int g = loc.g, m0 = loc.local * BM;
+  const int rows = min(BM, rows_of(p, g) - m0);
+  const int64_t slot0 = row_start(p, g) + m0;
+  const int tid = threadIdx.x, lane = tid & 63, lc = lane & 15, lg = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  if (tid < BM) {
+    int tok = -1, pair = -1;
+    float w = 0.0f;
+    if (tid < rows) row_info<DT>(p, g, slot0 + tid, m0 + tid, tok, w, pair);
+    s_tok[tid] = tok;
+    s_pair[tid] = pair;
+    s_w[tid] = w;
+    s_dtw[4][tid] = 0.0f;
+  }
+  __syncthreads();
+
+  const int d = p.d, H = p.H, twoH = 2 * p.H;
+  const int ar = tid >> 2, ac = (tid & 3) ^ swz<DT>(ar);
+  const int atok = s_tok[ar];
+  const T* xrow = atok >= 0 ? (const T*)p.x + (int64_t)atok * d + ac * G::VE : nullptr;
+  const T* drow = atok >= 0 ? (const T*)p.dout + (int64_t)atok * d + ac * G::VE : nullptr;
+  const char* zero = (const char*)g_zero_kib + lane * 16;
+  const char* P1 = p.p_in + (int64_t)g * p.in_nb * p.in_kb * G::PKB + lane * G::FRAGB;
+  // W_out fragment rows: lane l reads row (jb * 16 + l % 16), k elements 8 * (l / 16) ..
+  const T* Wout = per_group<T>(p.w_out, p.w_sh_out, g, p.E, (int64_t)H * d);
+  const int wk = (lane >> 4) * 8;
+  const int nk = p.in_kb;
+
+  auto issue = [&](int s) {
+    char* st = s_ring[s % S];
+    char* bw = st + 2 * A_BYTES + wave * WB;
+    const int k0 = s * G::KC;
+    const bool av = k0 + ac * G::VE < d;
+    async_copy16(xrow && av ? (const void*)(xrow + k0) : (const void*)zero, st + wave * 1024);
+    async_copy16(drow && av ? (const void*)(drow + k0) : (const void*)zero,
+                 st + A_BYTES + wave * 1024);
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) {
+      const int jb = wave * NBW + j;
+      async_copy16(P1 + ((int64_t)jb * nk + s) * G::PKB, bw + j * G::PKB);
+      async_copy16(P1 + ((int64_t)(HPMAX / 16 + jb) * nk + s) * G::PKB,
+                   bw + (NBW + j) * G::PKB);
+      const int n = jb * 16 + lc;
+      const bool wv = n < H && k0 + wk < d;
+      async_copy16(wv ? (const void*)(Wout + (int64_t)n * d + k0 + wk) : (const void*)zero,
+                   bw + (2 * NBW + j) * G::PKB);
+    }
+  };
+  auto wait_for = [&](int s) {
+    if (s + S - 2 < nk) wait_vmcnt<(S - 2) * LOADS>();
+    else wait_step<S>(s, nk, [&](int) { return LOADS; });
+  };
+
+  for (int s = 0; s < S - 1 && s < nk; ++s) issue(s);
+  f32x4 accg[4][NBW], accu[4][NBW], accG[4][NBW];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < NBW; ++j)
+      accg[i][j] = accu[i][j] = accG[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < nk; ++s) {
+    wait_for(s);
+    barrier_lds();
+    if (s + S - 1 < nk) issue(s + S - 1);
+    const char* st = s_ring[s % S];
+    const char* bw = st + 2 * A_BYTES + wave * WB + lane * G::FRAGB;
+    Frag wg[NBW], wu[NBW], wo[NBW];
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) {
+      wg[j] = M::load(bw + j * G::PKB);
+      wu[j] = M::load(bw + (NBW + j) * G::PKB);
+      wo[j] = M::load(bw + (2 * NBW + j) * G::PKB);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const Frag xf = frag_sw<DT>(st, i * 16);
+      const Frag df = frag_sw<DT>(st + A_BYTES, i * 16);
+#pragma unroll
+      for (int j = 0; j < NBW; ++j) {
+        M::run(accg[i][j], wg[j], xf);
+        M::run(accu[i][j], wu[j], xf);
+        M::run(accG[i][j], wo[j], df);
+      }
+    }
+  }
+
+  // ---- GLU backward, lane-local: lane (lc, lg) of block (i, j) holds row i*16 + lc,
+  // hidden columns n0 .. n0 + 3 ----
+  const T* bin = (g < p.E ? p.b_in : p.b_sh_in)
+                     ? per_group<T>(p.b_in, p.b_sh_in, g, p.E, twoH) : nullptr;
+  T* DA = (T*)p.da1 + slot0 * twoH;
+  T* HB = (T*)p.hbuf + slot0 * H;
+  float wrow[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) wrow[i] = s_w[i * 16 + lc];
+  float part[4] = {0.f, 0.f, 0.f, 0.f};
+  with_act(p.act, [&]<int ACT>() {
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) {
+      const int n0 = (wave * NBW + j) * 16 + lg * 4;
+      if (n0 >= H) continue;  // H % 4 == 0: a group of 4 columns is all in or all out
+      float bg[4] = {0.f, 0.f, 0.f, 0.f}, bu[4] = {0.f, 0.f, 0.f, 0.f};
+      if (bin) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          bg[r] = Elem<DT>::to_f(bin[n0 + r]);
+          bu[r] = Elem<DT>::to_f(bin[H + n0 + r]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = i * 16 + lc;
+        const float w = wrow[i];
+        float dg[4], du[4], wh[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float gg = accg[i][j][r] + bg[r], uu = accu[i][j][r] + bu[r];
+          const float Gv = accG[i][j][r];
+          float a, da;
+          act_both_t<ACT>(gg, a, da);
+          const float hv = a * uu;
+          part[i] += Gv * hv;
+          const float dh = w * Gv;
+          dg[r] = dh * uu * da;
+          du[r] = dh * a;
+          wh[r] = w * hv;
+        }
+        if (m < rows) {
+          T* da_row = DA + (int64_t)m * twoH;
+          *(uint2*)(da_row + n0) = make_uint2(pack2<DT>(dg[0], dg[1]), pack2<DT>(dg[2], dg[3]));
+          *(uint2*)(da_row + H + n0) =
+              make_uint2(pack2<DT>(du[0], du[1]), pack2<DT>(du[2], du[3]));
+          *(uint2*)(HB + (int64_t)m * H + n0) =
+              make_uint2(pack2<DT>(wh[0], wh[1]), pack2<DT>(wh[2], wh[3]));
+        }
+      }
+    }
+  });
+  // dtopk_w: sum of G h over the row's hidden columns (4 lanes per wave, then 4 waves).
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float v = part[i];
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    if (lg == 0) s_dtw[wave][i * 16 + lc] = v;
+  }
+  // <dout[tok], b_out[g]>: four lanes per row, strided over d.
+  if (g < p.E && p.b_out) {
+    const T* bo = (const T*)p.b_out + (int64_t)g * d;
+    const int m = tid >> 2, q = tid & 3;
+    float v = 0.0f;
+    if (m < rows) {
+      const T* dr = (const T*)p.dout + (int64_t)s_tok[m] * d;
+      for (int c = q; c < d; c += 4) v += Elem<DT>::to_f(dr[c]) * Elem<DT>::to_f(bo[c]);
+    }
+    v += __shfl_xor(v, 1, 64);
+    v += __shfl_xor(v, 2, 64);
+    if (q == 0 && m < rows) s_dtw[4][m] = v;
+  }
+  __syncthreads();
+  if (g < p.E && tid < rows) {
+    const float v = s_dtw[0][tid] + s_dtw[1][tid] + s_dtw[2][tid] + s_dtw[3][tid] + s_dtw[4][tid];
+    ((T*)p.dtw)[s_pair[tid]] = Elem<DT>::from_f(v);
+  }
+}
+
+// expert_dx_async: dX rows = dA1 W_in^T, one workgroup per 64-row tile, computed
+// transposed (dX^T = W_in dA1^T): A = W_in rows (contiguous along 2H, the contraction
+// index), B = the tile's dA1 rows; both through the ring, in passes of NP2 output columns
+// (48 per wave).  Rows are reduced per token by `combine`.
+template <int DT, int S>
+__global__ void __launch_bounds__(NT, 2) expert_dx_async_kernel(ExpParams p) {
+  using G = Geo<DT>;
+  using T = typename G::T;
+  using M = Mma<DT>;
+  using Frag = typename M::Frag;
+  static_assert(G::ES == 2, "16-bit types only");
+  constexpr int A_BYTES = BM * G::ROWB;
+  constexpr int NBF = 3;
+  constexpr int WB = NBF * G::PKB;
+  constexpr int STAGE = A_BYTES + 4 * WB;
+  constexpr int LOADS = 1 + NBF;
+  __shared__ __attribute__((aligned(1024))) char s_ring[S][STAGE];
+  __shared__ int s_loc[3];
+
+  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  Located loc;
+  if (!locate(tile, p.E + p.S, [&](int g) { return (rows_of(p, g) + BM - 1) / BM; },
+              [](int) { return 0; }, s_loc, loc))
+    return;
+  const int g = loc.g, m0 = loc.local * BM;
+  const int rows = min(BM, rows_of(p, g) - m0);
+  const int64_t slot0 = row_start(p, g) + m0;
+  const int tid = threadIdx.x, lane = tid & 63, lc = lane & 15, lg = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int d = p.d, twoH = 2 * p.H;
+  const int ar = tid >> 2, ac = (tid & 3) ^ swz<DT>(ar);
+  const T* arow = ar < rows ? (const T*)p.da1 + (slot0 + ar) * twoH + ac * G::VE : nullptr;
+  const char* zero = (const char*)g_zero_kib + lane * 16;
+  const T* Win = per_group<T>(p.w_in, p.w_sh_in, g, p.E, (int64_t)d * twoH);
+  const int wk = (lane >> 4) * 8;
+  const int nkk = (twoH + G::KC - 1) / G::KC;
+  const int npass = (d + NP2 - 1) / NP2;
+  const int nsteps = npass * nkk;
+
+  auto issue = [&](int s) {
+    char* st = s_ring[s % S];
+    char* bw = st + A_BYTES + wave * WB;
+    const int pass = s / nkk, k0 = (s - pass * nkk) * G::KC;
+    async_copy16(arow && k0 + ac * G::VE < twoH ? (const void*)(arow + k0) : (const void*)zero,
+                 st + wave * 1024);
+#pragma unroll
+    for (int j = 0; j < NBF; ++j) {
+      const int c = (pass * (NP2 / 16) + wave * 3 + j) * 16 + lc;
+      const bool v = c < d && k0 + wk < twoH;
+      async_copy16(v ? (const void*)(Win + (int64_t)c * twoH + k0 + wk) : (const void*)zero,
+                   bw + j * G::PKB);
+    }
+  };
+  auto wait_for = [&](int s) {
+    if (s + S - 2 < nsteps) wait_vmcnt<(S - 2) * LOADS>();
+    else wait_step<S>(s, nsteps, [&](int) { return LOADS; });
+  };
+
+  for (int s = 0; s < S - 1 && s < nsteps; ++s) issue(s);
+  T* DX = (T*)p.dxrow + slot0 * d;
+  for (int pass = 0; pass < npass; ++pass) {
+    f32x4 acc[4][3];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 3; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int kk = 0; kk < nkk; ++kk) {
+      const int s = pass * nkk + kk;
+      wait_for(s);
+      barrier_lds();
+      if (s + S - 1 < nsteps) issue(s + S - 1);
+      const char* st = s_ring[s % S];
+      const char* bw = st + A_BYTES + wave * WB + lane * G::FRAGB;
+      Frag wf[3];
+#pragma unroll
+      for (int j = 0; j < 3; ++j) wf[j] = M::load(bw + j * G::PKB);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const Frag af = frag_sw<DT>(st, i * 16);
+#pragma unroll
+        for (int j = 0; j < 3; ++j) M::run(acc[i][j], wf[j], af);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const int c0 = (pass * (NP2 / 16) + wave * 3 + j) * 16 + lg * 4;
+      if (c0 >= d) continue;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = i * 16 + lc;
+        if (m < rows)
+          *(uint2*)(DX + (int64_t)m * d + c0) =
+              make_uint2(pack2<DT>(acc[i][j][0], acc[i][j][1]),
+                         pack2<DT>(acc[i][j][2], acc[i][j][3]));
+      }
+    }
+  }
+  wait_vmcnt<0>();
+}
+
+int launch_bwd_async(int dtype, const ExpParams& p, int nbw, int64_t grid, hipStream_t s) {
+  if (!p.fast || nbw > 2 || (dtype != DT_BF16 && dtype != DT_F16)) return -1;
+  if (grid <= 0) return NSMOE_OK;
+  {
+    constexpr int S = 2;
+    KernelTimer timer("expert_bwd", s);
+    if (dtype == DT_BF16) {
+      if (nbw == 1) expert_bwd_async_kernel<DT_BF16, 1, S><<<(unsigned)grid, NT, 0, s>>>(p);
+      else expert_bwd_async_kernel<DT_BF16, 2, S><<<(unsigned)grid, NT, 0, s>>>(p);
+    } else {
+      if (nbw == 1) expert_bwd_async_kernel<DT_F16, 1, S><<<(unsigned)grid, NT, 0, s>>>(p);
+      else expert_bwd_async_kernel<DT_F16, 2, S><<<(unsigned)grid, NT, 0, s>>>(p);
+    }
+    timer.stop();
+    NSMOE_TRY(check_launch("expert_bwd_async_kernel"));
+  }
+  {
+    constexpr int S = 3;
+    KernelTimer timer("expert_dx", s);
+    if (dtype == DT_BF16) expert_dx_async_kernel<DT_BF16, S><<<(unsigned)grid, NT, 0, s>>>(p);
+    else expert_dx_async_kernel<DT_F16, S><<<(unsigned)grid, NT, 0, s>>>(p);
+    timer.stop();
+    NSMOE_TRY(check_launch("expert_dx_async_kernel"));
+  }
+  return NSMOE_OK;
+}
+
 int launch_fwd_async(int dtype, const ExpParams& p, int nbw, int64_t grid, hipStream_t s) {
   if (!p.fast || nbw > 2 || (dtype != DT_BF16 && dtype != DT_F16)) return -1;
   if (grid <= 0) return NSMOE_OK;

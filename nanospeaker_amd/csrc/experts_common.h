@@ -107,5 +107,7 @@ __device__ __forceinline__ void copy_out(const char* tile, int pitch, int rows,
 // Async (direct-to-LDS) variants for 16-bit types and d_hidden <= 128; each returns
 // NSMOE_OK after launching, or -1 when the shape is not one they take.
 int launch_fwd_async(int dtype, const ExpParams& p, int nbw, int64_t grid, hipStream_t s);
+// Backward tiles (GLU backward) and dX rows; fills p.da1, p.hbuf, p.dxrow and p.dtw.
+int launch_bwd_async(int dtype, const ExpParams& p, int nbw, int64_t grid, hipStream_t s);
 
 }  // namespace nsmoe
