@@ -516,10 +516,6 @@ __global__ void __launch_bounds__(NT) expert_bwd_kernel(ExpParams p) {
 // disjoint thread ranges so every wave shares the transposes.  The row -> token lookups
 // of the work item's rows are read once into LDS.  Tile BMo x BNo =
 // (WGM * TM * 16) x (WGN * TN * 16).
-__device__ __forceinline__ int dw_chunks(int rows) {
-  const int c = (rows + DW_RC - 1) / DW_RC;
-  return c < 1 ? 1 : c;  // an empty group still owns one (all-zero) chunk
-}
 
 template <int MODE> struct DwShape;
 template <> struct DwShape<0> {  // dW_in: 64 x 128 tiles, waves side by side along N
@@ -986,11 +982,16 @@ static int experts_bwd_impl(const nsmoe_experts_args* a, const int32_t* inv, con
     q.dw_a = gr->dw_in;
     q.dw_sh = gr->dw_sh_in;
     q.partial = (float*)(ws + L.p_in);
-    const int64_t ntiles = cdiv(d, 64) * cdiv(2 * H, 128);
-    KernelTimer timer("dw_in", s);
-    dw_kernel<DT, 0><<<(unsigned)(gc * ntiles), NT, 0, s>>>(q);
-    timer.stop();
-    NSMOE_TRY(check_launch("dw_kernel<in>"));
+    const int rc = launch_dw_async(DT, 0, q, gc, s);
+    if (rc != -1) {
+      NSMOE_TRY(rc);
+    } else {
+      const int64_t ntiles = cdiv(d, 64) * cdiv(2 * H, 128);
+      KernelTimer timer("dw_in", s);
+      dw_kernel<DT, 0><<<(unsigned)(gc * ntiles), NT, 0, s>>>(q);
+      timer.stop();
+      NSMOE_TRY(check_launch("dw_kernel<in>"));
+    }
     dim3 rg((unsigned)std::min<int64_t>(cdiv((int64_t)d * 2 * H, NT), 1024), (unsigned)G);
     dw_reduce_kernel<DT, 0><<<rg, NT, 0, s>>>(q);
     NSMOE_TRY(check_launch("dw_reduce_kernel<in>"));
@@ -1000,11 +1001,16 @@ static int experts_bwd_impl(const nsmoe_experts_args* a, const int32_t* inv, con
     q.dw_a = gr->dw_out;
     q.dw_sh = gr->dw_sh_out;
     q.partial = (float*)(ws + L.p_out);
-    const int64_t ntiles = cdiv(H, 128) * cdiv(d, 64);
-    KernelTimer timer("dw_out", s);
-    dw_kernel<DT, 1><<<(unsigned)(gc * ntiles), NT, 0, s>>>(q);
-    timer.stop();
-    NSMOE_TRY(check_launch("dw_kernel<out>"));
+    const int rc = launch_dw_async(DT, 1, q, gc, s);
+    if (rc != -1) {
+      NSMOE_TRY(rc);
+    } else {
+      const int64_t ntiles = cdiv(H, 128) * cdiv(d, 64);
+      KernelTimer timer("dw_out", s);
+      dw_kernel<DT, 1><<<(unsigned)(gc * ntiles), NT, 0, s>>>(q);
+      timer.stop();
+      NSMOE_TRY(check_launch("dw_kernel<out>"));
+    }
     dim3 rg((unsigned)std::min<int64_t>(cdiv((int64_t)H * d, NT), 1024), (unsigned)G);
     dw_reduce_kernel<DT, 1><<<rg, NT, 0, s>>>(q);
     NSMOE_TRY(check_launch("dw_reduce_kernel<out>"));

@@ -12,6 +12,8 @@
 // Taken for bf16 / fp16 when d and H are multiples of 8, the operands are 16-byte aligned
 // and H <= 128 (the ring and the h tile fit one workgroup's LDS); other shapes use the
 // register-staged kernels.
+#include <type_traits>
+
 #include "experts_common.h"
 
 namespace nsmoe {
@@ -575,6 +577,208 @@ int launch_bwd_async(int dtype, const ExpParams& p, int nbw, int64_t grid, hipSt
     NSMOE_TRY(check_launch("expert_dx_async_kernel"));
   }
   return NSMOE_OK;
+}
+
+// ============================ backward: dW ===============================================
+//
+// dW of one (group, row chunk, output tile), computed transposed:
+//   D[n][m] = sum_r P[r][n] Q[r][m]
+// where P rows carry the output's column index n (contiguous in dW) and Q rows its row
+// index m, so each lane ends with 4 consecutive n of one m (8-byte dW stores, or 16-byte
+// fp32 partials for groups split over several chunks).
+//   MODE 0: dW_in[g]  [d, 2H] = sum_r x[tok_r]^T dA1[slot_r]      Q = x[tok], P = dA1[slot]
+//   MODE 1: dW_out[g] [H, d]  = sum_r (w h)[slot_r]^T dout[tok_r] Q = w h,   P = dout[tok]
+// Both operand tiles are 32 rows x tile width, row-major in LDS, filled by lane-linear
+// async copies (the chunk swizzle applied on the source side) and read as MFMA operands
+// with ds_read_b64_tr_b16, which transposes on the way out: no register transposes.
+//
+// Chunk swizzle: a transpose read of one fragment touches 2 chunks (32 B) of each of 4
+// rows per 16 lanes; the swizzle spreads the 8 rows a half-wave reads over all 64 banks.
+template <int ROWB>
+__device__ __forceinline__ int dw_swz(int r) {
+  static_assert(ROWB % 128 == 0, "rows of whole 128-byte lines");
+  if constexpr (ROWB % 256 == 0) return ((r & 3) | (((r >> 3) & 1) << 2)) << 1;
+  else return (((r >> 1) ^ (r >> 2)) & 3) << 1;
+}
+
+template <int MODE> struct DwTile;
+template <> struct DwTile<0> {  // dW_in [d, 2H]: 192 x 128 tiles
+  static constexpr int BMT = 192, BNT = 128, WM = 2, WN = 2;
+};
+template <> struct DwTile<1> {  // dW_out [H, d]: 128 x 192 tiles
+  static constexpr int BMT = 128, BNT = 192, WM = 2, WN = 2;
+};
+
+template <int DT, int MODE, int S>
+__global__ void __launch_bounds__(NT, 2) dw_async_kernel(ExpParams p) {
+  using G = Geo<DT>;
+  using T = typename G::T;
+  using M = Mma<DT>;
+  using Frag = typename M::Frag;
+  using Tl = DwTile<MODE>;
+  static_assert(G::ES == 2, "16-bit types only");
+  constexpr int BMT = Tl::BMT, BNT = Tl::BNT;
+  constexpr int TMB = BMT / 16 / Tl::WM, TNB = BNT / 16 / Tl::WN;  // blocks per wave
+  constexpr int QROWB = BMT * 2, PROWB = BNT * 2;                 // LDS row bytes
+  constexpr int QCPR = BMT / 8, PCPR = BNT / 8;                   // 16-byte chunks per row
+  constexpr int QBYTES = G::KC * QROWB, PBYTES = G::KC * PROWB;
+  constexpr int QBLK = QBYTES / 1024, PBLK = PBYTES / 1024;       // 1 KiB copy blocks
+  constexpr int STAGE = QBYTES + PBYTES;
+  constexpr int NBLK = QBLK + PBLK;
+  static_assert(NBLK % 4 == 0, "copy blocks split evenly over the 4 waves");
+  constexpr int LOADS = NBLK / 4;
+  __shared__ __attribute__((aligned(1024))) char s_ring[S][STAGE];
+  __shared__ int s_tok[DW_RC];
+  __shared__ int s_loc[3];
+
+  const int d = p.d, H = p.H, twoH = 2 * p.H;
+  const int Md = MODE == 0 ? d : H;
+  const int Nd = MODE == 0 ? twoH : d;
+  const int tn = (Nd + BNT - 1) / BNT, ntiles = ((Md + BMT - 1) / BMT) * tn;
+  const int item = xcd_remap(blockIdx.x, gridDim.x);
+  Located loc;
+  if (!locate(item, p.E + p.S, [&](int g) { return dw_chunks(rows_of(p, g)) * ntiles; },
+              [&](int g) {
+                const int c = dw_chunks(rows_of(p, g));
+                return c > 1 ? c : 0;
+              },
+              s_loc, loc))
+    return;
+  const int g = loc.g;
+  const int rows_g = rows_of(p, g);
+  const int nch = dw_chunks(rows_g);
+  const int chunk = loc.local / ntiles, t = loc.local % ntiles;
+  const int m0 = (t / tn) * BMT, n0 = (t % tn) * BNT;
+  const int r0 = chunk * DW_RC, nr = max(0, min(rows_g, r0 + DW_RC) - r0);
+  const int64_t rs = row_start(p, g) + r0;
+  const int tid = threadIdx.x, lane = tid & 63, lc = lane & 15, lg = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / Tl::WN, wn = wave % Tl::WN;
+
+  for (int r = tid; r < nr; r += NT) s_tok[r] = g < p.E ? p.sorted_ids[rs + r] / p.k : r0 + r;
+  __syncthreads();
+
+  const T* X = (const T*)p.x;
+  const T* DA = (const T*)p.da1;
+  const T* HB = (const T*)p.hbuf;
+  const T* DO = (const T*)p.dout;
+  const char* zero = (const char*)g_zero_kib + lane * 16;
+  // Row r (0 .. nr) of the chunk: Q and P source rows, pointing at the tile's first column.
+  auto qrow = [&](int r) -> const T* {
+    if constexpr (MODE == 0) return X + (int64_t)s_tok[r] * d + m0;
+    else return HB + (rs + r) * H + m0;
+  };
+  auto prow = [&](int r) -> const T* {
+    if constexpr (MODE == 0) return DA + (rs + r) * twoH + n0;
+    else return DO + (int64_t)s_tok[r] * d + n0;
+  };
+  const int nsteps = (nr + G::KC - 1) / G::KC;
+
+  auto issue = [&](int s) {
+    char* st = s_ring[s % S];
+    const int k0 = s * G::KC;
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) {
+      const int b = wave + 4 * u;  // wave-uniform block index
+      const void* src = zero;
+      if (b < QBLK) {
+        const int q = b * 64 + lane, row = q / QCPR, cp = q % QCPR;
+        const int c = cp ^ dw_swz<QROWB>(row);
+        if (k0 + row < nr && m0 + c * 8 < Md) src = qrow(k0 + row) + c * 8;
+      } else {
+        const int q = (b - QBLK) * 64 + lane, row = q / PCPR, cp = q % PCPR;
+        const int c = cp ^ dw_swz<PROWB>(row);
+        if (k0 + row < nr && n0 + c * 8 < Nd) src = prow(k0 + row) + c * 8;
+      }
+      async_copy16(src, st + b * 1024);
+    }
+  };
+  auto wait_for = [&](int s) {
+    if (s + S - 2 < nsteps) wait_vmcnt<(S - 2) * LOADS>();
+    else wait_step<S>(s, nsteps, [&](int) { return LOADS; });
+  };
+  // Transposed fragment of 16 columns (col0 .. col0 + 15) of a 32-row tile.
+  auto frag_tr = [&](const char* tile, auto rowb_tag, int col0) -> Frag {
+    constexpr int RB = decltype(rowb_tag)::value;
+    const int i = lane & 15, gq = lane >> 4;
+    const int col = col0 + 4 * (i & 3);
+    const int c = col >> 3, cb = (col & 7) * 2;
+    const int ra = 8 * gq + (i >> 2), rb = ra + 4;
+    const uint2 lo = lds_read_tr16(tile + ra * RB + ((c ^ dw_swz<RB>(ra)) << 4) + cb);
+    const uint2 hi = lds_read_tr16(tile + rb * RB + ((c ^ dw_swz<RB>(rb)) << 4) + cb);
+    Frag f;
+    f.v = u32x4{lo.x, lo.y, hi.x, hi.y};
+    return f;
+  };
+
+  f32x4 acc[TNB][TMB];
+#pragma unroll
+  for (int j = 0; j < TNB; ++j)
+#pragma unroll
+    for (int i = 0; i < TMB; ++i) acc[j][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < S - 1 && s < nsteps; ++s) issue(s);
+  for (int s = 0; s < nsteps; ++s) {
+    wait_for(s);
+    barrier_lds();
+    if (s + S - 1 < nsteps) issue(s + S - 1);
+    const char* st = s_ring[s % S];
+    Frag qf[TMB], pf[TNB];
+#pragma unroll
+    for (int i = 0; i < TMB; ++i)
+      qf[i] = frag_tr(st, std::integral_constant<int, QROWB>{}, (wm * TMB + i) * 16);
+#pragma unroll
+    for (int j = 0; j < TNB; ++j)
+      pf[j] = frag_tr(st + QBYTES, std::integral_constant<int, PROWB>{}, (wn * TNB + j) * 16);
+#pragma unroll
+    for (int j = 0; j < TNB; ++j)
+#pragma unroll
+      for (int i = 0; i < TMB; ++i) M::run(acc[j][i], pf[j], qf[i]);
+  }
+  wait_vmcnt<0>();
+
+  const int64_t mn = (int64_t)Md * Nd;
+  T* dst = nullptr;
+  float* pdst = nullptr;
+  if (nch == 1) dst = g < p.E ? (T*)p.dw_a + (int64_t)g * mn : (T*)p.dw_sh + (int64_t)(g - p.E) * mn;
+  else pdst = p.partial + (int64_t)(loc.aux + chunk) * mn;
+#pragma unroll
+  for (int j = 0; j < TNB; ++j) {
+    const int n = n0 + (wn * TNB + j) * 16 + lg * 4;
+    if (n >= Nd) continue;  // Nd % 4 == 0
+#pragma unroll
+    for (int i = 0; i < TMB; ++i) {
+      const int m = m0 + (wm * TMB + i) * 16 + lc;
+      if (m >= Md) continue;
+      const f32x4 v = acc[j][i];
+      if (dst)
+        *(uint2*)(dst + (int64_t)m * Nd + n) = make_uint2(pack2<DT>(v[0], v[1]), pack2<DT>(v[2], v[3]));
+      else
+        *(f32x4*)(pdst + (int64_t)m * Nd + n) = v;
+    }
+  }
+}
+
+int launch_dw_async(int dtype, int mode, const ExpParams& q, int64_t groups_chunks,
+                    hipStream_t s) {
+  if (!q.fast || (dtype != DT_BF16 && dtype != DT_F16)) return -1;
+  const int d = q.d, H = q.H;
+  const int Md = mode == 0 ? d : H, Nd = mode == 0 ? 2 * H : d;
+  const int BMT = mode == 0 ? DwTile<0>::BMT : DwTile<1>::BMT;
+  const int BNT = mode == 0 ? DwTile<0>::BNT : DwTile<1>::BNT;
+  const int64_t ntiles = cdiv(Md, BMT) * cdiv(Nd, BNT);
+  const int64_t grid = groups_chunks * ntiles;
+  if (grid <= 0) return NSMOE_OK;
+  constexpr int S = 3;
+  KernelTimer timer(mode == 0 ? "dw_in" : "dw_out", s);
+  if (dtype == DT_BF16) {
+    if (mode == 0) dw_async_kernel<DT_BF16, 0, S><<<(unsigned)grid, NT, 0, s>>>(q);
+    else dw_async_kernel<DT_BF16, 1, S><<<(unsigned)grid, NT, 0, s>>>(q);
+  } else {
+    if (mode == 0) dw_async_kernel<DT_F16, 0, S><<<(unsigned)grid, NT, 0, s>>>(q);
+    else dw_async_kernel<DT_F16, 1, S><<<(unsigned)grid, NT, 0, s>>>(q);
+  }
+  timer.stop();
+  return check_launch("dw_async_kernel");
 }
 
 int launch_fwd_async(int dtype, const ExpParams& p, int nbw, int64_t grid, hipStream_t s) {

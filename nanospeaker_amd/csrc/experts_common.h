@@ -8,7 +8,7 @@ namespace nsmoe {
 
 constexpr int BM = 64;      // rows per tile
 constexpr int NT = 256;     // threads per workgroup
-constexpr int DW_RC = 2048; // rows per dW chunk
+constexpr int DW_RC = 768;  // rows per dW chunk (work items of similar size)
 constexpr int NP2 = 192;  // output columns per pass of the second GEMMs
 
 struct ExpParams {
@@ -104,9 +104,17 @@ __device__ __forceinline__ void copy_out(const char* tile, int pitch, int rows,
 }
 
 
+// Row chunks of group g in the dW work decomposition.
+__device__ __forceinline__ int dw_chunks(int rows) {
+  const int c = (rows + DW_RC - 1) / DW_RC;
+  return c < 1 ? 1 : c;  // an empty group still owns one (all-zero) chunk
+}
+
 // Async (direct-to-LDS) variants for 16-bit types and d_hidden <= 128; each returns
 // NSMOE_OK after launching, or -1 when the shape is not one they take.
 int launch_fwd_async(int dtype, const ExpParams& p, int nbw, int64_t grid, hipStream_t s);
+// dW of every (group, row chunk, tile): mode 0 dW_in, 1 dW_out (partials as dw_reduce expects).
+int launch_dw_async(int dtype, int mode, const ExpParams& q, int64_t groups_chunks, hipStream_t s);
 // Backward tiles (GLU backward) and dX rows; fills p.da1, p.hbuf, p.dxrow and p.dtw.
 int launch_bwd_async(int dtype, const ExpParams& p, int nbw, int64_t grid, hipStream_t s);
 

@@ -205,6 +205,23 @@ __device__ __forceinline__ void async_copy16(const void* gsrc, char* lds_wave_ba
       : "memory");
 }
 
+// ---- LDS transpose reads (gfx950 ds_read_b64_tr_b16) -------------------------------------
+//
+// Within each 16-lane group, lane i supplies the address of 4 consecutive 16-bit elements
+// M[i][0..3]; lane j receives M[4e + j / 4][j % 4] for e = 0..3.  So if lane i points at
+// row (k0 + i / 4), columns 4 * (i % 4) .. + 3 of a row-major tile (rows = contraction
+// index), lane j receives column j of rows k0 .. k0 + 3: the MFMA operand layout, read
+// straight from a tile that was stored untransposed.
+typedef __attribute__((ext_vector_type(4))) short i16x4;
+
+__device__ __forceinline__ uint2 lds_read_tr16(const char* p) {
+  const i16x4 v =
+      __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)p);
+  uint2 u;
+  __builtin_memcpy(&u, &v, 8);
+  return u;
+}
+
 // Workgroup barrier that orders LDS accesses only: outstanding vector-memory loads (the
 // asynchronous copies of later steps) stay in flight across it.
 __device__ __forceinline__ void barrier_lds() {
