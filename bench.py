@@ -100,6 +100,7 @@ def time_gpu(m, x, g, steps: int, warmup: int):
     t0 = time.perf_counter()
     for _ in range(steps):
         step()
+    host_ms = (time.perf_counter() - t0) * 1e3 / steps   # enqueue time, before the wait
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / steps
     kernels = {}
@@ -120,7 +121,7 @@ def time_gpu(m, x, g, steps: int, warmup: int):
             m(x)
         torch.cuda.synchronize()
         fwd_ms = (time.perf_counter() - t0) * 1e3 / steps
-    return ms, fwd_ms, kernels
+    return ms, fwd_ms, kernels, host_ms
 
 
 def cpu_baseline(seconds: float):
@@ -164,7 +165,7 @@ def main():
     m, x, g = build_block(T)
     m = m.cuda()
     x, g = x.cuda(), g.cuda()
-    ms, fwd_ms, kernels = time_gpu(m, x, g, a.steps, a.warmup)
+    ms, fwd_ms, kernels, host_ms = time_gpu(m, x, g, a.steps, a.warmup)
 
     k, S, d, H, E = 6, 2, 576, 128, 76
     dom = max(kernels, key=lambda n: kernels[n][0] * kernels[n][1]) if kernels else None
@@ -198,6 +199,7 @@ def main():
                    "d_hidden": H, "mode": "train, aux_loss 1e-2"},
         "fwd_tokens_per_s": round(T / (fwd_ms / 1e3), 1),
         "fwd_ms": round(fwd_ms, 4),
+        "host_enqueue_ms_per_step": round(host_ms, 4),
         "kernels_us": {n: round(v[0] * 1e3, 2) for n, v in kernels.items()},
         "roofline": roofline,
     }

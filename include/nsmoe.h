@@ -46,7 +46,7 @@ int32_t nsmoe_abi_version(void);
 /* Measurement hooks (no counterpart in the reference; used by bench.py).  When enabled,
  * the library records a HIP event pair on the launch stream around each launch of its
  * main kernels ("pack", "route_fwd", "dispatch", "expert_fwd", "combine",
- * "expert_bwd", "dw_in", "dw_out") until `capacity` pairs are used.
+ * "expert_bwd", "expert_dx", "dw_in", "dw_out") until `capacity` pairs are used.
  * nsmoe_timing_read waits for the recorded events of one kernel and returns their
  * summed duration.  capacity 0 disables timing and frees the events. */
 int nsmoe_timing_enable(int32_t capacity);
@@ -54,31 +54,51 @@ int nsmoe_timing_read(const char* kernel_name, double* total_ms, int64_t* launch
 
 /* ---- router tail ----------------------------------------------------------------------
  * Replaces the softmax / topk / renormalise / cast tail of TopKRouter.forward
- * (src/model/router.py:79-98); the logits GEMM `(x @ W).float()` (router.py:69) is the
- * caller's.
- *   logits    [n_tokens, n_experts] fp32
- *   flags     bit 0 NSMOE_ROUTE_PROBS: training branch (router.py:79-81): probs =
+ * (src/model/router.py:79-98); the logits GEMM `(x @ W)` (router.py:69) is the caller's.
+ *   logits    [n_tokens, n_experts]: fp32, or -- with NSMOE_ROUTE_LOGITS16 -- the 16-bit
+ *             GEMM output in w_dtype, widened in the kernel exactly as router.py:69's
+ *             .float() widens it.
+ *   flags     NSMOE_ROUTE_PROBS: training branch (router.py:79-81): probs =
  *             softmax(logits) is written to `probs` [n_tokens, n_experts] fp32 and the
  *             top-k runs on it; otherwise top-k runs on the logits (router.py:86-92).
- *             bit 1 NSMOE_ROUTE_NORMALIZE: normalize_weights.
+ *             NSMOE_ROUTE_NORMALIZE: normalize_weights.
+ *             NSMOE_ROUTE_LOGITS16: logits (and, in the backward, the eval branch's
+ *             `src` and grad_logits) are stored in w_dtype (bf16 / fp16 only).
  *   topk_w    [n_tokens, top_k] in w_dtype; topk_idx [n_tokens, top_k] int64, in the
  *             order CPU torch.topk returns them, ties included.
  * Limits: 1 <= top_k <= n_experts <= 128.
  */
 #define NSMOE_ROUTE_PROBS 1
 #define NSMOE_ROUTE_NORMALIZE 2
-int nsmoe_route_fwd(const float* logits, int64_t n_tokens, int32_t n_experts, int32_t top_k,
+#define NSMOE_ROUTE_LOGITS16 4
+int nsmoe_route_fwd(const void* logits, int64_t n_tokens, int32_t n_experts, int32_t top_k,
                     int32_t flags, int32_t w_dtype, void* topk_w, int64_t* topk_idx,
                     float* probs, void* stream);
 
-/* Backward of nsmoe_route_fwd to d(logits) [n_tokens, n_experts] fp32 (torch autograd
- * through router.py:79-98).  `src` is the probs of the forward when flags has
- * NSMOE_ROUTE_PROBS, else the logits.  grad_probs (the balance-loss gradient,
- * router.py:110-111) may be NULL. */
-int nsmoe_route_bwd(const float* src, const int64_t* topk_idx, const void* grad_topk_w,
-                    int32_t w_dtype, const float* grad_probs, int64_t n_tokens,
-                    int32_t n_experts, int32_t top_k, int32_t flags, float* grad_logits,
+/* Backward of nsmoe_route_fwd to d(logits) [n_tokens, n_experts] (torch autograd through
+ * router.py:79-98).  `src` is the probs of the forward (fp32) when flags has
+ * NSMOE_ROUTE_PROBS, else the logits.  d(probs) is the sum of two optional terms:
+ *   grad_probs  [n_tokens, n_experts] fp32, any upstream gradient of probs (or NULL);
+ *   the balance loss aux = aux_coef * E * sum_e f_e * mean_t probs[t, e] with
+ *   f = aux_counts / max(sum aux_counts, 1) (router.py:100-111; f is constant), given
+ *   its upstream gradient grad_aux (device fp32 scalar) and aux_counts [n_experts] int32
+ *   -- both NULL to leave it out.  grad_logits is fp32, or w_dtype under
+ *   NSMOE_ROUTE_LOGITS16. */
+int nsmoe_route_bwd(const void* src, const int64_t* topk_idx, const void* grad_topk_w,
+                    int32_t w_dtype, const float* grad_probs, const float* grad_aux,
+                    const int32_t* aux_counts, float aux_coef, int64_t n_tokens,
+                    int32_t n_experts, int32_t top_k, int32_t flags, void* grad_logits,
                     void* stream);
+
+/* Balance loss TopKRouter.balance_loss (router.py:100-111):
+ *   aux[0] = coef * n_experts * sum_e (counts[e] / max(sum counts, 1)) * mean_t probs[t, e]
+ * probs [n_tokens, n_experts] fp32, counts [n_experts] int32, aux [1] fp32 (device).
+ * Deterministic (fixed summation order).  workspace >=
+ * nsmoe_balance_loss_workspace_size(n_tokens, n_experts) bytes. */
+size_t nsmoe_balance_loss_workspace_size(int64_t n_tokens, int32_t n_experts);
+int nsmoe_balance_loss(const float* probs, const int32_t* counts, int64_t n_tokens,
+                       int32_t n_experts, float coef, float* aux, void* workspace,
+                       size_t workspace_bytes, void* stream);
 
 /* ---- dispatch -------------------------------------------------------------------------
  * Replaces moe_dispatch (src/model/moe_kernel.py:180-218) with the permutation of

@@ -14,7 +14,8 @@ from pathlib import Path
 LIB_PATH = Path(os.environ.get("NSMOE_LIB", Path(__file__).resolve().parent / "libnsmoe.so"))
 
 BF16, F16, F32 = 0, 1, 2
-ROUTE_PROBS, ROUTE_NORMALIZE = 1, 2
+ROUTE_PROBS, ROUTE_NORMALIZE, ROUTE_LOGITS16 = 1, 2, 4
+ABI_VERSION = 2
 
 # Every symbol include/nsmoe.h declares, with (restype, argtypes).
 _vp, _i32, _i64, _sz = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t
@@ -50,7 +51,11 @@ SIGNATURES = {
     "nsmoe_timing_read": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double),
                                          ctypes.POINTER(_i64)]),
     "nsmoe_route_fwd": (ctypes.c_int, [_vp, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
-    "nsmoe_route_bwd": (ctypes.c_int, [_vp, _vp, _vp, _i32, _vp, _i64, _i32, _i32, _i32, _vp, _vp]),
+    "nsmoe_route_bwd": (ctypes.c_int, [_vp, _vp, _vp, _i32, _vp, _vp, _vp, ctypes.c_float, _i64,
+                                       _i32, _i32, _i32, _vp, _vp]),
+    "nsmoe_balance_loss_workspace_size": (_sz, [_i64, _i32]),
+    "nsmoe_balance_loss": (ctypes.c_int, [_vp, _vp, _i64, _i32, ctypes.c_float, _vp, _vp, _sz,
+                                          _vp]),
     "nsmoe_align_m": (_i64, []),
     "nsmoe_dispatch_l_cap": (_i64, [_i64, _i32]),
     "nsmoe_dispatch_workspace_size": (_sz, [_i64, _i32]),
@@ -89,7 +94,7 @@ def lib() -> ctypes.CDLL:
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(handle, name)
         fn.restype, fn.argtypes = res, args
-    if handle.nsmoe_abi_version() != 1:
+    if handle.nsmoe_abi_version() != ABI_VERSION:
         raise NativeLibraryError("libnsmoe.so ABI version mismatch; rebuild it")
     _LIB = handle
     return handle

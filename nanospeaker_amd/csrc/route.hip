@@ -251,9 +251,11 @@ __device__ __forceinline__ float wave_max(float v) {
 // softmax(topk logits) (normalize) or softmax(logits)[idx] (router.py:83-92).
 // With want_probs and normalize and k > 1 the gates are p / sum(p) (router.py:96-97).
 // E <= 128: each lane holds row elements lane and lane + 64.
+// flags bit 2 (logits16): the logits are stored in the gate dtype DT (the bf16 / fp16 GEMM
+//   output that router.py:69 widens with .float()); they are widened here on load.
 template <int DT>
 __global__ void __launch_bounds__(ROUTE_THREADS)
-route_fwd_kernel(const float* __restrict__ logits, int64_t T, int E, int k, int flags,
+route_fwd_kernel(const void* __restrict__ logits, int64_t T, int E, int k, int flags,
                  typename Elem<DT>::T* __restrict__ topk_w, int64_t* __restrict__ topk_idx,
                  float* __restrict__ probs) {
   extern __shared__ uint64_t lds_q[];  // [ROUTE_WAVES][E]
@@ -267,9 +269,15 @@ route_fwd_kernel(const float* __restrict__ logits, int64_t T, int E, int k, int 
 
   float v0 = -INFINITY, v1 = -INFINITY;
   if (active) {
-    const float* lrow = logits + row * E;
-    if (has0) v0 = lrow[lane];
-    if (has1) v1 = lrow[lane + 64];
+    if (flags & 4) {
+      const typename Elem<DT>::T* lrow = (const typename Elem<DT>::T*)logits + row * E;
+      if (has0) v0 = Elem<DT>::to_f(lrow[lane]);
+      if (has1) v1 = Elem<DT>::to_f(lrow[lane + 64]);
+    } else {
+      const float* lrow = (const float*)logits + row * E;
+      if (has0) v0 = lrow[lane];
+      if (has1) v1 = lrow[lane + 64];
+    }
   }
   // Row max (NaN-propagating, like torch's softmax) and sum of exp.
   const bool nan_here = (has0 && __builtin_isnan(v0)) || (has1 && __builtin_isnan(v1));
@@ -292,12 +300,36 @@ route_fwd_kernel(const float* __restrict__ logits, int64_t T, int E, int k, int 
       }
     }
   }
-  if (active) {
+  // Fast path: k rounds of a wave-wide arg-max.  If every round's maximum is unique among
+  // the values still in play (no NaN, no tie inside the top k, none at its boundary),
+  // the sorted top k is unique, so any selection returns CPU topk's answer.  A row with
+  // a tie anywhere that matters takes the exact restatement below instead.
+  bool exact = any_nan || !active;
+  if (!exact) {
+    bool av0 = has0, av1 = has1;
+    for (int t = 0; t < k; ++t) {
+      const float c = fmaxf(av0 ? k0 : -INFINITY, av1 ? k1 : -INFINITY);
+      const float mx = wave_max(c);
+      const unsigned long long b0 = __ballot(av0 && k0 == mx);
+      const unsigned long long b1 = __ballot(av1 && k1 == mx);
+      if (__popcll(b0) + __popcll(b1) != 1) {
+        exact = true;
+        break;
+      }
+      const int src = b0 ? __ffsll((long long)b0) - 1 : __ffsll((long long)b1) - 1 + 64;
+      if (lane == (src & 63)) {
+        if (src < 64) av0 = false;
+        else av1 = false;
+      }
+      if (lane == 0) q[t] = pack(mx, src);
+    }
+  }
+  if (exact && active) {
     if (has0) q[lane] = pack(k0, lane);
     if (has1) q[lane + 64] = pack(k1, lane + 64);
   }
   __syncthreads();
-  if (active && lane == 0) topk_select(LaneRow{q}, E, k);
+  if (exact && active && lane == 0) topk_select(LaneRow{q}, E, k);
   __syncthreads();
   if (!active) return;
 
@@ -340,12 +372,18 @@ route_fwd_kernel(const float* __restrict__ logits, int64_t T, int E, int k, int 
 //   eval !normalize:  w = softmax(l)[idx] -> softmax backward of scatter(dw)
 // `src` holds probs for the train branch and logits otherwise.  Ids outside [0, E)
 // (not produced by route_fwd) give the row a zero gradient.
+// The balance loss aux = coef E sum_e f_e mean_t p[t, e] (router.py:110-111, f constant)
+// adds d aux / d p[t, e] = grad_aux coef E f_e / T to d(probs), computed here from the
+// counts (aux_counts non-NULL) instead of being materialised as a [T, E] tensor.
+// flags bit 2 (logits16): in the eval branches `src` is stored in DT, and grad_logits is
+// written in DT (the gradient of router.py:69's .float()); otherwise both are fp32.
 template <int DT>
 __global__ void __launch_bounds__(ROUTE_THREADS)
-route_bwd_kernel(const float* __restrict__ src, const int64_t* __restrict__ topk_idx,
+route_bwd_kernel(const void* __restrict__ src, const int64_t* __restrict__ topk_idx,
                  const typename Elem<DT>::T* __restrict__ grad_w,
-                 const float* __restrict__ grad_probs, int64_t T, int E, int k, int flags,
-                 float* __restrict__ grad_logits) {
+                 const float* __restrict__ grad_probs, const float* __restrict__ grad_aux,
+                 const int32_t* __restrict__ aux_counts, float aux_coef, int64_t T, int E,
+                 int k, int flags, void* __restrict__ grad_logits_v) {
   extern __shared__ float lds_f[];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * ROUTE_WAVES + wave;
@@ -355,23 +393,45 @@ route_bwd_kernel(const float* __restrict__ src, const int64_t* __restrict__ topk
   float* sv = lds_f + wave * 2 * E;  // the row's src values
   float* sg = sv + E;                // running d(probs) or d(logits) row
   const bool has0 = lane < E, has1 = lane + 64 < E;
-  const float* srow = src + row * E;
-  const float x0 = has0 ? srow[lane] : 0.0f, x1 = has1 ? srow[lane + 64] : 0.0f;
+  const bool w16 = (flags & 4) != 0;
+  using ET = typename Elem<DT>::T;
+  float x0 = 0.0f, x1 = 0.0f;
+  if (w16 && !want_probs) {
+    const ET* srow = (const ET*)src + row * E;
+    if (has0) x0 = Elem<DT>::to_f(srow[lane]);
+    if (has1) x1 = Elem<DT>::to_f(srow[lane + 64]);
+  } else {
+    const float* srow = (const float*)src + row * E;
+    if (has0) x0 = srow[lane];
+    if (has1) x1 = srow[lane + 64];
+  }
   float g0 = 0.0f, g1 = 0.0f;
   if (grad_probs && want_probs) {
     const float* gp = grad_probs + row * E;
     if (has0) g0 = gp[lane];
     if (has1) g1 = gp[lane + 64];
   }
+  if (aux_counts && grad_aux && want_probs) {
+    const float c0 = has0 ? (float)aux_counts[lane] : 0.0f;
+    const float c1 = has1 ? (float)aux_counts[lane + 64] : 0.0f;
+    const float scale = grad_aux[0] * aux_coef * (float)E / fmaxf(wave_sum(c0 + c1), 1.0f) /
+                        (float)T;
+    g0 += c0 * scale;
+    g1 += c1 * scale;
+  }
+  // d(logits) is stored through these (fp32, or DT under logits16 in the eval branches).
+  auto put = [&](int e, float v) {
+    if (w16) ((ET*)grad_logits_v)[row * E + e] = Elem<DT>::from_f(v);
+    else ((float*)grad_logits_v)[row * E + e] = v;
+  };
   if (has0) { sv[lane] = x0; sg[lane] = want_probs ? g0 : 0.0f; }
   if (has1) { sv[lane + 64] = x1; sg[lane + 64] = want_probs ? g1 : 0.0f; }
   const bool o0 = lane < k, o1 = lane + 64 < k;
   int64_t i0 = o0 ? topk_idx[row * k + lane] : 0, i1 = o1 ? topk_idx[row * k + lane + 64] : 0;
   const bool bad = (o0 && (i0 < 0 || i0 >= E)) || (o1 && (i1 < 0 || i1 >= E));
-  float* drow = grad_logits + row * E;
   if (__ballot(bad) != 0ull) {
-    if (has0) drow[lane] = 0.0f;
-    if (has1) drow[lane + 64] = 0.0f;
+    if (has0) put(lane, 0.0f);
+    if (has1) put(lane + 64, 0.0f);
     return;
   }
   const float d0 = o0 ? Elem<DT>::to_f(grad_w[row * k + lane]) : 0.0f;
@@ -406,8 +466,8 @@ route_bwd_kernel(const float* __restrict__ src, const int64_t* __restrict__ topk
     if (o1) sg[i1] = w1 * (d1 - dot);
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    if (has0) drow[lane] = sg[lane];
-    if (has1) drow[lane + 64] = sg[lane + 64];
+    if (has0) put(lane, sg[lane]);
+    if (has1) put(lane + 64, sg[lane + 64]);
     return;
   } else {
     const float m = wave_max(fmaxf(has0 ? x0 : -INFINITY, has1 ? x1 : -INFINITY));
@@ -423,8 +483,51 @@ route_bwd_kernel(const float* __restrict__ src, const int64_t* __restrict__ topk
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   const float q0 = has0 ? sg[lane] : 0.0f, q1 = has1 ? sg[lane + 64] : 0.0f;
   const float pd = wave_sum((has0 ? p0 * q0 : 0.0f) + (has1 ? p1 * q1 : 0.0f));
-  if (has0) drow[lane] = p0 * (q0 - pd);
-  if (has1) drow[lane + 64] = p1 * (q1 - pd);
+  if (has0) put(lane, p0 * (q0 - pd));
+  if (has1) put(lane + 64, p1 * (q1 - pd));
+}
+
+// ---- balance loss (router.py:100-111) ----------------------------------------------------
+//
+// aux = coef * E * sum_e f_e * mean_t probs[t, e],  f = counts / max(sum counts, 1).
+// Pass 1: each block sums BL_ROWS rows of probs per expert (coalesced along the row);
+// pass 2: one block adds the partials in block order and forms the scalar, so the result
+// is deterministic.
+constexpr int BL_ROWS = 64;
+
+__global__ void __launch_bounds__(128)
+balance_partial_kernel(const float* __restrict__ probs, int64_t T, int E,
+                       float* __restrict__ partial) {
+  const int e = threadIdx.x;
+  if (e >= E) return;
+  const int64_t r0 = (int64_t)blockIdx.x * BL_ROWS;
+  const int64_t r1 = r0 + BL_ROWS < T ? r0 + BL_ROWS : T;
+  float s = 0.0f;
+  for (int64_t r = r0; r < r1; ++r) s += probs[r * E + e];
+  partial[(int64_t)blockIdx.x * E + e] = s;
+}
+
+__global__ void __launch_bounds__(128)
+balance_final_kernel(const float* __restrict__ partial, int64_t nblk, const int32_t* counts,
+                     int64_t T, int E, float coef, float* __restrict__ aux) {
+  __shared__ float s_part[2][2];
+  const int e = threadIdx.x, lane = e & 63, wave = e >> 6;
+  float col = 0.0f, c = 0.0f;
+  if (e < E) {
+    for (int64_t b = 0; b < nblk; ++b) col += partial[b * E + e];
+    c = (float)counts[e];
+  }
+  float num = wave_sum(c * col), den = wave_sum(c);
+  if (lane == 0) {
+    s_part[wave][0] = num;
+    s_part[wave][1] = den;
+  }
+  __syncthreads();
+  if (e == 0) {
+    const float n = s_part[0][0] + s_part[1][0];
+    const float dsum = fmaxf(s_part[0][1] + s_part[1][1], 1.0f);
+    aux[0] = coef * (float)E * (n / dsum / (float)T);
+  }
 }
 
 constexpr int ROUTE_MAX_EXPERTS = 128;  // two row elements per lane
@@ -433,7 +536,7 @@ constexpr int ROUTE_MAX_EXPERTS = 128;  // two row elements per lane
 
 using namespace nsmoe;
 
-extern "C" int nsmoe_route_fwd(const float* logits, int64_t n_tokens, int32_t n_experts,
+extern "C" int nsmoe_route_fwd(const void* logits, int64_t n_tokens, int32_t n_experts,
                                int32_t top_k, int32_t flags, int32_t w_dtype, void* topk_w,
                                int64_t* topk_idx, float* probs, void* stream) {
   NSMOE_REQUIRE(n_tokens >= 0, "route_fwd: n_tokens < 0");
@@ -442,6 +545,7 @@ extern "C" int nsmoe_route_fwd(const float* logits, int64_t n_tokens, int32_t n_
   NSMOE_REQUIRE(top_k >= 1 && top_k <= n_experts, "route_fwd: top_k %d outside [1, %d]",
                 top_k, n_experts);
   NSMOE_REQUIRE(!(flags & 1) || probs, "route_fwd: probs requested but NULL");
+  NSMOE_REQUIRE(!(flags & 4) || w_dtype != DT_F32, "route_fwd: 16-bit logits need a 16-bit dtype");
   if (n_tokens == 0) return NSMOE_OK;
   NSMOE_REQUIRE(logits && topk_w && topk_idx, "route_fwd: NULL pointer");
   dim3 grid((unsigned)cdiv(n_tokens, ROUTE_WAVES)), block(ROUTE_THREADS);
@@ -468,34 +572,73 @@ extern "C" int nsmoe_route_fwd(const float* logits, int64_t n_tokens, int32_t n_
   return check_launch("route_fwd_kernel");
 }
 
-extern "C" int nsmoe_route_bwd(const float* src, const int64_t* topk_idx, const void* grad_w,
-                               int32_t w_dtype, const float* grad_probs, int64_t n_tokens,
+extern "C" int nsmoe_route_bwd(const void* src, const int64_t* topk_idx, const void* grad_w,
+                               int32_t w_dtype, const float* grad_probs, const float* grad_aux,
+                               const int32_t* aux_counts, float aux_coef, int64_t n_tokens,
                                int32_t n_experts, int32_t top_k, int32_t flags,
-                               float* grad_logits, void* stream) {
+                               void* grad_logits, void* stream) {
   NSMOE_REQUIRE(n_tokens >= 0, "route_bwd: n_tokens < 0");
   NSMOE_REQUIRE(n_experts >= 1 && n_experts <= ROUTE_MAX_EXPERTS,
                 "route_bwd: n_experts %d outside [1, %d]", n_experts, ROUTE_MAX_EXPERTS);
   NSMOE_REQUIRE(top_k >= 1 && top_k <= n_experts, "route_bwd: bad top_k %d", top_k);
   if (n_tokens == 0) return NSMOE_OK;
   NSMOE_REQUIRE(src && topk_idx && grad_w && grad_logits, "route_bwd: NULL pointer");
+  NSMOE_REQUIRE(!(flags & 4) || w_dtype != DT_F32, "route_bwd: 16-bit logits need a 16-bit dtype");
   dim3 grid((unsigned)cdiv(n_tokens, ROUTE_WAVES)), block(ROUTE_THREADS);
   size_t lds = (size_t)n_experts * ROUTE_WAVES * sizeof(float) * 2;
   hipStream_t s = (hipStream_t)stream;
   switch (w_dtype) {
     case DT_BF16:
       route_bwd_kernel<DT_BF16><<<grid, block, lds, s>>>(src, topk_idx, (const uint16_t*)grad_w,
-          grad_probs, n_tokens, n_experts, top_k, flags, grad_logits);
+          grad_probs, grad_aux, aux_counts, aux_coef, n_tokens, n_experts, top_k, flags,
+          grad_logits);
       break;
     case DT_F16:
       route_bwd_kernel<DT_F16><<<grid, block, lds, s>>>(src, topk_idx, (const uint16_t*)grad_w,
-          grad_probs, n_tokens, n_experts, top_k, flags, grad_logits);
+          grad_probs, grad_aux, aux_counts, aux_coef, n_tokens, n_experts, top_k, flags,
+          grad_logits);
       break;
     case DT_F32:
       route_bwd_kernel<DT_F32><<<grid, block, lds, s>>>(src, topk_idx, (const float*)grad_w,
-          grad_probs, n_tokens, n_experts, top_k, flags, grad_logits);
+          grad_probs, grad_aux, aux_counts, aux_coef, n_tokens, n_experts, top_k, flags,
+          grad_logits);
       break;
     default:
       NSMOE_REQUIRE(false, "route_bwd: unknown dtype %d", w_dtype);
   }
   return check_launch("route_bwd_kernel");
+}
+
+extern "C" size_t nsmoe_balance_loss_workspace_size(int64_t n_tokens, int32_t n_experts) {
+  if (n_tokens <= 0 || n_experts <= 0) return 0;
+  return (size_t)cdiv(n_tokens, BL_ROWS) * (size_t)n_experts * sizeof(float);
+}
+
+extern "C" int nsmoe_balance_loss(const float* probs, const int32_t* counts, int64_t n_tokens,
+                                  int32_t n_experts, float coef, float* aux, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+  NSMOE_REQUIRE(n_tokens >= 0, "balance_loss: n_tokens < 0");
+  NSMOE_REQUIRE(n_experts >= 1 && n_experts <= ROUTE_MAX_EXPERTS,
+                "balance_loss: n_experts %d outside [1, %d]", n_experts, ROUTE_MAX_EXPERTS);
+  NSMOE_REQUIRE(aux && counts, "balance_loss: NULL pointer");
+  hipStream_t s = (hipStream_t)stream;
+  if (n_tokens == 0) {
+    // mean over no rows is NaN in torch (router.py:111 on an empty batch); the block never
+    // calls this with T = 0, but keep the definition total.
+    balance_final_kernel<<<1, 128, 0, s>>>(nullptr, 0, counts, 0, n_experts, coef, aux);
+    return check_launch("balance_final_kernel");
+  }
+  NSMOE_REQUIRE(probs && workspace, "balance_loss: NULL pointer");
+  const size_t need = nsmoe_balance_loss_workspace_size(n_tokens, n_experts);
+  if (workspace_bytes < need) {
+    set_error("balance_loss: workspace %zu B < %zu B", workspace_bytes, need);
+    return NSMOE_EWORKSPACE;
+  }
+  const int64_t nblk = cdiv(n_tokens, BL_ROWS);
+  balance_partial_kernel<<<(unsigned)nblk, 128, 0, s>>>(probs, n_tokens, n_experts,
+                                                        (float*)workspace);
+  NSMOE_TRY(check_launch("balance_partial_kernel"));
+  balance_final_kernel<<<1, 128, 0, s>>>((const float*)workspace, nblk, counts, n_tokens,
+                                         n_experts, coef, aux);
+  return check_launch("balance_final_kernel");
 }

@@ -136,8 +136,8 @@ def route_bwd(src: Tensor, topk_idx: Tensor, grad_w: Tensor, grad_probs: Optiona
     if n:
         nat.check(nat.lib().nsmoe_route_bwd(
             src.data_ptr(), topk_idx.contiguous().data_ptr(), grad_w.data_ptr(),
-            _DT[grad_w.dtype], _p(gp), n, e, k, _route_flags(want_probs, normalize),
-            out.data_ptr(), _stream()), "nsmoe_route_bwd")
+            _DT[grad_w.dtype], _p(gp), None, None, 0.0, n, e, k,
+            _route_flags(want_probs, normalize), out.data_ptr(), _stream()), "nsmoe_route_bwd")
     return out
 
 
@@ -532,3 +532,123 @@ def fused_moe_block_forward(x, w_in, w_out, topk_w, topk_idx, b_in, b_out, w_sh_
                        cast(b_out), cast(b_sh_in), cast(b_sh_out), topk_w.to(x.dtype), sids,
                        offs, counts, inv, activation)
     return out, counts
+
+
+# ---------------------------------------------------------------------------------------
+# the whole block as one autograd node (the MoEBlock fast path)
+# ---------------------------------------------------------------------------------------
+
+class _BlockFunction(torch.autograd.Function):
+    """
+    MoEBlock.forward's kernel path in one autograd node: router GEMM `x @ W` (torch),
+    then through the C ABI the router tail, the dispatch, the weight pack, the grouped
+    routed + shared experts with the combine, and the balance loss; the backward is the
+    experts' backward, the router tail's backward (with the balance-loss gradient folded
+    in analytically) and the two router GEMMs.  Same arithmetic as composing the ops
+    above (route / moe_dispatch / moe_block / balance loss), with a fraction of their
+    per-call host overhead: the block is otherwise bound by the host issuing ~40 small
+    launches per training step.
+    """
+
+    @staticmethod
+    def forward(ctx, x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out,
+                top_k: int, want_probs: bool, normalize: bool, activation: str,
+                aux_coef: float):
+        lib = nat.lib()
+        stream = _stream()
+        dev, dt = x.device, x.dtype
+        n, d = x.shape
+        e = W_r.shape[1]
+        half = dt in (torch.bfloat16, torch.float16)
+        # router.py:69: the GEMM in x's dtype; the kernel widens 16-bit logits itself.
+        logits = x @ W_r
+        if not half:
+            logits = logits.float()
+        flags = _route_flags(want_probs, normalize) | (nat.ROUTE_LOGITS16 if half else 0)
+        topk_w = torch.empty((n, top_k), dtype=dt, device=dev)
+        topk_idx = torch.empty((n, top_k), dtype=torch.int64, device=dev)
+        probs = torch.empty((n, e) if want_probs else (0,), dtype=torch.float32, device=dev)
+        nat.check(lib.nsmoe_route_fwd(logits.data_ptr(), n, e, top_k, flags, _DT[dt],
+                                      topk_w.data_ptr(), topk_idx.data_ptr(), _p(probs),
+                                      stream), "nsmoe_route_fwd")
+        m = n * top_k
+        l_cap = _l_cap(m, e)
+        i32 = torch.int32
+        ibuf = torch.empty(l_cap + l_cap // ALIGN_M + (e + 1) + e + 1 + m, dtype=i32, device=dev)
+        sids, eids, offs, counts, npp, inv = torch.split(
+            ibuf, [l_cap, l_cap // ALIGN_M, e + 1, e, 1, m])
+        ws = _ws(lib.nsmoe_dispatch_workspace_size(m, e), dev)
+        nat.check(lib.nsmoe_dispatch(topk_idx.data_ptr(), m, e, _p(sids), _p(eids),
+                                     offs.data_ptr(), counts.data_ptr(), npp.data_ptr(),
+                                     _p(inv), ws.data_ptr(), ws.numel(), stream),
+                  "nsmoe_dispatch")
+        out, p_in = _experts_forward(x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in,
+                                     b_sh_out, topk_w, sids, offs, counts, inv, activation)
+        if want_probs:
+            aux = torch.empty((), dtype=torch.float32, device=dev)
+            bws = _ws(lib.nsmoe_balance_loss_workspace_size(n, e), dev)
+            nat.check(lib.nsmoe_balance_loss(probs.data_ptr(), counts.data_ptr(), n, e,
+                                             float(aux_coef), aux.data_ptr(), bws.data_ptr(),
+                                             bws.numel(), stream), "nsmoe_balance_loss")
+        else:
+            aux = torch.zeros((), dtype=dt, device=dev)
+        ctx.mark_non_differentiable(counts, topk_idx)
+        ctx.save_for_backward(x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in,
+                              topk_w, topk_idx, probs if want_probs else logits, sids, offs,
+                              counts, inv, p_in)
+        ctx.cfg = (top_k, want_probs, normalize, activation, float(aux_coef), flags,
+                   b_sh_out is not None)
+        return out, aux, counts, topk_idx
+
+    @staticmethod
+    def backward(ctx, g_out, g_aux, g_counts, g_idx):
+        (x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, topk_w, topk_idx, src,
+         sids, offs, counts, inv, p_in) = ctx.saved_tensors
+        top_k, want_probs, normalize, activation, aux_coef, flags, has_b_sh_out = ctx.cfg
+        need = ctx.needs_input_grad
+        n, d = x.shape
+        e = W_r.shape[1]
+        if g_out is None:
+            g_out = torch.zeros_like(x)
+        (dx, dw_in, dw_out, dw_sh_in, dw_sh_out, dtw, db_in, db_out, db_sh_in,
+         db_sh_out) = _experts_backward(g_out, x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out,
+                                        b_sh_in, topk_w, sids, offs, counts, inv, activation,
+                                        b_in is not None, b_out is not None,
+                                        b_sh_in is not None, has_b_sh_out, p_in)
+        half = flags & nat.ROUTE_LOGITS16
+        dlogits = torch.empty((n, e), dtype=x.dtype if half else torch.float32, device=x.device)
+        ga = None
+        if want_probs and g_aux is not None:
+            ga = g_aux.detach().to(torch.float32).reshape(1).contiguous()
+        if n:
+            nat.check(nat.lib().nsmoe_route_bwd(
+                src.data_ptr(), topk_idx.data_ptr(), dtw.data_ptr(), _DT[dtw.dtype], None,
+                _p(ga), counts.data_ptr() if ga is not None else None, aux_coef, n, e, top_k,
+                flags, dlogits.data_ptr(), _stream()), "nsmoe_route_bwd")
+        dl = dlogits if half else dlogits.to(x.dtype)
+        dW_r = x.t().mm(dl) if need[1] else None
+        if need[0]:
+            dx.addmm_(dl, W_r.t())
+        s = w_sh_in is not None
+        return (dx if need[0] else None, dW_r, dw_in, dw_out,
+                dw_sh_in if s else None, dw_sh_out if s else None,
+                db_in if b_in is not None else None, db_out if b_out is not None else None,
+                db_sh_in if b_sh_in is not None else None,
+                db_sh_out if has_b_sh_out else None,
+                None, None, None, None, None)
+
+
+def block_forward(x, router_W, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out,
+                  top_k, want_probs, normalize, activation, aux_coef):
+    """
+    The MoE block on the kernel path: (out [N, d], aux_loss, counts [E] int32,
+    topk_idx [N, k] int64).  aux_loss is the balance loss (fp32) when want_probs, else a
+    zero of x's dtype (router.py:52-54, moe.py:367-372).  Parameters are cast to x's
+    dtype, as the eager matmuls would run.
+    """
+    _check_activation(activation)
+    cast = lambda t: None if t is None else t.to(x.dtype)
+    return _BlockFunction.apply(
+        x.contiguous(), cast(router_W), cast(w_in), cast(w_out), cast(w_sh_in), cast(w_sh_out),
+        cast(b_in), cast(b_out), cast(b_sh_in), cast(b_sh_out), top_k, want_probs, normalize,
+        activation, aux_coef)

@@ -43,7 +43,7 @@ def test_struct_layouts_match_the_header():
 
 
 def test_abi_version_and_alignment():
-    assert nat.lib().nsmoe_abi_version() == 1
+    assert nat.lib().nsmoe_abi_version() == nat.ABI_VERSION == 2
     assert nat.lib().nsmoe_align_m() == mk.ALIGN_M
 
 
@@ -85,7 +85,11 @@ def test_pack_sizes_match_the_fragment_layout():
     (lambda L: L.nsmoe_route_fwd(None, 4, 300, 1, 0, 0, None, None, None, None), "n_experts"),
     (lambda L: L.nsmoe_route_fwd(None, 4, 8, 9, 0, 0, None, None, None, None), "top_k"),
     (lambda L: L.nsmoe_route_fwd(None, 4, 8, 2, 1, 0, None, None, None, None), "probs"),
-    (lambda L: L.nsmoe_route_bwd(None, None, None, 0, None, 4, 8, 0, 0, None, None), "top_k"),
+    (lambda L: L.nsmoe_route_bwd(None, None, None, 0, None, None, None, 0.0, 4, 8, 0, 0, None,
+                                 None), "top_k"),
+    (lambda L: L.nsmoe_route_fwd(None, 4, 8, 2, 4, 2, None, None, None, None), "16-bit"),
+    (lambda L: L.nsmoe_balance_loss(None, None, 4, 0, 0.01, None, None, 0, None), "n_experts"),
+    (lambda L: L.nsmoe_balance_loss(None, None, 4, 8, 0.01, None, None, 0, None), "NULL"),
     (lambda L: L.nsmoe_dispatch(None, -1, 8, None, None, None, None, None, None, None, 0, None),
      "n_pairs"),
     (lambda L: L.nsmoe_dispatch(None, 10, 0, None, None, None, None, None, None, None, 0, None),

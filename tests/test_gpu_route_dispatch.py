@@ -46,6 +46,32 @@ def test_route_indices_bit_exact_with_ties(E, k, train, normalize, levels):
         torch.testing.assert_close(p, p_ref, rtol=2e-6, atol=1e-8)
 
 
+@pytest.mark.parametrize("train", [True, False])
+def test_route_rows_with_and_without_ties_in_one_launch(train):
+    """The kernel takes a fast arg-max path on rows whose top k is unique and the exact
+    introselect on rows with ties; rows of both kinds, interleaved, plus signed zeros,
+    infinities and NaN rows, must all equal CPU torch.topk."""
+    E, k, T = 76, 6, 1024
+    g = torch.Generator().manual_seed(11)
+    logits = (torch.randn(T, E, generator=g) * 0.48).bfloat16().float()
+    ties = tie_heavy(T, E, 3, seed=12)
+    logits[1::3] = ties[1::3]                                  # every third row tie-heavy
+    logits[5, :] = 0.0
+    logits[5, 10] = -0.0                                       # -0 and +0 compare equal
+    logits[7, :6] = torch.tensor([3.0, 2.0, 1.0, 0.5, -0.0, 0.0])
+    logits[8, :] = -float("inf")
+    logits[8, 3] = 1.0                                         # one finite value, rest -inf
+    logits[9, 2] = float("inf")
+    logits[10, 40] = float("nan")
+    logits[11, :8] = torch.arange(8.0)                         # tie exactly at the boundary
+    logits[11, 8:] = 1.0
+    w_ref, idx_ref, _ = R.route_from_logits(logits, k, train, True, torch.float32)
+    w, idx, _ = _gpu_route(logits, k, train, True, torch.float32)
+    assert torch.equal(idx, idx_ref)
+    ok = torch.isfinite(w_ref).all(dim=1)
+    torch.testing.assert_close(w[ok], w_ref[ok], rtol=2e-6, atol=2e-7)
+
+
 def test_route_bf16_gates_and_probs():
     """nanoSpeaker router shape, bf16 gates: at most one bf16 ulp from the CPU cast."""
     p, x, _ = nanospeaker_inputs(4096)
