@@ -210,6 +210,53 @@ int nsmoe_experts_bwd(const nsmoe_experts_args* args, const int32_t* inv,
                       const void* grad_out, const nsmoe_experts_grads* grads,
                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- the whole block, one call per direction ------------------------------------------
+ * MoEBlock.forward's kernel branch (src/model/moe.py:345-418: router tail router.py:79-98,
+ * fused_moe_forward moe_kernel.py:785-803 with the shared experts moe.py:310-329, balance
+ * loss router.py:100-111) and its backward, as a sequence of the entry points above over
+ * caller buffers.  The router GEMM (router.py:69) stays the caller's, before the forward
+ * (logits) and after the backward (grad_logits -> dW_router, dx).
+ *
+ * `args` carries dims, dtype, activation, x, weights and biases; its routing pointers
+ * (topk_w, sorted_ids, pad_offsets, counts, w_in_packed, w_out_packed) and l_cap are
+ * ignored -- the calls place them in `saved`.
+ *
+ * `saved` (nsmoe_block_saved_layout: total bytes and the offset of each part) is written
+ * by the forward and read by the backward: topk_w [T, k] (args dtype), topk_idx [T, k]
+ * int64, probs [T, E] fp32 (train branch only), the dispatch buffers of nsmoe_dispatch,
+ * and the packed weights.
+ *
+ * Forward: out [T, d]; aux [1] fp32 = the balance loss (train branch, route_flags has
+ * NSMOE_ROUTE_PROBS; otherwise untouched).  Backward: grads as nsmoe_experts_bwd
+ * (dtopk_w is ignored: the gate gradient goes straight into the router backward),
+ * grad_logits [T, E] as nsmoe_route_bwd; grad_aux (device fp32 scalar) may be NULL.
+ * `logits` is needed again by the backward in the eval branch.
+ */
+#define NSMOE_SAVED_TOPK_W 0
+#define NSMOE_SAVED_TOPK_IDX 1
+#define NSMOE_SAVED_PROBS 2
+#define NSMOE_SAVED_SORTED_IDS 3
+#define NSMOE_SAVED_EXPERT_IDS 4
+#define NSMOE_SAVED_PAD_OFFSETS 5
+#define NSMOE_SAVED_COUNTS 6
+#define NSMOE_SAVED_N_POST_PAD 7
+#define NSMOE_SAVED_INV 8
+#define NSMOE_SAVED_W_IN_PACKED 9
+#define NSMOE_SAVED_W_OUT_PACKED 10
+#define NSMOE_BLOCK_NSAVED 11
+
+int nsmoe_block_saved_layout(const nsmoe_experts_args* args, int32_t route_flags,
+                             size_t* offsets /* [NSMOE_BLOCK_NSAVED] */, size_t* total_bytes);
+size_t nsmoe_block_fwd_workspace_size(const nsmoe_experts_args* args, int32_t route_flags);
+int nsmoe_block_fwd(const nsmoe_experts_args* args, const void* logits, int32_t route_flags,
+                    float aux_coef, void* saved, void* out, float* aux, void* workspace,
+                    size_t workspace_bytes, void* stream);
+size_t nsmoe_block_bwd_workspace_size(const nsmoe_experts_args* args, int32_t route_flags);
+int nsmoe_block_bwd(const nsmoe_experts_args* args, const void* logits, int32_t route_flags,
+                    float aux_coef, const void* saved, const void* grad_out,
+                    const float* grad_aux, const nsmoe_experts_grads* grads,
+                    void* grad_logits, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

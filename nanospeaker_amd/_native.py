@@ -68,7 +68,19 @@ SIGNATURES = {
     "nsmoe_experts_bwd_workspace_size": (_sz, [ctypes.POINTER(ExpertsArgs)]),
     "nsmoe_experts_bwd": (ctypes.c_int, [ctypes.POINTER(ExpertsArgs), _vp, _vp,
                                          ctypes.POINTER(ExpertsGrads), _vp, _sz, _vp]),
+    "nsmoe_block_saved_layout": (ctypes.c_int, [ctypes.POINTER(ExpertsArgs), _i32,
+                                                ctypes.POINTER(_sz), ctypes.POINTER(_sz)]),
+    "nsmoe_block_fwd_workspace_size": (_sz, [ctypes.POINTER(ExpertsArgs), _i32]),
+    "nsmoe_block_fwd": (ctypes.c_int, [ctypes.POINTER(ExpertsArgs), _vp, _i32, ctypes.c_float,
+                                       _vp, _vp, _vp, _vp, _sz, _vp]),
+    "nsmoe_block_bwd_workspace_size": (_sz, [ctypes.POINTER(ExpertsArgs), _i32]),
+    "nsmoe_block_bwd": (ctypes.c_int, [ctypes.POINTER(ExpertsArgs), _vp, _i32, ctypes.c_float,
+                                       _vp, _vp, _vp, ctypes.POINTER(ExpertsGrads), _vp, _vp,
+                                       _sz, _vp]),
 }
+
+# Parts of the block's `saved` buffer (NSMOE_SAVED_* in nsmoe.h).
+SAVED_TOPK_W, SAVED_TOPK_IDX, SAVED_PROBS, SAVED_COUNTS, BLOCK_NSAVED = 0, 1, 2, 6, 11
 
 
 class NativeLibraryError(RuntimeError):

@@ -490,10 +490,12 @@ route_bwd_kernel(const void* __restrict__ src, const int64_t* __restrict__ topk_
 // ---- balance loss (router.py:100-111) ----------------------------------------------------
 //
 // aux = coef * E * sum_e f_e * mean_t probs[t, e],  f = counts / max(sum counts, 1).
-// Pass 1: each block sums BL_ROWS rows of probs per expert (coalesced along the row);
-// pass 2: one block adds the partials in block order and forms the scalar, so the result
-// is deterministic.
+// Pass 1: each block sums BL_ROWS rows of probs per expert (coalesced along the row, 8
+// independent accumulators so the loads overlap); pass 2: one block adds the partials in a
+// fixed order (8 interleaved partial sums per expert, then combined in order) and forms
+// the scalar, so the result is deterministic.
 constexpr int BL_ROWS = 64;
+constexpr int BL_UNROLL = 8;
 
 __global__ void __launch_bounds__(128)
 balance_partial_kernel(const float* __restrict__ probs, int64_t T, int E,
@@ -501,29 +503,56 @@ balance_partial_kernel(const float* __restrict__ probs, int64_t T, int E,
   const int e = threadIdx.x;
   if (e >= E) return;
   const int64_t r0 = (int64_t)blockIdx.x * BL_ROWS;
-  const int64_t r1 = r0 + BL_ROWS < T ? r0 + BL_ROWS : T;
+  const int nr = (int)(r0 + BL_ROWS < T ? BL_ROWS : T - r0);
+  float acc[BL_UNROLL];
+#pragma unroll
+  for (int u = 0; u < BL_UNROLL; ++u) acc[u] = 0.0f;
+  for (int r = 0; r < nr; r += BL_UNROLL) {
+#pragma unroll
+    for (int u = 0; u < BL_UNROLL; ++u)
+      if (r + u < nr) acc[u] += probs[(r0 + r + u) * E + e];
+  }
   float s = 0.0f;
-  for (int64_t r = r0; r < r1; ++r) s += probs[r * E + e];
+#pragma unroll
+  for (int u = 0; u < BL_UNROLL; ++u) s += acc[u];
   partial[(int64_t)blockIdx.x * E + e] = s;
 }
 
-__global__ void __launch_bounds__(128)
+// 1024 threads: thread (q, e) with q = tid / 128 sums partial blocks q, q + 8, q + 16, ...
+// of expert e; the 8 slices are then added in q order.
+__global__ void __launch_bounds__(1024)
 balance_final_kernel(const float* __restrict__ partial, int64_t nblk, const int32_t* counts,
                      int64_t T, int E, float coef, float* __restrict__ aux) {
+  __shared__ float s_q[8][128];
   __shared__ float s_part[2][2];
-  const int e = threadIdx.x, lane = e & 63, wave = e >> 6;
-  float col = 0.0f, c = 0.0f;
+  const int tid = threadIdx.x, e = tid & 127, q = tid >> 7;
   if (e < E) {
-    for (int64_t b = 0; b < nblk; ++b) col += partial[b * E + e];
-    c = (float)counts[e];
-  }
-  float num = wave_sum(c * col), den = wave_sum(c);
-  if (lane == 0) {
-    s_part[wave][0] = num;
-    s_part[wave][1] = den;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    int64_t b = q;
+    for (; b + 24 < nblk; b += 32) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc[u] += partial[(b + 8 * u) * E + e];
+    }
+    for (int u = 0; b < nblk; b += 8, ++u) acc[u & 3] += partial[b * E + e];
+    s_q[q][e] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
   }
   __syncthreads();
-  if (e == 0) {
+  if (tid < 128) {
+    const int lane = tid & 63, wave = tid >> 6;
+    float col = 0.0f, c = 0.0f;
+    if (e < E) {
+#pragma unroll
+      for (int qq = 0; qq < 8; ++qq) col += s_q[qq][e];
+      c = (float)counts[e];
+    }
+    const float num = wave_sum(c * col), den = wave_sum(c);
+    if (lane == 0) {
+      s_part[wave][0] = num;
+      s_part[wave][1] = den;
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
     const float n = s_part[0][0] + s_part[1][0];
     const float dsum = fmaxf(s_part[0][1] + s_part[1][1], 1.0f);
     aux[0] = coef * (float)E * (n / dsum / (float)T);
@@ -625,7 +654,7 @@ extern "C" int nsmoe_balance_loss(const float* probs, const int32_t* counts, int
   if (n_tokens == 0) {
     // mean over no rows is NaN in torch (router.py:111 on an empty batch); the block never
     // calls this with T = 0, but keep the definition total.
-    balance_final_kernel<<<1, 128, 0, s>>>(nullptr, 0, counts, 0, n_experts, coef, aux);
+    balance_final_kernel<<<1, 1024, 0, s>>>(nullptr, 0, counts, 0, n_experts, coef, aux);
     return check_launch("balance_final_kernel");
   }
   NSMOE_REQUIRE(probs && workspace, "balance_loss: NULL pointer");
@@ -638,7 +667,7 @@ extern "C" int nsmoe_balance_loss(const float* probs, const int32_t* counts, int
   balance_partial_kernel<<<(unsigned)nblk, 128, 0, s>>>(probs, n_tokens, n_experts,
                                                         (float*)workspace);
   NSMOE_TRY(check_launch("balance_partial_kernel"));
-  balance_final_kernel<<<1, 128, 0, s>>>((const float*)workspace, nblk, counts, n_tokens,
-                                         n_experts, coef, aux);
+  balance_final_kernel<<<1, 1024, 0, s>>>((const float*)workspace, nblk, counts, n_tokens,
+                                          n_experts, coef, aux);
   return check_launch("balance_final_kernel");
 }

@@ -21,6 +21,7 @@ There is no fallback: on a GPU tensor a missing library raises.
 from __future__ import annotations
 
 import ctypes
+import threading
 from typing import Optional
 
 import torch
@@ -538,104 +539,144 @@ def fused_moe_block_forward(x, w_in, w_out, topk_w, topk_idx, b_in, b_out, w_sh_
 # the whole block as one autograd node (the MoEBlock fast path)
 # ---------------------------------------------------------------------------------------
 
+class _BlockPlan:
+    """Host state of the block call for one shape: the args struct (dims filled once,
+    pointers refilled before every call), the `saved` layout and the workspace sizes."""
+
+    def __init__(self, dt, activation, n, d, h, e, s, k, flags):
+        lib = nat.lib()
+        self.args = nat.ExpertsArgs(
+            dtype=_DT[dt], activation=KERNEL_ACTIVATIONS[activation], n_tokens=n, d_model=d,
+            d_hidden=h, n_experts=e, n_shared=s, top_k=k, reserved0=0, l_cap=0)
+        self.grads = nat.ExpertsGrads()
+        offs = (ctypes.c_size_t * nat.BLOCK_NSAVED)()
+        total = ctypes.c_size_t()
+        nat.check(lib.nsmoe_block_saved_layout(self.args, flags, offs, ctypes.byref(total)),
+                  "nsmoe_block_saved_layout")
+        self.off = list(offs)
+        self.saved_bytes = total.value
+        self.fwd_ws = lib.nsmoe_block_fwd_workspace_size(self.args, flags)
+        self.bwd_ws = lib.nsmoe_block_bwd_workspace_size(self.args, flags)
+
+    def bind(self, x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out):
+        a = self.args
+        a.x, a.w_in, a.w_out = x.data_ptr(), w_in.data_ptr(), w_out.data_ptr()
+        a.w_sh_in, a.w_sh_out = _p(w_sh_in), _p(w_sh_out)
+        a.b_in, a.b_out, a.b_sh_in, a.b_sh_out = _p(b_in), _p(b_out), _p(b_sh_in), _p(b_sh_out)
+        return a
+
+
+_PLANS = threading.local()
+
+
+def _plan(dt, activation, n, d, h, e, s, k, flags) -> _BlockPlan:
+    cache = getattr(_PLANS, "cache", None)
+    if cache is None:
+        cache = _PLANS.cache = {}
+    key = (dt, activation, n, d, h, e, s, k, flags)
+    plan = cache.get(key)
+    if plan is None:
+        plan = cache[key] = _BlockPlan(dt, activation, n, d, h, e, s, k, flags)
+    return plan
+
+
 class _BlockFunction(torch.autograd.Function):
     """
-    MoEBlock.forward's kernel path in one autograd node: router GEMM `x @ W` (torch),
-    then through the C ABI the router tail, the dispatch, the weight pack, the grouped
-    routed + shared experts with the combine, and the balance loss; the backward is the
-    experts' backward, the router tail's backward (with the balance-loss gradient folded
-    in analytically) and the two router GEMMs.  Same arithmetic as composing the ops
-    above (route / moe_dispatch / moe_block / balance loss), with a fraction of their
-    per-call host overhead: the block is otherwise bound by the host issuing ~40 small
-    launches per training step.
+    MoEBlock.forward's kernel path in one autograd node: the router GEMM `x @ W` (torch),
+    then one C call (nsmoe_block_fwd: router tail, dispatch, weight pack, routed + shared
+    experts with the combine, balance loss); the backward is one C call (nsmoe_block_bwd:
+    experts' backward, router tail's backward with the balance-loss gradient folded in)
+    and the two router GEMMs.  Same arithmetic as composing the per-stage ops above
+    (route / moe_dispatch / moe_block / balance loss) with a fraction of their host cost:
+    at nanoSpeaker's shape the block is otherwise bound by the host issuing its launches.
     """
 
     @staticmethod
     def forward(ctx, x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out,
                 top_k: int, want_probs: bool, normalize: bool, activation: str,
                 aux_coef: float):
-        lib = nat.lib()
-        stream = _stream()
         dev, dt = x.device, x.dtype
         n, d = x.shape
-        e = W_r.shape[1]
+        e, h2 = W_r.shape[1], w_in.shape[2]
+        s = 0 if w_sh_in is None else w_sh_in.shape[0]
         half = dt in (torch.bfloat16, torch.float16)
         # router.py:69: the GEMM in x's dtype; the kernel widens 16-bit logits itself.
         logits = x @ W_r
         if not half:
             logits = logits.float()
         flags = _route_flags(want_probs, normalize) | (nat.ROUTE_LOGITS16 if half else 0)
-        topk_w = torch.empty((n, top_k), dtype=dt, device=dev)
-        topk_idx = torch.empty((n, top_k), dtype=torch.int64, device=dev)
-        probs = torch.empty((n, e) if want_probs else (0,), dtype=torch.float32, device=dev)
-        nat.check(lib.nsmoe_route_fwd(logits.data_ptr(), n, e, top_k, flags, _DT[dt],
-                                      topk_w.data_ptr(), topk_idx.data_ptr(), _p(probs),
-                                      stream), "nsmoe_route_fwd")
-        m = n * top_k
-        l_cap = _l_cap(m, e)
-        i32 = torch.int32
-        ibuf = torch.empty(l_cap + l_cap // ALIGN_M + (e + 1) + e + 1 + m, dtype=i32, device=dev)
-        sids, eids, offs, counts, npp, inv = torch.split(
-            ibuf, [l_cap, l_cap // ALIGN_M, e + 1, e, 1, m])
-        ws = _ws(lib.nsmoe_dispatch_workspace_size(m, e), dev)
-        nat.check(lib.nsmoe_dispatch(topk_idx.data_ptr(), m, e, _p(sids), _p(eids),
-                                     offs.data_ptr(), counts.data_ptr(), npp.data_ptr(),
-                                     _p(inv), ws.data_ptr(), ws.numel(), stream),
-                  "nsmoe_dispatch")
-        out, p_in = _experts_forward(x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in,
-                                     b_sh_out, topk_w, sids, offs, counts, inv, activation)
-        if want_probs:
-            aux = torch.empty((), dtype=torch.float32, device=dev)
-            bws = _ws(lib.nsmoe_balance_loss_workspace_size(n, e), dev)
-            nat.check(lib.nsmoe_balance_loss(probs.data_ptr(), counts.data_ptr(), n, e,
-                                             float(aux_coef), aux.data_ptr(), bws.data_ptr(),
-                                             bws.numel(), stream), "nsmoe_balance_loss")
+        plan = _plan(dt, activation, n, d, h2 // 2, e, s, top_k, flags)
+        saved = torch.empty(plan.saved_bytes, dtype=torch.uint8, device=dev)
+        out = torch.empty((n, d), dtype=dt, device=dev)
+        aux = (torch.empty((), dtype=torch.float32, device=dev) if want_probs
+               else torch.zeros((), dtype=dt, device=dev))
+        if n:
+            ws = torch.empty(plan.fwd_ws, dtype=torch.uint8, device=dev)
+            a = plan.bind(x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out)
+            nat.check(nat.lib().nsmoe_block_fwd(
+                a, logits.data_ptr(), flags, aux_coef, saved.data_ptr(), out.data_ptr(),
+                aux.data_ptr() if want_probs else None, ws.data_ptr(), plan.fwd_ws, _stream()),
+                "nsmoe_block_fwd")
         else:
-            aux = torch.zeros((), dtype=dt, device=dev)
+            saved.zero_()
+        oc, oi = plan.off[nat.SAVED_COUNTS], plan.off[nat.SAVED_TOPK_IDX]
+        counts = saved[oc:oc + 4 * e].view(torch.int32)
+        topk_idx = saved[oi:oi + 8 * n * top_k].view(torch.int64).view(n, top_k)
         ctx.mark_non_differentiable(counts, topk_idx)
         ctx.save_for_backward(x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in,
-                              topk_w, topk_idx, probs if want_probs else logits, sids, offs,
-                              counts, inv, p_in)
-        ctx.cfg = (top_k, want_probs, normalize, activation, float(aux_coef), flags,
-                   b_sh_out is not None)
+                              logits, saved)
+        ctx.cfg = (plan, flags, float(aux_coef), b_sh_out is not None)
         return out, aux, counts, topk_idx
 
     @staticmethod
     def backward(ctx, g_out, g_aux, g_counts, g_idx):
-        (x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, topk_w, topk_idx, src,
-         sids, offs, counts, inv, p_in) = ctx.saved_tensors
-        top_k, want_probs, normalize, activation, aux_coef, flags, has_b_sh_out = ctx.cfg
+        x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, logits, saved = \
+            ctx.saved_tensors
+        plan, flags, aux_coef, has_b_sh_out = ctx.cfg
         need = ctx.needs_input_grad
         n, d = x.shape
         e = W_r.shape[1]
-        if g_out is None:
-            g_out = torch.zeros_like(x)
-        (dx, dw_in, dw_out, dw_sh_in, dw_sh_out, dtw, db_in, db_out, db_sh_in,
-         db_sh_out) = _experts_backward(g_out, x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out,
-                                        b_sh_in, topk_w, sids, offs, counts, inv, activation,
-                                        b_in is not None, b_out is not None,
-                                        b_sh_in is not None, has_b_sh_out, p_in)
-        half = flags & nat.ROUTE_LOGITS16
-        dlogits = torch.empty((n, e), dtype=x.dtype if half else torch.float32, device=x.device)
-        ga = None
-        if want_probs and g_aux is not None:
-            ga = g_aux.detach().to(torch.float32).reshape(1).contiguous()
+        dev, dt = x.device, x.dtype
+        half = bool(flags & nat.ROUTE_LOGITS16)
+        g_out = torch.zeros_like(x) if g_out is None else g_out.to(dt).contiguous()
+        dx = torch.empty_like(x)
+        dw_in, dw_out = torch.empty_like(w_in), torch.empty_like(w_out)
+        s = w_sh_in is not None
+        dw_sh_in = torch.empty_like(w_sh_in) if s else None
+        dw_sh_out = torch.empty_like(w_sh_out) if s else None
+        db_in = torch.empty_like(b_in) if b_in is not None else None
+        db_out = torch.empty_like(b_out) if b_out is not None else None
+        db_sh_in = torch.empty_like(b_sh_in) if b_sh_in is not None else None
+        db_sh_out = (torch.empty((w_sh_in.shape[0], d), dtype=dt, device=dev)
+                     if has_b_sh_out else None)
+        dlogits = torch.empty((n, e), dtype=dt if half else torch.float32, device=dev)
         if n:
-            nat.check(nat.lib().nsmoe_route_bwd(
-                src.data_ptr(), topk_idx.data_ptr(), dtw.data_ptr(), _DT[dtw.dtype], None,
-                _p(ga), counts.data_ptr() if ga is not None else None, aux_coef, n, e, top_k,
-                flags, dlogits.data_ptr(), _stream()), "nsmoe_route_bwd")
-        dl = dlogits if half else dlogits.to(x.dtype)
+            ga = None
+            if (flags & nat.ROUTE_PROBS) and g_aux is not None:
+                ga = g_aux.detach().to(torch.float32).reshape(1).contiguous()
+            gr = plan.grads
+            gr.dx, gr.dw_in, gr.dw_out = dx.data_ptr(), dw_in.data_ptr(), dw_out.data_ptr()
+            gr.dw_sh_in, gr.dw_sh_out, gr.dtopk_w = _p(dw_sh_in), _p(dw_sh_out), None
+            gr.db_in, gr.db_out = _p(db_in), _p(db_out)
+            gr.db_sh_in, gr.db_sh_out = _p(db_sh_in), _p(db_sh_out)
+            ws = torch.empty(plan.bwd_ws, dtype=torch.uint8, device=dev)
+            # b_sh_out does not enter the backward (the shared experts have no gate).
+            a = plan.bind(x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, None)
+            nat.check(nat.lib().nsmoe_block_bwd(
+                a, logits.data_ptr(), flags, aux_coef, saved.data_ptr(), g_out.data_ptr(),
+                _p(ga), gr, dlogits.data_ptr(), ws.data_ptr(), plan.bwd_ws, _stream()),
+                "nsmoe_block_bwd")
+        else:
+            for t in (dw_in, dw_out, dw_sh_in, dw_sh_out, db_in, db_out, db_sh_in, db_sh_out,
+                      dlogits):
+                if t is not None:
+                    t.zero_()
+        dl = dlogits if half else dlogits.to(dt)
         dW_r = x.t().mm(dl) if need[1] else None
         if need[0]:
             dx.addmm_(dl, W_r.t())
-        s = w_sh_in is not None
-        return (dx if need[0] else None, dW_r, dw_in, dw_out,
-                dw_sh_in if s else None, dw_sh_out if s else None,
-                db_in if b_in is not None else None, db_out if b_out is not None else None,
-                db_sh_in if b_sh_in is not None else None,
-                db_sh_out if has_b_sh_out else None,
-                None, None, None, None, None)
+        return (dx if need[0] else None, dW_r, dw_in, dw_out, dw_sh_in, dw_sh_out, db_in, db_out,
+                db_sh_in, db_sh_out, None, None, None, None, None)
 
 
 def block_forward(x, router_W, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out,
