@@ -730,7 +730,12 @@ __global__ void __launch_bounds__(NT) dw_kernel(ExpParams p) {
       }
 }
 
-// Sums the fp32 partials of multi-chunk groups in chunk order.  grid.y = group.
+// Sums the fp32 partials of multi-chunk groups in chunk order.  grid = (DWR_BLOCKS, group).
+// Each thread sums 4 consecutive elements (one 16-byte vector per chunk, chunk loads
+// issued 4 at a time), so the pass streams the partials at full width; the order of the
+// additions is the chunk order for every element, whatever the launch shape.
+constexpr int DWR_BLOCKS = 64;
+
 template <int DT, int MODE>
 __global__ void __launch_bounds__(NT) dw_reduce_kernel(ExpParams p) {
   using T = typename Elem<DT>::T;
@@ -751,10 +756,29 @@ __global__ void __launch_bounds__(NT) dw_reduce_kernel(ExpParams p) {
   const int64_t mn = MODE == 0 ? (int64_t)d * 2 * H : (int64_t)H * d;
   T* dst = g < p.E ? (T*)p.dw_a + (int64_t)g * mn : (T*)p.dw_sh + (int64_t)(g - p.E) * mn;
   const float* src = p.partial + (int64_t)s_base * mn;
-  for (int64_t i = (int64_t)blockIdx.x * NT + threadIdx.x; i < mn; i += (int64_t)gridDim.x * NT) {
-    float s = 0.0f;
-    for (int c = 0; c < nch; ++c) s += src[(int64_t)c * mn + i];
-    dst[i] = Elem<DT>::from_f(s);
+  const int64_t n4 = (mn % 4 == 0) ? mn / 4 : 0;  // 16-byte vectors (every partial is 16-B aligned)
+  for (int64_t i = (int64_t)blockIdx.x * NT + threadIdx.x; i < n4; i += (int64_t)gridDim.x * NT) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    int c = 0;
+    for (; c + 4 <= nch; c += 4) {
+      const f32x4 a0 = ((const f32x4*)(src + (int64_t)c * mn))[i];
+      const f32x4 a1 = ((const f32x4*)(src + (int64_t)(c + 1) * mn))[i];
+      const f32x4 a2 = ((const f32x4*)(src + (int64_t)(c + 2) * mn))[i];
+      const f32x4 a3 = ((const f32x4*)(src + (int64_t)(c + 3) * mn))[i];
+      acc += a0;
+      acc += a1;
+      acc += a2;
+      acc += a3;
+    }
+    for (; c < nch; ++c) acc += ((const f32x4*)(src + (int64_t)c * mn))[i];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dst[i * 4 + e] = Elem<DT>::from_f(acc[e]);
+  }
+  for (int64_t i = n4 * 4 + (int64_t)blockIdx.x * NT + threadIdx.x; i < mn;
+       i += (int64_t)gridDim.x * NT) {
+    float acc = 0.0f;
+    for (int c = 0; c < nch; ++c) acc += src[(int64_t)c * mn + i];
+    dst[i] = Elem<DT>::from_f(acc);
   }
 }
 
@@ -992,7 +1016,7 @@ static int experts_bwd_impl(const nsmoe_experts_args* a, const int32_t* inv, con
       timer.stop();
       NSMOE_TRY(check_launch("dw_kernel<in>"));
     }
-    dim3 rg((unsigned)std::min<int64_t>(cdiv((int64_t)d * 2 * H, NT), 1024), (unsigned)G);
+    dim3 rg(DWR_BLOCKS, (unsigned)G);
     dw_reduce_kernel<DT, 0><<<rg, NT, 0, s>>>(q);
     NSMOE_TRY(check_launch("dw_reduce_kernel<in>"));
   }
@@ -1011,7 +1035,7 @@ static int experts_bwd_impl(const nsmoe_experts_args* a, const int32_t* inv, con
       timer.stop();
       NSMOE_TRY(check_launch("dw_kernel<out>"));
     }
-    dim3 rg((unsigned)std::min<int64_t>(cdiv((int64_t)H * d, NT), 1024), (unsigned)G);
+    dim3 rg(DWR_BLOCKS, (unsigned)G);
     dw_reduce_kernel<DT, 1><<<rg, NT, 0, s>>>(q);
     NSMOE_TRY(check_launch("dw_reduce_kernel<out>"));
   }
