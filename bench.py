@@ -15,6 +15,9 @@ on.  `cpu_baseline` times the CPU restatement of the reference's eager bf16 path
 cores over a bounded sample.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+       python bench.py --calibrate-copy ...      (under rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)
+       python bench.py --pmc-summary FETCH_CSV WRITE_CSV   (-> profiles/hbm_traffic_T8192.md)
+       python bench.py --stats-summary KERNEL_STATS_CSV    (-> profiles/*_kernel_stats.md)
 """
 
 from __future__ import annotations
@@ -29,6 +32,7 @@ import torch
 
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+COPY_BYTES = 256 << 20      # the calibration copy: bytes read and bytes written
 
 
 def parse():
@@ -39,6 +43,13 @@ def parse():
     ap.add_argument("--tokens", type=int, default=8192)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="first run one plain 256 MiB copy kernel, the HBM-counter yardstick")
+    ap.add_argument("--stats-summary", metavar="KERNEL_STATS_CSV",
+                    help="print a rocprofv3 --stats kernel table as markdown, and exit")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="print the HBM-traffic table from two rocprofv3 --pmc runs "
+                         "(FETCH_SIZE, WRITE_SIZE) of `bench.py --calibrate-copy`, and exit")
     return ap.parse_args()
 
 
@@ -69,8 +80,8 @@ def kernel_units(name: str, T: int, k: int, S: int, d: int, H: int, E: int):
         return rows * (2 * H * d), "mfma", "TFLOP/s"
     if name == "combine":           # read k + S rows, write one, per token (+ inv)
         return T * ((k + S) * d * 2 + d * 2 + k * 4), "hbm", "GB/s"
-    if name == "route_fwd":         # logits in, probs out, ids + gates out
-        return T * (E * 4 * 2 + k * 8 + k * 2), "hbm", "GB/s"
+    if name == "route_fwd":         # bf16 logits in, fp32 probs out, ids + gates out
+        return T * (E * 2 + E * 4 + k * 8 + k * 2), "hbm", "GB/s"
     if name == "dispatch":          # ids read twice, sorted ids + inverse written
         return T * k * (8 * 2 + 4 + 4), "hbm", "GB/s"
     if name == "pack":              # W_in (routed + shared) read once and written once
@@ -124,6 +135,104 @@ def time_gpu(m, x, g, steps: int, warmup: int):
     return ms, fwd_ms, kernels, host_ms
 
 
+# bench.py kernel name -> the symbol prefix of the HIP kernel(s) it times.
+KERNEL_SYMBOLS = {
+    "expert_fwd": ("nsmoe::expert_fwd_async_kernel", "nsmoe::expert_fwd_kernel"),
+    "expert_bwd": ("nsmoe::expert_bwd_async_kernel", "nsmoe::expert_bwd_kernel"),
+    "expert_dx": ("nsmoe::expert_dx_async_kernel",),
+    "dw_in": ("nsmoe::dw_async_kernel<0, 0", "nsmoe::dw_kernel<0, 0"),
+    "dw_out": ("nsmoe::dw_async_kernel<0, 1", "nsmoe::dw_kernel<0, 1"),
+    "route_fwd": ("nsmoe::route_fwd_kernel",),
+    "combine": ("nsmoe::combine_kernel",),
+}
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                            "hbm_traffic_T8192.md")
+COPY_SYMBOL = "neg_kernel_cuda"
+
+
+def _pmc_per_kernel(path):
+    """{short kernel name: (dispatches, mean counter value)} from a counter_collection.csv."""
+    import csv
+
+    acc = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            name = r["Kernel_Name"].replace("void ", "").split("(")[0]
+            n, s = acc.get(name, (0, 0.0))
+            acc[name] = (n + 1, s + float(r["Counter_Value"]))
+    return {k: (n, s / n) for k, (n, s) in acc.items()}
+
+
+def pmc_summary(fetch_csv, write_csv):
+    """Markdown table of HBM bytes per launch: FETCH_SIZE and WRITE_SIZE (KiB per
+    dispatch), each scaled by what the same counter reads for the calibration copy
+    (COPY_BYTES read and written) -- the factor that turns the counter into bytes."""
+    fetch, write = _pmc_per_kernel(fetch_csv), _pmc_per_kernel(write_csv)
+
+    def copy_factor(tab):
+        hits = [v for k, v in tab.items() if COPY_SYMBOL in k]
+        if not hits:
+            raise SystemExit("no calibration copy in " + str(tab.keys()))
+        return COPY_BYTES / (hits[0][1] * 1024.0)
+
+    ff, fw = copy_factor(fetch), copy_factor(write)
+    lines = [
+        f"Calibration: the {COPY_BYTES >> 20} MiB copy reads {next(v[1] for k, v in fetch.items() if COPY_SYMBOL in k):.1f} KiB"
+        f" by FETCH_SIZE and {next(v[1] for k, v in write.items() if COPY_SYMBOL in k):.1f} KiB by WRITE_SIZE:"
+        f" bytes = FETCH_SIZE x 1024 x {ff:.4f} and WRITE_SIZE x 1024 x {fw:.4f}.",
+        "",
+        "| bench kernel | HIP kernel | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM bytes / launch |",
+        "|---|---|---|---|---|---|",
+    ]
+    for bname, prefixes in KERNEL_SYMBOLS.items():
+        for sym, (n, fv) in fetch.items():
+            if sym.startswith(prefixes) and sym in write:
+                wv = write[sym][1]
+                tb = fv * 1024 * ff + wv * 1024 * fw
+                lines.append(f"| {bname} | `{sym}` | {n} | {fv:.1f} | {wv:.1f} | {tb:.0f} |")
+    return "\n".join(lines)
+
+
+def stats_summary(path, top=30):
+    """Markdown table of a rocprofv3 `*_kernel_stats.csv`, longest total first."""
+    import csv
+
+    with open(path) as f:
+        rows = sorted(csv.DictReader(f), key=lambda r: -float(r["TotalDurationNs"]))
+    out = ["| kernel | calls | avg us | min us | max us | total ms | % |",
+           "|---|---|---|---|---|---|---|"]
+    for r in rows[:top]:
+        out.append(f"| {r['Name'][:80]} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+                   f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} | "
+                   f"{float(r['TotalDurationNs']) / 1e6:.2f} | {float(r['Percentage']):.1f} |")
+    return "\n".join(out)
+
+
+def committed_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed counter table, or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                cells = [c.strip() for c in line.strip().strip("|").split("|")]
+                if len(cells) == 6 and cells[0] == kernel:
+                    return int(cells[5])
+    except (OSError, ValueError):
+        return None
+    return None
+
+
+def calibrate_copy():
+    """One dispatch of torch's elementwise negation over 256 MiB of bf16: it reads and
+    writes exactly COPY_BYTES each, so under `rocprofv3 --pmc FETCH_SIZE` (or WRITE_SIZE)
+    its counter value fixes the KiB-to-bytes factor applied to the other kernels."""
+    src = torch.ones(COPY_BYTES // 2, dtype=torch.bfloat16, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+
+
 def cpu_baseline(seconds: float):
     """The reference's eager bf16 CPU path (restated in oracle/moe_ref.py), fwd + bwd."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
@@ -154,6 +263,12 @@ def cpu_baseline(seconds: float):
 
 def main():
     a = parse()
+    if a.pmc_summary:
+        print(pmc_summary(*a.pmc_summary))
+        return
+    if a.stats_summary:
+        print(stats_summary(a.stats_summary))
+        return
     if a.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; multi-GPU sharding is "
                                    "design-only, so --gpus must be 1"}))
@@ -162,6 +277,8 @@ def main():
         print(json.dumps({"error": "no GPU visible"}))
         sys.exit(1)
     T = a.tokens
+    if a.calibrate_copy:
+        calibrate_copy()
     m, x, g = build_block(T)
     m = m.cuda()
     x, g = x.cuda(), g.cuda()
@@ -179,7 +296,9 @@ def main():
             achieved, peak = units / avg_s / 1e9, PEAK_HBM_GBS
         roofline = {"kernel": dom, "bound": bound, "achieved": round(achieved, 2),
                     "peak": peak, "unit": unit, "frac": round(achieved / peak, 4),
-                    "traffic": None, "avg_launch_us": round(kernels[dom][0] * 1e3, 2),
+                    "traffic": committed_traffic(dom) if T == 8192 else None,
+                    "traffic_source": "profiles/" + os.path.basename(TRAFFIC_FILE),
+                    "avg_launch_us": round(kernels[dom][0] * 1e3, 2),
                     "algorithmic_per_launch": units}
     rec = {
         "metric": "MoE-block tokens/s fwd & fwd+bwd at T=8192 bf16; % of MFMA / HBM peak",
