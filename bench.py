@@ -84,6 +84,10 @@ def kernel_units(name: str, T: int, k: int, S: int, d: int, H: int, E: int):
         return T * (E * 2 + E * 4 + k * 8 + k * 2), "hbm", "GB/s"
     if name == "dispatch":          # ids read twice, sorted ids + inverse written
         return T * k * (8 * 2 + 4 + 4), "hbm", "GB/s"
+    if name == "combine_dx":        # expert dX rows + d(logits) in, dx out, per token
+        return T * ((k + S) * d * 2 + (E + 7) // 8 * 8 * 2 + d * 2 + k * 4), "hbm", "GB/s"
+    if name == "router_dw":         # x and d(logits) read once
+        return T * (d * 2 + (E + 7) // 8 * 8 * 2), "hbm", "GB/s"
     if name == "pack":              # W_in (routed + shared) read once and written once
         return (E + S) * d * 2 * H * 2 * 2, "hbm", "GB/s"
     return None
@@ -116,7 +120,7 @@ def time_gpu(m, x, g, steps: int, warmup: int):
     ms = (time.perf_counter() - t0) * 1e3 / steps
     kernels = {}
     for name in ("route_fwd", "dispatch", "pack", "expert_fwd", "combine", "expert_bwd",
-                 "expert_dx", "dw_in", "dw_out"):
+                 "expert_dx", "dw_in", "dw_out", "combine_dx", "router_dw"):
         tot, n = nat.timing_read(name)
         if n:
             kernels[name] = (tot / n, n // steps)

@@ -46,7 +46,8 @@ int32_t nsmoe_abi_version(void);
 /* Measurement hooks (no counterpart in the reference; used by bench.py).  When enabled,
  * the library records a HIP event pair on the launch stream around each launch of its
  * main kernels ("pack", "route_fwd", "dispatch", "expert_fwd", "combine",
- * "expert_bwd", "expert_dx", "dw_in", "dw_out") until `capacity` pairs are used.
+ * "expert_bwd", "expert_dx", "dw_in", "dw_out", "combine_dx", "router_dw") until
+ * `capacity` pairs are used.
  * nsmoe_timing_read waits for the recorded events of one kernel and returns their
  * summed duration.  capacity 0 disables timing and frees the events. */
 int nsmoe_timing_enable(int32_t capacity);
@@ -214,8 +215,10 @@ int nsmoe_experts_bwd(const nsmoe_experts_args* args, const int32_t* inv,
  * MoEBlock.forward's kernel branch (src/model/moe.py:345-418: router tail router.py:79-98,
  * fused_moe_forward moe_kernel.py:785-803 with the shared experts moe.py:310-329, balance
  * loss router.py:100-111) and its backward, as a sequence of the entry points above over
- * caller buffers.  The router GEMM (router.py:69) stays the caller's, before the forward
- * (logits) and after the backward (grad_logits -> dW_router, dx).
+ * caller buffers.  The router GEMM's forward (router.py:69) is the caller's: it passes
+ * the logits in.  Its backward is either done here (w_router given: dx gets
+ * d(logits) W^T, grad_w_router gets x^T d(logits)) or left to the caller (w_router NULL:
+ * grad_logits receives d(logits)).
  *
  * `args` carries dims, dtype, activation, x, weights and biases; its routing pointers
  * (topk_w, sorted_ids, pad_offsets, counts, w_in_packed, w_out_packed) and l_cap are
@@ -228,9 +231,16 @@ int nsmoe_experts_bwd(const nsmoe_experts_args* args, const int32_t* inv,
  *
  * Forward: out [T, d]; aux [1] fp32 = the balance loss (train branch, route_flags has
  * NSMOE_ROUTE_PROBS; otherwise untouched).  Backward: grads as nsmoe_experts_bwd
- * (dtopk_w is ignored: the gate gradient goes straight into the router backward),
- * grad_logits [T, E] as nsmoe_route_bwd; grad_aux (device fp32 scalar) may be NULL.
- * `logits` is needed again by the backward in the eval branch.
+ * (dtopk_w is ignored: the gate gradient goes straight into the router backward);
+ * grad_aux (device fp32 scalar) may be NULL.  `logits` is needed again by the backward in
+ * the eval branch.
+ *   w_router [d, E] non-NULL (bf16/fp16, d % 16 == 0, E % 4 == 0, E <= 128): grads->dx
+ *     is the whole input gradient (experts + router), grad_w_router [d, E] receives the
+ *     router weight's gradient, grad_logits is unused; the workspace is
+ *     nsmoe_block_bwd_workspace_size(args, route_flags, 1).
+ *   w_router NULL: grads->dx holds the experts' part only, grad_logits [T, E] receives
+ *     d(logits) as nsmoe_route_bwd writes it, grad_w_router is unused; workspace
+ *     nsmoe_block_bwd_workspace_size(args, route_flags, 0).
  */
 #define NSMOE_SAVED_TOPK_W 0
 #define NSMOE_SAVED_TOPK_IDX 1
@@ -251,11 +261,13 @@ size_t nsmoe_block_fwd_workspace_size(const nsmoe_experts_args* args, int32_t ro
 int nsmoe_block_fwd(const nsmoe_experts_args* args, const void* logits, int32_t route_flags,
                     float aux_coef, void* saved, void* out, float* aux, void* workspace,
                     size_t workspace_bytes, void* stream);
-size_t nsmoe_block_bwd_workspace_size(const nsmoe_experts_args* args, int32_t route_flags);
+size_t nsmoe_block_bwd_workspace_size(const nsmoe_experts_args* args, int32_t route_flags,
+                                      int32_t fuse_router);
 int nsmoe_block_bwd(const nsmoe_experts_args* args, const void* logits, int32_t route_flags,
                     float aux_coef, const void* saved, const void* grad_out,
                     const float* grad_aux, const nsmoe_experts_grads* grads,
-                    void* grad_logits, void* workspace, size_t workspace_bytes, void* stream);
+                    const void* w_router, void* grad_w_router, void* grad_logits,
+                    void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

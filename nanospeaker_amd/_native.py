@@ -15,7 +15,7 @@ LIB_PATH = Path(os.environ.get("NSMOE_LIB", Path(__file__).resolve().parent / "l
 
 BF16, F16, F32 = 0, 1, 2
 ROUTE_PROBS, ROUTE_NORMALIZE, ROUTE_LOGITS16 = 1, 2, 4
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # Every symbol include/nsmoe.h declares, with (restype, argtypes).
 _vp, _i32, _i64, _sz = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t
@@ -73,10 +73,10 @@ SIGNATURES = {
     "nsmoe_block_fwd_workspace_size": (_sz, [ctypes.POINTER(ExpertsArgs), _i32]),
     "nsmoe_block_fwd": (ctypes.c_int, [ctypes.POINTER(ExpertsArgs), _vp, _i32, ctypes.c_float,
                                        _vp, _vp, _vp, _vp, _sz, _vp]),
-    "nsmoe_block_bwd_workspace_size": (_sz, [ctypes.POINTER(ExpertsArgs), _i32]),
+    "nsmoe_block_bwd_workspace_size": (_sz, [ctypes.POINTER(ExpertsArgs), _i32, _i32]),
     "nsmoe_block_bwd": (ctypes.c_int, [ctypes.POINTER(ExpertsArgs), _vp, _i32, ctypes.c_float,
                                        _vp, _vp, _vp, ctypes.POINTER(ExpertsGrads), _vp, _vp,
-                                       _sz, _vp]),
+                                       _vp, _vp, _sz, _vp]),
 }
 
 # Parts of the block's `saved` buffer (NSMOE_SAVED_* in nsmoe.h).

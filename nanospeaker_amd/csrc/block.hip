@@ -16,6 +16,7 @@
 
 #include "experts_common.h"
 #include "pack.h"
+#include "router_grad.h"
 #include "../../include/nsmoe.h"
 
 namespace nsmoe {
@@ -127,57 +128,117 @@ extern "C" int nsmoe_block_fwd(const nsmoe_experts_args* a, const void* logits,
                                                    : nullptr;
   int64_t* topk_idx = (int64_t*)(sv + L.off[NSMOE_SAVED_TOPK_IDX]);
   int32_t* inv = (int32_t*)(sv + L.off[NSMOE_SAVED_INV]);
-  NSMOE_TRY(nsmoe_route_fwd(logits, T, E, k, route_flags, a->dtype, (void*)b.topk_w, topk_idx,
-                            probs, stream));
+  // In training the route kernel also leaves the balance loss's per-workgroup column
+  // sums of probs in the workspace, so probs is not read back for the loss.
+  float* colsum = probs ? (float*)(ws + dsp + exp) : nullptr;
+  NSMOE_TRY(route_fwd_launch(logits, T, E, k, route_flags, a->dtype, (void*)b.topk_w, topk_idx,
+                             probs, colsum, (hipStream_t)stream));
   NSMOE_TRY(nsmoe_dispatch(topk_idx, m, E, (int32_t*)b.sorted_ids,
                            (int32_t*)(sv + L.off[NSMOE_SAVED_EXPERT_IDS]),
                            (int32_t*)b.pad_offsets, (int32_t*)b.counts,
                            (int32_t*)(sv + L.off[NSMOE_SAVED_N_POST_PAD]), inv, ws, dsp, stream));
   NSMOE_TRY(nsmoe_pack_weights(&b, (void*)b.w_in_packed, (void*)b.w_out_packed, stream));
   NSMOE_TRY(nsmoe_experts_fwd(&b, inv, out, ws + dsp, exp, stream));
-  if (route_flags & NSMOE_ROUTE_PROBS)
-    NSMOE_TRY(nsmoe_balance_loss(probs, b.counts, T, E, aux_coef, aux, ws + dsp + exp, bal,
-                                 stream));
+  if (probs)
+    NSMOE_TRY(balance_final_launch(colsum, T, E, b.counts, aux_coef, aux, (hipStream_t)stream));
   return NSMOE_OK;
 }
 
+namespace nsmoe {
+
+// Backward workspace: the gate gradient (T x k), the expert backward's workspace, and on
+// the fused router path d(logits) at pitch ep plus the router dW partials.
+struct BwdWs {
+  size_t tw, exp, gl, part, total;
+};
+
+static BwdWs bwd_ws(const nsmoe_experts_args* b, bool router) {
+  const size_t es = b->dtype == DT_F32 ? 4 : 2;
+  BwdWs w;
+  w.tw = 0;
+  w.exp = al256((size_t)b->n_tokens * b->top_k * es);
+  w.gl = w.exp + al256(nsmoe_experts_bwd_workspace_size(b));
+  w.part = w.gl;
+  w.total = w.gl;
+  if (router) {
+    w.part = w.gl + al256((size_t)b->n_tokens * router_logits_pitch(b->n_experts) * es);
+    w.total = w.part + al256(router_dw_partial_bytes(b->n_tokens, b->d_model, b->n_experts));
+  }
+  return w;
+}
+
+}  // namespace nsmoe
+
 extern "C" size_t nsmoe_block_bwd_workspace_size(const nsmoe_experts_args* a,
-                                                 int32_t route_flags) {
+                                                 int32_t route_flags, int32_t fuse_router) {
   if (!a) return 0;
   nsmoe_experts_args b = *a;
   b.l_cap = nsmoe_dispatch_l_cap(a->n_tokens * a->top_k, a->n_experts);
   (void)route_flags;
-  const size_t es = a->dtype == DT_F32 ? 4 : 2;
-  return al256((size_t)a->n_tokens * a->top_k * es) + nsmoe_experts_bwd_workspace_size(&b);
+  return bwd_ws(&b, fuse_router != 0).total;
 }
 
 extern "C" int nsmoe_block_bwd(const nsmoe_experts_args* a, const void* logits,
                                int32_t route_flags, float aux_coef, const void* saved,
                                const void* grad_out, const float* grad_aux,
-                               const nsmoe_experts_grads* grads, void* grad_logits,
-                               void* workspace, size_t workspace_bytes, void* stream) {
-  NSMOE_REQUIRE(a && saved && grad_out && grads && grad_logits, "block_bwd: NULL pointer");
+                               const nsmoe_experts_grads* grads, const void* w_router,
+                               void* grad_w_router, void* grad_logits, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  NSMOE_REQUIRE(a && saved && grad_out && grads, "block_bwd: NULL pointer");
+  const bool fuse = w_router != nullptr;
+  NSMOE_REQUIRE(fuse ? grad_w_router != nullptr : grad_logits != nullptr,
+                "block_bwd: NULL %s", fuse ? "grad_w_router" : "grad_logits");
+  NSMOE_REQUIRE(!fuse || router_grad_supported(a->dtype, (int)a->d_model, a->n_experts),
+                "block_bwd: the fused router backward takes bf16/fp16, d %% 16 == 0, "
+                "E %% 4 == 0 and E <= 128 (d %d, E %d)", (int)a->d_model, a->n_experts);
   if (a->n_tokens == 0) return NSMOE_OK;
   const BlockLayout L = block_layout(a, route_flags);
   char* sv = (char*)saved;
   nsmoe_experts_args b = with_routing(a, L, sv);
-  const size_t es = a->dtype == DT_F32 ? 4 : 2;
-  const size_t tw_bytes = al256((size_t)a->n_tokens * a->top_k * es);
-  const size_t need = tw_bytes + nsmoe_experts_bwd_workspace_size(&b);
-  if (!workspace || workspace_bytes < need) {
-    set_error("block_bwd: workspace %zu B < %zu B", workspace_bytes, need);
+  const BwdWs W = bwd_ws(&b, fuse);
+  if (!workspace || workspace_bytes < W.total) {
+    set_error("block_bwd: workspace %zu B < %zu B", workspace_bytes, W.total);
     return NSMOE_EWORKSPACE;
   }
+  hipStream_t s = (hipStream_t)stream;
   char* ws = (char*)workspace;
+  const int32_t* inv = (const int32_t*)(sv + L.off[NSMOE_SAVED_INV]);
   nsmoe_experts_grads g = *grads;
-  g.dtopk_w = ws;  // the gate gradient stays internal: it feeds the router backward
-  NSMOE_TRY(nsmoe_experts_bwd(&b, (const int32_t*)(sv + L.off[NSMOE_SAVED_INV]), grad_out, &g,
-                              ws + tw_bytes, workspace_bytes - tw_bytes, stream));
+  g.dtopk_w = ws + W.tw;  // the gate gradient stays internal: it feeds the router backward
+  NSMOE_TRY(experts_bwd_launch(&b, inv, grad_out, &g, ws + W.exp, W.gl - W.exp, !fuse, s));
   const bool probs = route_flags & NSMOE_ROUTE_PROBS;
   const void* src = probs ? (const void*)(sv + L.off[NSMOE_SAVED_PROBS]) : logits;
   NSMOE_REQUIRE(src, "block_bwd: NULL logits (eval branch)");
-  return nsmoe_route_bwd(src, (const int64_t*)(sv + L.off[NSMOE_SAVED_TOPK_IDX]), ws, a->dtype,
-                         nullptr, probs ? grad_aux : nullptr, probs && grad_aux ? b.counts : nullptr,
-                         aux_coef, a->n_tokens, a->n_experts, a->top_k, route_flags, grad_logits,
-                         stream);
+  const int E = a->n_experts;
+  const int ldg = fuse ? router_logits_pitch(E) : E;
+  void* gl = fuse ? (void*)(ws + W.gl) : grad_logits;
+  NSMOE_TRY(route_bwd_launch(src, (const int64_t*)(sv + L.off[NSMOE_SAVED_TOPK_IDX]),
+                             ws + W.tw, a->dtype, nullptr, probs ? grad_aux : nullptr,
+                             probs && grad_aux ? b.counts : nullptr, aux_coef, a->n_tokens, E,
+                             a->top_k, route_flags, gl, ldg, s));
+  if (!fuse) return NSMOE_OK;
+  CombineDxArgs c;
+  c.rows = ws + W.exp + experts_bwd_dxrows_offset(&b);
+  c.inv = inv;
+  c.glogits = gl;
+  c.w = w_router;
+  c.dx = grads->dx;
+  c.T = a->n_tokens;
+  c.l_cap = b.l_cap;
+  c.d = (int)a->d_model;
+  c.k = a->top_k;
+  c.S = a->n_shared;
+  c.E = E;
+  c.ep = ldg;
+  NSMOE_TRY(combine_dx_launch(a->dtype, c, s));
+  RouterDwArgs r;
+  r.x = a->x;
+  r.glogits = gl;
+  r.partial = (float*)(ws + W.part);
+  r.dw = grad_w_router;
+  r.T = a->n_tokens;
+  r.d = (int)a->d_model;
+  r.E = E;
+  r.ep = ldg;
+  return router_dw_launch(a->dtype, r, s);
 }

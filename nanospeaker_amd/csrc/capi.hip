@@ -117,4 +117,4 @@ extern "C" uint64_t nsmoe_launch_count(void) {
   return nsmoe::g_launches.load(std::memory_order_relaxed);
 }
 
-extern "C" int32_t nsmoe_abi_version(void) { return 2; }
+extern "C" int32_t nsmoe_abi_version(void) { return 3; }

@@ -971,9 +971,12 @@ static BwdLayout bwd_layout(const nsmoe_experts_args* a) {
   return L;
 }
 
+// combine = false leaves the per-row dX in the workspace (bwd_layout(a).dxrow) for the
+// caller to reduce, and gr->dx is not written.
 template <int DT>
 static int experts_bwd_impl(const nsmoe_experts_args* a, const int32_t* inv, const void* dout,
-                            const nsmoe_experts_grads* gr, char* ws, hipStream_t s) {
+                            const nsmoe_experts_grads* gr, char* ws, bool combine,
+                            hipStream_t s) {
   const BwdLayout L = bwd_layout(a);
   ExpParams p = make_params(a);
   const int nbw = nbw_for(a);
@@ -996,8 +999,9 @@ static int experts_bwd_impl(const nsmoe_experts_args* a, const int32_t* inv, con
     timer.stop();
     NSMOE_TRY(check_launch("expert_bwd_kernel"));
   }
-  NSMOE_TRY(launch_combine<DT>(ws + L.dxrow, inv, a->n_tokens, a->d_model, a->top_k,
-                               a->n_shared, a->l_cap, gr->dx, p.fast && aligned16(gr->dx), s));
+  if (combine)
+    NSMOE_TRY(launch_combine<DT>(ws + L.dxrow, inv, a->n_tokens, a->d_model, a->top_k,
+                                 a->n_shared, a->l_cap, gr->dx, p.fast && aligned16(gr->dx), s));
 
   const int d = a->d_model, H = a->d_hidden;
   const int64_t gc = dw_groups_chunks(a);
@@ -1093,15 +1097,17 @@ extern "C" size_t nsmoe_experts_bwd_workspace_size(const nsmoe_experts_args* a) 
   return bwd_layout(a).total;
 }
 
-extern "C" int nsmoe_experts_bwd(const nsmoe_experts_args* a, const int32_t* inv,
-                                 const void* grad_out, const nsmoe_experts_grads* grads,
-                                 void* workspace, size_t workspace_bytes, void* stream) {
+namespace nsmoe {
+
+int experts_bwd_launch(const nsmoe_experts_args* a, const int32_t* inv, const void* grad_out,
+                       const nsmoe_experts_grads* grads, void* workspace,
+                       size_t workspace_bytes, bool combine, hipStream_t s) {
   NSMOE_TRY(validate(a));
   NSMOE_REQUIRE(grads, "experts_bwd: NULL grads");
   if (a->n_tokens == 0) return NSMOE_OK;
   NSMOE_REQUIRE(a->x && a->w_in && a->w_out && a->topk_w && a->sorted_ids && a->pad_offsets &&
-                    a->counts && inv && grad_out && grads->dx && grads->dw_in &&
-                    grads->dw_out && grads->dtopk_w,
+                    a->counts && inv && grad_out && (grads->dx || !combine) &&
+                    grads->dw_in && grads->dw_out && grads->dtopk_w,
                 "experts_bwd: NULL pointer");
   NSMOE_REQUIRE(a->n_shared == 0 || (grads->dw_sh_in && grads->dw_sh_out),
                 "experts_bwd: shared weight gradients missing");
@@ -1111,15 +1117,25 @@ extern "C" int nsmoe_experts_bwd(const nsmoe_experts_args* a, const int32_t* inv
     set_error("experts_bwd: workspace %zu B < %zu B", workspace_bytes, need);
     return NSMOE_EWORKSPACE;
   }
-  hipStream_t s = (hipStream_t)stream;
   switch (a->dtype) {
     case DT_BF16:
-      return experts_bwd_impl<DT_BF16>(a, inv, grad_out, grads, (char*)workspace, s);
+      return experts_bwd_impl<DT_BF16>(a, inv, grad_out, grads, (char*)workspace, combine, s);
     case DT_F16:
-      return experts_bwd_impl<DT_F16>(a, inv, grad_out, grads, (char*)workspace, s);
+      return experts_bwd_impl<DT_F16>(a, inv, grad_out, grads, (char*)workspace, combine, s);
     default:
-      return experts_bwd_impl<DT_F32>(a, inv, grad_out, grads, (char*)workspace, s);
+      return experts_bwd_impl<DT_F32>(a, inv, grad_out, grads, (char*)workspace, combine, s);
   }
+}
+
+size_t experts_bwd_dxrows_offset(const nsmoe_experts_args* a) { return bwd_layout(a).dxrow; }
+
+}  // namespace nsmoe
+
+extern "C" int nsmoe_experts_bwd(const nsmoe_experts_args* a, const int32_t* inv,
+                                 const void* grad_out, const nsmoe_experts_grads* grads,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+  return experts_bwd_launch(a, inv, grad_out, grads, workspace, workspace_bytes, true,
+                            (hipStream_t)stream);
 }
 
 extern "C" int nsmoe_pack_sizes(const nsmoe_experts_args* a, size_t* w_in_bytes,

@@ -18,21 +18,6 @@
 
 namespace nsmoe {
 
-namespace {
-
-// Loads per lane that step s issues, and the vmcnt wait that leaves exactly the steps
-// after s in flight: s + 1 .. s + S - 2 (the issue for s + S - 1 comes after the wait).
-template <int S, class LoadsOf>
-__device__ __forceinline__ void wait_step(int s, int nsteps, LoadsOf loads_of) {
-  int n = 0;
-#pragma unroll
-  for (int u = 1; u <= S - 2; ++u)
-    if (s + u < nsteps) n += loads_of(s + u);
-  wait_vmcnt_dyn(n);
-}
-
-}  // namespace
-
 // ============================ forward ====================================================
 //
 // One workgroup = 4 waves = one 64-row tile of one group.

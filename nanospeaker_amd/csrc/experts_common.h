@@ -119,3 +119,15 @@ int launch_dw_async(int dtype, int mode, const ExpParams& q, int64_t groups_chun
 int launch_bwd_async(int dtype, const ExpParams& p, int nbw, int64_t grid, hipStream_t s);
 
 }  // namespace nsmoe
+
+struct nsmoe_experts_args;
+struct nsmoe_experts_grads;
+
+namespace nsmoe {
+// nsmoe_experts_bwd; with combine = false the per-row dX stay in the workspace at
+// experts_bwd_dxrows_offset(a) (rows as the forward's row space) and grads->dx is unused.
+int experts_bwd_launch(const ::nsmoe_experts_args* a, const int32_t* inv, const void* grad_out,
+                       const ::nsmoe_experts_grads* grads, void* workspace,
+                       size_t workspace_bytes, bool combine, hipStream_t stream);
+size_t experts_bwd_dxrows_offset(const ::nsmoe_experts_args* a);
+}  // namespace nsmoe

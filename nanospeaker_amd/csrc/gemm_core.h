@@ -253,6 +253,18 @@ __device__ __forceinline__ void wait_vmcnt_dyn(int n) {
   }
 }
 
+// For an S-stage copy ring: loads_of(s) is the number of copies per lane that step s
+// issues; waits until step s's copies have landed while steps s + 1 .. s + S - 2 stay in
+// flight (the issue for s + S - 1 comes after the wait).
+template <int S, class LoadsOf>
+__device__ __forceinline__ void wait_step(int s, int nsteps, LoadsOf loads_of) {
+  int n = 0;
+#pragma unroll
+  for (int u = 1; u <= S - 2; ++u)
+    if (s + u < nsteps) n += loads_of(s + u);
+  wait_vmcnt_dyn(n);
+}
+
 // ---- staging: global -> registers -> swizzled LDS -------------------------------------
 //
 // DirectStage copies NROWS rows of 32 contraction elements whose source is contiguous in

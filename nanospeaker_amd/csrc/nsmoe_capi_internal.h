@@ -65,3 +65,21 @@ class KernelTimer {
   hipStream_t stream_;
 };
 }  // namespace nsmoe
+
+namespace nsmoe {
+// Router entry points with the options the block path uses (route.hip).
+// route_fwd_launch: nsmoe_route_fwd, plus optional per-workgroup column sums of probs
+// ([balance_partial_count(n_tokens), n_experts] fp32) for balance_final_launch.
+int route_fwd_launch(const void* logits, int64_t n_tokens, int32_t n_experts, int32_t top_k,
+                     int32_t flags, int32_t w_dtype, void* topk_w, int64_t* topk_idx,
+                     float* probs, float* prob_colsum, hipStream_t stream);
+// route_bwd_launch: nsmoe_route_bwd with grad_logits rows of pitch ldg (pad columns zero).
+int route_bwd_launch(const void* src, const int64_t* topk_idx, const void* grad_w,
+                     int32_t w_dtype, const float* grad_probs, const float* grad_aux,
+                     const int32_t* aux_counts, float aux_coef, int64_t n_tokens,
+                     int32_t n_experts, int32_t top_k, int32_t flags, void* grad_logits,
+                     int32_t ldg, hipStream_t stream);
+int64_t balance_partial_count(int64_t n_tokens);
+int balance_final_launch(const float* partial, int64_t n_tokens, int32_t n_experts,
+                         const int32_t* counts, float coef, float* aux, hipStream_t stream);
+}  // namespace nsmoe

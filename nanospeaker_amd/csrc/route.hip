@@ -1,109 +1,178 @@
 // Router tail on device: softmax, top-k selection with torch-CPU tie order, gate
-// renormalisation, and the matching backward to d(logits).
+// renormalisation, the matching backward to d(logits), and the balance loss.
 //
-// Reference: TopKRouter.forward (src/model/router.py:69-98).  The logits GEMM
-// `(x @ W).float()` (router.py:69) and the optional exploration noise (router.py:76-77)
-// stay in torch; this file takes the fp32 logits from there.
+// Reference: TopKRouter.forward (src/model/router.py:69-98) and balance_loss
+// (router.py:100-111).  The logits GEMM `x @ W` (router.py:69) and the optional
+// exploration noise (router.py:76-77) stay with the caller; this file takes the logits.
 //
-// Layout: one token row per wavefront, four rows per workgroup.  The wave's lanes load
-// the row (coalesced), reduce max / sum for the softmax and write probs; the row's
-// (key, expert id) pairs are staged in LDS as 64-bit words (key bits << 32 | id) so a
-// swap in the selection is one 64-bit move.  The selection itself is sequential (lane 0
-// of the wave): with one row per wave no lane waits on another row's control flow, and
-// T rows give T independent waves to hide the LDS latency of the sequential passes.
+// Forward layout: one token row per wavefront at a time; each workgroup owns RF_ROWS
+// rows (RF_RPW per wave), whose probs it also sums per expert for the balance loss.  A lane holds row elements lane and lane + 64.
+// Row max / sum are DPP butterflies inside each 16-lane row, combined across the four
+// rows through v_readlane in a fixed order.
 //
 // Selection has to reproduce torch's CPU topk bit for bit, ties included: the order of
 // equal keys is whatever libstdc++'s nth_element / sort / partial_sort leave (see
-// ATen/native/TopKImpl.h:44-94).  The routines below restate those published
-// algorithms (introselect with median-of-three, unguarded Hoare partition, heap select,
-// insertion sort, introsort) on the row in LDS.
+// ATen/native/TopKImpl.h:44-94).
+//   * Fast path: k rounds of a wave-wide arg-max.  If every round's maximum is unique
+//     among the values still in play (no NaN, no tie inside the top k, none at its
+//     boundary), the sorted top k is unique, so any selection returns CPU topk's answer.
+//   * Exact path, for rows with a tie that matters: the routines below restate those
+//     published algorithms (introselect with median-of-three, unguarded Hoare partition,
+//     heap select, insertion sort, introsort) on the row as the wave holds it in
+//     registers.  Every access takes a wave-uniform index (a v_readlane, or a lane
+//     compare-and-select for a store), so the sequential algorithm runs in uniform (scalar) control flow
+//     with register latency instead of one lane walking the row through LDS.
 #include "nsmoe_capi_internal.h"
 #include "nsmoe_common.h"
 
 namespace nsmoe {
 
-constexpr int ROUTE_WAVES = 4;  // rows (waves) per workgroup
+constexpr int ROUTE_MAX_EXPERTS = 128;       // two row elements per lane
+constexpr int RF_WAVES = 16;                 // route_fwd: waves per workgroup
+constexpr int RF_RPW = 1;                    // route_fwd: rows per wave (one row per wave
+                                             // measured fastest: a tie row's exact path
+                                             // then delays no other row)
+constexpr int RF_ROWS = RF_WAVES * RF_RPW;   // rows per route_fwd workgroup = rows per
+                                             // balance-loss partial
+constexpr int ROUTE_WAVES = 4;               // route_bwd: rows (waves) per workgroup
 constexpr int ROUTE_THREADS = 64 * ROUTE_WAVES;
 
-struct LaneRow {
-  uint64_t* base;  // the row's element i
-  __device__ __forceinline__ uint64_t& operator[](int i) const { return base[i]; }
+// ---- wave primitives -----------------------------------------------------------------
+
+__device__ __forceinline__ int rl(int v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
+__device__ __forceinline__ float rlf(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
+// Butterfly inside each 16-lane row (xor 1, xor 2, half-row mirror, row mirror: every
+// lane of a row ends with the same value, by commutativity), then the four rows in order.
+template <class Op>
+__device__ __forceinline__ float wave_reduce(float v, Op op) {
+  v = op(v, dpp<0xB1>(v));   // quad_perm [1, 0, 3, 2]
+  v = op(v, dpp<0x4E>(v));   // quad_perm [2, 3, 0, 1]
+  v = op(v, dpp<0x141>(v));  // row_half_mirror
+  v = op(v, dpp<0x140>(v));  // row_mirror
+  return op(op(rlf(v, 0), rlf(v, 16)), op(rlf(v, 32), rlf(v, 48)));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  return wave_reduce(v, [](float a, float b) { return a + b; });
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  return wave_reduce(v, [](float a, float b) { return fmaxf(a, b); });
+}
+
+// ---- the row in registers --------------------------------------------------------------
+
+struct KV {
+  float key;
+  int id;
 };
 
-__device__ __forceinline__ float key_of(uint64_t e) { return __uint_as_float((uint32_t)(e >> 32)); }
-__device__ __forceinline__ int id_of(uint64_t e) { return (int)(uint32_t)e; }
-__device__ __forceinline__ uint64_t pack(float key, int id) {
-  return ((uint64_t)__float_as_uint(key) << 32) | (uint32_t)id;
-}
-
 // "x ranks before y": x is NaN and y is not, or x > y (TopKImpl.h:68-69).
-__device__ __forceinline__ bool gt(uint64_t x, uint64_t y) {
-  float a = key_of(x), b = key_of(y);
+__device__ __forceinline__ bool gt(float a, float b) {
   return (__builtin_isnan(a) && !__builtin_isnan(b)) || a > b;
 }
+__device__ __forceinline__ bool gt(KV x, KV y) { return gt(x.key, y.key); }
 
-__device__ __forceinline__ void swap_at(const LaneRow& a, int i, int j) {
-  uint64_t t = a[i];
-  a[i] = a[j];
-  a[j] = t;
-}
+// Lane `l` of v replaced by x (l wave-uniform): a compare and a select, the VALU
+// equivalent of v_writelane.
+__device__ __forceinline__ int put_lane(int v, int x, int l, int lane) { return lane == l ? x : v; }
+
+// Element i of the row: lane i % 64 of register pair i / 64.  Indices are wave-uniform.
+struct RegRow {
+  int k0, k1;  // key bits of elements lane, lane + 64
+  int i0, i1;  // their ids
+  int lane;
+  // Value selects only: `c ? k0 : k1` on the members would be an lvalue (a select of
+  // member addresses), which keeps the struct in memory -- the compiler then places it
+  // in LDS, and every access becomes an LDS round trip.
+  __device__ __forceinline__ KV get(int i) const {
+    const int l = i & 63;
+    const int ka = rl(k0, l), kb = rl(k1, l), ia = rl(i0, l), ib = rl(i1, l);
+    return i < 64 ? KV{__int_as_float(ka), ia} : KV{__int_as_float(kb), ib};
+  }
+  // Both halves are written through selects (lane -1 matches no lane), so the compiler
+  // keeps the four registers as registers instead of an indexed private array.
+  __device__ __forceinline__ void set(int i, KV v) {
+    const bool lo = i < 64;
+    const int l0 = lo ? i : -1, l1 = lo ? -1 : i - 64;
+    const int kb = __float_as_int(v.key);
+    k0 = put_lane(k0, kb, l0, lane);
+    i0 = put_lane(i0, v.id, l0, lane);
+    k1 = put_lane(k1, kb, l1, lane);
+    i1 = put_lane(i1, v.id, l1, lane);
+  }
+  __device__ __forceinline__ void swap(int i, int j) {
+    const KV t = get(i);
+    set(i, get(j));
+    set(j, t);
+  }
+};
 
 __device__ __forceinline__ int lg2i(int n) { return 31 - __builtin_clz(n); }
 
 // ---- heap primitives on a[first, first + len) ------------------------------------------
 
-__device__ void push_heap_d(const LaneRow& a, int f, int hole, int top, uint64_t value) {
+__device__ __forceinline__ void push_heap_d(RegRow& a, int f, int hole, int top, KV value) {
   int parent = (hole - 1) / 2;
-  while (hole > top && gt(a[f + parent], value)) {
-    a[f + hole] = a[f + parent];
+  while (hole > top) {
+    const KV p = a.get(f + parent);
+    if (!gt(p, value)) break;
+    a.set(f + hole, p);
     hole = parent;
     parent = (hole - 1) / 2;
   }
-  a[f + hole] = value;
+  a.set(f + hole, value);
 }
 
-__device__ void adjust_heap_d(const LaneRow& a, int f, int hole, int len, uint64_t value) {
+__device__ __forceinline__ void adjust_heap_d(RegRow& a, int f, int hole, int len, KV value) {
   const int top = hole;
   int second = hole;
   while (second < (len - 1) / 2) {
     second = 2 * (second + 1);
-    if (gt(a[f + second], a[f + second - 1])) second--;
-    a[f + hole] = a[f + second];
+    if (gt(a.get(f + second), a.get(f + second - 1))) second--;
+    a.set(f + hole, a.get(f + second));
     hole = second;
   }
   if ((len & 1) == 0 && second == (len - 2) / 2) {
     second = 2 * (second + 1);
-    a[f + hole] = a[f + second - 1];
+    a.set(f + hole, a.get(f + second - 1));
     hole = second - 1;
   }
   push_heap_d(a, f, hole, top, value);
 }
 
-__device__ void make_heap_d(const LaneRow& a, int f, int len) {
+__device__ __forceinline__ void make_heap_d(RegRow& a, int f, int len) {
   if (len < 2) return;
   int parent = (len - 2) / 2;
   for (;;) {
-    uint64_t value = a[f + parent];
-    adjust_heap_d(a, f, parent, len, value);
+    adjust_heap_d(a, f, parent, len, a.get(f + parent));
     if (parent == 0) return;
     parent--;
   }
 }
 
 // heap is a[f, f + len); the displaced element is a[f + res]
-__device__ void pop_heap_d(const LaneRow& a, int f, int len, int res) {
-  uint64_t value = a[f + res];
-  a[f + res] = a[f];
+__device__ __forceinline__ void pop_heap_d(RegRow& a, int f, int len, int res) {
+  const KV value = a.get(f + res);
+  a.set(f + res, a.get(f));
   adjust_heap_d(a, f, 0, len, value);
 }
 
-__device__ void heap_select_d(const LaneRow& a, int f, int middle, int last) {
+__device__ __forceinline__ void heap_select_d(RegRow& a, int f, int middle, int last) {
   make_heap_d(a, f, middle);
   for (int i = middle; i < last; ++i)
-    if (gt(a[f + i], a[f])) pop_heap_d(a, f, middle, i);
+    if (gt(a.get(f + i), a.get(f))) pop_heap_d(a, f, middle, i);
 }
 
-__device__ void sort_heap_d(const LaneRow& a, int f, int last) {
+__device__ __forceinline__ void sort_heap_d(RegRow& a, int f, int last) {
   while (last > 1) {
     --last;
     pop_heap_d(a, f, last, last);
@@ -112,24 +181,29 @@ __device__ void sort_heap_d(const LaneRow& a, int f, int last) {
 
 // ---- insertion sorts -----------------------------------------------------------------
 
-__device__ void unguarded_linear_insert_d(const LaneRow& a, int last) {
-  uint64_t val = a[last];
+// The scans below are "unguarded" in libstdc++: a sentinel stops them.  They also stop at
+// the row's ends here, which changes nothing while the sentinels hold and keeps every
+// loop bounded regardless.
+__device__ __forceinline__ void unguarded_linear_insert_d(RegRow& a, int last) {
+  const KV val = a.get(last);
   int next = last - 1;
-  while (gt(val, a[next])) {
-    a[last] = a[next];
+  while (next >= 0) {
+    const KV n = a.get(next);
+    if (!gt(val, n)) break;
+    a.set(last, n);
     last = next;
     --next;
   }
-  a[last] = val;
+  a.set(last, val);
 }
 
-__device__ void insertion_sort_d(const LaneRow& a, int first, int last) {
+__device__ __forceinline__ void insertion_sort_d(RegRow& a, int first, int last) {
   if (first == last) return;
   for (int i = first + 1; i != last; ++i) {
-    if (gt(a[i], a[first])) {
-      uint64_t val = a[i];
-      for (int j = i; j > first; --j) a[j] = a[j - 1];
-      a[first] = val;
+    const KV v = a.get(i);
+    if (gt(v, a.get(first))) {
+      for (int j = i; j > first; --j) a.set(j, a.get(j - 1));
+      a.set(first, v);
     } else {
       unguarded_linear_insert_d(a, i);
     }
@@ -138,64 +212,52 @@ __device__ void insertion_sort_d(const LaneRow& a, int first, int last) {
 
 // ---- partitioning --------------------------------------------------------------------
 
-__device__ void move_median_to_first_d(const LaneRow& a, int result, int x, int y, int z) {
-  if (gt(a[x], a[y])) {
-    if (gt(a[y], a[z])) swap_at(a, result, y);
-    else if (gt(a[x], a[z])) swap_at(a, result, z);
-    else swap_at(a, result, x);
-  } else if (gt(a[x], a[z])) {
-    swap_at(a, result, x);
-  } else if (gt(a[y], a[z])) {
-    swap_at(a, result, z);
+__device__ __forceinline__ void move_median_to_first_d(RegRow& a, int result, int x, int y,
+                                                       int z) {
+  const KV ax = a.get(x), ay = a.get(y), az = a.get(z);
+  if (gt(ax, ay)) {
+    if (gt(ay, az)) a.swap(result, y);
+    else if (gt(ax, az)) a.swap(result, z);
+    else a.swap(result, x);
+  } else if (gt(ax, az)) {
+    a.swap(result, x);
+  } else if (gt(ay, az)) {
+    a.swap(result, z);
   } else {
-    swap_at(a, result, y);
+    a.swap(result, y);
   }
 }
 
-__device__ int unguarded_partition_pivot_d(const LaneRow& a, int first, int last) {
-  int mid = first + (last - first) / 2;
+__device__ __forceinline__ int unguarded_partition_pivot_d(RegRow& a, int first, int last) {
+  const int mid = first + (last - first) / 2;
   move_median_to_first_d(a, first, first + 1, mid, last - 1);
-  const uint64_t pivot = a[first];  // the pivot slot is not touched by the partition
+  const KV pivot = a.get(first);  // the pivot slot is not touched by the partition
   int lo = first + 1, hi = last;
   for (;;) {
-    while (gt(a[lo], pivot)) ++lo;
+    while (lo < last - 1 && gt(a.get(lo), pivot)) ++lo;
     --hi;
-    while (gt(pivot, a[hi])) --hi;
+    while (hi > first && gt(pivot, a.get(hi))) --hi;
     if (!(lo < hi)) return lo;
-    swap_at(a, lo, hi);
+    a.swap(lo, hi);
     ++lo;
   }
 }
 
-__device__ void nth_element_d(const LaneRow& a, int nth, int n) {
-  if (n == 0 || nth == n) return;
-  int first = 0, last = n, depth = lg2i(n) * 2;
-  while (last - first > 3) {
-    if (depth == 0) {
-      heap_select_d(a, first, nth + 1 - first, last - first);
-      swap_at(a, first, nth);
-      return;
-    }
-    --depth;
-    int cut = unguarded_partition_pivot_d(a, first, last);
-    if (cut <= nth) first = cut;
-    else last = cut;
-  }
-  insertion_sort_d(a, first, last);
-}
-
 // std::sort on a[0, n).  introsort_loop recurses on the right part and loops on the
 // left; the subranges it leaves are disjoint, so visiting them from an explicit stack
-// in another order gives the same array.
-__device__ void sort_d(const LaneRow& a, int n) {
+// in another order gives the same array.  The stack lives in lanes of three registers
+// (entry sp in lane sp; at most 2 log2(n) + 1 <= 15 entries for n <= 128).
+__device__ __forceinline__ void sort_d(RegRow& a, int n) {
   if (n == 0) return;
   if (n > 16) {
-    int st_first[40], st_last[40], st_depth[40];
-    int sp = 0;
-    st_first[0] = 0; st_last[0] = n; st_depth[0] = lg2i(n) * 2; sp = 1;
+    int st_first = 0, st_last = 0, st_depth = 0;
+    st_first = put_lane(st_first, 0, 0, a.lane);
+    st_last = put_lane(st_last, n, 0, a.lane);
+    st_depth = put_lane(st_depth, lg2i(n) * 2, 0, a.lane);
+    int sp = 1;
     while (sp > 0) {
       --sp;
-      int first = st_first[sp], last = st_last[sp], depth = st_depth[sp];
+      int first = rl(st_first, sp), last = rl(st_last, sp), depth = rl(st_depth, sp);
       while (last - first > 16) {
         if (depth == 0) {
           heap_select_d(a, first, last - first, last - first);
@@ -203,8 +265,11 @@ __device__ void sort_d(const LaneRow& a, int n) {
           break;
         }
         --depth;
-        int cut = unguarded_partition_pivot_d(a, first, last);
-        st_first[sp] = cut; st_last[sp] = last; st_depth[sp] = depth; ++sp;
+        const int cut = unguarded_partition_pivot_d(a, first, last);
+        st_first = put_lane(st_first, cut, sp, a.lane);
+        st_last = put_lane(st_last, last, sp, a.lane);
+        st_depth = put_lane(st_depth, depth, sp, a.lane);
+        ++sp;
         last = cut;
       }
     }
@@ -215,31 +280,124 @@ __device__ void sort_d(const LaneRow& a, int n) {
   }
 }
 
-// torch CPU topk(largest=True, sorted=True) over the lane's row: afterwards a[0, k)
-// holds the selected (key, id) pairs in output order.
-__device__ void topk_select(const LaneRow& a, int n, int k) {
-  if (k == 0) return;
+// ---- the same steps, wave-parallel ---------------------------------------------------
+//
+// Unguarded Hoare partition of [first, last) around pivot a[first], computed from ranks.
+// On the array as move_median_to_first left it, let L be the ascending positions in
+// (first, last) where the left scan stops (!gt(a[p], pivot)) and R the descending
+// positions in [first, last) where the right scan stops (!gt(pivot, a[p])).  Iteration i
+// of the sequential loop meets lo = L[i], hi = R[i] and swaps them exactly while
+// L[i] < R[i] (positions between the last swapped pair are untouched originals, and a
+// swapped slot stops the opposite scan).  So the loop makes i* = #{i : L[i] < R[i]}
+// swaps, all disjoint, and returns min(L[i*], R[i*-1]) (L[0] when i* = 0).
+// L[i] < R[i] <=> more than i right stoppers lie above L[i]: each lane tests its own
+// positions with ballots, exchanges partner positions through LDS and partner values
+// with ds_bpermute.  `pos` is the wave's [2][128] LDS scratch.
+__device__ __forceinline__ int partition_parallel(RegRow& a, int first, int last, int* pos) {
+  const float pk = a.get(first).key;
+  const int lane = a.lane;
+  const int p0 = lane, p1 = lane + 64;
+  const float x0 = __int_as_float(a.k0), x1 = __int_as_float(a.k1);
+  const bool isL0 = p0 > first && p0 < last && !gt(x0, pk);
+  const bool isL1 = p1 > first && p1 < last && !gt(x1, pk);
+  const bool isR0 = p0 >= first && p0 < last && !gt(pk, x0);
+  const bool isR1 = p1 >= first && p1 < last && !gt(pk, x1);
+  const uint64_t bl0 = __ballot(isL0), bl1 = __ballot(isL1);
+  const uint64_t br0 = __ballot(isR0), br1 = __ballot(isR1);
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  const uint64_t above = lane == 63 ? 0ull : (~0ull << (lane + 1));
+  const int rl0 = __popcll(bl0 & below), rl1 = __popcll(bl0) + __popcll(bl1 & below);
+  const int ar0 = __popcll(br0 & above) + __popcll(br1), ar1 = __popcll(br1 & above);
+  const int istar = __popcll(__ballot(isL0 && ar0 > rl0)) + __popcll(__ballot(isL1 && ar1 > rl1));
+  int* lpos = pos;
+  int* rpos = pos + 128;
+  const bool sl0 = isL0 && rl0 < istar, sl1 = isL1 && rl1 < istar;
+  const bool sr0 = isR0 && ar0 < istar, sr1 = isR1 && ar1 < istar;
+  if (sl0) lpos[rl0] = p0;
+  if (sl1) lpos[rl1] = p1;
+  if (sr0) rpos[ar0] = p0;
+  if (sr1) rpos[ar1] = p1;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const int q0 = sl0 ? rpos[rl0] : sr0 ? lpos[ar0] : p0;
+  const int q1 = sl1 ? rpos[rl1] : sr1 ? lpos[ar1] : p1;
+  const int ad0 = (q0 & 63) * 4, ad1 = (q1 & 63) * 4;
+  const int k00 = __builtin_amdgcn_ds_bpermute(ad0, a.k0), k01 = __builtin_amdgcn_ds_bpermute(ad0, a.k1);
+  const int i00 = __builtin_amdgcn_ds_bpermute(ad0, a.i0), i01 = __builtin_amdgcn_ds_bpermute(ad0, a.i1);
+  const int k10 = __builtin_amdgcn_ds_bpermute(ad1, a.k0), k11 = __builtin_amdgcn_ds_bpermute(ad1, a.k1);
+  const int i10 = __builtin_amdgcn_ds_bpermute(ad1, a.i0), i11 = __builtin_amdgcn_ds_bpermute(ad1, a.i1);
+  // the next round's writes to pos must not overtake these reads
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  a.k0 = q0 < 64 ? k00 : k01;
+  a.i0 = q0 < 64 ? i00 : i01;
+  a.k1 = q1 < 64 ? k10 : k11;
+  a.i1 = q1 < 64 ? i10 : i11;
+  if (istar == 0) return bl0 ? __ffsll((long long)bl0) - 1 : 63 + __ffsll((long long)bl1);
+  const uint64_t n0 = __ballot(isL0 && rl0 == istar), n1 = __ballot(isL1 && rl1 == istar);
+  const uint64_t m0 = __ballot(isR0 && ar0 == istar - 1), m1 = __ballot(isR1 && ar1 == istar - 1);
+  const int lnext = n0 ? __ffsll((long long)n0) - 1 : n1 ? 63 + __ffsll((long long)n1) : 1 << 20;
+  const int rprev = m0 ? __ffsll((long long)m0) - 1 : 63 + __ffsll((long long)m1);
+  return lnext < rprev ? lnext : rprev;
+}
+
+// libstdc++'s insertion sort with a strict comparator moves an element left only past
+// elements it ranks strictly before, so it is the stable sort: the element at p lands at
+// first + #{q : a[q] before a[p]} + #{q < p : a[q] equivalent to a[p]}.  For ranges
+// inside the first 64 slots the ranks are counted in parallel and applied with one
+// ds_permute; other ranges take the sequential routine.
+__device__ __forceinline__ void stable_sort_d(RegRow& a, int first, int last) {
+  if (last - first < 2) return;
+  if (last > 64) {
+    insertion_sort_d(a, first, last);
+    return;
+  }
+  const int p = a.lane;
+  const bool in = p >= first && p < last;
+  const float kp = __int_as_float(a.k0);
+  int rank = first;
+  for (int q = first; q < last; ++q) {
+    const float kq = __int_as_float(rl(a.k0, q));
+    rank += (in && (gt(kq, kp) || (q < p && !gt(kp, kq)))) ? 1 : 0;
+  }
+  const int dst = (in ? rank : p) * 4;
+  a.k0 = __builtin_amdgcn_ds_permute(dst, a.k0);
+  a.i0 = __builtin_amdgcn_ds_permute(dst, a.i0);
+}
+
+// nth_element (introselect) with the partitions and the final insertion sort done
+// wave-parallel; the heap-select fallback at depth 0 stays sequential.
+__device__ __forceinline__ void nth_element_par(RegRow& a, int nth, int n, int* pos) {
+  if (n == 0 || nth == n) return;
+  int first = 0, last = n, depth = lg2i(n) * 2;
+  while (last - first > 3) {
+    if (depth == 0) {
+      heap_select_d(a, first, nth + 1 - first, last - first);
+      a.swap(first, nth);
+      return;
+    }
+    --depth;
+    move_median_to_first_d(a, first, first + 1, first + (last - first) / 2, last - 1);
+    const int cut = partition_parallel(a, first, last, pos);
+    if (cut <= nth) first = cut;
+    else last = cut;
+  }
+  stable_sort_d(a, first, last);
+}
+
+// torch CPU topk(largest=True, sorted=True) over the row: afterwards a[0, k) holds the
+// selected (key, id) pairs in output order.
+__device__ __forceinline__ void topk_select(RegRow& a, int n, int k, int* pos) {
   if (k * 64 <= n) {
     heap_select_d(a, 0, k, n);
     sort_heap_d(a, 0, k);
   } else {
-    nth_element_d(a, k - 1, n);
-    sort_d(a, k - 1);
+    nth_element_par(a, k - 1, n, pos);
+    if (k - 1 <= 16) stable_sort_d(a, 0, k - 1);  // std::sort's insertion-sort branch
+    else sort_d(a, k - 1);
   }
-}
-
-// ---- wave reductions ---------------------------------------------------------------------
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
 }
 
 // ---- forward ---------------------------------------------------------------------------
@@ -250,116 +408,191 @@ __device__ __forceinline__ float wave_max(float v) {
 // Without want_probs the selection runs on the logits and the gates are
 // softmax(topk logits) (normalize) or softmax(logits)[idx] (router.py:83-92).
 // With want_probs and normalize and k > 1 the gates are p / sum(p) (router.py:96-97).
-// E <= 128: each lane holds row elements lane and lane + 64.
 // flags bit 2 (logits16): the logits are stored in the gate dtype DT (the bf16 / fp16 GEMM
 //   output that router.py:69 widens with .float()); they are widened here on load.
+// prob_colsum (optional, want_probs only): [gridDim.x, E] sums of probs over the
+//   workgroup's RF_ROWS rows, in a fixed order -- the first level of the balance loss's
+//   mean over tokens.
 template <int DT>
-__global__ void __launch_bounds__(ROUTE_THREADS)
+__global__ void __launch_bounds__(RF_WAVES * 64)
 route_fwd_kernel(const void* __restrict__ logits, int64_t T, int E, int k, int flags,
                  typename Elem<DT>::T* __restrict__ topk_w, int64_t* __restrict__ topk_idx,
-                 float* __restrict__ probs) {
-  extern __shared__ uint64_t lds_q[];  // [ROUTE_WAVES][E]
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * ROUTE_WAVES + wave;
-  const bool active = row < T;
+                 float* __restrict__ probs, float* __restrict__ prob_colsum) {
+  __shared__ float s_col[RF_WAVES][ROUTE_MAX_EXPERTS];
+  __shared__ int s_pos[RF_WAVES][2 * ROUTE_MAX_EXPERTS];  // exact path: partner positions
+  using OutT = typename Elem<DT>::T;
+  // readfirstlane: the compiler then knows the wave index, and every row condition
+  // below, is wave-uniform (scalar branches, not exec masks).
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const bool want_probs = flags & 1;
   const bool normalize = flags & 2;
-  uint64_t* q = lds_q + wave * E;
   const bool has0 = lane < E, has1 = lane + 64 < E;
+  const int64_t row0 = (int64_t)blockIdx.x * RF_ROWS + wave;  // the wave's rows: row0 + j W
 
-  float v0 = -INFINITY, v1 = -INFINITY;
-  if (active) {
-    if (flags & 4) {
-      const typename Elem<DT>::T* lrow = (const typename Elem<DT>::T*)logits + row * E;
-      if (has0) v0 = Elem<DT>::to_f(lrow[lane]);
-      if (has1) v1 = Elem<DT>::to_f(lrow[lane + 64]);
-    } else {
-      const float* lrow = (const float*)logits + row * E;
-      if (has0) v0 = lrow[lane];
-      if (has1) v1 = lrow[lane + 64];
+  // Phase 0: every row's logits in flight at once (branch-free: lanes past E and rows
+  // past T read a valid element and are masked afterwards).  On gfx9 vmcnt counts stores
+  // as well, so nothing is loaded after the first store.
+  uint32_t raw[RF_RPW][2];
+#pragma unroll
+  for (int j = 0; j < RF_RPW; ++j) {
+    const int64_t row = min(row0 + (int64_t)j * RF_WAVES, T - 1);
+    const int c0 = has0 ? lane : 0, c1 = has1 ? lane + 64 : 0;
+    if constexpr (DT != DT_F32) {
+      if (flags & 4) {
+        const OutT* lrow = (const OutT*)logits + row * E;
+        raw[j][0] = lrow[c0];
+        raw[j][1] = lrow[c1];
+        continue;
+      }
     }
+    const float* lrow = (const float*)logits + row * E;
+    raw[j][0] = __float_as_uint(lrow[c0]);
+    raw[j][1] = __float_as_uint(lrow[c1]);
   }
-  // Row max (NaN-propagating, like torch's softmax) and sum of exp.
-  const bool nan_here = (has0 && __builtin_isnan(v0)) || (has1 && __builtin_isnan(v1));
-  const bool any_nan = __ballot(nan_here) != 0ull;
-  float m = wave_max(fmaxf(v0, v1));
-  if (any_nan) m = __uint_as_float(0x7fc00000u);
-  float row_inv_sum = 0.0f;
-  float k0 = v0, k1 = v1;
-  if (want_probs || !normalize) {
-    const float e0 = has0 ? expf(v0 - m) : 0.0f;
-    const float e1 = has1 ? expf(v1 - m) : 0.0f;
-    row_inv_sum = 1.0f / wave_sum(e0 + e1);
+  // Widened right away, so the one wait for the loads comes before the first store.
+  float val[RF_RPW][2];
+#pragma unroll
+  for (int j = 0; j < RF_RPW; ++j) {
+    float v0, v1;
+    if (DT != DT_F32 && (flags & 4)) {
+      v0 = Elem<DT>::to_f((OutT)raw[j][0]);
+      v1 = Elem<DT>::to_f((OutT)raw[j][1]);
+    } else {
+      v0 = __uint_as_float(raw[j][0]);
+      v1 = __uint_as_float(raw[j][1]);
+    }
+    val[j][0] = has0 ? v0 : -INFINITY;
+    val[j][1] = has1 ? v1 : -INFINITY;
+    // pins the values (and so the load wait) here, ahead of every store below
+    asm volatile("" : "+v"(val[j][0]), "+v"(val[j][1]));
+  }
+
+  // Stores the row's outputs: lane j < k holds output j (and j + 64): key s, id d.
+  auto write_out = [&](int64_t row, float s0, float s1, int d0, int d1, float m,
+                       float row_inv_sum) {
+    int64_t* idx_out = topk_idx + row * k;
+    OutT* w_out = topk_w + row * k;
+    const bool o0 = lane < k, o1 = lane + 64 < k;
+    if (!o0) s0 = 0.0f;
+    if (!o1) s1 = 0.0f;
+    if (o0) idx_out[lane] = d0;
+    if (o1) idx_out[lane + 64] = d1;
+    float w0 = s0, w1 = s1;
     if (want_probs) {
-      k0 = e0 * row_inv_sum;
-      k1 = e1 * row_inv_sum;
-      if (active) {
+      if (normalize && k > 1) {
+        const float S = wave_sum(s0 + s1);
+        w0 = s0 / S;
+        w1 = s1 / S;
+      }
+    } else if (normalize) {
+      const float mk = wave_max(fmaxf(o0 ? s0 : -INFINITY, o1 ? s1 : -INFINITY));
+      const float e0 = o0 ? expf(s0 - mk) : 0.0f, e1 = o1 ? expf(s1 - mk) : 0.0f;
+      const float inv = 1.0f / wave_sum(e0 + e1);
+      w0 = e0 * inv;
+      w1 = e1 * inv;
+    } else {
+      w0 = expf(s0 - m) * row_inv_sum;
+      w1 = expf(s1 - m) * row_inv_sum;
+    }
+    if (o0) w_out[lane] = Elem<DT>::from_f(w0);
+    if (o1) w_out[lane + 64] = Elem<DT>::from_f(w1);
+  };
+
+  // Phase A: softmax, probs, column sums and the fast selection for every row; rows with
+  // a tie that matters are marked for phase B with their keys kept in registers.
+  float key[RF_RPW][2], rmax[RF_RPW], rinv[RF_RPW];
+  unsigned exact_rows = 0;  // wave-uniform bit set
+  float col0 = 0.0f, col1 = 0.0f;  // this wave's sums of probs, elements lane, lane + 64
+#pragma unroll
+  for (int j = 0; j < RF_RPW; ++j) {
+    const int64_t row = row0 + (int64_t)j * RF_WAVES;
+    key[j][0] = key[j][1] = 0.0f;
+    rmax[j] = rinv[j] = 0.0f;
+    if (row >= T) continue;  // wave-uniform
+    const float v0 = val[j][0], v1 = val[j][1];
+    // Row max (NaN-propagating, like torch's softmax) and sum of exp.
+    const bool nan_here = (has0 && __builtin_isnan(v0)) || (has1 && __builtin_isnan(v1));
+    const bool any_nan = __ballot(nan_here) != 0ull;
+    float m = wave_max(fmaxf(v0, v1));
+    if (any_nan) m = __uint_as_float(0x7fc00000u);
+    float row_inv_sum = 0.0f;
+    float k0 = v0, k1 = v1;
+    if (want_probs || !normalize) {
+      const float e0 = has0 ? expf(v0 - m) : 0.0f;
+      const float e1 = has1 ? expf(v1 - m) : 0.0f;
+      row_inv_sum = 1.0f / wave_sum(e0 + e1);
+      if (want_probs) {
+        k0 = e0 * row_inv_sum;
+        k1 = e1 * row_inv_sum;
         float* prow = probs + row * E;
         if (has0) prow[lane] = k0;
         if (has1) prow[lane + 64] = k1;
+        col0 += has0 ? k0 : 0.0f;
+        col1 += has1 ? k1 : 0.0f;
       }
     }
-  }
-  // Fast path: k rounds of a wave-wide arg-max.  If every round's maximum is unique among
-  // the values still in play (no NaN, no tie inside the top k, none at its boundary),
-  // the sorted top k is unique, so any selection returns CPU topk's answer.  A row with
-  // a tie anywhere that matters takes the exact restatement below instead.
-  bool exact = any_nan || !active;
-  if (!exact) {
-    bool av0 = has0, av1 = has1;
-    for (int t = 0; t < k; ++t) {
-      const float c = fmaxf(av0 ? k0 : -INFINITY, av1 ? k1 : -INFINITY);
-      const float mx = wave_max(c);
-      const unsigned long long b0 = __ballot(av0 && k0 == mx);
-      const unsigned long long b1 = __ballot(av1 && k1 == mx);
-      if (__popcll(b0) + __popcll(b1) != 1) {
-        exact = true;
-        break;
+    key[j][0] = k0;
+    key[j][1] = k1;
+    rmax[j] = m;
+    rinv[j] = row_inv_sum;
+    float s0 = 0.0f, s1 = 0.0f;
+    int d0 = 0, d1 = 0;
+    bool exact = any_nan;
+    if (!exact) {
+      bool av0 = has0, av1 = has1;
+      for (int t = 0; t < k; ++t) {
+        const float c = fmaxf(av0 ? k0 : -INFINITY, av1 ? k1 : -INFINITY);
+        const float mx = wave_max(c);
+        const unsigned long long b0 = __ballot(av0 && k0 == mx);
+        const unsigned long long b1 = __ballot(av1 && k1 == mx);
+        if (__popcll(b0) + __popcll(b1) != 1) {
+          exact = true;
+          break;
+        }
+        const int src = b0 ? __ffsll((long long)b0) - 1 : __ffsll((long long)b1) - 1 + 64;
+        if (lane == (src & 63)) {
+          if (src < 64) av0 = false;
+          else av1 = false;
+        }
+        if (lane == (t & 63)) {
+          if (t < 64) { s0 = mx; d0 = src; }
+          else { s1 = mx; d1 = src; }
+        }
       }
-      const int src = b0 ? __ffsll((long long)b0) - 1 : __ffsll((long long)b1) - 1 + 64;
-      if (lane == (src & 63)) {
-        if (src < 64) av0 = false;
-        else av1 = false;
-      }
-      if (lane == 0) q[t] = pack(mx, src);
     }
+    if (exact) exact_rows |= 1u << j;
+    else write_out(row, s0, s1, d0, d1, m, row_inv_sum);
   }
-  if (exact && active) {
-    if (has0) q[lane] = pack(k0, lane);
-    if (has1) q[lane + 64] = pack(k1, lane + 64);
-  }
-  __syncthreads();
-  if (exact && active && lane == 0) topk_select(LaneRow{q}, E, k);
-  __syncthreads();
-  if (!active) return;
 
-  // Lane j < k handles output j (and j + 64 when k > 64).
-  using OutT = typename Elem<DT>::T;
-  int64_t* idx_out = topk_idx + row * k;
-  OutT* w_out = topk_w + row * k;
-  const bool o0 = lane < k, o1 = lane + 64 < k;
-  const float s0 = o0 ? key_of(q[lane]) : 0.0f, s1 = o1 ? key_of(q[lane + 64]) : 0.0f;
-  if (o0) idx_out[lane] = id_of(q[lane]);
-  if (o1) idx_out[lane + 64] = id_of(q[lane + 64]);
-  float w0 = s0, w1 = s1;
-  if (want_probs) {
-    if (normalize && k > 1) {
-      const float S = wave_sum(s0 + s1);
-      w0 = s0 / S;
-      w1 = s1 / S;
-    }
-  } else if (normalize) {
-    const float mk = wave_max(fmaxf(o0 ? s0 : -INFINITY, o1 ? s1 : -INFINITY));
-    const float e0 = o0 ? expf(s0 - mk) : 0.0f, e1 = o1 ? expf(s1 - mk) : 0.0f;
-    const float inv = 1.0f / wave_sum(e0 + e1);
-    w0 = e0 * inv;
-    w1 = e1 * inv;
-  } else {
-    w0 = expf(s0 - m) * row_inv_sum;
-    w1 = expf(s1 - m) * row_inv_sum;
+  // Phase B: the exact restatement for the marked rows.
+  for (int j = 0; j < RF_RPW; ++j) {
+    if (!(exact_rows & (1u << j))) continue;  // wave-uniform
+    float k0 = 0.0f, k1 = 0.0f, m = 0.0f, inv = 0.0f;
+#pragma unroll
+    for (int u = 0; u < RF_RPW; ++u)
+      if (u == j) {
+        k0 = key[u][0];
+        k1 = key[u][1];
+        m = rmax[u];
+        inv = rinv[u];
+      }
+    RegRow r{__float_as_int(k0), __float_as_int(k1), lane, lane + 64, lane};
+    topk_select(r, E, k, s_pos[wave]);
+    write_out(row0 + (int64_t)j * RF_WAVES, __int_as_float(r.k0), __int_as_float(r.k1), r.i0,
+              r.i1, m, inv);
   }
-  if (o0) w_out[lane] = Elem<DT>::from_f(w0);
-  if (o1) w_out[lane + 64] = Elem<DT>::from_f(w1);
+
+  if (prob_colsum) {  // uniform: every wave reaches the barrier
+    s_col[wave][lane] = col0;
+    s_col[wave][lane + 64] = col1;
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+      float s = 0.0f;
+#pragma unroll
+      for (int w = 0; w < RF_WAVES; ++w) s += s_col[w][e];
+      prob_colsum[(int64_t)blockIdx.x * E + e] = s;
+    }
+  }
 }
 
 // ---- backward --------------------------------------------------------------------------
@@ -377,13 +610,14 @@ route_fwd_kernel(const void* __restrict__ logits, int64_t T, int E, int k, int f
 // counts (aux_counts non-NULL) instead of being materialised as a [T, E] tensor.
 // flags bit 2 (logits16): in the eval branches `src` is stored in DT, and grad_logits is
 // written in DT (the gradient of router.py:69's .float()); otherwise both are fp32.
+// grad_logits rows have pitch ldg >= E; the pad columns are written as zeros.
 template <int DT>
 __global__ void __launch_bounds__(ROUTE_THREADS)
 route_bwd_kernel(const void* __restrict__ src, const int64_t* __restrict__ topk_idx,
                  const typename Elem<DT>::T* __restrict__ grad_w,
                  const float* __restrict__ grad_probs, const float* __restrict__ grad_aux,
                  const int32_t* __restrict__ aux_counts, float aux_coef, int64_t T, int E,
-                 int k, int flags, void* __restrict__ grad_logits_v) {
+                 int k, int flags, void* __restrict__ grad_logits_v, int ldg) {
   extern __shared__ float lds_f[];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * ROUTE_WAVES + wave;
@@ -421,9 +655,12 @@ route_bwd_kernel(const void* __restrict__ src, const int64_t* __restrict__ topk_
   }
   // d(logits) is stored through these (fp32, or DT under logits16 in the eval branches).
   auto put = [&](int e, float v) {
-    if (w16) ((ET*)grad_logits_v)[row * E + e] = Elem<DT>::from_f(v);
-    else ((float*)grad_logits_v)[row * E + e] = v;
+    if (w16) ((ET*)grad_logits_v)[row * ldg + e] = Elem<DT>::from_f(v);
+    else ((float*)grad_logits_v)[row * ldg + e] = v;
   };
+  // Pad columns [E, ldg) of the row are zero (ldg - E < 64: lanes past E hold them).
+  if (!has0 && lane < ldg) put(lane, 0.0f);
+  if (!has1 && lane + 64 < ldg) put(lane + 64, 0.0f);
   if (has0) { sv[lane] = x0; sg[lane] = want_probs ? g0 : 0.0f; }
   if (has1) { sv[lane + 64] = x1; sg[lane + 64] = want_probs ? g1 : 0.0f; }
   const bool o0 = lane < k, o1 = lane + 64 < k;
@@ -490,36 +727,36 @@ route_bwd_kernel(const void* __restrict__ src, const int64_t* __restrict__ topk_
 // ---- balance loss (router.py:100-111) ----------------------------------------------------
 //
 // aux = coef * E * sum_e f_e * mean_t probs[t, e],  f = counts / max(sum counts, 1).
-// Pass 1: each block sums BL_ROWS rows of probs per expert (coalesced along the row, 8
-// independent accumulators so the loads overlap); pass 2: one block adds the partials in a
-// fixed order (8 interleaved partial sums per expert, then combined in order) and forms
-// the scalar, so the result is deterministic.
-constexpr int BL_ROWS = 64;
-constexpr int BL_UNROLL = 8;
-
-__global__ void __launch_bounds__(128)
+// Level 1 sums probs over each run of RF_ROWS rows per expert: route_fwd does it on the
+// way (prob_colsum), or balance_partial_kernel from a probs tensor.  Level 2
+// (balance_final_kernel) adds the partials in a fixed order and forms the scalar, so the
+// result is deterministic.
+//
+// balance_partial_kernel: 256 threads per RF_ROWS rows; thread (h, e) sums the rows
+// h * RF_ROWS / 2 + [0, RF_ROWS / 2) of column e with all loads independent, and the
+// two halves are added in order.
+__global__ void __launch_bounds__(256)
 balance_partial_kernel(const float* __restrict__ probs, int64_t T, int E,
                        float* __restrict__ partial) {
-  const int e = threadIdx.x;
-  if (e >= E) return;
-  const int64_t r0 = (int64_t)blockIdx.x * BL_ROWS;
-  const int nr = (int)(r0 + BL_ROWS < T ? BL_ROWS : T - r0);
-  float acc[BL_UNROLL];
+  constexpr int HALF = RF_ROWS / 2;
+  __shared__ float s_half[ROUTE_MAX_EXPERTS];
+  const int e = threadIdx.x & 127, h = threadIdx.x >> 7;
+  const int64_t r0 = (int64_t)blockIdx.x * RF_ROWS + h * HALF;
+  float v[HALF];
 #pragma unroll
-  for (int u = 0; u < BL_UNROLL; ++u) acc[u] = 0.0f;
-  for (int r = 0; r < nr; r += BL_UNROLL) {
-#pragma unroll
-    for (int u = 0; u < BL_UNROLL; ++u)
-      if (r + u < nr) acc[u] += probs[(r0 + r + u) * E + e];
-  }
+  for (int u = 0; u < HALF; ++u)
+    v[u] = (e < E && r0 + u < T) ? probs[(r0 + u) * E + e] : 0.0f;
   float s = 0.0f;
 #pragma unroll
-  for (int u = 0; u < BL_UNROLL; ++u) s += acc[u];
-  partial[(int64_t)blockIdx.x * E + e] = s;
+  for (int u = 0; u < HALF; ++u) s += v[u];
+  if (h == 1) s_half[e] = s;
+  __syncthreads();
+  if (h == 0 && e < E) partial[(int64_t)blockIdx.x * E + e] = s + s_half[e];
 }
 
 // 1024 threads: thread (q, e) with q = tid / 128 sums partial blocks q, q + 8, q + 16, ...
-// of expert e; the 8 slices are then added in q order.
+// of expert e (8 running sums, one per stride-64 phase, combined pairwise); the 8 slices
+// are then added in q order.
 __global__ void __launch_bounds__(1024)
 balance_final_kernel(const float* __restrict__ partial, int64_t nblk, const int32_t* counts,
                      int64_t T, int E, float coef, float* __restrict__ aux) {
@@ -527,14 +764,13 @@ balance_final_kernel(const float* __restrict__ partial, int64_t nblk, const int3
   __shared__ float s_part[2][2];
   const int tid = threadIdx.x, e = tid & 127, q = tid >> 7;
   if (e < E) {
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    int64_t b = q;
-    for (; b + 24 < nblk; b += 32) {
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int64_t b = q; b < nblk; b += 64) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) acc[u] += partial[(b + 8 * u) * E + e];
+      for (int u = 0; u < 8; ++u)
+        if (b + 8 * u < nblk) acc[u] += partial[(b + 8 * u) * E + e];
     }
-    for (int u = 0; b < nblk; b += 8, ++u) acc[u & 3] += partial[b * E + e];
-    s_q[q][e] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    s_q[q][e] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
   }
   __syncthreads();
   if (tid < 128) {
@@ -559,15 +795,15 @@ balance_final_kernel(const float* __restrict__ partial, int64_t nblk, const int3
   }
 }
 
-constexpr int ROUTE_MAX_EXPERTS = 128;  // two row elements per lane
-
 }  // namespace nsmoe
 
 using namespace nsmoe;
 
-extern "C" int nsmoe_route_fwd(const void* logits, int64_t n_tokens, int32_t n_experts,
-                               int32_t top_k, int32_t flags, int32_t w_dtype, void* topk_w,
-                               int64_t* topk_idx, float* probs, void* stream) {
+namespace nsmoe {
+
+int route_fwd_launch(const void* logits, int64_t n_tokens, int32_t n_experts, int32_t top_k,
+                     int32_t flags, int32_t w_dtype, void* topk_w, int64_t* topk_idx,
+                     float* probs, float* prob_colsum, hipStream_t s) {
   NSMOE_REQUIRE(n_tokens >= 0, "route_fwd: n_tokens < 0");
   NSMOE_REQUIRE(n_experts >= 1 && n_experts <= ROUTE_MAX_EXPERTS,
                 "route_fwd: n_experts %d outside [1, %d]", n_experts, ROUTE_MAX_EXPERTS);
@@ -575,24 +811,23 @@ extern "C" int nsmoe_route_fwd(const void* logits, int64_t n_tokens, int32_t n_e
                 top_k, n_experts);
   NSMOE_REQUIRE(!(flags & 1) || probs, "route_fwd: probs requested but NULL");
   NSMOE_REQUIRE(!(flags & 4) || w_dtype != DT_F32, "route_fwd: 16-bit logits need a 16-bit dtype");
+  NSMOE_REQUIRE(!prob_colsum || (flags & 1), "route_fwd: column sums need probs");
   if (n_tokens == 0) return NSMOE_OK;
   NSMOE_REQUIRE(logits && topk_w && topk_idx, "route_fwd: NULL pointer");
-  dim3 grid((unsigned)cdiv(n_tokens, ROUTE_WAVES)), block(ROUTE_THREADS);
-  size_t lds = (size_t)n_experts * ROUTE_WAVES * sizeof(uint64_t);
-  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)cdiv(n_tokens, RF_ROWS)), block(RF_WAVES * 64);
   KernelTimer timer("route_fwd", s);
   switch (w_dtype) {
     case DT_BF16:
-      route_fwd_kernel<DT_BF16><<<grid, block, lds, s>>>(logits, n_tokens, n_experts, top_k,
-          flags, (uint16_t*)topk_w, topk_idx, probs);
+      route_fwd_kernel<DT_BF16><<<grid, block, 0, s>>>(logits, n_tokens, n_experts, top_k,
+          flags, (uint16_t*)topk_w, topk_idx, probs, prob_colsum);
       break;
     case DT_F16:
-      route_fwd_kernel<DT_F16><<<grid, block, lds, s>>>(logits, n_tokens, n_experts, top_k,
-          flags, (uint16_t*)topk_w, topk_idx, probs);
+      route_fwd_kernel<DT_F16><<<grid, block, 0, s>>>(logits, n_tokens, n_experts, top_k,
+          flags, (uint16_t*)topk_w, topk_idx, probs, prob_colsum);
       break;
     case DT_F32:
-      route_fwd_kernel<DT_F32><<<grid, block, lds, s>>>(logits, n_tokens, n_experts, top_k,
-          flags, (float*)topk_w, topk_idx, probs);
+      route_fwd_kernel<DT_F32><<<grid, block, 0, s>>>(logits, n_tokens, n_experts, top_k,
+          flags, (float*)topk_w, topk_idx, probs, prob_colsum);
       break;
     default:
       NSMOE_REQUIRE(false, "route_fwd: unknown dtype %d", w_dtype);
@@ -601,36 +836,57 @@ extern "C" int nsmoe_route_fwd(const void* logits, int64_t n_tokens, int32_t n_e
   return check_launch("route_fwd_kernel");
 }
 
-extern "C" int nsmoe_route_bwd(const void* src, const int64_t* topk_idx, const void* grad_w,
-                               int32_t w_dtype, const float* grad_probs, const float* grad_aux,
-                               const int32_t* aux_counts, float aux_coef, int64_t n_tokens,
-                               int32_t n_experts, int32_t top_k, int32_t flags,
-                               void* grad_logits, void* stream) {
+int64_t balance_partial_count(int64_t n_tokens) { return cdiv(n_tokens, RF_ROWS); }
+
+int balance_final_launch(const float* partial, int64_t n_tokens, int32_t n_experts,
+                         const int32_t* counts, float coef, float* aux, hipStream_t s) {
+  const int64_t nblk = n_tokens > 0 ? balance_partial_count(n_tokens) : 0;
+  balance_final_kernel<<<1, 1024, 0, s>>>(partial, nblk, counts, n_tokens, n_experts, coef,
+                                          aux);
+  return check_launch("balance_final_kernel");
+}
+
+}  // namespace nsmoe
+
+extern "C" int nsmoe_route_fwd(const void* logits, int64_t n_tokens, int32_t n_experts,
+                               int32_t top_k, int32_t flags, int32_t w_dtype, void* topk_w,
+                               int64_t* topk_idx, float* probs, void* stream) {
+  return route_fwd_launch(logits, n_tokens, n_experts, top_k, flags, w_dtype, topk_w,
+                          topk_idx, probs, nullptr, (hipStream_t)stream);
+}
+
+namespace nsmoe {
+
+int route_bwd_launch(const void* src, const int64_t* topk_idx, const void* grad_w,
+                     int32_t w_dtype, const float* grad_probs, const float* grad_aux,
+                     const int32_t* aux_counts, float aux_coef, int64_t n_tokens,
+                     int32_t n_experts, int32_t top_k, int32_t flags, void* grad_logits,
+                     int32_t ldg, hipStream_t s) {
   NSMOE_REQUIRE(n_tokens >= 0, "route_bwd: n_tokens < 0");
   NSMOE_REQUIRE(n_experts >= 1 && n_experts <= ROUTE_MAX_EXPERTS,
                 "route_bwd: n_experts %d outside [1, %d]", n_experts, ROUTE_MAX_EXPERTS);
   NSMOE_REQUIRE(top_k >= 1 && top_k <= n_experts, "route_bwd: bad top_k %d", top_k);
+  NSMOE_REQUIRE(ldg >= n_experts && ldg - n_experts < 64, "route_bwd: bad row pitch %d", ldg);
   if (n_tokens == 0) return NSMOE_OK;
   NSMOE_REQUIRE(src && topk_idx && grad_w && grad_logits, "route_bwd: NULL pointer");
   NSMOE_REQUIRE(!(flags & 4) || w_dtype != DT_F32, "route_bwd: 16-bit logits need a 16-bit dtype");
   dim3 grid((unsigned)cdiv(n_tokens, ROUTE_WAVES)), block(ROUTE_THREADS);
   size_t lds = (size_t)n_experts * ROUTE_WAVES * sizeof(float) * 2;
-  hipStream_t s = (hipStream_t)stream;
   switch (w_dtype) {
     case DT_BF16:
       route_bwd_kernel<DT_BF16><<<grid, block, lds, s>>>(src, topk_idx, (const uint16_t*)grad_w,
           grad_probs, grad_aux, aux_counts, aux_coef, n_tokens, n_experts, top_k, flags,
-          grad_logits);
+          grad_logits, ldg);
       break;
     case DT_F16:
       route_bwd_kernel<DT_F16><<<grid, block, lds, s>>>(src, topk_idx, (const uint16_t*)grad_w,
           grad_probs, grad_aux, aux_counts, aux_coef, n_tokens, n_experts, top_k, flags,
-          grad_logits);
+          grad_logits, ldg);
       break;
     case DT_F32:
       route_bwd_kernel<DT_F32><<<grid, block, lds, s>>>(src, topk_idx, (const float*)grad_w,
           grad_probs, grad_aux, aux_counts, aux_coef, n_tokens, n_experts, top_k, flags,
-          grad_logits);
+          grad_logits, ldg);
       break;
     default:
       NSMOE_REQUIRE(false, "route_bwd: unknown dtype %d", w_dtype);
@@ -638,9 +894,21 @@ extern "C" int nsmoe_route_bwd(const void* src, const int64_t* topk_idx, const v
   return check_launch("route_bwd_kernel");
 }
 
+}  // namespace nsmoe
+
+extern "C" int nsmoe_route_bwd(const void* src, const int64_t* topk_idx, const void* grad_w,
+                               int32_t w_dtype, const float* grad_probs, const float* grad_aux,
+                               const int32_t* aux_counts, float aux_coef, int64_t n_tokens,
+                               int32_t n_experts, int32_t top_k, int32_t flags,
+                               void* grad_logits, void* stream) {
+  return route_bwd_launch(src, topk_idx, grad_w, w_dtype, grad_probs, grad_aux, aux_counts,
+                          aux_coef, n_tokens, n_experts, top_k, flags, grad_logits, n_experts,
+                          (hipStream_t)stream);
+}
+
 extern "C" size_t nsmoe_balance_loss_workspace_size(int64_t n_tokens, int32_t n_experts) {
   if (n_tokens <= 0 || n_experts <= 0) return 0;
-  return (size_t)cdiv(n_tokens, BL_ROWS) * (size_t)n_experts * sizeof(float);
+  return (size_t)balance_partial_count(n_tokens) * (size_t)n_experts * sizeof(float);
 }
 
 extern "C" int nsmoe_balance_loss(const float* probs, const int32_t* counts, int64_t n_tokens,
@@ -651,23 +919,19 @@ extern "C" int nsmoe_balance_loss(const float* probs, const int32_t* counts, int
                 "balance_loss: n_experts %d outside [1, %d]", n_experts, ROUTE_MAX_EXPERTS);
   NSMOE_REQUIRE(aux && counts, "balance_loss: NULL pointer");
   hipStream_t s = (hipStream_t)stream;
-  if (n_tokens == 0) {
+  if (n_tokens == 0)
     // mean over no rows is NaN in torch (router.py:111 on an empty batch); the block never
     // calls this with T = 0, but keep the definition total.
-    balance_final_kernel<<<1, 1024, 0, s>>>(nullptr, 0, counts, 0, n_experts, coef, aux);
-    return check_launch("balance_final_kernel");
-  }
+    return balance_final_launch(nullptr, 0, n_experts, counts, coef, aux, s);
   NSMOE_REQUIRE(probs && workspace, "balance_loss: NULL pointer");
   const size_t need = nsmoe_balance_loss_workspace_size(n_tokens, n_experts);
   if (workspace_bytes < need) {
     set_error("balance_loss: workspace %zu B < %zu B", workspace_bytes, need);
     return NSMOE_EWORKSPACE;
   }
-  const int64_t nblk = cdiv(n_tokens, BL_ROWS);
-  balance_partial_kernel<<<(unsigned)nblk, 128, 0, s>>>(probs, n_tokens, n_experts,
-                                                        (float*)workspace);
+  balance_partial_kernel<<<(unsigned)balance_partial_count(n_tokens), 256, 0, s>>>(
+      probs, n_tokens, n_experts, (float*)workspace);
   NSMOE_TRY(check_launch("balance_partial_kernel"));
-  balance_final_kernel<<<1, 1024, 0, s>>>((const float*)workspace, nblk, counts, n_tokens,
-                                          n_experts, coef, aux);
-  return check_launch("balance_final_kernel");
+  return balance_final_launch((const float*)workspace, n_tokens, n_experts, counts, coef, aux,
+                              s);
 }

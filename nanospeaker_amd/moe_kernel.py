@@ -556,7 +556,12 @@ class _BlockPlan:
         self.off = list(offs)
         self.saved_bytes = total.value
         self.fwd_ws = lib.nsmoe_block_fwd_workspace_size(self.args, flags)
-        self.bwd_ws = lib.nsmoe_block_bwd_workspace_size(self.args, flags)
+        # The router GEMM's backward runs inside nsmoe_block_bwd for 16-bit types when
+        # d % 16 == 0 and E % 4 == 0 (E <= 128 always holds here); otherwise in torch.
+        self.fuse_router = (dt in (torch.bfloat16, torch.float16) and d % 16 == 0
+                            and e % 4 == 0 and e <= 128)
+        self.bwd_ws = lib.nsmoe_block_bwd_workspace_size(self.args, flags,
+                                                         int(self.fuse_router))
 
     def bind(self, x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out):
         a = self.args
@@ -585,8 +590,10 @@ class _BlockFunction(torch.autograd.Function):
     MoEBlock.forward's kernel path in one autograd node: the router GEMM `x @ W` (torch),
     then one C call (nsmoe_block_fwd: router tail, dispatch, weight pack, routed + shared
     experts with the combine, balance loss); the backward is one C call (nsmoe_block_bwd:
-    experts' backward, router tail's backward with the balance-loss gradient folded in)
-    and the two router GEMMs.  Same arithmetic as composing the per-stage ops above
+    experts' backward, router tail's backward with the balance-loss gradient folded in,
+    and for 16-bit types the router GEMM's backward, d(logits) W^T fused into the dx
+    combine and x^T d(logits) as a split-K kernel; other types finish the router GEMM's
+    backward in torch).  Same arithmetic as composing the per-stage ops above
     (route / moe_dispatch / moe_block / balance loss) with a fraction of their host cost:
     at nanoSpeaker's shape the block is otherwise bound by the host issuing its launches.
     """
@@ -649,7 +656,10 @@ class _BlockFunction(torch.autograd.Function):
         db_sh_in = torch.empty_like(b_sh_in) if b_sh_in is not None else None
         db_sh_out = (torch.empty((w_sh_in.shape[0], d), dtype=dt, device=dev)
                      if has_b_sh_out else None)
-        dlogits = torch.empty((n, e), dtype=dt if half else torch.float32, device=dev)
+        fuse = plan.fuse_router
+        dlogits = None if fuse else torch.empty((n, e), dtype=dt if half else torch.float32,
+                                                device=dev)
+        dW_r = torch.empty_like(W_r) if fuse else None
         if n:
             ga = None
             if (flags & nat.ROUTE_PROBS) and g_aux is not None:
@@ -664,19 +674,20 @@ class _BlockFunction(torch.autograd.Function):
             a = plan.bind(x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, None)
             nat.check(nat.lib().nsmoe_block_bwd(
                 a, logits.data_ptr(), flags, aux_coef, saved.data_ptr(), g_out.data_ptr(),
-                _p(ga), gr, dlogits.data_ptr(), ws.data_ptr(), plan.bwd_ws, _stream()),
-                "nsmoe_block_bwd")
+                _p(ga), gr, _p(W_r if fuse else None), _p(dW_r), _p(dlogits), ws.data_ptr(),
+                plan.bwd_ws, _stream()), "nsmoe_block_bwd")
         else:
             for t in (dw_in, dw_out, dw_sh_in, dw_sh_out, db_in, db_out, db_sh_in, db_sh_out,
-                      dlogits):
+                      dlogits, dW_r):
                 if t is not None:
                     t.zero_()
-        dl = dlogits if half else dlogits.to(dt)
-        dW_r = x.t().mm(dl) if need[1] else None
-        if need[0]:
-            dx.addmm_(dl, W_r.t())
-        return (dx if need[0] else None, dW_r, dw_in, dw_out, dw_sh_in, dw_sh_out, db_in, db_out,
-                db_sh_in, db_sh_out, None, None, None, None, None)
+        if not fuse:
+            dl = dlogits if half else dlogits.to(dt)
+            dW_r = x.t().mm(dl) if need[1] else None
+            if need[0]:
+                dx.addmm_(dl, W_r.t())
+        return (dx if need[0] else None, dW_r if need[1] else None, dw_in, dw_out, dw_sh_in,
+                dw_sh_out, db_in, db_out, db_sh_in, db_sh_out, None, None, None, None, None)
 
 
 def block_forward(x, router_W, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out,
@@ -690,6 +701,6 @@ def block_forward(x, router_W, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh
     _check_activation(activation)
     cast = lambda t: None if t is None else t.to(x.dtype)
     return _BlockFunction.apply(
-        x.contiguous(), cast(router_W), cast(w_in), cast(w_out), cast(w_sh_in), cast(w_sh_out),
+        x.contiguous(), cast(router_W).contiguous(), cast(w_in), cast(w_out), cast(w_sh_in), cast(w_sh_out),
         cast(b_in), cast(b_out), cast(b_sh_in), cast(b_sh_out), top_k, want_probs, normalize,
         activation, aux_coef)

@@ -43,7 +43,7 @@ def test_struct_layouts_match_the_header():
 
 
 def test_abi_version_and_alignment():
-    assert nat.lib().nsmoe_abi_version() == nat.ABI_VERSION == 2
+    assert nat.lib().nsmoe_abi_version() == nat.ABI_VERSION == 3
     assert nat.lib().nsmoe_align_m() == mk.ALIGN_M
 
 
