@@ -62,6 +62,10 @@ dispatch_scan_kernel(int32_t* __restrict__ hist, int64_t n_chunks, int E, int64_
   // Per-expert exclusive sums down the chunk column.  Thread (e, seg) owns chunks
   // [seg * L, (seg + 1) * L) of expert e's column: it sums them (independent loads),
   // the segment totals are scanned in LDS, then it rewrites its chunks as bases.
+  // Segments of up to SEG_REG chunks are held in registers between the two passes, so
+  // the rewrite issues no load after a store (the loads would wait for each store:
+  // hist is read and written through the same pointer).
+  constexpr int SEG_REG = 16;
   __shared__ int32_t s_seg[1024];
   const int nseg = E <= (int)blockDim.x ? (int)blockDim.x / E : 1;
   const int64_t L = (n_chunks + nseg - 1) / nseg;
@@ -69,18 +73,37 @@ dispatch_scan_kernel(int32_t* __restrict__ hist, int64_t n_chunks, int E, int64_
     const int e = base_e + tid / nseg, seg = tid % nseg;
     const bool own = tid / nseg < (int)blockDim.x / nseg && e < E;
     const int64_t c0 = seg * L, c1 = c0 + L < n_chunks ? c0 + L : n_chunks;
+    const bool in_reg = L <= SEG_REG;
+    int32_t buf[SEG_REG];
     int32_t sum = 0;
-    if (own)
-      for (int64_t c = c0; c < c1; ++c) sum += hist[c * E + e];
+    if (own) {
+      if (in_reg) {
+#pragma unroll
+        for (int i = 0; i < SEG_REG; ++i) buf[i] = c0 + i < c1 ? hist[(c0 + i) * E + e] : 0;
+#pragma unroll
+        for (int i = 0; i < SEG_REG; ++i) sum += buf[i];
+      } else {
+        for (int64_t c = c0; c < c1; ++c) sum += hist[c * E + e];
+      }
+    }
     s_seg[tid] = own ? sum : 0;
     __syncthreads();
     if (own) {
       int32_t run = 0;
       for (int q = 0; q < seg; ++q) run += s_seg[tid - seg + q];
-      for (int64_t c = c0; c < c1; ++c) {
-        const int32_t v = hist[c * E + e];
-        hist[c * E + e] = run;
-        run += v;
+      if (in_reg) {
+#pragma unroll
+        for (int i = 0; i < SEG_REG; ++i)
+          if (c0 + i < c1) {
+            hist[(c0 + i) * E + e] = run;
+            run += buf[i];
+          }
+      } else {
+        for (int64_t c = c0; c < c1; ++c) {
+          const int32_t v = hist[c * E + e];
+          hist[c * E + e] = run;
+          run += v;
+        }
       }
       if (seg == nseg - 1) {
         s_cnt[e] = run;

@@ -742,15 +742,17 @@ __global__ void __launch_bounds__(NT) dw_reduce_kernel(ExpParams p) {
   const int g = blockIdx.y;
   const int nch = dw_chunks(rows_of(p, g));
   if (nch <= 1) return;
+  // First partial of group g: the chunk counts of the multi-chunk groups before it,
+  // counted by all threads at once (integer sum: the order does not matter).
   __shared__ int s_base;
-  if (threadIdx.x == 0) {
-    int base = 0;
-    for (int q = 0; q < g; ++q) {
-      const int c = dw_chunks(rows_of(p, q));
-      if (c > 1) base += c;
-    }
-    s_base = base;
+  if (threadIdx.x == 0) s_base = 0;
+  __syncthreads();
+  int part = 0;
+  for (int q = threadIdx.x; q < g; q += NT) {
+    const int c = dw_chunks(rows_of(p, q));
+    if (c > 1) part += c;
   }
+  if (part) atomicAdd(&s_base, part);
   __syncthreads();
   const int d = p.d, H = p.H;
   const int64_t mn = MODE == 0 ? (int64_t)d * 2 * H : (int64_t)H * d;

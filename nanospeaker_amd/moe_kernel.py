@@ -630,6 +630,9 @@ class _BlockFunction(torch.autograd.Function):
         counts = saved[oc:oc + 4 * e].view(torch.int32)
         topk_idx = saved[oi:oi + 8 * n * top_k].view(torch.int64).view(n, top_k)
         ctx.mark_non_differentiable(counts, topk_idx)
+        # Unused output gradients arrive as None instead of materialised zeros (two fill
+        # kernels per step for counts and topk_idx otherwise).
+        ctx.set_materialize_grads(False)
         ctx.save_for_backward(x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in,
                               logits, saved)
         ctx.cfg = (plan, flags, float(aux_coef), b_sh_out is not None)
