@@ -12,6 +12,8 @@
 // Taken for bf16 / fp16 when d and H are multiples of 8, the operands are 16-byte aligned
 // and H <= 128 (the ring and the h tile fit one workgroup's LDS); other shapes use the
 // register-staged kernels.
+#include <stdlib.h>
+
 #include <type_traits>
 
 #include "experts_common.h"
@@ -233,6 +235,246 @@ __global__ void __launch_bounds__(NT, 2) expert_fwd_async_kernel(ExpParams p) {
       }
     }
   }
+  wait_vmcnt<0>();  // nothing may be in flight when the workgroup retires
+}
+
+// expert_fwd_reg: the same tile and arithmetic as expert_fwd_async_kernel, with the
+// weights -- private to each wave -- loaded from L2 straight into registers two k-steps
+// ahead (two fragment sets in flight), and only the token tile (shared by the 4 waves)
+// copied through the LDS ring.  That halves the LDS traffic of a step and issues one
+// LDS-DMA copy per wave per step instead of 1 + 2 NBW.  GEMM2 reads h from LDS and its
+// weights from registers, so it runs without workgroup barriers.
+//
+// Step s issues, after its MFMAs, the weights of step s + 2 and then the token copy of
+// step s + 2; step s therefore waits (vmcnt) until only what step s - 1 issued is in
+// flight, which also covers the weights of step s (issued just before the copy).  Every
+// load is unconditional (out-of-range fragments read a zero page), so the compiler's own
+// waits for the weight registers count exactly and leave the next step's loads in flight.
+// Shapes: d % 64 == 0 (an even number of GEMM1 steps) and an even number of GEMM2 steps.
+template <int DT, int NBW>
+__global__ void __launch_bounds__(NT, 2) expert_fwd_reg_kernel(ExpParams p) {
+  using G = Geo<DT>;
+  using T = typename G::T;
+  using M = Mma<DT>;
+  using Frag = typename M::Frag;
+  static_assert(G::ES == 2, "16-bit types only");
+  constexpr int S = 3;                   // token-tile ring stages
+  constexpr int HPMAX = 64 * NBW;
+  constexpr int A_BYTES = BM * G::ROWB;  // 64 rows x 32 elements = 4 KiB = one copy per lane
+  constexpr int NB1 = 2 * NBW;           // GEMM1 fragments per wave per step
+  constexpr int NB2 = 3;                 // GEMM2 fragments per wave per step
+  constexpr int NBMAX = NB1 > NB2 ? NB1 : NB2;
+  constexpr int HP_PITCH = HPMAX * G::ES + 16;
+  __shared__ __attribute__((aligned(1024))) char s_ring[S][A_BYTES];
+  __shared__ __attribute__((aligned(16))) char s_h[BM * HP_PITCH];
+  __shared__ int s_tok[BM];
+  __shared__ float s_w[BM];
+  __shared__ int s_loc[3];
+
+  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  Located loc;
+  if (!locate(tile, p.E + p.S, [&](int g) { return (rows_of(p, g) + BM - 1) / BM; },
+              [](int) { return 0; }, s_loc, loc))
+    return;
+  const int g = loc.g, m0 = loc.local * BM;
+  const int rows = min(BM, rows_of(p, g) - m0);
+  const int64_t slot0 = row_start(p, g) + m0;
+  const int tid = threadIdx.x, lane = tid & 63, lc = lane & 15, lg = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  if (tid < BM) {
+    int tok = -1, pair;
+    float w = 0.0f;
+    if (tid < rows) row_info<DT>(p, g, slot0 + tid, m0 + tid, tok, w, pair);
+    s_tok[tid] = tok;
+    s_w[tid] = w;
+  }
+  __syncthreads();
+
+  const int d = p.d, H = p.H, twoH = 2 * p.H;
+  const int ar = tid >> 2, ac = (tid & 3) ^ swz<DT>(ar);
+  const int atok = s_tok[ar];
+  const T* arow = atok >= 0 ? (const T*)p.x + (int64_t)atok * d + ac * G::VE : nullptr;
+  const char* zero = (const char*)g_zero_kib + lane * 16;
+  const char* P1 = p.p_in + (int64_t)g * p.in_nb * p.in_kb * G::PKB + lane * G::FRAGB;
+  const char* P4 = p.p_out + (int64_t)g * p.out_nb * p.out_kb * G::PKB + lane * G::FRAGB;
+  const int nk1 = p.in_kb, nk2 = p.out_kb;
+  const int npass = (d + NP2 - 1) / NP2;
+  const int n2 = npass * nk2;
+
+  // A step's weight fragments, as a value (fragment sets passed by reference end up in
+  // scratch memory).
+  struct WSet {
+    Frag f[NBMAX];
+  };
+  auto load_w1 = [&](int s) __attribute__((always_inline)) -> WSet {  // s < nk1
+    WSet w;
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) {
+      const int jb = wave * NBW + j;
+      w.f[j] = M::load(P1 + ((int64_t)jb * nk1 + s) * G::PKB);
+      w.f[NBW + j] = M::load(P1 + ((int64_t)(HPMAX / 16 + jb) * nk1 + s) * G::PKB);
+    }
+#pragma unroll
+    for (int j = NB1; j < NBMAX; ++j) w.f[j] = M::zero();
+    return w;
+  };
+  auto load_w2 = [&](int q) __attribute__((always_inline)) -> WSet {  // q < n2
+    const int pass = q / nk2, kb = q - pass * nk2;
+    const int nbase = pass * (NP2 / 16) + wave * 3;
+    WSet w;
+#pragma unroll
+    for (int j = 0; j < NB2; ++j) {
+      const int nb = nbase + j;
+      w.f[j] = M::load(nb < p.out_nb ? P4 + ((int64_t)nb * nk2 + kb) * G::PKB : zero);
+    }
+#pragma unroll
+    for (int j = NB2; j < NBMAX; ++j) w.f[j] = M::zero();
+    return w;
+  };
+  auto issue_x = [&](int s) __attribute__((always_inline)) {
+    const int k0 = s * G::KC;
+    const bool av = arow && k0 + ac * G::VE < d;
+    async_copy16(av ? (const void*)(arow + k0) : (const void*)zero, s_ring[s % S] + wave * 1024);
+  };
+
+  // ---- GEMM1 (transposed): acc[i][j] = W_in[:, cols of block j]^T x[rows of block i]^T ----
+  f32x4 accg[4][NBW], accu[4][NBW];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) accg[i][j] = accu[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto g1mma = [&](int s, const WSet& w) __attribute__((always_inline)) {
+    barrier_dma();
+    const char* st = s_ring[s % S];
+    Frag xf[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xf[i] = frag_sw<DT>(st, i * 16);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < NBW; ++j) {
+        M::run(accg[i][j], w.f[j], xf[i]);
+        M::run(accu[i][j], w.f[NBW + j], xf[i]);
+      }
+  };
+
+  WSet wa = load_w1(0);
+  issue_x(0);
+  WSet wb = load_w1(1);
+  issue_x(1);
+  int s = 0;
+  for (; s + 2 < nk1; s += 2) {  // steady state: the steps two ahead are GEMM1 steps
+    wait_vmcnt<NB1 + 1>();
+    g1mma(s, wa);
+    wa = load_w1(s + 2);
+    issue_x(s + 2);
+    wait_vmcnt<NB1 + 1>();
+    g1mma(s + 1, wb);
+    wb = load_w1(s + 3);
+    issue_x(s + 3);
+  }
+  // The last two GEMM1 steps prefetch GEMM2's first two weight sets.
+  wait_vmcnt<NB1 + 1>();
+  g1mma(s, wa);
+  wa = load_w2(0);
+  wait_vmcnt<NB2>();
+  g1mma(s + 1, wb);
+  wb = load_w2(1);
+
+  // ---- GEMM1 epilogue: bias, h = act(gate) * up -> LDS --------------------------------------
+  const T* bin = (g < p.E ? p.b_in : p.b_sh_in)
+                     ? per_group<T>(p.b_in, p.b_sh_in, g, p.E, twoH) : nullptr;
+  with_act(p.act, [&]<int ACT>() {
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) {
+      const int n0 = (wave * NBW + j) * 16 + lg * 4;
+      float bg[4] = {0.f, 0.f, 0.f, 0.f}, bu[4] = {0.f, 0.f, 0.f, 0.f};
+      if (bin) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if (n0 + r < H) {
+            bg[r] = Elem<DT>::to_f(bin[n0 + r]);
+            bu[r] = Elem<DT>::to_f(bin[H + n0 + r]);
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float hv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          hv[r] = n0 + r < H ? act_fwd_t<ACT>(accg[i][j][r] + bg[r]) * (accu[i][j][r] + bu[r])
+                             : 0.0f;
+        const uint32_t lo = pack2<DT>(hv[0], hv[1]), hi = pack2<DT>(hv[2], hv[3]);
+        *(uint2*)(s_h + (i * 16 + lc) * HP_PITCH + n0 * G::ES) = make_uint2(lo, hi);
+      }
+    }
+  });
+  // h published: its ds_write stores complete, then a bare barrier (a fence here would
+  // also wait for the GEMM2 weights in flight).  No barrier after this point.
+  wait_lgkm0();
+  barrier_dma();
+
+  // ---- GEMM2 (transposed): y^T = W_out^T h^T, + b_out, * gate, 8-byte row stores ----
+  const T* bout = (g < p.E ? p.b_out : p.b_sh_out)
+                      ? per_group<T>(p.b_out, p.b_sh_out, g, p.E, d) : nullptr;
+  float wrow[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) wrow[i] = s_w[i * 16 + lc];
+  T* Y = (T*)p.y + slot0 * d;
+  f32x4 acc[4][3];
+  auto g2step = [&](int q, const WSet& w) __attribute__((always_inline)) {
+    const int pass = q / nk2, kb = q - pass * nk2;
+    if (kb == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    Frag hf[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) hf[i] = frag_at<DT>(s_h, HP_PITCH, i * 16, kb * G::ROWB);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 3; ++j) M::run(acc[i][j], w.f[j], hf[i]);
+    if (kb == nk2 - 1) {
+#pragma unroll
+      for (int j = 0; j < 3; ++j) {
+        const int n0 = (pass * (NP2 / 16) + wave * 3 + j) * 16 + lg * 4;
+        if (n0 >= d) continue;
+        float bo[4] = {0.f, 0.f, 0.f, 0.f};
+        if (bout) {
+          const uint2 b = *(const uint2*)(bout + n0);
+          bo[0] = unpack2<DT>(b.x, 0);
+          bo[1] = unpack2<DT>(b.x, 1);
+          bo[2] = unpack2<DT>(b.y, 0);
+          bo[3] = unpack2<DT>(b.y, 1);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = i * 16 + lc;
+          if (m < rows) {
+            const float wt = wrow[i];
+            const uint32_t lo =
+                pack2<DT>((acc[i][j][0] + bo[0]) * wt, (acc[i][j][1] + bo[1]) * wt);
+            const uint32_t hi =
+                pack2<DT>((acc[i][j][2] + bo[2]) * wt, (acc[i][j][3] + bo[3]) * wt);
+            *(uint2*)(Y + (int64_t)m * d + n0) = make_uint2(lo, hi);
+          }
+        }
+      }
+    }
+  };
+  int q = 0;
+  for (; q + 2 < n2; q += 2) {
+    g2step(q, wa);
+    wa = load_w2(q + 2);
+    g2step(q + 1, wb);
+    wb = load_w2(q + 3);
+  }
+  g2step(q, wa);
+  g2step(q + 1, wb);
   wait_vmcnt<0>();  // nothing may be in flight when the workgroup retires
 }
 
@@ -771,6 +1013,19 @@ int launch_fwd_async(int dtype, const ExpParams& p, int nbw, int64_t grid, hipSt
   if (grid <= 0) return NSMOE_OK;
   constexpr int S = 3;
   KernelTimer timer("expert_fwd", s);
+  static const bool reg = getenv("NSMOE_FWD_LDSW") == nullptr;
+  const int n2 = ((p.d + NP2 - 1) / NP2) * p.out_kb;
+  if (reg && p.d % 64 == 0 && n2 % 2 == 0) {
+    if (dtype == DT_BF16) {
+      if (nbw == 1) expert_fwd_reg_kernel<DT_BF16, 1><<<(unsigned)grid, NT, 0, s>>>(p);
+      else expert_fwd_reg_kernel<DT_BF16, 2><<<(unsigned)grid, NT, 0, s>>>(p);
+    } else {
+      if (nbw == 1) expert_fwd_reg_kernel<DT_F16, 1><<<(unsigned)grid, NT, 0, s>>>(p);
+      else expert_fwd_reg_kernel<DT_F16, 2><<<(unsigned)grid, NT, 0, s>>>(p);
+    }
+    timer.stop();
+    return check_launch("expert_fwd_reg_kernel");
+  }
   if (dtype == DT_BF16) {
     if (nbw == 1) expert_fwd_async_kernel<DT_BF16, 1, S><<<(unsigned)grid, NT, 0, s>>>(p);
     else expert_fwd_async_kernel<DT_BF16, 2, S><<<(unsigned)grid, NT, 0, s>>>(p);

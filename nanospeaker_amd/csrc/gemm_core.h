@@ -222,6 +222,14 @@ __device__ __forceinline__ uint2 lds_read_tr16(const char* p) {
   return u;
 }
 
+// Workgroup barrier for data that reached LDS by LDS-DMA copies the caller has already
+// waited for (vmcnt) and that no wave writes with ds_* stores in between: a bare
+// s_barrier plus a compiler barrier.  Unlike barrier_lds, no fence is involved, so loads
+// into registers that are still in flight (prefetched operands) are not waited for.
+__device__ __forceinline__ void barrier_dma() {
+  asm volatile("s_barrier" ::: "memory");
+}
+
 // Workgroup barrier that orders LDS accesses only: outstanding vector-memory loads (the
 // asynchronous copies of later steps) stay in flight across it.
 __device__ __forceinline__ void barrier_lds() {
@@ -237,6 +245,9 @@ __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
+
+// s_waitcnt lgkmcnt(0) alone (vmcnt 63, expcnt 7 = no wait on those counters).
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
 // vmcnt(n) for a wave-uniform run-time n; n above 31 waits down to 31 outstanding, which
 // is stricter than needed and therefore safe.

@@ -755,8 +755,7 @@ balance_partial_kernel(const float* __restrict__ probs, int64_t T, int E,
 }
 
 // 1024 threads: thread (q, e) with q = tid / 128 sums partial blocks q, q + 8, q + 16, ...
-// of expert e (8 running sums, one per stride-64 phase, combined pairwise); the 8 slices
-// are then added in q order.
+// of expert e in that order; the 8 slices are then added in q order.
 __global__ void __launch_bounds__(1024)
 balance_final_kernel(const float* __restrict__ partial, int64_t nblk, const int32_t* counts,
                      int64_t T, int E, float coef, float* __restrict__ aux) {
@@ -764,13 +763,21 @@ balance_final_kernel(const float* __restrict__ partial, int64_t nblk, const int3
   __shared__ float s_part[2][2];
   const int tid = threadIdx.x, e = tid & 127, q = tid >> 7;
   if (e < E) {
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int64_t b = q; b < nblk; b += 64) {
+    // Slice q holds partials q, q + 8, q + 16, ... of expert e; they are fetched 32 at a
+    // time (all loads in flight together) and added in that order.
+    constexpr int DEPTH = 32;
+    float acc = 0.0f;
+    for (int64_t b0 = q; b0 < nblk; b0 += 8 * DEPTH) {
+      float v[DEPTH];
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (b + 8 * u < nblk) acc[u] += partial[(b + 8 * u) * E + e];
+      for (int u = 0; u < DEPTH; ++u) {
+        const int64_t b = b0 + 8 * u;
+        v[u] = b < nblk ? partial[b * E + e] : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < DEPTH; ++u) acc += v[u];
     }
-    s_q[q][e] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+    s_q[q][e] = acc;
   }
   __syncthreads();
   if (tid < 128) {
