@@ -243,7 +243,10 @@ __global__ void __launch_bounds__(NT, 2) expert_fwd_async_kernel(ExpParams p) {
 // ahead (two fragment sets in flight), and only the token tile (shared by the 4 waves)
 // copied through the LDS ring.  That halves the LDS traffic of a step and issues one
 // LDS-DMA copy per wave per step instead of 1 + 2 NBW.  GEMM2 reads h from LDS and its
-// weights from registers, so it runs without workgroup barriers.
+// weights from registers; its only barriers are those of the output staging: each
+// 192-column pass of y is assembled in LDS (over the token ring, idle by then) and leaves
+// as whole 384-byte row segments in 16-byte stores -- 8-byte stores straight from the
+// accumulators would write 16 separate 32-byte segments per instruction.
 //
 // Step s issues, after its MFMAs, the weights of step s + 2 and then the token copy of
 // step s + 2; step s therefore waits (vmcnt) until only what step s - 1 issued is in
@@ -265,7 +268,11 @@ __global__ void __launch_bounds__(NT, 2) expert_fwd_reg_kernel(ExpParams p) {
   constexpr int NB2 = 3;                 // GEMM2 fragments per wave per step
   constexpr int NBMAX = NB1 > NB2 ? NB1 : NB2;
   constexpr int HP_PITCH = HPMAX * G::ES + 16;
-  __shared__ __attribute__((aligned(1024))) char s_ring[S][A_BYTES];
+  constexpr int Y_PITCH = NP2 * G::ES + 16;  // staged y rows: one pass's 192 columns
+  constexpr int RING_BYTES = S * A_BYTES > BM * Y_PITCH ? S * A_BYTES : BM * Y_PITCH;
+  __shared__ __attribute__((aligned(1024))) char s_ring_raw[RING_BYTES];
+  char (*s_ring)[A_BYTES] = (char (*)[A_BYTES])s_ring_raw;
+  char* s_y = s_ring_raw;  // GEMM2 output staging, after GEMM1 is done with the ring
   __shared__ __attribute__((aligned(16))) char s_h[BM * HP_PITCH];
   __shared__ int s_tok[BM];
   __shared__ float s_w[BM];
@@ -439,9 +446,14 @@ __global__ void __launch_bounds__(NT, 2) expert_fwd_reg_kernel(ExpParams p) {
 #pragma unroll
       for (int j = 0; j < 3; ++j) M::run(acc[i][j], w.f[j], hf[i]);
     if (kb == nk2 - 1) {
+      // + b_out, * gate, packed into the staging tile (the previous pass's reads are done
+      // once every wave has passed this barrier).
+      wait_lgkm0();
+      barrier_dma();
 #pragma unroll
       for (int j = 0; j < 3; ++j) {
-        const int n0 = (pass * (NP2 / 16) + wave * 3 + j) * 16 + lg * 4;
+        const int c0 = (wave * 3 + j) * 16 + lg * 4;  // column inside the pass
+        const int n0 = pass * NP2 + c0;
         if (n0 >= d) continue;
         float bo[4] = {0.f, 0.f, 0.f, 0.f};
         if (bout) {
@@ -454,14 +466,23 @@ __global__ void __launch_bounds__(NT, 2) expert_fwd_reg_kernel(ExpParams p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int m = i * 16 + lc;
-          if (m < rows) {
-            const float wt = wrow[i];
-            const uint32_t lo =
-                pack2<DT>((acc[i][j][0] + bo[0]) * wt, (acc[i][j][1] + bo[1]) * wt);
-            const uint32_t hi =
-                pack2<DT>((acc[i][j][2] + bo[2]) * wt, (acc[i][j][3] + bo[3]) * wt);
-            *(uint2*)(Y + (int64_t)m * d + n0) = make_uint2(lo, hi);
-          }
+          const float wt = wrow[i];
+          const uint32_t lo = pack2<DT>((acc[i][j][0] + bo[0]) * wt, (acc[i][j][1] + bo[1]) * wt);
+          const uint32_t hi = pack2<DT>((acc[i][j][2] + bo[2]) * wt, (acc[i][j][3] + bo[3]) * wt);
+          *(uint2*)(s_y + m * Y_PITCH + c0 * G::ES) = make_uint2(lo, hi);
+        }
+      }
+      wait_lgkm0();
+      barrier_dma();
+      // 64 rows x 24 chunks of 16 bytes; a wave's store covers 2.67 whole 384-byte rows.
+      const int ncols = min(NP2, d - pass * NP2);
+      constexpr int CPR = NP2 / G::VE;  // chunks per staged row
+#pragma unroll
+      for (int u = 0; u < BM * CPR / NT; ++u) {
+        const int c = tid + u * NT, m = c / CPR, cc = c % CPR;
+        if (m < rows && cc * G::VE < ncols) {
+          const u32x4 v = *(const u32x4*)(s_y + m * Y_PITCH + cc * 16);
+          *(u32x4*)(Y + (int64_t)m * d + pass * NP2 + cc * G::VE) = v;
         }
       }
     }
