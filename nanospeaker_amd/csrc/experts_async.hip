@@ -800,9 +800,386 @@ __global__ void __launch_bounds__(NT, 2) expert_dx_async_kernel(ExpParams p) {
   wait_vmcnt<0>();
 }
 
+// expert_bwd_reg / expert_dx_reg: expert_bwd_async / expert_dx_async with the schedule of
+// expert_fwd_reg -- each wave's private weight fragments loaded from L2 into registers two
+// k-steps ahead, only the shared token tiles (x and dout; dA1 rows) copied through the
+// LDS ring, and every row output assembled in LDS and written as whole row segments with
+// 16-byte stores.  Step s waits until only what slot s - 1 issued is in flight; all loads
+// of a steady step are unconditional (zero page for fragments past the edge).
+// Shapes: an even number of k-steps.
+
+template <int DT, int NBW>
+__global__ void __launch_bounds__(NT, 2) expert_bwd_reg_kernel(ExpParams p) {
+  using G = Geo<DT>;
+  using T = typename G::T;
+  using M = Mma<DT>;
+  using Frag = typename M::Frag;
+  static_assert(G::ES == 2, "16-bit types only");
+  constexpr int S = 3;
+  constexpr int HPMAX = 64 * NBW;
+  constexpr int A_BYTES = BM * G::ROWB;  // one token tile (x or dout): 4 KiB
+  constexpr int NBF = 3 * NBW;           // gate, up and G fragments per wave per step
+  constexpr int SLOT = NBF + 2;          // VM operations a steady slot issues
+  constexpr int DA_PITCH = 2 * HPMAX * G::ES + 16;  // staged dA1 rows
+  constexpr int HB_PITCH = HPMAX * G::ES + 16;      // staged w h rows
+  constexpr int RING = S * 2 * A_BYTES;
+  constexpr int STAGE_BYTES = BM * (DA_PITCH + HB_PITCH);
+  constexpr int LDS_BYTES = RING > STAGE_BYTES ? RING : STAGE_BYTES;
+  __shared__ __attribute__((aligned(1024))) char s_lds[LDS_BYTES];
+  __shared__ int s_tok[BM];
+  __shared__ int s_pair[BM];
+  __shared__ float s_w[BM];
+  __shared__ float s_dtw[5][BM];
+  __shared__ int s_loc[3];
+  char* s_da = s_lds;                   // epilogue staging, over the ring
+  char* s_hb = s_lds + BM * DA_PITCH;
+  auto ring = [&](int s) __attribute__((always_inline)) { return s_lds + (s % S) * 2 * A_BYTES; };
+
+  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  Located loc;
+  if (!locate(tile, p.E + p.S, [&](int g) { return (rows_of(p, g) + BM - 1) / BM; },
+              [](int) { return 0; }, s_loc, loc))
+    return;
+  const int g = loc.g, m0 = loc.local * BM;
+  const int rows = min(BM, rows_of(p, g) - m0);
+  const int64_t slot0 = row_start(p, g) + m0;
+  const int tid = threadIdx.x, lane = tid & 63, lc = lane & 15, lg = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int d = p.d, H = p.H, twoH = 2 * p.H;
+  const char* zero = (const char*)g_zero_kib + lane * 16;
+  const char* P1 = p.p_in + (int64_t)g * p.in_nb * p.in_kb * G::PKB + lane * G::FRAGB;
+  // W_out fragment rows: lane l reads row (jb * 16 + l % 16), k elements 8 * (l / 16) ..
+  const T* Wout = per_group<T>(p.w_out, p.w_sh_out, g, p.E, (int64_t)H * d);
+  const int wk = (lane >> 4) * 8;
+  const int nk = p.in_kb;
+
+  struct WSet {
+    Frag f[NBF];
+  };
+  auto load_w = [&](int s) __attribute__((always_inline)) -> WSet {
+    const int k0 = s * G::KC;
+    WSet w;
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) {
+      const int jb = wave * NBW + j;
+      w.f[j] = M::load(P1 + ((int64_t)jb * nk + s) * G::PKB);
+      w.f[NBW + j] = M::load(P1 + ((int64_t)(HPMAX / 16 + jb) * nk + s) * G::PKB);
+      const int n = jb * 16 + lc;
+      w.f[2 * NBW + j] = M::load(n < H ? (const char*)(Wout + (int64_t)n * d + k0 + wk) : zero);
+    }
+    return w;
+  };
+  WSet wa = load_w(0), wb = load_w(1);
+
+  if (tid < BM) {
+    int tok = -1, pair = -1;
+    float w = 0.0f;
+    if (tid < rows) row_info<DT>(p, g, slot0 + tid, m0 + tid, tok, w, pair);
+    s_tok[tid] = tok;
+    s_pair[tid] = pair;
+    s_w[tid] = w;
+    s_dtw[4][tid] = 0.0f;
+  }
+  __syncthreads();
+
+  const int ar = tid >> 2, ac = (tid & 3) ^ swz<DT>(ar);
+  const int atok = s_tok[ar];
+  const T* xrow = atok >= 0 ? (const T*)p.x + (int64_t)atok * d + ac * G::VE : nullptr;
+  const T* drow = atok >= 0 ? (const T*)p.dout + (int64_t)atok * d + ac * G::VE : nullptr;
+  auto issue_x = [&](int s) __attribute__((always_inline)) {
+    char* st = ring(s);
+    const int k0 = s * G::KC;
+    async_copy16(xrow ? (const void*)(xrow + k0) : (const void*)zero, st + wave * 1024);
+    async_copy16(drow ? (const void*)(drow + k0) : (const void*)zero, st + A_BYTES + wave * 1024);
+  };
+  issue_x(0);
+  issue_x(1);
+
+  f32x4 accg[4][NBW], accu[4][NBW], accG[4][NBW];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < NBW; ++j)
+      accg[i][j] = accu[i][j] = accG[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto mma = [&](int s, const WSet& w) __attribute__((always_inline)) {
+    barrier_dma();
+    const char* st = ring(s);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const Frag xf = frag_sw<DT>(st, i * 16);
+      const Frag df = frag_sw<DT>(st + A_BYTES, i * 16);
+#pragma unroll
+      for (int j = 0; j < NBW; ++j) {
+        M::run(accg[i][j], w.f[j], xf);
+        M::run(accu[i][j], w.f[NBW + j], xf);
+        M::run(accG[i][j], w.f[2 * NBW + j], df);
+      }
+    }
+  };
+  wait_vmcnt<2>();  // prologue order: w(0) w(1) [row lookups] x(0) d(0) x(1) d(1)
+  mma(0, wa);
+  wa = load_w(2);
+  issue_x(2);
+  wait_vmcnt<SLOT>();
+  mma(1, wb);
+  wb = load_w(3);
+  issue_x(3);
+  int s = 2;
+  for (; s + 2 < nk; s += 2) {
+    wait_vmcnt<SLOT>();
+    mma(s, wa);
+    wa = load_w(s + 2);
+    issue_x(s + 2);
+    wait_vmcnt<SLOT>();
+    mma(s + 1, wb);
+    wb = load_w(s + 3);
+    issue_x(s + 3);
+  }
+  wait_vmcnt<SLOT>();
+  mma(s, wa);
+  wait_vmcnt<0>();
+  mma(s + 1, wb);
+  wait_lgkm0();
+  barrier_dma();  // every wave is done with the ring: the staging may overwrite it
+
+  // ---- GLU backward, lane-local: lane (lc, lg) of block (i, j) holds row i*16 + lc,
+  // hidden columns n0 .. n0 + 3 ----
+  const T* bin = (g < p.E ? p.b_in : p.b_sh_in)
+                     ? per_group<T>(p.b_in, p.b_sh_in, g, p.E, twoH) : nullptr;
+  float wrow[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) wrow[i] = s_w[i * 16 + lc];
+  float part[4] = {0.f, 0.f, 0.f, 0.f};
+  with_act(p.act, [&]<int ACT>() {
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) {
+      const int n0 = (wave * NBW + j) * 16 + lg * 4;
+      if (n0 >= H) continue;  // H % 4 == 0: a group of 4 columns is all in or all out
+      float bg[4] = {0.f, 0.f, 0.f, 0.f}, bu[4] = {0.f, 0.f, 0.f, 0.f};
+      if (bin) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          bg[r] = Elem<DT>::to_f(bin[n0 + r]);
+          bu[r] = Elem<DT>::to_f(bin[H + n0 + r]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = i * 16 + lc;
+        const float w = wrow[i];
+        float dg[4], du[4], wh[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float gg = accg[i][j][r] + bg[r], uu = accu[i][j][r] + bu[r];
+          const float Gv = accG[i][j][r];
+          float a, da;
+          act_both_t<ACT>(gg, a, da);
+          const float hv = a * uu;
+          part[i] += Gv * hv;
+          const float dh = w * Gv;
+          dg[r] = dh * uu * da;
+          du[r] = dh * a;
+          wh[r] = w * hv;
+        }
+        char* da_row = s_da + m * DA_PITCH;
+        *(uint2*)(da_row + n0 * G::ES) =
+            make_uint2(pack2<DT>(dg[0], dg[1]), pack2<DT>(dg[2], dg[3]));
+        *(uint2*)(da_row + (H + n0) * G::ES) =
+            make_uint2(pack2<DT>(du[0], du[1]), pack2<DT>(du[2], du[3]));
+        *(uint2*)(s_hb + m * HB_PITCH + n0 * G::ES) =
+            make_uint2(pack2<DT>(wh[0], wh[1]), pack2<DT>(wh[2], wh[3]));
+      }
+    }
+  });
+  // dtopk_w: sum of G h over the row's hidden columns (4 lanes per wave, then 4 waves).
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float v = part[i];
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    if (lg == 0) s_dtw[wave][i * 16 + lc] = v;
+  }
+  // <dout[tok], b_out[g]>: four lanes per row, strided over d.
+  if (g < p.E && p.b_out) {
+    const T* bo = (const T*)p.b_out + (int64_t)g * d;
+    const int m = tid >> 2, q = tid & 3;
+    float v = 0.0f;
+    if (m < rows) {
+      const T* dr = (const T*)p.dout + (int64_t)s_tok[m] * d;
+      for (int c = q; c < d; c += 4) v += Elem<DT>::to_f(dr[c]) * Elem<DT>::to_f(bo[c]);
+    }
+    v += __shfl_xor(v, 1, 64);
+    v += __shfl_xor(v, 2, 64);
+    if (q == 0 && m < rows) s_dtw[4][m] = v;
+  }
+  __syncthreads();
+  // Whole rows out: dA1 rows of 2H elements, w h rows of H elements, 16-byte chunks.
+  T* DA = (T*)p.da1 + slot0 * twoH;
+  T* HB = (T*)p.hbuf + slot0 * H;
+  const int da_cpr = twoH / G::VE, hb_cpr = H / G::VE;
+  for (int c = tid; c < BM * da_cpr; c += NT) {
+    const int m = c / da_cpr, cc = c - m * da_cpr;
+    if (m < rows) {
+      const int col = cc * G::VE;  // the staged row has the final layout: [gate H | up H]
+      *(u32x4*)(DA + (int64_t)m * twoH + col) = *(const u32x4*)(s_da + m * DA_PITCH + col * G::ES);
+    }
+  }
+  for (int c = tid; c < BM * hb_cpr; c += NT) {
+    const int m = c / hb_cpr, cc = c - m * hb_cpr;
+    if (m < rows)
+      *(u32x4*)(HB + (int64_t)m * H + cc * G::VE) = *(const u32x4*)(s_hb + m * HB_PITCH + cc * 16);
+  }
+  if (g < p.E && tid < rows) {
+    const float v = s_dtw[0][tid] + s_dtw[1][tid] + s_dtw[2][tid] + s_dtw[3][tid] + s_dtw[4][tid];
+    ((T*)p.dtw)[s_pair[tid]] = Elem<DT>::from_f(v);
+  }
+}
+
+template <int DT>
+__global__ void __launch_bounds__(NT, 2) expert_dx_reg_kernel(ExpParams p) {
+  using G = Geo<DT>;
+  using T = typename G::T;
+  using M = Mma<DT>;
+  using Frag = typename M::Frag;
+  static_assert(G::ES == 2, "16-bit types only");
+  constexpr int S = 3;
+  constexpr int A_BYTES = BM * G::ROWB;
+  constexpr int NBF = 3;
+  constexpr int SLOT = NBF + 1;
+  constexpr int Y_PITCH = NP2 * G::ES + 16;
+  __shared__ __attribute__((aligned(1024))) char s_ring[S][A_BYTES];
+  __shared__ __attribute__((aligned(16))) char s_y[BM * Y_PITCH];
+  __shared__ int s_loc[3];
+
+  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  Located loc;
+  if (!locate(tile, p.E + p.S, [&](int g) { return (rows_of(p, g) + BM - 1) / BM; },
+              [](int) { return 0; }, s_loc, loc))
+    return;
+  const int g = loc.g, m0 = loc.local * BM;
+  const int rows = min(BM, rows_of(p, g) - m0);
+  const int64_t slot0 = row_start(p, g) + m0;
+  const int tid = threadIdx.x, lane = tid & 63, lc = lane & 15, lg = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int d = p.d, twoH = 2 * p.H;
+  const char* zero = (const char*)g_zero_kib + lane * 16;
+  const T* Win = per_group<T>(p.w_in, p.w_sh_in, g, p.E, (int64_t)d * twoH);
+  const int wk = (lane >> 4) * 8;
+  const int nkk = twoH / G::KC;
+  const int npass = (d + NP2 - 1) / NP2;
+  const int nsteps = npass * nkk;
+
+  struct WSet {
+    Frag f[NBF];
+  };
+  auto load_w = [&](int s) __attribute__((always_inline)) -> WSet {
+    const int pass = s / nkk, k0 = (s - pass * nkk) * G::KC;
+    WSet w;
+#pragma unroll
+    for (int j = 0; j < NBF; ++j) {
+      const int c = (pass * (NP2 / 16) + wave * 3 + j) * 16 + lc;
+      w.f[j] = M::load(c < d ? (const char*)(Win + (int64_t)c * twoH + k0 + wk) : zero);
+    }
+    return w;
+  };
+  const int ar = tid >> 2, ac = (tid & 3) ^ swz<DT>(ar);
+  const T* arow = ar < rows ? (const T*)p.da1 + (slot0 + ar) * twoH + ac * G::VE : nullptr;
+  auto issue_x = [&](int s) __attribute__((always_inline)) {
+    const int k0 = (s % nkk) * G::KC;
+    async_copy16(arow ? (const void*)(arow + k0) : (const void*)zero, s_ring[s % S] + wave * 1024);
+  };
+  WSet wa = load_w(0);
+  issue_x(0);
+  WSet wb = load_w(1);
+  issue_x(1);
+
+  T* DX = (T*)p.dxrow + slot0 * d;
+  f32x4 acc[4][3];
+  auto step = [&](int s, const WSet& w) __attribute__((always_inline)) {
+    const int pass = s / nkk, kk = s - pass * nkk;
+    if (kk == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    barrier_dma();
+    const char* st = s_ring[s % S];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const Frag af = frag_sw<DT>(st, i * 16);
+#pragma unroll
+      for (int j = 0; j < 3; ++j) M::run(acc[i][j], w.f[j], af);
+    }
+    if (kk == nkk - 1) {  // the pass's 192 columns: staged, then whole row segments out
+#pragma unroll
+      for (int j = 0; j < 3; ++j) {
+        const int c0 = (wave * 3 + j) * 16 + lg * 4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = i * 16 + lc;
+          *(uint2*)(s_y + m * Y_PITCH + c0 * G::ES) =
+              make_uint2(pack2<DT>(acc[i][j][0], acc[i][j][1]),
+                         pack2<DT>(acc[i][j][2], acc[i][j][3]));
+        }
+      }
+      wait_lgkm0();
+      barrier_dma();
+      const int ncols = min(NP2, d - pass * NP2);
+      constexpr int CPR = NP2 / G::VE;
+#pragma unroll
+      for (int u = 0; u < BM * CPR / NT; ++u) {
+        const int c = tid + u * NT, m = c / CPR, cc = c % CPR;
+        if (m < rows && cc * G::VE < ncols)
+          *(u32x4*)(DX + (int64_t)m * d + pass * NP2 + cc * G::VE) =
+              *(const u32x4*)(s_y + m * Y_PITCH + cc * 16);
+      }
+      wait_lgkm0();
+      barrier_dma();  // the staging is read out before the next pass writes it
+    }
+  };
+  int s = 0;
+  for (; s + 2 < nsteps; s += 2) {
+    wait_vmcnt<SLOT>();
+    step(s, wa);
+    wa = load_w(s + 2);
+    issue_x(s + 2);
+    wait_vmcnt<SLOT>();
+    step(s + 1, wb);
+    wb = load_w(s + 3);
+    issue_x(s + 3);
+  }
+  wait_vmcnt<SLOT>();
+  step(s, wa);
+  wait_vmcnt<0>();
+  step(s + 1, wb);
+  wait_vmcnt<0>();
+}
+
 int launch_bwd_async(int dtype, const ExpParams& p, int nbw, int64_t grid, hipStream_t s) {
   if (!p.fast || nbw > 2 || (dtype != DT_BF16 && dtype != DT_F16)) return -1;
   if (grid <= 0) return NSMOE_OK;
+  static const bool reg = getenv("NSMOE_BWD_LDSW") == nullptr;
+  const int nsteps_dx = ((p.d + NP2 - 1) / NP2) * (2 * p.H / 32);
+  if (reg && p.d % 64 == 0 && (2 * p.H) % 32 == 0 && nsteps_dx % 2 == 0 && p.in_kb >= 4) {
+    {
+      KernelTimer timer("expert_bwd", s);
+      if (dtype == DT_BF16) {
+        if (nbw == 1) expert_bwd_reg_kernel<DT_BF16, 1><<<(unsigned)grid, NT, 0, s>>>(p);
+        else expert_bwd_reg_kernel<DT_BF16, 2><<<(unsigned)grid, NT, 0, s>>>(p);
+      } else {
+        if (nbw == 1) expert_bwd_reg_kernel<DT_F16, 1><<<(unsigned)grid, NT, 0, s>>>(p);
+        else expert_bwd_reg_kernel<DT_F16, 2><<<(unsigned)grid, NT, 0, s>>>(p);
+      }
+      timer.stop();
+      NSMOE_TRY(check_launch("expert_bwd_reg_kernel"));
+    }
+    KernelTimer timer("expert_dx", s);
+    if (dtype == DT_BF16) expert_dx_reg_kernel<DT_BF16><<<(unsigned)grid, NT, 0, s>>>(p);
+    else expert_dx_reg_kernel<DT_F16><<<(unsigned)grid, NT, 0, s>>>(p);
+    timer.stop();
+    return check_launch("expert_dx_reg_kernel");
+  }
   {
     constexpr int S = 2;
     KernelTimer timer("expert_bwd", s);

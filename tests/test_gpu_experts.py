@@ -79,6 +79,8 @@ def check(name, got, ref, dtype):
 SHAPES = {  # d, E, d_ff (H = 2 * d_ff // 3)
     "tiny_h42": (32, 8, 64),
     "mid_h64": (64, 8, 96),
+    "wide_h64": (256, 8, 96),    # one 64-column hidden block per wave; last pass 64 wide
+    "wide_h96": (256, 8, 144),   # hidden blocks past H inside the 128-wide tile
     "ns_h128": (576, 76, 192),
 }
 
