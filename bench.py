@@ -7,8 +7,10 @@ router GEMM, the HIP route / dispatch / grouped-expert / combine kernels, and th
 backward producing dX, dW for all 78 experts and the router gradient.  Inputs and
 weights are resident in HBM before the timed region.
 
-Prints ONE JSON line.  `value` is forward+backward tokens/s; the forward-only rate
-(train mode, no_grad) is reported beside it.  `roofline` covers the step's dominant
+Prints ONE JSON line.  `value` is forward+backward tokens/s with the step captured once in
+a HIP graph and replayed (every kernel of the step runs on every replay; `--eager`
+reports the eagerly issued step instead, which is always reported beside it as
+`eager_tokens_per_s`); the forward-only rate (train mode, no_grad) is reported too.  `roofline` covers the step's dominant
 kernel, timed live with HIP events recorded by the library on the stream it launches
 on.  `cpu_baseline` times the CPU restatement of the reference's eager bf16 path
 (oracle/moe_ref.py, pinned bit-exact to the reference by tests/golden) on this host's
@@ -42,6 +44,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--tokens", type=int, default=8192)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--eager", action="store_true",
+                    help="report the eagerly issued step as `value` (default: HIP-graph replay)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run one plain 256 MiB copy kernel, the HBM-counter yardstick")
@@ -225,6 +229,55 @@ def committed_traffic(kernel):
     return None
 
 
+def time_gpu_graph(m, x, g, steps: int, warmup: int):
+    """The same fwd+bwd step (and the forward alone), captured once in a HIP graph and
+    replayed: every replay runs every kernel of the step on the resident inputs; only the
+    host-side enqueue (Python, autograd, the library's argument setup) is removed.
+    torch's capture recipe: warm-up on a side stream, then capture; parameter gradients
+    are cleared inside the captured step (each replay writes them afresh), the input's
+    gradient buffer is zeroed in the graph."""
+    params = [p for p in m.parameters()]
+    xg = x.detach().requires_grad_(True)
+
+    def step():
+        for p in params:
+            p.grad = None
+        if xg.grad is not None:
+            xg.grad.zero_()
+        out = m(xg)
+        torch.autograd.backward([out, m.aux_loss], [g, torch.ones_like(m.aux_loss)])
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(max(warmup, 2)):
+            step()
+        with torch.no_grad():
+            for _ in range(2):
+                m(x)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    fwd_graph = torch.cuda.CUDAGraph()
+    with torch.no_grad():
+        with torch.cuda.graph(fwd_graph):
+            m(x)
+
+    def timed(gr):
+        for _ in range(warmup):
+            gr.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            gr.replay()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / steps
+
+    return timed(graph), timed(fwd_graph)
+
+
 def calibrate_copy():
     """One dispatch of torch's elementwise negation over 256 MiB of bf16: it reads and
     writes exactly COPY_BYTES each, so under `rocprofv3 --pmc FETCH_SIZE` (or WRITE_SIZE)
@@ -286,7 +339,12 @@ def main():
     m, x, g = build_block(T)
     m = m.cuda()
     x, g = x.cuda(), g.cuda()
+    if not a.eager:  # captured before any eager use of the module (torch's recipe)
+        graph_ms, graph_fwd_ms = time_gpu_graph(m, x, g, a.steps, a.warmup)
     ms, fwd_ms, kernels, host_ms = time_gpu(m, x, g, a.steps, a.warmup)
+    eager_ms, eager_fwd_ms = ms, fwd_ms
+    if not a.eager:
+        ms, fwd_ms = graph_ms, graph_fwd_ms
 
     k, S, d, H, E = 6, 2, 576, 128, 76
     dom = max(kernels, key=lambda n: kernels[n][0] * kernels[n][1]) if kernels else None
@@ -319,9 +377,13 @@ def main():
         "data": "synthetic",
         "config": {"workload": f"nanoSpeaker MoE block fwd+bwd, T={T} (training shape)",
                    "n_tokens": T, "d_model": d, "n_experts": E, "n_shared": S, "top_k": k,
-                   "d_hidden": H, "mode": "train, aux_loss 1e-2"},
+                   "d_hidden": H, "mode": "train, aux_loss 1e-2",
+                   "issue": "eager" if a.eager else "hip_graph"},
         "fwd_tokens_per_s": round(T / (fwd_ms / 1e3), 1),
         "fwd_ms": round(fwd_ms, 4),
+        "eager_tokens_per_s": round(T / (eager_ms / 1e3), 1),
+        "eager_ms_per_step": round(eager_ms, 4),
+        "eager_fwd_tokens_per_s": round(T / (eager_fwd_ms / 1e3), 1),
         "host_enqueue_ms_per_step": round(host_ms, 4),
         "kernels_us": {n: round(v[0] * 1e3, 2) for n, v in kernels.items()},
         "roofline": roofline,

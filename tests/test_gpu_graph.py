@@ -1,0 +1,103 @@
+"""
+The block's kernel path inside a captured HIP graph: a training step (forward + autograd
+backward) and a forward are captured once and replayed several times, with eager work and
+host synchronisations between the replays; every replay must equal an eager step bit for
+bit (the kernels are deterministic), which also shows the library records no memsets or
+host synchronisations that a replay would not repeat.
+
+Capture follows torch's recipe: warm-up on a side stream, then capture.  Parameter
+gradients are cleared (set to None) inside the captured step, so each replay writes them
+afresh; the input's gradient buffer exists from the warm-up and is zeroed in the graph.
+"""
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+mk = pytest.importorskip("nanospeaker_amd.moe_kernel")
+from nanospeaker_amd import MoEBlock  # noqa: E402
+
+DEV = "cuda"
+
+
+def _block(T, seed=0):
+    torch.manual_seed(seed)
+    m = MoEBlock(576, 76, d_ff=192, top_k=6, n_shared=2, capacity_factor=None, fused=False)
+    m = m.to(torch.bfloat16).to(DEV).train()
+    x = torch.randn(T, 576, device=DEV).to(torch.bfloat16)
+    g = torch.randn(T, 576, device=DEV).to(torch.bfloat16)
+    return m, x, g
+
+
+@pytest.mark.parametrize("T", [2048, 8192])
+def test_training_step_replays_equal_eager(T):
+    m, x, g = _block(T)
+    params = list(m.parameters())
+    xg = x.detach().requires_grad_(True)
+
+    def step():
+        for p in params:
+            p.grad = None
+        if xg.grad is not None:
+            xg.grad.zero_()
+        out = m(xg)
+        torch.autograd.backward([out, m.aux_loss], [g, torch.ones_like(m.aux_loss)])
+        return out
+
+    print(f"[graph] T={T} warm-up", flush=True)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    print(f"[graph] T={T} capture", flush=True)
+    with torch.cuda.graph(graph):
+        out = step()
+    aux = m.aux_loss  # the captured tensors (eager calls below rebind the attributes)
+    grads = [xg.grad] + [p.grad for p in params]
+    got = []
+    for r in range(3):
+        scratch = torch.randn(T, 576, device=DEV).to(torch.bfloat16)
+        with torch.no_grad():
+            m(scratch)  # eager work between replays, on other buffers
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        print(f"[graph] T={T} replay {r}", flush=True)
+        got.append([out.clone(), aux.detach().clone()] + [t.clone() for t in grads])
+    # the eager step, on fresh gradient buffers
+    xg.grad = None
+    ref_out = step().detach()
+    ref = [ref_out, m.aux_loss.detach()] + [xg.grad] + [p.grad for p in params]
+    for r, vals in enumerate(got):
+        for i, (a, b) in enumerate(zip(vals, ref)):
+            assert torch.equal(a, b), f"replay {r}: tensor {i}"
+
+
+def test_forward_replays_equal_eager():
+    m, x, _ = _block(4096, seed=1)
+    with torch.no_grad():
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                m(x)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out = m(x)
+        got = []
+        for r in range(3):
+            m(torch.randn_like(x))
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            got.append(out.clone())
+        ref = m(x)
+        for r, v in enumerate(got):
+            assert torch.equal(v, ref), f"replay {r}"
