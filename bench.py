@@ -82,6 +82,8 @@ def kernel_units(name: str, T: int, k: int, S: int, d: int, H: int, E: int):
         return rows * (2 * d * 2 * H), "mfma", "TFLOP/s"
     if name == "dw_out":
         return rows * (2 * H * d), "mfma", "TFLOP/s"
+    if name == "dw":                # dW_in and dW_out in one launch
+        return rows * (2 * d * 2 * H + 2 * H * d), "mfma", "TFLOP/s"
     if name == "combine":           # read k + S rows, write one, per token (+ inv)
         return T * ((k + S) * d * 2 + d * 2 + k * 4), "hbm", "GB/s"
     if name == "route_fwd":         # bf16 logits in, fp32 probs out, ids + gates out
@@ -124,7 +126,7 @@ def time_gpu(m, x, g, steps: int, warmup: int):
     ms = (time.perf_counter() - t0) * 1e3 / steps
     kernels = {}
     for name in ("route_fwd", "dispatch", "pack", "expert_fwd", "combine", "expert_bwd",
-                 "expert_dx", "dw_in", "dw_out", "combine_dx", "router_dw"):
+                 "expert_dx", "dw_in", "dw_out", "dw", "combine_dx", "router_dw"):
         tot, n = nat.timing_read(name)
         if n:
             kernels[name] = (tot / n, n // steps)
@@ -148,6 +150,7 @@ KERNEL_SYMBOLS = {
     "expert_fwd": ("nsmoe::expert_fwd_async_kernel", "nsmoe::expert_fwd_kernel"),
     "expert_bwd": ("nsmoe::expert_bwd_async_kernel", "nsmoe::expert_bwd_kernel"),
     "expert_dx": ("nsmoe::expert_dx_async_kernel",),
+    "dw": ("nsmoe::dw_pair_kernel",),
     "dw_in": ("nsmoe::dw_async_kernel<0, 0", "nsmoe::dw_kernel<0, 0"),
     "dw_out": ("nsmoe::dw_async_kernel<0, 1", "nsmoe::dw_kernel<0, 1"),
     "route_fwd": ("nsmoe::route_fwd_kernel",),

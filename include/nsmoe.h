@@ -46,7 +46,8 @@ int32_t nsmoe_abi_version(void);
 /* Measurement hooks (no counterpart in the reference; used by bench.py).  When enabled,
  * the library records a HIP event pair on the launch stream around each launch of its
  * main kernels ("pack", "route_fwd", "dispatch", "expert_fwd", "combine",
- * "expert_bwd", "expert_dx", "dw_in", "dw_out", "combine_dx", "router_dw") until
+ * "expert_bwd", "expert_dx", "dw" (or "dw_in" and "dw_out" where they run apart),
+ * "combine_dx", "router_dw") until
  * `capacity` pairs are used.
  * nsmoe_timing_read waits for the recorded events of one kernel and returns their
  * summed duration.  capacity 0 disables timing and frees the events. */

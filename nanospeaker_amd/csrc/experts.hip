@@ -737,9 +737,8 @@ __global__ void __launch_bounds__(NT) dw_kernel(ExpParams p) {
 constexpr int DWR_BLOCKS = 64;
 
 template <int DT, int MODE>
-__global__ void __launch_bounds__(NT) dw_reduce_kernel(ExpParams p) {
+__device__ __forceinline__ void dw_reduce_group(const ExpParams& p, int g) {
   using T = typename Elem<DT>::T;
-  const int g = blockIdx.y;
   const int nch = dw_chunks(rows_of(p, g));
   if (nch <= 1) return;
   // First partial of group g: the chunk counts of the multi-chunk groups before it,
@@ -782,6 +781,20 @@ __global__ void __launch_bounds__(NT) dw_reduce_kernel(ExpParams p) {
     for (int c = 0; c < nch; ++c) acc += src[(int64_t)c * mn + i];
     dst[i] = Elem<DT>::from_f(acc);
   }
+}
+
+template <int DT, int MODE>
+__global__ void __launch_bounds__(NT) dw_reduce_kernel(ExpParams p) {
+  dw_reduce_group<DT, MODE>(p, blockIdx.y);
+}
+
+// Both modes in one launch: grid.y in [0, G) reduces dW_in groups, [G, 2G) dW_out groups.
+template <int DT>
+__global__ void __launch_bounds__(NT) dw_reduce_pair_kernel(ExpParams p_in, ExpParams p_out,
+                                                            int G) {
+  const int gy = blockIdx.y;
+  if (gy < G) dw_reduce_group<DT, 0>(p_in, gy);
+  else dw_reduce_group<DT, 1>(p_out, gy - G);
 }
 
 // Bias gradients: WHICH 0 -> db_in[g] = sum_r dA1[slot_r]; 1 -> db_out[g] = sum_r w_r dout[tok_r].
@@ -1007,43 +1020,52 @@ static int experts_bwd_impl(const nsmoe_experts_args* a, const int32_t* inv, con
 
   const int d = a->d_model, H = a->d_hidden;
   const int64_t gc = dw_groups_chunks(a);
-  {  // dW_in
-    ExpParams q = p;
-    q.dw_a = gr->dw_in;
-    q.dw_sh = gr->dw_sh_in;
-    q.partial = (float*)(ws + L.p_in);
-    const int rc = launch_dw_async(DT, 0, q, gc, s);
-    if (rc != -1) {
-      NSMOE_TRY(rc);
-    } else {
-      const int64_t ntiles = cdiv(d, 64) * cdiv(2 * H, 128);
-      KernelTimer timer("dw_in", s);
-      dw_kernel<DT, 0><<<(unsigned)(gc * ntiles), NT, 0, s>>>(q);
-      timer.stop();
-      NSMOE_TRY(check_launch("dw_kernel<in>"));
+  ExpParams q_in = p, q_out = p;
+  q_in.dw_a = gr->dw_in;
+  q_in.dw_sh = gr->dw_sh_in;
+  q_in.partial = (float*)(ws + L.p_in);
+  q_out.dw_a = gr->dw_out;
+  q_out.dw_sh = gr->dw_sh_out;
+  q_out.partial = (float*)(ws + L.p_out);
+  const int prc = launch_dw_pair_async(DT, q_in, q_out, gc, s);
+  if (prc != -1) {
+    NSMOE_TRY(prc);
+    dim3 rg(DWR_BLOCKS, (unsigned)(2 * G));
+    dw_reduce_pair_kernel<DT><<<rg, NT, 0, s>>>(q_in, q_out, G);
+    NSMOE_TRY(check_launch("dw_reduce_pair_kernel"));
+  } else {
+    {  // dW_in
+      const ExpParams& q = q_in;
+      const int rc = launch_dw_async(DT, 0, q, gc, s);
+      if (rc != -1) {
+        NSMOE_TRY(rc);
+      } else {
+        const int64_t ntiles = cdiv(d, 64) * cdiv(2 * H, 128);
+        KernelTimer timer("dw_in", s);
+        dw_kernel<DT, 0><<<(unsigned)(gc * ntiles), NT, 0, s>>>(q);
+        timer.stop();
+        NSMOE_TRY(check_launch("dw_kernel<in>"));
+      }
+      dim3 rg(DWR_BLOCKS, (unsigned)G);
+      dw_reduce_kernel<DT, 0><<<rg, NT, 0, s>>>(q);
+      NSMOE_TRY(check_launch("dw_reduce_kernel<in>"));
     }
-    dim3 rg(DWR_BLOCKS, (unsigned)G);
-    dw_reduce_kernel<DT, 0><<<rg, NT, 0, s>>>(q);
-    NSMOE_TRY(check_launch("dw_reduce_kernel<in>"));
-  }
-  {  // dW_out
-    ExpParams q = p;
-    q.dw_a = gr->dw_out;
-    q.dw_sh = gr->dw_sh_out;
-    q.partial = (float*)(ws + L.p_out);
-    const int rc = launch_dw_async(DT, 1, q, gc, s);
-    if (rc != -1) {
-      NSMOE_TRY(rc);
-    } else {
-      const int64_t ntiles = cdiv(H, 128) * cdiv(d, 64);
-      KernelTimer timer("dw_out", s);
-      dw_kernel<DT, 1><<<(unsigned)(gc * ntiles), NT, 0, s>>>(q);
-      timer.stop();
-      NSMOE_TRY(check_launch("dw_kernel<out>"));
+    {  // dW_out
+      const ExpParams& q = q_out;
+      const int rc = launch_dw_async(DT, 1, q, gc, s);
+      if (rc != -1) {
+        NSMOE_TRY(rc);
+      } else {
+        const int64_t ntiles = cdiv(H, 128) * cdiv(d, 64);
+        KernelTimer timer("dw_out", s);
+        dw_kernel<DT, 1><<<(unsigned)(gc * ntiles), NT, 0, s>>>(q);
+        timer.stop();
+        NSMOE_TRY(check_launch("dw_kernel<out>"));
+      }
+      dim3 rg(DWR_BLOCKS, (unsigned)G);
+      dw_reduce_kernel<DT, 1><<<rg, NT, 0, s>>>(q);
+      NSMOE_TRY(check_launch("dw_reduce_kernel<out>"));
     }
-    dim3 rg(DWR_BLOCKS, (unsigned)G);
-    dw_reduce_kernel<DT, 1><<<rg, NT, 0, s>>>(q);
-    NSMOE_TRY(check_launch("dw_reduce_kernel<out>"));
   }
   if (gr->db_in || gr->db_sh_in) {
     ExpParams q = p;

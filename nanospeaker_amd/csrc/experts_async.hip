@@ -1234,8 +1234,19 @@ template <> struct DwTile<1> {  // dW_out [H, d]: 128 x 192 tiles
   static constexpr int BMT = 128, BNT = 192, WM = 2, WN = 2;
 };
 
+template <int DT, int S>
+struct DwLds {
+  static constexpr int STAGE = Geo<DT>::KC * (DwTile<0>::BMT + DwTile<0>::BNT) * 2;
+  static_assert(STAGE == Geo<DT>::KC * (DwTile<1>::BMT + DwTile<1>::BNT) * 2,
+                "both modes stage the same bytes per step");
+  char ring[S][STAGE];
+  int tok[DW_RC];
+  int loc[3];
+};
+
+// One (group, row chunk, output tile) item of dW; `item` indexes the mode's item space.
 template <int DT, int MODE, int S>
-__global__ void __launch_bounds__(NT, 2) dw_async_kernel(ExpParams p) {
+__device__ __forceinline__ void dw_item(const ExpParams& p, int item, DwLds<DT, S>& L) {
   using G = Geo<DT>;
   using T = typename G::T;
   using M = Mma<DT>;
@@ -1252,15 +1263,15 @@ __global__ void __launch_bounds__(NT, 2) dw_async_kernel(ExpParams p) {
   constexpr int NBLK = QBLK + PBLK;
   static_assert(NBLK % 4 == 0, "copy blocks split evenly over the 4 waves");
   constexpr int LOADS = NBLK / 4;
-  __shared__ __attribute__((aligned(1024))) char s_ring[S][STAGE];
-  __shared__ int s_tok[DW_RC];
-  __shared__ int s_loc[3];
+  static_assert(STAGE == DwLds<DT, S>::STAGE, "stage layout");
+  auto& s_ring = L.ring;
+  int* s_tok = L.tok;
+  int* s_loc = L.loc;
 
   const int d = p.d, H = p.H, twoH = 2 * p.H;
   const int Md = MODE == 0 ? d : H;
   const int Nd = MODE == 0 ? twoH : d;
   const int tn = (Nd + BNT - 1) / BNT, ntiles = ((Md + BMT - 1) / BMT) * tn;
-  const int item = xcd_remap(blockIdx.x, gridDim.x);
   Located loc;
   if (!locate(item, p.E + p.S, [&](int g) { return dw_chunks(rows_of(p, g)) * ntiles; },
               [&](int g) {
@@ -1383,6 +1394,24 @@ __global__ void __launch_bounds__(NT, 2) dw_async_kernel(ExpParams p) {
   }
 }
 
+template <int DT, int MODE, int S>
+__global__ void __launch_bounds__(NT, 2) dw_async_kernel(ExpParams p) {
+  __shared__ __attribute__((aligned(1024))) DwLds<DT, S> lds;
+  dw_item<DT, MODE, S>(p, xcd_remap(blockIdx.x, gridDim.x), lds);
+}
+
+// dW_in and dW_out items in one launch: blocks [0, grid_in) take dW_in items, the rest
+// dW_out items (each part remapped XCD-major on its own).  One launch fills the machine's
+// workgroup slots with both item sets instead of leaving a nearly empty round after each.
+template <int DT, int S>
+__global__ void __launch_bounds__(NT, 2) dw_pair_kernel(ExpParams p_in, ExpParams p_out,
+                                                        int grid_in) {
+  __shared__ __attribute__((aligned(1024))) DwLds<DT, S> lds;
+  const int b = blockIdx.x;
+  if (b < grid_in) dw_item<DT, 0, S>(p_in, xcd_remap(b, grid_in), lds);
+  else dw_item<DT, 1, S>(p_out, xcd_remap(b - grid_in, (int)gridDim.x - grid_in), lds);
+}
+
 int launch_dw_async(int dtype, int mode, const ExpParams& q, int64_t groups_chunks,
                     hipStream_t s) {
   if (!q.fast || (dtype != DT_BF16 && dtype != DT_F16)) return -1;
@@ -1404,6 +1433,23 @@ int launch_dw_async(int dtype, int mode, const ExpParams& q, int64_t groups_chun
   }
   timer.stop();
   return check_launch("dw_async_kernel");
+}
+
+int launch_dw_pair_async(int dtype, const ExpParams& q_in, const ExpParams& q_out,
+                         int64_t groups_chunks, hipStream_t s) {
+  if (!q_in.fast || (dtype != DT_BF16 && dtype != DT_F16)) return -1;
+  const int d = q_in.d, H = q_in.H;
+  const int64_t g_in = groups_chunks * cdiv(d, DwTile<0>::BMT) * cdiv(2 * H, DwTile<0>::BNT);
+  const int64_t g_out = groups_chunks * cdiv(H, DwTile<1>::BMT) * cdiv(d, DwTile<1>::BNT);
+  if (g_in + g_out <= 0) return NSMOE_OK;
+  constexpr int S = 3;
+  KernelTimer timer("dw", s);
+  if (dtype == DT_BF16)
+    dw_pair_kernel<DT_BF16, S><<<(unsigned)(g_in + g_out), NT, 0, s>>>(q_in, q_out, (int)g_in);
+  else
+    dw_pair_kernel<DT_F16, S><<<(unsigned)(g_in + g_out), NT, 0, s>>>(q_in, q_out, (int)g_in);
+  timer.stop();
+  return check_launch("dw_pair_kernel");
 }
 
 int launch_fwd_async(int dtype, const ExpParams& p, int nbw, int64_t grid, hipStream_t s) {
