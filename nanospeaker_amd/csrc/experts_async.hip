@@ -55,7 +55,7 @@ __global__ void __launch_bounds__(NT, 2) expert_fwd_async_kernel(ExpParams p) {
   __shared__ float s_w[BM];
   __shared__ int s_loc[3];
 
-  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int tile = tile_of_block(p);
   Located loc;
   if (!locate(tile, p.E + p.S, [&](int g) { return (rows_of(p, g) + BM - 1) / BM; },
               [](int) { return 0; }, s_loc, loc))
@@ -278,7 +278,7 @@ __global__ void __launch_bounds__(NT, 2) expert_fwd_reg_kernel(ExpParams p) {
   __shared__ float s_w[BM];
   __shared__ int s_loc[3];
 
-  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int tile = tile_of_block(p);
   Located loc;
   if (!locate(tile, p.E + p.S, [&](int g) { return (rows_of(p, g) + BM - 1) / BM; },
               [](int) { return 0; }, s_loc, loc))
@@ -529,7 +529,7 @@ __global__ void __launch_bounds__(NT, 2) expert_bwd_async_kernel(ExpParams p) {
   __shared__ float s_dtw[5][BM];
   __shared__ int s_loc[3];
 
-  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int tile = tile_of_block(p);
   Located loc;
   if (!locate(tile, p.E + p.S, [&](int g) { return (rows_of(p, g) + BM - 1) / BM; },
               [](int) { return 0; }, s_loc, loc))
@@ -719,7 +719,7 @@ __global__ void __launch_bounds__(NT, 2) expert_dx_async_kernel(ExpParams p) {
   __shared__ __attribute__((aligned(1024))) char s_ring[S][STAGE];
   __shared__ int s_loc[3];
 
-  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int tile = tile_of_block(p);
   Located loc;
   if (!locate(tile, p.E + p.S, [&](int g) { return (rows_of(p, g) + BM - 1) / BM; },
               [](int) { return 0; }, s_loc, loc))
@@ -835,7 +835,7 @@ __global__ void __launch_bounds__(NT, 2) expert_bwd_reg_kernel(ExpParams p) {
   char* s_hb = s_lds + BM * DA_PITCH;
   auto ring = [&](int s) __attribute__((always_inline)) { return s_lds + (s % S) * 2 * A_BYTES; };
 
-  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int tile = tile_of_block(p);
   Located loc;
   if (!locate(tile, p.E + p.S, [&](int g) { return (rows_of(p, g) + BM - 1) / BM; },
               [](int) { return 0; }, s_loc, loc))
@@ -1051,7 +1051,7 @@ __global__ void __launch_bounds__(NT, 2) expert_dx_reg_kernel(ExpParams p) {
   __shared__ __attribute__((aligned(16))) char s_y[BM * Y_PITCH];
   __shared__ int s_loc[3];
 
-  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int tile = tile_of_block(p);
   Located loc;
   if (!locate(tile, p.E + p.S, [&](int g) { return (rows_of(p, g) + BM - 1) / BM; },
               [](int) { return 0; }, s_loc, loc))
@@ -1394,22 +1394,34 @@ __device__ __forceinline__ void dw_item(const ExpParams& p, int item, DwLds<DT, 
   }
 }
 
+// Output tiles per (group, row chunk) of a dW mode: the run of items that read the same
+// token rows, dealt to one XCD together.
+template <int MODE>
+__device__ __forceinline__ int dw_run(const ExpParams& p) {
+  using Tl = DwTile<MODE>;
+  const int Md = MODE == 0 ? p.d : p.H, Nd = MODE == 0 ? 2 * p.H : p.d;
+  return ((Md + Tl::BMT - 1) / Tl::BMT) * ((Nd + Tl::BNT - 1) / Tl::BNT);
+}
+
 template <int DT, int MODE, int S>
 __global__ void __launch_bounds__(NT, 2) dw_async_kernel(ExpParams p) {
   __shared__ __attribute__((aligned(1024))) DwLds<DT, S> lds;
-  dw_item<DT, MODE, S>(p, xcd_remap(blockIdx.x, gridDim.x), lds);
+  dw_item<DT, MODE, S>(p, xcd_deal(blockIdx.x, gridDim.x, dw_run<MODE>(p)), lds);
 }
 
 // dW_in and dW_out items in one launch: blocks [0, grid_in) take dW_in items, the rest
-// dW_out items (each part remapped XCD-major on its own).  One launch fills the machine's
+// dW_out items (each part dealt over the XCDs on its own; grid_in is a multiple of 8 so
+// that block b - grid_in sits on the same XCD as b).  One launch fills the machine's
 // workgroup slots with both item sets instead of leaving a nearly empty round after each.
 template <int DT, int S>
 __global__ void __launch_bounds__(NT, 2) dw_pair_kernel(ExpParams p_in, ExpParams p_out,
                                                         int grid_in) {
   __shared__ __attribute__((aligned(1024))) DwLds<DT, S> lds;
   const int b = blockIdx.x;
-  if (b < grid_in) dw_item<DT, 0, S>(p_in, xcd_remap(b, grid_in), lds);
-  else dw_item<DT, 1, S>(p_out, xcd_remap(b - grid_in, (int)gridDim.x - grid_in), lds);
+  if (b < grid_in) dw_item<DT, 0, S>(p_in, xcd_deal(b, grid_in, dw_run<0>(p_in)), lds);
+  else
+    dw_item<DT, 1, S>(p_out, xcd_deal(b - grid_in, (int)gridDim.x - grid_in, dw_run<1>(p_out)),
+                      lds);
 }
 
 int launch_dw_async(int dtype, int mode, const ExpParams& q, int64_t groups_chunks,
@@ -1439,7 +1451,9 @@ int launch_dw_pair_async(int dtype, const ExpParams& q_in, const ExpParams& q_ou
                          int64_t groups_chunks, hipStream_t s) {
   if (!q_in.fast || (dtype != DT_BF16 && dtype != DT_F16)) return -1;
   const int d = q_in.d, H = q_in.H;
-  const int64_t g_in = groups_chunks * cdiv(d, DwTile<0>::BMT) * cdiv(2 * H, DwTile<0>::BNT);
+  // Rounded up to whole XCD rounds (the extra items are past the last real one and exit).
+  const int64_t g_in =
+      cdiv(groups_chunks * cdiv(d, DwTile<0>::BMT) * cdiv(2 * H, DwTile<0>::BNT), 8) * 8;
   const int64_t g_out = groups_chunks * cdiv(H, DwTile<1>::BMT) * cdiv(d, DwTile<1>::BNT);
   if (g_in + g_out <= 0) return NSMOE_OK;
   constexpr int S = 3;

@@ -10,6 +10,7 @@ constexpr int BM = 64;      // rows per tile
 constexpr int NT = 256;     // threads per workgroup
 constexpr int DW_RC = 768;  // rows per dW chunk (work items of similar size)
 constexpr int NP2 = 192;  // output columns per pass of the second GEMMs
+constexpr int XCD_RUN = 16;  // default tiles per XCD run of the token-tile kernels
 
 struct ExpParams {
   const void* x;
@@ -29,6 +30,9 @@ struct ExpParams {
   int64_t l_cap;
   int d, H, E, S, k, act;
   int fast;
+  // Token-tile kernels: runs of xcd_run consecutive tiles are dealt round-robin over the
+  // XCDs (0: each XCD takes one contiguous eighth of the grid).
+  int xcd_run;
   // fragment-order weight packs (pack.hip): W_in for GEMM1, W_out for GEMM2
   const char* p_in;
   const char* p_out;
@@ -48,6 +52,11 @@ struct ExpParams {
   void* db;        // bias grad (routed)
   void* db_sh;     // bias grad (shared)
 };
+
+__device__ __forceinline__ int tile_of_block(const ExpParams& p) {
+  return p.xcd_run > 0 ? xcd_deal(blockIdx.x, gridDim.x, p.xcd_run)
+                       : xcd_remap(blockIdx.x, gridDim.x);
+}
 
 __device__ __forceinline__ int rows_of(const ExpParams& p, int g) {
   return g < p.E ? p.counts[g] : (int)p.T;

@@ -481,4 +481,17 @@ __device__ __forceinline__ int xcd_remap(int bid, int grid) {
   return x * q + (x < rr ? x : rr) + j;
 }
 
+// Runs of C consecutive work items are dealt round-robin over the 8 XCDs: the j-th
+// workgroup on XCD x takes item ((j / C) * 8 + x) * C + j % C. Grids sized as an upper
+// bound keep their real items at the low ids, so a contiguous split per XCD (xcd_remap)
+// would leave the last XCDs with only empty items; dealing runs spreads the real items
+// evenly while the C items of a run (same group, shared operand rows) share one L2.
+// Ids past the last whole 8*C span map to themselves, so the map is a bijection.
+__device__ __forceinline__ int xcd_deal(int bid, int grid, int C) {
+  const int span = 8 * C;
+  if (bid >= grid / span * span) return bid;
+  const int x = bid % 8, j = bid / 8;
+  return (j / C * 8 + x) * C + j % C;
+}
+
 }  // namespace nsmoe
