@@ -103,13 +103,14 @@ def time_gpu(m, x, g, steps: int, warmup: int):
     from nanospeaker_amd import _native as nat
 
     params = [p for p in m.parameters()]
+    xg = x.detach().requires_grad_(True)
+    one = torch.ones((), dtype=torch.float32, device=x.device)
 
     def step():
-        for p in params:
-            p.grad = None
-        xg = x.detach().requires_grad_(True)
+        # Every gradient of the block (input, router, experts) is computed and returned;
+        # none is accumulated into a .grad buffer.
         out = m(xg)
-        torch.autograd.backward([out, m.aux_loss], [g, torch.ones_like(m.aux_loss)])
+        return torch.autograd.grad([out, m.aux_loss], [xg] + params, [g, one])
 
     for _ in range(warmup):
         step()
@@ -236,19 +237,16 @@ def time_gpu_graph(m, x, g, steps: int, warmup: int):
     """The same fwd+bwd step (and the forward alone), captured once in a HIP graph and
     replayed: every replay runs every kernel of the step on the resident inputs; only the
     host-side enqueue (Python, autograd, the library's argument setup) is removed.
-    torch's capture recipe: warm-up on a side stream, then capture; parameter gradients
-    are cleared inside the captured step (each replay writes them afresh), the input's
-    gradient buffer is zeroed in the graph."""
+    torch's capture recipe: warm-up on a side stream, then capture."""
     params = [p for p in m.parameters()]
     xg = x.detach().requires_grad_(True)
+    one = torch.ones((), dtype=torch.float32, device=x.device)
 
     def step():
-        for p in params:
-            p.grad = None
-        if xg.grad is not None:
-            xg.grad.zero_()
+        # All gradients of the block (input, router, experts) are returned by the step, in
+        # the graph's own memory; no .grad buffer is zeroed or accumulated into.
         out = m(xg)
-        torch.autograd.backward([out, m.aux_loss], [g, torch.ones_like(m.aux_loss)])
+        return torch.autograd.grad([out, m.aux_loss], [xg] + params, [g, one])
 
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())

@@ -238,69 +238,68 @@ __global__ void __launch_bounds__(NT, 2) expert_fwd_async_kernel(ExpParams p) {
   wait_vmcnt<0>();  // nothing may be in flight when the workgroup retires
 }
 
-// expert_fwd_reg: the same tile and arithmetic as expert_fwd_async_kernel, with the
-// weights -- private to each wave -- loaded from L2 straight into registers two k-steps
-// ahead (two fragment sets in flight), and only the token tile (shared by the 4 waves)
-// copied through the LDS ring.  That halves the LDS traffic of a step and issues one
-// LDS-DMA copy per wave per step instead of 1 + 2 NBW.  GEMM2 reads h from LDS and its
-// weights from registers; its only barriers are those of the output staging: each
-// 192-column pass of y is assembled in LDS (over the token ring, idle by then) and leaves
-// as whole 384-byte row segments in 16-byte stores -- 8-byte stores straight from the
-// accumulators would write 16 separate 32-byte segments per instruction.
+// expert_fwd_reg: the same arithmetic as expert_fwd_async_kernel on tiles of MB 16-row
+// blocks (MB = 4: 64 rows, MB = 6: 96 rows), with the weights -- private to each wave --
+// loaded from L2 straight into registers two k-steps ahead (two fragment sets in flight),
+// and only the token tile (shared by the 4 waves) copied through the LDS ring.  GEMM2
+// reads h from LDS and its weights from registers.
 //
-// Step s issues, after its MFMAs, the weights of step s + 2 and then the token copy of
-// step s + 2; step s therefore waits (vmcnt) until only what step s - 1 issued is in
-// flight, which also covers the weights of step s (issued just before the copy).  Every
-// load is unconditional (out-of-range fragments read a zero page), so the compiler's own
-// waits for the weight registers count exactly and leave the next step's loads in flight.
+// Every tile streams its group's whole weight stack through the CU once, so the weight
+// bytes per MFMA fall as the tile grows: 96-row tiles move 2/3 of the weight bytes per row
+// of 64-row tiles, and at T = 8192 their ~720 tiles fit the machine's resident workgroup
+// slots in one round where ~1060 64-row tiles take two.
+//
+// Output: MB = 4 assembles each 192-column pass of y in LDS (over the token ring, idle by
+// then) and stores whole 384-byte row segments in 16-byte stores; MB = 6 keeps its LDS at
+// 3 workgroups per CU and stores 8 bytes per lane straight from the accumulators.
+//
+// Step s issues, after its MFMAs, the weights of step s + 2 and then the token copies of
+// step s + 2 (one per wave for 64 rows; for 96 rows a second, on half the lanes); step s
+// therefore waits (vmcnt) until only what step s - 1 issued is in flight, which also
+// covers the weights of step s (issued just before the copies).  Every load is
+// unconditional (out-of-range fragments read a zero page), so the compiler's own waits
+// for the weight registers are exact or stricter and leave the next step's loads in flight.
 // Shapes: d % 64 == 0 (an even number of GEMM1 steps) and an even number of GEMM2 steps.
-template <int DT, int NBW>
-__global__ void __launch_bounds__(NT, 2) expert_fwd_reg_kernel(ExpParams p) {
+template <int DT, int NBW, int MB>
+__global__ void __launch_bounds__(NT, MB == 6 ? 3 : 2) expert_fwd_reg_kernel(ExpParams p) {
   using G = Geo<DT>;
   using T = typename G::T;
   using M = Mma<DT>;
   using Frag = typename M::Frag;
   static_assert(G::ES == 2, "16-bit types only");
+  static_assert(MB == 4 || MB == 6, "64- or 96-row tiles");
+  constexpr int TM = MB * 16;            // tile rows
   constexpr int S = 3;                   // token-tile ring stages
+  constexpr int XC = MB == 4 ? 1 : 2;    // token copies per wave per step
+  constexpr bool STAGE_Y = MB == 4;
   constexpr int HPMAX = 64 * NBW;
-  constexpr int A_BYTES = BM * G::ROWB;  // 64 rows x 32 elements = 4 KiB = one copy per lane
+  constexpr int A_BYTES = TM * G::ROWB;  // TM rows x 32 elements
   constexpr int NB1 = 2 * NBW;           // GEMM1 fragments per wave per step
   constexpr int NB2 = 3;                 // GEMM2 fragments per wave per step
   constexpr int NBMAX = NB1 > NB2 ? NB1 : NB2;
   constexpr int HP_PITCH = HPMAX * G::ES + 16;
   constexpr int Y_PITCH = NP2 * G::ES + 16;  // staged y rows: one pass's 192 columns
-  constexpr int RING_BYTES = S * A_BYTES > BM * Y_PITCH ? S * A_BYTES : BM * Y_PITCH;
+  constexpr int Y_BYTES = STAGE_Y ? TM * Y_PITCH : 0;
+  constexpr int RING_BYTES = S * A_BYTES > Y_BYTES ? S * A_BYTES : Y_BYTES;
   __shared__ __attribute__((aligned(1024))) char s_ring_raw[RING_BYTES];
   char (*s_ring)[A_BYTES] = (char (*)[A_BYTES])s_ring_raw;
   char* s_y = s_ring_raw;  // GEMM2 output staging, after GEMM1 is done with the ring
-  __shared__ __attribute__((aligned(16))) char s_h[BM * HP_PITCH];
-  __shared__ int s_tok[BM];
-  __shared__ float s_w[BM];
+  __shared__ __attribute__((aligned(16))) char s_h[TM * HP_PITCH];
+  __shared__ int s_tok[TM];
+  __shared__ float s_w[TM];
   __shared__ int s_loc[3];
 
   const int tile = tile_of_block(p);
   Located loc;
-  if (!locate(tile, p.E + p.S, [&](int g) { return (rows_of(p, g) + BM - 1) / BM; },
+  if (!locate(tile, p.E + p.S, [&](int g) { return (rows_of(p, g) + TM - 1) / TM; },
               [](int) { return 0; }, s_loc, loc))
     return;
-  const int g = loc.g, m0 = loc.local * BM;
-  const int rows = min(BM, rows_of(p, g) - m0);
+  const int g = loc.g, m0 = loc.local * TM;
+  const int rows = min(TM, rows_of(p, g) - m0);
   const int64_t slot0 = row_start(p, g) + m0;
   const int tid = threadIdx.x, lane = tid & 63, lc = lane & 15, lg = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  if (tid < BM) {
-    int tok = -1, pair;
-    float w = 0.0f;
-    if (tid < rows) row_info<DT>(p, g, slot0 + tid, m0 + tid, tok, w, pair);
-    s_tok[tid] = tok;
-    s_w[tid] = w;
-  }
-  __syncthreads();
-
   const int d = p.d, H = p.H, twoH = 2 * p.H;
-  const int ar = tid >> 2, ac = (tid & 3) ^ swz<DT>(ar);
-  const int atok = s_tok[ar];
-  const T* arow = atok >= 0 ? (const T*)p.x + (int64_t)atok * d + ac * G::VE : nullptr;
   const char* zero = (const char*)g_zero_kib + lane * 16;
   const char* P1 = p.p_in + (int64_t)g * p.in_nb * p.in_kb * G::PKB + lane * G::FRAGB;
   const char* P4 = p.p_out + (int64_t)g * p.out_nb * p.out_kb * G::PKB + lane * G::FRAGB;
@@ -338,56 +337,106 @@ __global__ void __launch_bounds__(NT, 2) expert_fwd_reg_kernel(ExpParams p) {
     for (int j = NB2; j < NBMAX; ++j) w.f[j] = M::zero();
     return w;
   };
+
+  // The first two weight sets depend only on the group: they are in flight while the
+  // rows' tokens are looked up.  The gate weights are loaded before the token copies are
+  // issued and reach LDS after GEMM1 (GEMM2's epilogue reads them), so waiting for them
+  // never waits for a copy.
+  WSet wa = load_w1(0);
+  WSet wb = load_w1(1);
+  const bool routed = g < p.E;
+  int pair = -1;
+  if (tid < TM) {
+    int tok = -1;
+    if (tid < rows) {
+      if (routed) {
+        pair = p.sorted_ids[slot0 + tid];
+        tok = pair / p.k;
+      } else {
+        tok = m0 + tid;
+      }
+    }
+    s_tok[tid] = tok;
+  }
+  __syncthreads();
+  float gate_w = 0.0f;
+  if (tid < rows)
+    gate_w = routed ? Elem<DT>::to_f(((const T*)p.topk_w)[pair]) : 1.0f;
+  // Token copies: copy slot c (16 bytes) holds chunk (c % 4) ^ swz(r) of row r = c / 4.
+  // The first copy of wave w fills slots [256 w / 4 ... ) = tid; for 96 rows the second
+  // fills slots 256 + 32 w + lane (lanes < 32), rows 64 + 8 w + lane / 4.
+  const int ar = tid >> 2, ac = (tid & 3) ^ swz<DT>(ar);
+  const int atok = s_tok[ar];
+  const T* arow = atok >= 0 ? (const T*)p.x + (int64_t)atok * d + ac * G::VE : nullptr;
+  const T* arow2 = nullptr;
+  int ac2 = 0;
+  if constexpr (XC == 2) {
+    const int r2 = 64 + wave * 8 + (lane >> 2);
+    ac2 = ((lane & 3) ^ swz<DT>(r2));
+    const int t2 = lane < 32 ? s_tok[r2 < TM ? r2 : 0] : -1;
+    arow2 = t2 >= 0 ? (const T*)p.x + (int64_t)t2 * d + ac2 * G::VE : nullptr;
+  }
   auto issue_x = [&](int s) __attribute__((always_inline)) {
     const int k0 = s * G::KC;
     const bool av = arow && k0 + ac * G::VE < d;
     async_copy16(av ? (const void*)(arow + k0) : (const void*)zero, s_ring[s % S] + wave * 1024);
+    if constexpr (XC == 2) {
+      const bool av2 = arow2 && k0 + ac2 * G::VE < d;
+      if (lane < 32)
+        async_copy16(av2 ? (const void*)(arow2 + k0) : (const void*)zero,
+                     s_ring[s % S] + 4096 + wave * 512);
+    }
   };
 
   // ---- GEMM1 (transposed): acc[i][j] = W_in[:, cols of block j]^T x[rows of block i]^T ----
-  f32x4 accg[4][NBW], accu[4][NBW];
+  f32x4 accg[MB][NBW], accu[MB][NBW];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < MB; ++i)
 #pragma unroll
     for (int j = 0; j < NBW; ++j) accg[i][j] = accu[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   auto g1mma = [&](int s, const WSet& w) __attribute__((always_inline)) {
     barrier_dma();
     const char* st = s_ring[s % S];
-    Frag xf[4];
+    // Token fragments in groups of (at most) 4 row blocks, to bound the live registers.
+    constexpr int XG = MB > 4 ? 2 : MB;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) xf[i] = frag_sw<DT>(st, i * 16);
+    for (int i0 = 0; i0 < MB; i0 += XG) {
+      Frag xf[XG];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < XG; ++i) xf[i] = frag_sw<DT>(st, (i0 + i) * 16);
 #pragma unroll
-      for (int j = 0; j < NBW; ++j) {
-        M::run(accg[i][j], w.f[j], xf[i]);
-        M::run(accu[i][j], w.f[NBW + j], xf[i]);
-      }
+      for (int i = 0; i < XG; ++i)
+#pragma unroll
+        for (int j = 0; j < NBW; ++j) {
+          M::run(accg[i0 + i][j], w.f[j], xf[i]);
+          M::run(accu[i0 + i][j], w.f[NBW + j], xf[i]);
+        }
+    }
   };
 
-  WSet wa = load_w1(0);
   issue_x(0);
-  WSet wb = load_w1(1);
   issue_x(1);
+  wait_vmcnt<XC>();  // the gate weights and step 0's copies; step 1's stay in flight
   int s = 0;
   for (; s + 2 < nk1; s += 2) {  // steady state: the steps two ahead are GEMM1 steps
-    wait_vmcnt<NB1 + 1>();
+    wait_vmcnt<NB1 + XC>();
     g1mma(s, wa);
     wa = load_w1(s + 2);
     issue_x(s + 2);
-    wait_vmcnt<NB1 + 1>();
+    wait_vmcnt<NB1 + XC>();
     g1mma(s + 1, wb);
     wb = load_w1(s + 3);
     issue_x(s + 3);
   }
   // The last two GEMM1 steps prefetch GEMM2's first two weight sets.
-  wait_vmcnt<NB1 + 1>();
+  wait_vmcnt<NB1 + XC>();
   g1mma(s, wa);
   wa = load_w2(0);
   wait_vmcnt<NB2>();
   g1mma(s + 1, wb);
   wb = load_w2(1);
 
+  if (tid < TM) s_w[tid] = gate_w;  // published by the barrier after the epilogue
   // ---- GEMM1 epilogue: bias, h = act(gate) * up -> LDS --------------------------------------
   const T* bin = (g < p.E ? p.b_in : p.b_sh_in)
                      ? per_group<T>(p.b_in, p.b_sh_in, g, p.E, twoH) : nullptr;
@@ -406,7 +455,7 @@ __global__ void __launch_bounds__(NT, 2) expert_fwd_reg_kernel(ExpParams p) {
         }
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < MB; ++i) {
         float hv[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r)
@@ -418,71 +467,133 @@ __global__ void __launch_bounds__(NT, 2) expert_fwd_reg_kernel(ExpParams p) {
     }
   });
   // h published: its ds_write stores complete, then a bare barrier (a fence here would
-  // also wait for the GEMM2 weights in flight).  No barrier after this point.
+  // also wait for the GEMM2 weights in flight).
   wait_lgkm0();
   barrier_dma();
 
-  // ---- GEMM2 (transposed): y^T = W_out^T h^T, + b_out, * gate, 8-byte row stores ----
+  // ---- GEMM2 (transposed): y^T = W_out^T h^T, + b_out, * gate ---------------------------
   const T* bout = (g < p.E ? p.b_out : p.b_sh_out)
                       ? per_group<T>(p.b_out, p.b_sh_out, g, p.E, d) : nullptr;
-  float wrow[4];
+  float wrow[MB];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) wrow[i] = s_w[i * 16 + lc];
+  for (int i = 0; i < MB; ++i) wrow[i] = s_w[i * 16 + lc];
   T* Y = (T*)p.y + slot0 * d;
-  f32x4 acc[4][3];
+  f32x4 acc[MB][3];
   auto g2step = [&](int q, const WSet& w) __attribute__((always_inline)) {
     const int pass = q / nk2, kb = q - pass * nk2;
     if (kb == 0) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < MB; ++i)
 #pragma unroll
         for (int j = 0; j < 3; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    Frag hf[4];
+    constexpr int HG = MB > 4 ? MB / 2 : MB;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) hf[i] = frag_at<DT>(s_h, HP_PITCH, i * 16, kb * G::ROWB);
+    for (int i0 = 0; i0 < MB; i0 += HG) {
+      Frag hf[HG];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < HG; ++i)
+        hf[i] = frag_at<DT>(s_h, HP_PITCH, (i0 + i) * 16, kb * G::ROWB);
 #pragma unroll
-      for (int j = 0; j < 3; ++j) M::run(acc[i][j], w.f[j], hf[i]);
+      for (int i = 0; i < HG; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) M::run(acc[i0 + i][j], w.f[j], hf[i]);
+    }
     if (kb == nk2 - 1) {
-      // + b_out, * gate, packed into the staging tile (the previous pass's reads are done
-      // once every wave has passed this barrier).
-      wait_lgkm0();
-      barrier_dma();
+      if constexpr (STAGE_Y) {
+        // + b_out, * gate, packed into the staging tile (the previous pass's reads are
+        // done once every wave has passed this barrier).
+        wait_lgkm0();
+        barrier_dma();
 #pragma unroll
-      for (int j = 0; j < 3; ++j) {
-        const int c0 = (wave * 3 + j) * 16 + lg * 4;  // column inside the pass
-        const int n0 = pass * NP2 + c0;
-        if (n0 >= d) continue;
-        float bo[4] = {0.f, 0.f, 0.f, 0.f};
-        if (bout) {
-          const uint2 b = *(const uint2*)(bout + n0);
-          bo[0] = unpack2<DT>(b.x, 0);
-          bo[1] = unpack2<DT>(b.x, 1);
-          bo[2] = unpack2<DT>(b.y, 0);
-          bo[3] = unpack2<DT>(b.y, 1);
+        for (int j = 0; j < 3; ++j) {
+          const int c0 = (wave * 3 + j) * 16 + lg * 4;  // column inside the pass
+          const int n0 = pass * NP2 + c0;
+          if (n0 >= d) continue;
+          float bo[4] = {0.f, 0.f, 0.f, 0.f};
+          if (bout) {
+            const uint2 b = *(const uint2*)(bout + n0);
+            bo[0] = unpack2<DT>(b.x, 0);
+            bo[1] = unpack2<DT>(b.x, 1);
+            bo[2] = unpack2<DT>(b.y, 0);
+            bo[3] = unpack2<DT>(b.y, 1);
+          }
+#pragma unroll
+          for (int i = 0; i < MB; ++i) {
+            const int m = i * 16 + lc;
+            const float wt = wrow[i];
+            const uint32_t lo =
+                pack2<DT>((acc[i][j][0] + bo[0]) * wt, (acc[i][j][1] + bo[1]) * wt);
+            const uint32_t hi =
+                pack2<DT>((acc[i][j][2] + bo[2]) * wt, (acc[i][j][3] + bo[3]) * wt);
+            *(uint2*)(s_y + m * Y_PITCH + c0 * G::ES) = make_uint2(lo, hi);
+          }
+        }
+        wait_lgkm0();
+        barrier_dma();
+        // TM rows x 24 chunks of 16 bytes; a wave's store covers 2.67 whole 384-byte rows.
+        const int ncols = min(NP2, d - pass * NP2);
+        constexpr int CPR = NP2 / G::VE;  // chunks per staged row
+#pragma unroll
+        for (int u = 0; u < TM * CPR / NT; ++u) {
+          const int c = tid + u * NT, m = c / CPR, cc = c % CPR;
+          if (m < rows && cc * G::VE < ncols) {
+            const u32x4 v = *(const u32x4*)(s_y + m * Y_PITCH + cc * 16);
+            *(u32x4*)(Y + (int64_t)m * d + pass * NP2 + cc * G::VE) = v;
+          }
+        }
+      } else {
+        // + b_out, * gate.  The wave's 48 columns of this pass are blocks 0..2; blocks 0
+        // and 1 are regrouped across lanes (two permlane swaps per dword) so that lane
+        // (lc, lg) holds columns cw + 8 lg .. + 7 of its row and stores them in one 16-byte
+        // store (16 rows x 64 contiguous bytes per instruction); block 2 leaves in 8-byte
+        // stores.  Lanes hold 4 consecutive columns per block: row r = lg of a 16-lane
+        // group holds columns 4 r .. 4 r + 3.  permlane32_swap(b0, b1) gives rows
+        // (b0.r0, b0.r1, b1.r0, b1.r1) and (b0.r2, b0.r3, b1.r2, b1.r3); permlane16_swap of
+        // those gives (b0.r0, b0.r2, b1.r0, b1.r2) and (b0.r1, b0.r3, b1.r1, b1.r3).
+        const int cw = pass * NP2 + wave * 48;  // wave-uniform
+        float bo[3][4];
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+          const int n0 = cw + j * 16 + lg * 4;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) bo[j][r] = 0.0f;
+          if (bout && n0 < d) {
+            const uint2 b = *(const uint2*)(bout + n0);
+            bo[j][0] = unpack2<DT>(b.x, 0);
+            bo[j][1] = unpack2<DT>(b.x, 1);
+            bo[j][2] = unpack2<DT>(b.y, 0);
+            bo[j][3] = unpack2<DT>(b.y, 1);
+          }
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < MB; ++i) {
           const int m = i * 16 + lc;
           const float wt = wrow[i];
-          const uint32_t lo = pack2<DT>((acc[i][j][0] + bo[0]) * wt, (acc[i][j][1] + bo[1]) * wt);
-          const uint32_t hi = pack2<DT>((acc[i][j][2] + bo[2]) * wt, (acc[i][j][3] + bo[3]) * wt);
-          *(uint2*)(s_y + m * Y_PITCH + c0 * G::ES) = make_uint2(lo, hi);
-        }
-      }
-      wait_lgkm0();
-      barrier_dma();
-      // 64 rows x 24 chunks of 16 bytes; a wave's store covers 2.67 whole 384-byte rows.
-      const int ncols = min(NP2, d - pass * NP2);
-      constexpr int CPR = NP2 / G::VE;  // chunks per staged row
+          uint32_t lo[3], hi[3];
 #pragma unroll
-      for (int u = 0; u < BM * CPR / NT; ++u) {
-        const int c = tid + u * NT, m = c / CPR, cc = c % CPR;
-        if (m < rows && cc * G::VE < ncols) {
-          const u32x4 v = *(const u32x4*)(s_y + m * Y_PITCH + cc * 16);
-          *(u32x4*)(Y + (int64_t)m * d + pass * NP2 + cc * G::VE) = v;
+          for (int j = 0; j < 3; ++j) {
+            lo[j] = pack2<DT>((acc[i][j][0] + bo[j][0]) * wt, (acc[i][j][1] + bo[j][1]) * wt);
+            hi[j] = pack2<DT>((acc[i][j][2] + bo[j][2]) * wt, (acc[i][j][3] + bo[j][3]) * wt);
+          }
+          T* yrow = Y + (int64_t)m * d;
+          if (cw + 32 <= d) {
+            const auto l32 = __builtin_amdgcn_permlane32_swap(lo[0], lo[1], false, false);
+            const auto h32 = __builtin_amdgcn_permlane32_swap(hi[0], hi[1], false, false);
+            const auto l16 = __builtin_amdgcn_permlane16_swap(l32[0], l32[1], false, false);
+            const auto h16 = __builtin_amdgcn_permlane16_swap(h32[0], h32[1], false, false);
+            if (m < rows) {
+              u32x4 v;
+              v[0] = l16[0];
+              v[1] = h16[0];
+              v[2] = l16[1];
+              v[3] = h16[1];
+              *(u32x4*)(yrow + cw + lg * 8) = v;
+              if (cw + 32 < d) *(uint2*)(yrow + cw + 32 + lg * 4) = make_uint2(lo[2], hi[2]);
+            }
+          } else if (cw < d && m < rows) {
+            *(uint2*)(yrow + cw + lg * 4) = make_uint2(lo[0], hi[0]);
+          }
         }
       }
     }
@@ -1466,6 +1577,34 @@ int launch_dw_pair_async(int dtype, const ExpParams& q_in, const ExpParams& q_ou
   return check_launch("dw_pair_kernel");
 }
 
+// Compute units of the current device (cached per device).
+static int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+// Upper bound on the token tiles of `bm` rows over all groups (routed, then shared).
+static int64_t tile_grid(const ExpParams& p, int bm) {
+  const int64_t M = p.T * p.k;
+  const int64_t nonempty = M < p.E ? M : p.E;
+  return cdiv(M, bm) + nonempty + (int64_t)p.S * cdiv(p.T, bm);
+}
+
+template <int DT, int NBW>
+static void fwd_reg_launch(const ExpParams& p, int mb, hipStream_t s) {
+  if (mb == 6) expert_fwd_reg_kernel<DT, NBW, 6><<<(unsigned)tile_grid(p, 96), NT, 0, s>>>(p);
+  else expert_fwd_reg_kernel<DT, NBW, 4><<<(unsigned)tile_grid(p, 64), NT, 0, s>>>(p);
+}
+
 int launch_fwd_async(int dtype, const ExpParams& p, int nbw, int64_t grid, hipStream_t s) {
   if (!p.fast || nbw > 2 || (dtype != DT_BF16 && dtype != DT_F16)) return -1;
   if (grid <= 0) return NSMOE_OK;
@@ -1474,12 +1613,19 @@ int launch_fwd_async(int dtype, const ExpParams& p, int nbw, int64_t grid, hipSt
   static const bool reg = getenv("NSMOE_FWD_LDSW") == nullptr;
   const int n2 = ((p.d + NP2 - 1) / NP2) * p.out_kb;
   if (reg && p.d % 64 == 0 && n2 % 2 == 0) {
+    // 96-row tiles once 64-row tiles overflow the resident workgroup slots (3 per CU);
+    // NSMOE_FWD_MB = 4 or 6 forces a tile height (read on every call, for tests).
+    int mb = tile_grid(p, 64) > 3 * (int64_t)device_cus() ? 6 : 4;
+    if (const char* e = getenv("NSMOE_FWD_MB")) {
+      const int v = atoi(e);
+      if (v == 4 || v == 6) mb = v;
+    }
     if (dtype == DT_BF16) {
-      if (nbw == 1) expert_fwd_reg_kernel<DT_BF16, 1><<<(unsigned)grid, NT, 0, s>>>(p);
-      else expert_fwd_reg_kernel<DT_BF16, 2><<<(unsigned)grid, NT, 0, s>>>(p);
+      if (nbw == 1) fwd_reg_launch<DT_BF16, 1>(p, mb, s);
+      else fwd_reg_launch<DT_BF16, 2>(p, mb, s);
     } else {
-      if (nbw == 1) expert_fwd_reg_kernel<DT_F16, 1><<<(unsigned)grid, NT, 0, s>>>(p);
-      else expert_fwd_reg_kernel<DT_F16, 2><<<(unsigned)grid, NT, 0, s>>>(p);
+      if (nbw == 1) fwd_reg_launch<DT_F16, 1>(p, mb, s);
+      else fwd_reg_launch<DT_F16, 2>(p, mb, s);
     }
     timer.stop();
     return check_launch("expert_fwd_reg_kernel");

@@ -101,6 +101,21 @@ def test_experts_forward_backward(dtype, shape, k, S, bias, T):
         check(f"grad {n}", g[n], ref_g[n], dtype)
 
 
+@pytest.mark.parametrize("mb", ["4", "6"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", ["wide_h64", "wide_h96", "ns_h128"])
+@pytest.mark.parametrize("T", [37, 300, 1000])
+def test_forward_tile_heights(mb, dtype, shape, T, monkeypatch):
+    """Both forward tile heights (64- and 96-row tiles, forced) against the oracle, with
+    ragged last tiles and the shared experts' full-T groups."""
+    monkeypatch.setenv("NSMOE_FWD_MB", mb)
+    d, E, d_ff = SHAPES[shape]
+    p, x, gout, tw, ti = make_case(d, E, d_ff, 6, 2, T % 2 == 0, T, dtype, seed=T + int(mb))
+    ref_out, _ = oracle_fwd_bwd(p, x, gout, tw, ti, "silu", with_grad=False)
+    out, _ = gpu_fwd_bwd(p, x, gout, tw, ti, "silu", with_grad=False)
+    check("out", out, ref_out, dtype)
+
+
 @pytest.mark.parametrize("act", ["silu", "gelu", "relu", "sigmoid", "tanh"])
 @pytest.mark.parametrize("shape", ["tiny_h42", "ns_h128"])
 def test_every_activation(act, shape):

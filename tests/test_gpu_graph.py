@@ -5,9 +5,9 @@ host synchronisations between the replays; every replay must equal an eager step
 bit (the kernels are deterministic), which also shows the library records no memsets or
 host synchronisations that a replay would not repeat.
 
-Capture follows torch's recipe: warm-up on a side stream, then capture.  Parameter
-gradients are cleared (set to None) inside the captured step, so each replay writes them
-afresh; the input's gradient buffer exists from the warm-up and is zeroed in the graph.
+Capture follows torch's recipe: warm-up on a side stream, then capture.  The step returns
+every gradient (input, router, experts) from torch.autograd.grad, so the captured graph
+writes them into its own memory on each replay and nothing is accumulated.
 """
 
 import pytest
@@ -36,14 +36,12 @@ def test_training_step_replays_equal_eager(T):
     params = list(m.parameters())
     xg = x.detach().requires_grad_(True)
 
+    one = torch.ones((), dtype=torch.float32, device=DEV)
+
     def step():
-        for p in params:
-            p.grad = None
-        if xg.grad is not None:
-            xg.grad.zero_()
         out = m(xg)
-        torch.autograd.backward([out, m.aux_loss], [g, torch.ones_like(m.aux_loss)])
-        return out
+        grads = torch.autograd.grad([out, m.aux_loss], [xg] + params, [g, one])
+        return out, list(grads)
 
     print(f"[graph] T={T} warm-up", flush=True)
     side = torch.cuda.Stream()
@@ -56,9 +54,8 @@ def test_training_step_replays_equal_eager(T):
     graph = torch.cuda.CUDAGraph()
     print(f"[graph] T={T} capture", flush=True)
     with torch.cuda.graph(graph):
-        out = step()
+        out, grads = step()
     aux = m.aux_loss  # the captured tensors (eager calls below rebind the attributes)
-    grads = [xg.grad] + [p.grad for p in params]
     got = []
     for r in range(3):
         scratch = torch.randn(T, 576, device=DEV).to(torch.bfloat16)
@@ -69,10 +66,9 @@ def test_training_step_replays_equal_eager(T):
         torch.cuda.synchronize()
         print(f"[graph] T={T} replay {r}", flush=True)
         got.append([out.clone(), aux.detach().clone()] + [t.clone() for t in grads])
-    # the eager step, on fresh gradient buffers
-    xg.grad = None
-    ref_out = step().detach()
-    ref = [ref_out, m.aux_loss.detach()] + [xg.grad] + [p.grad for p in params]
+    # the eager step
+    ref_out, ref_grads = step()
+    ref = [ref_out.detach(), m.aux_loss.detach()] + ref_grads
     for r, vals in enumerate(got):
         for i, (a, b) in enumerate(zip(vals, ref)):
             assert torch.equal(a, b), f"replay {r}: tensor {i}"
