@@ -12,14 +12,15 @@
 // global atomics deciding it:
 //   1. hist:    one workgroup per chunk of pairs (1024, or 256 for E > 256) counts its
 //               experts in LDS;
-//   2. scan:    one workgroup turns the [chunks, E] counts into per-chunk run bases (a
-//               segmented scan down each expert's column: every thread owns one
-//               segment, so the loads of a column are issued together, not one by
-//               one), the padded run offsets, the block -> expert map and the sentinels;
-//   3. scatter: each chunk ranks its pairs inside each expert.  Every lane sets its bit
-//               in a per-wave 64-bit LDS mask for its expert (ds_or_b64, order-free);
-//               the rank is then popcount(mask & lanes-below) plus the popcounts of the
-//               same expert's masks of the waves before it.
+//   2. place:   one workgroup per chunk again.  Each derives its chunk's base in every
+//               expert's run (column sums of the [chunks, E] counts over the chunks
+//               before it), the experts' totals and the padded run offsets by itself, so
+//               no single-workgroup scan sits between the two launches.  It ranks its
+//               pairs inside each expert -- every lane sets its bit in a per-wave 64-bit
+//               LDS mask for its expert (ds_or_b64, order-free); the rank is then
+//               popcount(mask & lanes-below) plus the popcounts of the same expert's
+//               masks of the waves before it -- and places them; the block -> expert map
+//               and the sentinels are split over the workgroups.
 #include "nsmoe_capi_internal.h"
 #include "nsmoe_common.h"
 
@@ -48,117 +49,139 @@ dispatch_hist_kernel(const int64_t* __restrict__ topk_idx, int64_t M, int E,
   for (int e = threadIdx.x; e < E; e += blockDim.x) row[e] = s_cnt[e];
 }
 
-// One workgroup.  hist is rewritten in place into exclusive per-chunk bases.
+// One workgroup per chunk (the hist kernel's chunks).  Every workgroup derives what it
+// needs from the [chunks, E] counts itself -- its chunk's base in each expert's run (the
+// column sum over the chunks before it), the experts' totals and the ALIGN_M-padded run
+// offsets -- then ranks and places its pairs.  The block -> expert map and the sentinel
+// fill are split over the workgroups; workgroup 0 also writes counts, offsets and the
+// padded total.  Column sums: thread (e, seg) owns a segment of expert e's column and
+// issues its loads together; the segment sums are added in LDS.
 __global__ void __launch_bounds__(1024)
-dispatch_scan_kernel(int32_t* __restrict__ hist, int64_t n_chunks, int E, int64_t M,
-                     int64_t l_cap, int32_t* __restrict__ sorted_ids,
-                     int32_t* __restrict__ expert_ids, int32_t* __restrict__ offs,
-                     int32_t* __restrict__ counts, int32_t* __restrict__ npp) {
+dispatch_place_kernel(const int64_t* __restrict__ topk_idx, int64_t M, int E,
+                      const int32_t* __restrict__ hist, int64_t n_chunks, int64_t l_cap,
+                      int32_t* __restrict__ sorted_ids, int32_t* __restrict__ expert_ids,
+                      int32_t* __restrict__ offs, int32_t* __restrict__ counts,
+                      int32_t* __restrict__ npp, int32_t* __restrict__ inv) {
+  extern __shared__ unsigned long long s_mask[];  // [waves][E]
+  __shared__ int32_t s_base[DISPATCH_MAX_EXPERTS];
+  __shared__ int32_t s_tot[DISPATCH_MAX_EXPERTS];
   __shared__ int32_t s_off[DISPATCH_MAX_EXPERTS + 1];
-  __shared__ int32_t s_cnt[DISPATCH_MAX_EXPERTS];
+  __shared__ int32_t s_seg_b[1024], s_seg_t[1024];
   __shared__ int32_t s_wave[16];
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, nt = blockDim.x;
+  const int lane = tid & 63, wave = tid >> 6, waves = nt >> 6;
+  const int64_t chunk = blockIdx.x;
 
-  // Per-expert exclusive sums down the chunk column.  Thread (e, seg) owns chunks
-  // [seg * L, (seg + 1) * L) of expert e's column: it sums them (independent loads),
-  // the segment totals are scanned in LDS, then it rewrites its chunks as bases.
-  // Segments of up to SEG_REG chunks are held in registers between the two passes, so
-  // the rewrite issues no load after a store (the loads would wait for each store:
-  // hist is read and written through the same pointer).
-  constexpr int SEG_REG = 16;
-  __shared__ int32_t s_seg[1024];
-  const int nseg = E <= (int)blockDim.x ? (int)blockDim.x / E : 1;
+  // This workgroup's pairs (the loads go out first) and the rank masks.
+  const int64_t p = chunk * nt + tid;
+  int e_mine = -1;
+  if (p < M) {
+    const int64_t v = topk_idx[p];
+    if (v >= 0 && v < E) e_mine = (int)v;
+  }
+  for (int i = tid; i < waves * E; i += nt) s_mask[i] = 0ull;
+
+  // Column sums of hist: before this chunk, and over all chunks.
+  constexpr int UNR = 8;
+  const int nseg = E <= nt ? nt / E : 1;
   const int64_t L = (n_chunks + nseg - 1) / nseg;
-  for (int base_e = 0; base_e < E; base_e += (int)blockDim.x / nseg) {
+  for (int base_e = 0; base_e < E; base_e += nt / nseg) {
     const int e = base_e + tid / nseg, seg = tid % nseg;
-    const bool own = tid / nseg < (int)blockDim.x / nseg && e < E;
-    const int64_t c0 = seg * L, c1 = c0 + L < n_chunks ? c0 + L : n_chunks;
-    const bool in_reg = L <= SEG_REG;
-    int32_t buf[SEG_REG];
-    int32_t sum = 0;
+    const bool own = tid / nseg < nt / nseg && e < E;
+    int32_t before = 0, total = 0;
     if (own) {
-      if (in_reg) {
+      const int64_t c0 = seg * L, c1 = c0 + L < n_chunks ? c0 + L : n_chunks;
+      for (int64_t c = c0; c < c1; c += UNR) {
+        int32_t v[UNR];
 #pragma unroll
-        for (int i = 0; i < SEG_REG; ++i) buf[i] = c0 + i < c1 ? hist[(c0 + i) * E + e] : 0;
+        for (int u = 0; u < UNR; ++u) v[u] = c + u < c1 ? hist[(c + u) * E + e] : 0;
 #pragma unroll
-        for (int i = 0; i < SEG_REG; ++i) sum += buf[i];
-      } else {
-        for (int64_t c = c0; c < c1; ++c) sum += hist[c * E + e];
-      }
-    }
-    s_seg[tid] = own ? sum : 0;
-    __syncthreads();
-    if (own) {
-      int32_t run = 0;
-      for (int q = 0; q < seg; ++q) run += s_seg[tid - seg + q];
-      if (in_reg) {
-#pragma unroll
-        for (int i = 0; i < SEG_REG; ++i)
-          if (c0 + i < c1) {
-            hist[(c0 + i) * E + e] = run;
-            run += buf[i];
-          }
-      } else {
-        for (int64_t c = c0; c < c1; ++c) {
-          const int32_t v = hist[c * E + e];
-          hist[c * E + e] = run;
-          run += v;
+        for (int u = 0; u < UNR; ++u) {
+          total += v[u];
+          if (c + u < chunk) before += v[u];
         }
       }
-      if (seg == nseg - 1) {
-        s_cnt[e] = run;
-        counts[e] = run;
+    }
+    s_seg_b[tid] = before;
+    s_seg_t[tid] = total;
+    __syncthreads();
+    if (own && seg == 0) {
+      int32_t b = 0, t = 0;
+      for (int q = 0; q < nseg; ++q) {
+        b += s_seg_b[tid + q];
+        t += s_seg_t[tid + q];
       }
+      s_base[e] = b;
+      s_tot[e] = t;
     }
     __syncthreads();
   }
 
-  // Exclusive scan of the ALIGN_M-padded counts (E <= 1024: one pass per thread chunk).
-  const int per = (E + blockDim.x - 1) / blockDim.x;
+  // Exclusive scan of the padded totals (one run of `per` experts per thread).
+  const int per = (E + nt - 1) / nt;
   int32_t local = 0;
   const int e0 = tid * per;
   for (int i = 0; i < per; ++i) {
-    int e = e0 + i;
-    if (e < E) local += (s_cnt[e] + ALIGN_M - 1) / ALIGN_M * ALIGN_M;
+    const int e = e0 + i;
+    if (e < E) local += (s_tot[e] + ALIGN_M - 1) / ALIGN_M * ALIGN_M;
   }
-  // block-wide exclusive scan of `local`
-  const int lane = tid & 63, wave = tid >> 6;
   int32_t incl = local;
   for (int o = 1; o < 64; o <<= 1) {
-    int32_t v = __shfl_up(incl, o, 64);
+    const int32_t v = __shfl_up(incl, o, 64);
     if (lane >= o) incl += v;
   }
   if (lane == 63) s_wave[wave] = incl;
+  if (e_mine >= 0) atomicOr(&s_mask[wave * E + e_mine], 1ull << lane);
   __syncthreads();
   int32_t wave_base = 0;
   for (int w = 0; w < wave; ++w) wave_base += s_wave[w];
   int32_t run = wave_base + incl - local;
   for (int i = 0; i < per; ++i) {
-    int e = e0 + i;
+    const int e = e0 + i;
     if (e < E) {
       s_off[e] = run;
-      run += (s_cnt[e] + ALIGN_M - 1) / ALIGN_M * ALIGN_M;
+      run += (s_tot[e] + ALIGN_M - 1) / ALIGN_M * ALIGN_M;
     }
   }
-  if (tid == blockDim.x - 1) {
+  if (tid == nt - 1) {
     int32_t total = 0;
-    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) total += s_wave[w];
+    for (int w = 0; w < waves; ++w) total += s_wave[w];
     s_off[E] = total;
   }
   __syncthreads();
-  for (int e = tid; e <= E; e += blockDim.x) offs[e] = s_off[e];
-  const int32_t total = s_off[E];
-  if (tid == 0) npp[0] = total;
 
-  // Aligned block -> owning expert: the last expert whose run starts at or before it.
+  // Place this chunk's pairs: rank inside the expert = set bits below this lane in the
+  // wave's mask plus the same expert's bits in the waves before.
+  if (p < M) {
+    if (e_mine < 0) {
+      inv[p] = -1;
+    } else {
+      const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+      int rank = __popcll(s_mask[wave * E + e_mine] & below);
+      for (int w = 0; w < wave; ++w) rank += __popcll(s_mask[w * E + e_mine]);
+      const int32_t slot = s_off[e_mine] + s_base[e_mine] + rank;
+      sorted_ids[slot] = (int32_t)p;
+      inv[p] = slot;
+    }
+  }
+
+  const int32_t total = s_off[E];
+  const int64_t G = gridDim.x;
+  if (chunk == 0) {
+    for (int e = tid; e <= E; e += nt) offs[e] = s_off[e];
+    for (int e = tid; e < E; e += nt) counts[e] = s_tot[e];
+    if (tid == 0) npp[0] = total;
+  }
+  // Aligned block -> owning expert (the last expert whose run starts at or before it),
+  // workgroup-strided over the blocks.
   const int64_t n_blocks = l_cap / ALIGN_M;
-  for (int64_t b = tid; b < n_blocks; b += blockDim.x) {
+  for (int64_t b = chunk * nt + tid; b < n_blocks; b += G * nt) {
     int32_t owner = 0;
     const int64_t pos = b * ALIGN_M;
     if (pos < total) {
-      int lo = 0, hi = E - 1;  // largest e with s_off[e] <= pos
+      int lo = 0, hi = E - 1;
       while (lo < hi) {
-        int mid = (lo + hi + 1) >> 1;
+        const int mid = (lo + hi + 1) >> 1;
         if (s_off[mid] <= pos) lo = mid;
         else hi = mid - 1;
       }
@@ -166,44 +189,10 @@ dispatch_scan_kernel(int32_t* __restrict__ hist, int64_t n_chunks, int E, int64_
     }
     expert_ids[b] = owner;
   }
-
   // Sentinel M in every pad slot and in the unused tail [total, l_cap).
-  for (int e = tid; e < E; e += blockDim.x) {
-    for (int32_t s = s_off[e] + s_cnt[e]; s < s_off[e + 1]; ++s) sorted_ids[s] = (int32_t)M;
-  }
-  for (int64_t s = total + tid; s < l_cap; s += blockDim.x) sorted_ids[s] = (int32_t)M;
-}
-
-__global__ void __launch_bounds__(1024)
-dispatch_scatter_kernel(const int64_t* __restrict__ topk_idx, int64_t M, int E,
-                        const int32_t* __restrict__ chunk_base,
-                        const int32_t* __restrict__ offs, int32_t* __restrict__ sorted_ids,
-                        int32_t* __restrict__ inv) {
-  extern __shared__ unsigned long long s_mask[];  // [waves][E]
-  const int waves = blockDim.x >> 6;
-  for (int i = threadIdx.x; i < waves * E; i += blockDim.x) s_mask[i] = 0ull;
-  __syncthreads();
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  int e = -1;
-  if (p < M) {
-    int64_t v = topk_idx[p];
-    if (v >= 0 && v < E) e = (int)v;
-  }
-  if (e >= 0) atomicOr(&s_mask[wave * E + e], 1ull << lane);
-  __syncthreads();
-  if (p < M) {
-    if (e < 0) {
-      inv[p] = -1;
-      return;
-    }
-    const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    int rank = __popcll(s_mask[wave * E + e] & below);
-    for (int w = 0; w < wave; ++w) rank += __popcll(s_mask[w * E + e]);
-    const int32_t slot = offs[e] + chunk_base[(int64_t)blockIdx.x * E + e] + rank;
-    sorted_ids[slot] = (int32_t)p;
-    inv[p] = slot;
-  }
+  for (int64_t e = chunk * nt + tid; e < E; e += G * nt)
+    for (int32_t q = s_off[e] + s_tot[e]; q < s_off[e + 1]; ++q) sorted_ids[q] = (int32_t)M;
+  for (int64_t q = total + chunk * nt + tid; q < l_cap; q += G * nt) sorted_ids[q] = (int32_t)M;
 }
 
 }  // namespace nsmoe
@@ -259,13 +248,10 @@ extern "C" int nsmoe_dispatch(const int64_t* topk_idx, int64_t n_pairs, int32_t 
   dispatch_hist_kernel<<<(unsigned)n_chunks, chunk, n_experts * sizeof(int32_t), s>>>(
       topk_idx, n_pairs, n_experts, hist);
   NSMOE_TRY(check_launch("dispatch_hist_kernel"));
-  dispatch_scan_kernel<<<1, 1024, 0, s>>>(hist, n_chunks, n_experts, n_pairs, l_cap,
-                                          sorted_ids, expert_ids, pad_offsets, counts,
-                                          n_post_pad);
-  NSMOE_TRY(check_launch("dispatch_scan_kernel"));
-  dispatch_scatter_kernel<<<(unsigned)n_chunks, chunk,
-                            (chunk / 64) * n_experts * sizeof(unsigned long long), s>>>(
-      topk_idx, n_pairs, n_experts, hist, pad_offsets, sorted_ids, inv);
+  dispatch_place_kernel<<<(unsigned)n_chunks, chunk,
+                          (chunk / 64) * n_experts * sizeof(unsigned long long), s>>>(
+      topk_idx, n_pairs, n_experts, hist, n_chunks, l_cap, sorted_ids, expert_ids, pad_offsets,
+      counts, n_post_pad, inv);
   timer.stop();
-  return check_launch("dispatch_scatter_kernel");
+  return check_launch("dispatch_place_kernel");
 }

@@ -198,7 +198,10 @@ __global__ void __launch_bounds__(NT) expert_fwd_kernel(ExpParams p) {
 }
 
 // ============================ combine ====================================================
-// out[t] = sum_j rows[inv[t * k + j]] + sum_s rows[l_cap + s * T + t], fp32 accumulation.
+// out[t] = sum_j rows[inv[t * k + j]] + sum_s rows[l_cap + s * T + t], fp32 accumulation
+// in the order routed j = 0 .. k - 1, then shared s = 0 .. S - 1.
+constexpr int COMBINE_KMAX = 8;  // top_k and shared-expert counts of the gather fast path
+constexpr int COMBINE_SMAX = 2;
 template <int DT>
 __global__ void __launch_bounds__(NT)
 combine_kernel(const typename Elem<DT>::T* __restrict__ rows, const int32_t* __restrict__ inv,
@@ -206,7 +209,46 @@ combine_kernel(const typename Elem<DT>::T* __restrict__ rows, const int32_t* __r
                typename Elem<DT>::T* __restrict__ out, int fast) {
   using G = Geo<DT>;
   using TT = typename G::T;
-  if (fast) {
+  if (fast && k <= COMBINE_KMAX && S <= COMBINE_SMAX && ntok * (d / G::VE) < INT32_MAX) {
+    // Every slot index is loaded first, then every row chunk: all of a thread's loads
+    // are in flight together instead of one dependent pair per row.
+    const int vpr = d / G::VE;
+    const int n = (int)(ntok * vpr);
+    for (int i = blockIdx.x * NT + threadIdx.x; i < n; i += gridDim.x * NT) {
+      const int t = i / vpr;
+      const int c = (i - t * vpr) * G::VE;
+      int32_t sl[COMBINE_KMAX];
+#pragma unroll
+      for (int j = 0; j < COMBINE_KMAX; ++j) sl[j] = j < k ? inv[(int64_t)t * k + j] : -1;
+      u32x4 v[COMBINE_KMAX + COMBINE_SMAX];
+#pragma unroll
+      for (int j = 0; j < COMBINE_KMAX; ++j) {
+        v[j] = u32x4{0u, 0u, 0u, 0u};
+        if (sl[j] >= 0) v[j] = *(const u32x4*)(rows + (int64_t)sl[j] * d + c);
+      }
+#pragma unroll
+      for (int q = 0; q < COMBINE_SMAX; ++q) {
+        v[COMBINE_KMAX + q] = u32x4{0u, 0u, 0u, 0u};
+        if (q < S) v[COMBINE_KMAX + q] = *(const u32x4*)(rows + (l_cap + (int64_t)q * ntok + t) * d + c);
+      }
+      float acc[G::VE];
+#pragma unroll
+      for (int e = 0; e < G::VE; ++e) acc[e] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < COMBINE_KMAX + COMBINE_SMAX; ++j) {
+        TT tmp[G::VE];
+        __builtin_memcpy(tmp, &v[j], 16);
+#pragma unroll
+        for (int e = 0; e < G::VE; ++e) acc[e] += Elem<DT>::to_f(tmp[e]);
+      }
+      TT o[G::VE];
+#pragma unroll
+      for (int e = 0; e < G::VE; ++e) o[e] = Elem<DT>::from_f(acc[e]);
+      u32x4 ov;
+      __builtin_memcpy(&ov, o, 16);
+      *(u32x4*)(out + (int64_t)t * d + c) = ov;
+    }
+  } else if (fast) {
     const int vpr = d / G::VE;
     const int64_t n = ntok * vpr;
     for (int64_t i = (int64_t)blockIdx.x * NT + threadIdx.x; i < n; i += (int64_t)gridDim.x * NT) {

@@ -23,6 +23,8 @@ namespace nsmoe {
 constexpr int CDX_TOK = 64;   // tokens per combine_dx workgroup (16 per wave)
 constexpr int CDX_COLS = 64;  // columns of dx per combine_dx workgroup
 constexpr int CDX_PITCH = CDX_COLS + 4;  // fp32 LDS row pitch (4 banks of skew per row)
+constexpr int CDX_KMAX = 8;   // top_k and shared counts of the gather fast path
+constexpr int CDX_SMAX = 2;
 constexpr int RDW_RC = 256;   // tokens per router_dw chunk
 constexpr int RDW_BMT = 64;   // columns of x (rows of W) per router_dw tile
 constexpr int RDW_BNT = 128;  // experts per router_dw tile (all of them: E <= 128)
@@ -99,9 +101,7 @@ __global__ void __launch_bounds__(NT) combine_dx_kernel(CombineDxArgs a) {
     for (int e = 0; e < 4; ++e) sum[4 * q + e] = v[e];
   }
   const T* R = (const T*)a.rows;
-  auto add_row = [&](int64_t r) {
-    const u32x4* src = (const u32x4*)(R + r * a.d + c0);
-    const u32x4 v0 = src[0], v1 = src[1];
+  auto add = [&](const u32x4& v0, const u32x4& v1) __attribute__((always_inline)) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       sum[2 * e] += unpack2<DT>(v0[e], 0);
@@ -110,11 +110,37 @@ __global__ void __launch_bounds__(NT) combine_dx_kernel(CombineDxArgs a) {
       sum[8 + 2 * e + 1] += unpack2<DT>(v1[e], 1);
     }
   };
-  for (int j = 0; j < a.k; ++j) {
-    const int32_t s = a.inv[t * a.k + j];
-    if (s >= 0) add_row(s);
+  if (a.k <= CDX_KMAX && a.S <= CDX_SMAX) {
+    // Slot indices first, then every row's two chunks: all loads in flight together.
+    constexpr int NR = CDX_KMAX + CDX_SMAX;
+    int64_t r[NR];
+#pragma unroll
+    for (int j = 0; j < CDX_KMAX; ++j) r[j] = j < a.k ? (int64_t)a.inv[t * a.k + j] : -1;
+#pragma unroll
+    for (int q = 0; q < CDX_SMAX; ++q) r[CDX_KMAX + q] = q < a.S ? a.l_cap + (int64_t)q * a.T + t : -1;
+    u32x4 v[NR][2];
+#pragma unroll
+    for (int j = 0; j < NR; ++j) {
+      v[j][0] = v[j][1] = u32x4{0u, 0u, 0u, 0u};
+      if (r[j] >= 0) {
+        const u32x4* src = (const u32x4*)(R + r[j] * a.d + c0);
+        v[j][0] = src[0];
+        v[j][1] = src[1];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NR; ++j) add(v[j][0], v[j][1]);
+  } else {
+    auto add_row = [&](int64_t rr) {
+      const u32x4* src = (const u32x4*)(R + rr * a.d + c0);
+      add(src[0], src[1]);
+    };
+    for (int j = 0; j < a.k; ++j) {
+      const int32_t sj = a.inv[t * a.k + j];
+      if (sj >= 0) add_row(sj);
+    }
+    for (int sh = 0; sh < a.S; ++sh) add_row(a.l_cap + (int64_t)sh * a.T + t);
   }
-  for (int sh = 0; sh < a.S; ++sh) add_row(a.l_cap + (int64_t)sh * a.T + t);
   u32x4 o0, o1;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
