@@ -801,19 +801,18 @@ __device__ __forceinline__ void dw_reduce_group(const ExpParams& p, int g) {
   const float* src = p.partial + (int64_t)s_base * mn;
   const int64_t n4 = (mn % 4 == 0) ? mn / 4 : 0;  // 16-byte vectors (every partial is 16-B aligned)
   for (int64_t i = (int64_t)blockIdx.x * NT + threadIdx.x; i < n4; i += (int64_t)gridDim.x * NT) {
+    // Up to DEPTH chunks' loads in flight at once, added in chunk order.
+    constexpr int DEPTH = 16;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    int c = 0;
-    for (; c + 4 <= nch; c += 4) {
-      const f32x4 a0 = ((const f32x4*)(src + (int64_t)c * mn))[i];
-      const f32x4 a1 = ((const f32x4*)(src + (int64_t)(c + 1) * mn))[i];
-      const f32x4 a2 = ((const f32x4*)(src + (int64_t)(c + 2) * mn))[i];
-      const f32x4 a3 = ((const f32x4*)(src + (int64_t)(c + 3) * mn))[i];
-      acc += a0;
-      acc += a1;
-      acc += a2;
-      acc += a3;
+    for (int c0 = 0; c0 < nch; c0 += DEPTH) {
+      f32x4 a[DEPTH];
+#pragma unroll
+      for (int u = 0; u < DEPTH; ++u)
+        if (c0 + u < nch) a[u] = ((const f32x4*)(src + (int64_t)(c0 + u) * mn))[i];
+#pragma unroll
+      for (int u = 0; u < DEPTH; ++u)
+        if (c0 + u < nch) acc += a[u];
     }
-    for (; c < nch; ++c) acc += ((const f32x4*)(src + (int64_t)c * mn))[i];
 #pragma unroll
     for (int e = 0; e < 4; ++e) dst[i * 4 + e] = Elem<DT>::from_f(acc[e]);
   }

@@ -113,17 +113,18 @@ __global__ void __launch_bounds__(NT) combine_dx_kernel(CombineDxArgs a) {
   if (a.k <= CDX_KMAX && a.S <= CDX_SMAX) {
     // Slot indices first, then every row's two chunks: all loads in flight together.
     constexpr int NR = CDX_KMAX + CDX_SMAX;
-    int64_t r[NR];
+    int32_t r[NR];  // row indices (the launcher checks that they fit 31 bits)
 #pragma unroll
-    for (int j = 0; j < CDX_KMAX; ++j) r[j] = j < a.k ? (int64_t)a.inv[t * a.k + j] : -1;
+    for (int j = 0; j < CDX_KMAX; ++j) r[j] = j < a.k ? a.inv[t * a.k + j] : -1;
 #pragma unroll
-    for (int q = 0; q < CDX_SMAX; ++q) r[CDX_KMAX + q] = q < a.S ? a.l_cap + (int64_t)q * a.T + t : -1;
+    for (int q = 0; q < CDX_SMAX; ++q)
+      r[CDX_KMAX + q] = q < a.S ? (int32_t)(a.l_cap + (int64_t)q * a.T + t) : -1;
     u32x4 v[NR][2];
 #pragma unroll
     for (int j = 0; j < NR; ++j) {
       v[j][0] = v[j][1] = u32x4{0u, 0u, 0u, 0u};
       if (r[j] >= 0) {
-        const u32x4* src = (const u32x4*)(R + r[j] * a.d + c0);
+        const u32x4* src = (const u32x4*)(R + (int64_t)r[j] * a.d + c0);
         v[j][0] = src[0];
         v[j][1] = src[1];
       }
@@ -318,6 +319,8 @@ int combine_dx_launch(int dtype, const CombineDxArgs& a, hipStream_t s) {
   NSMOE_REQUIRE(router_grad_supported(dtype, a.d, a.E) && a.ep == router_logits_pitch(a.E),
                 "combine_dx: unsupported shape (d %d, E %d, pitch %d)", a.d, a.E, a.ep);
   if (a.T == 0) return NSMOE_OK;
+  NSMOE_REQUIRE(a.l_cap + (int64_t)a.S * a.T < INT32_MAX, "combine_dx: %lld rows exceed 2^31",
+                (long long)(a.l_cap + (int64_t)a.S * a.T));
   const dim3 grid((unsigned)cdiv(a.T, CDX_TOK), (unsigned)cdiv(a.d, CDX_COLS));
   KernelTimer timer("combine_dx", s);
   if (dtype == DT_BF16) combine_dx_kernel<DT_BF16><<<grid, NT, 0, s>>>(a);
