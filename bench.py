@@ -148,14 +148,20 @@ def time_gpu(m, x, g, steps: int, warmup: int):
 
 # bench.py kernel name -> the symbol prefix of the HIP kernel(s) it times.
 KERNEL_SYMBOLS = {
-    "expert_fwd": ("nsmoe::expert_fwd_async_kernel", "nsmoe::expert_fwd_kernel"),
-    "expert_bwd": ("nsmoe::expert_bwd_async_kernel", "nsmoe::expert_bwd_kernel"),
-    "expert_dx": ("nsmoe::expert_dx_async_kernel",),
+    "expert_fwd": ("nsmoe::expert_fwd_reg_kernel", "nsmoe::expert_fwd_async_kernel",
+                   "nsmoe::expert_fwd_kernel"),
+    "expert_bwd": ("nsmoe::expert_bwd_reg_kernel", "nsmoe::expert_bwd_async_kernel",
+                   "nsmoe::expert_bwd_kernel"),
+    "expert_dx": ("nsmoe::expert_dx_reg_kernel", "nsmoe::expert_dx_async_kernel"),
     "dw": ("nsmoe::dw_pair_kernel",),
     "dw_in": ("nsmoe::dw_async_kernel<0, 0", "nsmoe::dw_kernel<0, 0"),
     "dw_out": ("nsmoe::dw_async_kernel<0, 1", "nsmoe::dw_kernel<0, 1"),
     "route_fwd": ("nsmoe::route_fwd_kernel",),
     "combine": ("nsmoe::combine_kernel",),
+    "combine_dx": ("nsmoe::combine_dx_kernel",),
+    "pack": ("nsmoe::pack_kernel",),
+    "dispatch": ("nsmoe::dispatch_hist_kernel", "nsmoe::dispatch_place_kernel"),
+    "router_dw": ("nsmoe::router_dw_kernel", "nsmoe::router_dw_reduce_kernel"),
 }
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                             "hbm_traffic_T8192.md")

@@ -39,7 +39,7 @@ def test_traffic_table_scales_by_the_copy(tmp_path, monkeypatch):
 
 
 def test_committed_traffic_table_has_the_expert_kernels():
-    for k in ("expert_fwd", "expert_bwd", "expert_dx", "dw_in", "dw_out", "combine"):
+    for k in ("expert_fwd", "expert_bwd", "expert_dx", "dw", "combine", "route_fwd"):
         assert bench.committed_traffic(k) > 0, k
 
 
