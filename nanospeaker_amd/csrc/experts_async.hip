@@ -260,16 +260,17 @@ __global__ void __launch_bounds__(NT, 2) expert_fwd_async_kernel(ExpParams p) {
 // unconditional (out-of-range fragments read a zero page), so the compiler's own waits
 // for the weight registers are exact or stricter and leave the next step's loads in flight.
 // Shapes: d % 64 == 0 (an even number of GEMM1 steps) and an even number of GEMM2 steps.
-template <int DT, int NBW, int MB>
-__global__ void __launch_bounds__(NT, MB == 6 ? 3 : 2) expert_fwd_reg_kernel(ExpParams p) {
+template <int DT, int NBW, int MB, int D>
+__global__ void __launch_bounds__(NT, MB == 6 || D == 3 ? 3 : 2) expert_fwd_reg_kernel(ExpParams p) {
   using G = Geo<DT>;
   using T = typename G::T;
   using M = Mma<DT>;
   using Frag = typename M::Frag;
   static_assert(G::ES == 2, "16-bit types only");
   static_assert(MB == 4 || MB == 6, "64- or 96-row tiles");
+  static_assert(D == 2 || D == 3, "prefetch distance");
   constexpr int TM = MB * 16;            // tile rows
-  constexpr int S = 3;                   // token-tile ring stages
+  constexpr int S = D + 1;               // token-tile ring stages
   constexpr int XC = MB == 4 ? 1 : 2;    // token copies per wave per step
   constexpr bool STAGE_Y = MB == 4;
   constexpr int HPMAX = 64 * NBW;
@@ -342,8 +343,9 @@ __global__ void __launch_bounds__(NT, MB == 6 ? 3 : 2) expert_fwd_reg_kernel(Exp
   // rows' tokens are looked up.  The gate weights are loaded before the token copies are
   // issued and reach LDS after GEMM1 (GEMM2's epilogue reads them), so waiting for them
   // never waits for a copy.
-  WSet wa = load_w1(0);
-  WSet wb = load_w1(1);
+  WSet wset[D];
+#pragma unroll
+  for (int j = 0; j < D; ++j) wset[j] = load_w1(j);
   const bool routed = g < p.E;
   int pair = -1;
   if (tid < TM) {
@@ -414,27 +416,32 @@ __global__ void __launch_bounds__(NT, MB == 6 ? 3 : 2) expert_fwd_reg_kernel(Exp
     }
   };
 
-  issue_x(0);
-  issue_x(1);
-  wait_vmcnt<XC>();  // the gate weights and step 0's copies; step 1's stay in flight
+#pragma unroll
+  for (int j = 0; j < D; ++j) issue_x(j);
+  // Every prologue load but step D - 1's copies.  The steady-state count below assumes
+  // that step s's copies are followed only by the loads of steps s + 1 .. s + D - 1 in
+  // issue order; the prologue issues all D weight sets ahead of the copies, so for steps
+  // below D - 1 that holds only once their copies are already complete.
+  wait_vmcnt<XC>();
   int s = 0;
-  for (; s + 2 < nk1; s += 2) {  // steady state: the steps two ahead are GEMM1 steps
-    wait_vmcnt<NB1 + XC>();
-    g1mma(s, wa);
-    wa = load_w1(s + 2);
-    issue_x(s + 2);
-    wait_vmcnt<NB1 + XC>();
-    g1mma(s + 1, wb);
-    wb = load_w1(s + 3);
-    issue_x(s + 3);
+  for (; s + D < nk1; s += D) {  // steady state: the steps D ahead are GEMM1 steps
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      wait_vmcnt<(D - 1) * (NB1 + XC)>();  // step s + j's weights and copies have landed
+      g1mma(s + j, wset[j]);
+      wset[j] = load_w1(s + j + D);
+      issue_x(s + j + D);
+    }
   }
-  // The last two GEMM1 steps prefetch GEMM2's first two weight sets.
-  wait_vmcnt<NB1 + XC>();
-  g1mma(s, wa);
-  wa = load_w2(0);
-  wait_vmcnt<NB2>();
-  g1mma(s + 1, wb);
-  wb = load_w2(1);
+  // The last D GEMM1 steps prefetch GEMM2's first D weight sets: before step s + j, the
+  // GEMM1 loads of steps s + j + 1 .. s + D - 1 and the GEMM2 sets 0 .. j - 1 may be
+  // outstanding.
+#pragma unroll
+  for (int j = 0; j < D; ++j) {
+    wait_vmcnt_dyn((D - 1 - j) * (NB1 + XC) + j * NB2);  // a constant once unrolled
+    g1mma(s + j, wset[j]);
+    wset[j] = load_w2(j);
+  }
 
   if (tid < TM) s_w[tid] = gate_w;  // published by the barrier after the epilogue
   // ---- GEMM1 epilogue: bias, h = act(gate) * up -> LDS --------------------------------------
@@ -599,14 +606,15 @@ __global__ void __launch_bounds__(NT, MB == 6 ? 3 : 2) expert_fwd_reg_kernel(Exp
     }
   };
   int q = 0;
-  for (; q + 2 < n2; q += 2) {
-    g2step(q, wa);
-    wa = load_w2(q + 2);
-    g2step(q + 1, wb);
-    wb = load_w2(q + 3);
+  for (; q + D < n2; q += D) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      g2step(q + j, wset[j]);
+      wset[j] = load_w2(q + j + D);
+    }
   }
-  g2step(q, wa);
-  g2step(q + 1, wb);
+#pragma unroll
+  for (int j = 0; j < D; ++j) g2step(q + j, wset[j]);
   wait_vmcnt<0>();  // nothing may be in flight when the workgroup retires
 }
 
@@ -919,14 +927,15 @@ __global__ void __launch_bounds__(NT, 2) expert_dx_async_kernel(ExpParams p) {
 // of a steady step are unconditional (zero page for fragments past the edge).
 // Shapes: an even number of k-steps.
 
-template <int DT, int NBW>
+template <int DT, int NBW, int D>
 __global__ void __launch_bounds__(NT, 2) expert_bwd_reg_kernel(ExpParams p) {
   using G = Geo<DT>;
   using T = typename G::T;
   using M = Mma<DT>;
   using Frag = typename M::Frag;
   static_assert(G::ES == 2, "16-bit types only");
-  constexpr int S = 3;
+  static_assert(D == 2 || D == 3, "prefetch distance");
+  constexpr int S = D + 1;
   constexpr int HPMAX = 64 * NBW;
   constexpr int A_BYTES = BM * G::ROWB;  // one token tile (x or dout): 4 KiB
   constexpr int NBF = 3 * NBW;           // gate, up and G fragments per wave per step
@@ -980,7 +989,9 @@ __global__ void __launch_bounds__(NT, 2) expert_bwd_reg_kernel(ExpParams p) {
     }
     return w;
   };
-  WSet wa = load_w(0), wb = load_w(1);
+  WSet wset[D];
+#pragma unroll
+  for (int j = 0; j < D; ++j) wset[j] = load_w(j);
 
   if (tid < BM) {
     int tok = -1, pair = -1;
@@ -1003,8 +1014,8 @@ __global__ void __launch_bounds__(NT, 2) expert_bwd_reg_kernel(ExpParams p) {
     async_copy16(xrow ? (const void*)(xrow + k0) : (const void*)zero, st + wave * 1024);
     async_copy16(drow ? (const void*)(drow + k0) : (const void*)zero, st + A_BYTES + wave * 1024);
   };
-  issue_x(0);
-  issue_x(1);
+#pragma unroll
+  for (int j = 0; j < D; ++j) issue_x(j);
 
   f32x4 accg[4][NBW], accu[4][NBW], accG[4][NBW];
 #pragma unroll
@@ -1027,29 +1038,26 @@ __global__ void __launch_bounds__(NT, 2) expert_bwd_reg_kernel(ExpParams p) {
       }
     }
   };
-  wait_vmcnt<2>();  // prologue order: w(0) w(1) [row lookups] x(0) d(0) x(1) d(1)
-  mma(0, wa);
-  wa = load_w(2);
-  issue_x(2);
-  wait_vmcnt<SLOT>();
-  mma(1, wb);
-  wb = load_w(3);
-  issue_x(3);
-  int s = 2;
-  for (; s + 2 < nk; s += 2) {
-    wait_vmcnt<SLOT>();
-    mma(s, wa);
-    wa = load_w(s + 2);
-    issue_x(s + 2);
-    wait_vmcnt<SLOT>();
-    mma(s + 1, wb);
-    wb = load_w(s + 3);
-    issue_x(s + 3);
+  // Prologue order: w(0) .. w(D - 1) [row lookups] x(0) d(0) .. x(D - 1) d(D - 1).  Every
+  // prologue load but step D - 1's two copies: the steady-state count below assumes that
+  // step s's copies are followed only by the loads of steps s + 1 .. s + D - 1, which
+  // holds for the prologue steps below D - 1 only once their copies are complete.
+  wait_vmcnt<2>();
+  int s = 0;
+  for (; s + D < nk; s += D) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      wait_vmcnt<(D - 1) * SLOT>();  // step s + j's weights and copies have landed
+      mma(s + j, wset[j]);
+      wset[j] = load_w(s + j + D);
+      issue_x(s + j + D);
+    }
   }
-  wait_vmcnt<SLOT>();
-  mma(s, wa);
-  wait_vmcnt<0>();
-  mma(s + 1, wb);
+#pragma unroll
+  for (int j = 0; j < D; ++j) {
+    wait_vmcnt_dyn((D - 1 - j) * SLOT);  // a constant once unrolled
+    mma(s + j, wset[j]);
+  }
   wait_lgkm0();
   barrier_dma();  // every wave is done with the ring: the staging may overwrite it
 
@@ -1146,29 +1154,77 @@ __global__ void __launch_bounds__(NT, 2) expert_bwd_reg_kernel(ExpParams p) {
   }
 }
 
-template <int DT>
-__global__ void __launch_bounds__(NT, 2) expert_dx_reg_kernel(ExpParams p) {
+// Rows of a wave's 48-column slice of one 192-column pass, straight from the MFMA
+// accumulators (acc[i][j]: row block i, column block j; lane (lc, lg) holds columns
+// 4 lg .. 4 lg + 3 of row lc in each).  Blocks 0 and 1 are regrouped across lanes (two
+// permlane swaps per dword) so that lane (lc, lg) holds columns cw + 8 lg .. + 7 of its
+// row and stores them with one 16-byte store; block 2 leaves in 8-byte stores.
+// permlane32_swap(b0, b1) gives rows (b0.r0, b0.r1, b1.r0, b1.r1) and (b0.r2, b0.r3, b1.r2,
+// b1.r3); permlane16_swap of those gives (b0.r0, b0.r2, b1.r0, b1.r2) and (b0.r1, b0.r3,
+// b1.r1, b1.r3).  cw is wave-uniform; columns at or past d are not written.
+template <int DT, int MB>
+__device__ __forceinline__ void store_rows_direct(const f32x4 (&acc)[MB][3],
+                                                  typename Elem<DT>::T* Y, int d, int rows,
+                                                  int cw, int lc, int lg) {
+  using T = typename Elem<DT>::T;
+#pragma unroll
+  for (int i = 0; i < MB; ++i) {
+    const int m = i * 16 + lc;
+    uint32_t lo[3], hi[3];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      lo[j] = pack2<DT>(acc[i][j][0], acc[i][j][1]);
+      hi[j] = pack2<DT>(acc[i][j][2], acc[i][j][3]);
+    }
+    T* yrow = Y + (int64_t)m * d;
+    if (cw + 32 <= d) {
+      const auto l32 = __builtin_amdgcn_permlane32_swap(lo[0], lo[1], false, false);
+      const auto h32 = __builtin_amdgcn_permlane32_swap(hi[0], hi[1], false, false);
+      const auto l16 = __builtin_amdgcn_permlane16_swap(l32[0], l32[1], false, false);
+      const auto h16 = __builtin_amdgcn_permlane16_swap(h32[0], h32[1], false, false);
+      if (m < rows) {
+        u32x4 v;
+        v[0] = l16[0];
+        v[1] = h16[0];
+        v[2] = l16[1];
+        v[3] = h16[1];
+        *(u32x4*)(yrow + cw + lg * 8) = v;
+        if (cw + 32 < d) *(uint2*)(yrow + cw + 32 + lg * 4) = make_uint2(lo[2], hi[2]);
+      }
+    } else if (cw < d && m < rows) {
+      *(uint2*)(yrow + cw + lg * 4) = make_uint2(lo[0], hi[0]);
+    }
+  }
+}
+
+template <int DT, int D, int MB>
+__global__ void __launch_bounds__(NT, D > 2 || MB == 6 ? 3 : 2) expert_dx_reg_kernel(ExpParams p) {
   using G = Geo<DT>;
   using T = typename G::T;
   using M = Mma<DT>;
   using Frag = typename M::Frag;
   static_assert(G::ES == 2, "16-bit types only");
-  constexpr int S = 3;
-  constexpr int A_BYTES = BM * G::ROWB;
+  static_assert(D >= 2 && D <= 4, "prefetch distance");
+  static_assert(MB == 4 || MB == 6, "64- or 96-row tiles");
+  constexpr int TM = MB * 16;            // tile rows
+  constexpr int XC = MB == 4 ? 1 : 2;    // dA1 copies per wave per step
+  constexpr bool STAGE_Y = MB == 4;      // 64-row tiles stage each pass of dX rows in LDS
+  constexpr int S = D + 1;
+  constexpr int A_BYTES = TM * G::ROWB;
   constexpr int NBF = 3;
-  constexpr int SLOT = NBF + 1;
+  constexpr int SLOT = NBF + XC;
   constexpr int Y_PITCH = NP2 * G::ES + 16;
   __shared__ __attribute__((aligned(1024))) char s_ring[S][A_BYTES];
-  __shared__ __attribute__((aligned(16))) char s_y[BM * Y_PITCH];
+  __shared__ __attribute__((aligned(16))) char s_y[STAGE_Y ? TM * Y_PITCH : 16];
   __shared__ int s_loc[3];
 
   const int tile = tile_of_block(p);
   Located loc;
-  if (!locate(tile, p.E + p.S, [&](int g) { return (rows_of(p, g) + BM - 1) / BM; },
+  if (!locate(tile, p.E + p.S, [&](int g) { return (rows_of(p, g) + TM - 1) / TM; },
               [](int) { return 0; }, s_loc, loc))
     return;
-  const int g = loc.g, m0 = loc.local * BM;
-  const int rows = min(BM, rows_of(p, g) - m0);
+  const int g = loc.g, m0 = loc.local * TM;
+  const int rows = min(TM, rows_of(p, g) - m0);
   const int64_t slot0 = row_start(p, g) + m0;
   const int tid = threadIdx.x, lane = tid & 63, lc = lane & 15, lg = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1193,41 +1249,61 @@ __global__ void __launch_bounds__(NT, 2) expert_dx_reg_kernel(ExpParams p) {
     }
     return w;
   };
+  // dA1 copies: copy slot c (16 bytes) holds chunk (c % 4) ^ swz(r) of row r = c / 4.  The
+  // first copy of wave w fills slots 256 w / 4 ... = tid; for 96 rows the second fills
+  // slots 256 + 32 w + lane (lanes < 32), rows 64 + 8 w + lane / 4.
   const int ar = tid >> 2, ac = (tid & 3) ^ swz<DT>(ar);
   const T* arow = ar < rows ? (const T*)p.da1 + (slot0 + ar) * twoH + ac * G::VE : nullptr;
+  const T* arow2 = nullptr;
+  if constexpr (XC == 2) {
+    const int r2 = 64 + wave * 8 + (lane >> 2);
+    const int ac2 = (lane & 3) ^ swz<DT>(r2);
+    if (lane < 32 && r2 < rows) arow2 = (const T*)p.da1 + (slot0 + r2) * twoH + ac2 * G::VE;
+  }
   auto issue_x = [&](int s) __attribute__((always_inline)) {
     const int k0 = (s % nkk) * G::KC;
     async_copy16(arow ? (const void*)(arow + k0) : (const void*)zero, s_ring[s % S] + wave * 1024);
+    if constexpr (XC == 2) {
+      if (lane < 32)
+        async_copy16(arow2 ? (const void*)(arow2 + k0) : (const void*)zero,
+                     s_ring[s % S] + 4096 + wave * 512);
+    }
   };
-  WSet wa = load_w(0);
-  issue_x(0);
-  WSet wb = load_w(1);
-  issue_x(1);
+  // Step s's weights and copies are issued together, D steps ahead of its MFMAs.
+  WSet wset[D];
+#pragma unroll
+  for (int j = 0; j < D; ++j) {
+    wset[j] = load_w(j);
+    issue_x(j);
+  }
 
   T* DX = (T*)p.dxrow + slot0 * d;
-  f32x4 acc[4][3];
+  f32x4 acc[MB][3];
   auto step = [&](int s, const WSet& w) __attribute__((always_inline)) {
     const int pass = s / nkk, kk = s - pass * nkk;
     if (kk == 0) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < MB; ++i)
 #pragma unroll
         for (int j = 0; j < 3; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
     barrier_dma();
     const char* st = s_ring[s % S];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < MB; ++i) {
       const Frag af = frag_sw<DT>(st, i * 16);
 #pragma unroll
       for (int j = 0; j < 3; ++j) M::run(acc[i][j], w.f[j], af);
     }
-    if (kk == nkk - 1) {  // the pass's 192 columns: staged, then whole row segments out
+    if constexpr (!STAGE_Y) {
+      if (kk == nkk - 1) store_rows_direct<DT, MB>(acc, DX, d, rows, pass * NP2 + wave * 48,
+                                                    lc, lg);
+    } else if (kk == nkk - 1) {  // the pass's 192 columns: staged, then whole row segments out
 #pragma unroll
       for (int j = 0; j < 3; ++j) {
         const int c0 = (wave * 3 + j) * 16 + lg * 4;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < MB; ++i) {
           const int m = i * 16 + lc;
           *(uint2*)(s_y + m * Y_PITCH + c0 * G::ES) =
               make_uint2(pack2<DT>(acc[i][j][0], acc[i][j][1]),
@@ -1239,7 +1315,7 @@ __global__ void __launch_bounds__(NT, 2) expert_dx_reg_kernel(ExpParams p) {
       const int ncols = min(NP2, d - pass * NP2);
       constexpr int CPR = NP2 / G::VE;
 #pragma unroll
-      for (int u = 0; u < BM * CPR / NT; ++u) {
+      for (int u = 0; u < TM * CPR / NT; ++u) {
         const int c = tid + u * NT, m = c / CPR, cc = c % CPR;
         if (m < rows && cc * G::VE < ncols)
           *(u32x4*)(DX + (int64_t)m * d + pass * NP2 + cc * G::VE) =
@@ -1250,21 +1326,49 @@ __global__ void __launch_bounds__(NT, 2) expert_dx_reg_kernel(ExpParams p) {
     }
   };
   int s = 0;
-  for (; s + 2 < nsteps; s += 2) {
-    wait_vmcnt<SLOT>();
-    step(s, wa);
-    wa = load_w(s + 2);
-    issue_x(s + 2);
-    wait_vmcnt<SLOT>();
-    step(s + 1, wb);
-    wb = load_w(s + 3);
-    issue_x(s + 3);
+  for (; s + D < nsteps; s += D) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      wait_vmcnt<(D - 1) * SLOT>();  // only steps s + j + 1 .. s + j + D - 1 in flight
+      step(s + j, wset[j]);
+      wset[j] = load_w(s + j + D);
+      issue_x(s + j + D);
+    }
   }
-  wait_vmcnt<SLOT>();
-  step(s, wa);
+#pragma unroll
+  for (int j = 0; j < D; ++j) {
+    wait_vmcnt_dyn((D - 1 - j) * SLOT);  // a constant once unrolled
+    step(s + j, wset[j]);
+  }
   wait_vmcnt<0>();
-  step(s + 1, wb);
-  wait_vmcnt<0>();
+}
+
+static int device_cus();
+static int64_t tile_grid(const ExpParams& p, int bm);
+
+template <int DT>
+static void bwd_reg_launch(const ExpParams& p, int nbw, int dist, unsigned grid, hipStream_t s) {
+  if (dist == 3) {
+    if (nbw == 1) expert_bwd_reg_kernel<DT, 1, 3><<<grid, NT, 0, s>>>(p);
+    else expert_bwd_reg_kernel<DT, 2, 3><<<grid, NT, 0, s>>>(p);
+  } else {
+    if (nbw == 1) expert_bwd_reg_kernel<DT, 1, 2><<<grid, NT, 0, s>>>(p);
+    else expert_bwd_reg_kernel<DT, 2, 2><<<grid, NT, 0, s>>>(p);
+  }
+}
+
+template <int DT>
+static void dx_reg_launch(const ExpParams& p, int mb, int dist, hipStream_t s) {
+  const unsigned g4 = (unsigned)tile_grid(p, 64), g6 = (unsigned)tile_grid(p, 96);
+  if (mb == 6) {
+    if (dist == 4) expert_dx_reg_kernel<DT, 4, 6><<<g6, NT, 0, s>>>(p);
+    else if (dist == 3) expert_dx_reg_kernel<DT, 3, 6><<<g6, NT, 0, s>>>(p);
+    else expert_dx_reg_kernel<DT, 2, 6><<<g6, NT, 0, s>>>(p);
+  } else {
+    if (dist == 4) expert_dx_reg_kernel<DT, 4, 4><<<g4, NT, 0, s>>>(p);
+    else if (dist == 3) expert_dx_reg_kernel<DT, 3, 4><<<g4, NT, 0, s>>>(p);
+    else expert_dx_reg_kernel<DT, 2, 4><<<g4, NT, 0, s>>>(p);
+  }
 }
 
 int launch_bwd_async(int dtype, const ExpParams& p, int nbw, int64_t grid, hipStream_t s) {
@@ -1274,20 +1378,36 @@ int launch_bwd_async(int dtype, const ExpParams& p, int nbw, int64_t grid, hipSt
   const int nsteps_dx = ((p.d + NP2 - 1) / NP2) * (2 * p.H / 32);
   if (reg && p.d % 64 == 0 && (2 * p.H) % 32 == 0 && nsteps_dx % 2 == 0 && p.in_kb >= 4) {
     {
-      KernelTimer timer("expert_bwd", s);
-      if (dtype == DT_BF16) {
-        if (nbw == 1) expert_bwd_reg_kernel<DT_BF16, 1><<<(unsigned)grid, NT, 0, s>>>(p);
-        else expert_bwd_reg_kernel<DT_BF16, 2><<<(unsigned)grid, NT, 0, s>>>(p);
-      } else {
-        if (nbw == 1) expert_bwd_reg_kernel<DT_F16, 1><<<(unsigned)grid, NT, 0, s>>>(p);
-        else expert_bwd_reg_kernel<DT_F16, 2><<<(unsigned)grid, NT, 0, s>>>(p);
+      // Weight prefetch distance 3 steps where the step count divides by 3, else 2;
+      // NSMOE_BWD_D = 2 or 3 forces one (read on every call, for tests).
+      int dist = p.in_kb % 3 == 0 ? 3 : 2;
+      if (const char* e = getenv("NSMOE_BWD_D")) {
+        const int v = atoi(e);
+        if (v == 2 || (v == 3 && p.in_kb % 3 == 0)) dist = v;
       }
+      KernelTimer timer("expert_bwd", s);
+      if (dtype == DT_BF16) bwd_reg_launch<DT_BF16>(p, nbw, dist, (unsigned)grid, s);
+      else bwd_reg_launch<DT_F16>(p, nbw, dist, (unsigned)grid, s);
       timer.stop();
       NSMOE_TRY(check_launch("expert_bwd_reg_kernel"));
     }
+    // 96-row tiles once 64-row tiles overflow the resident workgroup slots (3 per CU), as
+    // in the forward; weight prefetch distance 2 steps.  NSMOE_DX_MB = 4 or 6 and
+    // NSMOE_DX_D = 2, 3 or 4 force a tile height and a distance (read on every call, for
+    // tests).
+    int mb = tile_grid(p, 64) > 3 * (int64_t)device_cus() ? 6 : 4;
+    if (const char* e = getenv("NSMOE_DX_MB")) {
+      const int v = atoi(e);
+      if (v == 4 || v == 6) mb = v;
+    }
+    int dist = 2;
+    if (const char* e = getenv("NSMOE_DX_D")) {
+      const int v = atoi(e);
+      if (v >= 2 && v <= 4 && nsteps_dx % v == 0) dist = v;
+    }
     KernelTimer timer("expert_dx", s);
-    if (dtype == DT_BF16) expert_dx_reg_kernel<DT_BF16><<<(unsigned)grid, NT, 0, s>>>(p);
-    else expert_dx_reg_kernel<DT_F16><<<(unsigned)grid, NT, 0, s>>>(p);
+    if (dtype == DT_BF16) dx_reg_launch<DT_BF16>(p, mb, dist, s);
+    else dx_reg_launch<DT_F16>(p, mb, dist, s);
     timer.stop();
     return check_launch("expert_dx_reg_kernel");
   }
@@ -1600,9 +1720,14 @@ static int64_t tile_grid(const ExpParams& p, int bm) {
 }
 
 template <int DT, int NBW>
-static void fwd_reg_launch(const ExpParams& p, int mb, hipStream_t s) {
-  if (mb == 6) expert_fwd_reg_kernel<DT, NBW, 6><<<(unsigned)tile_grid(p, 96), NT, 0, s>>>(p);
-  else expert_fwd_reg_kernel<DT, NBW, 4><<<(unsigned)tile_grid(p, 64), NT, 0, s>>>(p);
+static void fwd_reg_launch(const ExpParams& p, int mb, int dist, hipStream_t s) {
+  if (dist == 3) {
+    if (mb == 6) expert_fwd_reg_kernel<DT, NBW, 6, 3><<<(unsigned)tile_grid(p, 96), NT, 0, s>>>(p);
+    else expert_fwd_reg_kernel<DT, NBW, 4, 3><<<(unsigned)tile_grid(p, 64), NT, 0, s>>>(p);
+  } else {
+    if (mb == 6) expert_fwd_reg_kernel<DT, NBW, 6, 2><<<(unsigned)tile_grid(p, 96), NT, 0, s>>>(p);
+    else expert_fwd_reg_kernel<DT, NBW, 4, 2><<<(unsigned)tile_grid(p, 64), NT, 0, s>>>(p);
+  }
 }
 
 int launch_fwd_async(int dtype, const ExpParams& p, int nbw, int64_t grid, hipStream_t s) {
@@ -1620,12 +1745,20 @@ int launch_fwd_async(int dtype, const ExpParams& p, int nbw, int64_t grid, hipSt
       const int v = atoi(e);
       if (v == 4 || v == 6) mb = v;
     }
+    // Prefetch distance: 3 steps where both GEMMs' step counts are multiples of 3;
+    // NSMOE_FWD_D = 2 or 3 forces one (read on every call, for tests).
+    const int nk1 = p.in_kb;
+    int dist = 2;
+    if (const char* e = getenv("NSMOE_FWD_D")) {
+      if (atoi(e) == 3) dist = 3;
+    }
+    if (dist == 3 && (nk1 % 3 != 0 || n2 % 3 != 0)) dist = 2;
     if (dtype == DT_BF16) {
-      if (nbw == 1) fwd_reg_launch<DT_BF16, 1>(p, mb, s);
-      else fwd_reg_launch<DT_BF16, 2>(p, mb, s);
+      if (nbw == 1) fwd_reg_launch<DT_BF16, 1>(p, mb, dist, s);
+      else fwd_reg_launch<DT_BF16, 2>(p, mb, dist, s);
     } else {
-      if (nbw == 1) fwd_reg_launch<DT_F16, 1>(p, mb, s);
-      else fwd_reg_launch<DT_F16, 2>(p, mb, s);
+      if (nbw == 1) fwd_reg_launch<DT_F16, 1>(p, mb, dist, s);
+      else fwd_reg_launch<DT_F16, 2>(p, mb, dist, s);
     }
     timer.stop();
     return check_launch("expert_fwd_reg_kernel");
