@@ -131,14 +131,24 @@ extern "C" int nsmoe_block_fwd(const nsmoe_experts_args* a, const void* logits,
   // In training the route kernel also leaves the balance loss's per-workgroup column
   // sums of probs in the workspace, so probs is not read back for the loss.
   float* colsum = probs ? (float*)(ws + dsp + exp) : nullptr;
-  NSMOE_TRY(route_fwd_launch(logits, T, E, k, route_flags, a->dtype, (void*)b.topk_w, topk_idx,
-                             probs, colsum, (hipStream_t)stream));
-  NSMOE_TRY(nsmoe_dispatch(topk_idx, m, E, (int32_t*)b.sorted_ids,
-                           (int32_t*)(sv + L.off[NSMOE_SAVED_EXPERT_IDS]),
-                           (int32_t*)b.pad_offsets, (int32_t*)b.counts,
-                           (int32_t*)(sv + L.off[NSMOE_SAVED_N_POST_PAD]), inv, ws, dsp, stream));
-  NSMOE_TRY(nsmoe_pack_weights(&b, (void*)b.w_in_packed, (void*)b.w_out_packed, stream));
-  NSMOE_TRY(nsmoe_experts_fwd(&b, inv, out, ws + dsp, exp, stream));
+  // The weight packing does not depend on the routing: it runs on the side stream while
+  // the (latency-bound) route and dispatch kernels run on the caller's stream.
+  hipStream_t s = (hipStream_t)stream;
+  hipStream_t s_pack = side_fork(s, kSideSlotPack);
+  const int prc = nsmoe_pack_weights(&b, (void*)b.w_in_packed, (void*)b.w_out_packed, s_pack);
+  int rc = prc;
+  if (rc == NSMOE_OK)
+    rc = route_fwd_launch(logits, T, E, k, route_flags, a->dtype, (void*)b.topk_w, topk_idx,
+                          probs, colsum, s);
+  if (rc == NSMOE_OK)
+    rc = nsmoe_dispatch(topk_idx, m, E, (int32_t*)b.sorted_ids,
+                        (int32_t*)(sv + L.off[NSMOE_SAVED_EXPERT_IDS]), (int32_t*)b.pad_offsets,
+                        (int32_t*)b.counts, (int32_t*)(sv + L.off[NSMOE_SAVED_N_POST_PAD]), inv,
+                        ws, dsp, s);
+  const int jrc = side_join(s, s_pack, kSideSlotPack);  // joined on every path
+  NSMOE_TRY(rc);
+  NSMOE_TRY(jrc);
+  NSMOE_TRY(nsmoe_experts_fwd(&b, inv, out, ws + dsp, exp, s));
   if (probs)
     NSMOE_TRY(balance_final_launch(colsum, T, E, b.counts, aux_coef, aux, (hipStream_t)stream));
   return NSMOE_OK;
@@ -167,6 +177,14 @@ static BwdWs bwd_ws(const nsmoe_experts_args* b, bool router) {
   return w;
 }
 
+}  // namespace nsmoe
+
+namespace nsmoe {
+int block_bwd_router(const nsmoe_experts_args* a, const nsmoe_experts_args& b,
+                     const BlockLayout& L, char* sv, const void* logits, int32_t route_flags,
+                     float aux_coef, const float* grad_aux, const nsmoe_experts_grads* grads,
+                     const void* w_router, void* grad_w_router, void* grad_logits, char* ws,
+                     const BwdWs& W, const int32_t* inv, bool fuse, hipStream_t s);
 }  // namespace nsmoe
 
 extern "C" size_t nsmoe_block_bwd_workspace_size(const nsmoe_experts_args* a,
@@ -205,7 +223,25 @@ extern "C" int nsmoe_block_bwd(const nsmoe_experts_args* a, const void* logits,
   const int32_t* inv = (const int32_t*)(sv + L.off[NSMOE_SAVED_INV]);
   nsmoe_experts_grads g = *grads;
   g.dtopk_w = ws + W.tw;  // the gate gradient stays internal: it feeds the router backward
-  NSMOE_TRY(experts_bwd_launch(&b, inv, grad_out, &g, ws + W.exp, W.gl - W.exp, !fuse, s));
+  // dW runs on the side stream beside everything below; joined before returning.
+  hipStream_t s_dw = s;
+  NSMOE_TRY(experts_bwd_launch(&b, inv, grad_out, &g, ws + W.exp, W.gl - W.exp, !fuse, s, &s_dw));
+  const int rc = block_bwd_router(a, b, L, sv, logits, route_flags, aux_coef, grad_aux, grads,
+                                  w_router, grad_w_router, grad_logits, ws, W, inv, fuse, s);
+  const int jrc = side_join(s, s_dw, kSideSlotDw);
+  NSMOE_TRY(rc);
+  return jrc;
+}
+
+namespace nsmoe {
+
+// The router's part of the block backward, after the experts' (block.hip's
+// nsmoe_block_bwd): d(logits) from the gate gradient, then dx and W_router's gradient.
+int block_bwd_router(const nsmoe_experts_args* a, const nsmoe_experts_args& b,
+                     const BlockLayout& L, char* sv, const void* logits, int32_t route_flags,
+                     float aux_coef, const float* grad_aux, const nsmoe_experts_grads* grads,
+                     const void* w_router, void* grad_w_router, void* grad_logits, char* ws,
+                     const BwdWs& W, const int32_t* inv, bool fuse, hipStream_t s) {
   const bool probs = route_flags & NSMOE_ROUTE_PROBS;
   const void* src = probs ? (const void*)(sv + L.off[NSMOE_SAVED_PROBS]) : logits;
   NSMOE_REQUIRE(src, "block_bwd: NULL logits (eval branch)");
@@ -242,3 +278,5 @@ extern "C" int nsmoe_block_bwd(const nsmoe_experts_args* a, const void* logits,
   r.ep = ldg;
   return router_dw_launch(a->dtype, r, s);
 }
+
+}  // namespace nsmoe

@@ -1,5 +1,6 @@
 // C-ABI housekeeping: the thread-local error string, the launch counter and small
 // utility kernels shared by the entry points in route.hip, dispatch.hip and experts.hip.
+#include <stdlib.h>
 #include <string.h>
 
 #include <mutex>
@@ -33,6 +34,84 @@ int fill_i32(int32_t* dst, int64_t n, int32_t value, hipStream_t stream) {
   if (blocks > 1024) blocks = 1024;
   fill_i32_kernel<<<(unsigned)blocks, 256, 0, stream>>>(dst, n, value);
   return check_launch("fill_i32_kernel");
+}
+
+// ---- side stream -------------------------------------------------------------------------
+//
+// Per host thread and device: one extra stream (default priority, non-blocking) and a
+// fork and a join event per slot, all created on first use.  side_fork makes the side
+// stream wait for the work already enqueued on `s` and returns it; side_join makes `s`
+// wait for everything enqueued on the side stream since.  Both are event-ordered, so the
+// pattern is also what a HIP graph capture of `s` records (the side stream joins the
+// capture at the fork and leaves it at the join).  Measured on MI355X under ROCm 7, a
+// replayed graph gains nothing from the fork (its branches are not overlapped) and pays
+// for the extra nodes, so work enqueued while `s` is being captured stays on `s`; so does
+// everything in a process with NSMOE_SINGLE_STREAM set.
+constexpr int kSideSlots = 4;
+constexpr int kMaxDevices = 64;
+
+struct SideState {
+  hipStream_t stream = nullptr;
+  hipEvent_t fork[kSideSlots] = {};
+  hipEvent_t join[kSideSlots] = {};
+  bool failed = false;
+};
+
+static thread_local SideState g_side[kMaxDevices];
+
+static bool side_init(SideState& st, hipStream_t s) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+    return false;  // captured work stays on s
+  if (st.stream) return true;
+  if (st.failed) return false;
+  bool ok = hipStreamCreateWithFlags(&st.stream, hipStreamNonBlocking) == hipSuccess;
+  for (int i = 0; ok && i < kSideSlots; ++i)
+    ok = hipEventCreateWithFlags(&st.fork[i], hipEventDisableTiming) == hipSuccess &&
+         hipEventCreateWithFlags(&st.join[i], hipEventDisableTiming) == hipSuccess;
+  if (!ok) {
+    for (int i = 0; i < kSideSlots; ++i) {
+      if (st.fork[i]) hipEventDestroy(st.fork[i]);
+      if (st.join[i]) hipEventDestroy(st.join[i]);
+      st.fork[i] = st.join[i] = nullptr;
+    }
+    if (st.stream) hipStreamDestroy(st.stream);
+    st.stream = nullptr;
+    st.failed = true;
+    (void)hipGetLastError();
+  }
+  return ok;
+}
+
+hipStream_t side_fork(hipStream_t s, int slot) {
+  if (getenv("NSMOE_SINGLE_STREAM") || slot < 0 || slot >= kSideSlots) return s;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return s;
+  SideState& st = g_side[dev];
+  if (!side_init(st, s)) return s;
+  if (hipEventRecord(st.fork[slot], s) != hipSuccess ||
+      hipStreamWaitEvent(st.stream, st.fork[slot], 0) != hipSuccess) {
+    (void)hipGetLastError();
+    return s;
+  }
+  return st.stream;
+}
+
+int side_join(hipStream_t s, hipStream_t side, int slot) {
+  if (side == s) return NSMOE_OK;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("side_join: no current device");
+    return NSMOE_EHIP;
+  }
+  SideState& st = g_side[dev];
+  hipError_t e = hipEventRecord(st.join[slot], side);
+  if (e == hipSuccess) e = hipStreamWaitEvent(s, st.join[slot], 0);
+  if (e != hipSuccess) {
+    set_error("side_join: %s", hipGetErrorString(e));
+    return NSMOE_EHIP;
+  }
+  return NSMOE_OK;
 }
 
 // ---- kernel timing ----------------------------------------------------------------------

@@ -1032,38 +1032,13 @@ static BwdLayout bwd_layout(const nsmoe_experts_args* a) {
   return L;
 }
 
-// combine = false leaves the per-row dX in the workspace (bwd_layout(a).dxrow) for the
-// caller to reduce, and gr->dx is not written.
+// dW_in / dW_out (and the bias gradients) of every group from the backward's dA1 and w h
+// rows, on stream s.
 template <int DT>
-static int experts_bwd_impl(const nsmoe_experts_args* a, const int32_t* inv, const void* dout,
-                            const nsmoe_experts_grads* gr, char* ws, bool combine,
-                            hipStream_t s) {
-  const BwdLayout L = bwd_layout(a);
-  ExpParams p = make_params(a);
-  const int nbw = nbw_for(a);
-  const int64_t grid = fwd_grid(a);
+static int experts_dw(const nsmoe_experts_args* a, const ExpParams& p,
+                      const nsmoe_experts_grads* gr, char* ws, const BwdLayout& L,
+                      hipStream_t s) {
   const int G = a->n_experts + a->n_shared;
-  p.dout = dout;
-  p.da1 = ws + L.da1;
-  p.hbuf = ws + L.hbuf;
-  p.dxrow = ws + L.dxrow;
-  p.dtw = gr->dtopk_w;
-  p.fast = p.fast && aligned16(dout);
-  const int arc = launch_bwd_async(DT, p, nbw, grid, s);
-  if (arc != -1) {
-    NSMOE_TRY(arc);
-  } else if (grid > 0) {
-    KernelTimer timer("expert_bwd", s);
-    if (nbw == 1) expert_bwd_kernel<DT, 1><<<(unsigned)grid, NT, 0, s>>>(p);
-    else if (nbw == 2) expert_bwd_kernel<DT, 2><<<(unsigned)grid, NT, 0, s>>>(p);
-    else if constexpr (DT != DT_F32) expert_bwd_kernel<DT, 4><<<(unsigned)grid, NT, 0, s>>>(p);
-    timer.stop();
-    NSMOE_TRY(check_launch("expert_bwd_kernel"));
-  }
-  if (combine)
-    NSMOE_TRY(launch_combine<DT>(ws + L.dxrow, inv, a->n_tokens, a->d_model, a->top_k,
-                                 a->n_shared, a->l_cap, gr->dx, p.fast && aligned16(gr->dx), s));
-
   const int d = a->d_model, H = a->d_hidden;
   const int64_t gc = dw_groups_chunks(a);
   ExpParams q_in = p, q_out = p;
@@ -1132,6 +1107,51 @@ static int experts_bwd_impl(const nsmoe_experts_args* a, const int32_t* inv, con
   return NSMOE_OK;
 }
 
+// combine = false leaves the per-row dX in the workspace (bwd_layout(a).dxrow) for the
+// caller to reduce, and gr->dx is not written.  dW runs on the calling thread's side stream
+// (forked after the GLU backward) beside the dX rows on s; with side_out the caller gets
+// that stream and must join it (side_join(s, *side_out, kSideSlotDw)), else it is joined
+// here.
+template <int DT>
+static int experts_bwd_impl(const nsmoe_experts_args* a, const int32_t* inv, const void* dout,
+                            const nsmoe_experts_grads* gr, char* ws, bool combine,
+                            hipStream_t s, hipStream_t* side_out) {
+  const BwdLayout L = bwd_layout(a);
+  ExpParams p = make_params(a);
+  const int nbw = nbw_for(a);
+  const int64_t grid = fwd_grid(a);
+  p.dout = dout;
+  p.da1 = ws + L.da1;
+  p.hbuf = ws + L.hbuf;
+  p.dxrow = ws + L.dxrow;
+  p.dtw = gr->dtopk_w;
+  p.fast = p.fast && aligned16(dout);
+  const int arc = launch_bwd_async(DT, p, nbw, grid, 0, s);
+  if (arc != -1) {
+    NSMOE_TRY(arc);
+  } else if (grid > 0) {
+    KernelTimer timer("expert_bwd", s);
+    if (nbw == 1) expert_bwd_kernel<DT, 1><<<(unsigned)grid, NT, 0, s>>>(p);
+    else if (nbw == 2) expert_bwd_kernel<DT, 2><<<(unsigned)grid, NT, 0, s>>>(p);
+    else if constexpr (DT != DT_F32) expert_bwd_kernel<DT, 4><<<(unsigned)grid, NT, 0, s>>>(p);
+    timer.stop();
+    NSMOE_TRY(check_launch("expert_bwd_kernel"));
+  }
+  hipStream_t s2 = side_fork(s, kSideSlotDw);
+  int rc = experts_dw<DT>(a, p, gr, ws, L, s2);
+  if (rc == NSMOE_OK && arc != -1) rc = launch_bwd_async(DT, p, nbw, grid, 1, s);
+  if (rc == NSMOE_OK && combine)
+    rc = launch_combine<DT>(ws + L.dxrow, inv, a->n_tokens, a->d_model, a->top_k, a->n_shared,
+                            a->l_cap, gr->dx, p.fast && aligned16(gr->dx), s);
+  if (rc == NSMOE_OK && side_out) {
+    *side_out = s2;
+    return NSMOE_OK;
+  }
+  const int jrc = side_join(s, s2, kSideSlotDw);  // joined on every other path
+  NSMOE_TRY(rc);
+  return jrc;
+}
+
 }  // namespace nsmoe
 
 using namespace nsmoe;
@@ -1171,7 +1191,8 @@ namespace nsmoe {
 
 int experts_bwd_launch(const nsmoe_experts_args* a, const int32_t* inv, const void* grad_out,
                        const nsmoe_experts_grads* grads, void* workspace,
-                       size_t workspace_bytes, bool combine, hipStream_t s) {
+                       size_t workspace_bytes, bool combine, hipStream_t s,
+                       hipStream_t* side_out) {
   NSMOE_TRY(validate(a));
   NSMOE_REQUIRE(grads, "experts_bwd: NULL grads");
   if (a->n_tokens == 0) return NSMOE_OK;
@@ -1189,11 +1210,14 @@ int experts_bwd_launch(const nsmoe_experts_args* a, const int32_t* inv, const vo
   }
   switch (a->dtype) {
     case DT_BF16:
-      return experts_bwd_impl<DT_BF16>(a, inv, grad_out, grads, (char*)workspace, combine, s);
+      return experts_bwd_impl<DT_BF16>(a, inv, grad_out, grads, (char*)workspace, combine, s,
+                                       side_out);
     case DT_F16:
-      return experts_bwd_impl<DT_F16>(a, inv, grad_out, grads, (char*)workspace, combine, s);
+      return experts_bwd_impl<DT_F16>(a, inv, grad_out, grads, (char*)workspace, combine, s,
+                                       side_out);
     default:
-      return experts_bwd_impl<DT_F32>(a, inv, grad_out, grads, (char*)workspace, combine, s);
+      return experts_bwd_impl<DT_F32>(a, inv, grad_out, grads, (char*)workspace, combine, s,
+                                       side_out);
   }
 }
 
@@ -1205,7 +1229,7 @@ extern "C" int nsmoe_experts_bwd(const nsmoe_experts_args* a, const int32_t* inv
                                  const void* grad_out, const nsmoe_experts_grads* grads,
                                  void* workspace, size_t workspace_bytes, void* stream) {
   return experts_bwd_launch(a, inv, grad_out, grads, workspace, workspace_bytes, true,
-                            (hipStream_t)stream);
+                            (hipStream_t)stream, nullptr);
 }
 
 extern "C" int nsmoe_pack_sizes(const nsmoe_experts_args* a, size_t* w_in_bytes,

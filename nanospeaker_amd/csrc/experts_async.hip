@@ -1371,13 +1371,14 @@ static void dx_reg_launch(const ExpParams& p, int mb, int dist, hipStream_t s) {
   }
 }
 
-int launch_bwd_async(int dtype, const ExpParams& p, int nbw, int64_t grid, hipStream_t s) {
+int launch_bwd_async(int dtype, const ExpParams& p, int nbw, int64_t grid, int part,
+                     hipStream_t s) {
   if (!p.fast || nbw > 2 || (dtype != DT_BF16 && dtype != DT_F16)) return -1;
   if (grid <= 0) return NSMOE_OK;
   static const bool reg = getenv("NSMOE_BWD_LDSW") == nullptr;
   const int nsteps_dx = ((p.d + NP2 - 1) / NP2) * (2 * p.H / 32);
   if (reg && p.d % 64 == 0 && (2 * p.H) % 32 == 0 && nsteps_dx % 2 == 0 && p.in_kb >= 4) {
-    {
+    if (part == 0) {
       // Weight prefetch distance 3 steps where the step count divides by 3, else 2;
       // NSMOE_BWD_D = 2 or 3 forces one (read on every call, for tests).
       int dist = p.in_kb % 3 == 0 ? 3 : 2;
@@ -1389,7 +1390,7 @@ int launch_bwd_async(int dtype, const ExpParams& p, int nbw, int64_t grid, hipSt
       if (dtype == DT_BF16) bwd_reg_launch<DT_BF16>(p, nbw, dist, (unsigned)grid, s);
       else bwd_reg_launch<DT_F16>(p, nbw, dist, (unsigned)grid, s);
       timer.stop();
-      NSMOE_TRY(check_launch("expert_bwd_reg_kernel"));
+      return check_launch("expert_bwd_reg_kernel");
     }
     // 96-row tiles once 64-row tiles overflow the resident workgroup slots (3 per CU), as
     // in the forward; weight prefetch distance 2 steps.  NSMOE_DX_MB = 4 or 6 and
@@ -1411,7 +1412,7 @@ int launch_bwd_async(int dtype, const ExpParams& p, int nbw, int64_t grid, hipSt
     timer.stop();
     return check_launch("expert_dx_reg_kernel");
   }
-  {
+  if (part == 0) {
     constexpr int S = 2;
     KernelTimer timer("expert_bwd", s);
     if (dtype == DT_BF16) {
@@ -1422,17 +1423,14 @@ int launch_bwd_async(int dtype, const ExpParams& p, int nbw, int64_t grid, hipSt
       else expert_bwd_async_kernel<DT_F16, 2, S><<<(unsigned)grid, NT, 0, s>>>(p);
     }
     timer.stop();
-    NSMOE_TRY(check_launch("expert_bwd_async_kernel"));
+    return check_launch("expert_bwd_async_kernel");
   }
-  {
-    constexpr int S = 3;
-    KernelTimer timer("expert_dx", s);
-    if (dtype == DT_BF16) expert_dx_async_kernel<DT_BF16, S><<<(unsigned)grid, NT, 0, s>>>(p);
-    else expert_dx_async_kernel<DT_F16, S><<<(unsigned)grid, NT, 0, s>>>(p);
-    timer.stop();
-    NSMOE_TRY(check_launch("expert_dx_async_kernel"));
-  }
-  return NSMOE_OK;
+  constexpr int S = 3;
+  KernelTimer timer("expert_dx", s);
+  if (dtype == DT_BF16) expert_dx_async_kernel<DT_BF16, S><<<(unsigned)grid, NT, 0, s>>>(p);
+  else expert_dx_async_kernel<DT_F16, S><<<(unsigned)grid, NT, 0, s>>>(p);
+  timer.stop();
+  return check_launch("expert_dx_async_kernel");
 }
 
 // ============================ backward: dW ===============================================

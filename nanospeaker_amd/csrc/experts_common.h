@@ -127,8 +127,10 @@ int launch_dw_async(int dtype, int mode, const ExpParams& q, int64_t groups_chun
 // Both dW modes in one launch (q_in: dW_in, q_out: dW_out pointers and partials).
 int launch_dw_pair_async(int dtype, const ExpParams& q_in, const ExpParams& q_out,
                          int64_t groups_chunks, hipStream_t s);
-// Backward tiles (GLU backward) and dX rows; fills p.da1, p.hbuf, p.dxrow and p.dtw.
-int launch_bwd_async(int dtype, const ExpParams& p, int nbw, int64_t grid, hipStream_t s);
+// Backward tiles: part 0 the GLU backward (fills p.da1, p.hbuf and p.dtw), part 1 the dX
+// rows from p.da1 (fills p.dxrow).  Both parts take or refuse the same shapes.
+int launch_bwd_async(int dtype, const ExpParams& p, int nbw, int64_t grid, int part,
+                     hipStream_t s);
 
 }  // namespace nsmoe
 
@@ -138,8 +140,12 @@ struct nsmoe_experts_grads;
 namespace nsmoe {
 // nsmoe_experts_bwd; with combine = false the per-row dX stay in the workspace at
 // experts_bwd_dxrows_offset(a) (rows as the forward's row space) and grads->dx is unused.
+// The dW stage runs on the side stream (side_fork slot kSideSlotDw); with side_out != NULL
+// a successful call leaves that stream in *side_out for the caller to join with
+// side_join(stream, *side_out, kSideSlotDw), otherwise it is joined before returning.
 int experts_bwd_launch(const ::nsmoe_experts_args* a, const int32_t* inv, const void* grad_out,
                        const ::nsmoe_experts_grads* grads, void* workspace,
-                       size_t workspace_bytes, bool combine, hipStream_t stream);
+                       size_t workspace_bytes, bool combine, hipStream_t stream,
+                       hipStream_t* side_out);
 size_t experts_bwd_dxrows_offset(const ::nsmoe_experts_args* a);
 }  // namespace nsmoe

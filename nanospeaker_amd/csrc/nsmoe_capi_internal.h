@@ -47,6 +47,16 @@ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
   } while (0)
 
 namespace nsmoe {
+// Fork/join onto the calling thread's side stream for the current device (capi.hip).
+// side_fork returns the side stream, ordered after the work already on `s`, or `s` itself
+// when no side stream is available; side_join orders `s` after the side stream's work
+// (a no-op when side == s).  Slots 0 .. 3 each own a fork and a join event.
+hipStream_t side_fork(hipStream_t s, int slot);
+int side_join(hipStream_t s, hipStream_t side, int slot);
+// Slots in use: the block forward's weight packing and the experts backward's dW.
+constexpr int kSideSlotPack = 0;
+constexpr int kSideSlotDw = 1;
+
 // dst[0, n) = value, as a kernel (graph-capture safe, unlike hipMemsetAsync).
 int fill_i32(int32_t* dst, int64_t n, int32_t value, hipStream_t stream);
 }  // namespace nsmoe

@@ -97,3 +97,26 @@ def test_forward_replays_equal_eager():
         ref = m(x)
         for r, v in enumerate(got):
             assert torch.equal(v, ref), f"replay {r}"
+
+
+def test_side_stream_matches_single_stream(monkeypatch):
+    """The library runs the weight packing and the dW stage on a second stream (forked
+    and joined with events); with NSMOE_SINGLE_STREAM set everything stays on the caller's
+    stream.  Both orders must give the same bits, step after step."""
+    m, x, g = _block(8192, seed=2)
+    params = list(m.parameters())
+    one = torch.ones((), dtype=torch.float32, device=DEV)
+
+    def step():
+        xg = x.detach().requires_grad_(True)
+        out = m(xg)
+        grads = torch.autograd.grad([out, m.aux_loss], [xg] + params, [g, one])
+        return [out.detach(), m.aux_loss.detach()] + list(grads)
+
+    two = [step() for _ in range(2)]
+    monkeypatch.setenv("NSMOE_SINGLE_STREAM", "1")
+    single = step()
+    torch.cuda.synchronize()
+    for r, vals in enumerate(two):
+        for i, (a, b) in enumerate(zip(vals, single)):
+            assert torch.equal(a, b), f"step {r}: tensor {i}"
