@@ -116,22 +116,40 @@ def time_gpu(m, x, g, steps: int, warmup: int):
         step()
     torch.cuda.synchronize()
 
-    # fwd + bwd, timed
-    nat.timing_enable(64 * steps + 64)
-    torch.cuda.synchronize()
+    # fwd + bwd, timed, as the library issues it (eager calls overlap the weight pack and
+    # the dW stage with the rest on a second stream)
     t0 = time.perf_counter()
     for _ in range(steps):
         step()
     host_ms = (time.perf_counter() - t0) * 1e3 / steps   # enqueue time, before the wait
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / steps
-    kernels = {}
-    for name in ("route_fwd", "dispatch", "pack", "expert_fwd", "combine", "expert_bwd",
-                 "expert_dx", "dw_in", "dw_out", "dw", "combine_dx", "router_dw"):
-        tot, n = nat.timing_read(name)
-        if n:
-            kernels[name] = (tot / n, n // steps)
-    nat.timing_enable(0)
+
+    # Per-kernel launch times, from the library's HIP-event pairs on the launch stream, in a
+    # pass of its own on one stream, so that no other kernel shares the GPU with the one
+    # being timed.
+    prev = os.environ.get("NSMOE_SINGLE_STREAM")
+    os.environ["NSMOE_SINGLE_STREAM"] = "1"
+    try:
+        step()
+        torch.cuda.synchronize()
+        nat.timing_enable(64 * steps + 64)
+        torch.cuda.synchronize()
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        kernels = {}
+        for name in ("route_fwd", "dispatch", "pack", "expert_fwd", "combine", "expert_bwd",
+                     "expert_dx", "dw_in", "dw_out", "dw", "combine_dx", "router_dw"):
+            tot, n = nat.timing_read(name)
+            if n:
+                kernels[name] = (tot / n, n // steps)
+        nat.timing_enable(0)
+    finally:
+        if prev is None:
+            del os.environ["NSMOE_SINGLE_STREAM"]
+        else:
+            os.environ["NSMOE_SINGLE_STREAM"] = prev
 
     # forward only (train mode, no autograd)
     with torch.no_grad():
