@@ -140,18 +140,17 @@ extern "C" int nsmoe_block_fwd(const nsmoe_experts_args* a, const void* logits,
   if (rc == NSMOE_OK)
     rc = route_fwd_launch(logits, T, E, k, route_flags, a->dtype, (void*)b.topk_w, topk_idx,
                           probs, colsum, s);
+  // In training the balance loss is one more workgroup of the dispatch's second launch.
+  BalanceArgs fold{colsum, balance_partial_count(T), T, aux_coef, aux};
   if (rc == NSMOE_OK)
-    rc = nsmoe_dispatch(topk_idx, m, E, (int32_t*)b.sorted_ids,
-                        (int32_t*)(sv + L.off[NSMOE_SAVED_EXPERT_IDS]), (int32_t*)b.pad_offsets,
-                        (int32_t*)b.counts, (int32_t*)(sv + L.off[NSMOE_SAVED_N_POST_PAD]), inv,
-                        ws, dsp, s);
+    rc = dispatch_launch(topk_idx, m, E, (int32_t*)b.sorted_ids,
+                         (int32_t*)(sv + L.off[NSMOE_SAVED_EXPERT_IDS]), (int32_t*)b.pad_offsets,
+                         (int32_t*)b.counts, (int32_t*)(sv + L.off[NSMOE_SAVED_N_POST_PAD]), inv,
+                         ws, dsp, probs ? &fold : nullptr, s);
   const int jrc = side_join(s, s_pack, kSideSlotPack);  // joined on every path
   NSMOE_TRY(rc);
   NSMOE_TRY(jrc);
-  NSMOE_TRY(nsmoe_experts_fwd(&b, inv, out, ws + dsp, exp, s));
-  if (probs)
-    NSMOE_TRY(balance_final_launch(colsum, T, E, b.counts, aux_coef, aux, (hipStream_t)stream));
-  return NSMOE_OK;
+  return nsmoe_experts_fwd(&b, inv, out, ws + dsp, exp, s);
 }
 
 namespace nsmoe {

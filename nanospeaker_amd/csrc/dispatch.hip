@@ -21,6 +21,10 @@
 //               popcount(mask & lanes-below) plus the popcounts of the same expert's
 //               masks of the waves before it -- and places them; the block -> expert map
 //               and the sentinels are split over the workgroups.
+//   With the block's balance loss folded in, the place launch has one more workgroup: it
+//   forms the experts' totals the same way and reduces the router's column-sum partials
+//   to the loss (balance.h) while the others place their chunks.
+#include "balance.h"
 #include "nsmoe_capi_internal.h"
 #include "nsmoe_common.h"
 
@@ -61,13 +65,16 @@ dispatch_place_kernel(const int64_t* __restrict__ topk_idx, int64_t M, int E,
                       const int32_t* __restrict__ hist, int64_t n_chunks, int64_t l_cap,
                       int32_t* __restrict__ sorted_ids, int32_t* __restrict__ expert_ids,
                       int32_t* __restrict__ offs, int32_t* __restrict__ counts,
-                      int32_t* __restrict__ npp, int32_t* __restrict__ inv) {
+                      int32_t* __restrict__ npp, int32_t* __restrict__ inv,
+                      const float* __restrict__ bal_partial, int64_t bal_nblk, int64_t bal_T,
+                      float bal_coef, float* __restrict__ bal_aux) {
   extern __shared__ unsigned long long s_mask[];  // [waves][E]
   __shared__ int32_t s_base[DISPATCH_MAX_EXPERTS];
   __shared__ int32_t s_tot[DISPATCH_MAX_EXPERTS];
   __shared__ int32_t s_off[DISPATCH_MAX_EXPERTS + 1];
   __shared__ int32_t s_seg_b[1024], s_seg_t[1024];
   __shared__ int32_t s_wave[16];
+  __shared__ BalanceLds s_bal;
   const int tid = threadIdx.x, nt = blockDim.x;
   const int lane = tid & 63, wave = tid >> 6, waves = nt >> 6;
   const int64_t chunk = blockIdx.x;
@@ -115,6 +122,10 @@ dispatch_place_kernel(const int64_t* __restrict__ topk_idx, int64_t M, int E,
       s_tot[e] = t;
     }
     __syncthreads();
+  }
+  if (chunk == n_chunks) {  // the balance-loss workgroup (uniform): totals -> loss
+    balance_loss_block(bal_partial, bal_nblk, s_tot, bal_T, E, bal_coef, bal_aux, s_bal);
+    return;
   }
 
   // Exclusive scan of the padded totals (one run of `per` experts per thread).
@@ -166,7 +177,7 @@ dispatch_place_kernel(const int64_t* __restrict__ topk_idx, int64_t M, int E,
   }
 
   const int32_t total = s_off[E];
-  const int64_t G = gridDim.x;
+  const int64_t G = n_chunks;  // the placing workgroups
   if (chunk == 0) {
     for (int e = tid; e <= E; e += nt) offs[e] = s_off[e];
     for (int e = tid; e < E; e += nt) counts[e] = s_tot[e];
@@ -214,10 +225,12 @@ extern "C" size_t nsmoe_dispatch_workspace_size(int64_t n_pairs, int32_t n_exper
   return (size_t)cdiv(n_pairs, dispatch_chunk(n_experts)) * (size_t)n_experts * sizeof(int32_t);
 }
 
-extern "C" int nsmoe_dispatch(const int64_t* topk_idx, int64_t n_pairs, int32_t n_experts,
-                              int32_t* sorted_ids, int32_t* expert_ids, int32_t* pad_offsets,
-                              int32_t* counts, int32_t* n_post_pad, int32_t* inv,
-                              void* workspace, size_t workspace_bytes, void* stream) {
+namespace nsmoe {
+
+int dispatch_launch(const int64_t* topk_idx, int64_t n_pairs, int32_t n_experts,
+                    int32_t* sorted_ids, int32_t* expert_ids, int32_t* pad_offsets,
+                    int32_t* counts, int32_t* n_post_pad, int32_t* inv, void* workspace,
+                    size_t workspace_bytes, const BalanceArgs* bal, void* stream) {
   NSMOE_REQUIRE(n_pairs >= 0 && n_pairs < (int64_t)INT32_MAX / 2,
                 "dispatch: n_pairs %lld out of range", (long long)n_pairs);
   NSMOE_REQUIRE(n_experts >= 1 && n_experts <= DISPATCH_MAX_EXPERTS,
@@ -230,8 +243,13 @@ extern "C" int nsmoe_dispatch(const int64_t* topk_idx, int64_t n_pairs, int32_t 
     NSMOE_REQUIRE(pad_offsets && counts && n_post_pad, "dispatch: NULL pointer");
     NSMOE_TRY(fill_i32(pad_offsets, n_experts + 1, 0, s));
     NSMOE_TRY(fill_i32(counts, n_experts, 0, s));
-    return fill_i32(n_post_pad, 1, 0, s);
+    NSMOE_TRY(fill_i32(n_post_pad, 1, 0, s));
+    return bal ? balance_final_launch(bal->partial, bal->T, n_experts, counts, bal->coef,
+                                      bal->aux, s)
+               : NSMOE_OK;
   }
+  NSMOE_REQUIRE(!bal || (n_experts <= 128 && bal->partial && bal->aux),
+                "dispatch: the folded balance loss takes E <= 128 and its buffers");
   NSMOE_REQUIRE(topk_idx && sorted_ids && expert_ids && pad_offsets && counts && n_post_pad &&
                     inv && workspace, "dispatch: NULL pointer");
   const size_t need = nsmoe_dispatch_workspace_size(n_pairs, n_experts);
@@ -248,10 +266,22 @@ extern "C" int nsmoe_dispatch(const int64_t* topk_idx, int64_t n_pairs, int32_t 
   dispatch_hist_kernel<<<(unsigned)n_chunks, chunk, n_experts * sizeof(int32_t), s>>>(
       topk_idx, n_pairs, n_experts, hist);
   NSMOE_TRY(check_launch("dispatch_hist_kernel"));
-  dispatch_place_kernel<<<(unsigned)n_chunks, chunk,
+  const bool fold = bal != nullptr;
+  dispatch_place_kernel<<<(unsigned)(n_chunks + (fold ? 1 : 0)), chunk,
                           (chunk / 64) * n_experts * sizeof(unsigned long long), s>>>(
       topk_idx, n_pairs, n_experts, hist, n_chunks, l_cap, sorted_ids, expert_ids, pad_offsets,
-      counts, n_post_pad, inv);
+      counts, n_post_pad, inv, fold ? bal->partial : nullptr, fold ? bal->nblk : 0,
+      fold ? bal->T : 1, fold ? bal->coef : 0.0f, fold ? bal->aux : nullptr);
   timer.stop();
   return check_launch("dispatch_place_kernel");
+}
+
+}  // namespace nsmoe
+
+extern "C" int nsmoe_dispatch(const int64_t* topk_idx, int64_t n_pairs, int32_t n_experts,
+                              int32_t* sorted_ids, int32_t* expert_ids, int32_t* pad_offsets,
+                              int32_t* counts, int32_t* n_post_pad, int32_t* inv,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+  return dispatch_launch(topk_idx, n_pairs, n_experts, sorted_ids, expert_ids, pad_offsets,
+                         counts, n_post_pad, inv, workspace, workspace_bytes, nullptr, stream);
 }

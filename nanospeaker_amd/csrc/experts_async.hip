@@ -271,7 +271,11 @@ __global__ void __launch_bounds__(NT, MB == 6 || D == 3 ? 3 : 2) expert_fwd_reg_
   static_assert(D == 2 || D == 3, "prefetch distance");
   constexpr int TM = MB * 16;            // tile rows
   constexpr int S = D + 1;               // token-tile ring stages
-  constexpr int XC = MB == 4 ? 1 : 2;    // token copies per wave per step
+  // Token copies per wave per step: 4 16-byte slots per row, 256 per full copy; a tile
+  // whose slot count is an odd multiple of 128 ends with a copy on half of each wave.
+  constexpr int XC = (TM * 4 + NT - 1) / NT;
+  constexpr bool XHALF = (TM * 4) % NT != 0;
+  static_assert((TM * 4) % NT == 0 || (TM * 4) % NT == NT / 2, "whole or half copies");
   constexpr bool STAGE_Y = MB == 4;
   constexpr int HPMAX = 64 * NBW;
   constexpr int A_BYTES = TM * G::ROWB;  // TM rows x 32 elements
@@ -365,28 +369,29 @@ __global__ void __launch_bounds__(NT, MB == 6 || D == 3 ? 3 : 2) expert_fwd_reg_
   if (tid < rows)
     gate_w = routed ? Elem<DT>::to_f(((const T*)p.topk_w)[pair]) : 1.0f;
   // Token copies: copy slot c (16 bytes) holds chunk (c % 4) ^ swz(r) of row r = c / 4.
-  // The first copy of wave w fills slots [256 w / 4 ... ) = tid; for 96 rows the second
-  // fills slots 256 + 32 w + lane (lanes < 32), rows 64 + 8 w + lane / 4.
-  const int ar = tid >> 2, ac = (tid & 3) ^ swz<DT>(ar);
-  const int atok = s_tok[ar];
-  const T* arow = atok >= 0 ? (const T*)p.x + (int64_t)atok * d + ac * G::VE : nullptr;
-  const T* arow2 = nullptr;
-  int ac2 = 0;
-  if constexpr (XC == 2) {
-    const int r2 = 64 + wave * 8 + (lane >> 2);
-    ac2 = ((lane & 3) ^ swz<DT>(r2));
-    const int t2 = lane < 32 ? s_tok[r2 < TM ? r2 : 0] : -1;
-    arow2 = t2 >= 0 ? (const T*)p.x + (int64_t)t2 * d + ac2 * G::VE : nullptr;
+  // Full copy x of wave w fills slots 256 x + 64 w + lane (rows 64 x + tid / 4); a final
+  // half copy fills slots 256 x + 32 w + lane (lanes < 32), rows 64 x + 8 w + lane / 4.
+  const T* arow[XC];
+  int acol[XC];
+#pragma unroll
+  for (int x = 0; x < XC; ++x) {
+    const bool half = XHALF && x == XC - 1;
+    const int r = half ? 64 * x + wave * 8 + (lane >> 2) : 64 * x + (tid >> 2);
+    acol[x] = (lane & 3) ^ swz<DT>(r);
+    const int t = (!half || lane < 32) && r < TM ? s_tok[r] : -1;
+    arow[x] = t >= 0 ? (const T*)p.x + (int64_t)t * d + acol[x] * G::VE : nullptr;
   }
   auto issue_x = [&](int s) __attribute__((always_inline)) {
     const int k0 = s * G::KC;
-    const bool av = arow && k0 + ac * G::VE < d;
-    async_copy16(av ? (const void*)(arow + k0) : (const void*)zero, s_ring[s % S] + wave * 1024);
-    if constexpr (XC == 2) {
-      const bool av2 = arow2 && k0 + ac2 * G::VE < d;
-      if (lane < 32)
-        async_copy16(av2 ? (const void*)(arow2 + k0) : (const void*)zero,
-                     s_ring[s % S] + 4096 + wave * 512);
+#pragma unroll
+    for (int x = 0; x < XC; ++x) {
+      const bool av = arow[x] && k0 + acol[x] * G::VE < d;
+      const void* src = av ? (const void*)(arow[x] + k0) : (const void*)zero;
+      if (XHALF && x == XC - 1) {
+        if (lane < 32) async_copy16(src, s_ring[s % S] + 4096 * x + wave * 512);
+      } else {
+        async_copy16(src, s_ring[s % S] + 4096 * x + wave * 1024);
+      }
     }
   };
 

@@ -90,6 +90,21 @@ int route_bwd_launch(const void* src, const int64_t* topk_idx, const void* grad_
                      int32_t n_experts, int32_t top_k, int32_t flags, void* grad_logits,
                      int32_t ldg, hipStream_t stream);
 int64_t balance_partial_count(int64_t n_tokens);
+// The balance loss folded into the dispatch (dispatch_launch): column-sum partials of probs
+// from route_fwd_launch ([nblk = balance_partial_count(T), E] fp32), T, coef -> aux[0].
+struct BalanceArgs {
+  const float* partial;
+  int64_t nblk;
+  int64_t T;
+  float coef;
+  float* aux;
+};
+// nsmoe_dispatch, plus the balance loss in one extra workgroup of its second launch when
+// bal is non-NULL (E <= 128).
+int dispatch_launch(const int64_t* topk_idx, int64_t n_pairs, int32_t n_experts,
+                    int32_t* sorted_ids, int32_t* expert_ids, int32_t* pad_offsets,
+                    int32_t* counts, int32_t* n_post_pad, int32_t* inv, void* workspace,
+                    size_t workspace_bytes, const BalanceArgs* bal, void* stream);
 int balance_final_launch(const float* partial, int64_t n_tokens, int32_t n_experts,
                          const int32_t* counts, float coef, float* aux, hipStream_t stream);
 }  // namespace nsmoe
