@@ -15,6 +15,7 @@
 #include <stdlib.h>
 
 #include <type_traits>
+#include <utility>
 
 #include "experts_common.h"
 
@@ -1525,43 +1526,67 @@ __device__ __forceinline__ void dw_item(const ExpParams& p, int item, DwLds<DT, 
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / Tl::WN, wn = wave % Tl::WN;
 
-  for (int r = tid; r < nr; r += NT) s_tok[r] = g < p.E ? p.sorted_ids[rs + r] / p.k : r0 + r;
+  // s_tok holds each row's token as an element offset, tok * d (int32: the launchers
+  // require T * d < 2^31).
+  for (int r = tid; r < nr; r += NT)
+    s_tok[r] = (g < p.E ? p.sorted_ids[rs + r] / p.k : r0 + r) * d;
   __syncthreads();
 
   const T* X = (const T*)p.x;
   const T* DA = (const T*)p.da1;
   const T* HB = (const T*)p.hbuf;
   const T* DO = (const T*)p.dout;
-  const char* zero = (const char*)g_zero_kib + lane * 16;
-  // Row r (0 .. nr) of the chunk: Q and P source rows, pointing at the tile's first column.
-  auto qrow = [&](int r) -> const T* {
-    if constexpr (MODE == 0) return X + (int64_t)s_tok[r] * d + m0;
-    else return HB + (rs + r) * H + m0;
-  };
-  auto prow = [&](int r) -> const T* {
-    if constexpr (MODE == 0) return DA + (rs + r) * twoH + n0;
-    else return DO + (int64_t)s_tok[r] * d + n0;
-  };
+  const T* zero = (const T*)((const char*)g_zero_kib + lane * 16);
   const int nsteps = (nr + G::KC - 1) / G::KC;
 
-  auto issue = [&](int s) {
-    char* st = s_ring[s % S];
+  // The copy plan, fixed for the item.  Copy u of this wave moves one 16-byte chunk of
+  // the 1 KiB block b = 4u + wave: chunk column (swizzled on the source side) and row
+  // crow[u] of the step.  Blocks [0, QBLK) are Q and the rest P; QBLK % 4 == 0 makes that a
+  // compile-time property of u once the loops are unrolled.  The token operand (Q = x in
+  // MODE 0, P = dout in MODE 1) is gathered through s_tok, whose entries for the next step
+  // are read one issue ahead (ctok); the other operand's rows are consecutive slots, so
+  // its source is csrc[u] + k0 * stride.  A chunk past the tile's columns gets a row no
+  // step reaches, so it always reads the zero block.
+  static_assert(QBLK % 4 == 0, "Q / P split known per copy");
+  auto gathered = [](int u) { return (4 * u < QBLK) == (MODE == 0); };
+  const int lstride = MODE == 0 ? twoH : H;
+  int crow[LOADS], ctok[LOADS];
+  const T* csrc[LOADS];
+#pragma unroll
+  for (int u = 0; u < LOADS; ++u) {
+    const bool isq = 4 * u < QBLK;
+    const int q = (isq ? 4 * u + wave : 4 * u + wave - QBLK) * 64 + lane;
+    int row, col;
+    bool ok;
+    if (isq) {
+      row = q / QCPR;
+      col = m0 + ((q % QCPR) ^ dw_swz<QROWB>(row)) * 8;
+      ok = col < Md;
+    } else {
+      row = q / PCPR;
+      col = n0 + ((q % PCPR) ^ dw_swz<PROWB>(row)) * 8;
+      ok = col < Nd;
+    }
+    crow[u] = ok ? row : (1 << 20);
+    ctok[u] = 0;
+    if (gathered(u)) csrc[u] = (MODE == 0 ? X : DO) + col;
+    else csrc[u] = (MODE == 0 ? DA : HB) + (rs + row) * lstride + col;
+  }
+  const uint32_t ring = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)&L.ring[0][0];
+  auto read_tok = [&](int s) {
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u)
+      if (gathered(u)) ctok[u] = s_tok[s * G::KC + (crow[u] & 31)];
+  };
+  auto issue = [&](int s, int stage) {
     const int k0 = s * G::KC;
+    const uint32_t dst = ring + stage * STAGE + wave * 1024;
 #pragma unroll
     for (int u = 0; u < LOADS; ++u) {
-      const int b = wave + 4 * u;  // wave-uniform block index
-      const void* src = zero;
-      if (b < QBLK) {
-        const int q = b * 64 + lane, row = q / QCPR, cp = q % QCPR;
-        const int c = cp ^ dw_swz<QROWB>(row);
-        if (k0 + row < nr && m0 + c * 8 < Md) src = qrow(k0 + row) + c * 8;
-      } else {
-        const int q = (b - QBLK) * 64 + lane, row = q / PCPR, cp = q % PCPR;
-        const int c = cp ^ dw_swz<PROWB>(row);
-        if (k0 + row < nr && n0 + c * 8 < Nd) src = prow(k0 + row) + c * 8;
-      }
-      async_copy16(src, st + b * 1024);
+      const T* src = gathered(u) ? csrc[u] + ctok[u] : csrc[u] + (int64_t)k0 * lstride;
+      async_copy16_to(k0 + crow[u] < nr ? src : zero, dst + 4 * u * 1024);
     }
+    if (s + 1 < nsteps) read_tok(s + 1);
   };
   auto wait_for = [&](int s) {
     if (s + S - 2 < nsteps) wait_vmcnt<(S - 2) * LOADS>();
@@ -1586,12 +1611,14 @@ __device__ __forceinline__ void dw_item(const ExpParams& p, int item, DwLds<DT, 
   for (int j = 0; j < TNB; ++j)
 #pragma unroll
     for (int i = 0; i < TMB; ++i) acc[j][i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int s = 0; s < S - 1 && s < nsteps; ++s) issue(s);
-  for (int s = 0; s < nsteps; ++s) {
+  // One k-step on ring stage ST (a compile-time constant, so every fragment read is a
+  // per-lane offset plus an immediate).
+  auto step = [&](int s, auto stage_tag) {
+    constexpr int ST = decltype(stage_tag)::value;
     wait_for(s);
     barrier_lds();
-    if (s + S - 1 < nsteps) issue(s + S - 1);
-    const char* st = s_ring[s % S];
+    if (s + S - 1 < nsteps) issue(s + S - 1, (ST + S - 1) % S);
+    const char* st = L.ring[ST];
     Frag qf[TMB], pf[TNB];
 #pragma unroll
     for (int i = 0; i < TMB; ++i)
@@ -1603,6 +1630,15 @@ __device__ __forceinline__ void dw_item(const ExpParams& p, int item, DwLds<DT, 
     for (int j = 0; j < TNB; ++j)
 #pragma unroll
       for (int i = 0; i < TMB; ++i) M::run(acc[j][i], pf[j], qf[i]);
+  };
+  if (nsteps > 0) read_tok(0);
+  for (int s = 0; s < S - 1 && s < nsteps; ++s) issue(s, s);
+  // Steps in groups of S, so step s + I sits on stage I.
+  for (int s = 0; s < nsteps; s += S) {
+    [&]<int... I>(std::integer_sequence<int, I...>) {
+      (void)((s + I < nsteps ? (step(s + I, std::integral_constant<int, I>{}), true) : false) &&
+             ...);
+    }(std::make_integer_sequence<int, S>{});
   }
   wait_vmcnt<0>();
 
@@ -1661,6 +1697,7 @@ __global__ void __launch_bounds__(NT, 2) dw_pair_kernel(ExpParams p_in, ExpParam
 int launch_dw_async(int dtype, int mode, const ExpParams& q, int64_t groups_chunks,
                     hipStream_t s) {
   if (!q.fast || (dtype != DT_BF16 && dtype != DT_F16)) return -1;
+  if (q.T * q.d >= (int64_t(1) << 31)) return -1;  // token offsets are int32
   const int d = q.d, H = q.H;
   const int Md = mode == 0 ? d : H, Nd = mode == 0 ? 2 * H : d;
   const int BMT = mode == 0 ? DwTile<0>::BMT : DwTile<1>::BMT;
@@ -1684,6 +1721,7 @@ int launch_dw_async(int dtype, int mode, const ExpParams& q, int64_t groups_chun
 int launch_dw_pair_async(int dtype, const ExpParams& q_in, const ExpParams& q_out,
                          int64_t groups_chunks, hipStream_t s) {
   if (!q_in.fast || (dtype != DT_BF16 && dtype != DT_F16)) return -1;
+  if (q_in.T * q_in.d >= (int64_t(1) << 31)) return -1;  // token offsets are int32
   const int d = q_in.d, H = q_in.H;
   // Rounded up to whole XCD rounds (the extra items are past the last real one and exit).
   const int64_t g_in =

@@ -190,6 +190,22 @@ __device__ __forceinline__ void store_trans8(const u32x4 (&v)[8], char* tile, in
 // valid range, so every lane always issues its copy.  One copy per translation unit.
 static __device__ __attribute__((aligned(1024))) uint32_t g_zero_kib[256] = {0};
 
+// async_copy16_to takes the LDS byte address itself (wave-uniform), which spares the
+// generic-to-LDS pointer conversion per copy.
+__device__ __forceinline__ void async_copy16_to(const void* gsrc, uint32_t lds_addr) {
+  const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_addr);
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(gsrc), "s"(lds)
+      : "memory");
+}
+
 __device__ __forceinline__ void async_copy16(const void* gsrc, char* lds_wave_base) {
   const uint32_t lds = __builtin_amdgcn_readfirstlane(
       (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds_wave_base);
