@@ -933,7 +933,7 @@ __global__ void __launch_bounds__(NT, 2) expert_dx_async_kernel(ExpParams p) {
 // of a steady step are unconditional (zero page for fragments past the edge).
 // Shapes: an even number of k-steps.
 
-template <int DT, int NBW, int D>
+template <int DT, int NBW, int D, int MB>
 __global__ void __launch_bounds__(NT, 2) expert_bwd_reg_kernel(ExpParams p) {
   using G = Geo<DT>;
   using T = typename G::T;
@@ -941,33 +941,38 @@ __global__ void __launch_bounds__(NT, 2) expert_bwd_reg_kernel(ExpParams p) {
   using Frag = typename M::Frag;
   static_assert(G::ES == 2, "16-bit types only");
   static_assert(D == 2 || D == 3, "prefetch distance");
+  static_assert(MB >= 2 && MB <= 6, "tiles of 32 .. 96 rows");
   constexpr int S = D + 1;
+  constexpr int TM = MB * 16;            // tile rows
   constexpr int HPMAX = 64 * NBW;
-  constexpr int A_BYTES = BM * G::ROWB;  // one token tile (x or dout): 4 KiB
+  constexpr int A_BYTES = TM * G::ROWB;  // one token tile (x or dout)
+  // Copies per token tile and step: TM * 4 slots of 16 bytes, up to 256 per copy; copy x
+  // of wave w fills slots 256 x + CL w + lane for the lanes below CL = min(64, TM - 64 x).
+  constexpr int XC = (TM + 63) / 64;
   constexpr int NBF = 3 * NBW;           // gate, up and G fragments per wave per step
-  constexpr int SLOT = NBF + 2;          // VM operations a steady slot issues
+  constexpr int SLOT = NBF + 2 * XC;     // VM operations a steady slot issues
   constexpr int DA_PITCH = 2 * HPMAX * G::ES + 16;  // staged dA1 rows
   constexpr int HB_PITCH = HPMAX * G::ES + 16;      // staged w h rows
   constexpr int RING = S * 2 * A_BYTES;
-  constexpr int STAGE_BYTES = BM * (DA_PITCH + HB_PITCH);
+  constexpr int STAGE_BYTES = TM * (DA_PITCH + HB_PITCH);
   constexpr int LDS_BYTES = RING > STAGE_BYTES ? RING : STAGE_BYTES;
   __shared__ __attribute__((aligned(1024))) char s_lds[LDS_BYTES];
-  __shared__ int s_tok[BM];
-  __shared__ int s_pair[BM];
-  __shared__ float s_w[BM];
-  __shared__ float s_dtw[5][BM];
+  __shared__ int s_tok[TM];
+  __shared__ int s_pair[TM];
+  __shared__ float s_w[TM];
+  __shared__ float s_dtw[5][TM];
   __shared__ int s_loc[3];
   char* s_da = s_lds;                   // epilogue staging, over the ring
-  char* s_hb = s_lds + BM * DA_PITCH;
+  char* s_hb = s_lds + TM * DA_PITCH;
   auto ring = [&](int s) __attribute__((always_inline)) { return s_lds + (s % S) * 2 * A_BYTES; };
 
   const int tile = tile_of_block(p);
   Located loc;
-  if (!locate(tile, p.E + p.S, [&](int g) { return (rows_of(p, g) + BM - 1) / BM; },
+  if (!locate(tile, p.E + p.S, [&](int g) { return (rows_of(p, g) + TM - 1) / TM; },
               [](int) { return 0; }, s_loc, loc))
     return;
-  const int g = loc.g, m0 = loc.local * BM;
-  const int rows = min(BM, rows_of(p, g) - m0);
+  const int g = loc.g, m0 = loc.local * TM;
+  const int rows = min(TM, rows_of(p, g) - m0);
   const int64_t slot0 = row_start(p, g) + m0;
   const int tid = threadIdx.x, lane = tid & 63, lc = lane & 15, lg = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -999,33 +1004,59 @@ __global__ void __launch_bounds__(NT, 2) expert_bwd_reg_kernel(ExpParams p) {
 #pragma unroll
   for (int j = 0; j < D; ++j) wset[j] = load_w(j);
 
-  if (tid < BM) {
+  const bool routed = g < p.E;
+  if (tid < TM) {
     int tok = -1, pair = -1;
-    float w = 0.0f;
-    if (tid < rows) row_info<DT>(p, g, slot0 + tid, m0 + tid, tok, w, pair);
+    if (tid < rows) {
+      if (routed) {
+        pair = p.sorted_ids[slot0 + tid];
+        tok = pair / p.k;
+      } else {
+        tok = m0 + tid;
+      }
+    }
     s_tok[tid] = tok;
     s_pair[tid] = pair;
-    s_w[tid] = w;
     s_dtw[4][tid] = 0.0f;
   }
   __syncthreads();
 
-  const int ar = tid >> 2, ac = (tid & 3) ^ swz<DT>(ar);
-  const int atok = s_tok[ar];
-  const T* xrow = atok >= 0 ? (const T*)p.x + (int64_t)atok * d + ac * G::VE : nullptr;
-  const T* drow = atok >= 0 ? (const T*)p.dout + (int64_t)atok * d + ac * G::VE : nullptr;
+  // Copy slot q (16 bytes) holds chunk (q % 4) ^ swz(r) of row r = q / 4.
+  const T* xrow[XC];
+  const T* drow[XC];
+#pragma unroll
+  for (int x = 0; x < XC; ++x) {
+    const int cl = min(64, TM - 64 * x);
+    const int q = 256 * x + cl * wave + lane, ar = q >> 2, ac = (q & 3) ^ swz<DT>(ar);
+    const int atok = lane < cl ? s_tok[ar] : -1;
+    xrow[x] = atok >= 0 ? (const T*)p.x + (int64_t)atok * d + ac * G::VE : nullptr;
+    drow[x] = atok >= 0 ? (const T*)p.dout + (int64_t)atok * d + ac * G::VE : nullptr;
+  }
   auto issue_x = [&](int s) __attribute__((always_inline)) {
     char* st = ring(s);
     const int k0 = s * G::KC;
-    async_copy16(xrow ? (const void*)(xrow + k0) : (const void*)zero, st + wave * 1024);
-    async_copy16(drow ? (const void*)(drow + k0) : (const void*)zero, st + A_BYTES + wave * 1024);
+#pragma unroll
+    for (int x = 0; x < XC; ++x) {
+      const int cl = min(64, TM - 64 * x);
+      char* dst = st + 4096 * x + wave * cl * 16;
+      if (cl == 64 || lane < cl) {
+        async_copy16(xrow[x] ? (const void*)(xrow[x] + k0) : (const void*)zero, dst);
+        async_copy16(drow[x] ? (const void*)(drow[x] + k0) : (const void*)zero, dst + A_BYTES);
+      }
+    }
   };
 #pragma unroll
   for (int j = 0; j < D; ++j) issue_x(j);
+  // The gate weight of row tid % TM, needed only by the epilogue: its load goes out after
+  // the copies, so the copies do not wait for it.  Every lane issues it (a zero word for
+  // rows without one), which keeps each wave's count of outstanding loads uniform.
+  const int wr = tid % TM;
+  const int wpair = routed && wr < rows ? s_pair[wr] : -1;
+  const T wraw = *(wpair >= 0 ? (const T*)p.topk_w + wpair : (const T*)g_zero_kib);
 
-  f32x4 accg[4][NBW], accu[4][NBW], accG[4][NBW];
+  f32x4 accg[MB][NBW], accu[MB][NBW], accG[MB][NBW];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < MB; ++i)
 #pragma unroll
     for (int j = 0; j < NBW; ++j)
       accg[i][j] = accu[i][j] = accG[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1033,7 +1064,7 @@ __global__ void __launch_bounds__(NT, 2) expert_bwd_reg_kernel(ExpParams p) {
     barrier_dma();
     const char* st = ring(s);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < MB; ++i) {
       const Frag xf = frag_sw<DT>(st, i * 16);
       const Frag df = frag_sw<DT>(st + A_BYTES, i * 16);
 #pragma unroll
@@ -1044,11 +1075,13 @@ __global__ void __launch_bounds__(NT, 2) expert_bwd_reg_kernel(ExpParams p) {
       }
     }
   };
-  // Prologue order: w(0) .. w(D - 1) [row lookups] x(0) d(0) .. x(D - 1) d(D - 1).  Every
-  // prologue load but step D - 1's two copies: the steady-state count below assumes that
-  // step s's copies are followed only by the loads of steps s + 1 .. s + D - 1, which
-  // holds for the prologue steps below D - 1 only once their copies are complete.
-  wait_vmcnt<2>();
+  // Prologue order: w(0) .. w(D - 1) [row lookups] x(0) d(0) .. x(D - 1) d(D - 1), gate.
+  // Every prologue load but step D - 1's copies and the gate weight: the steady-state
+  // count below assumes that step s's copies are followed only by the loads of steps
+  // s + 1 .. s + D - 1, which holds for the prologue steps below D - 1 only once their
+  // copies are complete (and the gate load, older than every steady slot, is covered by
+  // the first steady wait).
+  wait_vmcnt<2 * XC + 1>();
   int s = 0;
   for (; s + D < nk; s += D) {
 #pragma unroll
@@ -1064,6 +1097,7 @@ __global__ void __launch_bounds__(NT, 2) expert_bwd_reg_kernel(ExpParams p) {
     wait_vmcnt_dyn((D - 1 - j) * SLOT);  // a constant once unrolled
     mma(s + j, wset[j]);
   }
+  if (tid < TM) s_w[tid] = routed ? (wr < rows ? Elem<DT>::to_f(wraw) : 0.0f) : (tid < rows ? 1.0f : 0.0f);
   wait_lgkm0();
   barrier_dma();  // every wave is done with the ring: the staging may overwrite it
 
@@ -1071,10 +1105,12 @@ __global__ void __launch_bounds__(NT, 2) expert_bwd_reg_kernel(ExpParams p) {
   // hidden columns n0 .. n0 + 3 ----
   const T* bin = (g < p.E ? p.b_in : p.b_sh_in)
                      ? per_group<T>(p.b_in, p.b_sh_in, g, p.E, twoH) : nullptr;
-  float wrow[4];
+  float wrow[MB], part[MB];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) wrow[i] = s_w[i * 16 + lc];
-  float part[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < MB; ++i) {
+    wrow[i] = s_w[i * 16 + lc];
+    part[i] = 0.0f;
+  }
   with_act(p.act, [&]<int ACT>() {
 #pragma unroll
     for (int j = 0; j < NBW; ++j) {
@@ -1089,7 +1125,7 @@ __global__ void __launch_bounds__(NT, 2) expert_bwd_reg_kernel(ExpParams p) {
         }
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < MB; ++i) {
         const int m = i * 16 + lc;
         const float w = wrow[i];
         float dg[4], du[4], wh[4];
@@ -1118,7 +1154,7 @@ __global__ void __launch_bounds__(NT, 2) expert_bwd_reg_kernel(ExpParams p) {
   });
   // dtopk_w: sum of G h over the row's hidden columns (4 lanes per wave, then 4 waves).
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < MB; ++i) {
     float v = part[i];
     v += __shfl_xor(v, 16, 64);
     v += __shfl_xor(v, 32, 64);
@@ -1127,29 +1163,31 @@ __global__ void __launch_bounds__(NT, 2) expert_bwd_reg_kernel(ExpParams p) {
   // <dout[tok], b_out[g]>: four lanes per row, strided over d.
   if (g < p.E && p.b_out) {
     const T* bo = (const T*)p.b_out + (int64_t)g * d;
-    const int m = tid >> 2, q = tid & 3;
-    float v = 0.0f;
-    if (m < rows) {
-      const T* dr = (const T*)p.dout + (int64_t)s_tok[m] * d;
-      for (int c = q; c < d; c += 4) v += Elem<DT>::to_f(dr[c]) * Elem<DT>::to_f(bo[c]);
+    for (int m0r = 0; m0r < TM; m0r += NT / 4) {  // the same trip count in every lane
+      const int m = m0r + (tid >> 2), q = tid & 3;
+      float v = 0.0f;
+      if (m < rows) {
+        const T* dr = (const T*)p.dout + (int64_t)s_tok[m] * d;
+        for (int c = q; c < d; c += 4) v += Elem<DT>::to_f(dr[c]) * Elem<DT>::to_f(bo[c]);
+      }
+      v += __shfl_xor(v, 1, 64);
+      v += __shfl_xor(v, 2, 64);
+      if (q == 0 && m < rows) s_dtw[4][m] = v;
     }
-    v += __shfl_xor(v, 1, 64);
-    v += __shfl_xor(v, 2, 64);
-    if (q == 0 && m < rows) s_dtw[4][m] = v;
   }
   __syncthreads();
   // Whole rows out: dA1 rows of 2H elements, w h rows of H elements, 16-byte chunks.
   T* DA = (T*)p.da1 + slot0 * twoH;
   T* HB = (T*)p.hbuf + slot0 * H;
   const int da_cpr = twoH / G::VE, hb_cpr = H / G::VE;
-  for (int c = tid; c < BM * da_cpr; c += NT) {
+  for (int c = tid; c < TM * da_cpr; c += NT) {
     const int m = c / da_cpr, cc = c - m * da_cpr;
     if (m < rows) {
       const int col = cc * G::VE;  // the staged row has the final layout: [gate H | up H]
       *(u32x4*)(DA + (int64_t)m * twoH + col) = *(const u32x4*)(s_da + m * DA_PITCH + col * G::ES);
     }
   }
-  for (int c = tid; c < BM * hb_cpr; c += NT) {
+  for (int c = tid; c < TM * hb_cpr; c += NT) {
     const int m = c / hb_cpr, cc = c - m * hb_cpr;
     if (m < rows)
       *(u32x4*)(HB + (int64_t)m * H + cc * G::VE) = *(const u32x4*)(s_hb + m * HB_PITCH + cc * 16);
@@ -1352,15 +1390,23 @@ __global__ void __launch_bounds__(NT, D > 2 || MB == 6 ? 3 : 2) expert_dx_reg_ke
 static int device_cus();
 static int64_t tile_grid(const ExpParams& p, int bm);
 
-template <int DT>
-static void bwd_reg_launch(const ExpParams& p, int nbw, int dist, unsigned grid, hipStream_t s) {
+template <int DT, int MB>
+static void bwd_reg_launch_mb(const ExpParams& p, int nbw, int dist, hipStream_t s) {
+  const unsigned grid = (unsigned)tile_grid(p, 16 * MB);
   if (dist == 3) {
-    if (nbw == 1) expert_bwd_reg_kernel<DT, 1, 3><<<grid, NT, 0, s>>>(p);
-    else expert_bwd_reg_kernel<DT, 2, 3><<<grid, NT, 0, s>>>(p);
+    if (nbw == 1) expert_bwd_reg_kernel<DT, 1, 3, MB><<<grid, NT, 0, s>>>(p);
+    else expert_bwd_reg_kernel<DT, 2, 3, MB><<<grid, NT, 0, s>>>(p);
   } else {
-    if (nbw == 1) expert_bwd_reg_kernel<DT, 1, 2><<<grid, NT, 0, s>>>(p);
-    else expert_bwd_reg_kernel<DT, 2, 2><<<grid, NT, 0, s>>>(p);
+    if (nbw == 1) expert_bwd_reg_kernel<DT, 1, 2, MB><<<grid, NT, 0, s>>>(p);
+    else expert_bwd_reg_kernel<DT, 2, 2, MB><<<grid, NT, 0, s>>>(p);
   }
+}
+
+template <int DT>
+static void bwd_reg_launch(const ExpParams& p, int nbw, int dist, int mb, hipStream_t s) {
+  if (mb == 3) bwd_reg_launch_mb<DT, 3>(p, nbw, dist, s);
+  else if (mb == 5) bwd_reg_launch_mb<DT, 5>(p, nbw, dist, s);
+  else bwd_reg_launch_mb<DT, 4>(p, nbw, dist, s);
 }
 
 template <int DT>
@@ -1385,16 +1431,27 @@ int launch_bwd_async(int dtype, const ExpParams& p, int nbw, int64_t grid, int p
   const int nsteps_dx = ((p.d + NP2 - 1) / NP2) * (2 * p.H / 32);
   if (reg && p.d % 64 == 0 && (2 * p.H) % 32 == 0 && nsteps_dx % 2 == 0 && p.in_kb >= 4) {
     if (part == 0) {
-      // Weight prefetch distance 3 steps where the step count divides by 3, else 2;
-      // NSMOE_BWD_D = 2 or 3 forces one (read on every call, for tests).
-      int dist = p.in_kb % 3 == 0 ? 3 : 2;
+      // 64-row tiles at 2 workgroups per CU with weight prefetch distance 3 (where the step
+      // count divides by 3, else 2); once those tiles overflow one round of the resident
+      // slots, 48-row tiles at distance 2, whose 162 registers fit 3 workgroups per CU (at
+      // T = 8192: 1406 tiles over 768 slots instead of 1064 over 512, the last third of a
+      // round nearly empty).  NSMOE_BWD_MB = 3, 4 or 5 and NSMOE_BWD_D = 2 or 3 force a
+      // tile height and a distance (read on every call, for tests); 80-row tiles take
+      // distance 2, which is all their registers allow.
+      int mb = tile_grid(p, 64) > 2 * (int64_t)device_cus() ? 3 : 4;
+      if (const char* e = getenv("NSMOE_BWD_MB")) {
+        const int v = atoi(e);
+        if (v >= 3 && v <= 5) mb = v;
+      }
+      int dist = mb != 3 && p.in_kb % 3 == 0 ? 3 : 2;
       if (const char* e = getenv("NSMOE_BWD_D")) {
         const int v = atoi(e);
         if (v == 2 || (v == 3 && p.in_kb % 3 == 0)) dist = v;
       }
+      if (mb == 5) dist = 2;
       KernelTimer timer("expert_bwd", s);
-      if (dtype == DT_BF16) bwd_reg_launch<DT_BF16>(p, nbw, dist, (unsigned)grid, s);
-      else bwd_reg_launch<DT_F16>(p, nbw, dist, (unsigned)grid, s);
+      if (dtype == DT_BF16) bwd_reg_launch<DT_BF16>(p, nbw, dist, mb, s);
+      else bwd_reg_launch<DT_F16>(p, nbw, dist, mb, s);
       timer.stop();
       return check_launch("expert_bwd_reg_kernel");
     }

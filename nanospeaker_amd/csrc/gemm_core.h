@@ -441,6 +441,20 @@ struct Located {
   int aux;  // prefix of aux(g) over the groups before g
 };
 
+// Inclusive prefix sum over the wave's 64 lanes: Hillis-Steele inside each 16-lane row
+// (DPP row_shr 1, 2, 4, 8), then row 0's total into row 1 and row 2's into row 3
+// (row_bcast:15), then rows 0-1's total into rows 2 and 3 (row_bcast:31).  Lanes a DPP
+// move does not write read 0 (the `old` operand).
+__device__ __forceinline__ int wave_scan_incl(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31
+  return v;
+}
+
 template <class Units, class Aux>
 __device__ __forceinline__ bool locate(int item, int G, Units units, Aux aux, int* s_loc,
                                        Located& out) {
@@ -452,29 +466,20 @@ __device__ __forceinline__ bool locate(int item, int G, Units units, Aux aux, in
       const int g = g0 + lane;
       const int u = g < G ? units(g) : 0;
       const int a = g < G ? aux(g) : 0;
-      int incl = u, aincl = a;
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        int t = __shfl_up(incl, o, 64);
-        int ta = __shfl_up(aincl, o, 64);
-        if (lane >= o) {
-          incl += t;
-          aincl += ta;
-        }
-      }
+      const int incl = wave_scan_incl(u), aincl = wave_scan_incl(a);
       const bool hit = item >= base + incl - u && item < base + incl;
       const unsigned long long m = __ballot(hit);
       if (m) {
-        const int src = __ffsll((long long)m) - 1;
-        const int excl = __shfl(incl - u, src, 64);
-        const int aexcl = __shfl(aincl - a, src, 64);
+        const int src = __ffsll((long long)m) - 1;  // wave-uniform
+        const int excl = __builtin_amdgcn_readlane(incl - u, src);
+        const int aexcl = __builtin_amdgcn_readlane(aincl - a, src);
         fg = g0 + src;
         floc = item - base - excl;
         faux = abase + aexcl;
         break;
       }
-      base += __shfl(incl, 63, 64);
-      abase += __shfl(aincl, 63, 64);
+      base += __builtin_amdgcn_readlane(incl, 63);
+      abase += __builtin_amdgcn_readlane(aincl, 63);
     }
     if (lane == 0) {
       s_loc[0] = fg;

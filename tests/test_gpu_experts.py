@@ -119,17 +119,19 @@ def test_forward_tile_heights(dist, mb, dtype, shape, T, monkeypatch):
     check("out", out, ref_out, dtype)
 
 
-@pytest.mark.parametrize("mb,dist,bwd_dist",
-                         [("4", "2", "2"), ("6", "2", "3"), ("4", "4", "3"), ("6", "3", "2")])
+@pytest.mark.parametrize("mb,dist,bwd_dist,bwd_mb",
+                         [("4", "2", "2", "4"), ("6", "2", "3", "4"), ("4", "4", "3", "3"),
+                          ("6", "3", "2", "3"), ("4", "2", "2", "5")])
 @pytest.mark.parametrize("shape", ["wide_h64", "ns_h128"])
 @pytest.mark.parametrize("T", [37, 1000])
-def test_backward_tile_heights_and_prefetch(mb, dist, bwd_dist, shape, T, monkeypatch):
+def test_backward_tile_heights_and_prefetch(mb, dist, bwd_dist, bwd_mb, shape, T, monkeypatch):
     """The dX-row kernel at both tile heights and several weight prefetch distances, and
-    the GLU-backward kernel at both of its prefetch distances (all forced), checked
-    through dx and every weight gradient."""
+    the GLU-backward kernel at 48-, 64- and 80-row tiles and both of its prefetch distances
+    (all forced), checked through dx and every weight gradient."""
     monkeypatch.setenv("NSMOE_DX_MB", mb)
     monkeypatch.setenv("NSMOE_DX_D", dist)
     monkeypatch.setenv("NSMOE_BWD_D", bwd_dist)
+    monkeypatch.setenv("NSMOE_BWD_MB", bwd_mb)
     d, E, d_ff = SHAPES[shape]
     p, x, gout, tw, ti = make_case(d, E, d_ff, 6, 2, T % 2 == 1, T, torch.bfloat16,
                                    seed=T + int(mb))
