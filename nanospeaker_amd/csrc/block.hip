@@ -158,7 +158,7 @@ namespace nsmoe {
 // Backward workspace: the gate gradient (T x k), the expert backward's workspace, and on
 // the fused router path d(logits) at pitch ep plus the router dW partials.
 struct BwdWs {
-  size_t tw, exp, gl, part, total;
+  size_t tw, exp, gl, part, wpk, total;
 };
 
 static BwdWs bwd_ws(const nsmoe_experts_args* b, bool router) {
@@ -168,10 +168,13 @@ static BwdWs bwd_ws(const nsmoe_experts_args* b, bool router) {
   w.exp = al256((size_t)b->n_tokens * b->top_k * es);
   w.gl = w.exp + al256(nsmoe_experts_bwd_workspace_size(b));
   w.part = w.gl;
+  w.wpk = w.gl;
   w.total = w.gl;
   if (router) {
-    w.part = w.gl + al256((size_t)b->n_tokens * router_logits_pitch(b->n_experts) * es);
-    w.total = w.part + al256(router_dw_partial_bytes(b->n_tokens, b->d_model, b->n_experts));
+    const int ep = router_logits_pitch(b->n_experts);
+    w.part = w.gl + al256((size_t)b->n_tokens * ep * es);
+    w.wpk = w.part + al256(router_dw_partial_bytes(b->n_tokens, b->d_model, b->n_experts));
+    w.total = w.wpk + al256(router_w_pack_bytes((int)b->d_model, (ep + 31) / 32));
   }
   return w;
 }
@@ -247,16 +250,18 @@ int block_bwd_router(const nsmoe_experts_args* a, const nsmoe_experts_args& b,
   const int E = a->n_experts;
   const int ldg = fuse ? router_logits_pitch(E) : E;
   void* gl = fuse ? (void*)(ws + W.gl) : grad_logits;
+  // With the router GEMM fused, the same launch packs W for combine_dx's router term.
+  const RouterWPack pack{w_router, ws + W.wpk, (int)a->d_model, E, (ldg + 31) / 32};
   NSMOE_TRY(route_bwd_launch(src, (const int64_t*)(sv + L.off[NSMOE_SAVED_TOPK_IDX]),
                              ws + W.tw, a->dtype, nullptr, probs ? grad_aux : nullptr,
                              probs && grad_aux ? b.counts : nullptr, aux_coef, a->n_tokens, E,
-                             a->top_k, route_flags, gl, ldg, s));
+                             a->top_k, route_flags, gl, ldg, s, fuse ? &pack : nullptr));
   if (!fuse) return NSMOE_OK;
   CombineDxArgs c;
   c.rows = ws + W.exp + experts_bwd_dxrows_offset(&b);
   c.inv = inv;
   c.glogits = gl;
-  c.w = w_router;
+  c.w = ws + W.wpk;
   c.dx = grads->dx;
   c.T = a->n_tokens;
   c.l_cap = b.l_cap;

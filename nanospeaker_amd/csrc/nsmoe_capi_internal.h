@@ -83,12 +83,23 @@ namespace nsmoe {
 int route_fwd_launch(const void* logits, int64_t n_tokens, int32_t n_experts, int32_t top_k,
                      int32_t flags, int32_t w_dtype, void* topk_w, int64_t* topk_idx,
                      float* probs, float* prob_colsum, hipStream_t stream);
-// route_bwd_launch: nsmoe_route_bwd with grad_logits rows of pitch ldg (pad columns zero).
+// The router weight W [d, E] (16-bit) packed as MFMA A-operand fragments for the router
+// term of combine_dx: fragment (mb, ks) = rows 16 mb .. + 15, k columns 32 ks .. + 31 (zero
+// past E or d) sits at bytes ((mb * nks + ks) * 64 + lane) * 16, lane l holding row
+// 16 mb + l % 16, columns 32 ks + 8 (l / 16) .. + 7.
+struct RouterWPack {
+  const void* w;
+  void* pk;
+  int d, E, nks;
+};
+inline size_t router_w_pack_bytes(int d, int nks) { return (size_t)((d + 15) / 16) * nks * 1024; }
+// route_bwd_launch: nsmoe_route_bwd with grad_logits rows of pitch ldg (pad columns zero);
+// with `pack` non-NULL (16-bit types) the launch also writes that pack, in extra workgroups.
 int route_bwd_launch(const void* src, const int64_t* topk_idx, const void* grad_w,
                      int32_t w_dtype, const float* grad_probs, const float* grad_aux,
                      const int32_t* aux_counts, float aux_coef, int64_t n_tokens,
                      int32_t n_experts, int32_t top_k, int32_t flags, void* grad_logits,
-                     int32_t ldg, hipStream_t stream);
+                     int32_t ldg, hipStream_t stream, const RouterWPack* pack = nullptr);
 int64_t balance_partial_count(int64_t n_tokens);
 // The balance loss folded into the dispatch (dispatch_launch): column-sum partials of probs
 // from route_fwd_launch ([nblk = balance_partial_count(T), E] fp32), T, coef -> aux[0].

@@ -581,14 +581,39 @@ route_fwd_kernel(const void* __restrict__ logits, int64_t T, int E, int k, int f
 // flags bit 2 (logits16): in the eval branches `src` is stored in DT, and grad_logits is
 // written in DT (the gradient of router.py:69's .float()); otherwise both are fp32.
 // grad_logits rows have pitch ldg >= E; the pad columns are written as zeros.
+// One 16-byte chunk of the router-weight pack (RouterWPack) per thread, chunk c.
+template <int DT>
+__device__ __forceinline__ void router_w_pack_chunk(const RouterWPack& pk, int64_t c) {
+  using T = typename Elem<DT>::T;
+  const int lane = (int)(c & 63);
+  const int64_t f = c >> 6;
+  const int ks = (int)(f % pk.nks), mb = (int)(f / pk.nks);
+  const int m = mb * 16 + (lane & 15), n = ks * 32 + 8 * (lane >> 4);
+  const T* w = (const T*)pk.w + (int64_t)m * pk.E;
+  T v[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = m < pk.d && n + e < pk.E ? w[n + e] : T(0);
+  uint4 o;
+  __builtin_memcpy(&o, v, 16);
+  *(uint4*)((char*)pk.pk + c * 16) = o;
+}
+
 template <int DT>
 __global__ void __launch_bounds__(ROUTE_THREADS)
 route_bwd_kernel(const void* __restrict__ src, const int64_t* __restrict__ topk_idx,
                  const typename Elem<DT>::T* __restrict__ grad_w,
                  const float* __restrict__ grad_probs, const float* __restrict__ grad_aux,
                  const int32_t* __restrict__ aux_counts, float aux_coef, int64_t T, int E,
-                 int k, int flags, void* __restrict__ grad_logits_v, int ldg) {
+                 int k, int flags, void* __restrict__ grad_logits_v, int ldg, RouterWPack pk,
+                 int64_t row_blocks) {
   extern __shared__ float lds_f[];
+  if ((int64_t)blockIdx.x >= row_blocks) {  // the extra workgroups: the router-weight pack
+    if constexpr (DT != DT_F32) {
+      const int64_t c = ((int64_t)blockIdx.x - row_blocks) * ROUTE_THREADS + threadIdx.x;
+      if (c < (int64_t)((pk.d + 15) / 16) * pk.nks * 64) router_w_pack_chunk<DT>(pk, c);
+    }
+    return;
+  }
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * ROUTE_WAVES + wave;
   if (row >= T) return;  // no workgroup barriers below: each wave works alone
@@ -798,7 +823,7 @@ int route_bwd_launch(const void* src, const int64_t* topk_idx, const void* grad_
                      int32_t w_dtype, const float* grad_probs, const float* grad_aux,
                      const int32_t* aux_counts, float aux_coef, int64_t n_tokens,
                      int32_t n_experts, int32_t top_k, int32_t flags, void* grad_logits,
-                     int32_t ldg, hipStream_t s) {
+                     int32_t ldg, hipStream_t s, const RouterWPack* pack) {
   NSMOE_REQUIRE(n_tokens >= 0, "route_bwd: n_tokens < 0");
   NSMOE_REQUIRE(n_experts >= 1 && n_experts <= ROUTE_MAX_EXPERTS,
                 "route_bwd: n_experts %d outside [1, %d]", n_experts, ROUTE_MAX_EXPERTS);
@@ -807,23 +832,30 @@ int route_bwd_launch(const void* src, const int64_t* topk_idx, const void* grad_
   if (n_tokens == 0) return NSMOE_OK;
   NSMOE_REQUIRE(src && topk_idx && grad_w && grad_logits, "route_bwd: NULL pointer");
   NSMOE_REQUIRE(!(flags & 4) || w_dtype != DT_F32, "route_bwd: 16-bit logits need a 16-bit dtype");
-  dim3 grid((unsigned)cdiv(n_tokens, ROUTE_WAVES)), block(ROUTE_THREADS);
+  NSMOE_REQUIRE(!pack || (w_dtype != DT_F32 && pack->w && pack->pk && pack->d > 0 &&
+                          pack->nks > 0 && pack->nks * 32 >= pack->E),
+                "route_bwd: bad router-weight pack");
+  const int64_t row_blocks = cdiv(n_tokens, ROUTE_WAVES);
+  const int64_t pack_blocks =
+      pack ? cdiv((int64_t)((pack->d + 15) / 16) * pack->nks * 64, ROUTE_THREADS) : 0;
+  const RouterWPack pk = pack ? *pack : RouterWPack{nullptr, nullptr, 0, 0, 1};
+  dim3 grid((unsigned)(row_blocks + pack_blocks)), block(ROUTE_THREADS);
   size_t lds = (size_t)n_experts * ROUTE_WAVES * sizeof(float) * 2;
   switch (w_dtype) {
     case DT_BF16:
       route_bwd_kernel<DT_BF16><<<grid, block, lds, s>>>(src, topk_idx, (const uint16_t*)grad_w,
           grad_probs, grad_aux, aux_counts, aux_coef, n_tokens, n_experts, top_k, flags,
-          grad_logits, ldg);
+          grad_logits, ldg, pk, row_blocks);
       break;
     case DT_F16:
       route_bwd_kernel<DT_F16><<<grid, block, lds, s>>>(src, topk_idx, (const uint16_t*)grad_w,
           grad_probs, grad_aux, aux_counts, aux_coef, n_tokens, n_experts, top_k, flags,
-          grad_logits, ldg);
+          grad_logits, ldg, pk, row_blocks);
       break;
     case DT_F32:
       route_bwd_kernel<DT_F32><<<grid, block, lds, s>>>(src, topk_idx, (const float*)grad_w,
           grad_probs, grad_aux, aux_counts, aux_coef, n_tokens, n_experts, top_k, flags,
-          grad_logits, ldg);
+          grad_logits, ldg, pk, row_blocks);
       break;
     default:
       NSMOE_REQUIRE(false, "route_bwd: unknown dtype %d", w_dtype);

@@ -12,7 +12,7 @@ struct CombineDxArgs {
   const void* rows;      // [rows_total, d] expert dX rows (routed slots, then shared)
   const int32_t* inv;    // [T, k] slot of each pair, -1 when dropped
   const void* glogits;   // [T, ep] d(logits), zero in the pad columns
-  const void* w;         // [d, E] router weight
+  const void* w;         // the router weight [d, E] packed as RouterWPack (nks = cdiv(ep, 32))
   void* dx;              // [T, d] output
   int64_t T, l_cap;
   int d, k, S, E, ep;

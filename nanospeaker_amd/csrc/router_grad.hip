@@ -25,6 +25,7 @@ constexpr int CDX_COLS = 64;  // columns of dx per combine_dx workgroup
 constexpr int CDX_PITCH = CDX_COLS + 4;  // fp32 LDS row pitch (4 banks of skew per row)
 constexpr int CDX_KMAX = 8;   // top_k and shared counts of the gather fast path
 constexpr int CDX_SMAX = 2;
+constexpr int CDX_KS = 4;    // k-steps of 32 experts in the router term (E <= 128)
 constexpr int RDW_RC = 256;   // tokens per router_dw chunk
 constexpr int RDW_BMT = 64;   // columns of x (rows of W) per router_dw tile
 constexpr int RDW_BNT = 128;  // experts per router_dw tile (all of them: E <= 128)
@@ -38,49 +39,83 @@ constexpr int RDW_S = 3;      // router_dw ring stages
 // token, written to the wave's LDS tile [16 tokens][64 columns] in fp32.  Epilogue: lane
 // (token l / 4, columns 16 (l % 4) .. + 15) adds its tile entries to the token's k + S
 // expert rows (two 16-byte loads per row) and stores dx with two 16-byte stores.
-// W rows have pitch E (E % 4 == 0): fragments are read as two 8-byte halves, a half past E
-// is zero.
-template <int DT>
-__global__ void __launch_bounds__(NT) combine_dx_kernel(CombineDxArgs a) {
+// W arrives packed in fragment order (RouterWPack: one 16-byte load per lane per fragment,
+// zero past E).
+template <int DT, int KM>
+__global__ void __launch_bounds__(NT, KM <= 6 ? 4 : 3) combine_dx_kernel(CombineDxArgs a) {
   using G = Geo<DT>;
   using T = typename G::T;
   using M = Mma<DT>;
   using Frag = typename M::Frag;
   __shared__ __attribute__((aligned(16))) float s_acc[4][16][CDX_PITCH];
+  __shared__ __attribute__((aligned(1024))) char s_w[4 * CDX_KS][1024];  // the W tile
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t t0 = (int64_t)blockIdx.x * CDX_TOK + 16 * wave;
   const int m0 = blockIdx.y * CDX_COLS;
-  const T* W = (const T*)a.w;
+  const char* WP = (const char*)a.w;
   const T* gl = (const T*)a.glogits;
   const int nks = (a.ep + 31) / 32;
+  const T* R = (const T*)a.rows;
+  // This lane's share of the sum: token t, columns c0 .. c0 + 15.
+  const int tt = lane >> 2, c0 = m0 + 16 * (lane & 3);
+  const int64_t t = t0 + tt;
+  const bool live = t < a.T && c0 < a.d;
+
+  // Load order: the router term's operands (the workgroup's W tile by LDS-DMA, this
+  // wave's g fragments), the slot indices, then the expert rows.  vmcnt retires in order:
+  // the wait for the slot indices covers the router operands, and the MFMAs then run
+  // while the rows are still in flight.
+  const int64_t tb = t0 + (lane & 15);  // this lane's token for the B operand
+  {
+    // Wave w copies the W fragments of row block w: LDS block w * nks + ks.
+    const int mbg = m0 / 16 + wave;
+    const uint32_t dst = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)&s_w[0][0] +
+                         wave * nks * 1024;
+    for (int ks = 0; ks < nks; ++ks) {
+      const void* src = mbg * 16 < a.d ? (const void*)(WP + ((int64_t)(mbg * nks + ks) * 64 + lane) * 16)
+                                      : (const void*)((const char*)g_zero_kib + lane * 16);
+      async_copy16_to(src, dst + ks * 1024);
+    }
+  }
+  Frag gb[CDX_KS];
+#pragma unroll
+  for (int ks = 0; ks < CDX_KS; ++ks) {
+    const int n = 32 * ks + 8 * (lane >> 4);
+    gb[ks] = M::zero();
+    if (ks < nks && tb < a.T && n < a.ep) gb[ks].v = *(const u32x4*)(gl + tb * a.ep + n);
+  }
+  // Up to KM routed rows and CDX_SMAX shared rows per token in registers (the fast path).
+  constexpr int NR = KM + CDX_SMAX;
+  const bool fast = a.k <= KM && a.S <= CDX_SMAX;
+  int32_t r[NR];  // row indices (the launcher checks that they fit 31 bits)
+#pragma unroll
+  for (int j = 0; j < KM; ++j) r[j] = fast && live && j < a.k ? a.inv[t * a.k + j] : -1;
+#pragma unroll
+  for (int q = 0; q < CDX_SMAX; ++q)
+    r[KM + q] = fast && live && q < a.S ? (int32_t)(a.l_cap + (int64_t)q * a.T + t) : -1;
+  wait_vmcnt<0>();  // the W copies, g and the slot indices
+  barrier_dma();    // every wave's W copies
+  u32x4 v[NR][2];
+#pragma unroll
+  for (int j = 0; j < NR; ++j) {
+    v[j][0] = v[j][1] = u32x4{0u, 0u, 0u, 0u};
+    if (r[j] >= 0) {
+      const u32x4* src = (const u32x4*)(R + (int64_t)r[j] * a.d + c0);
+      v[j][0] = src[0];
+      v[j][1] = src[1];
+    }
+  }
 
   f32x4 acc[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const int64_t tb = t0 + (lane & 15);  // this lane's token for the B operand
-  for (int ks = 0; ks < nks; ++ks) {
-    const int n = 32 * ks + 8 * (lane >> 4);
-    Frag b = M::zero();
-    if (tb < a.T && n < a.ep) b.v = *(const u32x4*)(gl + tb * a.ep + n);
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
-      const int m = m0 + 16 * mb + (lane & 15);
-      Frag w = M::zero();
-      if (m < a.d) {
-        const T* wr = W + (int64_t)m * a.E + n;
-        if (n < a.E) {
-          const uint2 lo = *(const uint2*)wr;
-          w.v[0] = lo.x;
-          w.v[1] = lo.y;
-        }
-        if (n + 4 < a.E) {
-          const uint2 hi = *(const uint2*)(wr + 4);
-          w.v[2] = hi.x;
-          w.v[3] = hi.y;
-        }
-      }
-      M::run(acc[mb], w, b);
+  for (int ks = 0; ks < CDX_KS; ++ks) {
+    if (ks < nks) {
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+        M::run(acc[mb], M::load(&s_w[0][0] + (mb * nks + ks) * 1024 + lane * 16), gb[ks]);
     }
   }
 #pragma unroll
@@ -90,17 +125,14 @@ __global__ void __launch_bounds__(NT) combine_dx_kernel(CombineDxArgs a) {
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-  const int tt = lane >> 2, c0 = m0 + 16 * (lane & 3);
-  const int64_t t = t0 + tt;
-  if (t >= a.T || c0 >= a.d) return;  // no barriers below
+  if (!live) return;  // no barriers below
   float sum[16];
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    const f32x4 v = *(const f32x4*)&s_acc[wave][tt][16 * (lane & 3) + 4 * q];
+    const f32x4 x = *(const f32x4*)&s_acc[wave][tt][16 * (lane & 3) + 4 * q];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) sum[4 * q + e] = v[e];
+    for (int e = 0; e < 4; ++e) sum[4 * q + e] = x[e];
   }
-  const T* R = (const T*)a.rows;
   auto add = [&](const u32x4& v0, const u32x4& v1) __attribute__((always_inline)) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -110,25 +142,7 @@ __global__ void __launch_bounds__(NT) combine_dx_kernel(CombineDxArgs a) {
       sum[8 + 2 * e + 1] += unpack2<DT>(v1[e], 1);
     }
   };
-  if (a.k <= CDX_KMAX && a.S <= CDX_SMAX) {
-    // Slot indices first, then every row's two chunks: all loads in flight together.
-    constexpr int NR = CDX_KMAX + CDX_SMAX;
-    int32_t r[NR];  // row indices (the launcher checks that they fit 31 bits)
-#pragma unroll
-    for (int j = 0; j < CDX_KMAX; ++j) r[j] = j < a.k ? a.inv[t * a.k + j] : -1;
-#pragma unroll
-    for (int q = 0; q < CDX_SMAX; ++q)
-      r[CDX_KMAX + q] = q < a.S ? (int32_t)(a.l_cap + (int64_t)q * a.T + t) : -1;
-    u32x4 v[NR][2];
-#pragma unroll
-    for (int j = 0; j < NR; ++j) {
-      v[j][0] = v[j][1] = u32x4{0u, 0u, 0u, 0u};
-      if (r[j] >= 0) {
-        const u32x4* src = (const u32x4*)(R + (int64_t)r[j] * a.d + c0);
-        v[j][0] = src[0];
-        v[j][1] = src[1];
-      }
-    }
+  if (fast) {
 #pragma unroll
     for (int j = 0; j < NR; ++j) add(v[j][0], v[j][1]);
   } else {
@@ -323,8 +337,13 @@ int combine_dx_launch(int dtype, const CombineDxArgs& a, hipStream_t s) {
                 (long long)(a.l_cap + (int64_t)a.S * a.T));
   const dim3 grid((unsigned)cdiv(a.T, CDX_TOK), (unsigned)cdiv(a.d, CDX_COLS));
   KernelTimer timer("combine_dx", s);
-  if (dtype == DT_BF16) combine_dx_kernel<DT_BF16><<<grid, NT, 0, s>>>(a);
-  else combine_dx_kernel<DT_F16><<<grid, NT, 0, s>>>(a);
+  if (a.k <= 6) {
+    if (dtype == DT_BF16) combine_dx_kernel<DT_BF16, 6><<<grid, NT, 0, s>>>(a);
+    else combine_dx_kernel<DT_F16, 6><<<grid, NT, 0, s>>>(a);
+  } else {
+    if (dtype == DT_BF16) combine_dx_kernel<DT_BF16, CDX_KMAX><<<grid, NT, 0, s>>>(a);
+    else combine_dx_kernel<DT_F16, CDX_KMAX><<<grid, NT, 0, s>>>(a);
+  }
   timer.stop();
   return check_launch("combine_dx_kernel");
 }
