@@ -772,11 +772,10 @@ __global__ void __launch_bounds__(NT) dw_kernel(ExpParams p) {
       }
 }
 
-// Sums the fp32 partials of multi-chunk groups in chunk order.  grid = (DWR_BLOCKS, group).
-// Each thread sums 4 consecutive elements (one 16-byte vector per chunk, chunk loads
-// issued 4 at a time), so the pass streams the partials at full width; the order of the
-// additions is the chunk order for every element, whatever the launch shape.
-constexpr int DWR_BLOCKS = 64;
+// Sums the fp32 partials of multi-chunk groups in chunk order.  grid = (dwr_blocks, group).
+// Each thread sums 4 consecutive elements (one 16-byte vector per chunk, every chunk's
+// load in flight at once), so the pass streams the partials at full width; the order of
+// the additions is the chunk order for every element, whatever the launch shape.
 
 template <int DT, int MODE>
 __device__ __forceinline__ void dw_reduce_group(const ExpParams& p, int g) {
@@ -813,8 +812,12 @@ __device__ __forceinline__ void dw_reduce_group(const ExpParams& p, int g) {
       for (int u = 0; u < DEPTH; ++u)
         if (c0 + u < nch) acc += a[u];
     }
+    if (DT != DT_F32 && ((uintptr_t)dst & 7) == 0) {  // one 8-byte store (mn % 4 == 0)
+      *(uint2*)(dst + i * 4) = make_uint2(pack2<DT>(acc[0], acc[1]), pack2<DT>(acc[2], acc[3]));
+    } else {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) dst[i * 4 + e] = Elem<DT>::from_f(acc[e]);
+      for (int e = 0; e < 4; ++e) dst[i * 4 + e] = Elem<DT>::from_f(acc[e]);
+    }
   }
   for (int64_t i = n4 * 4 + (int64_t)blockIdx.x * NT + threadIdx.x; i < mn;
        i += (int64_t)gridDim.x * NT) {
@@ -829,13 +832,53 @@ __global__ void __launch_bounds__(NT) dw_reduce_kernel(ExpParams p) {
   dw_reduce_group<DT, MODE>(p, blockIdx.y);
 }
 
-// Both modes in one launch: grid.y in [0, G) reduces dW_in groups, [G, 2G) dW_out groups.
+// Both modes in one launch, over the groups that can have several chunks.  grid.y in
+// [0, 2 NY), NY = S + routed_rows: mode = y / NY, row j = y % NY.  Rows j < S take shared
+// group E + j.  With routed_rows = E, row S + r takes routed group r; with routed_rows = 1
+// the one row S finds the routed groups of several chunks (usually none or a few: routed
+// groups average fewer rows than a chunk) and takes them in turn.  A launch over all
+// 2 (E + S) groups spends most of its time on workgroups that only find one chunk.
 template <int DT>
 __global__ void __launch_bounds__(NT) dw_reduce_pair_kernel(ExpParams p_in, ExpParams p_out,
-                                                            int G) {
-  const int gy = blockIdx.y;
-  if (gy < G) dw_reduce_group<DT, 0>(p_in, gy);
-  else dw_reduce_group<DT, 1>(p_out, gy - G);
+                                                            int routed_rows) {
+  const int E = p_in.E, S = p_in.S, ny = S + routed_rows;
+  const int mode = (int)blockIdx.y >= ny ? 1 : 0, j = (int)blockIdx.y - mode * ny;
+  auto run = [&](int g) {
+    if (mode == 0) dw_reduce_group<DT, 0>(p_in, g);
+    else dw_reduce_group<DT, 1>(p_out, g);
+  };
+  if (j < S) {
+    run(E + j);
+  } else if (routed_rows == E) {
+    run(j - S);
+  } else {
+    __shared__ int s_list[NT];
+    __shared__ int s_n;
+    for (int g0 = 0; g0 < E; g0 += NT) {
+      if (threadIdx.x == 0) s_n = 0;
+      __syncthreads();
+      const int g = g0 + (int)threadIdx.x;
+      if (g < E && dw_chunks(rows_of(p_in, g)) > 1) s_list[atomicAdd(&s_n, 1)] = g;
+      __syncthreads();
+      const int n = s_n;
+      for (int i = 0; i < n; ++i) run(s_list[i]);
+      __syncthreads();  // the list is read before the next round rewrites it
+    }
+  }
+}
+
+// Rows of routed groups in dw_reduce_pair_kernel's grid: one per routed group when an
+// average routed group comes near a chunk (many of them then have several), else one row
+// for all of them.
+static int dw_reduce_routed_rows(const nsmoe_experts_args* a) {
+  return a->n_tokens * a->top_k > (int64_t)a->n_experts * (DW_RC * 9 / 10) ? a->n_experts : 1;
+}
+
+// Workgroups per group of the dW reduce: one 16-byte vector of the larger dW per thread,
+// so every thread issues its chunk loads once.
+static unsigned dwr_blocks(const nsmoe_experts_args* a) {
+  const int64_t big = (int64_t)a->d_model * 2 * a->d_hidden;  // dW_in, the larger of the two
+  return (unsigned)std::min<int64_t>(cdiv(cdiv(big, 4), NT), 1024);
 }
 
 // Bias gradients: WHICH 0 -> db_in[g] = sum_r dA1[slot_r]; 1 -> db_out[g] = sum_r w_r dout[tok_r].
@@ -1051,8 +1094,9 @@ static int experts_dw(const nsmoe_experts_args* a, const ExpParams& p,
   const int prc = launch_dw_pair_async(DT, q_in, q_out, gc, s);
   if (prc != -1) {
     NSMOE_TRY(prc);
-    dim3 rg(DWR_BLOCKS, (unsigned)(2 * G));
-    dw_reduce_pair_kernel<DT><<<rg, NT, 0, s>>>(q_in, q_out, G);
+    const int rr = dw_reduce_routed_rows(a);
+    dim3 rg(dwr_blocks(a), (unsigned)(2 * (a->n_shared + rr)));
+    dw_reduce_pair_kernel<DT><<<rg, NT, 0, s>>>(q_in, q_out, rr);
     NSMOE_TRY(check_launch("dw_reduce_pair_kernel"));
   } else {
     {  // dW_in
@@ -1067,7 +1111,7 @@ static int experts_dw(const nsmoe_experts_args* a, const ExpParams& p,
         timer.stop();
         NSMOE_TRY(check_launch("dw_kernel<in>"));
       }
-      dim3 rg(DWR_BLOCKS, (unsigned)G);
+      dim3 rg(dwr_blocks(a), (unsigned)G);
       dw_reduce_kernel<DT, 0><<<rg, NT, 0, s>>>(q);
       NSMOE_TRY(check_launch("dw_reduce_kernel<in>"));
     }
@@ -1083,7 +1127,7 @@ static int experts_dw(const nsmoe_experts_args* a, const ExpParams& p,
         timer.stop();
         NSMOE_TRY(check_launch("dw_kernel<out>"));
       }
-      dim3 rg(DWR_BLOCKS, (unsigned)G);
+      dim3 rg(dwr_blocks(a), (unsigned)G);
       dw_reduce_kernel<DT, 1><<<rg, NT, 0, s>>>(q);
       NSMOE_TRY(check_launch("dw_reduce_kernel<out>"));
     }

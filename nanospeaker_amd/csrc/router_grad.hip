@@ -30,6 +30,7 @@ constexpr int RDW_RC = 256;   // tokens per router_dw chunk
 constexpr int RDW_BMT = 64;   // columns of x (rows of W) per router_dw tile
 constexpr int RDW_BNT = 128;  // experts per router_dw tile (all of them: E <= 128)
 constexpr int RDW_S = 3;      // router_dw ring stages
+constexpr int RDW_LOADS = 8;  // router_dw_reduce: partials in flight per lane
 
 // ---- combine_dx ----------------------------------------------------------------------------
 //
@@ -288,32 +289,41 @@ __global__ void __launch_bounds__(NT, 2) router_dw_kernel(RouterDwArgs a) {
   }
 }
 
-// W.grad[m][n] = sum over chunks c (in order) of partial[c][m][n], n < E, 4 n per thread.
+// W.grad[m][n] = sum over the chunks of partial[c][m][n], n < E.  Four lanes per 4-wide
+// output group: lane q sums chunks q, q + 4, q + 8, ... (RDW_LOADS of them in flight at a
+// time, in that order), then the four lane sums are added as (q0 + q1) + (q2 + q3): a fixed
+// order, so the result does not vary between runs.
 template <int DT>
 __global__ void __launch_bounds__(NT) router_dw_reduce_kernel(RouterDwArgs a, int nchunks) {
   using T = typename Elem<DT>::T;
   const int n4 = a.ep / 4;
-  const int64_t i = (int64_t)blockIdx.x * NT + threadIdx.x;
-  if (i >= (int64_t)a.d * n4) return;
-  const int m = (int)(i / n4), n = (int)(i % n4) * 4;
-  if (n >= a.E) return;
+  const int64_t i = ((int64_t)blockIdx.x * NT + threadIdx.x) >> 2;
+  const int q = threadIdx.x & 3;
+  const bool live = i < (int64_t)a.d * n4;
+  const int m = live ? (int)(i / n4) : 0, n = live ? (int)(i % n4) * 4 : 0;
   const int64_t mn = (int64_t)a.d * a.ep;
   const float* src = a.partial + (int64_t)m * a.ep + n;
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-  int c = 0;
-  for (; c + 4 <= nchunks; c += 4) {
-    const f32x4 v0 = *(const f32x4*)(src + (int64_t)c * mn);
-    const f32x4 v1 = *(const f32x4*)(src + (int64_t)(c + 1) * mn);
-    const f32x4 v2 = *(const f32x4*)(src + (int64_t)(c + 2) * mn);
-    const f32x4 v3 = *(const f32x4*)(src + (int64_t)(c + 3) * mn);
-    acc += v0;
-    acc += v1;
-    acc += v2;
-    acc += v3;
+  for (int c0 = q; c0 < nchunks; c0 += 4 * RDW_LOADS) {
+    f32x4 v[RDW_LOADS];
+#pragma unroll
+    for (int u = 0; u < RDW_LOADS; ++u) {
+      const int c = c0 + 4 * u;
+      v[u] = live && c < nchunks ? *(const f32x4*)(src + (int64_t)c * mn) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int u = 0; u < RDW_LOADS; ++u) acc += v[u];
   }
-  for (; c < nchunks; ++c) acc += *(const f32x4*)(src + (int64_t)c * mn);
-  *(uint2*)((T*)a.dw + (int64_t)m * a.E + n) =
-      make_uint2(pack2<DT>(acc[0], acc[1]), pack2<DT>(acc[2], acc[3]));
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float x1 = __shfl_xor(acc[e], 1, 64);  // (q0 + q1), (q2 + q3), in lane order
+    const float s01 = (q & 1) ? x1 + acc[e] : acc[e] + x1;
+    const float x2 = __shfl_xor(s01, 2, 64);
+    acc[e] = (q & 2) ? x2 + s01 : s01 + x2;
+  }
+  if (live && q == 0 && n < a.E)
+    *(uint2*)((T*)a.dw + (int64_t)m * a.E + n) =
+        make_uint2(pack2<DT>(acc[0], acc[1]), pack2<DT>(acc[2], acc[3]));
 }
 
 // ---- launchers ------------------------------------------------------------------------------
@@ -358,7 +368,7 @@ int router_dw_launch(int dtype, const RouterDwArgs& a, hipStream_t s) {
   if (dtype == DT_BF16) router_dw_kernel<DT_BF16><<<grid, NT, 0, s>>>(a);
   else router_dw_kernel<DT_F16><<<grid, NT, 0, s>>>(a);
   NSMOE_TRY(check_launch("router_dw_kernel"));
-  const int64_t nthreads = (int64_t)a.d * (a.ep / 4);
+  const int64_t nthreads = (int64_t)a.d * (a.ep / 4) * 4;
   const unsigned rblocks = (unsigned)cdiv(nthreads, NT);
   if (dtype == DT_BF16) router_dw_reduce_kernel<DT_BF16><<<rblocks, NT, 0, s>>>(a, (int)nchunks);
   else router_dw_reduce_kernel<DT_F16><<<rblocks, NT, 0, s>>>(a, (int)nchunks);

@@ -142,6 +142,26 @@ def test_backward_tile_heights_and_prefetch(mb, dist, bwd_dist, bwd_mb, shape, T
         check(f"grad {n}", g[n], ref_g[n], torch.bfloat16)
 
 
+def test_dw_reduce_skewed_routing():
+    """Routed experts average far fewer rows than a dW chunk (768), so the dW reduce takes
+    them in its one looping row; expert 0 still gets 900 rows (two chunks) and must be
+    summed there, beside the shared experts."""
+    d, E, d_ff = SHAPES["ns_h128"]
+    T = 1100
+    p, x, gout, tw, _ = make_case(d, E, d_ff, 2, 2, False, T, torch.bfloat16, seed=11)
+    t = torch.arange(T)
+    first = torch.where(t < 900, torch.zeros_like(t), 1 + t % (E - 1))
+    second = 1 + (t * 7 + 3) % (E - 1)
+    second = torch.where(second == first, 1 + (second % (E - 1)), second)
+    ti = torch.stack([first, second], 1).to(torch.int64)
+    assert (ti[:, 0] != ti[:, 1]).all() and (ti == 0).sum() == 900
+    ref_out, ref_g = oracle_fwd_bwd(p, x, gout, tw, ti, "silu")
+    out, g = gpu_fwd_bwd(p, x, gout, tw, ti, "silu")
+    check("out", out, ref_out, torch.bfloat16)
+    for n in ref_g:
+        check(f"grad {n}", g[n], ref_g[n], torch.bfloat16)
+
+
 @pytest.mark.parametrize("act", ["silu", "gelu", "relu", "sigmoid", "tanh"])
 @pytest.mark.parametrize("shape", ["tiny_h42", "ns_h128"])
 def test_every_activation(act, shape):
