@@ -40,16 +40,25 @@ constexpr int ROUTE_THREADS = 64 * ROUTE_WAVES;
 
 // ---- the row in registers --------------------------------------------------------------
 
+// The exact path compares keys as order-preserving unsigned integers: x ranks before y
+// ("x is NaN and y is not, or x > y", TopKImpl.h:68-69) iff ord_key(x) > ord_key(y).
+// Every NaN maps to the top and -0 to +0's image, so equal keys stay equal.  Integer keys
+// let the sequential steps compare in scalar registers (gfx950's scalar unit has no float
+// compare); the output values are read back from the untouched row by id.
+__device__ __forceinline__ uint32_t ord_key(float f) {
+  if (__builtin_isnan(f)) return 0xFFFFFFFFu;
+  uint32_t b = __float_as_uint(f);
+  if (b == 0x80000000u) b = 0u;
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
 struct KV {
-  float key;
+  uint32_t key;  // ord_key of the value
   int id;
 };
 
-// "x ranks before y": x is NaN and y is not, or x > y (TopKImpl.h:68-69).
-__device__ __forceinline__ bool gt(float a, float b) {
-  return (__builtin_isnan(a) && !__builtin_isnan(b)) || a > b;
-}
-__device__ __forceinline__ bool gt(KV x, KV y) { return gt(x.key, y.key); }
+__device__ __forceinline__ bool gt(uint32_t a, uint32_t b) { return a > b; }
+__device__ __forceinline__ bool gt(KV x, KV y) { return x.key > y.key; }
 
 // Lane `l` of v replaced by x (l wave-uniform): a compare and a select, the VALU
 // equivalent of v_writelane.
@@ -66,14 +75,14 @@ struct RegRow {
   __device__ __forceinline__ KV get(int i) const {
     const int l = i & 63;
     const int ka = rl(k0, l), kb = rl(k1, l), ia = rl(i0, l), ib = rl(i1, l);
-    return i < 64 ? KV{__int_as_float(ka), ia} : KV{__int_as_float(kb), ib};
+    return i < 64 ? KV{(uint32_t)ka, ia} : KV{(uint32_t)kb, ib};
   }
   // Both halves are written through selects (lane -1 matches no lane), so the compiler
   // keeps the four registers as registers instead of an indexed private array.
   __device__ __forceinline__ void set(int i, KV v) {
     const bool lo = i < 64;
     const int l0 = lo ? i : -1, l1 = lo ? -1 : i - 64;
-    const int kb = __float_as_int(v.key);
+    const int kb = (int)v.key;
     k0 = put_lane(k0, kb, l0, lane);
     i0 = put_lane(i0, v.id, l0, lane);
     k1 = put_lane(k1, kb, l1, lane);
@@ -261,13 +270,14 @@ __device__ __forceinline__ void sort_d(RegRow& a, int n) {
 // swapped slot stops the opposite scan).  So the loop makes i* = #{i : L[i] < R[i]}
 // swaps, all disjoint, and returns min(L[i*], R[i*-1]) (L[0] when i* = 0).
 // L[i] < R[i] <=> more than i right stoppers lie above L[i]: each lane tests its own
-// positions with ballots, exchanges partner positions through LDS and partner values
-// with ds_bpermute.  `pos` is the wave's [2][128] LDS scratch.
-__device__ __forceinline__ int partition_parallel(RegRow& a, int first, int last, int* pos) {
-  const float pk = a.get(first).key;
+// positions with ballots.  The swaps go through LDS: the element at L[i] (i < i*) is
+// written to slot i and the one at R[i] to slot 128 + i; then L[i] reads slot 128 + i
+// and R[i] reads slot i.  `kv` is the wave's [256] LDS scratch of (key, id) pairs.
+__device__ __forceinline__ int partition_parallel(RegRow& a, int first, int last, int2* kv) {
+  const uint32_t pk = a.get(first).key;
   const int lane = a.lane;
   const int p0 = lane, p1 = lane + 64;
-  const float x0 = __int_as_float(a.k0), x1 = __int_as_float(a.k1);
+  const uint32_t x0 = (uint32_t)a.k0, x1 = (uint32_t)a.k1;
   const bool isL0 = p0 > first && p0 < last && !gt(x0, pk);
   const bool isL1 = p1 > first && p1 < last && !gt(x1, pk);
   const bool isR0 = p0 >= first && p0 < last && !gt(pk, x0);
@@ -279,32 +289,29 @@ __device__ __forceinline__ int partition_parallel(RegRow& a, int first, int last
   const int rl0 = __popcll(bl0 & below), rl1 = __popcll(bl0) + __popcll(bl1 & below);
   const int ar0 = __popcll(br0 & above) + __popcll(br1), ar1 = __popcll(br1 & above);
   const int istar = __popcll(__ballot(isL0 && ar0 > rl0)) + __popcll(__ballot(isL1 && ar1 > rl1));
-  int* lpos = pos;
-  int* rpos = pos + 128;
   const bool sl0 = isL0 && rl0 < istar, sl1 = isL1 && rl1 < istar;
   const bool sr0 = isR0 && ar0 < istar, sr1 = isR1 && ar1 < istar;
-  if (sl0) lpos[rl0] = p0;
-  if (sl1) lpos[rl1] = p1;
-  if (sr0) rpos[ar0] = p0;
-  if (sr1) rpos[ar1] = p1;
+  if (sl0) kv[rl0] = make_int2(a.k0, a.i0);
+  if (sl1) kv[rl1] = make_int2(a.k1, a.i1);
+  if (sr0) kv[128 + ar0] = make_int2(a.k0, a.i0);
+  if (sr1) kv[128 + ar1] = make_int2(a.k1, a.i1);
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  const int q0 = sl0 ? rpos[rl0] : sr0 ? lpos[ar0] : p0;
-  const int q1 = sl1 ? rpos[rl1] : sr1 ? lpos[ar1] : p1;
-  const int ad0 = (q0 & 63) * 4, ad1 = (q1 & 63) * 4;
-  const int k00 = __builtin_amdgcn_ds_bpermute(ad0, a.k0), k01 = __builtin_amdgcn_ds_bpermute(ad0, a.k1);
-  const int i00 = __builtin_amdgcn_ds_bpermute(ad0, a.i0), i01 = __builtin_amdgcn_ds_bpermute(ad0, a.i1);
-  const int k10 = __builtin_amdgcn_ds_bpermute(ad1, a.k0), k11 = __builtin_amdgcn_ds_bpermute(ad1, a.k1);
-  const int i10 = __builtin_amdgcn_ds_bpermute(ad1, a.i0), i11 = __builtin_amdgcn_ds_bpermute(ad1, a.i1);
-  // the next round's writes to pos must not overtake these reads
+  if (sl0 || sr0) {
+    const int2 v = kv[sl0 ? 128 + rl0 : ar0];
+    a.k0 = v.x;
+    a.i0 = v.y;
+  }
+  if (sl1 || sr1) {
+    const int2 v = kv[sl1 ? 128 + rl1 : ar1];
+    a.k1 = v.x;
+    a.i1 = v.y;
+  }
+  // the next round's writes to kv must not overtake these reads
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  a.k0 = q0 < 64 ? k00 : k01;
-  a.i0 = q0 < 64 ? i00 : i01;
-  a.k1 = q1 < 64 ? k10 : k11;
-  a.i1 = q1 < 64 ? i10 : i11;
   if (istar == 0) return bl0 ? __ffsll((long long)bl0) - 1 : 63 + __ffsll((long long)bl1);
   const uint64_t n0 = __ballot(isL0 && rl0 == istar), n1 = __ballot(isL1 && rl1 == istar);
   const uint64_t m0 = __ballot(isR0 && ar0 == istar - 1), m1 = __ballot(isR1 && ar1 == istar - 1);
@@ -326,10 +333,10 @@ __device__ __forceinline__ void stable_sort_d(RegRow& a, int first, int last) {
   }
   const int p = a.lane;
   const bool in = p >= first && p < last;
-  const float kp = __int_as_float(a.k0);
+  const uint32_t kp = (uint32_t)a.k0;
   int rank = first;
   for (int q = first; q < last; ++q) {
-    const float kq = __int_as_float(rl(a.k0, q));
+    const uint32_t kq = (uint32_t)rl(a.k0, q);
     rank += (in && (gt(kq, kp) || (q < p && !gt(kp, kq)))) ? 1 : 0;
   }
   const int dst = (in ? rank : p) * 4;
@@ -339,7 +346,7 @@ __device__ __forceinline__ void stable_sort_d(RegRow& a, int first, int last) {
 
 // nth_element (introselect) with the partitions and the final insertion sort done
 // wave-parallel; the heap-select fallback at depth 0 stays sequential.
-__device__ __forceinline__ void nth_element_par(RegRow& a, int nth, int n, int* pos) {
+__device__ __forceinline__ void nth_element_par(RegRow& a, int nth, int n, int2* pos) {
   if (n == 0 || nth == n) return;
   int first = 0, last = n, depth = lg2i(n) * 2;
   while (last - first > 3) {
@@ -359,7 +366,7 @@ __device__ __forceinline__ void nth_element_par(RegRow& a, int nth, int n, int* 
 
 // torch CPU topk(largest=True, sorted=True) over the row: afterwards a[0, k) holds the
 // selected (key, id) pairs in output order.
-__device__ __forceinline__ void topk_select(RegRow& a, int n, int k, int* pos) {
+__device__ __forceinline__ void topk_select(RegRow& a, int n, int k, int2* pos) {
   if (k * 64 <= n) {
     heap_select_d(a, 0, k, n);
     sort_heap_d(a, 0, k);
@@ -389,7 +396,7 @@ route_fwd_kernel(const void* __restrict__ logits, int64_t T, int E, int k, int f
                  typename Elem<DT>::T* __restrict__ topk_w, int64_t* __restrict__ topk_idx,
                  float* __restrict__ probs, float* __restrict__ prob_colsum) {
   __shared__ float s_col[RF_WAVES][ROUTE_MAX_EXPERTS];
-  __shared__ int s_pos[RF_WAVES][2 * ROUTE_MAX_EXPERTS];  // exact path: partner positions
+  __shared__ int2 s_pos[RF_WAVES][2 * ROUTE_MAX_EXPERTS];  // exact path: swap slots
   using OutT = typename Elem<DT>::T;
   // readfirstlane: the compiler then knows the wave index, and every row condition
   // below, is wave-uniform (scalar branches, not exec masks).
@@ -546,9 +553,15 @@ route_fwd_kernel(const void* __restrict__ logits, int64_t T, int E, int k, int f
         m = rmax[u];
         inv = rinv[u];
       }
-    RegRow r{__float_as_int(k0), __float_as_int(k1), lane, lane + 64, lane};
+    RegRow r{(int)ord_key(k0), (int)ord_key(k1), lane, lane + 64, lane};
     topk_select(r, E, k, s_pos[wave]);
-    write_out(row0 + (int64_t)j * RF_WAVES, __int_as_float(r.k0), __int_as_float(r.k1), r.i0,
+    // The selected values, bit for bit, from the row as loaded (element id of output j).
+    const int a0 = (r.i0 & 63) * 4, a1 = (r.i1 & 63) * 4;
+    const float lo0 = __int_as_float(__builtin_amdgcn_ds_bpermute(a0, __float_as_int(k0)));
+    const float hi0 = __int_as_float(__builtin_amdgcn_ds_bpermute(a0, __float_as_int(k1)));
+    const float lo1 = __int_as_float(__builtin_amdgcn_ds_bpermute(a1, __float_as_int(k0)));
+    const float hi1 = __int_as_float(__builtin_amdgcn_ds_bpermute(a1, __float_as_int(k1)));
+    write_out(row0 + (int64_t)j * RF_WAVES, r.i0 < 64 ? lo0 : hi0, r.i1 < 64 ? lo1 : hi1, r.i0,
               r.i1, m, inv);
   }
 
