@@ -177,7 +177,7 @@ KERNEL_SYMBOLS = {
     "route_fwd": ("nsmoe::route_fwd_kernel",),
     "combine": ("nsmoe::combine_kernel",),
     "combine_dx": ("nsmoe::combine_dx_kernel",),
-    "pack": ("nsmoe::pack_kernel",),
+    "pack": ("nsmoe::pack_kernel", "nsmoe::pack_ks_kernel"),
     "dispatch": ("nsmoe::dispatch_hist_kernel", "nsmoe::dispatch_place_kernel"),
     "router_dw": ("nsmoe::router_dw_kernel", "nsmoe::router_dw_reduce_kernel"),
 }

@@ -136,11 +136,7 @@ dispatch_place_kernel(const int64_t* __restrict__ topk_idx, int64_t M, int E,
     const int e = e0 + i;
     if (e < E) local += (s_tot[e] + ALIGN_M - 1) / ALIGN_M * ALIGN_M;
   }
-  int32_t incl = local;
-  for (int o = 1; o < 64; o <<= 1) {
-    const int32_t v = __shfl_up(incl, o, 64);
-    if (lane >= o) incl += v;
-  }
+  const int32_t incl = wave_scan_incl(local);
   if (lane == 63) s_wave[wave] = incl;
   if (e_mine >= 0) atomicOr(&s_mask[wave * E + e_mine], 1ull << lane);
   __syncthreads();

@@ -441,20 +441,6 @@ struct Located {
   int aux;  // prefix of aux(g) over the groups before g
 };
 
-// Inclusive prefix sum over the wave's 64 lanes: Hillis-Steele inside each 16-lane row
-// (DPP row_shr 1, 2, 4, 8), then row 0's total into row 1 and row 2's into row 3
-// (row_bcast:15), then rows 0-1's total into rows 2 and 3 (row_bcast:31).  Lanes a DPP
-// move does not write read 0 (the `old` operand).
-__device__ __forceinline__ int wave_scan_incl(int v) {
-  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);  // row_shr:1
-  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);  // row_shr:2
-  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4
-  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);  // row_shr:8
-  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15
-  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31
-  return v;
-}
-
 template <class Units, class Aux>
 __device__ __forceinline__ bool locate(int item, int G, Units units, Aux aux, int* s_loc,
                                        Located& out) {

@@ -61,6 +61,75 @@ pack_kernel(const typename Elem<DT>::T* __restrict__ routed,
   __builtin_memcpy(dst, &f, sizeof(f));
 }
 
+// 16-bit types: one workgroup packs KS k blocks of one 64-column tile.  Thread t < 32 KS
+// loads the 8 x 8 block (t % 32) of k block t / 32 (every load of the workgroup in flight
+// at once) and transposes it into that k block's LDS tile; after a barrier wave w writes
+// fragment (4 nt + w, kb) of each k block.  A workgroup per k block keeps only 32 threads
+// and 4 KB of loads in flight, which leaves the pass at about half of HBM's rate.
+template <int DT, int MODE, int KS>
+__global__ void __launch_bounds__(256)
+pack_ks_kernel(const typename Elem<DT>::T* __restrict__ routed,
+               const typename Elem<DT>::T* __restrict__ shared, int E, int d, int H, int HP,
+               int n_kb, int n_nb, char* __restrict__ out, int fast) {
+  using G = Geo<DT>;
+  using T = typename G::T;
+  static_assert(G::ES == 2 && KS * 32 <= 256, "16-bit types, at most 8 k blocks");
+  __shared__ __attribute__((aligned(16))) char tile[KS][64 * G::ROWB];
+  const int g = blockIdx.z, nt = blockIdx.y, kb0 = blockIdx.x * KS;
+  const int K = MODE == 0 ? d : H;
+  const int ld = MODE == 0 ? 2 * H : d;
+  const int64_t gstride = MODE == 0 ? (int64_t)d * 2 * H : (int64_t)H * d;
+  const T* W = g < E ? routed + (int64_t)g * gstride : shared + (int64_t)(g - E) * gstride;
+  int n0, nlim;
+  if (MODE == 0) {
+    const int c0 = nt * 64;  // packed column of the tile
+    if (c0 < HP) {
+      n0 = c0;
+      nlim = H;
+    } else {
+      n0 = H + (c0 - HP);
+      nlim = 2 * H;
+    }
+  } else {
+    n0 = nt * 64;
+    nlim = d;
+  }
+  // This thread's 8 x 8 block: rows kb * 32 + kbl * 8 + r, columns n0 + nbl * 8 .. + 7 (the
+  // block numbering of TransStage: k block blk % 4, n block blk / 4).
+  const int step = threadIdx.x >> 5, blk = threadIdx.x & 31;
+  const int kbl = blk & 3, nbl = blk >> 2;
+  const int kb = kb0 + step;
+  const bool on = step < KS && kb < n_kb;
+  const int col = n0 + nbl * G::VE;
+  u32x4 v[G::VE];
+#pragma unroll
+  for (int r = 0; r < G::VE; ++r) {
+    v[r] = u32x4{0u, 0u, 0u, 0u};
+    const int k = kb * G::KC + kbl * G::VE + r;
+    if (!on || k >= K) continue;
+    const T* src = W + (int64_t)k * ld;
+    if (fast) {
+      if (col < nlim) v[r] = *(const u32x4*)(src + col);
+    } else {
+      T tmp[G::VE];
+#pragma unroll
+      for (int e = 0; e < G::VE; ++e) tmp[e] = (col + e < nlim) ? src[col + e] : T(0);
+      __builtin_memcpy(&v[r], tmp, 16);
+    }
+  }
+  if (on) store_trans8<DT>(v, tile[step], nbl, kbl);
+  __syncthreads();
+  const int wave = threadIdx.x >> 6;
+  const int nb = nt * 4 + wave;
+#pragma unroll
+  for (int st = 0; st < KS; ++st) {
+    if (kb0 + st >= n_kb) break;
+    const typename Mma<DT>::Frag f = frag_sw<DT>(tile[st], wave * 16);
+    char* dst = out + (((int64_t)g * n_nb + nb) * n_kb + kb0 + st) * G::PKB + lane_id() * G::FRAGB;
+    __builtin_memcpy(dst, &f, sizeof(f));
+  }
+}
+
 PackGeom pack_geom(int dtype, int d, int H, int E, int S) {
   PackGeom pg;
   const int es = dtype == DT_F32 ? 4 : 2;
@@ -85,17 +154,34 @@ static int launch_pack(const PackGeom& pg, const void* w_in, const void* w_out,
   const int G = E + S;
   {
     KernelTimer timer("pack", s);
-    dim3 grid((unsigned)pg.in_kb, (unsigned)(pg.in_nb / 4), (unsigned)G);
-    pack_kernel<DT, 0><<<grid, 256, 0, s>>>((const T*)w_in, (const T*)w_sh_in, E, d, H, pg.hp,
-                                           pg.in_kb, pg.in_nb, (char*)p_in, fast ? 1 : 0);
+    if constexpr (DT != DT_F32) {
+      constexpr int KS = 6;
+      dim3 grid((unsigned)cdiv(pg.in_kb, KS), (unsigned)(pg.in_nb / 4), (unsigned)G);
+      pack_ks_kernel<DT, 0, KS><<<grid, 256, 0, s>>>((const T*)w_in, (const T*)w_sh_in, E, d,
+                                                     H, pg.hp, pg.in_kb, pg.in_nb, (char*)p_in,
+                                                     fast ? 1 : 0);
+    } else {
+      dim3 grid((unsigned)pg.in_kb, (unsigned)(pg.in_nb / 4), (unsigned)G);
+      pack_kernel<DT, 0><<<grid, 256, 0, s>>>((const T*)w_in, (const T*)w_sh_in, E, d, H,
+                                             pg.hp, pg.in_kb, pg.in_nb, (char*)p_in,
+                                             fast ? 1 : 0);
+    }
     timer.stop();
     NSMOE_TRY(check_launch("pack_kernel<w_in>"));
   }
   if (p_out) {
-    dim3 grid((unsigned)pg.out_kb, (unsigned)(pg.out_nb / 4), (unsigned)G);
-    pack_kernel<DT, 1><<<grid, 256, 0, s>>>((const T*)w_out, (const T*)w_sh_out, E, d, H,
-                                           pg.hp, pg.out_kb, pg.out_nb, (char*)p_out,
-                                           fast ? 1 : 0);
+    if constexpr (DT != DT_F32) {
+      constexpr int KS = 4;
+      dim3 grid((unsigned)cdiv(pg.out_kb, KS), (unsigned)(pg.out_nb / 4), (unsigned)G);
+      pack_ks_kernel<DT, 1, KS><<<grid, 256, 0, s>>>((const T*)w_out, (const T*)w_sh_out, E, d,
+                                                     H, pg.hp, pg.out_kb, pg.out_nb,
+                                                     (char*)p_out, fast ? 1 : 0);
+    } else {
+      dim3 grid((unsigned)pg.out_kb, (unsigned)(pg.out_nb / 4), (unsigned)G);
+      pack_kernel<DT, 1><<<grid, 256, 0, s>>>((const T*)w_out, (const T*)w_sh_out, E, d, H,
+                                             pg.hp, pg.out_kb, pg.out_nb, (char*)p_out,
+                                             fast ? 1 : 0);
+    }
     NSMOE_TRY(check_launch("pack_kernel<w_out>"));
   }
   return NSMOE_OK;
