@@ -128,8 +128,7 @@ def time_gpu(m, x, g, steps: int, warmup: int):
     # Per-kernel launch times, from the library's HIP-event pairs on the launch stream, in a
     # pass of its own on one stream, so that no other kernel shares the GPU with the one
     # being timed.
-    prev = os.environ.get("NSMOE_SINGLE_STREAM")
-    os.environ["NSMOE_SINGLE_STREAM"] = "1"
+    nat.set_option("single_stream", 1)
     try:
         step()
         torch.cuda.synchronize()
@@ -146,10 +145,7 @@ def time_gpu(m, x, g, steps: int, warmup: int):
                 kernels[name] = (tot / n, n // steps)
         nat.timing_enable(0)
     finally:
-        if prev is None:
-            del os.environ["NSMOE_SINGLE_STREAM"]
-        else:
-            os.environ["NSMOE_SINGLE_STREAM"] = prev
+        nat.set_option("single_stream", 0)
 
     # forward only (train mode, no autograd)
     with torch.no_grad():

@@ -54,6 +54,24 @@ int32_t nsmoe_abi_version(void);
 int nsmoe_timing_enable(int32_t capacity);
 int nsmoe_timing_read(const char* kernel_name, double* total_ms, int64_t* launches);
 
+/* Tuning options (no counterpart in the reference; for tests and measurements).  Each is
+ * process-wide, starts at 0 (= the library's own choice) and applies to calls made after
+ * it is set.  Names and accepted values:
+ *   "single_stream"  1: keep every kernel of a call on the caller's stream (no second
+ *                    stream for the weight packing or the dW stage)
+ *   "fwd_rows"       rows per tile of the 16-bit forward expert kernel: 64 or 96
+ *   "fwd_dist"       its weight prefetch distance in k-steps: 2 or 3
+ *   "bwd_rows"       rows per tile of the GLU-backward kernel: 48, 64 or 80
+ *   "bwd_dist"       its prefetch distance: 2 or 3
+ *   "dx_rows"        rows per tile of the dX kernel: 64 or 96
+ *   "dx_dist"        its prefetch distance: 2, 3 or 4
+ *   "xcd_run"        tiles of one group dealt to one XCD in a row: 1 .. 1024
+ * A value that does not fit a shape falls back to the library's choice for that call.
+ * nsmoe_set_option returns 1 for an unknown name or a value out of range (0 always
+ * restores the default); nsmoe_get_option returns -1 for an unknown name. */
+int nsmoe_set_option(const char* name, int64_t value);
+int64_t nsmoe_get_option(const char* name);
+
 /* ---- router tail ----------------------------------------------------------------------
  * Replaces the softmax / topk / renormalise / cast tail of TopKRouter.forward
  * (src/model/router.py:79-98); the logits GEMM `(x @ W)` (router.py:69) is the caller's.
@@ -221,14 +239,20 @@ int nsmoe_experts_bwd(const nsmoe_experts_args* args, const int32_t* inv,
  * d(logits) W^T, grad_w_router gets x^T d(logits)) or left to the caller (w_router NULL:
  * grad_logits receives d(logits)).
  *
- * `args` carries dims, dtype, activation, x, weights and biases; its routing pointers
- * (topk_w, sorted_ids, pad_offsets, counts, w_in_packed, w_out_packed) and l_cap are
- * ignored -- the calls place them in `saved`.
+ * `args` carries dims, dtype, activation, x, weights, biases and the packed weights
+ * (w_in_packed, w_out_packed: nsmoe_pack_weights layout, both required by the forward,
+ * w_in_packed by the backward); its routing pointers (topk_w, sorted_ids, pad_offsets,
+ * counts) and l_cap are ignored -- the calls place them in `saved`.  With
+ * NSMOE_BLOCK_PACK in route_flags the forward first packs the weights into
+ * w_in_packed / w_out_packed itself (on a second stream, beside the routing kernels);
+ * without it they must hold the current weights already, so a caller that keeps the
+ * packs while the weights do not change skips that pass.
  *
  * `saved` (nsmoe_block_saved_layout: total bytes and the offset of each part) is written
- * by the forward and read by the backward: topk_w [T, k] (args dtype), topk_idx [T, k]
- * int64, probs [T, E] fp32 (train branch only), the dispatch buffers of nsmoe_dispatch,
- * and the packed weights.
+ * by the forward and read by the backward: topk_w [T, k] (args dtype), probs [T, E] fp32
+ * (train branch only) and the dispatch buffers of nsmoe_dispatch.  The expert ids
+ * topk_idx [T, k] int64 and the routing counts [E] int32 are separate caller buffers
+ * (MoEBlock keeps both after the step), written by the forward and read by the backward.
  *
  * Forward: out [T, d]; aux [1] fp32 = the balance loss (train branch, route_flags has
  * NSMOE_ROUTE_PROBS; otherwise untouched).  Backward: grads as nsmoe_experts_bwd
@@ -243,32 +267,32 @@ int nsmoe_experts_bwd(const nsmoe_experts_args* args, const int32_t* inv,
  *     d(logits) as nsmoe_route_bwd writes it, grad_w_router is unused; workspace
  *     nsmoe_block_bwd_workspace_size(args, route_flags, 0).
  */
+#define NSMOE_BLOCK_PACK 8
+
 #define NSMOE_SAVED_TOPK_W 0
-#define NSMOE_SAVED_TOPK_IDX 1
-#define NSMOE_SAVED_PROBS 2
-#define NSMOE_SAVED_SORTED_IDS 3
-#define NSMOE_SAVED_EXPERT_IDS 4
-#define NSMOE_SAVED_PAD_OFFSETS 5
-#define NSMOE_SAVED_COUNTS 6
-#define NSMOE_SAVED_N_POST_PAD 7
-#define NSMOE_SAVED_INV 8
-#define NSMOE_SAVED_W_IN_PACKED 9
-#define NSMOE_SAVED_W_OUT_PACKED 10
-#define NSMOE_BLOCK_NSAVED 11
+#define NSMOE_SAVED_PROBS 1
+#define NSMOE_SAVED_SORTED_IDS 2
+#define NSMOE_SAVED_EXPERT_IDS 3
+#define NSMOE_SAVED_PAD_OFFSETS 4
+#define NSMOE_SAVED_N_POST_PAD 5
+#define NSMOE_SAVED_INV 6
+#define NSMOE_BLOCK_NSAVED 7
 
 int nsmoe_block_saved_layout(const nsmoe_experts_args* args, int32_t route_flags,
                              size_t* offsets /* [NSMOE_BLOCK_NSAVED] */, size_t* total_bytes);
 size_t nsmoe_block_fwd_workspace_size(const nsmoe_experts_args* args, int32_t route_flags);
 int nsmoe_block_fwd(const nsmoe_experts_args* args, const void* logits, int32_t route_flags,
-                    float aux_coef, void* saved, void* out, float* aux, void* workspace,
-                    size_t workspace_bytes, void* stream);
+                    float aux_coef, void* saved, int64_t* topk_idx, int32_t* counts,
+                    void* out, float* aux, void* workspace, size_t workspace_bytes,
+                    void* stream);
 size_t nsmoe_block_bwd_workspace_size(const nsmoe_experts_args* args, int32_t route_flags,
                                       int32_t fuse_router);
 int nsmoe_block_bwd(const nsmoe_experts_args* args, const void* logits, int32_t route_flags,
-                    float aux_coef, const void* saved, const void* grad_out,
-                    const float* grad_aux, const nsmoe_experts_grads* grads,
-                    const void* w_router, void* grad_w_router, void* grad_logits,
-                    void* workspace, size_t workspace_bytes, void* stream);
+                    float aux_coef, const void* saved, const int64_t* topk_idx,
+                    const int32_t* counts, const void* grad_out, const float* grad_aux,
+                    const nsmoe_experts_grads* grads, const void* w_router,
+                    void* grad_w_router, void* grad_logits, void* workspace,
+                    size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -8,14 +8,13 @@ moe_kernel.py goes through it.
 from __future__ import annotations
 
 import ctypes
-import os
 from pathlib import Path
 
-LIB_PATH = Path(os.environ.get("NSMOE_LIB", Path(__file__).resolve().parent / "libnsmoe.so"))
+LIB_PATH = Path(__file__).resolve().parent / "libnsmoe.so"
 
 BF16, F16, F32 = 0, 1, 2
-ROUTE_PROBS, ROUTE_NORMALIZE, ROUTE_LOGITS16 = 1, 2, 4
-ABI_VERSION = 3
+ROUTE_PROBS, ROUTE_NORMALIZE, ROUTE_LOGITS16, BLOCK_PACK = 1, 2, 4, 8
+ABI_VERSION = 4
 
 # Every symbol include/nsmoe.h declares, with (restype, argtypes).
 _vp, _i32, _i64, _sz = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t
@@ -50,6 +49,8 @@ SIGNATURES = {
     "nsmoe_timing_enable": (ctypes.c_int, [_i32]),
     "nsmoe_timing_read": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double),
                                          ctypes.POINTER(_i64)]),
+    "nsmoe_set_option": (ctypes.c_int, [ctypes.c_char_p, _i64]),
+    "nsmoe_get_option": (_i64, [ctypes.c_char_p]),
     "nsmoe_route_fwd": (ctypes.c_int, [_vp, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
     "nsmoe_route_bwd": (ctypes.c_int, [_vp, _vp, _vp, _i32, _vp, _vp, _vp, ctypes.c_float, _i64,
                                        _i32, _i32, _i32, _vp, _vp]),
@@ -72,15 +73,15 @@ SIGNATURES = {
                                                 ctypes.POINTER(_sz), ctypes.POINTER(_sz)]),
     "nsmoe_block_fwd_workspace_size": (_sz, [ctypes.POINTER(ExpertsArgs), _i32]),
     "nsmoe_block_fwd": (ctypes.c_int, [ctypes.POINTER(ExpertsArgs), _vp, _i32, ctypes.c_float,
-                                       _vp, _vp, _vp, _vp, _sz, _vp]),
+                                       _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "nsmoe_block_bwd_workspace_size": (_sz, [ctypes.POINTER(ExpertsArgs), _i32, _i32]),
     "nsmoe_block_bwd": (ctypes.c_int, [ctypes.POINTER(ExpertsArgs), _vp, _i32, ctypes.c_float,
-                                       _vp, _vp, _vp, ctypes.POINTER(ExpertsGrads), _vp, _vp,
-                                       _vp, _vp, _sz, _vp]),
+                                       _vp, _vp, _vp, _vp, _vp, ctypes.POINTER(ExpertsGrads),
+                                       _vp, _vp, _vp, _vp, _sz, _vp]),
 }
 
 # Parts of the block's `saved` buffer (NSMOE_SAVED_* in nsmoe.h).
-SAVED_TOPK_W, SAVED_TOPK_IDX, SAVED_PROBS, SAVED_COUNTS, BLOCK_NSAVED = 0, 1, 2, 6, 11
+SAVED_TOPK_W, SAVED_PROBS, SAVED_INV, BLOCK_NSAVED = 0, 1, 6, 7
 
 
 class NativeLibraryError(RuntimeError):
@@ -134,6 +135,18 @@ def launch_count() -> int:
 def timing_enable(capacity: int) -> None:
     """Start recording HIP event pairs around the library's kernels (0 stops)."""
     check(lib().nsmoe_timing_enable(capacity), "nsmoe_timing_enable")
+
+
+def set_option(name: str, value: int) -> None:
+    """A process-wide tuning option of the library (nsmoe_set_option; 0 = its default)."""
+    check(lib().nsmoe_set_option(name.encode(), int(value)), f"nsmoe_set_option({name})")
+
+
+def get_option(name: str) -> int:
+    v = int(lib().nsmoe_get_option(name.encode()))
+    if v < 0:
+        raise NativeLibraryError(f"unknown option {name!r}")
+    return v
 
 
 def timing_read(kernel: str) -> "tuple[float, int]":

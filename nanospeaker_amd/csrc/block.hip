@@ -9,9 +9,11 @@
 // two caller allocations, so a framework pays one host call per direction instead of
 // one per stage.
 //
-// `saved` holds what the forward produces and the backward reads again (routing, the
-// dispatch buffers, the packed weights); its layout is reported by
-// nsmoe_block_saved_layout.  `workspace` is scratch for one call.
+// `saved` holds what the forward produces and the backward reads again (gates, probs and
+// the dispatch buffers); its layout is reported by nsmoe_block_saved_layout.  The expert
+// ids and routing counts are separate caller buffers, because callers keep them past the
+// step, and the packed weights are the caller's too, so a caller can keep them across
+// calls while the weights do not change.  `workspace` is scratch for one call.
 #include <string.h>
 
 #include "experts_common.h"
@@ -33,19 +35,14 @@ static BlockLayout block_layout(const nsmoe_experts_args* a, int32_t flags) {
   const size_t es = a->dtype == DT_F32 ? 4 : 2;
   const int64_t m = (int64_t)(T * k);
   const size_t l_cap = (size_t)nsmoe_dispatch_l_cap(m, (int32_t)E);
-  const PackGeom pg = pack_geom(a->dtype, a->d_model, a->d_hidden, a->n_experts, a->n_shared);
   const size_t sizes[NSMOE_BLOCK_NSAVED] = {
       T * k * es,                                   // topk_w
-      T * k * 8,                                    // topk_idx
       (flags & NSMOE_ROUTE_PROBS) ? T * E * 4 : 0,  // probs
       l_cap * 4,                                    // sorted_ids
       (l_cap / (size_t)nsmoe_align_m()) * 4,        // expert_ids
       (E + 1) * 4,                                  // pad_offsets
-      E * 4,                                        // counts
       4,                                            // n_post_pad
       T * k * 4,                                    // inv
-      pg.in_bytes,                                  // packed W_in
-      pg.out_bytes,                                 // packed W_out
   };
   BlockLayout L;
   size_t o = 0;
@@ -57,17 +54,16 @@ static BlockLayout block_layout(const nsmoe_experts_args* a, int32_t flags) {
   return L;
 }
 
-// Points a copy of the caller's args at the routing state inside `saved`.
+// Points a copy of the caller's args at the routing state inside `saved` and at the
+// routing counts.
 static nsmoe_experts_args with_routing(const nsmoe_experts_args* a, const BlockLayout& L,
-                                       char* saved) {
+                                       char* saved, const int32_t* counts) {
   nsmoe_experts_args b = *a;
   b.l_cap = nsmoe_dispatch_l_cap(a->n_tokens * a->top_k, a->n_experts);
   b.topk_w = saved + L.off[NSMOE_SAVED_TOPK_W];
   b.sorted_ids = (const int32_t*)(saved + L.off[NSMOE_SAVED_SORTED_IDS]);
   b.pad_offsets = (const int32_t*)(saved + L.off[NSMOE_SAVED_PAD_OFFSETS]);
-  b.counts = (const int32_t*)(saved + L.off[NSMOE_SAVED_COUNTS]);
-  b.w_in_packed = saved + L.off[NSMOE_SAVED_W_IN_PACKED];
-  b.w_out_packed = saved + L.off[NSMOE_SAVED_W_OUT_PACKED];
+  b.counts = counts;
   return b;
 }
 
@@ -105,16 +101,17 @@ extern "C" size_t nsmoe_block_fwd_workspace_size(const nsmoe_experts_args* a,
 }
 
 extern "C" int nsmoe_block_fwd(const nsmoe_experts_args* a, const void* logits,
-                               int32_t route_flags, float aux_coef, void* saved, void* out,
-                               float* aux, void* workspace, size_t workspace_bytes,
-                               void* stream) {
-  NSMOE_REQUIRE(a && saved && out, "block_fwd: NULL pointer");
+                               int32_t route_flags, float aux_coef, void* saved,
+                               int64_t* topk_idx, int32_t* counts, void* out, float* aux,
+                               void* workspace, size_t workspace_bytes, void* stream) {
+  NSMOE_REQUIRE(a && saved && out && topk_idx && counts, "block_fwd: NULL pointer");
   NSMOE_REQUIRE(!(route_flags & NSMOE_ROUTE_PROBS) || aux, "block_fwd: NULL aux");
+  NSMOE_REQUIRE(a->w_in_packed && a->w_out_packed, "block_fwd: NULL packed weights");
   if (a->n_tokens == 0) return NSMOE_OK;
   NSMOE_REQUIRE(logits, "block_fwd: NULL logits");
   const BlockLayout L = block_layout(a, route_flags);
   char* sv = (char*)saved;
-  nsmoe_experts_args b = with_routing(a, L, sv);
+  nsmoe_experts_args b = with_routing(a, L, sv, counts);
   size_t dsp, exp, bal;
   const size_t need = fwd_ws_parts(&b, &dsp, &exp, &bal);
   if (!workspace || workspace_bytes < need) {
@@ -126,17 +123,17 @@ extern "C" int nsmoe_block_fwd(const nsmoe_experts_args* a, const void* logits,
   const int64_t T = a->n_tokens, m = T * k;
   float* probs = (route_flags & NSMOE_ROUTE_PROBS) ? (float*)(sv + L.off[NSMOE_SAVED_PROBS])
                                                    : nullptr;
-  int64_t* topk_idx = (int64_t*)(sv + L.off[NSMOE_SAVED_TOPK_IDX]);
   int32_t* inv = (int32_t*)(sv + L.off[NSMOE_SAVED_INV]);
   // In training the route kernel also leaves the balance loss's per-workgroup column
   // sums of probs in the workspace, so probs is not read back for the loss.
   float* colsum = probs ? (float*)(ws + dsp + exp) : nullptr;
-  // The weight packing does not depend on the routing: it runs on the side stream while
-  // the (latency-bound) route and dispatch kernels run on the caller's stream.
+  // The weight packing (when asked for) does not depend on the routing: it runs on the
+  // side stream while the latency-bound route and dispatch kernels run on the caller's.
   hipStream_t s = (hipStream_t)stream;
-  hipStream_t s_pack = side_fork(s, kSideSlotPack);
-  const int prc = nsmoe_pack_weights(&b, (void*)b.w_in_packed, (void*)b.w_out_packed, s_pack);
-  int rc = prc;
+  const bool pack = route_flags & NSMOE_BLOCK_PACK;
+  hipStream_t s_pack = pack ? side_fork(s, kSideSlotPack) : s;
+  int rc = pack ? nsmoe_pack_weights(&b, (void*)b.w_in_packed, (void*)b.w_out_packed, s_pack)
+                : NSMOE_OK;
   if (rc == NSMOE_OK)
     rc = route_fwd_launch(logits, T, E, k, route_flags, a->dtype, (void*)b.topk_w, topk_idx,
                           probs, colsum, s);
@@ -145,8 +142,8 @@ extern "C" int nsmoe_block_fwd(const nsmoe_experts_args* a, const void* logits,
   if (rc == NSMOE_OK)
     rc = dispatch_launch(topk_idx, m, E, (int32_t*)b.sorted_ids,
                          (int32_t*)(sv + L.off[NSMOE_SAVED_EXPERT_IDS]), (int32_t*)b.pad_offsets,
-                         (int32_t*)b.counts, (int32_t*)(sv + L.off[NSMOE_SAVED_N_POST_PAD]), inv,
-                         ws, dsp, probs ? &fold : nullptr, s);
+                         counts, (int32_t*)(sv + L.off[NSMOE_SAVED_N_POST_PAD]), inv, ws, dsp,
+                         probs ? &fold : nullptr, s);
   const int jrc = side_join(s, s_pack, kSideSlotPack);  // joined on every path
   NSMOE_TRY(rc);
   NSMOE_TRY(jrc);
@@ -183,8 +180,9 @@ static BwdWs bwd_ws(const nsmoe_experts_args* b, bool router) {
 
 namespace nsmoe {
 int block_bwd_router(const nsmoe_experts_args* a, const nsmoe_experts_args& b,
-                     const BlockLayout& L, char* sv, const void* logits, int32_t route_flags,
-                     float aux_coef, const float* grad_aux, const nsmoe_experts_grads* grads,
+                     const BlockLayout& L, char* sv, const int64_t* topk_idx,
+                     const void* logits, int32_t route_flags, float aux_coef,
+                     const float* grad_aux, const nsmoe_experts_grads* grads,
                      const void* w_router, void* grad_w_router, void* grad_logits, char* ws,
                      const BwdWs& W, const int32_t* inv, bool fuse, hipStream_t s);
 }  // namespace nsmoe
@@ -200,11 +198,14 @@ extern "C" size_t nsmoe_block_bwd_workspace_size(const nsmoe_experts_args* a,
 
 extern "C" int nsmoe_block_bwd(const nsmoe_experts_args* a, const void* logits,
                                int32_t route_flags, float aux_coef, const void* saved,
+                               const int64_t* topk_idx, const int32_t* counts,
                                const void* grad_out, const float* grad_aux,
                                const nsmoe_experts_grads* grads, const void* w_router,
                                void* grad_w_router, void* grad_logits, void* workspace,
                                size_t workspace_bytes, void* stream) {
-  NSMOE_REQUIRE(a && saved && grad_out && grads, "block_bwd: NULL pointer");
+  NSMOE_REQUIRE(a && saved && topk_idx && counts && grad_out && grads,
+                "block_bwd: NULL pointer");
+  NSMOE_REQUIRE(a->w_in_packed, "block_bwd: NULL packed W_in");
   const bool fuse = w_router != nullptr;
   NSMOE_REQUIRE(fuse ? grad_w_router != nullptr : grad_logits != nullptr,
                 "block_bwd: NULL %s", fuse ? "grad_w_router" : "grad_logits");
@@ -214,7 +215,7 @@ extern "C" int nsmoe_block_bwd(const nsmoe_experts_args* a, const void* logits,
   if (a->n_tokens == 0) return NSMOE_OK;
   const BlockLayout L = block_layout(a, route_flags);
   char* sv = (char*)saved;
-  nsmoe_experts_args b = with_routing(a, L, sv);
+  nsmoe_experts_args b = with_routing(a, L, sv, counts);
   const BwdWs W = bwd_ws(&b, fuse);
   if (!workspace || workspace_bytes < W.total) {
     set_error("block_bwd: workspace %zu B < %zu B", workspace_bytes, W.total);
@@ -228,7 +229,7 @@ extern "C" int nsmoe_block_bwd(const nsmoe_experts_args* a, const void* logits,
   // dW runs on the side stream beside everything below; joined before returning.
   hipStream_t s_dw = s;
   NSMOE_TRY(experts_bwd_launch(&b, inv, grad_out, &g, ws + W.exp, W.gl - W.exp, !fuse, s, &s_dw));
-  const int rc = block_bwd_router(a, b, L, sv, logits, route_flags, aux_coef, grad_aux, grads,
+  const int rc = block_bwd_router(a, b, L, sv, topk_idx, logits, route_flags, aux_coef, grad_aux, grads,
                                   w_router, grad_w_router, grad_logits, ws, W, inv, fuse, s);
   const int jrc = side_join(s, s_dw, kSideSlotDw);
   NSMOE_TRY(rc);
@@ -240,8 +241,9 @@ namespace nsmoe {
 // The router's part of the block backward, after the experts' (block.hip's
 // nsmoe_block_bwd): d(logits) from the gate gradient, then dx and W_router's gradient.
 int block_bwd_router(const nsmoe_experts_args* a, const nsmoe_experts_args& b,
-                     const BlockLayout& L, char* sv, const void* logits, int32_t route_flags,
-                     float aux_coef, const float* grad_aux, const nsmoe_experts_grads* grads,
+                     const BlockLayout& L, char* sv, const int64_t* topk_idx,
+                     const void* logits, int32_t route_flags, float aux_coef,
+                     const float* grad_aux, const nsmoe_experts_grads* grads,
                      const void* w_router, void* grad_w_router, void* grad_logits, char* ws,
                      const BwdWs& W, const int32_t* inv, bool fuse, hipStream_t s) {
   const bool probs = route_flags & NSMOE_ROUTE_PROBS;
@@ -252,7 +254,7 @@ int block_bwd_router(const nsmoe_experts_args* a, const nsmoe_experts_args& b,
   void* gl = fuse ? (void*)(ws + W.gl) : grad_logits;
   // With the router GEMM fused, the same launch packs W for combine_dx's router term.
   const RouterWPack pack{w_router, ws + W.wpk, (int)a->d_model, E, (ldg + 31) / 32};
-  NSMOE_TRY(route_bwd_launch(src, (const int64_t*)(sv + L.off[NSMOE_SAVED_TOPK_IDX]),
+  NSMOE_TRY(route_bwd_launch(src, topk_idx,
                              ws + W.tw, a->dtype, nullptr, probs ? grad_aux : nullptr,
                              probs && grad_aux ? b.counts : nullptr, aux_coef, a->n_tokens, E,
                              a->top_k, route_flags, gl, ldg, s, fuse ? &pack : nullptr));

@@ -36,6 +36,32 @@ int fill_i32(int32_t* dst, int64_t n, int32_t value, hipStream_t stream) {
   return check_launch("fill_i32_kernel");
 }
 
+// ---- tuning options ------------------------------------------------------------------
+struct OptionSpec {
+  const char* name;
+  int64_t lo, hi;           // accepted range besides 0
+  const int64_t* allowed;   // or an explicit list (terminated by 0), when non-NULL
+};
+static const int64_t kFwdRows[] = {64, 96, 0};
+static const int64_t kBwdRows[] = {48, 64, 80, 0};
+static const int64_t kDxRows[] = {64, 96, 0};
+static const OptionSpec kOptions[OPT_COUNT] = {
+    {"single_stream", 1, 1, nullptr}, {"fwd_rows", 0, 0, kFwdRows},
+    {"fwd_dist", 2, 3, nullptr},      {"bwd_rows", 0, 0, kBwdRows},
+    {"bwd_dist", 2, 3, nullptr},      {"dx_rows", 0, 0, kDxRows},
+    {"dx_dist", 2, 4, nullptr},       {"xcd_run", 1, 1024, nullptr},
+};
+static std::atomic<int64_t> g_options[OPT_COUNT];
+
+int64_t option(OptionId id) { return g_options[id].load(std::memory_order_relaxed); }
+
+static int option_index(const char* name) {
+  if (!name) return -1;
+  for (int i = 0; i < OPT_COUNT; ++i)
+    if (strcmp(kOptions[i].name, name) == 0) return i;
+  return -1;
+}
+
 // ---- side stream -------------------------------------------------------------------------
 //
 // Per host thread and device: one extra stream (default priority, non-blocking) and a
@@ -46,7 +72,7 @@ int fill_i32(int32_t* dst, int64_t n, int32_t value, hipStream_t stream) {
 // capture at the fork and leaves it at the join).  Measured on MI355X under ROCm 7, a
 // replayed graph gains nothing from the fork (its branches are not overlapped) and pays
 // for the extra nodes, so work enqueued while `s` is being captured stays on `s`; so does
-// everything in a process with NSMOE_SINGLE_STREAM set.
+// everything while the "single_stream" option is set.
 constexpr int kSideSlots = 4;
 constexpr int kMaxDevices = 64;
 
@@ -84,7 +110,7 @@ static bool side_init(SideState& st, hipStream_t s) {
 }
 
 hipStream_t side_fork(hipStream_t s, int slot) {
-  if (getenv("NSMOE_SINGLE_STREAM") || slot < 0 || slot >= kSideSlots) return s;
+  if (option(OPT_SINGLE_STREAM) || slot < 0 || slot >= kSideSlots) return s;
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return s;
   SideState& st = g_side[dev];
@@ -196,4 +222,30 @@ extern "C" uint64_t nsmoe_launch_count(void) {
   return nsmoe::g_launches.load(std::memory_order_relaxed);
 }
 
-extern "C" int32_t nsmoe_abi_version(void) { return 3; }
+extern "C" int32_t nsmoe_abi_version(void) { return 4; }
+
+extern "C" int nsmoe_set_option(const char* name, int64_t value) {
+  const int i = nsmoe::option_index(name);
+  if (i < 0) {
+    nsmoe::set_error("set_option: unknown option '%s'", name ? name : "(null)");
+    return nsmoe::NSMOE_EINVAL;
+  }
+  const nsmoe::OptionSpec& o = nsmoe::kOptions[i];
+  bool ok = value == 0;
+  if (!ok && o.allowed) {
+    for (const int64_t* v = o.allowed; *v; ++v) ok = ok || *v == value;
+  } else if (!ok) {
+    ok = value >= o.lo && value <= o.hi;
+  }
+  if (!ok) {
+    nsmoe::set_error("set_option: %lld is not a value of '%s'", (long long)value, name);
+    return nsmoe::NSMOE_EINVAL;
+  }
+  nsmoe::g_options[i].store(value, std::memory_order_relaxed);
+  return nsmoe::NSMOE_OK;
+}
+
+extern "C" int64_t nsmoe_get_option(const char* name) {
+  const int i = nsmoe::option_index(name);
+  return i < 0 ? -1 : nsmoe::option((nsmoe::OptionId)i);
+}

@@ -986,11 +986,8 @@ static ExpParams make_params(const nsmoe_experts_args* a) {
   p.fast = (a->d_model % 8 == 0) && (a->d_hidden % 8 == 0) && aligned16(a->x) &&
            aligned16(a->w_in) && aligned16(a->w_out) &&
            (a->n_shared == 0 || (aligned16(a->w_sh_in) && aligned16(a->w_sh_out)));
-  static const int xcd_run = [] {
-    const char* e = getenv("NSMOE_XCD_RUN");
-    return e ? atoi(e) : XCD_RUN;
-  }();
-  p.xcd_run = xcd_run;
+  const int64_t run = option(OPT_XCD_RUN);
+  p.xcd_run = run ? (int)run : XCD_RUN;
   return p;
 }
 

@@ -1427,27 +1427,20 @@ int launch_bwd_async(int dtype, const ExpParams& p, int nbw, int64_t grid, int p
                      hipStream_t s) {
   if (!p.fast || nbw > 2 || (dtype != DT_BF16 && dtype != DT_F16)) return -1;
   if (grid <= 0) return NSMOE_OK;
-  static const bool reg = getenv("NSMOE_BWD_LDSW") == nullptr;
   const int nsteps_dx = ((p.d + NP2 - 1) / NP2) * (2 * p.H / 32);
-  if (reg && p.d % 64 == 0 && (2 * p.H) % 32 == 0 && nsteps_dx % 2 == 0 && p.in_kb >= 4) {
+  if (p.d % 64 == 0 && (2 * p.H) % 32 == 0 && nsteps_dx % 2 == 0 && p.in_kb >= 4) {
     if (part == 0) {
       // 64-row tiles at 2 workgroups per CU with weight prefetch distance 3 (where the step
       // count divides by 3, else 2); once those tiles overflow one round of the resident
       // slots, 48-row tiles at distance 2, whose 162 registers fit 3 workgroups per CU (at
       // T = 8192: 1406 tiles over 768 slots instead of 1064 over 512, the last third of a
-      // round nearly empty).  NSMOE_BWD_MB = 3, 4 or 5 and NSMOE_BWD_D = 2 or 3 force a
-      // tile height and a distance (read on every call, for tests); 80-row tiles take
-      // distance 2, which is all their registers allow.
+      // round nearly empty).  The "bwd_rows" / "bwd_dist" options force a tile height and
+      // a distance; 80-row tiles take distance 2, which is all their registers allow.
       int mb = tile_grid(p, 64) > 2 * (int64_t)device_cus() ? 3 : 4;
-      if (const char* e = getenv("NSMOE_BWD_MB")) {
-        const int v = atoi(e);
-        if (v >= 3 && v <= 5) mb = v;
-      }
+      if (const int64_t v = option(OPT_BWD_ROWS)) mb = (int)(v / 16);
       int dist = mb != 3 && p.in_kb % 3 == 0 ? 3 : 2;
-      if (const char* e = getenv("NSMOE_BWD_D")) {
-        const int v = atoi(e);
-        if (v == 2 || (v == 3 && p.in_kb % 3 == 0)) dist = v;
-      }
+      if (const int64_t v = option(OPT_BWD_DIST))
+        if (v == 2 || p.in_kb % 3 == 0) dist = (int)v;
       if (mb == 5) dist = 2;
       KernelTimer timer("expert_bwd", s);
       if (dtype == DT_BF16) bwd_reg_launch<DT_BF16>(p, nbw, dist, mb, s);
@@ -1456,19 +1449,13 @@ int launch_bwd_async(int dtype, const ExpParams& p, int nbw, int64_t grid, int p
       return check_launch("expert_bwd_reg_kernel");
     }
     // 96-row tiles once 64-row tiles overflow the resident workgroup slots (3 per CU), as
-    // in the forward; weight prefetch distance 2 steps.  NSMOE_DX_MB = 4 or 6 and
-    // NSMOE_DX_D = 2, 3 or 4 force a tile height and a distance (read on every call, for
-    // tests).
+    // in the forward; weight prefetch distance 2 steps.  The "dx_rows" / "dx_dist" options
+    // force a tile height and a distance.
     int mb = tile_grid(p, 64) > 3 * (int64_t)device_cus() ? 6 : 4;
-    if (const char* e = getenv("NSMOE_DX_MB")) {
-      const int v = atoi(e);
-      if (v == 4 || v == 6) mb = v;
-    }
+    if (const int64_t v = option(OPT_DX_ROWS)) mb = (int)(v / 16);
     int dist = 2;
-    if (const char* e = getenv("NSMOE_DX_D")) {
-      const int v = atoi(e);
-      if (v >= 2 && v <= 4 && nsteps_dx % v == 0) dist = v;
-    }
+    if (const int64_t v = option(OPT_DX_DIST))
+      if (nsteps_dx % v == 0) dist = (int)v;
     KernelTimer timer("expert_dx", s);
     if (dtype == DT_BF16) dx_reg_launch<DT_BF16>(p, mb, dist, s);
     else dx_reg_launch<DT_F16>(p, mb, dist, s);
@@ -1833,23 +1820,16 @@ int launch_fwd_async(int dtype, const ExpParams& p, int nbw, int64_t grid, hipSt
   if (grid <= 0) return NSMOE_OK;
   constexpr int S = 3;
   KernelTimer timer("expert_fwd", s);
-  static const bool reg = getenv("NSMOE_FWD_LDSW") == nullptr;
   const int n2 = ((p.d + NP2 - 1) / NP2) * p.out_kb;
-  if (reg && p.d % 64 == 0 && n2 % 2 == 0) {
+  if (p.d % 64 == 0 && n2 % 2 == 0) {
     // 96-row tiles once 64-row tiles overflow the resident workgroup slots (3 per CU);
-    // NSMOE_FWD_MB = 4 or 6 forces a tile height (read on every call, for tests).
+    // the "fwd_rows" option forces a tile height.
     int mb = tile_grid(p, 64) > 3 * (int64_t)device_cus() ? 6 : 4;
-    if (const char* e = getenv("NSMOE_FWD_MB")) {
-      const int v = atoi(e);
-      if (v == 4 || v == 6) mb = v;
-    }
-    // Prefetch distance: 3 steps where both GEMMs' step counts are multiples of 3;
-    // NSMOE_FWD_D = 2 or 3 forces one (read on every call, for tests).
+    if (const int64_t v = option(OPT_FWD_ROWS)) mb = (int)(v / 16);
+    // Prefetch distance 2; the "fwd_dist" option asks for 3, taken where both GEMMs' step
+    // counts are multiples of 3.
     const int nk1 = p.in_kb;
-    int dist = 2;
-    if (const char* e = getenv("NSMOE_FWD_D")) {
-      if (atoi(e) == 3) dist = 3;
-    }
+    int dist = option(OPT_FWD_DIST) == 3 ? 3 : 2;
     if (dist == 3 && (nk1 % 3 != 0 || n2 % 3 != 0)) dist = 2;
     if (dtype == DT_BF16) {
       if (nbw == 1) fwd_reg_launch<DT_BF16, 1>(p, mb, dist, s);

@@ -47,6 +47,22 @@ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
   } while (0)
 
 namespace nsmoe {
+// Process-wide tuning options (nsmoe_set_option); 0 means the library's own choice.
+enum OptionId : int {
+  OPT_SINGLE_STREAM = 0,
+  OPT_FWD_ROWS,
+  OPT_FWD_DIST,
+  OPT_BWD_ROWS,
+  OPT_BWD_DIST,
+  OPT_DX_ROWS,
+  OPT_DX_DIST,
+  OPT_XCD_RUN,
+  OPT_COUNT
+};
+int64_t option(OptionId id);
+}  // namespace nsmoe
+
+namespace nsmoe {
 // Fork/join onto the calling thread's side stream for the current device (capi.hip).
 // side_fork returns the side stream, ordered after the work already on `s`, or `s` itself
 // when no side stream is available; side_join orders `s` after the side stream's work

@@ -22,6 +22,8 @@ from __future__ import annotations
 
 import ctypes
 import threading
+import weakref
+from collections import OrderedDict
 from typing import Optional
 
 import torch
@@ -57,7 +59,8 @@ def kernel_supported(t: Tensor) -> bool:
     """
     if not (t.is_cuda and t.dtype in KERNEL_DTYPES):
         return False
-    nat.lib()
+    if not torch.compiler.is_compiling():  # traced graphs load it when the op first runs
+        nat.lib()
     return True
 
 
@@ -239,17 +242,107 @@ def _c(t: Optional[Tensor]) -> Optional[Tensor]:
     return None if t is None else t.contiguous()
 
 
-def _pack(args: nat.ExpertsArgs, device, with_out: bool = True):
-    """Weights in MFMA fragment order (nsmoe_pack_weights): (packed W_in, packed W_out)."""
-    lib = nat.lib()
+class PackCache:
+    """
+    The expert weights' fragment-order packs (nsmoe_pack_weights), kept while the weights
+    do not change, so the pack pass (2 x 34.5 MB of traffic at nanoSpeaker's shape) runs
+    once per weight update instead of once per forward: eval and decode calls, the
+    checkpoint recompute and gradient-accumulation micro-steps all reuse it.
+
+    An entry belongs to the weight tensors themselves (weak references to the objects the
+    op was called with) and is valid while each is alive, still at the same storage
+    address and shape, and at the same autograd version.  Every in-place write through
+    the tensor or a view of it (an optimizer step, load_state_dict, `copy_`) bumps the
+    version, and the next call packs into a fresh buffer; an autograd graph that still
+    holds the old pack keeps it.  Writes through `.data` bypass the version counter: call
+    `clear()` after them.  While the current stream is being captured into a HIP graph
+    the cache is bypassed, so the graph packs on every replay.  At most `capacity`
+    weight sets are kept (least recently used out); an entry goes as soon as one of its
+    weights is freed.
+    """
+
+    def __init__(self, capacity: int = 64):
+        self.capacity = capacity
+        self.hits = 0
+        self.misses = 0
+        self._lock = threading.RLock()
+        self._entries: "OrderedDict[tuple, tuple]" = OrderedDict()
+
+    @staticmethod
+    def _state(t: Tensor) -> tuple:
+        return (t.data_ptr(), tuple(t.shape), tuple(t.stride()), t.dtype, t._version)
+
+    def _drop(self, key) -> None:
+        with self._lock:
+            self._entries.pop(key, None)
+
+    def clear(self) -> None:
+        with self._lock:
+            self._entries.clear()
+
+    def __len__(self) -> int:
+        return len(self._entries)
+
+    def lookup(self, nbytes: "tuple[int, int]", device, *weights):
+        """
+        (packed W_in, packed W_out, pending) for these weights (W_in, W_out, W_sh_in,
+        W_sh_out; the shared ones may be None).  pending is None on a hit; otherwise the
+        buffers are new and still to be packed, and `store(pending, ...)` files them once
+        the pack is enqueued.
+        """
+        present = tuple(w for w in weights if w is not None)
+        if torch.device(device).type == "cuda" and torch.cuda.is_current_stream_capturing():
+            pending = None, ()
+        else:
+            key = tuple(w.data_ptr() for w in present) + (len(present),)
+            with self._lock:
+                entry = self._entries.get(key)
+                if entry is not None:
+                    refs, states, p_in, p_out = entry
+                    if all(r() is w for r, w in zip(refs, present)) and all(
+                            s == self._state(w) for s, w in zip(states, present)):
+                        self._entries.move_to_end(key)
+                        self.hits += 1
+                        return p_in, p_out, None
+                    del self._entries[key]
+            pending = key, present
+        self.misses += 1
+        p_in = torch.empty(nbytes[0], dtype=torch.uint8, device=device)
+        p_out = torch.empty(nbytes[1], dtype=torch.uint8, device=device)
+        return p_in, p_out, pending
+
+    def store(self, pending, p_in: Tensor, p_out: Tensor) -> None:
+        key, present = pending
+        if not present:
+            return
+        cb = lambda _ref, key=key: self._drop(key)
+        entry = (tuple(weakref.ref(w, cb) for w in present),
+                 tuple(self._state(w) for w in present), p_in, p_out)
+        with self._lock:
+            self._entries[key] = entry
+            self._entries.move_to_end(key)
+            while len(self._entries) > self.capacity:
+                self._entries.popitem(last=False)
+
+
+PACKS = PackCache()
+
+
+def _pack_sizes(args: nat.ExpertsArgs) -> "tuple[int, int]":
     nb_in, nb_out = ctypes.c_size_t(), ctypes.c_size_t()
-    nat.check(lib.nsmoe_pack_sizes(args, ctypes.byref(nb_in), ctypes.byref(nb_out)),
+    nat.check(nat.lib().nsmoe_pack_sizes(args, ctypes.byref(nb_in), ctypes.byref(nb_out)),
               "nsmoe_pack_sizes")
-    p_in = torch.empty(nb_in.value, dtype=torch.uint8, device=device)
-    p_out = torch.empty(nb_out.value if with_out else 0, dtype=torch.uint8, device=device)
-    nat.check(lib.nsmoe_pack_weights(args, p_in.data_ptr(), _p(p_out), _stream()),
-              "nsmoe_pack_weights")
-    args.w_in_packed, args.w_out_packed = p_in.data_ptr(), _p(p_out)
+    return nb_in.value, nb_out.value
+
+
+def _pack(args: nat.ExpertsArgs, device, weights):
+    """Weights in MFMA fragment order, from the pack cache or packed now: (W_in, W_out)."""
+    p_in, p_out, pending = PACKS.lookup(_pack_sizes(args), device, *weights)
+    if pending is not None:
+        nat.check(nat.lib().nsmoe_pack_weights(args, p_in.data_ptr(), p_out.data_ptr(),
+                                               _stream()), "nsmoe_pack_weights")
+        PACKS.store(pending, p_in, p_out)
+    args.w_in_packed, args.w_out_packed = p_in.data_ptr(), p_out.data_ptr()
     return p_in, p_out
 
 
@@ -273,7 +366,7 @@ def _experts_forward(x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_
         return out, x.new_empty(0, dtype=torch.uint8)
     args = _args(x, w_in, w_out, topk_w, b_in, b_out, w_sh_in, w_sh_out, b_sh_in, b_sh_out,
                  sorted_ids, pad_offsets, counts, activation)
-    p_in, p_out = _pack(args, x.device)
+    p_in, p_out = _pack(args, x.device, (w_in, w_out, w_sh_in, w_sh_out))
     lib = nat.lib()
     ws = _ws(lib.nsmoe_experts_fwd_workspace_size(args), x.device)
     nat.check(lib.nsmoe_experts_fwd(args, _p(inv_ids), out.data_ptr(), ws.data_ptr(),
@@ -317,7 +410,7 @@ def _experts_backward(grad_out, x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, 
     if w_in_packed is not None and w_in_packed.numel():
         args.w_in_packed = w_in_packed.data_ptr()
     else:
-        w_in_packed, _ = _pack(args, dev, with_out=False)
+        w_in_packed, _ = _pack(args, dev, (w_in, w_out, w_sh_in, w_sh_out))
     lib = nat.lib()
     ws = _ws(lib.nsmoe_experts_bwd_workspace_size(args), dev)
     nat.check(lib.nsmoe_experts_bwd(args, _p(inv_ids), grad_out.data_ptr(), grads,
@@ -536,8 +629,28 @@ def fused_moe_block_forward(x, w_in, w_out, topk_w, topk_idx, b_in, b_out, w_sh_
 
 
 # ---------------------------------------------------------------------------------------
-# the whole block as one autograd node (the MoEBlock fast path)
+# the whole block as one op per direction (the MoEBlock fast path)
 # ---------------------------------------------------------------------------------------
+
+def _al256(b):
+    return (b + 255) // 256 * 256
+
+
+def block_saved_bytes(n: int, e: int, k: int, dtype: torch.dtype, want_probs: bool) -> int:
+    """
+    Size of the block forward's `saved` buffer (nsmoe_block_saved_layout): gates [n, k],
+    probs [n, e] fp32 (train branch), sorted ids [l_cap], block owners [l_cap / 16], run
+    offsets [e + 1], the padded total and inv [n k], each rounded up to 256 bytes.  Written
+    in Python so fake tensors with symbolic n get the same size; a CPU test holds it equal
+    to the library's.
+    """
+    es = 4 if dtype == torch.float32 else 2
+    m = n * k
+    l_cap = _l_cap(m, e)
+    parts = (m * es, n * e * 4 if want_probs else 0, l_cap * 4, (l_cap // ALIGN_M) * 4,
+             (e + 1) * 4, 4, m * 4)
+    return sum(_al256(b) for b in parts)
+
 
 class _BlockPlan:
     """Host state of the block call for one shape: the args struct (dims filled once,
@@ -556,6 +669,10 @@ class _BlockPlan:
         self.off = list(offs)
         self.saved_bytes = total.value
         self.fwd_ws = lib.nsmoe_block_fwd_workspace_size(self.args, flags)
+        nb_in, nb_out = ctypes.c_size_t(), ctypes.c_size_t()
+        nat.check(lib.nsmoe_pack_sizes(self.args, ctypes.byref(nb_in), ctypes.byref(nb_out)),
+                  "nsmoe_pack_sizes")
+        self.pack_bytes = (nb_in.value, nb_out.value)
         # The router GEMM's backward runs inside nsmoe_block_bwd for 16-bit types when
         # d % 16 == 0 and E % 4 == 0 (E <= 128 always holds here); otherwise in torch.
         self.fuse_router = (dt in (torch.bfloat16, torch.float16) and d % 16 == 0
@@ -572,129 +689,232 @@ class _BlockPlan:
 
 
 _PLANS = threading.local()
+_PLANS_MAX = 16  # shapes kept per host thread (least recently used out)
 
 
 def _plan(dt, activation, n, d, h, e, s, k, flags) -> _BlockPlan:
     cache = getattr(_PLANS, "cache", None)
     if cache is None:
-        cache = _PLANS.cache = {}
+        cache = _PLANS.cache = OrderedDict()
     key = (dt, activation, n, d, h, e, s, k, flags)
     plan = cache.get(key)
     if plan is None:
         plan = cache[key] = _BlockPlan(dt, activation, n, d, h, e, s, k, flags)
+        while len(cache) > _PLANS_MAX:
+            cache.popitem(last=False)
+    else:
+        cache.move_to_end(key)
     return plan
 
 
-class _BlockFunction(torch.autograd.Function):
-    """
-    MoEBlock.forward's kernel path in one autograd node: the router GEMM `x @ W` (torch),
-    then one C call (nsmoe_block_fwd: router tail, dispatch, weight pack, routed + shared
-    experts with the combine, balance loss); the backward is one C call (nsmoe_block_bwd:
-    experts' backward, router tail's backward with the balance-loss gradient folded in,
-    and for 16-bit types the router GEMM's backward, d(logits) W^T fused into the dx
-    combine and x^T d(logits) as a split-K kernel; other types finish the router GEMM's
-    backward in torch).  Same arithmetic as composing the per-stage ops above
-    (route / moe_dispatch / moe_block / balance loss) with a fraction of their host cost:
-    at nanoSpeaker's shape the block is otherwise bound by the host issuing its launches.
-    """
+def _route_bits(dt, want_probs, normalize) -> int:
+    half = dt in (torch.bfloat16, torch.float16)
+    return _route_flags(want_probs, normalize) | (nat.ROUTE_LOGITS16 if half else 0)
 
-    @staticmethod
-    def forward(ctx, x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out,
-                top_k: int, want_probs: bool, normalize: bool, activation: str,
-                aux_coef: float):
-        dev, dt = x.device, x.dtype
-        n, d = x.shape
-        e, h2 = W_r.shape[1], w_in.shape[2]
-        s = 0 if w_sh_in is None else w_sh_in.shape[0]
-        half = dt in (torch.bfloat16, torch.float16)
-        # router.py:69: the GEMM in x's dtype; the kernel widens 16-bit logits itself.
-        logits = x @ W_r
-        if not half:
-            logits = logits.float()
-        flags = _route_flags(want_probs, normalize) | (nat.ROUTE_LOGITS16 if half else 0)
-        plan = _plan(dt, activation, n, d, h2 // 2, e, s, top_k, flags)
-        saved = torch.empty(plan.saved_bytes, dtype=torch.uint8, device=dev)
-        out = torch.empty((n, d), dtype=dt, device=dev)
-        aux = (torch.empty((), dtype=torch.float32, device=dev) if want_probs
-               else torch.zeros((), dtype=dt, device=dev))
-        if n:
-            ws = torch.empty(plan.fwd_ws, dtype=torch.uint8, device=dev)
-            a = plan.bind(x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out)
-            nat.check(nat.lib().nsmoe_block_fwd(
-                a, logits.data_ptr(), flags, aux_coef, saved.data_ptr(), out.data_ptr(),
-                aux.data_ptr() if want_probs else None, ws.data_ptr(), plan.fwd_ws, _stream()),
-                "nsmoe_block_fwd")
-        else:
-            saved.zero_()
-        oc, oi = plan.off[nat.SAVED_COUNTS], plan.off[nat.SAVED_TOPK_IDX]
-        counts = saved[oc:oc + 4 * e].view(torch.int32)
-        topk_idx = saved[oi:oi + 8 * n * top_k].view(torch.int64).view(n, top_k)
-        ctx.mark_non_differentiable(counts, topk_idx)
-        # Unused output gradients arrive as None instead of materialised zeros (two fill
-        # kernels per step for counts and topk_idx otherwise).
-        ctx.set_materialize_grads(False)
-        ctx.save_for_backward(x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in,
-                              logits, saved)
-        ctx.cfg = (plan, flags, float(aux_coef), b_sh_out is not None)
-        return out, aux, counts, topk_idx
 
-    @staticmethod
-    def backward(ctx, g_out, g_aux, g_counts, g_idx):
-        x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, logits, saved = \
-            ctx.saved_tensors
-        plan, flags, aux_coef, has_b_sh_out = ctx.cfg
-        need = ctx.needs_input_grad
-        n, d = x.shape
-        e = W_r.shape[1]
-        dev, dt = x.device, x.dtype
-        half = bool(flags & nat.ROUTE_LOGITS16)
-        g_out = torch.zeros_like(x) if g_out is None else g_out.to(dt).contiguous()
-        dx = torch.empty_like(x)
-        dw_in, dw_out = torch.empty_like(w_in), torch.empty_like(w_out)
-        s = w_sh_in is not None
-        dw_sh_in = torch.empty_like(w_sh_in) if s else None
-        dw_sh_out = torch.empty_like(w_sh_out) if s else None
-        db_in = torch.empty_like(b_in) if b_in is not None else None
-        db_out = torch.empty_like(b_out) if b_out is not None else None
-        db_sh_in = torch.empty_like(b_sh_in) if b_sh_in is not None else None
-        db_sh_out = (torch.empty((w_sh_in.shape[0], d), dtype=dt, device=dev)
-                     if has_b_sh_out else None)
-        fuse = plan.fuse_router
-        dlogits = None if fuse else torch.empty((n, e), dtype=dt if half else torch.float32,
-                                                device=dev)
-        dW_r = torch.empty_like(W_r) if fuse else None
-        if n:
-            ga = None
-            if (flags & nat.ROUTE_PROBS) and g_aux is not None:
-                ga = g_aux.detach().to(torch.float32).reshape(1).contiguous()
-            gr = plan.grads
-            gr.dx, gr.dw_in, gr.dw_out = dx.data_ptr(), dw_in.data_ptr(), dw_out.data_ptr()
-            gr.dw_sh_in, gr.dw_sh_out, gr.dtopk_w = _p(dw_sh_in), _p(dw_sh_out), None
-            gr.db_in, gr.db_out = _p(db_in), _p(db_out)
-            gr.db_sh_in, gr.db_sh_out = _p(db_sh_in), _p(db_sh_out)
-            ws = torch.empty(plan.bwd_ws, dtype=torch.uint8, device=dev)
-            # b_sh_out does not enter the backward (the shared experts have no gate).
-            a = plan.bind(x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, None)
-            nat.check(nat.lib().nsmoe_block_bwd(
-                a, logits.data_ptr(), flags, aux_coef, saved.data_ptr(), g_out.data_ptr(),
-                _p(ga), gr, _p(W_r if fuse else None), _p(dW_r), _p(dlogits), ws.data_ptr(),
-                plan.bwd_ws, _stream()), "nsmoe_block_bwd")
-        else:
-            for t in (dw_in, dw_out, dw_sh_in, dw_sh_out, db_in, db_out, db_sh_in, db_sh_out,
-                      dlogits, dW_r):
-                if t is not None:
-                    t.zero_()
-        if not fuse:
-            dl = dlogits if half else dlogits.to(dt)
-            dW_r = x.t().mm(dl) if need[1] else None
-            if need[0]:
-                dx.addmm_(dl, W_r.t())
-        return (dx if need[0] else None, dW_r if need[1] else None, dw_in, dw_out, dw_sh_in,
-                dw_sh_out, db_in, db_out, db_sh_in, db_sh_out, None, None, None, None, None)
+@torch.library.custom_op("nsmoe::block_fwd", mutates_args=())
+def block_fwd(x: Tensor, W_r: Tensor, w_in: Tensor, w_out: Tensor, w_sh_in: Optional[Tensor],
+              w_sh_out: Optional[Tensor], b_in: Optional[Tensor], b_out: Optional[Tensor],
+              b_sh_in: Optional[Tensor], b_sh_out: Optional[Tensor], top_k: int,
+              want_probs: bool, normalize: bool, activation: str, aux_coef: float,
+              logit_bias: Optional[Tensor] = None
+              ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """
+    MoEBlock.forward's kernel path (moe.py:345-418): the router GEMM `x @ W_r` (torch,
+    router.py:69), then one C call (nsmoe_block_fwd: router tail, dispatch, routed + shared
+    experts with the combine, balance loss).  The weights' fragment-order packs come from
+    the pack cache, so the pack pass runs only when the weights changed.
+
+    Returns (out [N, d], aux, counts [E] int32, topk_idx [N, k] int64, logits [N, E],
+    saved, packed W_in); the last three only carry state to the backward.  aux is the
+    balance loss (fp32) when want_probs, else a zero of x's dtype (router.py:52-54,
+    moe.py:367-372).
+
+    `logit_bias` [E] fp32 is a harness hook with no counterpart in the reference router
+    (which has no bias): a per-expert offset added to the GEMM's output, the sum rounded
+    to the GEMM's dtype, before the router tail.  The skewed-routing workload uses it; its
+    gradient is not computed.
+    """
+    dev, dt = x.device, x.dtype
+    n, d = x.shape
+    e, h2 = W_r.shape[1], w_in.shape[2]
+    s = 0 if w_sh_in is None else w_sh_in.shape[0]
+    logits = x @ W_r
+    if dt not in (torch.bfloat16, torch.float16):
+        logits = logits.float()
+    if logit_bias is not None:
+        logits = (logits.float() + logit_bias.float()).to(logits.dtype)
+    flags = _route_bits(dt, want_probs, normalize)
+    plan = _plan(dt, activation, n, d, h2 // 2, e, s, top_k, flags)
+    saved = torch.empty(plan.saved_bytes, dtype=torch.uint8, device=dev)
+    out = torch.empty((n, d), dtype=dt, device=dev)
+    counts = torch.empty(e, dtype=torch.int32, device=dev)
+    topk_idx = torch.empty((n, top_k), dtype=torch.int64, device=dev)
+    aux = (torch.empty((), dtype=torch.float32, device=dev) if want_probs
+           else torch.zeros((), dtype=dt, device=dev))
+    a = plan.bind(x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out)
+    if n:
+        p_in, p_out, pending = PACKS.lookup(plan.pack_bytes, dev, w_in, w_out, w_sh_in,
+                                            w_sh_out)
+        a.w_in_packed, a.w_out_packed = p_in.data_ptr(), p_out.data_ptr()
+        ws = torch.empty(plan.fwd_ws, dtype=torch.uint8, device=dev)
+        nat.check(nat.lib().nsmoe_block_fwd(
+            a, logits.data_ptr(), flags | (nat.BLOCK_PACK if pending is not None else 0),
+            aux_coef, saved.data_ptr(), topk_idx.data_ptr(), counts.data_ptr(),
+            out.data_ptr(), aux.data_ptr() if want_probs else None, ws.data_ptr(),
+            plan.fwd_ws, _stream()), "nsmoe_block_fwd")
+        if pending is not None:
+            PACKS.store(pending, p_in, p_out)
+    else:
+        p_in = torch.empty(plan.pack_bytes[0], dtype=torch.uint8, device=dev)
+        counts.zero_()
+        if want_probs:
+            aux.zero_()
+    return out, aux, counts, topk_idx, logits, saved, p_in
+
+
+@block_fwd.register_fake
+def _(x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out, top_k,
+      want_probs, normalize, activation, aux_coef, logit_bias=None):
+    n, d = x.shape
+    e = W_r.shape[1]
+    half = x.dtype in (torch.bfloat16, torch.float16)
+    return (x.new_empty((n, d)),
+            x.new_empty((), dtype=torch.float32 if want_probs else x.dtype),
+            x.new_empty((e,), dtype=torch.int32),
+            x.new_empty((n, top_k), dtype=torch.int64),
+            x.new_empty((n, e), dtype=x.dtype if half else torch.float32),
+            x.new_empty((block_saved_bytes(n, e, top_k, x.dtype, want_probs),),
+                        dtype=torch.uint8),
+            x.new_empty((_packed_in_bytes(x, w_in, w_sh_in),), dtype=torch.uint8))
+
+
+@torch.library.custom_op("nsmoe::block_bwd", mutates_args=())
+def block_bwd(g_out: Tensor, g_aux: Optional[Tensor], x: Tensor, W_r: Tensor, w_in: Tensor,
+              w_out: Tensor, w_sh_in: Optional[Tensor], w_sh_out: Optional[Tensor],
+              b_in: Optional[Tensor], b_out: Optional[Tensor], b_sh_in: Optional[Tensor],
+              logits: Tensor, saved: Tensor, topk_idx: Tensor, counts: Tensor,
+              w_in_packed: Tensor, top_k: int, want_probs: bool, normalize: bool,
+              activation: str, aux_coef: float, has_b_sh_out: bool, need_dx: bool,
+              need_dW_r: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor,
+                                        Tensor, Tensor, Tensor]:
+    """
+    The block's backward in one C call (nsmoe_block_bwd: experts' backward, router tail's
+    backward with the balance-loss gradient folded in, and for 16-bit types the router
+    GEMM's backward: d(logits) W_r^T fused into the dx combine and x^T d(logits) as a
+    split-K kernel; other types finish the router GEMM's backward in torch).
+
+    Returns (dx, dW_r, dW_in, dW_out, dW_sh_in, dW_sh_out, db_in, db_out, db_sh_in,
+    db_sh_out); a gradient with no input (no shared experts, no bias, not needed) comes
+    back as an empty tensor.
+    """
+    n, d = x.shape
+    e, h2 = W_r.shape[1], w_in.shape[2]
+    s = 0 if w_sh_in is None else w_sh_in.shape[0]
+    dev, dt = x.device, x.dtype
+    flags = _route_bits(dt, want_probs, normalize)
+    half = bool(flags & nat.ROUTE_LOGITS16)
+    plan = _plan(dt, activation, n, d, h2 // 2, e, s, top_k, flags)
+    emp = lambda: x.new_empty(0)  # one per absent gradient: outputs may not alias
+    g_out = g_out.to(dt).contiguous()
+    dx = torch.empty_like(x)
+    dw_in, dw_out = torch.empty_like(w_in), torch.empty_like(w_out)
+    dw_sh_in = torch.empty_like(w_sh_in) if s else emp()
+    dw_sh_out = torch.empty_like(w_sh_out) if s else emp()
+    db_in = torch.empty_like(b_in) if b_in is not None else emp()
+    db_out = torch.empty_like(b_out) if b_out is not None else emp()
+    db_sh_in = torch.empty_like(b_sh_in) if b_sh_in is not None else emp()
+    db_sh_out = torch.empty((s, d), dtype=dt, device=dev) if has_b_sh_out else emp()
+    fuse = plan.fuse_router
+    dlogits = None if fuse else torch.empty((n, e), dtype=dt if half else torch.float32,
+                                            device=dev)
+    dW_r = torch.empty_like(W_r) if fuse else None
+    if n:
+        ga = None
+        if want_probs and g_aux is not None:
+            ga = g_aux.detach().to(torch.float32).reshape(1).contiguous()
+        gr = plan.grads
+        gr.dx, gr.dw_in, gr.dw_out = dx.data_ptr(), dw_in.data_ptr(), dw_out.data_ptr()
+        gr.dw_sh_in, gr.dw_sh_out, gr.dtopk_w = _p(dw_sh_in), _p(dw_sh_out), None
+        gr.db_in, gr.db_out = _p(db_in), _p(db_out)
+        gr.db_sh_in, gr.db_sh_out = _p(db_sh_in), _p(db_sh_out)
+        ws = torch.empty(plan.bwd_ws, dtype=torch.uint8, device=dev)
+        # b_sh_out does not enter the backward (the shared experts have no gate).
+        a = plan.bind(x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, None)
+        a.w_in_packed, a.w_out_packed = w_in_packed.data_ptr(), None
+        nat.check(nat.lib().nsmoe_block_bwd(
+            a, logits.data_ptr(), flags, aux_coef, saved.data_ptr(), topk_idx.data_ptr(),
+            counts.data_ptr(), g_out.data_ptr(), _p(ga), gr, _p(W_r if fuse else None),
+            _p(dW_r), _p(dlogits), ws.data_ptr(), plan.bwd_ws, _stream()), "nsmoe_block_bwd")
+    else:
+        for t in (dx, dw_in, dw_out, dw_sh_in, dw_sh_out, db_in, db_out, db_sh_in, db_sh_out,
+                  dlogits, dW_r):
+            if t is not None:
+                t.zero_()
+    if not fuse:
+        dl = dlogits if half else dlogits.to(dt)
+        dW_r = x.t().mm(dl) if need_dW_r else torch.zeros_like(W_r)
+        if need_dx:
+            dx.addmm_(dl, W_r.t())
+    return dx, dW_r, dw_in, dw_out, dw_sh_in, dw_sh_out, db_in, db_out, db_sh_in, db_sh_out
+
+
+@block_bwd.register_fake
+def _(g_out, g_aux, x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, logits,
+      saved, topk_idx, counts, w_in_packed, top_k, want_probs, normalize, activation, aux_coef,
+      has_b_sh_out, need_dx, need_dW_r):
+    s = 0 if w_sh_in is None else w_sh_in.shape[0]
+    like = lambda t: torch.empty_like(t) if t is not None else x.new_empty(0)
+    return (torch.empty_like(x), torch.empty_like(W_r), torch.empty_like(w_in),
+            torch.empty_like(w_out), like(w_sh_in), like(w_sh_out), like(b_in), like(b_out),
+            like(b_sh_in), x.new_empty((s, x.shape[1])) if has_b_sh_out else x.new_empty(0))
+
+
+def _block_fwd_setup(ctx, inputs, output):
+    (x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out, top_k,
+     want_probs, normalize, activation, aux_coef, logit_bias) = inputs
+    out, aux, counts, topk_idx, logits, saved, w_in_packed = output
+    ctx.mark_non_differentiable(counts, topk_idx, logits, saved, w_in_packed)
+    # Unused output gradients arrive as None instead of materialised zeros.
+    ctx.set_materialize_grads(False)
+    ctx.has = [t is not None for t in (w_sh_in, b_in, b_out, b_sh_in)]
+    opt = [t for t in (w_sh_in, w_sh_out, b_in, b_out, b_sh_in) if t is not None]
+    ctx.save_for_backward(x, W_r, w_in, w_out, logits, saved, topk_idx, counts, w_in_packed,
+                          *opt)
+    ctx.cfg = (top_k, want_probs, normalize, activation, aux_coef, b_sh_out is not None)
+
+
+def _block_fwd_backward(ctx, g_out, g_aux, g_counts, g_idx, g_logits, g_saved, g_packed):
+    x, W_r, w_in, w_out, logits, saved, topk_idx, counts, w_in_packed, *opt = ctx.saved_tensors
+    has_sh, has_b_in, has_b_out, has_b_sh_in = ctx.has
+    it = iter(opt)
+    w_sh_in = next(it) if has_sh else None
+    w_sh_out = next(it) if has_sh else None
+    b_in = next(it) if has_b_in else None
+    b_out = next(it) if has_b_out else None
+    b_sh_in = next(it) if has_b_sh_in else None
+    top_k, want_probs, normalize, activation, aux_coef, has_b_sh_out = ctx.cfg
+    need = ctx.needs_input_grad
+    if g_out is None:
+        g_out = torch.zeros_like(x)
+    (dx, dW_r, dw_in, dw_out, dw_sh_in, dw_sh_out, db_in, db_out, db_sh_in,
+     db_sh_out) = block_bwd(g_out, g_aux, x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out,
+                            b_sh_in, logits, saved, topk_idx, counts, w_in_packed, top_k,
+                            want_probs, normalize, activation, aux_coef, has_b_sh_out,
+                            need[0], need[1])
+    opt_grad = lambda present, g: g if present else None
+    return (dx if need[0] else None, dW_r if need[1] else None, dw_in, dw_out,
+            opt_grad(has_sh, dw_sh_in), opt_grad(has_sh, dw_sh_out),
+            opt_grad(has_b_in, db_in), opt_grad(has_b_out, db_out),
+            opt_grad(has_b_sh_in, db_sh_in), opt_grad(has_b_sh_out, db_sh_out),
+            None, None, None, None, None, None)
+
+
+block_fwd.register_autograd(_block_fwd_backward, setup_context=_block_fwd_setup)
 
 
 def block_forward(x, router_W, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out,
-                  top_k, want_probs, normalize, activation, aux_coef):
+                  top_k, want_probs, normalize, activation, aux_coef, logit_bias=None):
     """
     The MoE block on the kernel path: (out [N, d], aux_loss, counts [E] int32,
     topk_idx [N, k] int64).  aux_loss is the balance loss (fp32) when want_probs, else a
@@ -703,7 +923,9 @@ def block_forward(x, router_W, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh
     """
     _check_activation(activation)
     cast = lambda t: None if t is None else t.to(x.dtype)
-    return _BlockFunction.apply(
-        x.contiguous(), cast(router_W).contiguous(), cast(w_in), cast(w_out), cast(w_sh_in), cast(w_sh_out),
-        cast(b_in), cast(b_out), cast(b_sh_in), cast(b_sh_out), top_k, want_probs, normalize,
-        activation, aux_coef)
+    out, aux, counts, topk_idx, _, _, _ = block_fwd(
+        x.contiguous(), cast(router_W).contiguous(), cast(w_in).contiguous(),
+        cast(w_out).contiguous(), _c(cast(w_sh_in)), _c(cast(w_sh_out)), _c(cast(b_in)),
+        _c(cast(b_out)), _c(cast(b_sh_in)), _c(cast(b_sh_out)), top_k, want_probs, normalize,
+        activation, float(aux_coef), logit_bias)
+    return out, aux, counts, topk_idx

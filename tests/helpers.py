@@ -5,6 +5,7 @@ from __future__ import annotations
 import ctypes
 import json
 import subprocess
+from contextlib import contextmanager
 from functools import lru_cache
 from pathlib import Path
 
@@ -100,8 +101,24 @@ def tie_heavy(rows: int, n: int, levels: int, seed: int) -> torch.Tensor:
 
 
 def assert_close_bf16(name, got, ref, max_abs=BF16_MAX_ABS, rel_l2=BF16_REL_L2):
+    """The bf16 bar; prints the unscaled max-abs error and rel-L2 beside the bound."""
     ref = ref.cpu()
     scale = max(1.0, float(ref.abs().max())) if ref.numel() else 1.0
     ok, err, rl2 = R.is_close(got.cpu(), ref, max_abs * scale, rel_l2)
+    print(f"  {name}: max abs {err:.3e} (bound {max_abs * scale:.3e} = {max_abs} x "
+          f"{scale:.3g}), rel-L2 {rl2:.3e} (bound {rel_l2})")
     assert ok, (f"{name}: max abs {err:.3e} (<= {max_abs} x {scale:.3g}), "
                 f"rel-L2 {rl2:.3e} (<= {rel_l2})")
+
+
+@contextmanager
+def lib_options(**values):
+    """Sets libnsmoe tuning options (nsmoe_set_option) for the body, then restores 0."""
+    from nanospeaker_amd import _native as nat
+    try:
+        for name, v in values.items():
+            nat.set_option(name, v)
+        yield
+    finally:
+        for name in values:
+            nat.set_option(name, 0)

@@ -43,7 +43,7 @@ def test_struct_layouts_match_the_header():
 
 
 def test_abi_version_and_alignment():
-    assert nat.lib().nsmoe_abi_version() == nat.ABI_VERSION == 3
+    assert nat.lib().nsmoe_abi_version() == nat.ABI_VERSION == 4
     assert nat.lib().nsmoe_align_m() == mk.ALIGN_M
 
 
@@ -141,3 +141,48 @@ def test_kernel_supported_raises_on_a_gpu_tensor_without_the_library(monkeypatch
     monkeypatch.setattr(nat, "LIB_PATH", tmp_path / "missing.so")
     with pytest.raises(nat.NativeLibraryError):
         mk.kernel_supported(FakeCuda())
+
+
+@pytest.mark.parametrize("n,e,k,dt,probs", [
+    (8192, 76, 6, "bfloat16", True), (8192, 76, 6, "bfloat16", False), (1, 8, 2, "float32", True),
+    (37, 76, 6, "float16", True), (32768, 76, 6, "bfloat16", False), (5, 1000, 8, "float32", False),
+])
+def test_block_saved_layout_matches_the_python_mirror(n, e, k, dt, probs):
+    """The fake impl of nsmoe::block_fwd sizes `saved` in Python (symbolic shapes)."""
+    import torch
+    dtype = getattr(torch, dt)
+    a = nat.ExpertsArgs(dtype=mk._DT[dtype], activation=0, n_tokens=n, d_model=576,
+                        d_hidden=128, n_experts=e, n_shared=2, top_k=k, l_cap=0)
+    offs = (ctypes.c_size_t * nat.BLOCK_NSAVED)()
+    total = ctypes.c_size_t()
+    flags = nat.ROUTE_PROBS if probs else 0
+    assert nat.lib().nsmoe_block_saved_layout(a, flags, offs, ctypes.byref(total)) == 0
+    assert total.value == mk.block_saved_bytes(n, e, k, dtype, probs)
+    assert list(offs) == sorted(offs) and offs[0] == 0
+
+
+def test_tuning_options_round_trip_and_reject_bad_values():
+    lib = nat.lib()
+    for name, good, bad in (("single_stream", 1, 2), ("fwd_rows", 96, 80), ("bwd_rows", 48, 32),
+                            ("dx_rows", 64, 48), ("fwd_dist", 3, 4), ("bwd_dist", 2, 5),
+                            ("dx_dist", 4, 1), ("xcd_run", 8, 2048)):
+        assert nat.get_option(name) == 0
+        nat.set_option(name, good)
+        assert nat.get_option(name) == good
+        assert lib.nsmoe_set_option(name.encode(), bad) == 1
+        assert name in lib.nsmoe_last_error().decode()
+        assert nat.get_option(name) == good
+        nat.set_option(name, 0)
+        assert nat.get_option(name) == 0
+    assert lib.nsmoe_set_option(b"no_such_option", 1) == 1
+    assert lib.nsmoe_get_option(b"no_such_option") == -1
+
+
+def test_block_entry_points_reject_missing_buffers():
+    lib = nat.lib()
+    a = nat.ExpertsArgs(dtype=0, activation=0, n_tokens=4, d_model=64, d_hidden=64,
+                        n_experts=8, n_shared=0, top_k=2, l_cap=0)
+    assert lib.nsmoe_block_fwd(a, 1, 0, 0.0, 1, None, 1, 1, None, 1, 1 << 20, None) == 1
+    assert "NULL" in lib.nsmoe_last_error().decode()
+    assert lib.nsmoe_block_fwd(a, 1, 0, 0.0, 1, 1, 1, 1, None, 1, 1 << 20, None) == 1
+    assert "packed" in lib.nsmoe_last_error().decode()

@@ -1,21 +1,25 @@
 """
-End-to-end GPU parity of the drop-in MoEBlock at the benchmark's workloads.
+End-to-end GPU parity of the drop-in MoEBlock.
 
-The block runs on the GPU exactly as a caller runs it: one autograd node (router GEMM,
+The block runs on the GPU exactly as a caller runs it: one op per direction (router GEMM,
 HIP route / dispatch / grouped experts / combine / balance loss, HIP backward).  The
-block's router GEMM is recomputed on the GPU (the same bf16 GEMM, the same values) and
-handed to the CPU oracle, so both sides route the same logits; from there:
+block's router GEMM is recomputed on the GPU (the same GEMM, the same values) and handed
+to the CPU oracle, so both sides route the same logits; from there:
 
   * routing indices, the per-expert counts and the dispatch permutation: bit-exact;
-  * the output, dX, every expert weight gradient and router.W's gradient: within the
-    bf16 bar against the fp32-accumulated oracle (max abs <= 2e-2 on the tensor's scale,
-    rel-L2 <= 5e-3);
+  * the output, dX, every expert weight and bias gradient and router.W's gradient: within
+    the bf16 bar against the fp32-accumulated oracle (max abs <= 2e-2 on the tensor's
+    scale, rel-L2 <= 5e-3) for 16-bit blocks, and within fp32 rounding for fp32 blocks;
   * the balance loss: to fp32 rounding.
 
-Workloads (seed 0, parameters in the reference's draw order, x ~ N(0, 1) in bf16):
-  T = 2048 forward (train), T = 8192 forward + backward (train), T = 64 forward (eval),
-  T = 16384 forward + backward with the skewed (Zipf 1.2) logit offset of
-  tests/golden/zipf_logit_bias.npy, and a zero router (every token on the same experts).
+Workloads (seed 0, parameters in the reference's draw order, x ~ N(0, 1)): the benchmark's
+configurations -- T = 2048 forward (train), T = 8192 forward + backward (train), T = 64
+forward (eval), T = 16384 forward + backward with the skewed (Zipf 1.2) logit offset of
+tests/golden/zipf_logit_bias.npy, and T = 32768 forward (eval), the per-layer shape of the
+20-layer prefill -- a zero router (every token on the same experts), and a matrix of
+dtypes, biases, shared-expert counts and shapes that take the block's other code paths
+(the router backward in torch, the slow dx combine for k > 8 or more than two shared
+experts).
 """
 
 from pathlib import Path
@@ -34,35 +38,57 @@ from nanospeaker_amd import MoEBlock  # noqa: E402
 
 DEV = "cuda"
 ZIPF = Path(__file__).resolve().parent / "golden" / "zipf_logit_bias.npy"
+NS = dict(d=576, E=76, d_ff=192, k=6, S=2)
 
 
-def build(T, seed=0, zero_router=False):
+def build(T, *, d=576, E=76, d_ff=192, k=6, S=2, bias=False, dtype=torch.bfloat16, seed=0,
+          zero_router=False):
     torch.manual_seed(seed)
-    m = MoEBlock(576, 76, d_ff=192, top_k=6, n_shared=2, capacity_factor=None, fused=False)
-    m = m.to(torch.bfloat16)
+    m = MoEBlock(d, E, d_ff=d_ff, top_k=k, n_shared=S, bias=bias, capacity_factor=None,
+                 fused=False)
+    if bias:
+        g_b = torch.Generator().manual_seed(seed + 11)
+        with torch.no_grad():
+            for name in ("b_in", "b_out", "b_sh_in", "b_sh_out"):
+                t = getattr(m, name)
+                if t is not None:
+                    t.copy_(torch.randn(t.shape, generator=g_b) * 0.1)
+    m = m.to(dtype)
     if zero_router:
         with torch.no_grad():
             m.router.W.zero_()
-    x = torch.randn(T, 576).to(torch.bfloat16)
-    g = torch.randn(T, 576).to(torch.bfloat16)
-    p = R.Params(m.router.W.data.clone(), m.W_in.data.clone(), m.W_out.data.clone(),
-                 m.W_sh_in.data.clone(), m.W_sh_out.data.clone())
+    x = torch.randn(T, d).to(dtype)
+    g = torch.randn(T, d).to(dtype)
+    fields = ("W_in", "W_out", "W_sh_in", "W_sh_out", "b_in", "b_out", "b_sh_in", "b_sh_out")
+    p = R.Params(m.router.W.data.clone(), *(None if getattr(m, f) is None
+                                             else getattr(m, f).data.clone() for f in fields))
     return m, p, x, g
 
 
+def close(name, got, ref, dtype):
+    """16-bit blocks: the bf16 bar.  fp32 blocks: fp32 rounding (max abs <= 1e-4 on the
+    tensor's scale, rel-L2 <= 1e-5)."""
+    if dtype == torch.float32:
+        assert_close_bf16(name, got.float(), ref, max_abs=1e-4, rel_l2=1e-5)
+    else:
+        assert_close_bf16(name, got.float(), ref)
+
+
 def check_against_oracle(x, p, g, logits, idx, counts, out, aux, grads, train, backward,
-                         bias=None):
-    """Routing bit-exact, outputs and gradients to the bf16 bar, against the oracle run on
-    the GPU's own logits (the router GEMM's bf16 values)."""
-    ref = R.block(x, p, 6, train=train, grad_out=g if backward else None, fp32=True,
-                  logits=logits, logit_bias=bias)
+                         k=6):
+    """Routing bit-exact, outputs and gradients to the dtype's bar, against the oracle run
+    on the GPU's own logits (the router GEMM's values, offset included)."""
+    dt = x.dtype
+    E = p.W_in.shape[0]
+    ref = R.block(x, p, k, train=train, grad_out=g if backward else None, fp32=True,
+                  logits=logits)
     assert torch.equal(idx, ref.topk_idx), "routing indices differ"
     assert torch.equal(counts.long(), ref.counts), "counts differ"
-    sids, _, offs, dcounts, _, inv = mk.moe_dispatch(idx.to(DEV), 76)
-    r_sids, _, r_offs, r_counts, _, r_inv = R.dispatch_buffers(ref.topk_idx, 76, mk.ALIGN_M)
+    sids, _, offs, dcounts, _, inv = mk.moe_dispatch(idx.to(DEV), E)
+    r_sids, _, r_offs, r_counts, _, r_inv = R.dispatch_buffers(ref.topk_idx, E, mk.ALIGN_M)
     assert torch.equal(sids.cpu(), r_sids) and torch.equal(inv.cpu(), r_inv)
     assert torch.equal(offs.cpu(), r_offs) and torch.equal(dcounts.cpu(), r_counts)
-    assert_close_bf16("out", out.float(), ref.out)
+    close("out", out, ref.out, dt)
     if train:
         torch.testing.assert_close(aux.float().cpu().reshape(()), ref.aux_loss.float().reshape(()),
                                    rtol=1e-5, atol=1e-7)
@@ -72,59 +98,52 @@ def check_against_oracle(x, p, g, logits, idx, counts, out, aux, grads, train, b
         return ref
     gr = ref.grads
     d_logits = gr["logits"]
-    assert_close_bf16("dx", grads["x"].float(), gr["x"] + d_logits @ p.W.float().t())
-    assert_close_bf16("d router.W", grads["W"].float(), x.float().t() @ d_logits)
-    for name in ("W_in", "W_out", "W_sh_in", "W_sh_out"):
-        assert_close_bf16(f"d {name}", grads[name].float(), gr[name])
+    close("dx", grads["x"], gr["x"] + d_logits @ p.W.float().t(), dt)
+    close("d router.W", grads["W"], x.float().t() @ d_logits, dt)
+    for name in grads:
+        if name not in ("x", "W"):
+            close(f"d {name}", grads[name], gr[name], dt)
     return ref
 
 
-def run_case(T, train, backward, zero_router=False):
-    """The drop-in MoEBlock, as a caller runs it (one fused autograd node on the GPU)."""
-    m, p, x, g = build(T, zero_router=zero_router)
+def run_case(T, train, backward, *, logit_bias=None, **cfg):
+    """The drop-in MoEBlock, as a caller runs it (one op per direction on the GPU)."""
+    m, p, x, g = build(T, **cfg)
+    dt = x.dtype
     m = m.to(DEV).train(train)
     xg = x.to(DEV).requires_grad_(backward)
-    print(f"[block] T={T} train={train} backward={backward} zero_router={zero_router}",
-          flush=True)
-    out = m(xg)
-    assert m._use_kernel(xg.reshape(-1, 576)), "the HIP path was not taken"
+    print(f"[block] T={T} train={train} backward={backward} cfg={cfg} "
+          f"skewed={logit_bias is not None}", flush=True)
+    if logit_bias is None:
+        out = m(xg)
+        aux = m.aux_loss
+        idx, counts = m._routing, m.expert_counts
+        assert m._use_kernel(xg.reshape(-1, x.shape[1])), "the HIP path was not taken"
+    else:
+        # The reference router has no bias: the offset goes in through the op's hook.
+        out, aux, counts, idx = mk.block_forward(
+            xg, m.router.W, m.W_in, m.W_out, m.W_sh_in, m.W_sh_out, m.b_in, m.b_out,
+            m.b_sh_in, m.b_sh_out, m.top_k, m.router.wants_probs(),
+            m.router.normalize_weights, "silu", m.router.aux_loss_coef,
+            logit_bias=logit_bias.to(DEV))
     if backward:
-        torch.autograd.backward([out, m.aux_loss], [g.to(DEV), torch.ones_like(m.aux_loss)])
+        torch.autograd.backward([out, aux], [g.to(DEV), torch.ones_like(aux)])
     torch.cuda.synchronize()
-    logits = (x.to(DEV) @ m.router.W.detach()).float().cpu()  # the block's own router GEMM
+    logits = x.to(DEV) @ m.router.W.detach()  # the block's own router GEMM
+    if logit_bias is not None:
+        logits = (logits.float() + logit_bias.to(DEV)).to(logits.dtype)
+    logits = logits.float().cpu()
     grads = {}
     if backward:
         grads = {"x": xg.grad.cpu(), "W": m.router.W.grad.cpu()}
-        grads.update({n: getattr(m, n).grad.cpu() for n in ("W_in", "W_out", "W_sh_in",
-                                                            "W_sh_out")})
-    return check_against_oracle(x, p, g, logits, m._routing.cpu(), m.expert_counts.cpu(),
-                                out.detach().cpu(), m.aux_loss.detach().cpu(), grads, train,
-                                backward)
-
-
-def run_ops_case(T, bias):
-    """The same kernels composed op by op (route -> moe_dispatch -> moe_block, balance loss
-    in torch), with a harness-level per-expert offset added to the logits: the reference
-    router has no bias, so the skewed workload cannot go through MoEBlock itself."""
-    m, p, x, g = build(T)
-    m = m.to(DEV).train(True)
-    xg = x.to(DEV).requires_grad_(True)
-    print(f"[ops] T={T} skewed", flush=True)
-    logits = (xg @ m.router.W).float()
-    w, idx, probs = mk.route(logits + bias.to(DEV), 6, True, True,
-                             mk.route_dtype_code(torch.bfloat16))
-    sids, _, offs, counts, _, inv = mk.moe_dispatch(idx, 76)
-    out, _ = mk.moe_block(xg, m.W_in, m.W_out, m.W_sh_in, m.W_sh_out, None, None, None, None,
-                          w, sids, offs, counts, inv, "silu")
-    aux = m.router.balance_loss(probs, counts)
-    torch.autograd.backward([out, aux], [g.to(DEV), torch.ones_like(aux)])
-    torch.cuda.synchronize()
-    grads = {"x": xg.grad.cpu(), "W": m.router.W.grad.cpu()}
-    grads.update({n: getattr(m, n).grad.cpu() for n in ("W_in", "W_out", "W_sh_in",
-                                                        "W_sh_out")})
-    return check_against_oracle(x, p, g, logits.detach().cpu(), idx.cpu(), counts.cpu(),
-                                out.detach().cpu(), aux.detach().cpu(), grads, True, True,
-                                bias=bias)
+        for n in ("W_in", "W_out", "W_sh_in", "W_sh_out", "b_in", "b_out", "b_sh_in",
+                  "b_sh_out"):
+            t = getattr(m, n)
+            if t is not None:
+                grads[n] = t.grad.cpu()
+    return check_against_oracle(x, p, g, logits, idx.cpu(), counts.cpu(),
+                                out.detach().cpu(), aux.detach().cpu(), grads, train,
+                                backward, k=m.top_k)
 
 
 def test_forward_T2048_train():
@@ -146,13 +165,43 @@ def test_eval_forward_backward_T512():
     run_case(512, train=False, backward=True)
 
 
-def test_skewed_T16384_forward_backward():
-    bias = torch.from_numpy(np.load(ZIPF, allow_pickle=False))
-    ref = run_ops_case(16384, bias)
+def test_skewed_T16384_forward_backward_block_path():
+    """Config 4 through the block path itself: the fused router backward (combine_dx with
+    d(logits) W^T, router_dw's split-K), the in-launch balance loss and the dW split-K
+    under a hot expert holding ~15 % of the pairs."""
+    bias = torch.from_numpy(np.load(ZIPF, allow_pickle=False)).float()
+    ref = run_case(16384, train=True, backward=True, logit_bias=bias)
     share = ref.counts.double() / ref.counts.sum()
     assert 0.12 < float(share.max()) < 1 / 6 + 1e-9   # the hot expert holds ~15 %
+
+
+def test_prefill_layer_T32768_eval():
+    """One MoE call of the 20-layer prefill (batch 4 x 8192): T = 32768, 196,608 pairs,
+    about 262 k grouped-GEMM rows and 302 MB of expert output rows."""
+    ref = run_case(32768, train=False, backward=False)
+    assert int(ref.counts.sum()) == 32768 * 6
 
 
 def test_zero_router_sends_every_token_to_the_same_experts():
     ref = run_case(2048, train=True, backward=True, zero_router=True)
     assert int((ref.counts > 0).sum()) == 6 and int(ref.counts.max()) == 2048
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("bias", [False, True])
+@pytest.mark.parametrize("S", [0, 2])
+def test_block_dtype_bias_shared_matrix(dtype, bias, S):
+    """The block node at nanoSpeaker's shape in every dtype it takes, with and without
+    biases and shared experts (fp32 finishes the router GEMM's backward in torch)."""
+    run_case(300, train=True, backward=True, dtype=dtype, bias=bias, S=S)
+
+
+@pytest.mark.parametrize("cfg", [
+    dict(d=72, E=10, d_ff=96, k=3, S=1),    # d % 16 != 0, E % 4 != 0: router bwd in torch
+    dict(d=64, E=16, d_ff=96, k=10, S=2),   # k > 8: the general dx combine
+    dict(d=64, E=8, d_ff=96, k=2, S=3),     # more than two shared experts
+    dict(d=128, E=12, d_ff=192, k=4, S=0, bias=True),
+])
+@pytest.mark.parametrize("train", [True, False])
+def test_block_other_shapes(cfg, train):
+    run_case(257, train=train, backward=True, **cfg)

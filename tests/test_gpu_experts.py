@@ -11,7 +11,7 @@ import pytest
 import torch
 
 from oracle import moe_ref as R
-from tests.helpers import F32_ATOL, assert_close_bf16
+from tests.helpers import F32_ATOL, assert_close_bf16, lib_options
 
 pytestmark = pytest.mark.gpu
 
@@ -106,16 +106,15 @@ def test_experts_forward_backward(dtype, shape, k, S, bias, T):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("shape", ["wide_h64", "wide_h96", "ns_h128"])
 @pytest.mark.parametrize("T", [37, 300, 1000])
-def test_forward_tile_heights(dist, mb, dtype, shape, T, monkeypatch):
+def test_forward_tile_heights(dist, mb, dtype, shape, T):
     """Both forward tile heights (64- and 96-row tiles, forced) and both weight prefetch
     distances (2 and 3 steps; 3 only where the step counts divide) against the oracle,
     with ragged last tiles and the shared experts' full-T groups."""
-    monkeypatch.setenv("NSMOE_FWD_MB", mb)
-    monkeypatch.setenv("NSMOE_FWD_D", dist)
     d, E, d_ff = SHAPES[shape]
     p, x, gout, tw, ti = make_case(d, E, d_ff, 6, 2, T % 2 == 0, T, dtype, seed=T + int(mb))
     ref_out, _ = oracle_fwd_bwd(p, x, gout, tw, ti, "silu", with_grad=False)
-    out, _ = gpu_fwd_bwd(p, x, gout, tw, ti, "silu", with_grad=False)
+    with lib_options(fwd_rows=16 * int(mb), fwd_dist=int(dist)):
+        out, _ = gpu_fwd_bwd(p, x, gout, tw, ti, "silu", with_grad=False)
     check("out", out, ref_out, dtype)
 
 
@@ -124,19 +123,17 @@ def test_forward_tile_heights(dist, mb, dtype, shape, T, monkeypatch):
                           ("6", "3", "2", "3"), ("4", "2", "2", "5")])
 @pytest.mark.parametrize("shape", ["wide_h64", "ns_h128"])
 @pytest.mark.parametrize("T", [37, 1000])
-def test_backward_tile_heights_and_prefetch(mb, dist, bwd_dist, bwd_mb, shape, T, monkeypatch):
+def test_backward_tile_heights_and_prefetch(mb, dist, bwd_dist, bwd_mb, shape, T):
     """The dX-row kernel at both tile heights and several weight prefetch distances, and
     the GLU-backward kernel at 48-, 64- and 80-row tiles and both of its prefetch distances
     (all forced), checked through dx and every weight gradient."""
-    monkeypatch.setenv("NSMOE_DX_MB", mb)
-    monkeypatch.setenv("NSMOE_DX_D", dist)
-    monkeypatch.setenv("NSMOE_BWD_D", bwd_dist)
-    monkeypatch.setenv("NSMOE_BWD_MB", bwd_mb)
     d, E, d_ff = SHAPES[shape]
     p, x, gout, tw, ti = make_case(d, E, d_ff, 6, 2, T % 2 == 1, T, torch.bfloat16,
                                    seed=T + int(mb))
     ref_out, ref_g = oracle_fwd_bwd(p, x, gout, tw, ti, "silu")
-    out, g = gpu_fwd_bwd(p, x, gout, tw, ti, "silu")
+    with lib_options(dx_rows=16 * int(mb), dx_dist=int(dist), bwd_dist=int(bwd_dist),
+                     bwd_rows=16 * int(bwd_mb)):
+        out, g = gpu_fwd_bwd(p, x, gout, tw, ti, "silu")
     check("out", out, ref_out, torch.bfloat16)
     for n in ref_g:
         check(f"grad {n}", g[n], ref_g[n], torch.bfloat16)

@@ -17,6 +17,7 @@ pytestmark = pytest.mark.gpu
 
 mk = pytest.importorskip("nanospeaker_amd.moe_kernel")
 from nanospeaker_amd import MoEBlock  # noqa: E402
+from tests.helpers import lib_options  # noqa: E402
 
 DEV = "cuda"
 
@@ -99,24 +100,52 @@ def test_forward_replays_equal_eager():
             assert torch.equal(v, ref), f"replay {r}"
 
 
-def test_side_stream_matches_single_stream(monkeypatch):
+def test_side_stream_matches_single_stream():
     """The library runs the weight packing and the dW stage on a second stream (forked
-    and joined with events); with NSMOE_SINGLE_STREAM set everything stays on the caller's
-    stream.  Both orders must give the same bits, step after step."""
+    and joined with events); with the "single_stream" option everything stays on the
+    caller's stream.  Both orders must give the same bits, step after step (the pack
+    cache is emptied before each step, so every step packs on the side stream)."""
     m, x, g = _block(8192, seed=2)
     params = list(m.parameters())
     one = torch.ones((), dtype=torch.float32, device=DEV)
 
     def step():
+        mk.PACKS.clear()
         xg = x.detach().requires_grad_(True)
         out = m(xg)
         grads = torch.autograd.grad([out, m.aux_loss], [xg] + params, [g, one])
         return [out.detach(), m.aux_loss.detach()] + list(grads)
 
     two = [step() for _ in range(2)]
-    monkeypatch.setenv("NSMOE_SINGLE_STREAM", "1")
-    single = step()
+    with lib_options(single_stream=1):
+        single = step()
     torch.cuda.synchronize()
     for r, vals in enumerate(two):
         for i, (a, b) in enumerate(zip(vals, single)):
             assert torch.equal(a, b), f"step {r}: tensor {i}"
+
+
+def test_replay_repacks_weights_updated_in_place():
+    """The pack cache is bypassed while a graph is captured, so the captured forward packs
+    the weights on every replay: an in-place update between replays (an optimizer step
+    outside the graph) is seen by the next replay."""
+    m, x, _ = _block(1024, seed=3)
+    with torch.no_grad():
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                m(x)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out = m(x)
+        for r in range(3):
+            m.W_in.mul_(0.9)
+            m.W_sh_out.add_(0.01)
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            ref = m(x)
+            assert torch.equal(out, ref), f"replay {r} used stale packed weights"
