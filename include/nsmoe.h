@@ -144,6 +144,18 @@ int nsmoe_dispatch(const int64_t* topk_idx, int64_t n_pairs, int32_t n_experts,
                    int32_t* counts, int32_t* n_post_pad, int32_t* inv, void* workspace,
                    size_t workspace_bytes, void* stream);
 
+/* nsmoe_dispatch without a workspace: no counterpart in the reference.  For callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments, outputs and kernels as
+ * nsmoe_dispatch; the scratch is a 4 MiB array owned by the library on each device (held
+ * until the process ends), so it takes calls whose nsmoe_dispatch_workspace_size is at
+ * most 4 MiB -- up to 14,128,128 pairs at 76 experts, 262,144 at 1024 -- and rejects
+ * larger ones with error 1.  It allocates nothing.  Every call on a device shares that
+ * device's array: calls that overlap on one device (two streams, two threads) race. */
+int nsmoe_dispatch_noalloc(const int64_t* topk_idx, int64_t n_pairs, int32_t n_experts,
+                           int32_t* sorted_ids, int32_t* expert_ids, int32_t* pad_offsets,
+                           int32_t* counts, int32_t* n_post_pad, int32_t* inv, void* stream);
+
 /* ---- experts --------------------------------------------------------------------------
  * Routed experts (moe_experts, src/model/moe_kernel.py:558-617) plus, when n_shared > 0,
  * the always-on shared experts (MoEBlock._shared, src/model/moe.py:310-329) folded in

@@ -61,6 +61,8 @@ SIGNATURES = {
     "nsmoe_dispatch_l_cap": (_i64, [_i64, _i32]),
     "nsmoe_dispatch_workspace_size": (_sz, [_i64, _i32]),
     "nsmoe_dispatch": (ctypes.c_int, [_vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "nsmoe_dispatch_noalloc": (ctypes.c_int, [_vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
+                                              _vp]),
     "nsmoe_pack_sizes": (ctypes.c_int, [ctypes.POINTER(ExpertsArgs), ctypes.POINTER(_sz),
                                         ctypes.POINTER(_sz)]),
     "nsmoe_pack_weights": (ctypes.c_int, [ctypes.POINTER(ExpertsArgs), _vp, _vp, _vp]),

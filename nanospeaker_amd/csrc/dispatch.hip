@@ -24,6 +24,8 @@
 //   With the block's balance loss folded in, the place launch has one more workgroup: it
 //   forms the experts' totals the same way and reduces the router's column-sum partials
 //   to the loss (balance.h) while the others place their chunks.
+#include <mutex>
+
 #include "balance.h"
 #include "nsmoe_capi_internal.h"
 #include "nsmoe_common.h"
@@ -280,4 +282,66 @@ extern "C" int nsmoe_dispatch(const int64_t* topk_idx, int64_t n_pairs, int32_t 
                               void* workspace, size_t workspace_bytes, void* stream) {
   return dispatch_launch(topk_idx, n_pairs, n_experts, sorted_ids, expert_ids, pad_offsets,
                          counts, n_post_pad, inv, workspace, workspace_bytes, nullptr, stream);
+}
+
+// ---- nsmoe_dispatch_noalloc: the same dispatch with library-owned scratch ---------------
+//
+// The [chunks, E] histogram lives in a file-scope device array instead of a caller
+// workspace, for callers that cannot allocate.  Each device that loads the library holds
+// its own copy for the life of the process; its address on the current device comes from
+// hipGetSymbolAddress, once per device, on that device's first call (the array's name is
+// only a host-side stand-in and is never handed to a kernel).  The histogram kernel writes
+// every entry the place kernel reads, so nothing in the array has to start at zero; it
+// keeps the last call's contents.  Calls that overlap on one device race on it.
+
+namespace nsmoe {
+
+constexpr size_t kDispatchScratchBytes = 4u << 20;
+static __device__ __align__(256) unsigned char scratch[kDispatchScratchBytes];
+
+constexpr int kScratchDevices = 64;
+static void* g_scratch[kScratchDevices];
+static std::mutex g_scratch_mu;
+
+static int dispatch_scratch(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kScratchDevices) {
+    set_error("dispatch_noalloc: no usable current device (%s)", hipGetErrorString(e));
+    return NSMOE_EHIP;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      set_error("dispatch_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(e));
+      return NSMOE_EHIP;
+    }
+    g_scratch[dev] = p;
+  }
+  *out = g_scratch[dev];
+  return NSMOE_OK;
+}
+
+}  // namespace nsmoe
+
+extern "C" int nsmoe_dispatch_noalloc(const int64_t* topk_idx, int64_t n_pairs,
+                                      int32_t n_experts, int32_t* sorted_ids,
+                                      int32_t* expert_ids, int32_t* pad_offsets, int32_t* counts,
+                                      int32_t* n_post_pad, int32_t* inv, void* stream) {
+  NSMOE_REQUIRE(n_pairs >= 0 && n_pairs < (int64_t)INT32_MAX / 2,
+                "dispatch_noalloc: n_pairs %lld out of range", (long long)n_pairs);
+  NSMOE_REQUIRE(n_experts >= 1 && n_experts <= DISPATCH_MAX_EXPERTS,
+                "dispatch_noalloc: n_experts %d outside [1, %d]", n_experts,
+                DISPATCH_MAX_EXPERTS);
+  const size_t need = nsmoe_dispatch_workspace_size(n_pairs, n_experts);
+  NSMOE_REQUIRE(need <= kDispatchScratchBytes,
+                "dispatch_noalloc: %lld pairs over %d experts need %zu B of scratch, above "
+                "its %zu B maximum (use nsmoe_dispatch with a workspace)",
+                (long long)n_pairs, n_experts, need, kDispatchScratchBytes);
+  void* ws = nullptr;
+  if (need > 0) NSMOE_TRY(dispatch_scratch(&ws));
+  return dispatch_launch(topk_idx, n_pairs, n_experts, sorted_ids, expert_ids, pad_offsets,
+                         counts, n_post_pad, inv, ws, kDispatchScratchBytes, nullptr, stream);
 }
