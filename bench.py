@@ -44,6 +44,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--tokens", type=int, default=8192)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="time only the headline workload (T=8192 fwd+bwd)")
     ap.add_argument("--eager", action="store_true",
                     help="report the eagerly issued step as `value` (default: HIP-graph replay)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -100,7 +102,10 @@ def kernel_units(name: str, T: int, k: int, S: int, d: int, H: int, E: int):
 
 
 def time_gpu(m, x, g, steps: int, warmup: int):
+    """Eager fwd+bwd step time, its host enqueue time, per-kernel launch times and the
+    eager forward (no_grad, weights unchanged, so the forward reuses the cached packs)."""
     from nanospeaker_amd import _native as nat
+    from nanospeaker_amd import moe_kernel as mk
 
     params = [p for p in m.parameters()]
     xg = x.detach().requires_grad_(True)
@@ -108,7 +113,9 @@ def time_gpu(m, x, g, steps: int, warmup: int):
 
     def step():
         # Every gradient of the block (input, router, experts) is computed and returned;
-        # none is accumulated into a .grad buffer.
+        # none is accumulated into a .grad buffer.  A training step's weights are new each
+        # step, so the weight-pack cache is emptied first: every step packs.
+        mk.PACKS.clear()
         out = m(xg)
         return torch.autograd.grad([out, m.aux_loss], [xg] + params, [g, one])
 
@@ -253,52 +260,6 @@ def committed_traffic(kernel):
     return None
 
 
-def time_gpu_graph(m, x, g, steps: int, warmup: int):
-    """The same fwd+bwd step (and the forward alone), captured once in a HIP graph and
-    replayed: every replay runs every kernel of the step on the resident inputs; only the
-    host-side enqueue (Python, autograd, the library's argument setup) is removed.
-    torch's capture recipe: warm-up on a side stream, then capture."""
-    params = [p for p in m.parameters()]
-    xg = x.detach().requires_grad_(True)
-    one = torch.ones((), dtype=torch.float32, device=x.device)
-
-    def step():
-        # All gradients of the block (input, router, experts) are returned by the step, in
-        # the graph's own memory; no .grad buffer is zeroed or accumulated into.
-        out = m(xg)
-        return torch.autograd.grad([out, m.aux_loss], [xg] + params, [g, one])
-
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        for _ in range(max(warmup, 2)):
-            step()
-        with torch.no_grad():
-            for _ in range(2):
-                m(x)
-    torch.cuda.current_stream().wait_stream(side)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        step()
-    fwd_graph = torch.cuda.CUDAGraph()
-    with torch.no_grad():
-        with torch.cuda.graph(fwd_graph):
-            m(x)
-
-    def timed(gr):
-        for _ in range(warmup):
-            gr.replay()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(steps):
-            gr.replay()
-        torch.cuda.synchronize()
-        return (time.perf_counter() - t0) * 1e3 / steps
-
-    return timed(graph), timed(fwd_graph)
-
-
 def calibrate_copy():
     """One dispatch of torch's elementwise negation over 256 MiB of bf16: it reads and
     writes exactly COPY_BYTES each, so under `rocprofv3 --pmc FETCH_SIZE` (or WRITE_SIZE)
@@ -311,32 +272,272 @@ def calibrate_copy():
     del src, dst
 
 
-def cpu_baseline(seconds: float):
-    """The reference's eager bf16 CPU path (restated in oracle/moe_ref.py), fwd + bwd."""
+
+
+def graph_time(fn, steps: int, warmup: int) -> float:
+    """Milliseconds per replay of `fn` captured once in a HIP graph (torch's recipe:
+    warm-up on a side stream, then capture).  Every replay runs every kernel `fn`
+    issues; the weight packs are captured too (the pack cache is bypassed under
+    capture), so each replay re-packs the weights."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(max(warmup, 2)):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    del graph
+    return ms
+
+
+def eager_time(fn, steps: int, warmup: int) -> float:
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def train_step_fn(m, x, g, logit_bias=None):
+    """One fwd+bwd of the block returning every gradient (input, router, experts)."""
+    from nanospeaker_amd import moe_kernel as mk
+
+    params = list(m.parameters())
+    xg = x.detach().requires_grad_(True)
+    one = torch.ones((), dtype=torch.float32, device=x.device)
+
+    def step():
+        if logit_bias is None:
+            out, aux = m(xg), m.aux_loss
+        else:  # the skewed workload: the router offset enters through the op's hook
+            out, aux, _, _ = mk.block_forward(
+                xg, m.router.W, m.W_in, m.W_out, m.W_sh_in, m.W_sh_out, None, None, None,
+                None, 6, True, True, "silu", 1e-2, logit_bias=logit_bias)
+        return torch.autograd.grad([out, aux], [xg] + params, [g, one])
+
+    return step
+
+
+def zipf_bias():
+    import numpy as np
+
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "tests", "golden",
+                        "zipf_logit_bias.npy")
+    return torch.from_numpy(np.load(path, allow_pickle=False)).float()
+
+
+def config1(steps, warmup):
+    """T = 2048 forward (train mode, no autograd)."""
+    m, x, _ = build_block(2048)
+    m, x = m.cuda(), x.cuda()
+    with torch.no_grad():
+        g_ms = graph_time(lambda: m(x), steps, warmup)
+        e_ms = eager_time(lambda: m(x), steps, warmup)
+    return {"workload": "T=2048 forward, train mode, bf16",
+            "tokens_per_s": round(2048 / (g_ms / 1e3), 1), "ms": round(g_ms, 4),
+            "eager_tokens_per_s": round(2048 / (e_ms / 1e3), 1), "eager_ms": round(e_ms, 4)}
+
+
+def config3(steps, warmup):
+    """T = 64 decode call (eval branch): microseconds per call, eager with the packs
+    cached (weights unchanged between decode steps), eager re-packing every call, and
+    graph-replayed (packs inside the graph)."""
+    from nanospeaker_amd import moe_kernel as mk
+
+    m, x, _ = build_block(64)
+    m, x = m.cuda().eval(), x.cuda()
+    reps = max(steps, 50)
+    with torch.no_grad():
+        cached = eager_time(lambda: m(x), reps, warmup)
+
+        def repack():
+            mk.PACKS.clear()
+            m(x)
+
+        fresh = eager_time(repack, reps, warmup)
+        g_ms = graph_time(lambda: m(x), reps, warmup)
+        m(x)
+    empty = int((m.expert_counts == 0).sum())
+    return {"workload": "T=64 decode call, eval branch, bf16",
+            "us_per_call": round(g_ms * 1e3, 2),
+            "eager_us_per_call_cached_packs": round(cached * 1e3, 2),
+            "eager_us_per_call_repacking": round(fresh * 1e3, 2),
+            "empty_experts": empty}
+
+
+def config4(steps, warmup):
+    """T = 16384 fwd+bwd with the Zipf(1.2) router offset, through the block op."""
+    m, x, g = build_block(16384)
+    m, x, g = m.cuda(), x.cuda(), g.cuda()
+    bias = zipf_bias().cuda()
+    g_ms = graph_time(train_step_fn(m, x, g, bias), steps, warmup)
+    from nanospeaker_amd import moe_kernel as mk
+
+    with torch.no_grad():
+        _, _, counts, _ = mk.block_forward(
+            x, m.router.W, m.W_in, m.W_out, m.W_sh_in, m.W_sh_out, None, None, None, None, 6,
+            True, True, "silu", 1e-2, logit_bias=bias)
+    share = float(counts.max()) / float(counts.sum())
+    return {"workload": "T=16384 fwd+bwd, Zipf(1.2) router offset, train, bf16",
+            "tokens_per_s": round(16384 / (g_ms / 1e3), 1), "ms": round(g_ms, 4),
+            "hot_expert_share": round(share, 4)}
+
+
+def build_decoder(n_layers=20, seed=0):
+    from nanospeaker_amd.decoder import Decoder, DecoderConfig
+
+    torch.manual_seed(seed)
+    model = Decoder(DecoderConfig(n_layers=n_layers)).to(torch.bfloat16).eval()
+    idx = torch.randint(0, 32768, (4, 8192))
+    return model, idx
+
+
+def config5(steps, warmup):
+    """The 20-layer prefill (batch 4 x 8192, eval, bf16; attention on SDPA, window 512 with
+    every fourth layer global): tokens/s, and the MoE calls' share of the forward from
+    HIP events around each call."""
+    model, idx = build_decoder()
+    model, idx = model.cuda(), idx.cuda()
+    pairs = []
+
+    def hook(blk, h):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        y = blk.ffn(h)
+        b.record()
+        pairs.append((a, b))
+        return y
+
+    reps = max(2, min(steps, 3))
+    with torch.no_grad():
+        for _ in range(max(1, min(warmup, 2))):
+            model(idx)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            model(idx)
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / reps
+        model(idx, ffn_hook=hook)
+        torch.cuda.synchronize()
+        moe_ms = sum(a.elapsed_time(b) for a, b in pairs)
+        t0 = time.perf_counter()
+        model(idx, ffn_hook=hook)
+        torch.cuda.synchronize()
+        hooked_ms = (time.perf_counter() - t0) * 1e3
+    n = idx.numel()
+    return {"workload": "20-layer decoder prefill, batch 4 x 8192, eval, bf16; SDPA attention "
+                        "(window 512, global_every 4), HIP MoE in every layer",
+            "tokens_per_s": round(n / (ms / 1e3), 1), "ms": round(ms, 3),
+            "moe_ms": round(moe_ms, 3), "moe_share": round(moe_ms / hooked_ms, 4),
+            "moe_calls": len(pairs), "moe_tokens_per_call": n}
+
+
+def cpu_info():
+    model, flags = "unknown", set()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name") and model == "unknown":
+                    model = line.split(":", 1)[1].strip()
+                elif line.startswith("flags") and not flags:
+                    flags = set(line.split(":", 1)[1].split())
+    except OSError:
+        pass
+    return {"cpu": model, "amx_bf16": "amx_bf16" in flags, "avx512_bf16": "avx512_bf16" in flags}
+
+
+def cpu_threads() -> int:
+    """The threads the CPU baseline uses: every core of this process's affinity, capped at
+    OMP_NUM_THREADS where the launcher sets it (the GPU pool gives a one-GPU job a share
+    of 16 host cores and sets OMP_NUM_THREADS=16 to match)."""
+    n = len(os.sched_getaffinity(0))
+    cap = os.environ.get("OMP_NUM_THREADS")
+    return min(n, int(cap)) if cap and cap.isdigit() and int(cap) > 0 else n
+
+
+def _median_time(fn, reps, budget_s):
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < reps and (not times or time.perf_counter() - t_start < budget_s):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
+def cpu_baseline(seconds: float, configs: bool):
+    """The reference's eager bf16 CPU path (restated op for op in oracle/moe_ref.py,
+    pinned bit-exact to the reference by tests/golden), on this host's cores."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from oracle import moe_ref as R
 
-    cores = min(len(os.sched_getaffinity(0)), 16)
+    cores = cpu_threads()
     torch.set_num_threads(cores)
     c = R.nanospeaker_config()
     p = R.make_params(0, c["d"], c["E"], c["d_ff"], n_shared=c["n_shared"]).to(dtype=torch.bfloat16)
-    T = 8192
-    x = torch.randn(T, c["d"]).to(torch.bfloat16)
-    g = torch.randn(T, c["d"]).to(torch.bfloat16)
-    R.block(x[:512], p, c["top_k"], grad_out=g[:512])  # warm-up on a slice
-    times = []
-    t_start = time.perf_counter()
-    while len(times) < 5 and (time.perf_counter() - t_start) < seconds:
+
+    def data(T):
+        return torch.randn(T, c["d"]).to(torch.bfloat16), torch.randn(T, c["d"]).to(torch.bfloat16)
+
+    x, g = data(8192)
+    R.block(x[:512], p, 6, grad_out=g[:512])  # warm-up on a slice
+    med, n = _median_time(lambda: R.block(x, p, 6, grad_out=g), 5, seconds)
+    out = {"value": round(8192 / med, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
+           "sample": f"{n} fwd+bwd steps of the eager bf16 block at T=8192 (median "
+                     f"{med * 1e3:.0f} ms; oracle/moe_ref.py, torch CPU)", **cpu_info()}
+    if not configs:
+        return out
+    per = {}
+    x1, _ = data(2048)
+    with torch.no_grad():
+        med, n = _median_time(lambda: R.block(x1, p, 6), 5, seconds / 3)
+    per["c1_T2048_fwd"] = {"tokens_per_s": round(2048 / med, 1), "runs": n}
+    x3, _ = data(64)
+    with torch.no_grad():
+        R.block(x3, p, 6, train=False)
+        med, n = _median_time(lambda: R.block(x3, p, 6, train=False), 21, seconds / 3)
+    per["c3_T64_eval"] = {"us_per_call": round(med * 1e6, 1), "runs": n}
+    x4, g4 = data(16384)
+    bias = zipf_bias()
+    med, n = _median_time(lambda: R.block(x4, p, 6, grad_out=g4, logit_bias=bias), 3, seconds)
+    per["c4_T16384_skew_fwd_bwd"] = {"tokens_per_s": round(16384 / med, 1), "runs": n}
+    # config 5: a 4-layer stack in the 20-layer pattern (1 global + 3 windowed layers) at
+    # the full batch, on the block's eager path, scaled to 20 layers; the tied head once.
+    model, idx = build_decoder(n_layers=4)
+    with torch.no_grad():
+        def stack():
+            x5, _ = model.trunk(idx)
+            return x5
+
         t0 = time.perf_counter()
-        R.block(x, p, c["top_k"], grad_out=g)
-        times.append(time.perf_counter() - t0)
-    times.sort()
-    med = times[len(times) // 2]
-    return {
-        "value": round(T / med, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
-        "sample": f"{len(times)} fwd+bwd steps of the eager bf16 block at T=8192 "
-                  f"(median {med * 1e3:.0f} ms; oracle/moe_ref.py, torch CPU)",
-    }
+        h5 = stack()
+        t_stack = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        h5 @ model.embed.weight.t()
+        t_head = time.perf_counter() - t0
+    est = 5 * t_stack + t_head
+    per["c5_prefill"] = {"tokens_per_s": round(idx.numel() / est, 1),
+                         "sample": f"one pass of a 4-layer stack (1 global + 3 windowed) at "
+                                   f"batch 4 x 8192 ({t_stack:.1f} s) x 5 + the tied head "
+                                   f"({t_head:.1f} s)"}
+    out["configs"] = per
+    return out
 
 
 def main():
@@ -358,14 +559,19 @@ def main():
     if a.calibrate_copy:
         calibrate_copy()
     m, x, g = build_block(T)
-    m = m.cuda()
-    x, g = x.cuda(), g.cuda()
+    m, x, g = m.cuda(), x.cuda(), g.cuda()
+    graph_ms = graph_fwd_ms = None
     if not a.eager:  # captured before any eager use of the module (torch's recipe)
-        graph_ms, graph_fwd_ms = time_gpu_graph(m, x, g, a.steps, a.warmup)
+        print(f"[bench] T={T} fwd+bwd, HIP graph", file=sys.stderr, flush=True)
+        graph_ms = graph_time(train_step_fn(m, x, g), a.steps, a.warmup)
+        with torch.no_grad():
+            graph_fwd_ms = graph_time(lambda: m(x), a.steps, a.warmup)
+    print(f"[bench] T={T} eager and per-kernel timing", file=sys.stderr, flush=True)
     ms, fwd_ms, kernels, host_ms = time_gpu(m, x, g, a.steps, a.warmup)
     eager_ms, eager_fwd_ms = ms, fwd_ms
     if not a.eager:
         ms, fwd_ms = graph_ms, graph_fwd_ms
+    del m, x, g
 
     k, S, d, H, E = 6, 2, 576, 128, 76
     dom = max(kernels, key=lambda n: kernels[n][0] * kernels[n][1]) if kernels else None
@@ -409,8 +615,18 @@ def main():
         "kernels_us": {n: round(v[0] * 1e3, 2) for n, v in kernels.items()},
         "roofline": roofline,
     }
+    if not a.no_configs:
+        torch.cuda.empty_cache()
+        confs = {}
+        for name, fn in (("c1_T2048_fwd", config1), ("c3_T64_eval", config3),
+                         ("c4_T16384_skew_fwd_bwd", config4), ("c5_prefill", config5)):
+            print(f"[bench] {name}", file=sys.stderr, flush=True)
+            confs[name] = fn(a.steps, a.warmup)
+            torch.cuda.empty_cache()
+        rec["configs"] = confs
     if not a.no_cpu_baseline:
-        rec["cpu_baseline"] = cpu_baseline(a.cpu_seconds)
+        print("[bench] CPU baseline", file=sys.stderr, flush=True)
+        rec["cpu_baseline"] = cpu_baseline(a.cpu_seconds, not a.no_configs)
     print(json.dumps(rec), flush=True)
 
 

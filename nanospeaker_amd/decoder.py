@@ -1,0 +1,223 @@
+"""
+The decoder around the MoE block, for the 20-layer prefill workload (reference:
+src/model/nanospeaker.py:133-269 -- embedding, 20 pre-norm blocks of attention and MoE,
+final norm, tied unembedding; src/model/mha.py:245-287 for the attention, ln.py:30-36
+for RMSNorm, rope.py for the rotary embedding).
+
+Only the MoE block is this build's HIP code.  The rest is plain PyTorch: RMSNorm is
+`F.rms_norm`, the attention is `scaled_dot_product_attention` (the reference's SDPA path,
+`flex=False`), the projections are torch matmuls.  The stack runs the prefill of the
+benchmark's fifth workload (batch 4 x 8192 tokens, eval, bf16) with the MoE kernels in
+situ, so the block's share of a real forward can be measured.
+
+Attention follows the reference's semantics: grouped-query heads (9 query, 3 key/value,
+d_head 64), a per-head RMSNorm of Q and K before the rotation, rotary embeddings with the
+"rotate half" pairing over the whole head (base 500000 for this workload), causal
+masking, and a sliding window of 512 keys (the query's own position counted) on every
+layer but each `global_every`-th.  A windowed layer is computed in blocks of `window`
+queries, each against the `2 window` keys that can reach it, with SDPA and the band
+mask of that block -- the same result as one SDPA call under the full [T, T] band mask,
+at 2 window / T of its work.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from .moe import MoEBlock
+
+
+@dataclass
+class DecoderConfig:
+    """nanoSpeaker's decoder (nanospeaker.py:71-100) with the prefill workload's settings."""
+
+    vocab_size: int = 32768
+    d_model: int = 576
+    n_layers: int = 20
+    n_heads: int = 9
+    n_kv_heads: int = 3
+    d_head: int = 64
+    n_experts: int = 76
+    n_shared: int = 2
+    top_k: int = 6
+    d_expert: int = 128
+    aux_loss_coef: float = 1e-2
+    rope_base: float = 500_000.0
+    window: "int | None" = 512
+    global_every: "int | None" = 4
+    std: float = 0.02
+    norm_eps: float = 1e-6
+
+    def layer_window(self, i: int) -> "int | None":
+        """None (full causal attention) on every global_every-th layer, else the window."""
+        if self.global_every and i % self.global_every == 0:
+            return None
+        return self.window
+
+
+class RMSNorm(nn.Module):
+    """x / rms(x) * gamma over the last dim, computed by F.rms_norm (ln.py:30-36)."""
+
+    def __init__(self, d: int, eps: float = 1e-6):
+        super().__init__()
+        self.d, self.eps = d, eps
+        self.gamma = nn.Parameter(torch.ones(d))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return F.rms_norm(x, (self.d,), self.gamma, self.eps)
+
+
+class Rotary:
+    """Rotary position tables: plane j of a head turns by pos * base^(-2j / d_head); dim i
+    pairs with dim i + d_head / 2.  The angles are formed in fp32 and the cos / sin
+    tables cast once per compute dtype."""
+
+    def __init__(self, d_head: int, base: float):
+        self.d_head, self.base = d_head, base
+        self._tables: dict = {}
+
+    def tables(self, n: int, device, dtype):
+        key = (n, str(device), dtype)
+        hit = self._tables.get(key)
+        if hit is None:
+            half = self.d_head // 2
+            inv = self.base ** (-torch.arange(half, dtype=torch.float32, device=device) * 2.0
+                                / self.d_head)
+            ang = torch.arange(n, dtype=torch.float32, device=device)[:, None] * inv[None, :]
+            hit = self._tables[key] = (ang.cos().to(dtype), ang.sin().to(dtype))
+        return hit
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        cos, sin = self.tables(x.shape[-2], x.device, x.dtype)
+        half = self.d_head // 2
+        a, b = x[..., :half], x[..., half:]
+        return torch.cat((a * cos - b * sin, b * cos + a * sin), dim=-1)
+
+
+def band_attention(q, k, v, window: int) -> torch.Tensor:
+    """
+    Causal sliding-window attention (each query sees itself and the window - 1 keys before
+    it) for q [B, Hq, T, dh] and k, v [B, Hkv, T, dh], Hq a multiple of Hkv.  Queries are
+    taken in blocks of `window`; block b attends to keys [(b - 1) window, (b + 1) window)
+    under its band mask, one batched SDPA call for all blocks.
+    """
+    B, Hq, T, dh = q.shape
+    Hkv = k.shape[1]
+    w = window
+    nb = -(-T // w)
+    pad = nb * w - T
+    if pad:
+        q = F.pad(q, (0, 0, 0, pad))
+        k = F.pad(k, (0, 0, 0, pad))
+        v = F.pad(v, (0, 0, 0, pad))
+    # keys of block b: the previous block (zeros before the first) and block b itself
+    kb = k.view(B, Hkv, nb, w, dh)
+    vb = v.view(B, Hkv, nb, w, dh)
+    k2 = torch.cat((F.pad(kb, (0, 0, 0, 0, 1, 0))[:, :, :nb], kb), dim=3)
+    v2 = torch.cat((F.pad(vb, (0, 0, 0, 0, 1, 0))[:, :, :nb], vb), dim=3)
+    qb = q.view(B, Hq, nb, w, dh).transpose(1, 2).reshape(B * nb, Hq, w, dh)
+    k2 = k2.transpose(1, 2).reshape(B * nb, Hkv, 2 * w, dh)
+    v2 = v2.transpose(1, 2).reshape(B * nb, Hkv, 2 * w, dh)
+    # query i of a block sits at key position w + i; key j is allowed when
+    # 0 <= (w + i) - j < w, and the first block's previous-block keys do not exist
+    qi = torch.arange(w, device=q.device)[:, None] + w
+    kj = torch.arange(2 * w, device=q.device)[None, :]
+    band = (kj <= qi) & (qi - kj < w)
+    first = band & (kj >= w)
+    mask = band.expand(B, nb, w, 2 * w).clone()
+    mask[:, 0] = first
+    mask = mask.reshape(B * nb, 1, w, 2 * w)
+    out = F.scaled_dot_product_attention(qb, k2, v2, attn_mask=mask,
+                                         enable_gqa=Hq != Hkv)
+    out = out.view(B, nb, Hq, w, dh).transpose(1, 2).reshape(B, Hq, nb * w, dh)
+    return out[:, :, :T]
+
+
+class Attention(nn.Module):
+    """Grouped-query self-attention with QK-norm, rotary embeddings and an optional window
+    (reference: OptimizedMultiHeadAttention, mha.py:245-287, on its SDPA path)."""
+
+    def __init__(self, cfg: DecoderConfig, rotary: Rotary, window: "int | None"):
+        super().__init__()
+        d, h, hk, dh = cfg.d_model, cfg.n_heads, cfg.n_kv_heads, cfg.d_head
+        self.h, self.hk, self.dh, self.window, self.rotary = h, hk, dh, window, rotary
+        self.W_q = nn.Parameter(torch.randn(d, h * dh) * cfg.std)
+        self.W_k = nn.Parameter(torch.randn(d, hk * dh) * cfg.std)
+        self.W_v = nn.Parameter(torch.randn(d, hk * dh) * cfg.std)
+        # output projection damped by 1 / sqrt(2 n_layers), as the reference does
+        self.W_O = nn.Parameter(torch.randn(h * dh, d) * cfg.std / math.sqrt(2 * cfg.n_layers))
+        self.q_norm = RMSNorm(dh, cfg.norm_eps)
+        self.k_norm = RMSNorm(dh, cfg.norm_eps)
+
+    def forward(self, z: torch.Tensor) -> torch.Tensor:
+        B, T, _ = z.shape
+        q = (z @ self.W_q).view(B, T, self.h, self.dh).transpose(1, 2)
+        k = (z @ self.W_k).view(B, T, self.hk, self.dh).transpose(1, 2)
+        v = (z @ self.W_v).view(B, T, self.hk, self.dh).transpose(1, 2)
+        q = self.rotary(self.q_norm(q))
+        k = self.rotary(self.k_norm(k))
+        if self.window is None or self.window >= T:
+            o = F.scaled_dot_product_attention(q, k, v, is_causal=True,
+                                               enable_gqa=self.h != self.hk)
+        else:
+            o = band_attention(q, k, v, self.window)
+        return o.transpose(1, 2).reshape(B, T, self.h * self.dh) @ self.W_O
+
+
+class DecoderBlock(nn.Module):
+    """Pre-norm block (nanospeaker.py:138-169): x + attn(norm(x)), then x + moe(norm(x)).
+    Returns the new residual stream and the MoE block's balance loss."""
+
+    def __init__(self, cfg: DecoderConfig, rotary: Rotary, layer: int, kernel: bool = True):
+        super().__init__()
+        self.norm_attn = RMSNorm(cfg.d_model, cfg.norm_eps)
+        self.attn = Attention(cfg, rotary, cfg.layer_window(layer))
+        self.norm_ffn = RMSNorm(cfg.d_model, cfg.norm_eps)
+        self.ffn = MoEBlock(cfg.d_model, cfg.n_experts, 3 * cfg.d_expert // 2,
+                            top_k=cfg.top_k, n_shared=cfg.n_shared, capacity_factor=None,
+                            normalize_weights=True, aux_loss_coef=cfg.aux_loss_coef,
+                            std=cfg.std, fused=False, kernel=kernel)
+
+    def forward(self, x: torch.Tensor):
+        x = x + self.attn(self.norm_attn(x))
+        return x + self.ffn(self.norm_ffn(x)), self.ffn.aux_loss
+
+
+class Decoder(nn.Module):
+    """Embedding, the blocks, the final norm and the tied unembedding
+    (nanospeaker.py:172-245); `forward(idx)` returns the logits [B, T, vocab]."""
+
+    def __init__(self, cfg: DecoderConfig = DecoderConfig(), kernel: bool = True):
+        super().__init__()
+        self.cfg = cfg
+        self.embed = nn.Embedding(cfg.vocab_size, cfg.d_model)
+        nn.init.normal_(self.embed.weight, std=cfg.std)
+        rotary = Rotary(cfg.d_head, cfg.rope_base)
+        self.blocks = nn.ModuleList(DecoderBlock(cfg, rotary, i, kernel)
+                                    for i in range(cfg.n_layers))
+        self.norm_out = RMSNorm(cfg.d_model, cfg.norm_eps)
+
+    def trunk(self, idx: torch.Tensor, ffn_hook=None):
+        """(final normed hidden states, summed balance loss).  ffn_hook, when given, is
+        called as ffn_hook(block, x) in place of each block's MoE call and must return
+        what it returns (the benchmark times the MoE calls through it)."""
+        x = self.embed(idx)
+        aux = torch.zeros((), dtype=torch.float32, device=x.device)
+        for blk in self.blocks:
+            if ffn_hook is None:
+                x, a = blk(x)
+            else:
+                x = x + blk.attn(blk.norm_attn(x))
+                x = x + ffn_hook(blk, blk.norm_ffn(x))
+                a = blk.ffn.aux_loss
+            aux = aux + a
+        return self.norm_out(x), aux
+
+    def forward(self, idx: torch.Tensor, ffn_hook=None) -> torch.Tensor:
+        x, _ = self.trunk(idx, ffn_hook)
+        return x @ self.embed.weight.t()

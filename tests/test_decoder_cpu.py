@@ -1,0 +1,78 @@
+"""
+The decoder harness around the MoE block (nanospeaker_amd/decoder.py) on the CPU: the
+blocked sliding-window attention equals one SDPA call under the full band mask, the
+rotary embedding is a rotation whose attention logits depend only on the offset, the
+window / global layer pattern is the reference's (nanospeaker.py:102-114), and a small
+decoder runs end to end on the block's eager path.
+"""
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from nanospeaker_amd.decoder import (Decoder, DecoderConfig, Rotary, band_attention)
+
+
+@pytest.mark.parametrize("T,w,hq,hk", [(64, 16, 4, 2), (50, 16, 3, 3), (17, 8, 6, 2),
+                                       (8, 16, 2, 1)])
+def test_band_attention_equals_full_band_mask(T, w, hq, hk):
+    g = torch.Generator().manual_seed(T + w)
+    q = torch.randn(2, hq, T, 8, generator=g, dtype=torch.float64)
+    k = torch.randn(2, hk, T, 8, generator=g, dtype=torch.float64)
+    v = torch.randn(2, hk, T, 8, generator=g, dtype=torch.float64)
+    pos = torch.arange(T)
+    allowed = (pos[None, :] <= pos[:, None]) & (pos[:, None] - pos[None, :] < w)
+    ref = F.scaled_dot_product_attention(q, k, v, attn_mask=allowed, enable_gqa=hq != hk)
+    got = band_attention(q, k, v, w) if w < T else None
+    if got is not None:
+        torch.testing.assert_close(got, ref, rtol=1e-12, atol=1e-12)
+
+
+def test_rotary_is_a_rotation_with_relative_logits():
+    rot = Rotary(16, 500_000.0)
+    g = torch.Generator().manual_seed(1)
+    q = torch.randn(1, 1, 40, 16, generator=g, dtype=torch.float64)
+    k = torch.randn(1, 1, 40, 16, generator=g, dtype=torch.float64)
+    # the same vector at every position: q_m . k_n must depend on m - n only (the angles
+    # are formed in fp32, as the reference forms them: agreement to fp32 rounding)
+    qs, ks = q[:, :, :1].expand(-1, -1, 40, -1), k[:, :, :1].expand(-1, -1, 40, -1)
+    s = rot(qs)[0, 0] @ rot(ks)[0, 0].t()
+    for off in (0, 3, 17):
+        d = torch.diagonal(s, -off)
+        torch.testing.assert_close(d, d[:1].expand_as(d), rtol=1e-6, atol=1e-6)
+    # norms preserved (a rotation), and position 0 unchanged
+    torch.testing.assert_close(rot(q).norm(dim=-1), q.norm(dim=-1), rtol=1e-6, atol=1e-6)
+    torch.testing.assert_close(rot(q)[..., 0, :], q[..., 0, :])
+    # against complex multiplication: plane j = (x_j, x_{j+8}) turned by m * base^(-j/8)
+    m, j = 5, 3
+    theta = m * 500_000.0 ** (-2 * j / 16)
+    z = complex(q[0, 0, m, j], q[0, 0, m, j + 8]) * complex(torch.cos(torch.tensor(theta)),
+                                                          torch.sin(torch.tensor(theta)))
+    r = rot(q)[0, 0, m]
+    assert abs(float(r[j]) - z.real) < 1e-6 and abs(float(r[j + 8]) - z.imag) < 1e-6
+
+
+def test_layer_windows_follow_global_every():
+    cfg = DecoderConfig()
+    wins = [cfg.layer_window(i) for i in range(cfg.n_layers)]
+    assert wins.count(None) == 5 and all(wins[i] is None for i in range(0, 20, 4))
+    assert all(w == 512 for i, w in enumerate(wins) if i % 4)
+
+
+def test_small_decoder_runs_on_the_eager_block_path():
+    torch.manual_seed(0)
+    cfg = DecoderConfig(vocab_size=64, d_model=32, n_layers=4, n_heads=4, n_kv_heads=2,
+                        d_head=8, n_experts=8, n_shared=1, top_k=2, d_expert=16, window=8,
+                        global_every=2)
+    m = Decoder(cfg).eval()
+    idx = torch.randint(0, 64, (2, 20))
+    with torch.no_grad():
+        logits = m(idx)
+    assert logits.shape == (2, 20, 64) and torch.isfinite(logits).all()
+    # causality: changing a later token leaves earlier logits unchanged
+    idx2 = idx.clone()
+    idx2[:, 15] = (idx2[:, 15] + 1) % 64
+    with torch.no_grad():
+        logits2 = m(idx2)
+    torch.testing.assert_close(logits2[:, :15], logits[:, :15], rtol=0, atol=0)
+    assert not torch.equal(logits2[:, 15:], logits[:, 15:])
