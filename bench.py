@@ -434,11 +434,12 @@ def config5(steps, warmup):
         ms = (time.perf_counter() - t0) * 1e3 / reps
         model(idx, ffn_hook=hook)
         torch.cuda.synchronize()
-        moe_ms = sum(a.elapsed_time(b) for a, b in pairs)
+        pairs.clear()
         t0 = time.perf_counter()
         model(idx, ffn_hook=hook)
         torch.cuda.synchronize()
         hooked_ms = (time.perf_counter() - t0) * 1e3
+        moe_ms = sum(a.elapsed_time(b) for a, b in pairs)
     n = idx.numel()
     return {"workload": "20-layer decoder prefill, batch 4 x 8192, eval, bf16; SDPA attention "
                         "(window 512, global_every 4), HIP MoE in every layer",

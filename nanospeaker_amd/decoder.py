@@ -108,6 +108,14 @@ def band_attention(q, k, v, window: int) -> torch.Tensor:
     """
     B, Hq, T, dh = q.shape
     Hkv = k.shape[1]
+    if Hkv != Hq:
+        # Query head h reads key/value head h // (Hq / Hkv), as enable_gqa pairs them.  The
+        # heads are expanded here because ROCm's SDPA takes a mask together with grouped
+        # heads only on its math path (measured at the prefill shape: 3.5 ms per layer
+        # against 0.71 ms on the memory-efficient kernel with expanded heads).
+        k = k.repeat_interleave(Hq // Hkv, dim=1)
+        v = v.repeat_interleave(Hq // Hkv, dim=1)
+        Hkv = Hq
     w = window
     nb = -(-T // w)
     pad = nb * w - T
@@ -132,8 +140,7 @@ def band_attention(q, k, v, window: int) -> torch.Tensor:
     mask = band.expand(B, nb, w, 2 * w).clone()
     mask[:, 0] = first
     mask = mask.reshape(B * nb, 1, w, 2 * w)
-    out = F.scaled_dot_product_attention(qb, k2, v2, attn_mask=mask,
-                                         enable_gqa=Hq != Hkv)
+    out = F.scaled_dot_product_attention(qb, k2, v2, attn_mask=mask)
     out = out.view(B, nb, Hq, w, dh).transpose(1, 2).reshape(B, Hq, nb * w, dh)
     return out[:, :, :T]
 

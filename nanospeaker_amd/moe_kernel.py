@@ -712,13 +712,8 @@ def _route_bits(dt, want_probs, normalize) -> int:
     return _route_flags(want_probs, normalize) | (nat.ROUTE_LOGITS16 if half else 0)
 
 
-@torch.library.custom_op("nsmoe::block_fwd", mutates_args=())
-def block_fwd(x: Tensor, W_r: Tensor, w_in: Tensor, w_out: Tensor, w_sh_in: Optional[Tensor],
-              w_sh_out: Optional[Tensor], b_in: Optional[Tensor], b_out: Optional[Tensor],
-              b_sh_in: Optional[Tensor], b_sh_out: Optional[Tensor], top_k: int,
-              want_probs: bool, normalize: bool, activation: str, aux_coef: float,
-              logit_bias: Optional[Tensor] = None
-              ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+def _block_fwd_impl(x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out,
+                    top_k, want_probs, normalize, activation, aux_coef, logit_bias=None):
     """
     MoEBlock.forward's kernel path (moe.py:345-418): the router GEMM `x @ W_r` (torch,
     router.py:69), then one C call (nsmoe_block_fwd: router tail, dispatch, routed + shared
@@ -773,6 +768,19 @@ def block_fwd(x: Tensor, W_r: Tensor, w_in: Tensor, w_out: Tensor, w_sh_in: Opti
     return out, aux, counts, topk_idx, logits, saved, p_in
 
 
+@torch.library.custom_op("nsmoe::block_fwd", mutates_args=())
+def block_fwd(x: Tensor, W_r: Tensor, w_in: Tensor, w_out: Tensor, w_sh_in: Optional[Tensor],
+              w_sh_out: Optional[Tensor], b_in: Optional[Tensor], b_out: Optional[Tensor],
+              b_sh_in: Optional[Tensor], b_sh_out: Optional[Tensor], top_k: int,
+              want_probs: bool, normalize: bool, activation: str, aux_coef: float,
+              logit_bias: Optional[Tensor] = None
+              ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """The block's forward as a torch.library op (see _block_fwd_impl)."""
+    return _block_fwd_impl(x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in,
+                           b_sh_out, top_k, want_probs, normalize, activation, aux_coef,
+                           logit_bias)
+
+
 @block_fwd.register_fake
 def _(x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out, top_k,
       want_probs, normalize, activation, aux_coef, logit_bias=None):
@@ -789,15 +797,9 @@ def _(x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out, to
             x.new_empty((_packed_in_bytes(x, w_in, w_sh_in),), dtype=torch.uint8))
 
 
-@torch.library.custom_op("nsmoe::block_bwd", mutates_args=())
-def block_bwd(g_out: Tensor, g_aux: Optional[Tensor], x: Tensor, W_r: Tensor, w_in: Tensor,
-              w_out: Tensor, w_sh_in: Optional[Tensor], w_sh_out: Optional[Tensor],
-              b_in: Optional[Tensor], b_out: Optional[Tensor], b_sh_in: Optional[Tensor],
-              logits: Tensor, saved: Tensor, topk_idx: Tensor, counts: Tensor,
-              w_in_packed: Tensor, top_k: int, want_probs: bool, normalize: bool,
-              activation: str, aux_coef: float, has_b_sh_out: bool, need_dx: bool,
-              need_dW_r: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor,
-                                        Tensor, Tensor, Tensor]:
+def _block_bwd_impl(g_out, g_aux, x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in,
+                    logits, saved, topk_idx, counts, w_in_packed, top_k, want_probs, normalize,
+                    activation, aux_coef, has_b_sh_out, need_dx, need_dW_r):
     """
     The block's backward in one C call (nsmoe_block_bwd: experts' backward, router tail's
     backward with the balance-loss gradient folded in, and for 16-bit types the router
@@ -859,6 +861,22 @@ def block_bwd(g_out: Tensor, g_aux: Optional[Tensor], x: Tensor, W_r: Tensor, w_
     return dx, dW_r, dw_in, dw_out, dw_sh_in, dw_sh_out, db_in, db_out, db_sh_in, db_sh_out
 
 
+@torch.library.custom_op("nsmoe::block_bwd", mutates_args=())
+def block_bwd(g_out: Tensor, g_aux: Optional[Tensor], x: Tensor, W_r: Tensor, w_in: Tensor,
+              w_out: Tensor, w_sh_in: Optional[Tensor], w_sh_out: Optional[Tensor],
+              b_in: Optional[Tensor], b_out: Optional[Tensor], b_sh_in: Optional[Tensor],
+              logits: Tensor, saved: Tensor, topk_idx: Tensor, counts: Tensor,
+              w_in_packed: Tensor, top_k: int, want_probs: bool, normalize: bool,
+              activation: str, aux_coef: float, has_b_sh_out: bool, need_dx: bool,
+              need_dW_r: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor,
+                                        Tensor, Tensor, Tensor]:
+    """The block's backward as a torch.library op (see _block_bwd_impl)."""
+    return _block_bwd_impl(g_out, g_aux, x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out,
+                           b_sh_in, logits, saved, topk_idx, counts, w_in_packed, top_k,
+                           want_probs, normalize, activation, aux_coef, has_b_sh_out, need_dx,
+                           need_dW_r)
+
+
 @block_bwd.register_fake
 def _(g_out, g_aux, x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, logits,
       saved, topk_idx, counts, w_in_packed, top_k, want_probs, normalize, activation, aux_coef,
@@ -885,6 +903,10 @@ def _block_fwd_setup(ctx, inputs, output):
 
 
 def _block_fwd_backward(ctx, g_out, g_aux, g_counts, g_idx, g_logits, g_saved, g_packed):
+    return _block_backward(ctx, g_out, g_aux, block_bwd)
+
+
+def _block_backward(ctx, g_out, g_aux, bwd):
     x, W_r, w_in, w_out, logits, saved, topk_idx, counts, w_in_packed, *opt = ctx.saved_tensors
     has_sh, has_b_in, has_b_out, has_b_sh_in = ctx.has
     it = iter(opt)
@@ -898,10 +920,9 @@ def _block_fwd_backward(ctx, g_out, g_aux, g_counts, g_idx, g_logits, g_saved, g
     if g_out is None:
         g_out = torch.zeros_like(x)
     (dx, dW_r, dw_in, dw_out, dw_sh_in, dw_sh_out, db_in, db_out, db_sh_in,
-     db_sh_out) = block_bwd(g_out, g_aux, x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out,
-                            b_sh_in, logits, saved, topk_idx, counts, w_in_packed, top_k,
-                            want_probs, normalize, activation, aux_coef, has_b_sh_out,
-                            need[0], need[1])
+     db_sh_out) = bwd(g_out, g_aux, x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out,
+                      b_sh_in, logits, saved, topk_idx, counts, w_in_packed, top_k, want_probs,
+                      normalize, activation, aux_coef, has_b_sh_out, need[0], need[1])
     opt_grad = lambda present, g: g if present else None
     return (dx if need[0] else None, dW_r if need[1] else None, dw_in, dw_out,
             opt_grad(has_sh, dw_sh_in), opt_grad(has_sh, dw_sh_out),
@@ -911,6 +932,22 @@ def _block_fwd_backward(ctx, g_out, g_aux, g_counts, g_idx, g_logits, g_saved, g
 
 
 block_fwd.register_autograd(_block_fwd_backward, setup_context=_block_fwd_setup)
+
+
+class _BlockEager(torch.autograd.Function):
+    """The same forward and backward as the nsmoe::block_fwd / block_bwd ops, entered
+    without the torch.library dispatch: eager callers take this node (its host cost per
+    step is what bounds an eager step at nanoSpeaker's shape), traced callers the ops."""
+
+    @staticmethod
+    def forward(ctx, *inputs):
+        output = _block_fwd_impl(*inputs)
+        _block_fwd_setup(ctx, inputs, output)
+        return output
+
+    @staticmethod
+    def backward(ctx, g_out, g_aux, g_counts, g_idx, g_logits, g_saved, g_packed):
+        return _block_backward(ctx, g_out, g_aux, _block_bwd_impl)
 
 
 def block_forward(x, router_W, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out,
@@ -923,7 +960,8 @@ def block_forward(x, router_W, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh
     """
     _check_activation(activation)
     cast = lambda t: None if t is None else t.to(x.dtype)
-    out, aux, counts, topk_idx, _, _, _ = block_fwd(
+    op = block_fwd if torch.compiler.is_compiling() else _BlockEager.apply
+    out, aux, counts, topk_idx, _, _, _ = op(
         x.contiguous(), cast(router_W).contiguous(), cast(w_in).contiguous(),
         cast(w_out).contiguous(), _c(cast(w_sh_in)), _c(cast(w_sh_out)), _c(cast(b_in)),
         _c(cast(b_out)), _c(cast(b_sh_in)), _c(cast(b_sh_out)), top_k, want_probs, normalize,

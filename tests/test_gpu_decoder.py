@@ -50,4 +50,6 @@ def test_one_layer_with_hip_moe_matches_the_eager_block(window):
     assert model.blocks[0].ffn._use_kernel(hk.reshape(-1, 576))
     assert torch.equal(model.blocks[0].ffn.expert_counts.long(),
                        twin.blocks[0].ffn.expert_counts.long())
-    assert_close_bf16("hidden states", hk.float().cpu(), he.float().cpu())
+    # both sides are bf16 computations, each within the bf16 bar (rel-L2 5e-3) of an fp32
+    # one, so they are held to twice that against each other
+    assert_close_bf16("hidden states", hk.float().cpu(), he.float().cpu(), rel_l2=1e-2)
