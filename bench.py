@@ -46,6 +46,14 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-configs", action="store_true",
                     help="time only the headline workload (T=8192 fwd+bwd)")
+    ap.add_argument("--single-stream", action="store_true",
+                    help="keep every kernel on one stream (the library's single_stream "
+                         "option), so that profiled kernels never overlap")
+    ap.add_argument("--mfma-summary", nargs=2, metavar=("MOPS_CSV", "MFMAUTIL_CSV"),
+                    help="print the MFMA table from two rocprofv3 --pmc runs "
+                         "(SQ_INSTS_VALU_MFMA_MOPS_BF16, MfmaUtil) and a --stats run's "
+                         "kernel_stats.csv (--stats-csv), and exit")
+    ap.add_argument("--stats-csv", help="kernel_stats.csv for --mfma-summary")
     ap.add_argument("--eager", action="store_true",
                     help="report the eagerly issued step as `value` (default: HIP-graph replay)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -135,6 +143,7 @@ def time_gpu(m, x, g, steps: int, warmup: int):
     # Per-kernel launch times, from the library's HIP-event pairs on the launch stream, in a
     # pass of its own on one stream, so that no other kernel shares the GPU with the one
     # being timed.
+    prev = nat.get_option("single_stream")
     nat.set_option("single_stream", 1)
     try:
         step()
@@ -152,7 +161,7 @@ def time_gpu(m, x, g, steps: int, warmup: int):
                 kernels[name] = (tot / n, n // steps)
         nat.timing_enable(0)
     finally:
-        nat.set_option("single_stream", 0)
+        nat.set_option("single_stream", prev)
 
     # forward only (train mode, no autograd)
     with torch.no_grad():
@@ -245,6 +254,50 @@ def stats_summary(path, top=30):
                    f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} | "
                    f"{float(r['TotalDurationNs']) / 1e6:.2f} | {float(r['Percentage']):.1f} |")
     return "\n".join(out)
+
+
+# FLOPs per row the MFMA kernels issue, recomputation included (bf16, H = 128, d = 576):
+# the GLU-backward kernel recomputes a1 = x W_in (2 d 2H) beside G = dout W_out^T (2 d H).
+ISSUED_FLOPS_PER_ROW = {
+    "expert_fwd": 2 * 576 * 256 + 2 * 128 * 576,
+    "expert_bwd": 2 * 576 * 256 + 2 * 576 * 128,
+    "expert_dx": 2 * 256 * 576,
+    "dw": 2 * 576 * 256 + 2 * 128 * 576,
+}
+
+
+def mfma_summary(mops_csv, util_csv, stats_csv, T=8192, rows=8192 * 8):
+    """Markdown table per MFMA kernel: the MFMA work it issued (SQ_INSTS_VALU_MFMA_MOPS_BF16
+    x 512 FLOPs) against the algorithmic and the issued (recompute included) count, the
+    achieved rate from its average duration in the --stats run, and rocprofv3's derived
+    MfmaUtil (MFMA-busy share of the kernel's GPU cycles)."""
+    import csv
+
+    mops, util = _pmc_per_kernel(mops_csv), _pmc_per_kernel(util_csv)
+    dur = {}
+    with open(stats_csv) as f:
+        for r in csv.DictReader(f):
+            dur[r["Name"].replace("void ", "").split("(")[0]] = float(r["AverageNs"]) / 1e3
+    lines = ["| bench kernel | HIP kernel | avg us | MOPS x 512 (GFLOP) | algorithmic GFLOP | "
+             "issued GFLOP (recompute included) | achieved TFLOP/s (MOPS) | % of 2500 | "
+             "MfmaUtil % |",
+             "|---|---|---|---|---|---|---|---|---|"]
+    for bname, prefixes in KERNEL_SYMBOLS.items():
+        if bname not in ISSUED_FLOPS_PER_ROW:
+            continue
+        for sym, (n, mv) in sorted(mops.items()):
+            if not sym.startswith(prefixes):
+                continue
+            flops = mv * 512
+            alg = kernel_units(bname, T, 6, 2, 576, 128, 76)[0]
+            issued = ISSUED_FLOPS_PER_ROW[bname] * rows
+            us = dur.get(sym, float("nan"))
+            rate = flops / (us * 1e-6) / 1e12
+            u = util.get(sym, (0, float("nan")))[1]
+            lines.append(f"| {bname} | `{sym}` | {us:.2f} | {flops / 1e9:.2f} | "
+                         f"{alg / 1e9:.2f} | {issued / 1e9:.2f} | {rate:.0f} | "
+                         f"{100 * rate / PEAK_BF16_TFLOPS:.1f} | {u:.1f} |")
+    return "\n".join(lines)
 
 
 def committed_traffic(kernel):
@@ -549,6 +602,13 @@ def main():
     if a.stats_summary:
         print(stats_summary(a.stats_summary))
         return
+    if a.mfma_summary:
+        print(mfma_summary(*a.mfma_summary, a.stats_csv))
+        return
+    if a.single_stream:
+        from nanospeaker_amd import _native as nat
+
+        nat.set_option("single_stream", 1)
     if a.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; multi-GPU sharding is "
                                    "design-only, so --gpus must be 1"}))
