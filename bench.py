@@ -377,7 +377,7 @@ def train_step_fn(m, x, g, logit_bias=None):
         if logit_bias is None:
             out, aux = m(xg), m.aux_loss
         else:  # the skewed workload: the router offset enters through the op's hook
-            out, aux, _, _ = mk.block_forward(
+            out, aux, _, _, _ = mk.block_forward(
                 xg, m.router.W, m.W_in, m.W_out, m.W_sh_in, m.W_sh_out, None, None, None,
                 None, 6, True, True, "silu", 1e-2, logit_bias=logit_bias)
         return torch.autograd.grad([out, aux], [xg] + params, [g, one])
@@ -441,7 +441,7 @@ def config4(steps, warmup):
     from nanospeaker_amd import moe_kernel as mk
 
     with torch.no_grad():
-        _, _, counts, _ = mk.block_forward(
+        _, _, counts, _, _ = mk.block_forward(
             x, m.router.W, m.W_in, m.W_out, m.W_sh_in, m.W_sh_out, None, None, None, None, 6,
             True, True, "silu", 1e-2, logit_bias=bias)
     share = float(counts.max()) / float(counts.sum())

@@ -243,13 +243,20 @@ int nsmoe_experts_bwd(const nsmoe_experts_args* args, const int32_t* inv,
                       void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- the whole block, one call per direction ------------------------------------------
- * MoEBlock.forward's kernel branch (src/model/moe.py:345-418: router tail router.py:79-98,
+ * MoEBlock.forward's kernel branch (src/model/moe.py:345-418: the router, router.py:56-98,
  * fused_moe_forward moe_kernel.py:785-803 with the shared experts moe.py:310-329, balance
- * loss router.py:100-111) and its backward, as a sequence of the entry points above over
- * caller buffers.  The router GEMM's forward (router.py:69) is the caller's: it passes
- * the logits in.  Its backward is either done here (w_router given: dx gets
- * d(logits) W^T, grad_w_router gets x^T d(logits)) or left to the caller (w_router NULL:
- * grad_logits receives d(logits)).
+ * loss router.py:100-111) and its backward, as a sequence of kernels over caller buffers.
+ *
+ * The router GEMM (router.py:69):
+ *   forward, w_router [d, E] non-NULL: computed here, fused with the router tail and the
+ *     dispatch's histogram pass (bf16/fp16, d % 32 == 0, d <= 576, E % 4 == 0,
+ *     E <= 80, top_k <= 16).  `logits` [T, E] (args dtype) receives x W_r with fp32 accumulation,
+ *     plus logit_bias [E] fp32 when given (a harness hook with no counterpart in the
+ *     reference router, which has no bias; NULL in MoEBlock), rounded to the dtype.
+ *   forward, w_router NULL: `logits` holds the caller's GEMM output; logit_bias must be
+ *     NULL.
+ *   backward: either done here (w_router given: dx gets d(logits) W^T, grad_w_router gets
+ *     x^T d(logits)) or left to the caller (w_router NULL: grad_logits receives d(logits)).
  *
  * `args` carries dims, dtype, activation, x, weights, biases and the packed weights
  * (w_in_packed, w_out_packed: nsmoe_pack_weights layout, both required by the forward,
@@ -293,10 +300,10 @@ int nsmoe_experts_bwd(const nsmoe_experts_args* args, const int32_t* inv,
 int nsmoe_block_saved_layout(const nsmoe_experts_args* args, int32_t route_flags,
                              size_t* offsets /* [NSMOE_BLOCK_NSAVED] */, size_t* total_bytes);
 size_t nsmoe_block_fwd_workspace_size(const nsmoe_experts_args* args, int32_t route_flags);
-int nsmoe_block_fwd(const nsmoe_experts_args* args, const void* logits, int32_t route_flags,
-                    float aux_coef, void* saved, int64_t* topk_idx, int32_t* counts,
-                    void* out, float* aux, void* workspace, size_t workspace_bytes,
-                    void* stream);
+int nsmoe_block_fwd(const nsmoe_experts_args* args, const void* w_router,
+                    const float* logit_bias, void* logits, int32_t route_flags, float aux_coef,
+                    void* saved, int64_t* topk_idx, int32_t* counts, void* out, float* aux,
+                    void* workspace, size_t workspace_bytes, void* stream);
 size_t nsmoe_block_bwd_workspace_size(const nsmoe_experts_args* args, int32_t route_flags,
                                       int32_t fuse_router);
 int nsmoe_block_bwd(const nsmoe_experts_args* args, const void* logits, int32_t route_flags,

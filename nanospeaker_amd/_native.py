@@ -74,8 +74,8 @@ SIGNATURES = {
     "nsmoe_block_saved_layout": (ctypes.c_int, [ctypes.POINTER(ExpertsArgs), _i32,
                                                 ctypes.POINTER(_sz), ctypes.POINTER(_sz)]),
     "nsmoe_block_fwd_workspace_size": (_sz, [ctypes.POINTER(ExpertsArgs), _i32]),
-    "nsmoe_block_fwd": (ctypes.c_int, [ctypes.POINTER(ExpertsArgs), _vp, _i32, ctypes.c_float,
-                                       _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "nsmoe_block_fwd": (ctypes.c_int, [ctypes.POINTER(ExpertsArgs), _vp, _vp, _vp, _i32,
+                                       ctypes.c_float, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "nsmoe_block_bwd_workspace_size": (_sz, [ctypes.POINTER(ExpertsArgs), _i32, _i32]),
     "nsmoe_block_bwd": (ctypes.c_int, [ctypes.POINTER(ExpertsArgs), _vp, _i32, ctypes.c_float,
                                        _vp, _vp, _vp, _vp, _vp, ctypes.POINTER(ExpertsGrads),

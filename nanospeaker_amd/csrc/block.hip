@@ -18,6 +18,7 @@
 
 #include "experts_common.h"
 #include "pack.h"
+#include "router_fused.h"
 #include "router_grad.h"
 #include "../../include/nsmoe.h"
 
@@ -67,12 +68,17 @@ static nsmoe_experts_args with_routing(const nsmoe_experts_args* a, const BlockL
   return b;
 }
 
-static size_t fwd_ws_parts(const nsmoe_experts_args* b, size_t* dsp, size_t* exp, size_t* bal) {
+// Forward workspace: the dispatch's histograms (unfused router), the router's partials
+// (the balance loss's column sums, or the fused router's histograms, tie lists and column
+// sums) and the experts' per-row outputs.
+static size_t fwd_ws_parts(const nsmoe_experts_args* b, size_t* dsp, size_t* exp, size_t* rt) {
   const int64_t m = b->n_tokens * b->top_k;
   *dsp = al256(nsmoe_dispatch_workspace_size(m, b->n_experts));
   *exp = al256(nsmoe_experts_fwd_workspace_size(b));
-  *bal = al256(nsmoe_balance_loss_workspace_size(b->n_tokens, b->n_experts));
-  return *dsp + *exp + *bal;
+  const size_t bal = al256(nsmoe_balance_loss_workspace_size(b->n_tokens, b->n_experts));
+  const size_t fused = al256(router_fused_ws_bytes(b->n_tokens, b->n_experts));
+  *rt = bal > fused ? bal : fused;
+  return *dsp + *exp + *rt;
 }
 
 }  // namespace nsmoe
@@ -96,54 +102,88 @@ extern "C" size_t nsmoe_block_fwd_workspace_size(const nsmoe_experts_args* a,
   nsmoe_experts_args b = *a;
   b.l_cap = nsmoe_dispatch_l_cap(a->n_tokens * a->top_k, a->n_experts);
   (void)route_flags;
-  size_t dsp, exp, bal;
-  return fwd_ws_parts(&b, &dsp, &exp, &bal);
+  size_t dsp, exp, rt;
+  return fwd_ws_parts(&b, &dsp, &exp, &rt);
 }
 
-extern "C" int nsmoe_block_fwd(const nsmoe_experts_args* a, const void* logits,
-                               int32_t route_flags, float aux_coef, void* saved,
-                               int64_t* topk_idx, int32_t* counts, void* out, float* aux,
-                               void* workspace, size_t workspace_bytes, void* stream) {
-  NSMOE_REQUIRE(a && saved && out && topk_idx && counts, "block_fwd: NULL pointer");
+extern "C" int nsmoe_block_fwd(const nsmoe_experts_args* a, const void* w_router,
+                               const float* logit_bias, void* logits, int32_t route_flags,
+                               float aux_coef, void* saved, int64_t* topk_idx, int32_t* counts,
+                               void* out, float* aux, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+  NSMOE_REQUIRE(a && saved && out && topk_idx && counts && logits, "block_fwd: NULL pointer");
   NSMOE_REQUIRE(!(route_flags & NSMOE_ROUTE_PROBS) || aux, "block_fwd: NULL aux");
   NSMOE_REQUIRE(a->w_in_packed && a->w_out_packed, "block_fwd: NULL packed weights");
+  NSMOE_REQUIRE(w_router || !logit_bias, "block_fwd: logit_bias needs the fused router");
+  NSMOE_REQUIRE(!w_router || router_fused_supported(a->dtype, (int)a->d_model, a->n_experts,
+                                                    a->top_k),
+                "block_fwd: the fused router takes bf16/fp16, d %% 32 == 0, d <= 576, "
+                "E %% 4 == 0, E <= 80 and top_k <= 16 (d %d, E %d, k %d)", (int)a->d_model,
+                a->n_experts,
+                a->top_k);
   if (a->n_tokens == 0) return NSMOE_OK;
-  NSMOE_REQUIRE(logits, "block_fwd: NULL logits");
   const BlockLayout L = block_layout(a, route_flags);
   char* sv = (char*)saved;
   nsmoe_experts_args b = with_routing(a, L, sv, counts);
-  size_t dsp, exp, bal;
-  const size_t need = fwd_ws_parts(&b, &dsp, &exp, &bal);
+  size_t dsp, exp, rtb;
+  const size_t need = fwd_ws_parts(&b, &dsp, &exp, &rtb);
   if (!workspace || workspace_bytes < need) {
     set_error("block_fwd: workspace %zu B < %zu B", workspace_bytes, need);
     return NSMOE_EWORKSPACE;
   }
   char* ws = (char*)workspace;
+  char* ws_rt = ws + dsp + exp;
   const int32_t E = a->n_experts, k = a->top_k;
   const int64_t T = a->n_tokens, m = T * k;
   float* probs = (route_flags & NSMOE_ROUTE_PROBS) ? (float*)(sv + L.off[NSMOE_SAVED_PROBS])
                                                    : nullptr;
   int32_t* inv = (int32_t*)(sv + L.off[NSMOE_SAVED_INV]);
-  // In training the route kernel also leaves the balance loss's per-workgroup column
-  // sums of probs in the workspace, so probs is not read back for the loss.
-  float* colsum = probs ? (float*)(ws + dsp + exp) : nullptr;
+  int32_t* eids = (int32_t*)(sv + L.off[NSMOE_SAVED_EXPERT_IDS]);
+  int32_t* npp = (int32_t*)(sv + L.off[NSMOE_SAVED_N_POST_PAD]);
   // The weight packing (when asked for) does not depend on the routing: it runs on the
-  // side stream while the latency-bound route and dispatch kernels run on the caller's.
+  // side stream while the latency-bound routing and dispatch kernels run on the caller's.
   hipStream_t s = (hipStream_t)stream;
   const bool pack = route_flags & NSMOE_BLOCK_PACK;
   hipStream_t s_pack = pack ? side_fork(s, kSideSlotPack) : s;
   int rc = pack ? nsmoe_pack_weights(&b, (void*)b.w_in_packed, (void*)b.w_out_packed, s_pack)
                 : NSMOE_OK;
-  if (rc == NSMOE_OK)
-    rc = route_fwd_launch(logits, T, E, k, route_flags, a->dtype, (void*)b.topk_w, topk_idx,
-                          probs, colsum, s);
-  // In training the balance loss is one more workgroup of the dispatch's second launch.
-  BalanceArgs fold{colsum, balance_partial_count(T), T, aux_coef, aux};
-  if (rc == NSMOE_OK)
-    rc = dispatch_launch(topk_idx, m, E, (int32_t*)b.sorted_ids,
-                         (int32_t*)(sv + L.off[NSMOE_SAVED_EXPERT_IDS]), (int32_t*)b.pad_offsets,
-                         counts, (int32_t*)(sv + L.off[NSMOE_SAVED_N_POST_PAD]), inv, ws, dsp,
-                         probs ? &fold : nullptr, s);
+  if (w_router) {
+    // Router GEMM + tail + the dispatch's histograms in the router's two launches; the
+    // dispatch is then its place pass alone, with the balance loss in one more workgroup.
+    RouterArgs r = router_fused_args(ws_rt, T, E);
+    r.x = a->x;
+    r.w = w_router;
+    r.bias = logit_bias;
+    r.T = T;
+    r.d = (int)a->d_model;
+    r.E = E;
+    r.k = k;
+    r.flags = route_flags & (NSMOE_ROUTE_PROBS | NSMOE_ROUTE_NORMALIZE);
+    r.logits = logits;
+    r.probs = probs;
+    r.topk_w = (void*)b.topk_w;
+    r.topk_idx = topk_idx;
+    if (!probs) r.colsum = nullptr;
+    if (rc == NSMOE_OK) rc = router_fused_launch(r, a->dtype, s);
+    BalanceArgs fold{r.colsum, router_fused_chunks(T), T, aux_coef, aux};
+    if (rc == NSMOE_OK)
+      rc = dispatch_place_launch(topk_idx, m, E, r.hist, router_fused_chunks(T), RT_TOK * k,
+                                 (int32_t*)b.sorted_ids, eids, (int32_t*)b.pad_offsets, counts,
+                                 npp, inv, probs ? &fold : nullptr, s);
+  } else {
+    // In training the route kernel also leaves the balance loss's per-workgroup column
+    // sums of probs in the workspace, so probs is not read back for the loss.
+    float* colsum = probs ? (float*)ws_rt : nullptr;
+    if (rc == NSMOE_OK)
+      rc = route_fwd_launch(logits, T, E, k, route_flags, a->dtype, (void*)b.topk_w,
+                            topk_idx, probs, colsum, s);
+    // In training the balance loss is one more workgroup of the dispatch's second launch.
+    BalanceArgs fold{colsum, balance_partial_count(T), T, aux_coef, aux};
+    if (rc == NSMOE_OK)
+      rc = dispatch_launch(topk_idx, m, E, (int32_t*)b.sorted_ids, eids,
+                           (int32_t*)b.pad_offsets, counts, npp, inv, ws, dsp,
+                           probs ? &fold : nullptr, s);
+  }
   const int jrc = side_join(s, s_pack, kSideSlotPack);  // joined on every path
   NSMOE_TRY(rc);
   NSMOE_TRY(jrc);

@@ -64,7 +64,8 @@ dispatch_hist_kernel(const int64_t* __restrict__ topk_idx, int64_t M, int E,
 // issues its loads together; the segment sums are added in LDS.
 __global__ void __launch_bounds__(1024)
 dispatch_place_kernel(const int64_t* __restrict__ topk_idx, int64_t M, int E,
-                      const int32_t* __restrict__ hist, int64_t n_chunks, int64_t l_cap,
+                      const int32_t* __restrict__ hist, int64_t n_chunks, int hist_group,
+                      int chunk_pairs, int64_t l_cap,
                       int32_t* __restrict__ sorted_ids, int32_t* __restrict__ expert_ids,
                       int32_t* __restrict__ offs, int32_t* __restrict__ counts,
                       int32_t* __restrict__ npp, int32_t* __restrict__ inv,
@@ -81,10 +82,13 @@ dispatch_place_kernel(const int64_t* __restrict__ topk_idx, int64_t M, int E,
   const int lane = tid & 63, wave = tid >> 6, waves = nt >> 6;
   const int64_t chunk = blockIdx.x;
 
-  // This workgroup's pairs (the loads go out first) and the rank masks.
-  const int64_t p = chunk * nt + tid;
+  // This workgroup's pairs (the loads go out first) and the rank masks.  A workgroup
+  // places chunk_pairs <= blockDim.x pairs, one per thread from thread 0: hist_group
+  // consecutive rows of hist (n_chunks rows in all) count them.
+  const int64_t p = chunk * chunk_pairs + tid;
+  const bool mine = tid < chunk_pairs && p < M;
   int e_mine = -1;
-  if (p < M) {
+  if (mine) {
     const int64_t v = topk_idx[p];
     if (v >= 0 && v < E) e_mine = (int)v;
   }
@@ -107,7 +111,7 @@ dispatch_place_kernel(const int64_t* __restrict__ topk_idx, int64_t M, int E,
 #pragma unroll
         for (int u = 0; u < UNR; ++u) {
           total += v[u];
-          if (c + u < chunk) before += v[u];
+          if (c + u < chunk * hist_group) before += v[u];
         }
       }
     }
@@ -125,7 +129,8 @@ dispatch_place_kernel(const int64_t* __restrict__ topk_idx, int64_t M, int E,
     }
     __syncthreads();
   }
-  if (chunk == n_chunks) {  // the balance-loss workgroup (uniform): totals -> loss
+  const int64_t G = (n_chunks + hist_group - 1) / hist_group;  // the placing workgroups
+  if (chunk == G) {  // the balance-loss workgroup (uniform): totals -> loss
     balance_loss_block(bal_partial, bal_nblk, s_tot, bal_T, E, bal_coef, bal_aux, s_bal);
     return;
   }
@@ -161,7 +166,7 @@ dispatch_place_kernel(const int64_t* __restrict__ topk_idx, int64_t M, int E,
 
   // Place this chunk's pairs: rank inside the expert = set bits below this lane in the
   // wave's mask plus the same expert's bits in the waves before.
-  if (p < M) {
+  if (mine) {
     if (e_mine < 0) {
       inv[p] = -1;
     } else {
@@ -175,7 +180,6 @@ dispatch_place_kernel(const int64_t* __restrict__ topk_idx, int64_t M, int E,
   }
 
   const int32_t total = s_off[E];
-  const int64_t G = n_chunks;  // the placing workgroups
   if (chunk == 0) {
     for (int e = tid; e <= E; e += nt) offs[e] = s_off[e];
     for (int e = tid; e < E; e += nt) counts[e] = s_tot[e];
@@ -267,9 +271,40 @@ int dispatch_launch(const int64_t* topk_idx, int64_t n_pairs, int32_t n_experts,
   const bool fold = bal != nullptr;
   dispatch_place_kernel<<<(unsigned)(n_chunks + (fold ? 1 : 0)), chunk,
                           (chunk / 64) * n_experts * sizeof(unsigned long long), s>>>(
-      topk_idx, n_pairs, n_experts, hist, n_chunks, l_cap, sorted_ids, expert_ids, pad_offsets,
+      topk_idx, n_pairs, n_experts, hist, n_chunks, 1, chunk, l_cap, sorted_ids, expert_ids, pad_offsets,
       counts, n_post_pad, inv, fold ? bal->partial : nullptr, fold ? bal->nblk : 0,
       fold ? bal->T : 1, fold ? bal->coef : 0.0f, fold ? bal->aux : nullptr);
+  timer.stop();
+  return check_launch("dispatch_place_kernel");
+}
+
+// The place pass alone, from per-chunk histograms made elsewhere (the fused router):
+// chunk c holds pairs [c chunk_pairs, (c + 1) chunk_pairs), hist is [n_chunks, E].  Each
+// workgroup places as many whole chunks as fit 1024 pairs.
+int dispatch_place_launch(const int64_t* topk_idx, int64_t n_pairs, int32_t n_experts,
+                          const int32_t* hist, int64_t n_chunks, int chunk_pairs,
+                          int32_t* sorted_ids, int32_t* expert_ids, int32_t* pad_offsets,
+                          int32_t* counts, int32_t* n_post_pad, int32_t* inv,
+                          const BalanceArgs* bal, hipStream_t s) {
+  NSMOE_REQUIRE(n_pairs > 0 && n_pairs < (int64_t)INT32_MAX / 2,
+                "dispatch_place: n_pairs %lld out of range", (long long)n_pairs);
+  NSMOE_REQUIRE(n_experts >= 1 && n_experts <= 128 && chunk_pairs >= 1 &&
+                    chunk_pairs <= 1024 && n_chunks * chunk_pairs >= n_pairs,
+                "dispatch_place: bad chunking (E %d, %d pairs per chunk)", n_experts,
+                chunk_pairs);
+  NSMOE_REQUIRE(!bal || (bal->partial && bal->aux), "dispatch_place: balance buffers");
+  const int64_t l_cap = nsmoe_dispatch_l_cap(n_pairs, n_experts);
+  const bool fold = bal != nullptr;
+  const int group = 1024 / chunk_pairs;
+  const int64_t n_place = (n_chunks + group - 1) / group;
+  KernelTimer timer("dispatch", s);
+  dispatch_place_kernel<<<(unsigned)(n_place + (fold ? 1 : 0)), 1024,
+                          16 * n_experts * sizeof(unsigned long long), s>>>(
+      topk_idx, n_pairs, n_experts, hist, n_chunks, group, group * chunk_pairs, l_cap,
+      sorted_ids,
+      expert_ids, pad_offsets, counts, n_post_pad, inv, fold ? bal->partial : nullptr,
+      fold ? bal->nblk : 0, fold ? bal->T : 1, fold ? bal->coef : 0.0f,
+      fold ? bal->aux : nullptr);
   timer.stop();
   return check_launch("dispatch_place_kernel");
 }

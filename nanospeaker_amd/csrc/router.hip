@@ -1,0 +1,401 @@
+// The router on device, GEMM included: logits = x W_r, softmax, top-k with CPU torch.topk's
+// tie order, gates, the per-chunk expert histogram the dispatch places from, and the
+// balance loss's column sums -- MoEBlock.forward's routing (src/model/router.py:56-111)
+// for 16-bit blocks, in one launch instead of a library GEMM, the router tail and the
+// dispatch's histogram pass.
+//
+// router_fwd_kernel: one workgroup of 8 waves per 32 tokens (one workgroup per CU at
+// T = 8192).
+//   * GEMM, on 4 of the waves (16 tokens x half the experts each): v_mfma_f32_16x16x32 with
+//     the token rows as the A operand, read straight from global memory, and W_r as the B
+//     operand.  All of x
+//     and all of W_r are requested up front, one memory round trip for both.  W_r [d, E] is
+//     stored with the expert index contiguous, so chunks of its rows are staged
+//     untransposed in LDS and read back with ds_read_b64_tr_b16, which hands each lane 4
+//     consecutive k of one expert column.  The fp32 sums are rounded to the block's dtype
+//     -- the value router.py:69's GEMM produces -- stored as the logits, and kept in LDS.
+//   * Softmax and the selection, on all 8 waves: one token per 16-lane DPP row, a lane
+//     holding E / 16 of its experts.  The selection is k rounds of arg-max; a round whose
+//     maximum is not unique among the values still in play (or a NaN in the row) leaves
+//     the token to the exact pass, since only the restated library algorithm fixes the
+//     order of equal keys.
+//   * The exact pass, on all 8 waves: one undecided token per wave, the restatement of
+//     CPU topk (topk_exact.h) on the keys as the selection saw them.
+//   * Per workgroup it leaves the expert histogram of its tokens (a chunk of 32 k pairs for
+//     the dispatch's place pass) and, in training, the column sums of probs for the
+//     balance loss.
+#include "balance.h"
+#include "gemm_core.h"
+#include "nsmoe_capi_internal.h"
+#include "router_fused.h"
+#include "topk_exact.h"
+
+namespace nsmoe {
+
+constexpr int RT_MMA_SPLIT = 2;             // GEMM waves per 16-token tile (column halves)
+constexpr int RT_MMA_WAVES = RT_TOK / 16 * RT_MMA_SPLIT;  // waves that run the GEMM
+constexpr int RT_WAVES = 8;                 // waves per workgroup (selection, exact pass)
+constexpr int RT_THREADS = RT_WAVES * 64;
+
+// 16-lane DPP butterflies: every lane of each row of 16 ends with the row's reduction.
+template <class Op>
+__device__ __forceinline__ float row16(float v, Op op) {
+  v = op(v, dpp<0xB1>(v));   // quad_perm [1, 0, 3, 2]
+  v = op(v, dpp<0x4E>(v));   // quad_perm [2, 3, 0, 1]
+  v = op(v, dpp<0x141>(v));  // row_half_mirror
+  v = op(v, dpp<0x140>(v));  // row_mirror
+  return v;
+}
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
+}
+
+__device__ __forceinline__ int row16_sum_i(int v) {
+  v += dpp_i<0xB1>(v);
+  v += dpp_i<0x4E>(v);
+  v += dpp_i<0x141>(v);
+  v += dpp_i<0x140>(v);
+  return v;
+}
+
+__device__ __forceinline__ int row16_min_i(int v) {
+  v = min(v, dpp_i<0xB1>(v));
+  v = min(v, dpp_i<0x4E>(v));
+  v = min(v, dpp_i<0x141>(v));
+  v = min(v, dpp_i<0x140>(v));
+  return v;
+}
+
+__device__ __forceinline__ float fmax_(float a, float b) { return fmaxf(a, b); }
+__device__ __forceinline__ float fadd_(float a, float b) { return a + b; }
+
+// k-steps (32 rows of W_r) per staged chunk: the stage and the logit tile share the
+// workgroup's 64 KiB of LDS.
+template <int NB> constexpr int chunk_steps() { return 6; }
+
+template <int DT, int NB>
+__global__ void __launch_bounds__(RT_THREADS) router_fwd_kernel(RouterArgs a) {
+  using ET = typename Elem<DT>::T;
+  constexpr int NC = NB * 16;               // expert columns, padded to whole MFMA blocks
+  constexpr int PITCH = NC * 2 + 16;        // bytes per staged W_r row (16-byte pad)
+  constexpr int CS = chunk_steps<NB>();
+  constexpr int CK = CS * 32;               // W_r rows per staged chunk
+  constexpr int MAXC = (CK * (NC / 4) + RT_THREADS - 1) / RT_THREADS;  // pieces per thread
+  constexpr int MAXCH = (RT_MAX_STEPS + CS - 1) / CS;                    // chunks of W_r
+  constexpr int LGP = NC + 1;               // logit-tile pitch (floats)
+  constexpr int POS = RT_WAVES * 256 * (int)sizeof(int2);
+  constexpr int STAGE = CK * PITCH > POS ? CK * PITCH : POS;
+  // The W_r stage during the GEMM; the exact pass's swap slots afterwards.
+  __shared__ __align__(16) char s_stage[STAGE];
+  __shared__ float s_lg[RT_TOK * LGP];      // per token: the logits, then its keys
+  __shared__ float s_m[RT_TOK], s_inv[RT_TOK];
+  __shared__ int32_t s_hist[128];
+  __shared__ int32_t s_tie[RT_TOK];
+  __shared__ int32_t s_ntie;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, j = lane & 15;
+  const int64_t T = a.T;
+  const int d = a.d, E = a.E, k = a.k;
+  const bool train = a.flags & 1, normalize = a.flags & 2;
+  const int64_t tok0 = (int64_t)blockIdx.x * RT_TOK;
+  const bool mma_wave = wave < RT_MMA_WAVES;  // uniform
+  const int nks = d >> 5;
+
+  // ---- GEMM ------------------------------------------------------------------------------
+  // A GEMM wave's 16 token rows, whole (d <= 32 RT_MAX_STEPS), requested first: one HBM
+  // round trip for all of them.  Lane (g, j) holds row tok + j, elements 32 ks + 8 g .. + 7
+  // (the A operand of k-step ks).
+  constexpr int NBH = (NB + RT_MMA_SPLIT - 1) / RT_MMA_SPLIT;  // column blocks per GEMM wave
+  const int tile = wave / RT_MMA_SPLIT, cb0 = (wave % RT_MMA_SPLIT) * NBH;
+  u32x4 xr[RT_MAX_STEPS];
+  f32x4 acc[NBH];
+  if (mma_wave) {
+    const ET* xp = (const ET*)a.x + min(tok0 + tile * 16 + j, T - 1) * d + 8 * g;
+#pragma unroll
+    for (int ks = 0; ks < RT_MAX_STEPS; ++ks)
+      if (ks < nks) xr[ks] = *(const u32x4*)(xp + ks * 32);
+  }
+#pragma unroll
+  for (int nb = 0; nb < NBH; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // Pad columns [E, NC) of the stage stay zero: the loads never write them.
+  for (int i = tid; i < CK * (PITCH / 4); i += RT_THREADS) {
+    const int c = i % (PITCH / 4);
+    if (c * 4 >= E * 2) *(int32_t*)(s_stage + (i / (PITCH / 4)) * PITCH + c * 4) = 0;
+  }
+  for (int e = tid; e < 128; e += RT_THREADS) s_hist[e] = 0;
+  if (tid == 0) s_ntie = 0;
+  // W_r in chunks of CK rows: a chunk is CK E contiguous elements in global memory, read
+  // as 8-byte pieces (E % 4 == 0); piece f lands at row f / (E / 4), column
+  // 4 (f % (E / 4)) of the stage.
+  const int cpr = E >> 2;
+  const uint2* w8 = (const uint2*)a.w;
+  const int nchunk = (nks + CS - 1) / CS;
+  // Every chunk's pieces are requested now, beside x.
+  uint2 wreg[MAXCH][MAXC];
+#pragma unroll
+  for (int c = 0; c < MAXCH; ++c) {
+    if (c < nchunk) {
+      const int n8 = min(CK, d - c * CK) * cpr;
+      const uint2* src = w8 + (int64_t)c * CK * cpr;
+#pragma unroll
+      for (int u = 0; u < MAXC; ++u)
+        if (tid + u * RT_THREADS < n8) wreg[c][u] = src[tid + u * RT_THREADS];
+    }
+  }
+  // Stage offsets of this thread's pieces, the same for every chunk.
+  int lds_off[MAXC];
+#pragma unroll
+  for (int u = 0; u < MAXC; ++u) {
+    const int f = tid + u * RT_THREADS;
+    const int r = f / cpr;
+    lds_off[u] = r * PITCH + (f - r * cpr) * 8;
+  }
+  auto store_w = [&](int c) {
+    const int n8 = min(CK, d - c * CK) * cpr;
+#pragma unroll
+    for (int u = 0; u < MAXC; ++u)
+      if (tid + u * RT_THREADS < n8) *(uint2*)(s_stage + lds_off[u]) = wreg[c][u];
+  };
+  __syncthreads();  // the pad zeros are in place before the first stage
+  store_w(0);
+  // B fragment addresses inside a stage: lane (g, j) reads rows 8 g + 4 h + j / 4 and
+  // columns 16 nb + 4 (j % 4) .. + 3, for h = 0, 1, of the k-step's 32 rows.
+  const int boff = (8 * g + (j >> 2)) * PITCH + 8 * (j & 3);
+#pragma unroll
+  for (int c = 0; c < MAXCH; ++c) {  // unrolled, so every register index is static
+    if (c >= nchunk) break;           // uniform
+    const bool more = c + 1 < nchunk;
+    __syncthreads();                  // stage c is complete
+    if (mma_wave) {
+#pragma unroll
+      for (int s = 0; s < CS; ++s) {
+        const int ks = c * CS + s;
+        if (ks < RT_MAX_STEPS && ks < nks) {  // uniform
+          const char* sb = s_stage + s * 32 * PITCH + boff;
+#pragma unroll
+          for (int nb = 0; nb < NBH; ++nb) {
+            if (cb0 + nb < NB) {  // uniform
+              const uint2 lo = lds_read_tr16(sb + (cb0 + nb) * 32);
+              const uint2 hi = lds_read_tr16(sb + 4 * PITCH + (cb0 + nb) * 32);
+              const typename Mma<DT>::Frag b{u32x4{lo.x, lo.y, hi.x, hi.y}};
+              Mma<DT>::run(acc[nb], typename Mma<DT>::Frag{xr[ks < RT_MAX_STEPS ? ks : 0]},
+                           b);
+            }
+          }
+        }
+      }
+    }
+    if (more) {
+      __syncthreads();  // every GEMM wave is done with stage c
+      store_w(c + 1);
+    }
+  }
+
+  // ---- logits: rounded to the dtype, stored, and kept in LDS as fp32 -----------------
+  // acc[nb][i] holds the logit of token 16 tile + 4 g + i, expert 16 (cb0 + nb) + j.
+  if (mma_wave) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int tl = tile * 16 + 4 * g + i;
+      const int64_t t = tok0 + tl;
+#pragma unroll
+      for (int nb = 0; nb < NBH; ++nb) {
+        if (cb0 + nb >= NB) continue;  // uniform
+        const int e = 16 * (cb0 + nb) + j;
+        float l = acc[nb][i];
+        if (a.bias && e < E) l += a.bias[e];
+        const ET lv = Elem<DT>::from_f(l);
+        if (t < T && e < E) ((ET*)a.logits)[t * E + e] = lv;
+        s_lg[tl * LGP + e] = e < E ? Elem<DT>::to_f(lv) : -INFINITY;
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- softmax and the fast selection: token 4 wave + g on lanes 16 g .. 16 g + 15 ------
+  const int tl = wave * 4 + g;
+  const int64_t t = tok0 + tl;
+  const bool live = t < T;
+  float key[NB];
+  bool nan_here = false;
+  float m = -INFINITY;
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    key[nb] = s_lg[tl * LGP + 16 * nb + j];
+    nan_here |= __builtin_isnan(key[nb]);
+    m = fmaxf(m, key[nb]);
+  }
+  const bool nan_row = row16_sum_i(nan_here ? 1 : 0) != 0;
+  m = row16(m, fmax_);
+  if (nan_row) m = __uint_as_float(0x7fc00000u);
+  float inv = 0.0f;
+  if (train || !normalize) {  // uniform
+    float ex[NB], s = 0.0f;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      ex[nb] = 16 * nb + j < E ? expf(key[nb] - m) : 0.0f;
+      s += ex[nb];
+    }
+    inv = 1.0f / row16(s, fadd_);
+    if (train) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const int e = 16 * nb + j;
+        if (e < E) {
+          const float p = ex[nb] * inv;
+          if (live) a.probs[t * E + e] = p;
+          key[nb] = p;
+          s_lg[tl * LGP + e] = p;  // the exact pass's keys and the column sums
+        }
+      }
+    }
+  }
+  if (j == 0) {
+    s_m[tl] = m;
+    s_inv[tl] = inv;
+  }
+  uint32_t avail = 0;
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) avail |= (16 * nb + j < E ? 1u : 0u) << nb;
+  bool exact = nan_row;
+  float s_sel = 0.0f;
+  int d_sel = 0;
+  for (int r = 0; r < k; ++r) {
+    float c = -INFINITY;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+      if (avail >> nb & 1u) c = fmaxf(c, key[nb]);
+    const float mx = row16(c, fmax_);
+    int cnt = 0, loc = 1 << 20;
+#pragma unroll
+    for (int nb = NB - 1; nb >= 0; --nb)
+      if ((avail >> nb & 1u) && key[nb] == mx) {
+        ++cnt;
+        loc = 16 * nb + j;
+      }
+    exact |= row16_sum_i(cnt) != 1;
+    const int id = row16_min_i(loc);
+    if ((id & 15) == j && id < (1 << 20)) avail &= ~(1u << (id >> 4));
+    if (j == r) {
+      s_sel = mx;
+      d_sel = id;
+    }
+  }
+  {
+    const bool o = j < k;
+    const float s = o ? s_sel : 0.0f;
+    float wgt = s;
+    if (train) {
+      if (normalize && k > 1) wgt = s / row16(s, fadd_);
+    } else if (normalize) {
+      const float mk = row16(o ? s : -INFINITY, fmax_);
+      const float e = o ? expf(s - mk) : 0.0f;
+      wgt = e * (1.0f / row16(e, fadd_));
+    } else {
+      wgt = expf(s - m) * inv;
+    }
+    if (live && !exact && o) {
+      a.topk_idx[t * k + j] = d_sel;
+      ((ET*)a.topk_w)[t * k + j] = Elem<DT>::from_f(wgt);
+      atomicAdd(&s_hist[d_sel], 1);
+    }
+    if (live && exact && j == 0) s_tie[atomicAdd(&s_ntie, 1)] = tl;
+  }
+  __syncthreads();
+
+  // ---- the exact pass for the undecided tokens: one wave per token -------------------
+  // The keys come from LDS as the selection saw them; the stage holds the partitions'
+  // swap slots now.
+  const int nt = s_ntie;
+  int2* pos = (int2*)s_stage + wave * 256;
+  const bool has0 = lane < E, has1 = lane + 64 < E;
+  for (int q = wave; q < nt; q += RT_WAVES) {  // uniform
+    const int rt = s_tie[q];
+    const float* row = s_lg + rt * LGP;
+    const float k0 = has0 ? row[lane] : -INFINITY, k1 = has1 ? row[lane + 64] : -INFINITY;
+    RegRow rr{(int)ord_key(k0), (int)ord_key(k1), lane, lane + 64, lane};
+    topk_select(rr, E, k, pos);
+    const int a0 = (rr.i0 & 63) * 4, a1 = (rr.i1 & 63) * 4;
+    const float lo0 = __int_as_float(__builtin_amdgcn_ds_bpermute(a0, __float_as_int(k0)));
+    const float hi0 = __int_as_float(__builtin_amdgcn_ds_bpermute(a0, __float_as_int(k1)));
+    const float lo1 = __int_as_float(__builtin_amdgcn_ds_bpermute(a1, __float_as_int(k0)));
+    const float hi1 = __int_as_float(__builtin_amdgcn_ds_bpermute(a1, __float_as_int(k1)));
+    write_route_row<DT>(tok0 + rt, k, lane, train, normalize, rr.i0 < 64 ? lo0 : hi0,
+                        rr.i1 < 64 ? lo1 : hi1, rr.i0, rr.i1, s_m[rt], s_inv[rt],
+                        (ET*)a.topk_w, a.topk_idx);
+    if (lane < k) atomicAdd(&s_hist[rr.i0], 1);
+    if (lane + 64 < k) atomicAdd(&s_hist[rr.i1], 1);
+  }
+  __syncthreads();
+
+  // ---- this chunk's histogram and, in training, its column sums of probs -------------
+  const int64_t wg = blockIdx.x;
+  const int nlive = (int)min((int64_t)RT_TOK, T - tok0);
+  for (int e = tid; e < E; e += RT_THREADS) {
+    a.hist[wg * E + e] = s_hist[e];
+    if (train && a.colsum) {
+      float s = 0.0f;
+      for (int q = 0; q < nlive; ++q) s += s_lg[q * LGP + e];
+      a.colsum[wg * E + e] = s;
+    }
+  }
+}
+
+bool router_fused_supported(int dtype, int d, int E, int k) {
+  return (dtype == DT_BF16 || dtype == DT_F16) && d >= 32 && d % 32 == 0 &&
+         d <= 32 * RT_MAX_STEPS && E >= 1 && E <= RT_MAX_E && E % 4 == 0 && k >= 1 &&
+         k <= RT_MAXK && k <= E;
+}
+
+size_t router_fused_ws_bytes(int64_t T, int E) {
+  const int64_t nwg = router_fused_chunks(T);
+  auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+  return 2 * al(nwg * E * 4);
+}
+
+RouterArgs router_fused_args(void* ws, int64_t T, int E) {
+  const int64_t nwg = router_fused_chunks(T);
+  auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+  RouterArgs a{};
+  a.hist = (int32_t*)ws;
+  a.colsum = (float*)((char*)ws + al(nwg * E * 4));
+  return a;
+}
+
+template <int DT, int NB>
+static void launch_nb(const RouterArgs& a, unsigned grid, hipStream_t s) {
+  router_fwd_kernel<DT, NB><<<grid, RT_THREADS, 0, s>>>(a);
+}
+
+template <int DT>
+static void launch_fwd(const RouterArgs& a, unsigned grid, hipStream_t s) {
+  switch ((a.E + 15) / 16) {
+    case 1: launch_nb<DT, 1>(a, grid, s); break;
+    case 2: launch_nb<DT, 2>(a, grid, s); break;
+    case 3: launch_nb<DT, 3>(a, grid, s); break;
+    case 4: launch_nb<DT, 4>(a, grid, s); break;
+    default: launch_nb<DT, 5>(a, grid, s); break;
+  }
+}
+
+int router_fused_launch(const RouterArgs& a, int dtype, hipStream_t s) {
+  NSMOE_REQUIRE(router_fused_supported(dtype, a.d, a.E, a.k),
+                "router: the fused router takes bf16/fp16, d %% 32 == 0, d <= %d, "
+                "E %% 4 == 0, E <= %d, top_k <= %d (d %d, E %d, k %d)", 32 * RT_MAX_STEPS,
+                RT_MAX_E, RT_MAXK, a.d, a.E, a.k);
+  NSMOE_REQUIRE(a.x && a.w && a.logits && a.topk_w && a.topk_idx && a.hist &&
+                    (!(a.flags & 1) || a.probs), "router: NULL pointer");
+  if (a.T == 0) return NSMOE_OK;
+  const unsigned grid = (unsigned)router_fused_chunks(a.T);
+  KernelTimer timer("route_fwd", s);
+  if (dtype == DT_BF16) launch_fwd<DT_BF16>(a, grid, s);
+  else launch_fwd<DT_F16>(a, grid, s);
+  timer.stop();
+  return check_launch("router_fwd_kernel");
+}
+
+}  // namespace nsmoe

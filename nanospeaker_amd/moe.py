@@ -212,13 +212,14 @@ class MoEBlock(nn.Module):
                 self.training and self.router.noise_std):
             # The whole block as one autograd node (router GEMM + HIP router tail,
             # dispatch, experts, combine, balance loss; HIP backward).
-            out, aux, counts, topk_idx = moe_kernel.block_forward(
+            out, aux, counts, topk_idx, logits = moe_kernel.block_forward(
                 x, self.router.W, self.W_in, self.W_out, self.W_sh_in, self.W_sh_out,
                 self.b_in, self.b_out, self.b_sh_in, self.b_sh_out, self.top_k,
                 self.router.wants_probs(), self.router.normalize_weights, self._kernel_act,
                 self.router.aux_loss_coef)
             self.expert_counts = counts.detach()
-            self._routing = topk_idx  # the last call's expert ids, for inspection
+            self._routing = topk_idx  # the last call's expert ids and router logits,
+            self._logits = logits     # for inspection
             self.aux_loss = aux
             return out.view(shape)
 

@@ -677,6 +677,10 @@ class _BlockPlan:
         # d % 16 == 0 and E % 4 == 0 (E <= 128 always holds here); otherwise in torch.
         self.fuse_router = (dt in (torch.bfloat16, torch.float16) and d % 16 == 0
                             and e % 4 == 0 and e <= 128)
+        # The forward's router GEMM runs in the library, fused with the router tail, for
+        # 16-bit types with d % 32 == 0, d <= 576, E % 4 == 0, E <= 80 and top_k <= 16.
+        self.fuse_route = (self.fuse_router and d % 32 == 0 and d <= 576 and e <= 80
+                           and k <= 16)
         self.bwd_ws = lib.nsmoe_block_bwd_workspace_size(self.args, flags,
                                                          int(self.fuse_router))
 
@@ -734,13 +738,19 @@ def _block_fwd_impl(x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in
     n, d = x.shape
     e, h2 = W_r.shape[1], w_in.shape[2]
     s = 0 if w_sh_in is None else w_sh_in.shape[0]
-    logits = x @ W_r
-    if dt not in (torch.bfloat16, torch.float16):
-        logits = logits.float()
-    if logit_bias is not None:
-        logits = (logits.float() + logit_bias.float()).to(logits.dtype)
     flags = _route_bits(dt, want_probs, normalize)
     plan = _plan(dt, activation, n, d, h2 // 2, e, s, top_k, flags)
+    bias = None
+    if plan.fuse_route:
+        logits = torch.empty((n, e), dtype=dt, device=dev)  # written by the router kernel
+        if logit_bias is not None:
+            bias = logit_bias.to(device=dev, dtype=torch.float32).contiguous()
+    else:
+        logits = x @ W_r
+        if dt not in (torch.bfloat16, torch.float16):
+            logits = logits.float()
+        if logit_bias is not None:
+            logits = (logits.float() + logit_bias.float()).to(logits.dtype)
     saved = torch.empty(plan.saved_bytes, dtype=torch.uint8, device=dev)
     out = torch.empty((n, d), dtype=dt, device=dev)
     counts = torch.empty(e, dtype=torch.int32, device=dev)
@@ -754,10 +764,11 @@ def _block_fwd_impl(x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in
         a.w_in_packed, a.w_out_packed = p_in.data_ptr(), p_out.data_ptr()
         ws = torch.empty(plan.fwd_ws, dtype=torch.uint8, device=dev)
         nat.check(nat.lib().nsmoe_block_fwd(
-            a, logits.data_ptr(), flags | (nat.BLOCK_PACK if pending is not None else 0),
-            aux_coef, saved.data_ptr(), topk_idx.data_ptr(), counts.data_ptr(),
-            out.data_ptr(), aux.data_ptr() if want_probs else None, ws.data_ptr(),
-            plan.fwd_ws, _stream()), "nsmoe_block_fwd")
+            a, W_r.data_ptr() if plan.fuse_route else None, _p(bias), logits.data_ptr(),
+            flags | (nat.BLOCK_PACK if pending is not None else 0), aux_coef,
+            saved.data_ptr(), topk_idx.data_ptr(), counts.data_ptr(), out.data_ptr(),
+            aux.data_ptr() if want_probs else None, ws.data_ptr(), plan.fwd_ws, _stream()),
+            "nsmoe_block_fwd")
         if pending is not None:
             PACKS.store(pending, p_in, p_out)
     else:
@@ -954,16 +965,17 @@ def block_forward(x, router_W, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh
                   top_k, want_probs, normalize, activation, aux_coef, logit_bias=None):
     """
     The MoE block on the kernel path: (out [N, d], aux_loss, counts [E] int32,
-    topk_idx [N, k] int64).  aux_loss is the balance loss (fp32) when want_probs, else a
-    zero of x's dtype (router.py:52-54, moe.py:367-372).  Parameters are cast to x's
-    dtype, as the eager matmuls would run.
+    topk_idx [N, k] int64, logits [N, E]).  aux_loss is the balance loss (fp32) when
+    want_probs, else a zero of x's dtype (router.py:52-54, moe.py:367-372); logits are the
+    router GEMM's output the routing ran on (not differentiable).  Parameters are cast to
+    x's dtype, as the eager matmuls would run.
     """
     _check_activation(activation)
     cast = lambda t: None if t is None else t.to(x.dtype)
     op = block_fwd if torch.compiler.is_compiling() else _BlockEager.apply
-    out, aux, counts, topk_idx, _, _, _ = op(
+    out, aux, counts, topk_idx, logits, _, _ = op(
         x.contiguous(), cast(router_W).contiguous(), cast(w_in).contiguous(),
         cast(w_out).contiguous(), _c(cast(w_sh_in)), _c(cast(w_sh_out)), _c(cast(b_in)),
         _c(cast(b_out)), _c(cast(b_sh_in)), _c(cast(b_sh_out)), top_k, want_probs, normalize,
         activation, float(aux_coef), logit_bias)
-    return out, aux, counts, topk_idx
+    return out, aux, counts, topk_idx, logits

@@ -182,7 +182,20 @@ def test_block_entry_points_reject_missing_buffers():
     lib = nat.lib()
     a = nat.ExpertsArgs(dtype=0, activation=0, n_tokens=4, d_model=64, d_hidden=64,
                         n_experts=8, n_shared=0, top_k=2, l_cap=0)
-    assert lib.nsmoe_block_fwd(a, 1, 0, 0.0, 1, None, 1, 1, None, 1, 1 << 20, None) == 1
+    #      args w_router bias logits flags coef saved idx counts out aux ws ws_bytes stream
+    assert lib.nsmoe_block_fwd(a, None, None, 1, 0, 0.0, 1, None, 1, 1, None, 1, 1 << 20,
+                               None) == 1
     assert "NULL" in lib.nsmoe_last_error().decode()
-    assert lib.nsmoe_block_fwd(a, 1, 0, 0.0, 1, 1, 1, 1, None, 1, 1 << 20, None) == 1
+    assert lib.nsmoe_block_fwd(a, None, None, 1, 0, 0.0, 1, 1, 1, 1, None, 1, 1 << 20,
+                               None) == 1
     assert "packed" in lib.nsmoe_last_error().decode()
+    a.w_in_packed = a.w_out_packed = 1
+    assert lib.nsmoe_block_fwd(a, None, 1, 1, 0, 0.0, 1, 1, 1, 1, None, 1, 1 << 20,
+                               None) == 1
+    assert "logit_bias" in lib.nsmoe_last_error().decode()
+    odd = nat.ExpertsArgs(dtype=0, activation=0, n_tokens=4, d_model=48, d_hidden=64,
+                          n_experts=8, n_shared=0, top_k=2, l_cap=0, w_in_packed=1,
+                          w_out_packed=1)
+    assert lib.nsmoe_block_fwd(odd, 1, None, 1, 0, 0.0, 1, 1, 1, 1, None, 1, 1 << 20,
+                               None) == 1
+    assert "fused router" in lib.nsmoe_last_error().decode()

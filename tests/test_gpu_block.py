@@ -74,6 +74,30 @@ def close(name, got, ref, dtype):
         assert_close_bf16(name, got.float(), ref)
 
 
+def check_router_gemm(x, W, logits, logit_bias, dt):
+    """The block's logits are x W (+ the offset) accumulated in fp32 and rounded to the
+    block's dtype: within one rounding step of the fp32 product.  Also reports how many
+    tokens the CPU's own bf16 GEMM would route differently (accumulation order)."""
+    ref = x.double() @ W.double()
+    if logit_bias is not None:
+        ref = ref + logit_bias.double()
+    if dt == torch.float32:
+        torch.testing.assert_close(logits.double(), ref, rtol=1e-5, atol=1e-5)
+        return
+    step = {torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -11}[dt]
+    bound = step * ref.abs() * 1.01 + 1e-5
+    err = (logits.double() - ref).abs()
+    assert bool((err <= bound).all()), f"router GEMM off by {float((err / bound).max()):.2f} steps"
+    cpu = (x @ W).float()
+    if logit_bias is not None:
+        cpu = (cpu + logit_bias).to(dt).float()
+    k = 6 if W.shape[1] >= 6 else 1
+    flips = (R.route_from_logits(cpu, k, False, True, dt)[1]
+             != R.route_from_logits(logits, k, False, True, dt)[1]).any(1).float().mean()
+    print(f"  router GEMM: {float((logits != cpu).float().mean()):.4f} of logits differ from "
+          f"the CPU bf16 GEMM; routing flips on {float(flips):.4%} of tokens")
+
+
 def check_against_oracle(x, p, g, logits, idx, counts, out, aux, grads, train, backward,
                          k=6):
     """Routing bit-exact, outputs and gradients to the dtype's bar, against the oracle run
@@ -117,11 +141,11 @@ def run_case(T, train, backward, *, logit_bias=None, **cfg):
     if logit_bias is None:
         out = m(xg)
         aux = m.aux_loss
-        idx, counts = m._routing, m.expert_counts
+        idx, counts, kl = m._routing, m.expert_counts, m._logits
         assert m._use_kernel(xg.reshape(-1, x.shape[1])), "the HIP path was not taken"
     else:
         # The reference router has no bias: the offset goes in through the op's hook.
-        out, aux, counts, idx = mk.block_forward(
+        out, aux, counts, idx, kl = mk.block_forward(
             xg, m.router.W, m.W_in, m.W_out, m.W_sh_in, m.W_sh_out, m.b_in, m.b_out,
             m.b_sh_in, m.b_sh_out, m.top_k, m.router.wants_probs(),
             m.router.normalize_weights, "silu", m.router.aux_loss_coef,
@@ -129,10 +153,10 @@ def run_case(T, train, backward, *, logit_bias=None, **cfg):
     if backward:
         torch.autograd.backward([out, aux], [g.to(DEV), torch.ones_like(aux)])
     torch.cuda.synchronize()
-    logits = x.to(DEV) @ m.router.W.detach()  # the block's own router GEMM
-    if logit_bias is not None:
-        logits = (logits.float() + logit_bias.to(DEV)).to(logits.dtype)
-    logits = logits.float().cpu()
+    # The oracle routes the block's own router GEMM output (the values its routing ran
+    # on); that output is checked against an fp32 GEMM of the same operands.
+    logits = kl.float().cpu()
+    check_router_gemm(x, p.W, logits, logit_bias, dt)
     grads = {}
     if backward:
         grads = {"x": xg.grad.cpu(), "W": m.router.W.grad.cpu()}

@@ -151,7 +151,7 @@ def test_pack_cache_reuse_and_invalidation():
     assert mk.PACKS.misses - m0 == 2
     fields = ("W_in", "W_out", "W_sh_in", "W_sh_out")
     p = R.Params(m.router.W.detach().cpu(), *(getattr(m, f).detach().cpu() for f in fields))
-    logits = (xd @ m.router.W.detach()).float().cpu()
+    logits = m._logits.float().cpu()
     ref = R.block(x, p, 6, train=False, fp32=True, logits=logits)
     assert torch.equal(m._routing.cpu(), ref.topk_idx)
     assert_close_bf16("out after the update", out3.float().cpu(), ref.out)
