@@ -96,10 +96,10 @@ def kernel_units(name: str, T: int, k: int, S: int, d: int, H: int, E: int):
         return rows * (2 * d * 2 * H + 2 * H * d), "mfma", "TFLOP/s"
     if name == "combine":           # read k + S rows, write one, per token (+ inv)
         return T * ((k + S) * d * 2 + d * 2 + k * 4), "hbm", "GB/s"
-    if name == "route_fwd":         # bf16 logits in, fp32 probs out, ids + gates out
-        return T * (E * 2 + E * 4 + k * 8 + k * 2), "hbm", "GB/s"
-    if name == "dispatch":          # ids read twice, sorted ids + inverse written
-        return T * k * (8 * 2 + 4 + 4), "hbm", "GB/s"
+    if name == "route_fwd":         # x in; bf16 logits, fp32 probs, ids + gates out
+        return T * (d * 2 + E * 2 + E * 4 + k * 8 + k * 2), "hbm", "GB/s"
+    if name == "dispatch":          # ids read once (histograms come from the router),
+        return T * k * (8 + 4 + 4), "hbm", "GB/s"  # sorted ids + inverse written
     if name == "combine_dx":        # expert dX rows + d(logits) in, dx out, per token
         return T * ((k + S) * d * 2 + (E + 7) // 8 * 8 * 2 + d * 2 + k * 4), "hbm", "GB/s"
     if name == "router_dw":         # x and d(logits) read once
@@ -186,7 +186,7 @@ KERNEL_SYMBOLS = {
     "dw": ("nsmoe::dw_pair_kernel",),
     "dw_in": ("nsmoe::dw_async_kernel<0, 0", "nsmoe::dw_kernel<0, 0"),
     "dw_out": ("nsmoe::dw_async_kernel<0, 1", "nsmoe::dw_kernel<0, 1"),
-    "route_fwd": ("nsmoe::route_fwd_kernel",),
+    "route_fwd": ("nsmoe::router_fwd_kernel", "nsmoe::route_fwd_kernel"),
     "combine": ("nsmoe::combine_kernel",),
     "combine_dx": ("nsmoe::combine_dx_kernel",),
     "pack": ("nsmoe::pack_kernel", "nsmoe::pack_ks_kernel"),

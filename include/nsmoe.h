@@ -61,8 +61,10 @@ int nsmoe_timing_read(const char* kernel_name, double* total_ms, int64_t* launch
  *                    stream for the weight packing or the dW stage)
  *   "fwd_rows"       rows per tile of the 16-bit forward expert kernel: 64 or 96
  *   "fwd_dist"       its weight prefetch distance in k-steps: 2 or 3
- *   "bwd_rows"       rows per tile of the GLU-backward kernel: 48, 64 or 80
- *   "bwd_dist"       its prefetch distance: 2 or 3
+ *   "bwd_rows"       rows per tile of the GLU-backward kernel: 48, 64, 80 or 96 (96
+ *                    only when the forward saved the pre-activations)
+ *   "bwd_dist"       its prefetch distance: 2, 3 or 4 (4 only with the pre-activations
+ *                    saved); a distance that does not divide the k-steps is not taken
  *   "dx_rows"        rows per tile of the dX kernel: 64 or 96
  *   "dx_dist"        its prefetch distance: 2, 3 or 4
  *   "xcd_run"        tiles of one group dealt to one XCD in a row: 1 .. 1024
@@ -269,7 +271,16 @@ int nsmoe_experts_bwd(const nsmoe_experts_args* args, const int32_t* inv,
  *
  * `saved` (nsmoe_block_saved_layout: total bytes and the offset of each part) is written
  * by the forward and read by the backward: topk_w [T, k] (args dtype), probs [T, E] fp32
- * (train branch only) and the dispatch buffers of nsmoe_dispatch.  The expert ids
+ * (train branch only), the dispatch buffers of nsmoe_dispatch and, with
+ * NSMOE_BLOCK_SAVE_ACT in route_flags, the experts' pre-activations x W_in + b_in (args
+ * dtype, [gate | up] for the dispatch's l_cap rows and each shared expert's T rows rounded
+ * up to 16, stored in 16 x 16 blocks in the expert kernels' register order: opaque to the
+ * caller).  With them saved the backward does not recompute x W_in, which is two
+ * thirds of its expert GEMM work; the reference recomputes them in its backward
+ * (moe_kernel.py:663-672) and rounds them to the same dtype.  The part is empty (and the
+ * flag has no effect) where the register-tiled expert kernels do not apply: 16-bit
+ * types, d % 64 == 0, H % 16 == 0, H <= 128.  Pass the same route_flags to the forward,
+ * the backward and the layout and workspace queries.  The expert ids
  * topk_idx [T, k] int64 and the routing counts [E] int32 are separate caller buffers
  * (MoEBlock keeps both after the step), written by the forward and read by the backward.
  *
@@ -287,6 +298,7 @@ int nsmoe_experts_bwd(const nsmoe_experts_args* args, const int32_t* inv,
  *     nsmoe_block_bwd_workspace_size(args, route_flags, 0).
  */
 #define NSMOE_BLOCK_PACK 8
+#define NSMOE_BLOCK_SAVE_ACT 16
 
 #define NSMOE_SAVED_TOPK_W 0
 #define NSMOE_SAVED_PROBS 1
@@ -295,7 +307,8 @@ int nsmoe_experts_bwd(const nsmoe_experts_args* args, const int32_t* inv,
 #define NSMOE_SAVED_PAD_OFFSETS 4
 #define NSMOE_SAVED_N_POST_PAD 5
 #define NSMOE_SAVED_INV 6
-#define NSMOE_BLOCK_NSAVED 7
+#define NSMOE_SAVED_ACT 7
+#define NSMOE_BLOCK_NSAVED 8
 
 int nsmoe_block_saved_layout(const nsmoe_experts_args* args, int32_t route_flags,
                              size_t* offsets /* [NSMOE_BLOCK_NSAVED] */, size_t* total_bytes);

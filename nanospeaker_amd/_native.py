@@ -13,8 +13,8 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libnsmoe.so"
 
 BF16, F16, F32 = 0, 1, 2
-ROUTE_PROBS, ROUTE_NORMALIZE, ROUTE_LOGITS16, BLOCK_PACK = 1, 2, 4, 8
-ABI_VERSION = 4
+ROUTE_PROBS, ROUTE_NORMALIZE, ROUTE_LOGITS16, BLOCK_PACK, BLOCK_SAVE_ACT = 1, 2, 4, 8, 16
+ABI_VERSION = 5
 
 # Every symbol include/nsmoe.h declares, with (restype, argtypes).
 _vp, _i32, _i64, _sz = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t
@@ -83,7 +83,7 @@ SIGNATURES = {
 }
 
 # Parts of the block's `saved` buffer (NSMOE_SAVED_* in nsmoe.h).
-SAVED_TOPK_W, SAVED_PROBS, SAVED_INV, BLOCK_NSAVED = 0, 1, 6, 7
+SAVED_TOPK_W, SAVED_PROBS, SAVED_INV, SAVED_ACT, BLOCK_NSAVED = 0, 1, 6, 7, 8
 
 
 class NativeLibraryError(RuntimeError):

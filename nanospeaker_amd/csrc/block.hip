@@ -36,6 +36,9 @@ static BlockLayout block_layout(const nsmoe_experts_args* a, int32_t flags) {
   const size_t es = a->dtype == DT_F32 ? 4 : 2;
   const int64_t m = (int64_t)(T * k);
   const size_t l_cap = (size_t)nsmoe_dispatch_l_cap(m, (int32_t)E);
+  nsmoe_experts_args b = *a;
+  b.l_cap = (int64_t)l_cap;
+  const size_t act = (flags & NSMOE_BLOCK_SAVE_ACT) ? experts_save_act_bytes(&b) : 0;
   const size_t sizes[NSMOE_BLOCK_NSAVED] = {
       T * k * es,                                   // topk_w
       (flags & NSMOE_ROUTE_PROBS) ? T * E * 4 : 0,  // probs
@@ -44,6 +47,7 @@ static BlockLayout block_layout(const nsmoe_experts_args* a, int32_t flags) {
       (E + 1) * 4,                                  // pad_offsets
       4,                                            // n_post_pad
       T * k * 4,                                    // inv
+      act,                                          // pre-activations (SAVE_ACT)
   };
   BlockLayout L;
   size_t o = 0;
@@ -53,6 +57,12 @@ static BlockLayout block_layout(const nsmoe_experts_args* a, int32_t flags) {
   }
   L.total = o;
   return L;
+}
+
+// The saved pre-activations, or NULL when the layout has none.
+static char* act_part(const BlockLayout& L, char* saved, int32_t flags) {
+  const bool has = (flags & NSMOE_BLOCK_SAVE_ACT) && L.off[NSMOE_SAVED_ACT] < L.total;
+  return has ? saved + L.off[NSMOE_SAVED_ACT] : nullptr;
 }
 
 // Points a copy of the caller's args at the routing state inside `saved` and at the
@@ -187,7 +197,7 @@ extern "C" int nsmoe_block_fwd(const nsmoe_experts_args* a, const void* w_router
   const int jrc = side_join(s, s_pack, kSideSlotPack);  // joined on every path
   NSMOE_TRY(rc);
   NSMOE_TRY(jrc);
-  return nsmoe_experts_fwd(&b, inv, out, ws + dsp, exp, s);
+  return experts_fwd_launch(&b, inv, out, ws + dsp, exp, act_part(L, sv, route_flags), s);
 }
 
 namespace nsmoe {
@@ -268,7 +278,8 @@ extern "C" int nsmoe_block_bwd(const nsmoe_experts_args* a, const void* logits,
   g.dtopk_w = ws + W.tw;  // the gate gradient stays internal: it feeds the router backward
   // dW runs on the side stream beside everything below; joined before returning.
   hipStream_t s_dw = s;
-  NSMOE_TRY(experts_bwd_launch(&b, inv, grad_out, &g, ws + W.exp, W.gl - W.exp, !fuse, s, &s_dw));
+  NSMOE_TRY(experts_bwd_launch(&b, inv, grad_out, &g, ws + W.exp, W.gl - W.exp, !fuse, s, &s_dw,
+                               act_part(L, sv, route_flags)));
   const int rc = block_bwd_router(a, b, L, sv, topk_idx, logits, route_flags, aux_coef, grad_aux, grads,
                                   w_router, grad_w_router, grad_logits, ws, W, inv, fuse, s);
   const int jrc = side_join(s, s_dw, kSideSlotDw);

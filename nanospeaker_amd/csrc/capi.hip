@@ -43,12 +43,12 @@ struct OptionSpec {
   const int64_t* allowed;   // or an explicit list (terminated by 0), when non-NULL
 };
 static const int64_t kFwdRows[] = {64, 96, 0};
-static const int64_t kBwdRows[] = {48, 64, 80, 0};
+static const int64_t kBwdRows[] = {48, 64, 80, 96, 0};
 static const int64_t kDxRows[] = {64, 96, 0};
 static const OptionSpec kOptions[OPT_COUNT] = {
     {"single_stream", 1, 1, nullptr}, {"fwd_rows", 0, 0, kFwdRows},
     {"fwd_dist", 2, 3, nullptr},      {"bwd_rows", 0, 0, kBwdRows},
-    {"bwd_dist", 2, 3, nullptr},      {"dx_rows", 0, 0, kDxRows},
+    {"bwd_dist", 2, 4, nullptr},      {"dx_rows", 0, 0, kDxRows},
     {"dx_dist", 2, 4, nullptr},       {"xcd_run", 1, 1024, nullptr},
 };
 static std::atomic<int64_t> g_options[OPT_COUNT];
@@ -222,7 +222,7 @@ extern "C" uint64_t nsmoe_launch_count(void) {
   return nsmoe::g_launches.load(std::memory_order_relaxed);
 }
 
-extern "C" int32_t nsmoe_abi_version(void) { return 4; }
+extern "C" int32_t nsmoe_abi_version(void) { return 5; }
 
 extern "C" int nsmoe_set_option(const char* name, int64_t value) {
   const int i = nsmoe::option_index(name);

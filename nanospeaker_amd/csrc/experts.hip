@@ -1036,11 +1036,25 @@ static int launch_combine(const void* rows, const int32_t* inv, int64_t T, int d
   return check_launch("combine_kernel");
 }
 
+// Whether the register-tiled forward and backward both take this shape (launch_fwd_async,
+// launch_bwd_async): the pre-activations are then saved by the one and read by the other.
+static bool save_act_shape(const nsmoe_experts_args* a) {
+  if (a->dtype != DT_BF16 && a->dtype != DT_F16) return false;
+  const int d = a->d_model, H = a->d_hidden;
+  if (nbw_for(a) > 2 || d % 64 != 0 || H % 16 != 0) return false;
+  const PackGeom pg = pack_geom(a->dtype, d, H, a->n_experts, a->n_shared);
+  const int npass = (d + NP2 - 1) / NP2;
+  return (npass * pg.out_kb) % 2 == 0 && (npass * (2 * H / 32)) % 2 == 0 && pg.in_kb >= 4;
+}
+
 template <int DT>
 static int experts_fwd_impl(const nsmoe_experts_args* a, const int32_t* inv, void* out, void* ws,
-                            hipStream_t s) {
+                            void* act_out, hipStream_t s) {
   ExpParams p = make_params(a);
   p.y = ws;
+  // Saved only where the forward kernel that writes them runs (which needs p.fast); the
+  // backward's decision (experts_bwd_impl) is the same function of the same arguments.
+  p.a1_out = act_out && p.fast && save_act_shape(a) ? act_out : nullptr;
   const bool fast = p.fast && aligned16(out);
   NSMOE_TRY(launch_fwd_tiles<DT>(p, nbw_for(a), fwd_grid(a), s));
   return launch_combine<DT>(ws, inv, a->n_tokens, a->d_model, a->top_k, a->n_shared, a->l_cap,
@@ -1156,9 +1170,12 @@ static int experts_dw(const nsmoe_experts_args* a, const ExpParams& p,
 template <int DT>
 static int experts_bwd_impl(const nsmoe_experts_args* a, const int32_t* inv, const void* dout,
                             const nsmoe_experts_grads* gr, char* ws, bool combine,
-                            hipStream_t s, hipStream_t* side_out) {
+                            hipStream_t s, hipStream_t* side_out, const void* act_in) {
   const BwdLayout L = bwd_layout(a);
   ExpParams p = make_params(a);
+  // The forward wrote them under the same condition (p.fast here before dout's alignment
+  // is folded in); a backward that then takes another kernel recomputes them instead.
+  p.a1_in = act_in && p.fast && save_act_shape(a) ? act_in : nullptr;
   const int nbw = nbw_for(a);
   const int64_t grid = fwd_grid(a);
   p.dout = dout;
@@ -1204,6 +1221,22 @@ extern "C" size_t nsmoe_experts_fwd_workspace_size(const nsmoe_experts_args* a) 
 
 extern "C" int nsmoe_experts_fwd(const nsmoe_experts_args* a, const int32_t* inv, void* out,
                                  void* workspace, size_t workspace_bytes, void* stream) {
+  return experts_fwd_launch(a, inv, out, workspace, workspace_bytes, nullptr,
+                            (hipStream_t)stream);
+}
+
+namespace nsmoe {
+
+size_t experts_save_act_bytes(const nsmoe_experts_args* a) {
+  if (!a || !save_act_shape(a)) return 0;
+  // act_block's row blocks: the dispatch's l_cap rows (a multiple of 16), then each shared
+  // group's T rows rounded up to 16.
+  const int64_t rows = a->l_cap + (int64_t)a->n_shared * cdiv(a->n_tokens, 16) * 16;
+  return (size_t)rows * 2 * a->d_hidden * elem_size(a->dtype);
+}
+
+int experts_fwd_launch(const nsmoe_experts_args* a, const int32_t* inv, void* out,
+                       void* workspace, size_t workspace_bytes, void* act_out, hipStream_t s) {
   NSMOE_TRY(validate(a));
   if (a->n_tokens == 0) return NSMOE_OK;
   NSMOE_REQUIRE(a->x && a->w_in && a->w_out && a->topk_w && a->sorted_ids && a->pad_offsets &&
@@ -1215,13 +1248,14 @@ extern "C" int nsmoe_experts_fwd(const nsmoe_experts_args* a, const int32_t* inv
     set_error("experts_fwd: workspace %zu B < %zu B", workspace_bytes, need);
     return NSMOE_EWORKSPACE;
   }
-  hipStream_t s = (hipStream_t)stream;
   switch (a->dtype) {
-    case DT_BF16: return experts_fwd_impl<DT_BF16>(a, inv, out, workspace, s);
-    case DT_F16: return experts_fwd_impl<DT_F16>(a, inv, out, workspace, s);
-    default: return experts_fwd_impl<DT_F32>(a, inv, out, workspace, s);
+    case DT_BF16: return experts_fwd_impl<DT_BF16>(a, inv, out, workspace, act_out, s);
+    case DT_F16: return experts_fwd_impl<DT_F16>(a, inv, out, workspace, act_out, s);
+    default: return experts_fwd_impl<DT_F32>(a, inv, out, workspace, act_out, s);
   }
 }
+
+}  // namespace nsmoe
 
 extern "C" size_t nsmoe_experts_bwd_workspace_size(const nsmoe_experts_args* a) {
   if (!a) return 0;
@@ -1233,7 +1267,7 @@ namespace nsmoe {
 int experts_bwd_launch(const nsmoe_experts_args* a, const int32_t* inv, const void* grad_out,
                        const nsmoe_experts_grads* grads, void* workspace,
                        size_t workspace_bytes, bool combine, hipStream_t s,
-                       hipStream_t* side_out) {
+                       hipStream_t* side_out, const void* act_in) {
   NSMOE_TRY(validate(a));
   NSMOE_REQUIRE(grads, "experts_bwd: NULL grads");
   if (a->n_tokens == 0) return NSMOE_OK;
@@ -1252,13 +1286,13 @@ int experts_bwd_launch(const nsmoe_experts_args* a, const int32_t* inv, const vo
   switch (a->dtype) {
     case DT_BF16:
       return experts_bwd_impl<DT_BF16>(a, inv, grad_out, grads, (char*)workspace, combine, s,
-                                       side_out);
+                                       side_out, act_in);
     case DT_F16:
       return experts_bwd_impl<DT_F16>(a, inv, grad_out, grads, (char*)workspace, combine, s,
-                                       side_out);
+                                       side_out, act_in);
     default:
       return experts_bwd_impl<DT_F32>(a, inv, grad_out, grads, (char*)workspace, combine, s,
-                                       side_out);
+                                       side_out, act_in);
   }
 }
 

@@ -469,6 +469,22 @@ __global__ void __launch_bounds__(NT, MB == 6 || D == 3 ? 3 : 2) expert_fwd_reg_
       }
 #pragma unroll
       for (int i = 0; i < MB; ++i) {
+        if (p.a1_out) {
+          // The pre-activations [gate | up] (bias included, rounded to the element type)
+          // for the backward, which then does not recompute them: one 512-byte 16 x 16
+          // block per wave and store (act_block).  Saving requires H % 16 == 0, so a
+          // column block is all in or all out.
+          const int jb = wave * NBW + j;
+          if (i * 16 + lc < rows && jb * 16 < H) {
+            T* blk = (T*)p.a1_out + act_block(p, g, m0 + i * 16) * (twoH / 16) * 256 + lane * 4;
+            *(uint2*)(blk + jb * 256) =
+                make_uint2(pack2<DT>(accg[i][j][0] + bg[0], accg[i][j][1] + bg[1]),
+                           pack2<DT>(accg[i][j][2] + bg[2], accg[i][j][3] + bg[3]));
+            *(uint2*)(blk + (H / 16 + jb) * 256) =
+                make_uint2(pack2<DT>(accu[i][j][0] + bu[0], accu[i][j][1] + bu[1]),
+                           pack2<DT>(accu[i][j][2] + bu[2], accu[i][j][3] + bu[3]));
+          }
+        }
         float hv[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r)
@@ -933,27 +949,31 @@ __global__ void __launch_bounds__(NT, 2) expert_dx_async_kernel(ExpParams p) {
 // of a steady step are unconditional (zero page for fragments past the edge).
 // Shapes: an even number of k-steps.
 
-template <int DT, int NBW, int D, int MB>
-__global__ void __launch_bounds__(NT, 2) expert_bwd_reg_kernel(ExpParams p) {
+template <int DT, int NBW, int D, int MB, bool SA>
+__global__ void __launch_bounds__(NT, SA && MB <= 4 ? 3 : 2) expert_bwd_reg_kernel(ExpParams p) {
   using G = Geo<DT>;
   using T = typename G::T;
   using M = Mma<DT>;
   using Frag = typename M::Frag;
   static_assert(G::ES == 2, "16-bit types only");
-  static_assert(D == 2 || D == 3, "prefetch distance");
+  static_assert(D >= 2 && D <= 4, "prefetch distance");
   static_assert(MB >= 2 && MB <= 6, "tiles of 32 .. 96 rows");
   constexpr int S = D + 1;
   constexpr int TM = MB * 16;            // tile rows
   constexpr int HPMAX = 64 * NBW;
   constexpr int A_BYTES = TM * G::ROWB;  // one token tile (x or dout)
+  // Token tiles per ring stage: x and dout, or dout alone when the forward saved a1.
+  constexpr int NA = SA ? 1 : 2;
+  constexpr int DOFF = SA ? 0 : A_BYTES;  // dout's tile inside a stage
   // Copies per token tile and step: TM * 4 slots of 16 bytes, up to 256 per copy; copy x
   // of wave w fills slots 256 x + CL w + lane for the lanes below CL = min(64, TM - 64 x).
   constexpr int XC = (TM + 63) / 64;
-  constexpr int NBF = 3 * NBW;           // gate, up and G fragments per wave per step
-  constexpr int SLOT = NBF + 2 * XC;     // VM operations a steady slot issues
+  constexpr int GI = SA ? 0 : 2 * NBW;   // first G fragment of a step's set
+  constexpr int NBF = GI + NBW;          // (gate, up and) G fragments per wave per step
+  constexpr int SLOT = NBF + NA * XC;    // VM operations a steady slot issues
   constexpr int DA_PITCH = 2 * HPMAX * G::ES + 16;  // staged dA1 rows
   constexpr int HB_PITCH = HPMAX * G::ES + 16;      // staged w h rows
-  constexpr int RING = S * 2 * A_BYTES;
+  constexpr int RING = S * NA * A_BYTES;
   constexpr int STAGE_BYTES = TM * (DA_PITCH + HB_PITCH);
   constexpr int LDS_BYTES = RING > STAGE_BYTES ? RING : STAGE_BYTES;
   __shared__ __attribute__((aligned(1024))) char s_lds[LDS_BYTES];
@@ -964,7 +984,7 @@ __global__ void __launch_bounds__(NT, 2) expert_bwd_reg_kernel(ExpParams p) {
   __shared__ int s_loc[3];
   char* s_da = s_lds;                   // epilogue staging, over the ring
   char* s_hb = s_lds + TM * DA_PITCH;
-  auto ring = [&](int s) __attribute__((always_inline)) { return s_lds + (s % S) * 2 * A_BYTES; };
+  auto ring = [&](int s) __attribute__((always_inline)) { return s_lds + (s % S) * NA * A_BYTES; };
 
   const int tile = tile_of_block(p);
   Located loc;
@@ -993,10 +1013,12 @@ __global__ void __launch_bounds__(NT, 2) expert_bwd_reg_kernel(ExpParams p) {
 #pragma unroll
     for (int j = 0; j < NBW; ++j) {
       const int jb = wave * NBW + j;
-      w.f[j] = M::load(P1 + ((int64_t)jb * nk + s) * G::PKB);
-      w.f[NBW + j] = M::load(P1 + ((int64_t)(HPMAX / 16 + jb) * nk + s) * G::PKB);
+      if constexpr (!SA) {
+        w.f[j] = M::load(P1 + ((int64_t)jb * nk + s) * G::PKB);
+        w.f[NBW + j] = M::load(P1 + ((int64_t)(HPMAX / 16 + jb) * nk + s) * G::PKB);
+      }
       const int n = jb * 16 + lc;
-      w.f[2 * NBW + j] = M::load(n < H ? (const char*)(Wout + (int64_t)n * d + k0 + wk) : zero);
+      w.f[GI + j] = M::load(n < H ? (const char*)(Wout + (int64_t)n * d + k0 + wk) : zero);
     }
     return w;
   };
@@ -1040,11 +1062,31 @@ __global__ void __launch_bounds__(NT, 2) expert_bwd_reg_kernel(ExpParams p) {
       const int cl = min(64, TM - 64 * x);
       char* dst = st + 4096 * x + wave * cl * 16;
       if (cl == 64 || lane < cl) {
-        async_copy16(xrow[x] ? (const void*)(xrow[x] + k0) : (const void*)zero, dst);
-        async_copy16(drow[x] ? (const void*)(drow[x] + k0) : (const void*)zero, dst + A_BYTES);
+        if constexpr (!SA)
+          async_copy16(xrow[x] ? (const void*)(xrow[x] + k0) : (const void*)zero, dst);
+        async_copy16(drow[x] ? (const void*)(drow[x] + k0) : (const void*)zero, dst + DOFF);
       }
     }
   };
+  // With SA, the forward's pre-activations of this lane's rows and columns (8 bytes of
+  // gate and 8 of up per 16 x 16 block, act_block's layout: one 512-byte block per wave
+  // and load; zeros outside the tile), into registers for the epilogue.  They go out
+  // before the copies, so the first step's wait covers them and the steady state counts
+  // stay those of the copies and weights alone.
+  uint2 a1g[MB][NBW], a1u[MB][NBW];
+  if constexpr (SA) {
+    const T* A1 = (const T*)p.a1_in + act_block(p, g, m0) * (twoH / 16) * 256 + lane * 4;
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+      for (int j = 0; j < NBW; ++j) {
+        const int jb = wave * NBW + j;
+        const bool ok = i * 16 + lc < rows && jb * 16 < H;
+        const T* blk = A1 + (int64_t)i * (twoH / 16) * 256;
+        a1g[i][j] = *(const uint2*)(ok ? (const char*)(blk + jb * 256) : zero);
+        a1u[i][j] = *(const uint2*)(ok ? (const char*)(blk + (H / 16 + jb) * 256) : zero);
+      }
+  }
 #pragma unroll
   for (int j = 0; j < D; ++j) issue_x(j);
   // The gate weight of row tid % TM, needed only by the epilogue: its load goes out after
@@ -1065,14 +1107,17 @@ __global__ void __launch_bounds__(NT, 2) expert_bwd_reg_kernel(ExpParams p) {
     const char* st = ring(s);
 #pragma unroll
     for (int i = 0; i < MB; ++i) {
-      const Frag xf = frag_sw<DT>(st, i * 16);
-      const Frag df = frag_sw<DT>(st + A_BYTES, i * 16);
+      const Frag df = frag_sw<DT>(st + DOFF, i * 16);
+      if constexpr (!SA) {
+        const Frag xf = frag_sw<DT>(st, i * 16);
 #pragma unroll
-      for (int j = 0; j < NBW; ++j) {
-        M::run(accg[i][j], w.f[j], xf);
-        M::run(accu[i][j], w.f[NBW + j], xf);
-        M::run(accG[i][j], w.f[2 * NBW + j], df);
+        for (int j = 0; j < NBW; ++j) {
+          M::run(accg[i][j], w.f[j], xf);
+          M::run(accu[i][j], w.f[NBW + j], xf);
+        }
       }
+#pragma unroll
+      for (int j = 0; j < NBW; ++j) M::run(accG[i][j], w.f[GI + j], df);
     }
   };
   // Prologue order: w(0) .. w(D - 1) [row lookups] x(0) d(0) .. x(D - 1) d(D - 1), gate.
@@ -1081,7 +1126,7 @@ __global__ void __launch_bounds__(NT, 2) expert_bwd_reg_kernel(ExpParams p) {
   // s + 1 .. s + D - 1, which holds for the prologue steps below D - 1 only once their
   // copies are complete (and the gate load, older than every steady slot, is covered by
   // the first steady wait).
-  wait_vmcnt<2 * XC + 1>();
+  wait_vmcnt<NA * XC + 1>();
   int s = 0;
   for (; s + D < nk; s += D) {
 #pragma unroll
@@ -1103,7 +1148,8 @@ __global__ void __launch_bounds__(NT, 2) expert_bwd_reg_kernel(ExpParams p) {
 
   // ---- GLU backward, lane-local: lane (lc, lg) of block (i, j) holds row i*16 + lc,
   // hidden columns n0 .. n0 + 3 ----
-  const T* bin = (g < p.E ? p.b_in : p.b_sh_in)
+  // (The saved pre-activations already carry the bias.)
+  const T* bin = !SA && (g < p.E ? p.b_in : p.b_sh_in)
                      ? per_group<T>(p.b_in, p.b_sh_in, g, p.E, twoH) : nullptr;
   float wrow[MB], part[MB];
 #pragma unroll
@@ -1131,7 +1177,14 @@ __global__ void __launch_bounds__(NT, 2) expert_bwd_reg_kernel(ExpParams p) {
         float dg[4], du[4], wh[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float gg = accg[i][j][r] + bg[r], uu = accu[i][j][r] + bu[r];
+          float gg, uu;
+          if constexpr (SA) {
+            gg = unpack2<DT>(r < 2 ? a1g[i][j].x : a1g[i][j].y, r & 1);
+            uu = unpack2<DT>(r < 2 ? a1u[i][j].x : a1u[i][j].y, r & 1);
+          } else {
+            gg = accg[i][j][r] + bg[r];
+            uu = accu[i][j][r] + bu[r];
+          }
           const float Gv = accG[i][j][r];
           float a, da;
           act_both_t<ACT>(gg, a, da);
@@ -1390,23 +1443,39 @@ __global__ void __launch_bounds__(NT, D > 2 || MB == 6 ? 3 : 2) expert_dx_reg_ke
 static int device_cus();
 static int64_t tile_grid(const ExpParams& p, int bm);
 
-template <int DT, int MB>
+template <int DT, int MB, bool SA>
 static void bwd_reg_launch_mb(const ExpParams& p, int nbw, int dist, hipStream_t s) {
   const unsigned grid = (unsigned)tile_grid(p, 16 * MB);
-  if (dist == 3) {
-    if (nbw == 1) expert_bwd_reg_kernel<DT, 1, 3, MB><<<grid, NT, 0, s>>>(p);
-    else expert_bwd_reg_kernel<DT, 2, 3, MB><<<grid, NT, 0, s>>>(p);
-  } else {
-    if (nbw == 1) expert_bwd_reg_kernel<DT, 1, 2, MB><<<grid, NT, 0, s>>>(p);
-    else expert_bwd_reg_kernel<DT, 2, 2, MB><<<grid, NT, 0, s>>>(p);
+  if constexpr (SA) {  // distance 4 only without the gate / up accumulators
+    if (dist == 4) {
+      if (nbw == 1) expert_bwd_reg_kernel<DT, 1, 4, MB, SA><<<grid, NT, 0, s>>>(p);
+      else expert_bwd_reg_kernel<DT, 2, 4, MB, SA><<<grid, NT, 0, s>>>(p);
+      return;
+    }
   }
+  if (dist == 3) {
+    if (nbw == 1) expert_bwd_reg_kernel<DT, 1, 3, MB, SA><<<grid, NT, 0, s>>>(p);
+    else expert_bwd_reg_kernel<DT, 2, 3, MB, SA><<<grid, NT, 0, s>>>(p);
+  } else {
+    if (nbw == 1) expert_bwd_reg_kernel<DT, 1, 2, MB, SA><<<grid, NT, 0, s>>>(p);
+    else expert_bwd_reg_kernel<DT, 2, 2, MB, SA><<<grid, NT, 0, s>>>(p);
+  }
+}
+
+template <int DT, bool SA>
+static void bwd_reg_launch_sa(const ExpParams& p, int nbw, int dist, int mb, hipStream_t s) {
+  if constexpr (SA) {  // 96-row tiles only without the gate / up accumulators
+    if (mb == 6) return bwd_reg_launch_mb<DT, 6, SA>(p, nbw, dist, s);
+  }
+  if (mb == 3) bwd_reg_launch_mb<DT, 3, SA>(p, nbw, dist, s);
+  else if (mb == 5) bwd_reg_launch_mb<DT, 5, SA>(p, nbw, dist, s);
+  else bwd_reg_launch_mb<DT, 4, SA>(p, nbw, dist, s);
 }
 
 template <int DT>
 static void bwd_reg_launch(const ExpParams& p, int nbw, int dist, int mb, hipStream_t s) {
-  if (mb == 3) bwd_reg_launch_mb<DT, 3>(p, nbw, dist, s);
-  else if (mb == 5) bwd_reg_launch_mb<DT, 5>(p, nbw, dist, s);
-  else bwd_reg_launch_mb<DT, 4>(p, nbw, dist, s);
+  if (p.a1_in) bwd_reg_launch_sa<DT, true>(p, nbw, dist, mb, s);
+  else bwd_reg_launch_sa<DT, false>(p, nbw, dist, mb, s);
 }
 
 template <int DT>
@@ -1436,12 +1505,20 @@ int launch_bwd_async(int dtype, const ExpParams& p, int nbw, int64_t grid, int p
       // T = 8192: 1406 tiles over 768 slots instead of 1064 over 512, the last third of a
       // round nearly empty).  The "bwd_rows" / "bwd_dist" options force a tile height and
       // a distance; 80-row tiles take distance 2, which is all their registers allow.
-      int mb = tile_grid(p, 64) > 2 * (int64_t)device_cus() ? 3 : 4;
+      // With the forward's pre-activations saved (p.a1_in) the kernel streams dout alone
+      // and holds no gate / up accumulators: 96-row tiles are allowed as well, and
+      // distance 4 where the step count divides by 4.
+      // The tile heights and distances measured fastest at T = 8192 (nanoSpeaker's
+      // shape): without the saved pre-activations 48-row tiles at distance 2 once 64-row
+      // tiles overflow two workgroups per CU; with them 64-row tiles at distance 3 (three
+      // workgroups per CU).
+      int mb = !p.a1_in && tile_grid(p, 64) > 2 * (int64_t)device_cus() ? 3 : 4;
       if (const int64_t v = option(OPT_BWD_ROWS)) mb = (int)(v / 16);
+      if (mb < 3 || mb > (p.a1_in ? 6 : 5)) mb = 4;
       int dist = mb != 3 && p.in_kb % 3 == 0 ? 3 : 2;
       if (const int64_t v = option(OPT_BWD_DIST))
-        if (v == 2 || p.in_kb % 3 == 0) dist = (int)v;
-      if (mb == 5) dist = 2;
+        if ((v == 2 || v == 3 || (v == 4 && p.a1_in)) && p.in_kb % v == 0) dist = (int)v;
+      if (mb >= 5 && !p.a1_in) dist = 2;
       KernelTimer timer("expert_bwd", s);
       if (dtype == DT_BF16) bwd_reg_launch<DT_BF16>(p, nbw, dist, mb, s);
       else bwd_reg_launch<DT_F16>(p, nbw, dist, mb, s);

@@ -39,6 +39,11 @@ struct ExpParams {
   int in_kb, in_nb, out_kb, out_nb;
   // forward output rows
   void* y;
+  // The pre-activations a1 = x W_in + b_in in 16 x 16 blocks (act_block): written by the
+  // forward when a1_out is set, read by the backward (instead of being recomputed) when
+  // a1_in is set.
+  void* a1_out;
+  const void* a1_in;
   // backward
   const void* dout;
   void* da1;
@@ -69,6 +74,19 @@ __device__ __forceinline__ const T* per_group(const void* routed, const void* sh
                                               int E, int64_t stride) {
   return g < E ? (const T*)routed + (int64_t)g * stride
                : (const T*)shared + (int64_t)(g - E) * stride;
+}
+
+// The saved pre-activations (ExpParams::a1_out / a1_in) are stored in blocks of 16 rows x
+// 16 columns, 512 contiguous bytes each: lane l = 16 q + r of a wave holds row r, columns
+// 4 q .. 4 q + 3 of the block (the MFMA accumulator layout), so each 8-byte store or load
+// of a wave covers one whole block.  A row block holds the 2H / 16 column blocks of 16
+// rows [gate 0 .. H | up 0 .. H]; the row blocks are the routed groups' in dispatch order
+// (pad_offsets are multiples of 16), then each shared group's ceil(T / 16).
+// act_block(p, g, r) is the row block of local rows r .. r + 15 of group g (r % 16 == 0).
+__device__ __forceinline__ int64_t act_block(const ExpParams& p, int g, int r) {
+  const int64_t start = g < p.E ? (int64_t)p.offs[g]
+                                : p.l_cap + (int64_t)(g - p.E) * ((p.T + 15) / 16 * 16);
+  return (start + r) / 16;
 }
 
 // Token, gate weight and pair id of local row `r` of group g (slot = row_start + r).
@@ -143,9 +161,21 @@ namespace nsmoe {
 // The dW stage runs on the side stream (side_fork slot kSideSlotDw); with side_out != NULL
 // a successful call leaves that stream in *side_out for the caller to join with
 // side_join(stream, *side_out, kSideSlotDw), otherwise it is joined before returning.
+// act_in: the forward's saved pre-activations (experts_fwd_launch's act_out), or NULL to
+// recompute them.
 int experts_bwd_launch(const ::nsmoe_experts_args* a, const int32_t* inv, const void* grad_out,
                        const ::nsmoe_experts_grads* grads, void* workspace,
                        size_t workspace_bytes, bool combine, hipStream_t stream,
-                       hipStream_t* side_out);
+                       hipStream_t* side_out, const void* act_in = nullptr);
 size_t experts_bwd_dxrows_offset(const ::nsmoe_experts_args* a);
+// nsmoe_experts_fwd that also writes the pre-activations a1 = x W_in + b_in (rows of
+// [gate | up], in the row space of the dispatch plus the shared experts' rows) to act_out
+// when experts_save_act_bytes(a) > 0; the backward then reads them instead of recomputing.
+int experts_fwd_launch(const ::nsmoe_experts_args* a, const int32_t* inv, void* out,
+                       void* workspace, size_t workspace_bytes, void* act_out,
+                       hipStream_t stream);
+// Bytes of the saved pre-activations for this shape (a->l_cap set), 0 where the kernels
+// that write and read them do not apply (16-bit types, d % 64 == 0, H % 16 == 0, H <= 128
+// and the step-count parities of the register-tiled forward and backward).
+size_t experts_save_act_bytes(const ::nsmoe_experts_args* a);
 }  // namespace nsmoe

@@ -327,6 +327,12 @@ class PackCache:
 
 PACKS = PackCache()
 
+# Whether a block forward that autograd will differentiate keeps the experts'
+# pre-activations for its backward (NSMOE_BLOCK_SAVE_ACT: rows x 2H elements more of
+# `saved` per call, against recomputing x W_in in the backward).  On by default; False
+# reproduces the recomputing backward.
+SAVE_ACT = True
+
 
 def _pack_sizes(args: nat.ExpertsArgs) -> "tuple[int, int]":
     nb_in, nb_out = ctypes.c_size_t(), ctypes.c_size_t()
@@ -636,19 +642,34 @@ def _al256(b):
     return (b + 255) // 256 * 256
 
 
-def block_saved_bytes(n: int, e: int, k: int, dtype: torch.dtype, want_probs: bool) -> int:
+def save_act_supported(dtype: torch.dtype, d: int, h: int) -> bool:
+    """Whether the block forward can save the experts' pre-activations for the backward
+    (nsmoe.h NSMOE_BLOCK_SAVE_ACT): the shapes where the register-tiled expert kernels
+    run -- 16-bit types, d % 64 == 0, h % 16 == 0, h <= 128, and the even step counts
+    those kernels unroll by (one pass of 192 output columns per 32-row step of H or 2H)."""
+    if dtype not in (torch.bfloat16, torch.float16) or d % 64 or h % 16 or h > 128:
+        return False
+    npass = -(-d // 192)
+    return (npass * -(-h // 32)) % 2 == 0 and (npass * (2 * h // 32)) % 2 == 0 and d >= 128
+
+
+def block_saved_bytes(n: int, e: int, k: int, dtype: torch.dtype, want_probs: bool,
+                      save_act: bool = False, d: int = 0, h: int = 0, s: int = 0) -> int:
     """
     Size of the block forward's `saved` buffer (nsmoe_block_saved_layout): gates [n, k],
     probs [n, e] fp32 (train branch), sorted ids [l_cap], block owners [l_cap / 16], run
-    offsets [e + 1], the padded total and inv [n k], each rounded up to 256 bytes.  Written
-    in Python so fake tensors with symbolic n get the same size; a CPU test holds it equal
-    to the library's.
+    offsets [e + 1], the padded total, inv [n k] and -- with save_act, where
+    save_act_supported(dtype, d, h) -- the pre-activations, 2 h columns of l_cap rows and
+    s times n rows rounded up to 16, each part rounded up to 256 bytes.  Written in Python so fake tensors with symbolic n get the
+    same size; a CPU test holds it equal to the library's.
     """
     es = 4 if dtype == torch.float32 else 2
     m = n * k
     l_cap = _l_cap(m, e)
+    act = ((l_cap + s * (-(-n // 16) * 16)) * 2 * h * es
+           if save_act and save_act_supported(dtype, d, h) else 0)
     parts = (m * es, n * e * 4 if want_probs else 0, l_cap * 4, (l_cap // ALIGN_M) * 4,
-             (e + 1) * 4, 4, m * 4)
+             (e + 1) * 4, 4, m * 4, act)
     return sum(_al256(b) for b in parts)
 
 
@@ -711,13 +732,15 @@ def _plan(dt, activation, n, d, h, e, s, k, flags) -> _BlockPlan:
     return plan
 
 
-def _route_bits(dt, want_probs, normalize) -> int:
+def _route_bits(dt, want_probs, normalize, save_act=False) -> int:
     half = dt in (torch.bfloat16, torch.float16)
-    return _route_flags(want_probs, normalize) | (nat.ROUTE_LOGITS16 if half else 0)
+    return (_route_flags(want_probs, normalize) | (nat.ROUTE_LOGITS16 if half else 0)
+            | (nat.BLOCK_SAVE_ACT if save_act else 0))
 
 
 def _block_fwd_impl(x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out,
-                    top_k, want_probs, normalize, activation, aux_coef, logit_bias=None):
+                    top_k, want_probs, normalize, activation, aux_coef, logit_bias=None,
+                    save_act=False):
     """
     MoEBlock.forward's kernel path (moe.py:345-418): the router GEMM `x @ W_r` (torch,
     router.py:69), then one C call (nsmoe_block_fwd: router tail, dispatch, routed + shared
@@ -733,12 +756,15 @@ def _block_fwd_impl(x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in
     (which has no bias): a per-expert offset added to the GEMM's output, the sum rounded
     to the GEMM's dtype, before the router tail.  The skewed-routing workload uses it; its
     gradient is not computed.
+
+    With `save_act` the experts' pre-activations are kept in `saved` for the backward
+    (nsmoe.h NSMOE_BLOCK_SAVE_ACT), which then skips recomputing x W_in.
     """
     dev, dt = x.device, x.dtype
     n, d = x.shape
     e, h2 = W_r.shape[1], w_in.shape[2]
     s = 0 if w_sh_in is None else w_sh_in.shape[0]
-    flags = _route_bits(dt, want_probs, normalize)
+    flags = _route_bits(dt, want_probs, normalize, save_act)
     plan = _plan(dt, activation, n, d, h2 // 2, e, s, top_k, flags)
     bias = None
     if plan.fuse_route:
@@ -784,33 +810,34 @@ def block_fwd(x: Tensor, W_r: Tensor, w_in: Tensor, w_out: Tensor, w_sh_in: Opti
               w_sh_out: Optional[Tensor], b_in: Optional[Tensor], b_out: Optional[Tensor],
               b_sh_in: Optional[Tensor], b_sh_out: Optional[Tensor], top_k: int,
               want_probs: bool, normalize: bool, activation: str, aux_coef: float,
-              logit_bias: Optional[Tensor] = None
+              logit_bias: Optional[Tensor] = None, save_act: bool = False
               ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
     """The block's forward as a torch.library op (see _block_fwd_impl)."""
     return _block_fwd_impl(x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in,
                            b_sh_out, top_k, want_probs, normalize, activation, aux_coef,
-                           logit_bias)
+                           logit_bias, save_act)
 
 
 @block_fwd.register_fake
 def _(x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out, top_k,
-      want_probs, normalize, activation, aux_coef, logit_bias=None):
+      want_probs, normalize, activation, aux_coef, logit_bias=None, save_act=False):
     n, d = x.shape
     e = W_r.shape[1]
+    s = 0 if w_sh_in is None else w_sh_in.shape[0]
     half = x.dtype in (torch.bfloat16, torch.float16)
     return (x.new_empty((n, d)),
             x.new_empty((), dtype=torch.float32 if want_probs else x.dtype),
             x.new_empty((e,), dtype=torch.int32),
             x.new_empty((n, top_k), dtype=torch.int64),
             x.new_empty((n, e), dtype=x.dtype if half else torch.float32),
-            x.new_empty((block_saved_bytes(n, e, top_k, x.dtype, want_probs),),
-                        dtype=torch.uint8),
+            x.new_empty((block_saved_bytes(n, e, top_k, x.dtype, want_probs, save_act, d,
+                                           w_in.shape[2] // 2, s),), dtype=torch.uint8),
             x.new_empty((_packed_in_bytes(x, w_in, w_sh_in),), dtype=torch.uint8))
 
 
 def _block_bwd_impl(g_out, g_aux, x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in,
                     logits, saved, topk_idx, counts, w_in_packed, top_k, want_probs, normalize,
-                    activation, aux_coef, has_b_sh_out, need_dx, need_dW_r):
+                    activation, aux_coef, has_b_sh_out, need_dx, need_dW_r, save_act=False):
     """
     The block's backward in one C call (nsmoe_block_bwd: experts' backward, router tail's
     backward with the balance-loss gradient folded in, and for 16-bit types the router
@@ -825,7 +852,7 @@ def _block_bwd_impl(g_out, g_aux, x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, 
     e, h2 = W_r.shape[1], w_in.shape[2]
     s = 0 if w_sh_in is None else w_sh_in.shape[0]
     dev, dt = x.device, x.dtype
-    flags = _route_bits(dt, want_probs, normalize)
+    flags = _route_bits(dt, want_probs, normalize, save_act)
     half = bool(flags & nat.ROUTE_LOGITS16)
     plan = _plan(dt, activation, n, d, h2 // 2, e, s, top_k, flags)
     emp = lambda: x.new_empty(0)  # one per absent gradient: outputs may not alias
@@ -879,19 +906,20 @@ def block_bwd(g_out: Tensor, g_aux: Optional[Tensor], x: Tensor, W_r: Tensor, w_
               logits: Tensor, saved: Tensor, topk_idx: Tensor, counts: Tensor,
               w_in_packed: Tensor, top_k: int, want_probs: bool, normalize: bool,
               activation: str, aux_coef: float, has_b_sh_out: bool, need_dx: bool,
-              need_dW_r: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor,
-                                        Tensor, Tensor, Tensor]:
+              need_dW_r: bool, save_act: bool = False
+              ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor,
+                         Tensor]:
     """The block's backward as a torch.library op (see _block_bwd_impl)."""
     return _block_bwd_impl(g_out, g_aux, x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out,
                            b_sh_in, logits, saved, topk_idx, counts, w_in_packed, top_k,
                            want_probs, normalize, activation, aux_coef, has_b_sh_out, need_dx,
-                           need_dW_r)
+                           need_dW_r, save_act)
 
 
 @block_bwd.register_fake
 def _(g_out, g_aux, x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, logits,
       saved, topk_idx, counts, w_in_packed, top_k, want_probs, normalize, activation, aux_coef,
-      has_b_sh_out, need_dx, need_dW_r):
+      has_b_sh_out, need_dx, need_dW_r, save_act=False):
     s = 0 if w_sh_in is None else w_sh_in.shape[0]
     like = lambda t: torch.empty_like(t) if t is not None else x.new_empty(0)
     return (torch.empty_like(x), torch.empty_like(W_r), torch.empty_like(w_in),
@@ -901,7 +929,7 @@ def _(g_out, g_aux, x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in
 
 def _block_fwd_setup(ctx, inputs, output):
     (x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out, top_k,
-     want_probs, normalize, activation, aux_coef, logit_bias) = inputs
+     want_probs, normalize, activation, aux_coef, logit_bias, save_act) = inputs
     out, aux, counts, topk_idx, logits, saved, w_in_packed = output
     ctx.mark_non_differentiable(counts, topk_idx, logits, saved, w_in_packed)
     # Unused output gradients arrive as None instead of materialised zeros.
@@ -910,7 +938,8 @@ def _block_fwd_setup(ctx, inputs, output):
     opt = [t for t in (w_sh_in, w_sh_out, b_in, b_out, b_sh_in) if t is not None]
     ctx.save_for_backward(x, W_r, w_in, w_out, logits, saved, topk_idx, counts, w_in_packed,
                           *opt)
-    ctx.cfg = (top_k, want_probs, normalize, activation, aux_coef, b_sh_out is not None)
+    ctx.cfg = (top_k, want_probs, normalize, activation, aux_coef, b_sh_out is not None,
+               save_act)
 
 
 def _block_fwd_backward(ctx, g_out, g_aux, g_counts, g_idx, g_logits, g_saved, g_packed):
@@ -926,20 +955,20 @@ def _block_backward(ctx, g_out, g_aux, bwd):
     b_in = next(it) if has_b_in else None
     b_out = next(it) if has_b_out else None
     b_sh_in = next(it) if has_b_sh_in else None
-    top_k, want_probs, normalize, activation, aux_coef, has_b_sh_out = ctx.cfg
+    top_k, want_probs, normalize, activation, aux_coef, has_b_sh_out, save_act = ctx.cfg
     need = ctx.needs_input_grad
     if g_out is None:
         g_out = torch.zeros_like(x)
     (dx, dW_r, dw_in, dw_out, dw_sh_in, dw_sh_out, db_in, db_out, db_sh_in,
      db_sh_out) = bwd(g_out, g_aux, x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out,
                       b_sh_in, logits, saved, topk_idx, counts, w_in_packed, top_k, want_probs,
-                      normalize, activation, aux_coef, has_b_sh_out, need[0], need[1])
+                      normalize, activation, aux_coef, has_b_sh_out, need[0], need[1], save_act)
     opt_grad = lambda present, g: g if present else None
     return (dx if need[0] else None, dW_r if need[1] else None, dw_in, dw_out,
             opt_grad(has_sh, dw_sh_in), opt_grad(has_sh, dw_sh_out),
             opt_grad(has_b_in, db_in), opt_grad(has_b_out, db_out),
             opt_grad(has_b_sh_in, db_sh_in), opt_grad(has_b_sh_out, db_sh_out),
-            None, None, None, None, None, None)
+            None, None, None, None, None, None, None)
 
 
 block_fwd.register_autograd(_block_fwd_backward, setup_context=_block_fwd_setup)
@@ -973,9 +1002,14 @@ def block_forward(x, router_W, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh
     _check_activation(activation)
     cast = lambda t: None if t is None else t.to(x.dtype)
     op = block_fwd if torch.compiler.is_compiling() else _BlockEager.apply
+    # The pre-activations are saved only for a forward that autograd will run backward
+    # through (a checkpointed block's first, gradient-free forward does not save them).
+    params = (router_W, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out)
+    save_act = SAVE_ACT and torch.is_grad_enabled() and (
+        x.requires_grad or any(t is not None and t.requires_grad for t in params))
     out, aux, counts, topk_idx, logits, _, _ = op(
         x.contiguous(), cast(router_W).contiguous(), cast(w_in).contiguous(),
         cast(w_out).contiguous(), _c(cast(w_sh_in)), _c(cast(w_sh_out)), _c(cast(b_in)),
         _c(cast(b_out)), _c(cast(b_sh_in)), _c(cast(b_sh_out)), top_k, want_probs, normalize,
-        activation, float(aux_coef), logit_bias)
+        activation, float(aux_coef), logit_bias, save_act)
     return out, aux, counts, topk_idx, logits

@@ -43,7 +43,7 @@ def test_struct_layouts_match_the_header():
 
 
 def test_abi_version_and_alignment():
-    assert nat.lib().nsmoe_abi_version() == nat.ABI_VERSION == 4
+    assert nat.lib().nsmoe_abi_version() == nat.ABI_VERSION == 5
     assert nat.lib().nsmoe_align_m() == mk.ALIGN_M
 
 
@@ -147,24 +147,47 @@ def test_kernel_supported_raises_on_a_gpu_tensor_without_the_library(monkeypatch
     (8192, 76, 6, "bfloat16", True), (8192, 76, 6, "bfloat16", False), (1, 8, 2, "float32", True),
     (37, 76, 6, "float16", True), (32768, 76, 6, "bfloat16", False), (5, 1000, 8, "float32", False),
 ])
-def test_block_saved_layout_matches_the_python_mirror(n, e, k, dt, probs):
-    """The fake impl of nsmoe::block_fwd sizes `saved` in Python (symbolic shapes)."""
+@pytest.mark.parametrize("save_act", [False, True])
+@pytest.mark.parametrize("d,h,s", [(576, 128, 2), (64, 64, 0), (128, 64, 1), (192, 96, 2),
+                                   (512, 256, 2), (320, 128, 2), (576, 48, 2)])
+def test_block_saved_layout_matches_the_python_mirror(n, e, k, dt, probs, save_act, d, h, s):
+    """The fake impl of nsmoe::block_fwd sizes `saved` in Python (symbolic shapes),
+    including which shapes keep the experts' pre-activations."""
     import torch
     dtype = getattr(torch, dt)
-    a = nat.ExpertsArgs(dtype=mk._DT[dtype], activation=0, n_tokens=n, d_model=576,
-                        d_hidden=128, n_experts=e, n_shared=2, top_k=k, l_cap=0)
+    a = nat.ExpertsArgs(dtype=mk._DT[dtype], activation=0, n_tokens=n, d_model=d,
+                        d_hidden=h, n_experts=e, n_shared=s, top_k=k, l_cap=0)
     offs = (ctypes.c_size_t * nat.BLOCK_NSAVED)()
     total = ctypes.c_size_t()
-    flags = nat.ROUTE_PROBS if probs else 0
+    flags = (nat.ROUTE_PROBS if probs else 0) | (nat.BLOCK_SAVE_ACT if save_act else 0)
     assert nat.lib().nsmoe_block_saved_layout(a, flags, offs, ctypes.byref(total)) == 0
-    assert total.value == mk.block_saved_bytes(n, e, k, dtype, probs)
+    assert total.value == mk.block_saved_bytes(n, e, k, dtype, probs, save_act, d, h, s)
     assert list(offs) == sorted(offs) and offs[0] == 0
+    act = total.value - offs[nat.SAVED_ACT]
+    if save_act and mk.save_act_supported(dtype, d, h):
+        l_cap = mk._l_cap(n * k, e)
+        assert act == mk._al256((l_cap + s * (-(-n // 16) * 16)) * 2 * h * 2)
+    else:
+        assert act == 0
+
+
+def test_save_act_shapes():
+    """The register-tiled kernels' shapes: nanoSpeaker's block takes them; fp32, H above
+    128, d off the 64 grid and odd GEMM2 step counts do not."""
+    import torch
+    ok = mk.save_act_supported
+    assert ok(torch.bfloat16, 576, 128) and ok(torch.float16, 576, 128)
+    assert ok(torch.bfloat16, 128, 64) and ok(torch.bfloat16, 384, 96)
+    assert not ok(torch.float32, 576, 128)
+    assert not ok(torch.bfloat16, 576, 256) and not ok(torch.bfloat16, 576, 120)
+    assert not ok(torch.bfloat16, 544, 128) and not ok(torch.bfloat16, 64, 64)
+    assert not ok(torch.bfloat16, 192, 32)  # one pass x one k-step of H: odd
 
 
 def test_tuning_options_round_trip_and_reject_bad_values():
     lib = nat.lib()
-    for name, good, bad in (("single_stream", 1, 2), ("fwd_rows", 96, 80), ("bwd_rows", 48, 32),
-                            ("dx_rows", 64, 48), ("fwd_dist", 3, 4), ("bwd_dist", 2, 5),
+    for name, good, bad in (("single_stream", 1, 2), ("fwd_rows", 96, 80), ("bwd_rows", 96, 32),
+                            ("dx_rows", 64, 48), ("fwd_dist", 3, 4), ("bwd_dist", 4, 5),
                             ("dx_dist", 4, 1), ("xcd_run", 8, 2048)):
         assert nat.get_option(name) == 0
         nat.set_option(name, good)

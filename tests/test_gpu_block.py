@@ -130,8 +130,9 @@ def check_against_oracle(x, p, g, logits, idx, counts, out, aux, grads, train, b
     return ref
 
 
-def run_case(T, train, backward, *, logit_bias=None, **cfg):
-    """The drop-in MoEBlock, as a caller runs it (one op per direction on the GPU)."""
+def run_case(T, train, backward, *, logit_bias=None, collect=None, **cfg):
+    """The drop-in MoEBlock, as a caller runs it (one op per direction on the GPU).  The
+    GPU's output and gradients also go into `collect` when a dict is given."""
     m, p, x, g = build(T, **cfg)
     dt = x.dtype
     m = m.to(DEV).train(train)
@@ -165,6 +166,8 @@ def run_case(T, train, backward, *, logit_bias=None, **cfg):
             t = getattr(m, n)
             if t is not None:
                 grads[n] = t.grad.cpu()
+    if collect is not None:
+        collect.update(grads, out=out.detach().cpu())
     return check_against_oracle(x, p, g, logits, idx.cpu(), counts.cpu(),
                                 out.detach().cpu(), aux.detach().cpu(), grads, train,
                                 backward, k=m.top_k)
@@ -209,6 +212,28 @@ def test_prefill_layer_T32768_eval():
 def test_zero_router_sends_every_token_to_the_same_experts():
     ref = run_case(2048, train=True, backward=True, zero_router=True)
     assert int((ref.counts > 0).sum()) == 6 and int(ref.counts.max()) == 2048
+
+
+@pytest.mark.parametrize("cfg", [dict(S=2), dict(S=0, bias=True, dtype=torch.float16),
+                                 dict(d=128, E=12, d_ff=96, k=4, S=1)])
+def test_saved_pre_activations_and_recompute_agree(monkeypatch, cfg):
+    """The default backward reads the forward's saved pre-activations x W_in + b_in
+    (rounded to the block's dtype, as the reference's backward rounds its recomputed
+    ones); the alternative recomputes them in fp32.  Both meet the bar against the oracle
+    and agree with each other to the same bar; the saved ones make `saved` larger."""
+    runs = {}
+    for save in (True, False):
+        monkeypatch.setattr(mk, "SAVE_ACT", save)
+        runs[save] = {}
+        run_case(1024, train=True, backward=True, collect=runs[save], **cfg)
+    dt = cfg.get("dtype", torch.bfloat16)
+    for name, ref in runs[False].items():
+        close(f"saved vs recomputed: {name}", runs[True][name], ref.float(), dt)
+    d, h = cfg.get("d", 576), cfg.get("d_ff", 192) * 2 // 3
+    assert mk.save_act_supported(dt, d, h)
+    e, k, S = cfg.get("E", 76), cfg.get("k", 6), cfg.get("S", 2)
+    assert (mk.block_saved_bytes(1024, e, k, dt, True, True, d, h, S)
+            > mk.block_saved_bytes(1024, e, k, dt, True, False, d, h, S))
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
