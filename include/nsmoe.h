@@ -47,7 +47,7 @@ int32_t nsmoe_abi_version(void);
  * the library records a HIP event pair on the launch stream around each launch of its
  * main kernels ("pack", "route_fwd", "dispatch", "expert_fwd", "combine",
  * "expert_bwd", "expert_dx", "dw" (or "dw_in" and "dw_out" where they run apart),
- * "combine_dx", "router_dw") until
+ * "combine_dx", "router_dw", "norm_bwd") until
  * `capacity` pairs are used.
  * nsmoe_timing_read waits for the recorded events of one kernel and returns their
  * summed duration.  capacity 0 disables timing and frees the events. */
@@ -296,7 +296,27 @@ int nsmoe_experts_bwd(const nsmoe_experts_args* args, const int32_t* inv,
  *   w_router NULL: grads->dx holds the experts' part only, grad_logits [T, E] receives
  *     d(logits) as nsmoe_route_bwd writes it, grad_w_router is unused; workspace
  *     nsmoe_block_bwd_workspace_size(args, route_flags, 0).
+ *
+ * The RMSNorm and residual around the block (`norm` non-NULL, NSMOE_BLOCK_NORM in
+ * route_flags; both or neither): the FFN half of the reference's Block.forward,
+ *   out = x + MoEBlock(RMSNorm(x))          (src/model/nanospeaker.py:169, ln.py:30-36)
+ * with args->x the residual stream.  RMSNorm is F.rms_norm's arithmetic: fp32
+ * rstd = 1 / sqrt(mean(x^2) + eps), xn = (x rstd) weight rounded once to the dtype.  The
+ * router kernel normalises the rows as it loads them and keeps xn and rstd in `saved`
+ * (the experts and the backward read xn); the combine adds x to the block's output,
+ * each rounded to the dtype as the separate ops round them.  The backward's grads->dx is
+ * the gradient of x through both paths, and norm->grad_weight [d] receives the gain's
+ * gradient.  Needs the fused router (w_router given, shapes as above).  Callers without
+ * the norm pass NULL.
  */
+typedef struct nsmoe_block_norm {
+  const void* weight;  /* [d] RMSNorm gain, args dtype */
+  void* grad_weight;   /* [d] backward output, args dtype */
+  float eps;
+  int32_t reserved;
+} nsmoe_block_norm;
+
+#define NSMOE_BLOCK_NORM 32
 #define NSMOE_BLOCK_PACK 8
 #define NSMOE_BLOCK_SAVE_ACT 16
 
@@ -308,18 +328,22 @@ int nsmoe_experts_bwd(const nsmoe_experts_args* args, const int32_t* inv,
 #define NSMOE_SAVED_N_POST_PAD 5
 #define NSMOE_SAVED_INV 6
 #define NSMOE_SAVED_ACT 7
-#define NSMOE_BLOCK_NSAVED 8
+#define NSMOE_SAVED_XN 8   /* NSMOE_BLOCK_NORM: [T, d] normalised input (args dtype) */
+#define NSMOE_SAVED_RSTD 9 /* NSMOE_BLOCK_NORM: [T] fp32 */
+#define NSMOE_BLOCK_NSAVED 10
 
 int nsmoe_block_saved_layout(const nsmoe_experts_args* args, int32_t route_flags,
                              size_t* offsets /* [NSMOE_BLOCK_NSAVED] */, size_t* total_bytes);
 size_t nsmoe_block_fwd_workspace_size(const nsmoe_experts_args* args, int32_t route_flags);
-int nsmoe_block_fwd(const nsmoe_experts_args* args, const void* w_router,
+int nsmoe_block_fwd(const nsmoe_experts_args* args, const nsmoe_block_norm* norm,
+                    const void* w_router,
                     const float* logit_bias, void* logits, int32_t route_flags, float aux_coef,
                     void* saved, int64_t* topk_idx, int32_t* counts, void* out, float* aux,
                     void* workspace, size_t workspace_bytes, void* stream);
 size_t nsmoe_block_bwd_workspace_size(const nsmoe_experts_args* args, int32_t route_flags,
                                       int32_t fuse_router);
-int nsmoe_block_bwd(const nsmoe_experts_args* args, const void* logits, int32_t route_flags,
+int nsmoe_block_bwd(const nsmoe_experts_args* args, const nsmoe_block_norm* norm,
+                    const void* logits, int32_t route_flags,
                     float aux_coef, const void* saved, const int64_t* topk_idx,
                     const int32_t* counts, const void* grad_out, const float* grad_aux,
                     const nsmoe_experts_grads* grads, const void* w_router,

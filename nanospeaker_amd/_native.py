@@ -13,8 +13,9 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libnsmoe.so"
 
 BF16, F16, F32 = 0, 1, 2
-ROUTE_PROBS, ROUTE_NORMALIZE, ROUTE_LOGITS16, BLOCK_PACK, BLOCK_SAVE_ACT = 1, 2, 4, 8, 16
-ABI_VERSION = 5
+ROUTE_PROBS, ROUTE_NORMALIZE, ROUTE_LOGITS16 = 1, 2, 4
+BLOCK_PACK, BLOCK_SAVE_ACT, BLOCK_NORM = 8, 16, 32
+ABI_VERSION = 6
 
 # Every symbol include/nsmoe.h declares, with (restype, argtypes).
 _vp, _i32, _i64, _sz = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t
@@ -40,6 +41,13 @@ class ExpertsGrads(ctypes.Structure):
     _fields_ = [(n, _vp) for n in (
         "dx", "dw_in", "dw_out", "dw_sh_in", "dw_sh_out", "dtopk_w",
         "db_in", "db_out", "db_sh_in", "db_sh_out")]
+
+
+class BlockNorm(ctypes.Structure):
+    """Mirror of `nsmoe_block_norm`."""
+
+    _fields_ = [("weight", _vp), ("grad_weight", _vp), ("eps", ctypes.c_float),
+                ("reserved", _i32)]
 
 
 SIGNATURES = {
@@ -74,16 +82,19 @@ SIGNATURES = {
     "nsmoe_block_saved_layout": (ctypes.c_int, [ctypes.POINTER(ExpertsArgs), _i32,
                                                 ctypes.POINTER(_sz), ctypes.POINTER(_sz)]),
     "nsmoe_block_fwd_workspace_size": (_sz, [ctypes.POINTER(ExpertsArgs), _i32]),
-    "nsmoe_block_fwd": (ctypes.c_int, [ctypes.POINTER(ExpertsArgs), _vp, _vp, _vp, _i32,
-                                       ctypes.c_float, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "nsmoe_block_fwd": (ctypes.c_int, [ctypes.POINTER(ExpertsArgs), ctypes.POINTER(BlockNorm),
+                                       _vp, _vp, _vp, _i32, ctypes.c_float, _vp, _vp, _vp, _vp,
+                                       _vp, _vp, _sz, _vp]),
     "nsmoe_block_bwd_workspace_size": (_sz, [ctypes.POINTER(ExpertsArgs), _i32, _i32]),
-    "nsmoe_block_bwd": (ctypes.c_int, [ctypes.POINTER(ExpertsArgs), _vp, _i32, ctypes.c_float,
-                                       _vp, _vp, _vp, _vp, _vp, ctypes.POINTER(ExpertsGrads),
-                                       _vp, _vp, _vp, _vp, _sz, _vp]),
+    "nsmoe_block_bwd": (ctypes.c_int, [ctypes.POINTER(ExpertsArgs), ctypes.POINTER(BlockNorm),
+                                       _vp, _i32, ctypes.c_float, _vp, _vp, _vp, _vp, _vp,
+                                       ctypes.POINTER(ExpertsGrads), _vp, _vp, _vp, _vp, _sz,
+                                       _vp]),
 }
 
 # Parts of the block's `saved` buffer (NSMOE_SAVED_* in nsmoe.h).
-SAVED_TOPK_W, SAVED_PROBS, SAVED_INV, SAVED_ACT, BLOCK_NSAVED = 0, 1, 6, 7, 8
+SAVED_TOPK_W, SAVED_PROBS, SAVED_INV, SAVED_ACT, SAVED_XN, SAVED_RSTD = 0, 1, 6, 7, 8, 9
+BLOCK_NSAVED = 10
 
 
 class NativeLibraryError(RuntimeError):

@@ -17,6 +17,7 @@
 #include <string.h>
 
 #include "experts_common.h"
+#include "norm.h"
 #include "pack.h"
 #include "router_fused.h"
 #include "router_grad.h"
@@ -39,6 +40,8 @@ static BlockLayout block_layout(const nsmoe_experts_args* a, int32_t flags) {
   nsmoe_experts_args b = *a;
   b.l_cap = (int64_t)l_cap;
   const size_t act = (flags & NSMOE_BLOCK_SAVE_ACT) ? experts_save_act_bytes(&b) : 0;
+  const bool norm = flags & NSMOE_BLOCK_NORM;
+  const size_t d = (size_t)a->d_model;
   const size_t sizes[NSMOE_BLOCK_NSAVED] = {
       T * k * es,                                   // topk_w
       (flags & NSMOE_ROUTE_PROBS) ? T * E * 4 : 0,  // probs
@@ -48,6 +51,8 @@ static BlockLayout block_layout(const nsmoe_experts_args* a, int32_t flags) {
       4,                                            // n_post_pad
       T * k * 4,                                    // inv
       act,                                          // pre-activations (SAVE_ACT)
+      norm ? T * d * es : 0,                        // normalised input (NORM)
+      norm ? T * 4 : 0,                             // rstd (NORM)
   };
   BlockLayout L;
   size_t o = 0;
@@ -116,7 +121,8 @@ extern "C" size_t nsmoe_block_fwd_workspace_size(const nsmoe_experts_args* a,
   return fwd_ws_parts(&b, &dsp, &exp, &rt);
 }
 
-extern "C" int nsmoe_block_fwd(const nsmoe_experts_args* a, const void* w_router,
+extern "C" int nsmoe_block_fwd(const nsmoe_experts_args* a, const nsmoe_block_norm* norm,
+                               const void* w_router,
                                const float* logit_bias, void* logits, int32_t route_flags,
                                float aux_coef, void* saved, int64_t* topk_idx, int32_t* counts,
                                void* out, float* aux, void* workspace, size_t workspace_bytes,
@@ -125,6 +131,10 @@ extern "C" int nsmoe_block_fwd(const nsmoe_experts_args* a, const void* w_router
   NSMOE_REQUIRE(!(route_flags & NSMOE_ROUTE_PROBS) || aux, "block_fwd: NULL aux");
   NSMOE_REQUIRE(a->w_in_packed && a->w_out_packed, "block_fwd: NULL packed weights");
   NSMOE_REQUIRE(w_router || !logit_bias, "block_fwd: logit_bias needs the fused router");
+  NSMOE_REQUIRE(!norm == !(route_flags & NSMOE_BLOCK_NORM),
+                "block_fwd: pass the norm together with NSMOE_BLOCK_NORM");
+  NSMOE_REQUIRE(!norm || (norm->weight && w_router), "block_fwd: the norm needs its weight "
+                "and the fused router (w_router)");
   NSMOE_REQUIRE(!w_router || router_fused_supported(a->dtype, (int)a->d_model, a->n_experts,
                                                     a->top_k),
                 "block_fwd: the fused router takes bf16/fp16, d %% 32 == 0, d <= 576, "
@@ -135,6 +145,8 @@ extern "C" int nsmoe_block_fwd(const nsmoe_experts_args* a, const void* w_router
   const BlockLayout L = block_layout(a, route_flags);
   char* sv = (char*)saved;
   nsmoe_experts_args b = with_routing(a, L, sv, counts);
+  // With the norm, everything past the router reads the normalised rows it stores.
+  if (norm) b.x = sv + L.off[NSMOE_SAVED_XN];
   size_t dsp, exp, rtb;
   const size_t need = fwd_ws_parts(&b, &dsp, &exp, &rtb);
   if (!workspace || workspace_bytes < need) {
@@ -174,6 +186,12 @@ extern "C" int nsmoe_block_fwd(const nsmoe_experts_args* a, const void* w_router
     r.topk_w = (void*)b.topk_w;
     r.topk_idx = topk_idx;
     if (!probs) r.colsum = nullptr;
+    if (norm) {
+      r.norm_w = norm->weight;
+      r.norm_eps = norm->eps;
+      r.xn = sv + L.off[NSMOE_SAVED_XN];
+      r.rstd = (float*)(sv + L.off[NSMOE_SAVED_RSTD]);
+    }
     if (rc == NSMOE_OK) rc = router_fused_launch(r, a->dtype, s);
     BalanceArgs fold{r.colsum, router_fused_chunks(T), T, aux_coef, aux};
     if (rc == NSMOE_OK)
@@ -197,7 +215,8 @@ extern "C" int nsmoe_block_fwd(const nsmoe_experts_args* a, const void* w_router
   const int jrc = side_join(s, s_pack, kSideSlotPack);  // joined on every path
   NSMOE_TRY(rc);
   NSMOE_TRY(jrc);
-  return experts_fwd_launch(&b, inv, out, ws + dsp, exp, act_part(L, sv, route_flags), s);
+  return experts_fwd_launch(&b, inv, out, ws + dsp, exp, act_part(L, sv, route_flags), s,
+                            norm ? a->x : nullptr);
 }
 
 namespace nsmoe {
@@ -205,10 +224,10 @@ namespace nsmoe {
 // Backward workspace: the gate gradient (T x k), the expert backward's workspace, and on
 // the fused router path d(logits) at pitch ep plus the router dW partials.
 struct BwdWs {
-  size_t tw, exp, gl, part, wpk, total;
+  size_t tw, exp, gl, part, wpk, dxn, npart, total;
 };
 
-static BwdWs bwd_ws(const nsmoe_experts_args* b, bool router) {
+static BwdWs bwd_ws(const nsmoe_experts_args* b, bool router, bool norm) {
   const size_t es = b->dtype == DT_F32 ? 4 : 2;
   BwdWs w;
   w.tw = 0;
@@ -223,6 +242,13 @@ static BwdWs bwd_ws(const nsmoe_experts_args* b, bool router) {
     w.wpk = w.part + al256(router_dw_partial_bytes(b->n_tokens, b->d_model, b->n_experts));
     w.total = w.wpk + al256(router_w_pack_bytes((int)b->d_model, (ep + 31) / 32));
   }
+  // With the norm: the block's input gradient before the norm's backward, and the gain's
+  // per-workgroup column sums.
+  w.dxn = w.npart = w.total;
+  if (norm) {
+    w.npart = w.dxn + al256((size_t)b->n_tokens * b->d_model * es);
+    w.total = w.npart + al256(norm_bwd_partial_bytes(b->n_tokens, (int)b->d_model));
+  }
   return w;
 }
 
@@ -234,7 +260,7 @@ int block_bwd_router(const nsmoe_experts_args* a, const nsmoe_experts_args& b,
                      const void* logits, int32_t route_flags, float aux_coef,
                      const float* grad_aux, const nsmoe_experts_grads* grads,
                      const void* w_router, void* grad_w_router, void* grad_logits, char* ws,
-                     const BwdWs& W, const int32_t* inv, bool fuse, hipStream_t s);
+                     const BwdWs& W, const int32_t* inv, bool fuse, void* dx, hipStream_t s);
 }  // namespace nsmoe
 
 extern "C" size_t nsmoe_block_bwd_workspace_size(const nsmoe_experts_args* a,
@@ -242,11 +268,11 @@ extern "C" size_t nsmoe_block_bwd_workspace_size(const nsmoe_experts_args* a,
   if (!a) return 0;
   nsmoe_experts_args b = *a;
   b.l_cap = nsmoe_dispatch_l_cap(a->n_tokens * a->top_k, a->n_experts);
-  (void)route_flags;
-  return bwd_ws(&b, fuse_router != 0).total;
+  return bwd_ws(&b, fuse_router != 0, route_flags & NSMOE_BLOCK_NORM).total;
 }
 
-extern "C" int nsmoe_block_bwd(const nsmoe_experts_args* a, const void* logits,
+extern "C" int nsmoe_block_bwd(const nsmoe_experts_args* a, const nsmoe_block_norm* norm,
+                               const void* logits,
                                int32_t route_flags, float aux_coef, const void* saved,
                                const int64_t* topk_idx, const int32_t* counts,
                                const void* grad_out, const float* grad_aux,
@@ -262,11 +288,16 @@ extern "C" int nsmoe_block_bwd(const nsmoe_experts_args* a, const void* logits,
   NSMOE_REQUIRE(!fuse || router_grad_supported(a->dtype, (int)a->d_model, a->n_experts),
                 "block_bwd: the fused router backward takes bf16/fp16, d %% 16 == 0, "
                 "E %% 4 == 0 and E <= 128 (d %d, E %d)", (int)a->d_model, a->n_experts);
+  NSMOE_REQUIRE(!norm == !(route_flags & NSMOE_BLOCK_NORM),
+                "block_bwd: pass the norm together with NSMOE_BLOCK_NORM");
+  NSMOE_REQUIRE(!norm || (norm->weight && norm->grad_weight && fuse),
+                "block_bwd: the norm needs its weight, grad_weight and the fused router");
   if (a->n_tokens == 0) return NSMOE_OK;
   const BlockLayout L = block_layout(a, route_flags);
   char* sv = (char*)saved;
   nsmoe_experts_args b = with_routing(a, L, sv, counts);
-  const BwdWs W = bwd_ws(&b, fuse);
+  if (norm) b.x = sv + L.off[NSMOE_SAVED_XN];
+  const BwdWs W = bwd_ws(&b, fuse, norm != nullptr);
   if (!workspace || workspace_bytes < W.total) {
     set_error("block_bwd: workspace %zu B < %zu B", workspace_bytes, W.total);
     return NSMOE_EWORKSPACE;
@@ -280,8 +311,26 @@ extern "C" int nsmoe_block_bwd(const nsmoe_experts_args* a, const void* logits,
   hipStream_t s_dw = s;
   NSMOE_TRY(experts_bwd_launch(&b, inv, grad_out, &g, ws + W.exp, W.gl - W.exp, !fuse, s, &s_dw,
                                act_part(L, sv, route_flags)));
-  const int rc = block_bwd_router(a, b, L, sv, topk_idx, logits, route_flags, aux_coef, grad_aux, grads,
-                                  w_router, grad_w_router, grad_logits, ws, W, inv, fuse, s);
+  // With the norm the combine's dx is the normalised input's gradient: it goes to the
+  // workspace, and the norm's backward turns it into grads->dx.
+  void* dxn = norm ? (void*)(ws + W.dxn) : grads->dx;
+  int rc = block_bwd_router(a, b, L, sv, topk_idx, logits, route_flags, aux_coef, grad_aux,
+                            grads, w_router, grad_w_router, grad_logits, ws, W, inv, fuse, dxn,
+                            s);
+  if (rc == NSMOE_OK && norm) {
+    NormBwdArgs n;
+    n.x = a->x;
+    n.rstd = (const float*)(sv + L.off[NSMOE_SAVED_RSTD]);
+    n.w = norm->weight;
+    n.dxn = dxn;
+    n.g = grad_out;
+    n.dx = grads->dx;
+    n.partial = (float*)(ws + W.npart);
+    n.dw = norm->grad_weight;
+    n.T = a->n_tokens;
+    n.d = (int)a->d_model;
+    rc = norm_bwd_launch(a->dtype, n, s);
+  }
   const int jrc = side_join(s, s_dw, kSideSlotDw);
   NSMOE_TRY(rc);
   return jrc;
@@ -296,7 +345,7 @@ int block_bwd_router(const nsmoe_experts_args* a, const nsmoe_experts_args& b,
                      const void* logits, int32_t route_flags, float aux_coef,
                      const float* grad_aux, const nsmoe_experts_grads* grads,
                      const void* w_router, void* grad_w_router, void* grad_logits, char* ws,
-                     const BwdWs& W, const int32_t* inv, bool fuse, hipStream_t s) {
+                     const BwdWs& W, const int32_t* inv, bool fuse, void* dx, hipStream_t s) {
   const bool probs = route_flags & NSMOE_ROUTE_PROBS;
   const void* src = probs ? (const void*)(sv + L.off[NSMOE_SAVED_PROBS]) : logits;
   NSMOE_REQUIRE(src, "block_bwd: NULL logits (eval branch)");
@@ -315,7 +364,7 @@ int block_bwd_router(const nsmoe_experts_args* a, const nsmoe_experts_args& b,
   c.inv = inv;
   c.glogits = gl;
   c.w = ws + W.wpk;
-  c.dx = grads->dx;
+  c.dx = dx;
   c.T = a->n_tokens;
   c.l_cap = b.l_cap;
   c.d = (int)a->d_model;
@@ -325,7 +374,7 @@ int block_bwd_router(const nsmoe_experts_args* a, const nsmoe_experts_args& b,
   c.ep = ldg;
   NSMOE_TRY(combine_dx_launch(a->dtype, c, s));
   RouterDwArgs r;
-  r.x = a->x;
+  r.x = b.x;
   r.glogits = gl;
   r.partial = (float*)(ws + W.part);
   r.dw = grad_w_router;

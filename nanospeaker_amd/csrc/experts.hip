@@ -199,16 +199,29 @@ __global__ void __launch_bounds__(NT) expert_fwd_kernel(ExpParams p) {
 
 // ============================ combine ====================================================
 // out[t] = sum_j rows[inv[t * k + j]] + sum_s rows[l_cap + s * T + t], fp32 accumulation
-// in the order routed j = 0 .. k - 1, then shared s = 0 .. S - 1.
+// in the order routed j = 0 .. k - 1, then shared s = 0 .. S - 1.  With `resid` the sum,
+// rounded to the dtype, is added to resid[t] and rounded again: the block output plus the
+// residual stream, as `x + ffn(norm(x))` computes it (nanospeaker.py:169).
 constexpr int COMBINE_KMAX = 8;  // top_k and shared-expert counts of the gather fast path
 constexpr int COMBINE_SMAX = 2;
 template <int DT>
 __global__ void __launch_bounds__(NT)
 combine_kernel(const typename Elem<DT>::T* __restrict__ rows, const int32_t* __restrict__ inv,
                int64_t ntok, int d, int k, int S, int64_t l_cap,
-               typename Elem<DT>::T* __restrict__ out, int fast) {
+               typename Elem<DT>::T* __restrict__ out, int fast,
+               const typename Elem<DT>::T* __restrict__ resid) {
   using G = Geo<DT>;
   using TT = typename G::T;
+  // The rounded block output plus the residual, rounded again.
+  auto plus_resid = [&](TT (&o)[G::VE], int64_t off) __attribute__((always_inline)) {
+    if (!resid) return;
+    u32x4 rv = *(const u32x4*)(resid + off);
+    TT r[G::VE];
+    __builtin_memcpy(r, &rv, 16);
+#pragma unroll
+    for (int e = 0; e < G::VE; ++e)
+      o[e] = Elem<DT>::from_f(Elem<DT>::to_f(r[e]) + Elem<DT>::to_f(o[e]));
+  };
   if (fast && k <= COMBINE_KMAX && S <= COMBINE_SMAX && ntok * (d / G::VE) < INT32_MAX) {
     // Every slot index is loaded first, then every row chunk: all of a thread's loads
     // are in flight together instead of one dependent pair per row.
@@ -244,6 +257,7 @@ combine_kernel(const typename Elem<DT>::T* __restrict__ rows, const int32_t* __r
       TT o[G::VE];
 #pragma unroll
       for (int e = 0; e < G::VE; ++e) o[e] = Elem<DT>::from_f(acc[e]);
+      plus_resid(o, (int64_t)t * d + c);
       u32x4 ov;
       __builtin_memcpy(&ov, o, 16);
       *(u32x4*)(out + (int64_t)t * d + c) = ov;
@@ -276,6 +290,7 @@ combine_kernel(const typename Elem<DT>::T* __restrict__ rows, const int32_t* __r
       TT o[G::VE];
 #pragma unroll
       for (int e = 0; e < G::VE; ++e) o[e] = Elem<DT>::from_f(acc[e]);
+      plus_resid(o, t * d + c);
       u32x4 ov;
       __builtin_memcpy(&ov, o, 16);
       *(u32x4*)(out + t * d + c) = ov;
@@ -292,7 +307,9 @@ combine_kernel(const typename Elem<DT>::T* __restrict__ rows, const int32_t* __r
       }
       for (int s = 0; s < S; ++s)
         acc += Elem<DT>::to_f(rows[(l_cap + (int64_t)s * ntok + t) * d + c]);
-      out[t * d + c] = Elem<DT>::from_f(acc);
+      TT o = Elem<DT>::from_f(acc);
+      if (resid) o = Elem<DT>::from_f(Elem<DT>::to_f(resid[t * d + c]) + Elem<DT>::to_f(o));
+      out[t * d + c] = o;
     }
   }
 }
@@ -1022,7 +1039,8 @@ static int launch_fwd_tiles(const ExpParams& p, int nbw, int64_t grid, hipStream
 
 template <int DT>
 static int launch_combine(const void* rows, const int32_t* inv, int64_t T, int d, int k, int S,
-                          int64_t l_cap, void* out, bool fast, hipStream_t s) {
+                          int64_t l_cap, void* out, bool fast, hipStream_t s,
+                          const void* resid = nullptr) {
   using TT = typename Elem<DT>::T;
   if (T <= 0) return NSMOE_OK;
   const int ve = 16 / (int)sizeof(TT);
@@ -1031,7 +1049,8 @@ static int launch_combine(const void* rows, const int32_t* inv, int64_t T, int d
   if (blocks > 65535) blocks = 65535;
   KernelTimer timer("combine", s);
   combine_kernel<DT><<<(unsigned)blocks, NT, 0, s>>>((const TT*)rows, inv, T, d, k, S, l_cap,
-                                                      (TT*)out, fast ? 1 : 0);
+                                                      (TT*)out, fast ? 1 : 0,
+                                                      (const TT*)resid);
   timer.stop();
   return check_launch("combine_kernel");
 }
@@ -1049,16 +1068,16 @@ static bool save_act_shape(const nsmoe_experts_args* a) {
 
 template <int DT>
 static int experts_fwd_impl(const nsmoe_experts_args* a, const int32_t* inv, void* out, void* ws,
-                            void* act_out, hipStream_t s) {
+                            void* act_out, const void* resid, hipStream_t s) {
   ExpParams p = make_params(a);
   p.y = ws;
   // Saved only where the forward kernel that writes them runs (which needs p.fast); the
   // backward's decision (experts_bwd_impl) is the same function of the same arguments.
   p.a1_out = act_out && p.fast && save_act_shape(a) ? act_out : nullptr;
-  const bool fast = p.fast && aligned16(out);
+  const bool fast = p.fast && aligned16(out) && aligned16(resid);
   NSMOE_TRY(launch_fwd_tiles<DT>(p, nbw_for(a), fwd_grid(a), s));
   return launch_combine<DT>(ws, inv, a->n_tokens, a->d_model, a->top_k, a->n_shared, a->l_cap,
-                            out, fast, s);
+                            out, fast, s, resid);
 }
 
 struct BwdLayout {
@@ -1236,7 +1255,8 @@ size_t experts_save_act_bytes(const nsmoe_experts_args* a) {
 }
 
 int experts_fwd_launch(const nsmoe_experts_args* a, const int32_t* inv, void* out,
-                       void* workspace, size_t workspace_bytes, void* act_out, hipStream_t s) {
+                       void* workspace, size_t workspace_bytes, void* act_out, hipStream_t s,
+                       const void* resid) {
   NSMOE_TRY(validate(a));
   if (a->n_tokens == 0) return NSMOE_OK;
   NSMOE_REQUIRE(a->x && a->w_in && a->w_out && a->topk_w && a->sorted_ids && a->pad_offsets &&
@@ -1249,9 +1269,9 @@ int experts_fwd_launch(const nsmoe_experts_args* a, const int32_t* inv, void* ou
     return NSMOE_EWORKSPACE;
   }
   switch (a->dtype) {
-    case DT_BF16: return experts_fwd_impl<DT_BF16>(a, inv, out, workspace, act_out, s);
-    case DT_F16: return experts_fwd_impl<DT_F16>(a, inv, out, workspace, act_out, s);
-    default: return experts_fwd_impl<DT_F32>(a, inv, out, workspace, act_out, s);
+    case DT_BF16: return experts_fwd_impl<DT_BF16>(a, inv, out, workspace, act_out, resid, s);
+    case DT_F16: return experts_fwd_impl<DT_F16>(a, inv, out, workspace, act_out, resid, s);
+    default: return experts_fwd_impl<DT_F32>(a, inv, out, workspace, act_out, resid, s);
   }
 }
 

@@ -168,12 +168,13 @@ int experts_bwd_launch(const ::nsmoe_experts_args* a, const int32_t* inv, const 
                        size_t workspace_bytes, bool combine, hipStream_t stream,
                        hipStream_t* side_out, const void* act_in = nullptr);
 size_t experts_bwd_dxrows_offset(const ::nsmoe_experts_args* a);
-// nsmoe_experts_fwd that also writes the pre-activations a1 = x W_in + b_in (rows of
-// [gate | up], in the row space of the dispatch plus the shared experts' rows) to act_out
-// when experts_save_act_bytes(a) > 0; the backward then reads them instead of recomputing.
+// nsmoe_experts_fwd that also writes the pre-activations a1 = x W_in + b_in (act_block's
+// layout) to act_out when experts_save_act_bytes(a) > 0 -- the backward then reads them
+// instead of recomputing -- and with resid [T, d] non-NULL returns resid + the block
+// output (each rounded to the dtype) in out.
 int experts_fwd_launch(const ::nsmoe_experts_args* a, const int32_t* inv, void* out,
                        void* workspace, size_t workspace_bytes, void* act_out,
-                       hipStream_t stream);
+                       hipStream_t stream, const void* resid = nullptr);
 // Bytes of the saved pre-activations for this shape (a->l_cap set), 0 where the kernels
 // that write and read them do not apply (16-bit types, d % 64 == 0, H % 16 == 0, H <= 128
 // and the step-count parities of the register-tiled forward and backward).

@@ -1,0 +1,144 @@
+// The RMSNorm in front of the block and the residual around it, backward (16-bit types).
+//
+// Reference: Block.forward's FFN half, x + ffn(norm_ffn(x)) (src/model/nanospeaker.py:169),
+// with norm_ffn an RMSNorm (src/model/ln.py:30-36, F.rms_norm).  Its forward is fused into
+// the block's other kernels: the router kernel normalises the rows it loads for the
+// router GEMM and stores them for the experts (router.hip), and the combine adds the
+// residual (experts.hip).  The backward, given the block's input gradient dxn (the
+// combine of the expert dX rows and the router term, rounded to the dtype):
+//
+//   norm_bwd_kernel     per token row, F.rms_norm's backward in fp32,
+//                         xh = x rstd,  gxh = dxn w,  s = sum_c xh gxh,
+//                         dx_norm = (gxh - (xh / d) s) rstd      (rounded to the dtype)
+//                       plus the residual's gradient: dx = g + dx_norm (rounded again), and
+//                       this workgroup's fp32 column sums of dxn xh for the gain's gradient;
+//   norm_dw_reduce      those partial sums added in workgroup order -> dw (the dtype).
+#include "gemm_core.h"
+#include "nsmoe_capi_internal.h"
+#include "norm.h"
+
+namespace nsmoe {
+
+constexpr int NB_THREADS = 256;
+constexpr int NB_MAXU = NORM_MAX_D / 8 / 64;  // 16-byte chunks per lane of a row
+
+template <int DT>
+__global__ void __launch_bounds__(NB_THREADS) norm_bwd_kernel(NormBwdArgs a) {
+  using ET = typename Elem<DT>::T;
+  __shared__ float s_part[NB_THREADS / 64][NORM_MAX_D];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int d = a.d, nch = d / 8;
+  const float inv_d = 1.0f / (float)d;
+  const int64_t r0 = (int64_t)blockIdx.x * NORM_ROWS;
+  const int64_t r1 = min(r0 + NORM_ROWS, a.T);
+  // The gain of this lane's chunks, and its column sums of dxn xh.
+  float w[NB_MAXU][8], dw[NB_MAXU][8];
+#pragma unroll
+  for (int u = 0; u < NB_MAXU; ++u) {
+    const int c = lane + 64 * u;
+    u32x4 wv = u32x4{0u, 0u, 0u, 0u};
+    if (c < nch) wv = *(const u32x4*)((const ET*)a.w + 8 * c);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      w[u][e] = unpack2<DT>(wv[e / 2], e & 1);
+      dw[u][e] = 0.0f;
+    }
+  }
+  for (int64_t t = r0 + wave; t < r1; t += NB_THREADS / 64) {  // uniform per wave
+    const float rstd = a.rstd[t];
+    float xh[NB_MAXU][8], gxh[NB_MAXU][8], g[NB_MAXU][8];
+    float dot = 0.0f;
+#pragma unroll
+    for (int u = 0; u < NB_MAXU; ++u) {
+      const int c = lane + 64 * u;
+      u32x4 xv = u32x4{0u, 0u, 0u, 0u}, dv = xv, gv = xv;
+      if (c < nch) {
+        xv = *(const u32x4*)((const ET*)a.x + t * d + 8 * c);
+        dv = *(const u32x4*)((const ET*)a.dxn + t * d + 8 * c);
+        gv = *(const u32x4*)((const ET*)a.g + t * d + 8 * c);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float dn = unpack2<DT>(dv[e / 2], e & 1);
+        xh[u][e] = unpack2<DT>(xv[e / 2], e & 1) * rstd;
+        gxh[u][e] = dn * w[u][e];
+        g[u][e] = unpack2<DT>(gv[e / 2], e & 1);
+        dot += xh[u][e] * gxh[u][e];
+        dw[u][e] += dn * xh[u][e];
+      }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) dot += __shfl_xor(dot, o, 64);
+#pragma unroll
+    for (int u = 0; u < NB_MAXU; ++u) {
+      const int c = lane + 64 * u;
+      if (c >= nch) continue;
+      u32x4 ov;
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        float v[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const float dnorm = Elem<DT>::to_f(
+              Elem<DT>::from_f((gxh[u][e + h] - (xh[u][e + h] * inv_d) * dot) * rstd));
+          v[h] = g[u][e + h] + dnorm;
+        }
+        ov[e / 2] = pack2<DT>(v[0], v[1]);
+      }
+      *(u32x4*)((ET*)a.dx + t * d + 8 * c) = ov;
+    }
+  }
+  // The workgroup's column sums: each wave's, then the 4 waves in order.
+#pragma unroll
+  for (int u = 0; u < NB_MAXU; ++u) {
+    const int c = lane + 64 * u;
+    if (c < nch) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s_part[wave][8 * c + e] = dw[u][e];
+    }
+  }
+  __syncthreads();
+  for (int c = threadIdx.x; c < d; c += NB_THREADS) {
+    float v = 0.0f;
+#pragma unroll
+    for (int q = 0; q < NB_THREADS / 64; ++q) v += s_part[q][c];
+    a.partial[(int64_t)blockIdx.x * d + c] = v;
+  }
+}
+
+template <int DT>
+__global__ void __launch_bounds__(NB_THREADS) norm_dw_reduce_kernel(NormBwdArgs a, int nwg) {
+  const int c = blockIdx.x * NB_THREADS + threadIdx.x;
+  if (c >= a.d) return;
+  float v = 0.0f;
+  for (int q = 0; q < nwg; ++q) v += a.partial[(int64_t)q * a.d + c];
+  ((typename Elem<DT>::T*)a.dw)[c] = Elem<DT>::from_f(v);
+}
+
+size_t norm_bwd_partial_bytes(int64_t T, int d) {
+  return (size_t)((T + NORM_ROWS - 1) / NORM_ROWS) * (size_t)d * sizeof(float);
+}
+
+int norm_bwd_launch(int dtype, const NormBwdArgs& a, hipStream_t s) {
+  NSMOE_REQUIRE(dtype == DT_BF16 || dtype == DT_F16, "norm_bwd: 16-bit types only");
+  NSMOE_REQUIRE(a.d >= 8 && a.d % 8 == 0 && a.d <= NORM_MAX_D,
+                "norm_bwd: d %% 8 == 0 and d <= %d (d %d)", NORM_MAX_D, a.d);
+  NSMOE_REQUIRE(a.x && a.rstd && a.w && a.dxn && a.g && a.dx && a.partial && a.dw,
+                "norm_bwd: NULL pointer");
+  if (a.T == 0) return NSMOE_OK;
+  const int nwg = (int)((a.T + NORM_ROWS - 1) / NORM_ROWS);
+  const unsigned rg = (unsigned)((a.d + NB_THREADS - 1) / NB_THREADS);
+  KernelTimer timer("norm_bwd", s);
+  if (dtype == DT_BF16) {
+    norm_bwd_kernel<DT_BF16><<<(unsigned)nwg, NB_THREADS, 0, s>>>(a);
+    norm_dw_reduce_kernel<DT_BF16><<<rg, NB_THREADS, 0, s>>>(a, nwg);
+  } else {
+    norm_bwd_kernel<DT_F16><<<(unsigned)nwg, NB_THREADS, 0, s>>>(a);
+    norm_dw_reduce_kernel<DT_F16><<<rg, NB_THREADS, 0, s>>>(a, nwg);
+  }
+  timer.stop();
+  return check_launch("norm_bwd_kernel");
+}
+
+}  // namespace nsmoe

@@ -21,6 +21,9 @@
 //     order of equal keys.
 //   * The exact pass, on all 8 waves: one undecided token per wave, the restatement of
 //     CPU topk (topk_exact.h) on the keys as the selection saw them.
+//   * With the RMSNorm in front (RouterArgs::norm_w), the GEMM waves normalise their rows
+//     in registers between the load and the first MFMA (the row's sum of squares over its
+//     4 lanes) and one of each row's two waves stores the normalised row.
 //   * Per workgroup it leaves the expert histogram of its tokens (a chunk of 32 k pairs for
 //     the dispatch's place pass) and, in training, the column sums of probs for the
 //     balance loss.
@@ -118,6 +121,41 @@ __global__ void __launch_bounds__(RT_THREADS) router_fwd_kernel(RouterArgs a) {
 #pragma unroll
     for (int ks = 0; ks < RT_MAX_STEPS; ++ks)
       if (ks < nks) xr[ks] = *(const u32x4*)(xp + ks * 32);
+  }
+  if (a.norm_w && mma_wave) {  // uniform: RMSNorm of the rows in place (RouterArgs)
+    // The row's sum of squares: this lane's 8 nks elements, then its 4 lanes (g = 0..3).
+    const int64_t trow = tok0 + tile * 16 + j;
+    float ss = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < RT_MAX_STEPS; ++ks) {
+      if (ks < nks) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float lo = unpack2<DT>(xr[ks][e], 0), hi = unpack2<DT>(xr[ks][e], 1);
+          ss += lo * lo + hi * hi;
+        }
+      }
+    }
+    ss += __shfl_xor(ss, 16, 64);
+    ss += __shfl_xor(ss, 32, 64);
+    const float rstd = 1.0f / sqrtf(ss / (float)d + a.norm_eps);
+    const ET* wn = (const ET*)a.norm_w + 8 * g;
+    ET* xo = (ET*)a.xn + trow * d + 8 * g;
+    const bool writer = cb0 == 0 && trow < T;  // one of the row's two GEMM waves
+#pragma unroll
+    for (int ks = 0; ks < RT_MAX_STEPS; ++ks) {
+      if (ks < nks) {
+        const u32x4 w = *(const u32x4*)(wn + ks * 32);
+        u32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          o[e] = pack2<DT>(unpack2<DT>(xr[ks][e], 0) * rstd * unpack2<DT>(w[e], 0),
+                           unpack2<DT>(xr[ks][e], 1) * rstd * unpack2<DT>(w[e], 1));
+        xr[ks] = o;
+        if (writer) *(u32x4*)(xo + ks * 32) = o;
+      }
+    }
+    if (writer && g == 0) a.rstd[trow] = rstd;
   }
 #pragma unroll
   for (int nb = 0; nb < NBH; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -388,7 +426,8 @@ int router_fused_launch(const RouterArgs& a, int dtype, hipStream_t s) {
                 "E %% 4 == 0, E <= %d, top_k <= %d (d %d, E %d, k %d)", 32 * RT_MAX_STEPS,
                 RT_MAX_E, RT_MAXK, a.d, a.E, a.k);
   NSMOE_REQUIRE(a.x && a.w && a.logits && a.topk_w && a.topk_idx && a.hist &&
-                    (!(a.flags & 1) || a.probs), "router: NULL pointer");
+                    (!(a.flags & 1) || a.probs) && (!a.norm_w || (a.xn && a.rstd)),
+                "router: NULL pointer");
   if (a.T == 0) return NSMOE_OK;
   const unsigned grid = (unsigned)router_fused_chunks(a.T);
   KernelTimer timer("route_fwd", s);

@@ -26,6 +26,14 @@ struct RouterArgs {
   // workspace (router_fused_args):
   int32_t* hist;         // [chunks, E] experts chosen by each workgroup's tokens
   float* colsum;         // [chunks, E] column sums of probs (training), or NULL
+  // RMSNorm ahead of the router (norm_w non-NULL): x is the residual stream, and the
+  // router runs on xn = x rsqrt(mean(x^2) + eps) norm_w (ln.py:30-36, F.rms_norm's fp32
+  // arithmetic, one rounding to the dtype), which it writes to xn [T, d] with the
+  // per-token rsqrt to rstd [T] (fp32).
+  const void* norm_w;    // [d] in the block's dtype
+  float norm_eps;
+  void* xn;
+  float* rstd;
 };
 
 inline int64_t router_fused_chunks(int64_t T) { return (T + RT_TOK - 1) / RT_TOK; }

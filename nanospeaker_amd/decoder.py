@@ -4,9 +4,11 @@ src/model/nanospeaker.py:133-269 -- embedding, 20 pre-norm blocks of attention a
 final norm, tied unembedding; src/model/mha.py:245-287 for the attention, ln.py:30-36
 for RMSNorm, rope.py for the rotary embedding).
 
-Only the MoE block is this build's HIP code.  The rest is plain PyTorch: RMSNorm is
-`F.rms_norm`, the attention is `scaled_dot_product_attention` (the reference's SDPA path,
-`flex=False`), the projections are torch matmuls.  The stack runs the prefill of the
+Only the MoE block and its FFN half is this build's HIP code: x + moe(norm_ffn(x)) runs
+through MoEBlock.forward_residual, which takes the RMSNorm and the residual add into the
+block's kernels.  The rest is plain PyTorch: the attention's RMSNorm is `F.rms_norm`, the
+attention is `scaled_dot_product_attention` (the reference's SDPA path, `flex=False`),
+the projections are torch matmuls.  The stack runs the prefill of the
 benchmark's fifth workload (batch 4 x 8192 tokens, eval, bf16) with the MoE kernels in
 situ, so the block's share of a real forward can be measured.
 
@@ -177,8 +179,9 @@ class Attention(nn.Module):
 
 
 class DecoderBlock(nn.Module):
-    """Pre-norm block (nanospeaker.py:138-169): x + attn(norm(x)), then x + moe(norm(x)).
-    Returns the new residual stream and the MoE block's balance loss."""
+    """Pre-norm block (nanospeaker.py:138-169): x + attn(norm(x)), then x + moe(norm(x))
+    (MoEBlock.forward_residual).  Returns the new residual stream and the MoE block's
+    balance loss."""
 
     def __init__(self, cfg: DecoderConfig, rotary: Rotary, layer: int, kernel: bool = True):
         super().__init__()
@@ -192,7 +195,7 @@ class DecoderBlock(nn.Module):
 
     def forward(self, x: torch.Tensor):
         x = x + self.attn(self.norm_attn(x))
-        return x + self.ffn(self.norm_ffn(x)), self.ffn.aux_loss
+        return self.ffn.forward_residual(x, self.norm_ffn), self.ffn.aux_loss
 
 
 class Decoder(nn.Module):
@@ -211,8 +214,9 @@ class Decoder(nn.Module):
 
     def trunk(self, idx: torch.Tensor, ffn_hook=None):
         """(final normed hidden states, summed balance loss).  ffn_hook, when given, is
-        called as ffn_hook(block, x) in place of each block's MoE call and must return
-        what it returns (the benchmark times the MoE calls through it)."""
+        called as ffn_hook(block, x) in place of each block's FFN half and must return
+        what it returns, x + moe(norm_ffn(x)) (the benchmark times those calls through
+        it)."""
         x = self.embed(idx)
         aux = torch.zeros((), dtype=torch.float32, device=x.device)
         for blk in self.blocks:
@@ -220,7 +224,7 @@ class Decoder(nn.Module):
                 x, a = blk(x)
             else:
                 x = x + blk.attn(blk.norm_attn(x))
-                x = x + ffn_hook(blk, blk.norm_ffn(x))
+                x = ffn_hook(blk, x)
                 a = blk.ffn.aux_loss
             aux = aux + a
         return self.norm_out(x), aux

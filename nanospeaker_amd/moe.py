@@ -246,6 +246,38 @@ class MoEBlock(nn.Module):
             return self._forward_padded(x, experts, order, token_idx, counts, topk_w, shape)
         return self._forward_eager(x, order, token_idx, counts, topk_w, shape)
 
+    def forward_residual(self, x: torch.Tensor, norm: nn.Module) -> torch.Tensor:
+        """
+        x + self(norm(x)): the FFN half of the reference's pre-norm Block.forward
+        (src/model/nanospeaker.py:169), with `norm` an RMSNorm (ln.py:30-36: a `gamma`
+        of shape [d_model] and `epsilon` or `eps`; F.rms_norm arithmetic).  On the kernel
+        path, for 16-bit blocks in the fused router's shapes, the norm runs inside the
+        router kernel and the residual add inside the combine, and the backward's norm
+        gradient and residual add in one more kernel (nsmoe.h NSMOE_BLOCK_NORM); the
+        side effects are those of forward().  Anything else is exactly those three ops.
+        """
+        gamma = getattr(norm, "gamma", None)
+        eps = getattr(norm, "epsilon", getattr(norm, "eps", None))
+        shape = x.shape
+        x2 = x.reshape(-1, self.d_model)
+        if (gamma is not None and eps is not None and getattr(norm, "fused", True)
+                and tuple(gamma.shape) == (self.d_model,) and x2.shape[0]
+                and self._use_kernel(x2) and self.router._on_kernel(x2)
+                and not (self.training and self.router.noise_std)
+                and moe_kernel.norm_fusable(x2.dtype, self.d_model, self.n_experts,
+                                            self.top_k)):
+            out, aux, counts, topk_idx, logits = moe_kernel.block_forward(
+                x2, self.router.W, self.W_in, self.W_out, self.W_sh_in, self.W_sh_out,
+                self.b_in, self.b_out, self.b_sh_in, self.b_sh_out, self.top_k,
+                self.router.wants_probs(), self.router.normalize_weights, self._kernel_act,
+                self.router.aux_loss_coef, norm_w=gamma, norm_eps=float(eps))
+            self.expert_counts = counts.detach()
+            self._routing = topk_idx
+            self._logits = logits
+            self.aux_loss = aux
+            return out.view(shape)
+        return x + self(norm(x))
+
     def dense_forward(self, x: torch.Tensor) -> torch.Tensor:
         """Every expert on every token, masked by the gates (reference: moe.py:420-474)."""
         if x.shape[-1] != self.d_model:

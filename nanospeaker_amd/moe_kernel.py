@@ -654,23 +654,36 @@ def save_act_supported(dtype: torch.dtype, d: int, h: int) -> bool:
 
 
 def block_saved_bytes(n: int, e: int, k: int, dtype: torch.dtype, want_probs: bool,
-                      save_act: bool = False, d: int = 0, h: int = 0, s: int = 0) -> int:
+                      save_act: bool = False, d: int = 0, h: int = 0, s: int = 0,
+                      norm: bool = False) -> int:
     """
     Size of the block forward's `saved` buffer (nsmoe_block_saved_layout): gates [n, k],
     probs [n, e] fp32 (train branch), sorted ids [l_cap], block owners [l_cap / 16], run
     offsets [e + 1], the padded total, inv [n k] and -- with save_act, where
     save_act_supported(dtype, d, h) -- the pre-activations, 2 h columns of l_cap rows and
-    s times n rows rounded up to 16, each part rounded up to 256 bytes.  Written in Python so fake tensors with symbolic n get the
+    s times n rows rounded up to 16, and with the norm the normalised input [n, d] and its
+    rstd [n] fp32, each part rounded up to 256 bytes.  Written in Python so fake tensors with symbolic n get the
     same size; a CPU test holds it equal to the library's.
     """
+    return block_saved_offsets(n, e, k, dtype, want_probs, save_act, d, h, s, norm)[-1]
+
+
+def block_saved_offsets(n: int, e: int, k: int, dtype: torch.dtype, want_probs: bool,
+                        save_act: bool = False, d: int = 0, h: int = 0, s: int = 0,
+                        norm: bool = False) -> list:
+    """The byte offset of each part of `saved` (nsmoe.h NSMOE_SAVED_*), then the total
+    (block_saved_bytes)."""
     es = 4 if dtype == torch.float32 else 2
     m = n * k
     l_cap = _l_cap(m, e)
     act = ((l_cap + s * (-(-n // 16) * 16)) * 2 * h * es
            if save_act and save_act_supported(dtype, d, h) else 0)
     parts = (m * es, n * e * 4 if want_probs else 0, l_cap * 4, (l_cap // ALIGN_M) * 4,
-             (e + 1) * 4, 4, m * 4, act)
-    return sum(_al256(b) for b in parts)
+             (e + 1) * 4, 4, m * 4, act, n * d * es if norm else 0, n * 4 if norm else 0)
+    offs = [0]
+    for b in parts:
+        offs.append(offs[-1] + _al256(b))
+    return offs
 
 
 class _BlockPlan:
@@ -683,6 +696,7 @@ class _BlockPlan:
             dtype=_DT[dt], activation=KERNEL_ACTIVATIONS[activation], n_tokens=n, d_model=d,
             d_hidden=h, n_experts=e, n_shared=s, top_k=k, reserved0=0, l_cap=0)
         self.grads = nat.ExpertsGrads()
+        self.norm = nat.BlockNorm()
         offs = (ctypes.c_size_t * nat.BLOCK_NSAVED)()
         total = ctypes.c_size_t()
         nat.check(lib.nsmoe_block_saved_layout(self.args, flags, offs, ctypes.byref(total)),
@@ -732,15 +746,23 @@ def _plan(dt, activation, n, d, h, e, s, k, flags) -> _BlockPlan:
     return plan
 
 
-def _route_bits(dt, want_probs, normalize, save_act=False) -> int:
+def _route_bits(dt, want_probs, normalize, save_act=False, norm=False) -> int:
     half = dt in (torch.bfloat16, torch.float16)
     return (_route_flags(want_probs, normalize) | (nat.ROUTE_LOGITS16 if half else 0)
-            | (nat.BLOCK_SAVE_ACT if save_act else 0))
+            | (nat.BLOCK_SAVE_ACT if save_act else 0) | (nat.BLOCK_NORM if norm else 0))
+
+
+def norm_fusable(dtype: torch.dtype, d: int, e: int, k: int) -> bool:
+    """Whether the block takes the RMSNorm and residual in its own kernels (nsmoe.h
+    NSMOE_BLOCK_NORM): the fused router's shapes -- bf16/fp16, d % 32 == 0, d <= 576,
+    E % 4 == 0, E <= 80, top_k <= 16."""
+    return (dtype in (torch.bfloat16, torch.float16) and d % 32 == 0 and d <= 576
+            and e % 4 == 0 and e <= 80 and k <= 16)
 
 
 def _block_fwd_impl(x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out,
                     top_k, want_probs, normalize, activation, aux_coef, logit_bias=None,
-                    save_act=False):
+                    save_act=False, norm_w=None, norm_eps=1e-6):
     """
     MoEBlock.forward's kernel path (moe.py:345-418): the router GEMM `x @ W_r` (torch,
     router.py:69), then one C call (nsmoe_block_fwd: router tail, dispatch, routed + shared
@@ -759,13 +781,20 @@ def _block_fwd_impl(x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in
 
     With `save_act` the experts' pre-activations are kept in `saved` for the backward
     (nsmoe.h NSMOE_BLOCK_SAVE_ACT), which then skips recomputing x W_in.
+
+    With `norm_w` [d] (an RMSNorm gain; norm_fusable shapes) x is the residual stream and
+    `out` is x + block(rms_norm(x, norm_w, norm_eps)) (nsmoe.h NSMOE_BLOCK_NORM): the
+    Block's FFN half, nanospeaker.py:169.
     """
     dev, dt = x.device, x.dtype
     n, d = x.shape
     e, h2 = W_r.shape[1], w_in.shape[2]
     s = 0 if w_sh_in is None else w_sh_in.shape[0]
-    flags = _route_bits(dt, want_probs, normalize, save_act)
+    flags = _route_bits(dt, want_probs, normalize, save_act, norm_w is not None)
     plan = _plan(dt, activation, n, d, h2 // 2, e, s, top_k, flags)
+    if norm_w is not None and not plan.fuse_route:
+        raise ValueError("block_fwd: the norm needs the fused router's shapes "
+                         "(norm_fusable)")
     bias = None
     if plan.fuse_route:
         logits = torch.empty((n, e), dtype=dt, device=dev)  # written by the router kernel
@@ -789,8 +818,12 @@ def _block_fwd_impl(x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in
                                             w_sh_out)
         a.w_in_packed, a.w_out_packed = p_in.data_ptr(), p_out.data_ptr()
         ws = torch.empty(plan.fwd_ws, dtype=torch.uint8, device=dev)
+        nrm = None
+        if norm_w is not None:
+            nrm = plan.norm
+            nrm.weight, nrm.grad_weight, nrm.eps = norm_w.data_ptr(), None, float(norm_eps)
         nat.check(nat.lib().nsmoe_block_fwd(
-            a, W_r.data_ptr() if plan.fuse_route else None, _p(bias), logits.data_ptr(),
+            a, nrm, W_r.data_ptr() if plan.fuse_route else None, _p(bias), logits.data_ptr(),
             flags | (nat.BLOCK_PACK if pending is not None else 0), aux_coef,
             saved.data_ptr(), topk_idx.data_ptr(), counts.data_ptr(), out.data_ptr(),
             aux.data_ptr() if want_probs else None, ws.data_ptr(), plan.fwd_ws, _stream()),
@@ -810,17 +843,19 @@ def block_fwd(x: Tensor, W_r: Tensor, w_in: Tensor, w_out: Tensor, w_sh_in: Opti
               w_sh_out: Optional[Tensor], b_in: Optional[Tensor], b_out: Optional[Tensor],
               b_sh_in: Optional[Tensor], b_sh_out: Optional[Tensor], top_k: int,
               want_probs: bool, normalize: bool, activation: str, aux_coef: float,
-              logit_bias: Optional[Tensor] = None, save_act: bool = False
+              logit_bias: Optional[Tensor] = None, save_act: bool = False,
+              norm_w: Optional[Tensor] = None, norm_eps: float = 1e-6
               ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
     """The block's forward as a torch.library op (see _block_fwd_impl)."""
     return _block_fwd_impl(x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in,
                            b_sh_out, top_k, want_probs, normalize, activation, aux_coef,
-                           logit_bias, save_act)
+                           logit_bias, save_act, norm_w, norm_eps)
 
 
 @block_fwd.register_fake
 def _(x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out, top_k,
-      want_probs, normalize, activation, aux_coef, logit_bias=None, save_act=False):
+      want_probs, normalize, activation, aux_coef, logit_bias=None, save_act=False,
+      norm_w=None, norm_eps=1e-6):
     n, d = x.shape
     e = W_r.shape[1]
     s = 0 if w_sh_in is None else w_sh_in.shape[0]
@@ -831,13 +866,15 @@ def _(x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out, to
             x.new_empty((n, top_k), dtype=torch.int64),
             x.new_empty((n, e), dtype=x.dtype if half else torch.float32),
             x.new_empty((block_saved_bytes(n, e, top_k, x.dtype, want_probs, save_act, d,
-                                           w_in.shape[2] // 2, s),), dtype=torch.uint8),
+                                           w_in.shape[2] // 2, s, norm_w is not None),),
+                        dtype=torch.uint8),
             x.new_empty((_packed_in_bytes(x, w_in, w_sh_in),), dtype=torch.uint8))
 
 
 def _block_bwd_impl(g_out, g_aux, x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in,
                     logits, saved, topk_idx, counts, w_in_packed, top_k, want_probs, normalize,
-                    activation, aux_coef, has_b_sh_out, need_dx, need_dW_r, save_act=False):
+                    activation, aux_coef, has_b_sh_out, need_dx, need_dW_r, save_act=False,
+                    norm_w=None):
     """
     The block's backward in one C call (nsmoe_block_bwd: experts' backward, router tail's
     backward with the balance-loss gradient folded in, and for 16-bit types the router
@@ -845,14 +882,15 @@ def _block_bwd_impl(g_out, g_aux, x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, 
     split-K kernel; other types finish the router GEMM's backward in torch).
 
     Returns (dx, dW_r, dW_in, dW_out, dW_sh_in, dW_sh_out, db_in, db_out, db_sh_in,
-    db_sh_out); a gradient with no input (no shared experts, no bias, not needed) comes
-    back as an empty tensor.
+    db_sh_out, dnorm_w); a gradient with no input (no shared experts, no bias, no norm,
+    not needed) comes back as an empty tensor.  With `norm_w`, dx is the residual
+    stream's gradient through both the norm and the residual.
     """
     n, d = x.shape
     e, h2 = W_r.shape[1], w_in.shape[2]
     s = 0 if w_sh_in is None else w_sh_in.shape[0]
     dev, dt = x.device, x.dtype
-    flags = _route_bits(dt, want_probs, normalize, save_act)
+    flags = _route_bits(dt, want_probs, normalize, save_act, norm_w is not None)
     half = bool(flags & nat.ROUTE_LOGITS16)
     plan = _plan(dt, activation, n, d, h2 // 2, e, s, top_k, flags)
     emp = lambda: x.new_empty(0)  # one per absent gradient: outputs may not alias
@@ -865,6 +903,7 @@ def _block_bwd_impl(g_out, g_aux, x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, 
     db_out = torch.empty_like(b_out) if b_out is not None else emp()
     db_sh_in = torch.empty_like(b_sh_in) if b_sh_in is not None else emp()
     db_sh_out = torch.empty((s, d), dtype=dt, device=dev) if has_b_sh_out else emp()
+    dnorm_w = torch.empty_like(norm_w) if norm_w is not None else emp()
     fuse = plan.fuse_router
     dlogits = None if fuse else torch.empty((n, e), dtype=dt if half else torch.float32,
                                             device=dev)
@@ -882,21 +921,28 @@ def _block_bwd_impl(g_out, g_aux, x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, 
         # b_sh_out does not enter the backward (the shared experts have no gate).
         a = plan.bind(x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, None)
         a.w_in_packed, a.w_out_packed = w_in_packed.data_ptr(), None
+        nrm = None
+        if norm_w is not None:
+            nrm = plan.norm
+            nrm.weight, nrm.grad_weight = norm_w.data_ptr(), dnorm_w.data_ptr()
         nat.check(nat.lib().nsmoe_block_bwd(
-            a, logits.data_ptr(), flags, aux_coef, saved.data_ptr(), topk_idx.data_ptr(),
+            a, nrm, logits.data_ptr(), flags, aux_coef, saved.data_ptr(), topk_idx.data_ptr(),
             counts.data_ptr(), g_out.data_ptr(), _p(ga), gr, _p(W_r if fuse else None),
             _p(dW_r), _p(dlogits), ws.data_ptr(), plan.bwd_ws, _stream()), "nsmoe_block_bwd")
     else:
         for t in (dx, dw_in, dw_out, dw_sh_in, dw_sh_out, db_in, db_out, db_sh_in, db_sh_out,
-                  dlogits, dW_r):
+                  dlogits, dW_r, dnorm_w):
             if t is not None:
                 t.zero_()
+        if norm_w is not None:
+            dx.copy_(g_out)  # no tokens: the residual's share only
     if not fuse:
         dl = dlogits if half else dlogits.to(dt)
         dW_r = x.t().mm(dl) if need_dW_r else torch.zeros_like(W_r)
         if need_dx:
             dx.addmm_(dl, W_r.t())
-    return dx, dW_r, dw_in, dw_out, dw_sh_in, dw_sh_out, db_in, db_out, db_sh_in, db_sh_out
+    return (dx, dW_r, dw_in, dw_out, dw_sh_in, dw_sh_out, db_in, db_out, db_sh_in, db_sh_out,
+            dnorm_w)
 
 
 @torch.library.custom_op("nsmoe::block_bwd", mutates_args=())
@@ -906,36 +952,38 @@ def block_bwd(g_out: Tensor, g_aux: Optional[Tensor], x: Tensor, W_r: Tensor, w_
               logits: Tensor, saved: Tensor, topk_idx: Tensor, counts: Tensor,
               w_in_packed: Tensor, top_k: int, want_probs: bool, normalize: bool,
               activation: str, aux_coef: float, has_b_sh_out: bool, need_dx: bool,
-              need_dW_r: bool, save_act: bool = False
+              need_dW_r: bool, save_act: bool = False, norm_w: Optional[Tensor] = None
               ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor,
-                         Tensor]:
+                         Tensor, Tensor]:
     """The block's backward as a torch.library op (see _block_bwd_impl)."""
     return _block_bwd_impl(g_out, g_aux, x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out,
                            b_sh_in, logits, saved, topk_idx, counts, w_in_packed, top_k,
                            want_probs, normalize, activation, aux_coef, has_b_sh_out, need_dx,
-                           need_dW_r, save_act)
+                           need_dW_r, save_act, norm_w)
 
 
 @block_bwd.register_fake
 def _(g_out, g_aux, x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, logits,
       saved, topk_idx, counts, w_in_packed, top_k, want_probs, normalize, activation, aux_coef,
-      has_b_sh_out, need_dx, need_dW_r, save_act=False):
+      has_b_sh_out, need_dx, need_dW_r, save_act=False, norm_w=None):
     s = 0 if w_sh_in is None else w_sh_in.shape[0]
     like = lambda t: torch.empty_like(t) if t is not None else x.new_empty(0)
     return (torch.empty_like(x), torch.empty_like(W_r), torch.empty_like(w_in),
             torch.empty_like(w_out), like(w_sh_in), like(w_sh_out), like(b_in), like(b_out),
-            like(b_sh_in), x.new_empty((s, x.shape[1])) if has_b_sh_out else x.new_empty(0))
+            like(b_sh_in), x.new_empty((s, x.shape[1])) if has_b_sh_out else x.new_empty(0),
+            like(norm_w))
 
 
 def _block_fwd_setup(ctx, inputs, output):
     (x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out, top_k,
-     want_probs, normalize, activation, aux_coef, logit_bias, save_act) = inputs
+     want_probs, normalize, activation, aux_coef, logit_bias, save_act, norm_w,
+     norm_eps) = inputs
     out, aux, counts, topk_idx, logits, saved, w_in_packed = output
     ctx.mark_non_differentiable(counts, topk_idx, logits, saved, w_in_packed)
     # Unused output gradients arrive as None instead of materialised zeros.
     ctx.set_materialize_grads(False)
-    ctx.has = [t is not None for t in (w_sh_in, b_in, b_out, b_sh_in)]
-    opt = [t for t in (w_sh_in, w_sh_out, b_in, b_out, b_sh_in) if t is not None]
+    ctx.has = [t is not None for t in (w_sh_in, b_in, b_out, b_sh_in, norm_w)]
+    opt = [t for t in (w_sh_in, w_sh_out, b_in, b_out, b_sh_in, norm_w) if t is not None]
     ctx.save_for_backward(x, W_r, w_in, w_out, logits, saved, topk_idx, counts, w_in_packed,
                           *opt)
     ctx.cfg = (top_k, want_probs, normalize, activation, aux_coef, b_sh_out is not None,
@@ -948,27 +996,29 @@ def _block_fwd_backward(ctx, g_out, g_aux, g_counts, g_idx, g_logits, g_saved, g
 
 def _block_backward(ctx, g_out, g_aux, bwd):
     x, W_r, w_in, w_out, logits, saved, topk_idx, counts, w_in_packed, *opt = ctx.saved_tensors
-    has_sh, has_b_in, has_b_out, has_b_sh_in = ctx.has
+    has_sh, has_b_in, has_b_out, has_b_sh_in, has_norm = ctx.has
     it = iter(opt)
     w_sh_in = next(it) if has_sh else None
     w_sh_out = next(it) if has_sh else None
     b_in = next(it) if has_b_in else None
     b_out = next(it) if has_b_out else None
     b_sh_in = next(it) if has_b_sh_in else None
+    norm_w = next(it) if has_norm else None
     top_k, want_probs, normalize, activation, aux_coef, has_b_sh_out, save_act = ctx.cfg
     need = ctx.needs_input_grad
     if g_out is None:
         g_out = torch.zeros_like(x)
-    (dx, dW_r, dw_in, dw_out, dw_sh_in, dw_sh_out, db_in, db_out, db_sh_in,
-     db_sh_out) = bwd(g_out, g_aux, x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out,
-                      b_sh_in, logits, saved, topk_idx, counts, w_in_packed, top_k, want_probs,
-                      normalize, activation, aux_coef, has_b_sh_out, need[0], need[1], save_act)
+    (dx, dW_r, dw_in, dw_out, dw_sh_in, dw_sh_out, db_in, db_out, db_sh_in, db_sh_out,
+     dnorm_w) = bwd(g_out, g_aux, x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out,
+                    b_sh_in, logits, saved, topk_idx, counts, w_in_packed, top_k, want_probs,
+                    normalize, activation, aux_coef, has_b_sh_out, need[0], need[1], save_act,
+                    norm_w)
     opt_grad = lambda present, g: g if present else None
     return (dx if need[0] else None, dW_r if need[1] else None, dw_in, dw_out,
             opt_grad(has_sh, dw_sh_in), opt_grad(has_sh, dw_sh_out),
             opt_grad(has_b_in, db_in), opt_grad(has_b_out, db_out),
             opt_grad(has_b_sh_in, db_sh_in), opt_grad(has_b_sh_out, db_sh_out),
-            None, None, None, None, None, None, None)
+            None, None, None, None, None, None, None, opt_grad(has_norm, dnorm_w), None)
 
 
 block_fwd.register_autograd(_block_fwd_backward, setup_context=_block_fwd_setup)
@@ -991,25 +1041,51 @@ class _BlockEager(torch.autograd.Function):
 
 
 def block_forward(x, router_W, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out,
-                  top_k, want_probs, normalize, activation, aux_coef, logit_bias=None):
+                  top_k, want_probs, normalize, activation, aux_coef, logit_bias=None,
+                  norm_w=None, norm_eps=1e-6):
+    """The MoE block on the kernel path: the first five results of block_forward_state."""
+    return block_forward_state(x, router_W, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out,
+                               b_sh_in, b_sh_out, top_k, want_probs, normalize, activation,
+                               aux_coef, logit_bias, norm_w, norm_eps)[:5]
+
+
+def block_forward_state(x, router_W, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in,
+                        b_sh_out, top_k, want_probs, normalize, activation, aux_coef,
+                        logit_bias=None, norm_w=None, norm_eps=1e-6):
     """
     The MoE block on the kernel path: (out [N, d], aux_loss, counts [E] int32,
     topk_idx [N, k] int64, logits [N, E]).  aux_loss is the balance loss (fp32) when
     want_probs, else a zero of x's dtype (router.py:52-54, moe.py:367-372); logits are the
     router GEMM's output the routing ran on (not differentiable).  Parameters are cast to
     x's dtype, as the eager matmuls would run.
+
+    With `norm_w` (an RMSNorm gain, eps `norm_eps`) x is the residual stream and `out` is
+    x + block(F.rms_norm(x)): in the block's kernels where norm_fusable holds, else as
+    those three ops.
+
+    block_forward_state also returns the forward's `saved` buffer and the flags that laid
+    it out (block_saved_offsets; None, 0 where the block did not run as one op), so a test
+    can read what the backward will read -- the normalised input among it.
     """
     _check_activation(activation)
+    if norm_w is not None and not norm_fusable(x.dtype, x.shape[-1], router_W.shape[1],
+                                               top_k):
+        xn = torch.nn.functional.rms_norm(x, (x.shape[-1],), norm_w.to(x.dtype), norm_eps)
+        out, aux, counts, topk_idx, logits, saved, flags = block_forward_state(
+            xn, router_W, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out,
+            top_k, want_probs, normalize, activation, aux_coef, logit_bias)
+        return x + out, aux, counts, topk_idx, logits, saved, flags
     cast = lambda t: None if t is None else t.to(x.dtype)
     op = block_fwd if torch.compiler.is_compiling() else _BlockEager.apply
     # The pre-activations are saved only for a forward that autograd will run backward
     # through (a checkpointed block's first, gradient-free forward does not save them).
-    params = (router_W, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out)
+    params = (router_W, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out, norm_w)
     save_act = SAVE_ACT and torch.is_grad_enabled() and (
         x.requires_grad or any(t is not None and t.requires_grad for t in params))
-    out, aux, counts, topk_idx, logits, _, _ = op(
+    out, aux, counts, topk_idx, logits, saved, _ = op(
         x.contiguous(), cast(router_W).contiguous(), cast(w_in).contiguous(),
         cast(w_out).contiguous(), _c(cast(w_sh_in)), _c(cast(w_sh_out)), _c(cast(b_in)),
         _c(cast(b_out)), _c(cast(b_sh_in)), _c(cast(b_sh_out)), top_k, want_probs, normalize,
-        activation, float(aux_coef), logit_bias, save_act)
-    return out, aux, counts, topk_idx, logits
+        activation, float(aux_coef), logit_bias, save_act, _c(cast(norm_w)), float(norm_eps))
+    flags = _route_bits(x.dtype, want_probs, normalize, save_act, norm_w is not None)
+    return out, aux, counts, topk_idx, logits, saved, flags

@@ -14,6 +14,9 @@ CPU restatement, op for op in torch, of the reference's eager dropless MoE path:
   eager forward  src/model/moe.py:345-418      (index_add_ in expert order 0..E-1)
   dense forward  src/model/moe.py:420-474      (every expert on every token)
   glu            src/model/glu.py:44-45        (act(gate) * up)
+  rms norm       src/model/ln.py:30-36         (F.rms_norm: fp32 rstd, (x rstd) w, one
+                                                rounding; its backward)
+  ffn sublayer   src/model/nanospeaker.py:169  (x + ffn(norm_ffn(x)))
 
 `eager_forward` keeps the reference's rounding points in the module dtype, so in bf16 it
 reproduces the reference's own CPU numbers bit for bit (pinned against fixtures the
@@ -316,6 +319,25 @@ def block(x: torch.Tensor, p: Params, top_k: int, *, train: bool = True,
         loss.backward()
         res.grads = {k: v.grad for k, v in leaves.items()}
     return res
+
+
+def rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float):
+    """(xn, rstd): F.rms_norm's arithmetic (ln.py:30-36) written out -- fp32 rstd =
+    1 / sqrt(mean(x^2) + eps), xn = (x rstd) w in fp32, rounded once to x's dtype."""
+    xf = x.float()
+    rstd = torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    return (xf * rstd * w.float()).to(x.dtype), rstd.squeeze(-1)
+
+
+def rms_norm_backward(g: torch.Tensor, x: torch.Tensor, w: torch.Tensor, rstd: torch.Tensor):
+    """(dx, dw) of rms_norm for the output gradient g, in fp32: with xh = x rstd and
+    gxh = g w, dx = (gxh - xh mean(xh gxh)) rstd and dw = sum over tokens of g xh."""
+    gf, xf, wf = g.float(), x.float(), w.float()
+    r = rstd.float().unsqueeze(-1)
+    xh = xf * r
+    gxh = gf * wf
+    dx = (gxh - xh * (xh * gxh).mean(-1, keepdim=True)) * r
+    return dx, (gf * xh).sum(0)
 
 
 def flops_per_token(d: int, H: int, k: int, n_shared: int, E: int) -> int:

@@ -43,7 +43,7 @@ def test_struct_layouts_match_the_header():
 
 
 def test_abi_version_and_alignment():
-    assert nat.lib().nsmoe_abi_version() == nat.ABI_VERSION == 5
+    assert nat.lib().nsmoe_abi_version() == nat.ABI_VERSION == 6
     assert nat.lib().nsmoe_align_m() == mk.ALIGN_M
 
 
@@ -148,22 +148,28 @@ def test_kernel_supported_raises_on_a_gpu_tensor_without_the_library(monkeypatch
     (37, 76, 6, "float16", True), (32768, 76, 6, "bfloat16", False), (5, 1000, 8, "float32", False),
 ])
 @pytest.mark.parametrize("save_act", [False, True])
+@pytest.mark.parametrize("norm", [False, True])
 @pytest.mark.parametrize("d,h,s", [(576, 128, 2), (64, 64, 0), (128, 64, 1), (192, 96, 2),
                                    (512, 256, 2), (320, 128, 2), (576, 48, 2)])
-def test_block_saved_layout_matches_the_python_mirror(n, e, k, dt, probs, save_act, d, h, s):
+def test_block_saved_layout_matches_the_python_mirror(n, e, k, dt, probs, save_act, norm, d,
+                                                      h, s):
     """The fake impl of nsmoe::block_fwd sizes `saved` in Python (symbolic shapes),
-    including which shapes keep the experts' pre-activations."""
+    including which shapes keep the experts' pre-activations, and the norm's parts."""
     import torch
     dtype = getattr(torch, dt)
     a = nat.ExpertsArgs(dtype=mk._DT[dtype], activation=0, n_tokens=n, d_model=d,
                         d_hidden=h, n_experts=e, n_shared=s, top_k=k, l_cap=0)
     offs = (ctypes.c_size_t * nat.BLOCK_NSAVED)()
     total = ctypes.c_size_t()
-    flags = (nat.ROUTE_PROBS if probs else 0) | (nat.BLOCK_SAVE_ACT if save_act else 0)
+    flags = ((nat.ROUTE_PROBS if probs else 0) | (nat.BLOCK_SAVE_ACT if save_act else 0)
+             | (nat.BLOCK_NORM if norm else 0))
     assert nat.lib().nsmoe_block_saved_layout(a, flags, offs, ctypes.byref(total)) == 0
-    assert total.value == mk.block_saved_bytes(n, e, k, dtype, probs, save_act, d, h, s)
+    assert total.value == mk.block_saved_bytes(n, e, k, dtype, probs, save_act, d, h, s, norm)
     assert list(offs) == sorted(offs) and offs[0] == 0
-    act = total.value - offs[nat.SAVED_ACT]
+    es = 4 if dtype == torch.float32 else 2
+    assert offs[nat.SAVED_RSTD] - offs[nat.SAVED_XN] == (mk._al256(n * d * es) if norm else 0)
+    assert total.value - offs[nat.SAVED_RSTD] == (mk._al256(n * 4) if norm else 0)
+    act = offs[nat.SAVED_XN] - offs[nat.SAVED_ACT]
     if save_act and mk.save_act_supported(dtype, d, h):
         l_cap = mk._l_cap(n * k, e)
         assert act == mk._al256((l_cap + s * (-(-n // 16) * 16)) * 2 * h * 2)
@@ -205,20 +211,39 @@ def test_block_entry_points_reject_missing_buffers():
     lib = nat.lib()
     a = nat.ExpertsArgs(dtype=0, activation=0, n_tokens=4, d_model=64, d_hidden=64,
                         n_experts=8, n_shared=0, top_k=2, l_cap=0)
-    #      args w_router bias logits flags coef saved idx counts out aux ws ws_bytes stream
-    assert lib.nsmoe_block_fwd(a, None, None, 1, 0, 0.0, 1, None, 1, 1, None, 1, 1 << 20,
-                               None) == 1
+    #      args norm w_router bias logits flags coef saved idx counts out aux ws ws_bytes
+    #      stream
+    assert lib.nsmoe_block_fwd(a, None, None, None, 1, 0, 0.0, 1, None, 1, 1, None, 1,
+                               1 << 20, None) == 1
     assert "NULL" in lib.nsmoe_last_error().decode()
-    assert lib.nsmoe_block_fwd(a, None, None, 1, 0, 0.0, 1, 1, 1, 1, None, 1, 1 << 20,
+    assert lib.nsmoe_block_fwd(a, None, None, None, 1, 0, 0.0, 1, 1, 1, 1, None, 1, 1 << 20,
                                None) == 1
     assert "packed" in lib.nsmoe_last_error().decode()
     a.w_in_packed = a.w_out_packed = 1
-    assert lib.nsmoe_block_fwd(a, None, 1, 1, 0, 0.0, 1, 1, 1, 1, None, 1, 1 << 20,
+    assert lib.nsmoe_block_fwd(a, None, None, 1, 1, 0, 0.0, 1, 1, 1, 1, None, 1, 1 << 20,
                                None) == 1
     assert "logit_bias" in lib.nsmoe_last_error().decode()
     odd = nat.ExpertsArgs(dtype=0, activation=0, n_tokens=4, d_model=48, d_hidden=64,
                           n_experts=8, n_shared=0, top_k=2, l_cap=0, w_in_packed=1,
                           w_out_packed=1)
-    assert lib.nsmoe_block_fwd(odd, 1, None, 1, 0, 0.0, 1, 1, 1, 1, None, 1, 1 << 20,
+    assert lib.nsmoe_block_fwd(odd, None, 1, None, 1, 0, 0.0, 1, 1, 1, 1, None, 1, 1 << 20,
                                None) == 1
     assert "fused router" in lib.nsmoe_last_error().decode()
+    # The norm and NSMOE_BLOCK_NORM go together, and the norm needs the fused router.
+    norm = nat.BlockNorm(weight=1, grad_weight=1, eps=1e-6)
+    assert lib.nsmoe_block_fwd(a, norm, 1, None, 1, 0, 0.0, 1, 1, 1, 1, None, 1, 1 << 20,
+                               None) == 1
+    assert "NSMOE_BLOCK_NORM" in lib.nsmoe_last_error().decode()
+    assert lib.nsmoe_block_fwd(a, None, 1, None, 1, nat.BLOCK_NORM, 0.0, 1, 1, 1, 1, None, 1,
+                               1 << 20, None) == 1
+    assert "NSMOE_BLOCK_NORM" in lib.nsmoe_last_error().decode()
+    assert lib.nsmoe_block_fwd(a, norm, None, None, 1, nat.BLOCK_NORM, 0.0, 1, 1, 1, 1, None,
+                               1, 1 << 20, None) == 1
+    assert "fused router" in lib.nsmoe_last_error().decode()
+    #      args norm logits flags coef saved idx counts g g_aux grads w_r gw_r glog ws
+    #      ws_bytes stream
+    gr = nat.ExpertsGrads(dx=1, dw_in=1, dw_out=1)
+    no_grad_w = nat.BlockNorm(weight=1, grad_weight=None, eps=1e-6)
+    assert lib.nsmoe_block_bwd(a, no_grad_w, 1, nat.BLOCK_NORM, 0.0, 1, 1, 1, 1, None, gr, 1,
+                               1, None, 1, 1 << 20, None) == 1
+    assert "grad_weight" in lib.nsmoe_last_error().decode()

@@ -8,6 +8,8 @@ The drop-in contract around the kernels, on the GPU (reference: tests/test_moe_k
     break and equal eager;
   * reentrant activation checkpointing (the trainer's use_reentrant=True) gives the
     unwrapped block's gradients bit for bit;
+  * the same three for the pre-norm FFN half x + moe(norm(x)) (MoEBlock.forward_residual,
+    the norm and residual inside the block's op);
   * the weight-pack cache: reused while the weights are unchanged, invalidated by an
     in-place optimizer update, with the updated block still matching the oracle.
 """
@@ -69,6 +71,64 @@ def test_opcheck_block_op(dtype):
     torch.library.opcheck(mk.block_fwd, args,
                           test_utils=("test_schema", "test_autograd_registration",
                                       "test_faketensor"))
+
+
+def test_opcheck_block_op_with_norm():
+    """nsmoe::block_fwd with the RMSNorm gain: x is the residual stream."""
+    print("[contract] opcheck block_fwd + norm", flush=True)
+    m = small_block(torch.bfloat16)
+    x = torch.randn(13, 32, device=DEV).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(32, device=DEV)).to(torch.bfloat16)
+    leaf = lambda t: t.detach().clone().requires_grad_(True)
+    args = (leaf(x), leaf(m.router.W), leaf(m.W_in), leaf(m.W_out), leaf(m.W_sh_in),
+            leaf(m.W_sh_out), None, None, None, None, 2, True, True, "silu", 1e-2, None,
+            True, leaf(w), 1e-6)
+    torch.library.opcheck(mk.block_fwd, args,
+                          test_utils=("test_schema", "test_autograd_registration",
+                                      "test_faketensor"))
+
+
+class PreNormFFN(torch.nn.Module):
+    """The FFN half of the reference's Block.forward (nanospeaker.py:169)."""
+
+    def __init__(self, dtype):
+        super().__init__()
+        from nanospeaker_amd.decoder import RMSNorm
+        self.ffn = small_block(dtype)
+        self.norm = RMSNorm(32).to(dtype).to(DEV)
+        with torch.no_grad():
+            self.norm.gamma.copy_(1 + 0.1 * torch.randn(32, device=DEV))
+
+    def forward(self, x):
+        return self.ffn.forward_residual(x, self.norm), self.ffn.aux_loss
+
+
+def test_pre_norm_ffn_compiles_fullgraph_and_checkpoints():
+    """torch.compile(fullgraph) and a reentrant checkpoint of x + moe(norm(x)) give the
+    eager module's output, balance loss and every gradient bit for bit."""
+    print("[contract] pre-norm FFN: compile + checkpoint", flush=True)
+    torch._dynamo.reset()
+    torch.manual_seed(1)
+    mods = [PreNormFFN(torch.bfloat16) for _ in range(3)]
+    for q in mods[1:]:
+        q.load_state_dict(mods[0].state_dict())
+    eager, comp, ckpt = mods
+    cm = torch.compile(comp, fullgraph=True, backend="aot_eager")
+    x = (2 * torch.randn(2, 33, 32, device=DEV)).to(torch.bfloat16)
+    g = torch.randn(2, 33, 32, device=DEV).to(torch.bfloat16)
+
+    def grads(fn, mod):
+        xg = x.clone().requires_grad_(True)
+        out, aux = fn(xg)
+        ((out.float() * g.float()).sum() + aux).backward()
+        return out.detach(), aux.detach(), [xg.grad] + [p.grad for p in mod.parameters()]
+
+    ref = grads(eager, eager)
+    for got in (grads(cm, comp),
+                grads(lambda t: checkpoint(ckpt, t, use_reentrant=True), ckpt)):
+        assert torch.equal(got[0], ref[0]) and torch.equal(got[1], ref[1])
+        for i, (a, b) in enumerate(zip(got[2], ref[2])):
+            assert torch.equal(a, b), f"gradient {i}"
 
 
 BACKENDS = ["aot_eager"] + (["inductor"] if importlib.util.find_spec("triton") else [])

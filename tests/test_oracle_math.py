@@ -151,3 +151,51 @@ def test_flops_per_token_matches_the_survey():
     """3,626,496 forward FLOPs per token at nanoSpeaker's shape: 8 pairs x (2*d*2H + 2*H*d) + 2*d*E."""
     c = R.nanospeaker_config()
     assert R.flops_per_token(c["d"], 128, c["top_k"], c["n_shared"], c["E"]) == 3_626_496
+
+
+# ---- the RMSNorm in front of the block (ln.py:30-36) ------------------------------------
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("T,d", [(257, 576), (64, 64), (33, 1024)])
+def test_rms_norm_equals_torch_rms_norm(dtype, T, d):
+    """The oracle's written-out norm is torch's F.rms_norm (a library routine) bit for bit
+    on the CPU: same fp32 rstd, same (x rstd) w order, one rounding."""
+    g = torch.Generator().manual_seed(T + d)
+    x = (torch.randn(T, d, generator=g) * 3).to(dtype)
+    w = (1 + 0.2 * torch.randn(d, generator=g)).to(dtype)
+    xn, rstd = R.rms_norm(x, w, 1e-6)
+    assert torch.equal(xn, torch.nn.functional.rms_norm(x, (d,), w, 1e-6))
+    ref = torch.rsqrt(x.double().pow(2).mean(-1) + 1e-6)
+    torch.testing.assert_close(rstd.double(), ref, rtol=1e-6, atol=0)
+
+
+def test_rms_norm_backward_equals_autograd():
+    """dx and dw of the oracle's closed form equal autograd through F.rms_norm in fp64."""
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(40, 96, generator=g, dtype=torch.float64, requires_grad=True)
+    w = (1 + 0.3 * torch.randn(96, generator=g, dtype=torch.float64)).requires_grad_()
+    dy = torch.randn(40, 96, generator=g, dtype=torch.float64)
+    y = torch.nn.functional.rms_norm(x, (96,), w, 1e-6)
+    ax, aw = torch.autograd.grad(y, [x, w], dy)
+    rstd = torch.rsqrt(x.detach().pow(2).mean(-1) + 1e-6)  # fp64, as autograd has it
+    dx, dw = R.rms_norm_backward(dy, x.detach(), w.detach(), rstd)
+    # rms_norm_backward works in fp32: compare at fp32 precision
+    torch.testing.assert_close(dx.double(), ax, rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(dw.double(), aw, rtol=1e-5, atol=1e-4)
+
+
+def test_rms_norm_backward_rejects_a_dropped_term():
+    """A planted mistake in the oracle (the mean term of dx dropped, or dw taken without
+    rstd) fails the autograd check above."""
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(16, 64, generator=g, dtype=torch.float64, requires_grad=True)
+    w = (1 + 0.3 * torch.randn(64, generator=g, dtype=torch.float64)).requires_grad_()
+    dy = torch.randn(16, 64, generator=g, dtype=torch.float64)
+    ax, aw = torch.autograd.grad(torch.nn.functional.rms_norm(x, (64,), w, 1e-6), [x, w], dy)
+    rstd = torch.rsqrt(x.detach().pow(2).mean(-1, keepdim=True) + 1e-6)
+    xh = x.detach() * rstd
+    no_mean = dy * w.detach() * rstd
+    assert not torch.allclose(no_mean, ax, rtol=1e-3, atol=1e-3)
+    no_rstd_dw = (dy * x.detach()).sum(0)
+    assert not torch.allclose(no_rstd_dw, aw, rtol=1e-3, atol=1e-3)
+    assert torch.allclose((dy * xh).sum(0), aw)
