@@ -84,7 +84,7 @@ def kernel_units(name: str, T: int, k: int, S: int, d: int, H: int, E: int):
     rows = T * k + S * T  # routed pairs + shared rows
     if name == "expert_fwd":        # GEMM1 + GEMM2 per row
         return rows * (2 * d * 2 * H + 2 * H * d), "mfma", "TFLOP/s"
-    if name == "expert_bwd":        # G = dout W_out^T per row (the a1 recompute not counted)
+    if name == "expert_bwd":        # G = dout W_out^T per row (a1 saved by the forward)
         return rows * (2 * d * H), "mfma", "TFLOP/s"
     if name == "expert_dx":         # dX rows = dA1 W_in^T
         return rows * (2 * 2 * H * d), "mfma", "TFLOP/s"
@@ -256,11 +256,12 @@ def stats_summary(path, top=30):
     return "\n".join(out)
 
 
-# FLOPs per row the MFMA kernels issue, recomputation included (bf16, H = 128, d = 576):
-# the GLU-backward kernel recomputes a1 = x W_in (2 d 2H) beside G = dout W_out^T (2 d H).
+# FLOPs per row the MFMA kernels issue (bf16, H = 128, d = 576).  With the forward's
+# pre-activations saved (the block's training default) the GLU-backward kernel runs
+# G = dout W_out^T (2 d H) alone; recomputing them would add a1 = x W_in (2 d 2H).
 ISSUED_FLOPS_PER_ROW = {
     "expert_fwd": 2 * 576 * 256 + 2 * 128 * 576,
-    "expert_bwd": 2 * 576 * 256 + 2 * 576 * 128,
+    "expert_bwd": 2 * 576 * 128,  # G only: a1 comes saved from the forward
     "expert_dx": 2 * 256 * 576,
     "dw": 2 * 576 * 256 + 2 * 128 * 576,
 }
@@ -268,7 +269,7 @@ ISSUED_FLOPS_PER_ROW = {
 
 def mfma_summary(mops_csv, util_csv, stats_csv, T=8192, rows=8192 * 8):
     """Markdown table per MFMA kernel: the MFMA work it issued (SQ_INSTS_VALU_MFMA_MOPS_BF16
-    x 512 FLOPs) against the algorithmic and the issued (recompute included) count, the
+    x 512 FLOPs) against the algorithmic and the issued count (ISSUED_FLOPS_PER_ROW), the
     achieved rate from its average duration in the --stats run, and rocprofv3's derived
     MfmaUtil (MFMA-busy share of the kernel's GPU cycles)."""
     import csv
@@ -279,7 +280,7 @@ def mfma_summary(mops_csv, util_csv, stats_csv, T=8192, rows=8192 * 8):
         for r in csv.DictReader(f):
             dur[r["Name"].replace("void ", "").split("(")[0]] = float(r["AverageNs"]) / 1e3
     lines = ["| bench kernel | HIP kernel | avg us | MOPS x 512 (GFLOP) | algorithmic GFLOP | "
-             "issued GFLOP (recompute included) | achieved TFLOP/s (MOPS) | % of 2500 | "
+             "issued GFLOP | achieved TFLOP/s (MOPS) | % of 2500 | "
              "MfmaUtil % |",
              "|---|---|---|---|---|---|---|---|---|"]
     for bname, prefixes in KERNEL_SYMBOLS.items():
