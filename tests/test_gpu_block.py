@@ -88,9 +88,12 @@ def check_router_gemm(x, W, logits, logit_bias, dt):
     bound = step * ref.abs() * 1.01 + 1e-5
     err = (logits.double() - ref).abs()
     assert bool((err <= bound).all()), f"router GEMM off by {float((err / bound).max()):.2f} steps"
-    cpu = (x @ W).float()
-    if logit_bias is not None:
-        cpu = (cpu + logit_bias).to(dt).float()
+    if logit_bias is None:
+        cpu = (x @ W).float()  # the CPU's own bf16 GEMM, as the reference computes it
+    else:
+        # the harness offset has no counterpart in the reference: its defined value is
+        # the fp32 product plus the offset, rounded once (what the kernel computes)
+        cpu = (x.float() @ W.float() + logit_bias.float()).to(dt).float()
     k = 6 if W.shape[1] >= 6 else 1
     flips = (R.route_from_logits(cpu, k, False, True, dt)[1]
              != R.route_from_logits(logits, k, False, True, dt)[1]).any(1).float().mean()
