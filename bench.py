@@ -47,8 +47,8 @@ def parse():
     ap.add_argument("--no-configs", action="store_true",
                     help="time only the headline workload (T=8192 fwd+bwd)")
     ap.add_argument("--single-stream", action="store_true",
-                    help="keep every kernel on one stream (the library's single_stream "
-                         "option), so that profiled kernels never overlap")
+                    help="keep every kernel on one stream (the library's default: the "
+                         "side_stream option off), so that profiled kernels never overlap")
     ap.add_argument("--mfma-summary", nargs=2, metavar=("MOPS_CSV", "MFMAUTIL_CSV"),
                     help="print the MFMA table from two rocprofv3 --pmc runs "
                          "(SQ_INSTS_VALU_MFMA_MOPS_BF16, MfmaUtil) and a --stats run's "
@@ -143,8 +143,8 @@ def time_gpu(m, x, g, steps: int, warmup: int):
     # Per-kernel launch times, from the library's HIP-event pairs on the launch stream, in a
     # pass of its own on one stream, so that no other kernel shares the GPU with the one
     # being timed.
-    prev = nat.get_option("single_stream")
-    nat.set_option("single_stream", 1)
+    prev = nat.get_option("side_stream")
+    nat.set_option("side_stream", 0)
     try:
         step()
         torch.cuda.synchronize()
@@ -161,7 +161,7 @@ def time_gpu(m, x, g, steps: int, warmup: int):
                 kernels[name] = (tot / n, n // steps)
         nat.timing_enable(0)
     finally:
-        nat.set_option("single_stream", prev)
+        nat.set_option("side_stream", prev)
 
     # forward only (train mode, no autograd)
     with torch.no_grad():
@@ -611,7 +611,7 @@ def main():
     if a.single_stream:
         from nanospeaker_amd import _native as nat
 
-        nat.set_option("single_stream", 1)
+        nat.set_option("side_stream", 0)
     if a.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; multi-GPU sharding is "
                                    "design-only, so --gpus must be 1"}))
@@ -622,15 +622,20 @@ def main():
     T = a.tokens
     if a.calibrate_copy:
         calibrate_copy()
-    m, x, g = build_block(T)
-    m, x, g = m.cuda(), x.cuda(), g.cuda()
     graph_ms = graph_fwd_ms = None
     if not a.eager:  # captured before any eager use of the module (torch's recipe)
         print(f"[bench] T={T} fwd+bwd, HIP graph", file=sys.stderr, flush=True)
+        m, x, g = (t.cuda() for t in build_block(T))
         graph_ms = graph_time(train_step_fn(m, x, g), a.steps, a.warmup)
         with torch.no_grad():
             graph_fwd_ms = graph_time(lambda: m(x), a.steps, a.warmup)
+        del m, x, g
+    # The eager timing on a fresh copy of the block (same seed, same weights): the graph
+    # recipe's side-stream warm-up leaves the parameters' gradient-accumulation nodes on
+    # that stream, and later eager steps of the same module would pay a cross-stream
+    # synchronisation per parameter.
     print(f"[bench] T={T} eager and per-kernel timing", file=sys.stderr, flush=True)
+    m, x, g = (t.cuda() for t in build_block(T))
     ms, fwd_ms, kernels, host_ms = time_gpu(m, x, g, a.steps, a.warmup)
     eager_ms, eager_fwd_ms = ms, fwd_ms
     if not a.eager:

@@ -57,8 +57,9 @@ int nsmoe_timing_read(const char* kernel_name, double* total_ms, int64_t* launch
 /* Tuning options (no counterpart in the reference; for tests and measurements).  Each is
  * process-wide, starts at 0 (= the library's own choice) and applies to calls made after
  * it is set.  Names and accepted values:
- *   "single_stream"  1: keep every kernel of a call on the caller's stream (no second
- *                    stream for the weight packing or the dW stage)
+ *   "side_stream"    1: run the weight packing and the dW stage of an eager block call on
+ *                    a second stream, forked and joined with events (default: every
+ *                    kernel on the caller's stream, which costs less host time)
  *   "fwd_rows"       rows per tile of the 16-bit forward expert kernel: 64 or 96
  *   "fwd_dist"       its weight prefetch distance in k-steps: 2 or 3
  *   "bwd_rows"       rows per tile of the GLU-backward kernel: 48, 64, 80 or 96 (96

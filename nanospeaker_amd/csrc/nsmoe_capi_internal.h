@@ -49,7 +49,7 @@ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 namespace nsmoe {
 // Process-wide tuning options (nsmoe_set_option); 0 means the library's own choice.
 enum OptionId : int {
-  OPT_SINGLE_STREAM = 0,
+  OPT_SIDE_STREAM = 0,
   OPT_FWD_ROWS,
   OPT_FWD_DIST,
   OPT_BWD_ROWS,

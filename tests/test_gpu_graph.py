@@ -101,9 +101,9 @@ def test_forward_replays_equal_eager():
 
 
 def test_side_stream_matches_single_stream():
-    """The library runs the weight packing and the dW stage on a second stream (forked
-    and joined with events); with the "single_stream" option everything stays on the
-    caller's stream.  Both orders must give the same bits, step after step (the pack
+    """With the "side_stream" option the library runs the weight packing and the dW stage
+    on a second stream (forked and joined with events); by default everything stays on
+    the caller's stream.  Both orders must give the same bits, step after step (the pack
     cache is emptied before each step, so every step packs on the side stream)."""
     m, x, g = _block(8192, seed=2)
     params = list(m.parameters())
@@ -116,9 +116,9 @@ def test_side_stream_matches_single_stream():
         grads = torch.autograd.grad([out, m.aux_loss], [xg] + params, [g, one])
         return [out.detach(), m.aux_loss.detach()] + list(grads)
 
-    two = [step() for _ in range(2)]
-    with lib_options(single_stream=1):
-        single = step()
+    with lib_options(side_stream=1):
+        two = [step() for _ in range(2)]
+    single = step()
     torch.cuda.synchronize()
     for r, vals in enumerate(two):
         for i, (a, b) in enumerate(zip(vals, single)):
