@@ -60,8 +60,10 @@ int nsmoe_timing_read(const char* kernel_name, double* total_ms, int64_t* launch
  *   "side_stream"    1: run the weight packing and the dW stage of an eager block call on
  *                    a second stream, forked and joined with events (default: every
  *                    kernel on the caller's stream, which costs less host time)
- *   "fwd_rows"       rows per tile of the 16-bit forward expert kernel: 64 or 96
- *   "fwd_dist"       its weight prefetch distance in k-steps: 2 or 3
+ *   "fwd_rows"       rows per tile of the 16-bit forward expert kernel: 32, 64 or 96
+ *   "fwd_dist"       its weight prefetch distance in k-steps: 2, 3 or 6 (6 with 32-row
+ *                    tiles only); a distance that does not divide both GEMMs' k-steps is
+ *                    not taken
  *   "bwd_rows"       rows per tile of the GLU-backward kernel: 48, 64, 80 or 96 (96
  *                    only when the forward saved the pre-activations)
  *   "bwd_dist"       its prefetch distance: 2, 3 or 4 (4 only with the pre-activations

@@ -42,12 +42,12 @@ struct OptionSpec {
   int64_t lo, hi;           // accepted range besides 0
   const int64_t* allowed;   // or an explicit list (terminated by 0), when non-NULL
 };
-static const int64_t kFwdRows[] = {64, 96, 0};
+static const int64_t kFwdRows[] = {32, 64, 96, 0};
 static const int64_t kBwdRows[] = {48, 64, 80, 96, 0};
 static const int64_t kDxRows[] = {64, 96, 0};
 static const OptionSpec kOptions[OPT_COUNT] = {
     {"side_stream", 1, 1, nullptr},   {"fwd_rows", 0, 0, kFwdRows},
-    {"fwd_dist", 2, 3, nullptr},      {"bwd_rows", 0, 0, kBwdRows},
+    {"fwd_dist", 2, 6, nullptr},      {"bwd_rows", 0, 0, kBwdRows},
     {"bwd_dist", 2, 4, nullptr},      {"dx_rows", 0, 0, kDxRows},
     {"dx_dist", 2, 4, nullptr},       {"xcd_run", 1, 1024, nullptr},
 };

@@ -262,14 +262,17 @@ __global__ void __launch_bounds__(NT, 2) expert_fwd_async_kernel(ExpParams p) {
 // for the weight registers are exact or stricter and leave the next step's loads in flight.
 // Shapes: d % 64 == 0 (an even number of GEMM1 steps) and an even number of GEMM2 steps.
 template <int DT, int NBW, int MB, int D>
-__global__ void __launch_bounds__(NT, MB == 6 || D == 3 ? 3 : 2) expert_fwd_reg_kernel(ExpParams p) {
+__global__ void __launch_bounds__(NT, MB > 2 && (MB == 6 || D == 3) ? 3 : 2)
+expert_fwd_reg_kernel(ExpParams p) {
   using G = Geo<DT>;
   using T = typename G::T;
   using M = Mma<DT>;
   using Frag = typename M::Frag;
   static_assert(G::ES == 2, "16-bit types only");
-  static_assert(MB == 4 || MB == 6, "64- or 96-row tiles");
-  static_assert(D == 2 || D == 3, "prefetch distance");
+  // 32-row tiles are for small problems (decode): few rows per group, so the tile streams
+  // the group's weights with a deeper prefetch instead of more rows.
+  static_assert(MB == 2 || MB == 4 || MB == 6, "32-, 64- or 96-row tiles");
+  static_assert(D == 2 || D == 3 || (MB == 2 && D == 6), "prefetch distance");
   constexpr int TM = MB * 16;            // tile rows
   constexpr int S = D + 1;               // token-tile ring stages
   // Token copies per wave per step: 4 16-byte slots per row, 256 per full copy; a tile
@@ -1883,6 +1886,13 @@ static int64_t tile_grid(const ExpParams& p, int bm) {
 
 template <int DT, int NBW>
 static void fwd_reg_launch(const ExpParams& p, int mb, int dist, hipStream_t s) {
+  if (mb == 2) {
+    const unsigned g2 = (unsigned)tile_grid(p, 32);
+    if (dist == 6) expert_fwd_reg_kernel<DT, NBW, 2, 6><<<g2, NT, 0, s>>>(p);
+    else if (dist == 3) expert_fwd_reg_kernel<DT, NBW, 2, 3><<<g2, NT, 0, s>>>(p);
+    else expert_fwd_reg_kernel<DT, NBW, 2, 2><<<g2, NT, 0, s>>>(p);
+    return;
+  }
   if (dist == 3) {
     if (mb == 6) expert_fwd_reg_kernel<DT, NBW, 6, 3><<<(unsigned)tile_grid(p, 96), NT, 0, s>>>(p);
     else expert_fwd_reg_kernel<DT, NBW, 4, 3><<<(unsigned)tile_grid(p, 64), NT, 0, s>>>(p);
@@ -1900,14 +1910,19 @@ int launch_fwd_async(int dtype, const ExpParams& p, int nbw, int64_t grid, hipSt
   const int n2 = ((p.d + NP2 - 1) / NP2) * p.out_kb;
   if (p.d % 64 == 0 && n2 % 2 == 0) {
     // 96-row tiles once 64-row tiles overflow the resident workgroup slots (3 per CU);
-    // the "fwd_rows" option forces a tile height.
-    int mb = tile_grid(p, 64) > 3 * (int64_t)device_cus() ? 6 : 4;
+    // 32-row tiles at prefetch distance 6 while 64-row tiles would fill under half the
+    // CUs (decode-sized calls: a tile's time is its weight stream's latency, not its
+    // rows).  The "fwd_rows" option forces a tile height.
+    const int64_t g64 = tile_grid(p, 64);
+    int mb = g64 > 3 * (int64_t)device_cus() ? 6 : 2 * g64 <= device_cus() ? 2 : 4;
     if (const int64_t v = option(OPT_FWD_ROWS)) mb = (int)(v / 16);
-    // Prefetch distance 2; the "fwd_dist" option asks for 3, taken where both GEMMs' step
-    // counts are multiples of 3.
+    // Prefetch distance 2 (6 for 32-row tiles); the "fwd_dist" option asks for another,
+    // taken where both GEMMs' step counts are multiples of it (6: 32-row tiles only).
     const int nk1 = p.in_kb;
-    int dist = option(OPT_FWD_DIST) == 3 ? 3 : 2;
-    if (dist == 3 && (nk1 % 3 != 0 || n2 % 3 != 0)) dist = 2;
+    auto divides = [&](int v) { return nk1 % v == 0 && n2 % v == 0; };
+    int dist = mb == 2 && divides(6) ? 6 : 2;
+    if (const int64_t v = option(OPT_FWD_DIST))
+      if ((v == 2 || v == 3 || (v == 6 && mb == 2)) && divides((int)v)) dist = (int)v;
     if (dtype == DT_BF16) {
       if (nbw == 1) fwd_reg_launch<DT_BF16, 1>(p, mb, dist, s);
       else fwd_reg_launch<DT_BF16, 2>(p, mb, dist, s);

@@ -101,15 +101,18 @@ def test_experts_forward_backward(dtype, shape, k, S, bias, T):
         check(f"grad {n}", g[n], ref_g[n], dtype)
 
 
-@pytest.mark.parametrize("dist", ["2", "3"])
-@pytest.mark.parametrize("mb", ["4", "6"])
+@pytest.mark.parametrize("dist", ["2", "3", "6"])
+@pytest.mark.parametrize("mb", ["2", "4", "6"])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("shape", ["wide_h64", "wide_h96", "ns_h128"])
 @pytest.mark.parametrize("T", [37, 300, 1000])
 def test_forward_tile_heights(dist, mb, dtype, shape, T):
-    """Both forward tile heights (64- and 96-row tiles, forced) and both weight prefetch
-    distances (2 and 3 steps; 3 only where the step counts divide) against the oracle,
-    with ragged last tiles and the shared experts' full-T groups."""
+    """Every forward tile height (32-, 64- and 96-row tiles, forced) and weight prefetch
+    distance (2, 3 and, for 32-row tiles, 6 steps; each only where the step counts
+    divide, else the library's own) against the oracle, with ragged last tiles and the
+    shared experts' full-T groups."""
+    if dist == "6" and mb != "2":
+        pytest.skip("distance 6 is for 32-row tiles")
     d, E, d_ff = SHAPES[shape]
     p, x, gout, tw, ti = make_case(d, E, d_ff, 6, 2, T % 2 == 0, T, dtype, seed=T + int(mb))
     ref_out, _ = oracle_fwd_bwd(p, x, gout, tw, ti, "silu", with_grad=False)

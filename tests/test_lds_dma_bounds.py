@@ -105,7 +105,7 @@ def dx_copies(MB):
     return out
 
 
-@pytest.mark.parametrize("kernel,MB", [("fwd", 4), ("fwd", 6), ("bwd", 3), ("bwd", 4),
+@pytest.mark.parametrize("kernel,MB", [("fwd", 2), ("fwd", 4), ("fwd", 6), ("bwd", 3), ("bwd", 4),
                                        ("bwd", 5), ("bwd", 6), ("dx", 4), ("dx", 6)])
 @pytest.mark.parametrize("d", [64, 128, 576])
 def test_copies_stay_in_bounds_and_match_the_fragment_layout(kernel, MB, d):
