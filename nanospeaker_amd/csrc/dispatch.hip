@@ -94,20 +94,31 @@ dispatch_place_kernel(const int64_t* __restrict__ topk_idx, int64_t M, int E,
   }
   for (int i = tid; i < waves * E; i += nt) s_mask[i] = 0ull;
 
-  // Column sums of hist: before this chunk, and over all chunks.
-  constexpr int UNR = 8;
+  // Column sums of hist: before this chunk, and over all chunks.  Thread tid owns expert
+  // base_e + tid % span and segment tid / span of that expert's column (span = E when the
+  // workgroup holds several segments per expert): a wave's lanes read consecutive experts
+  // of one chunk row, so each load instruction touches two or three cache lines.  A
+  // segment is requested in batches of UNR loads, one memory round trip for up to UNR
+  // chunk rows (256 chunks over 13 segments at T = 8192, E = 76).  The loads take 32-bit
+  // byte offsets from the uniform base (the launchers keep hist under 1 GiB), so each
+  // costs one VGPR.
+  constexpr int UNR = 24;
+  const char* hb = (const char*)hist;
   const int nseg = E <= nt ? nt / E : 1;
+  const int span = nseg > 1 ? E : nt;
   const int64_t L = (n_chunks + nseg - 1) / nseg;
-  for (int base_e = 0; base_e < E; base_e += nt / nseg) {
-    const int e = base_e + tid / nseg, seg = tid % nseg;
-    const bool own = tid / nseg < nt / nseg && e < E;
+  for (int base_e = 0; base_e < E; base_e += span) {
+    const int e = base_e + tid % span, seg = tid / span;
+    const bool own = seg < nseg && e < E;
     int32_t before = 0, total = 0;
     if (own) {
       const int64_t c0 = seg * L, c1 = c0 + L < n_chunks ? c0 + L : n_chunks;
       for (int64_t c = c0; c < c1; c += UNR) {
         int32_t v[UNR];
 #pragma unroll
-        for (int u = 0; u < UNR; ++u) v[u] = c + u < c1 ? hist[(c + u) * E + e] : 0;
+        for (int u = 0; u < UNR; ++u)
+          v[u] = c + u < c1 ? *(const int32_t*)(hb + (uint32_t)(((int)(c + u) * E + e) * 4))
+                            : 0;
 #pragma unroll
         for (int u = 0; u < UNR; ++u) {
           total += v[u];
@@ -118,11 +129,11 @@ dispatch_place_kernel(const int64_t* __restrict__ topk_idx, int64_t M, int E,
     s_seg_b[tid] = before;
     s_seg_t[tid] = total;
     __syncthreads();
-    if (own && seg == 0) {
+    if (own && seg == 0) {  // segments added in order
       int32_t b = 0, t = 0;
       for (int q = 0; q < nseg; ++q) {
-        b += s_seg_b[tid + q];
-        t += s_seg_t[tid + q];
+        b += s_seg_b[q * span + tid];
+        t += s_seg_t[q * span + tid];
       }
       s_base[e] = b;
       s_tot[e] = t;
@@ -261,6 +272,9 @@ int dispatch_launch(const int64_t* topk_idx, int64_t n_pairs, int32_t n_experts,
   }
   const int chunk = dispatch_chunk(n_experts);
   const int64_t n_chunks = cdiv(n_pairs, chunk);
+  NSMOE_REQUIRE(n_chunks * n_experts <= (int64_t)1 << 28,
+                "dispatch: %lld pairs over %d experts exceed the histogram's 1 GiB",
+                (long long)n_pairs, n_experts);
   const int64_t l_cap = nsmoe_dispatch_l_cap(n_pairs, n_experts);
   int32_t* hist = (int32_t*)workspace;
 
@@ -293,6 +307,9 @@ int dispatch_place_launch(const int64_t* topk_idx, int64_t n_pairs, int32_t n_ex
                 "dispatch_place: bad chunking (E %d, %d pairs per chunk)", n_experts,
                 chunk_pairs);
   NSMOE_REQUIRE(!bal || (bal->partial && bal->aux), "dispatch_place: balance buffers");
+  NSMOE_REQUIRE(n_chunks * n_experts <= (int64_t)1 << 28,
+                "dispatch_place: %lld chunks over %d experts exceed the histogram's 1 GiB",
+                (long long)n_chunks, n_experts);
   const int64_t l_cap = nsmoe_dispatch_l_cap(n_pairs, n_experts);
   const bool fold = bal != nullptr;
   const int group = 1024 / chunk_pairs;

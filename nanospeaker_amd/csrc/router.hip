@@ -4,8 +4,8 @@
 // for 16-bit blocks, in one launch instead of a library GEMM, the router tail and the
 // dispatch's histogram pass.
 //
-// router_fwd_kernel: one workgroup of 8 waves per 32 tokens (one workgroup per CU at
-// T = 8192).
+// router_fwd_kernel: one workgroup of 16 waves per 32 tokens (one workgroup per CU at
+// T = 8192).  All 16 waves issue the W_r loads.
 //   * GEMM, on 4 of the waves (16 tokens x half the experts each): v_mfma_f32_16x16x32 with
 //     the token rows as the A operand, read straight from global memory, and W_r as the B
 //     operand.  All of x
@@ -14,13 +14,15 @@
 //     untransposed in LDS and read back with ds_read_b64_tr_b16, which hands each lane 4
 //     consecutive k of one expert column.  The fp32 sums are rounded to the block's dtype
 //     -- the value router.py:69's GEMM produces -- stored as the logits, and kept in LDS.
-//   * Softmax and the selection, on all 8 waves: one token per 16-lane DPP row, a lane
+//   * Softmax and the selection, on 8 of the waves: one token per 16-lane DPP row, a lane
 //     holding E / 16 of its experts.  The selection is k rounds of arg-max; a round whose
 //     maximum is not unique among the values still in play (or a NaN in the row) leaves
 //     the token to the exact pass, since only the restated library algorithm fixes the
 //     order of equal keys.
-//   * The exact pass, on all 8 waves: one undecided token per wave, the restatement of
-//     CPU topk (topk_exact.h) on the keys as the selection saw them.
+//   * The exact pass, on all 16 waves: one undecided token per wave, the restatement of
+//     CPU topk (topk_exact.h) on the keys as the selection saw them.  About 17 % of bf16
+//     rows tie, 5.5 of a workgroup's 32 on average; with 16 waves no wave takes a second
+//     row unless more than 16 of the 32 tie, so the pass costs one row's latency.
 //   * With the RMSNorm in front (RouterArgs::norm_w), the GEMM waves normalise their rows
 //     in registers between the load and the first MFMA (the row's sum of squares over its
 //     4 lanes) and one of each row's two waves stores the normalised row.
@@ -37,8 +39,9 @@ namespace nsmoe {
 
 constexpr int RT_MMA_SPLIT = 2;             // GEMM waves per 16-token tile (column halves)
 constexpr int RT_MMA_WAVES = RT_TOK / 16 * RT_MMA_SPLIT;  // waves that run the GEMM
-constexpr int RT_WAVES = 8;                 // waves per workgroup (selection, exact pass)
+constexpr int RT_WAVES = 16;                // waves per workgroup (loads, exact pass)
 constexpr int RT_THREADS = RT_WAVES * 64;
+constexpr int RT_SEL_WAVES = RT_TOK / 4;    // waves of the selection: 4 tokens per wave
 
 // 16-lane DPP butterflies: every lane of each row of 16 ends with the row's reduction.
 template <class Op>
@@ -255,94 +258,96 @@ __global__ void __launch_bounds__(RT_THREADS) router_fwd_kernel(RouterArgs a) {
   __syncthreads();
 
   // ---- softmax and the fast selection: token 4 wave + g on lanes 16 g .. 16 g + 15 ------
-  const int tl = wave * 4 + g;
-  const int64_t t = tok0 + tl;
-  const bool live = t < T;
-  float key[NB];
-  bool nan_here = false;
-  float m = -INFINITY;
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    key[nb] = s_lg[tl * LGP + 16 * nb + j];
-    nan_here |= __builtin_isnan(key[nb]);
-    m = fmaxf(m, key[nb]);
-  }
-  const bool nan_row = row16_sum_i(nan_here ? 1 : 0) != 0;
-  m = row16(m, fmax_);
-  if (nan_row) m = __uint_as_float(0x7fc00000u);
-  float inv = 0.0f;
-  if (train || !normalize) {  // uniform
-    float ex[NB], s = 0.0f;
-#pragma unroll
+  if (wave < RT_SEL_WAVES) {  // uniform
+    const int tl = wave * 4 + g;
+    const int64_t t = tok0 + tl;
+    const bool live = t < T;
+    float key[NB];
+    bool nan_here = false;
+    float m = -INFINITY;
+  #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
-      ex[nb] = 16 * nb + j < E ? expf(key[nb] - m) : 0.0f;
-      s += ex[nb];
+      key[nb] = s_lg[tl * LGP + 16 * nb + j];
+      nan_here |= __builtin_isnan(key[nb]);
+      m = fmaxf(m, key[nb]);
     }
-    inv = 1.0f / row16(s, fadd_);
-    if (train) {
-#pragma unroll
+    const bool nan_row = row16_sum_i(nan_here ? 1 : 0) != 0;
+    m = row16(m, fmax_);
+    if (nan_row) m = __uint_as_float(0x7fc00000u);
+    float inv = 0.0f;
+    if (train || !normalize) {  // uniform
+      float ex[NB], s = 0.0f;
+  #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
-        const int e = 16 * nb + j;
-        if (e < E) {
-          const float p = ex[nb] * inv;
-          if (live) a.probs[t * E + e] = p;
-          key[nb] = p;
-          s_lg[tl * LGP + e] = p;  // the exact pass's keys and the column sums
+        ex[nb] = 16 * nb + j < E ? expf(key[nb] - m) : 0.0f;
+        s += ex[nb];
+      }
+      inv = 1.0f / row16(s, fadd_);
+      if (train) {
+  #pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          const int e = 16 * nb + j;
+          if (e < E) {
+            const float p = ex[nb] * inv;
+            if (live) a.probs[t * E + e] = p;
+            key[nb] = p;
+            s_lg[tl * LGP + e] = p;  // the exact pass's keys and the column sums
+          }
         }
       }
     }
-  }
-  if (j == 0) {
-    s_m[tl] = m;
-    s_inv[tl] = inv;
-  }
-  uint32_t avail = 0;
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) avail |= (16 * nb + j < E ? 1u : 0u) << nb;
-  bool exact = nan_row;
-  float s_sel = 0.0f;
-  int d_sel = 0;
-  for (int r = 0; r < k; ++r) {
-    float c = -INFINITY;
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-      if (avail >> nb & 1u) c = fmaxf(c, key[nb]);
-    const float mx = row16(c, fmax_);
-    int cnt = 0, loc = 1 << 20;
-#pragma unroll
-    for (int nb = NB - 1; nb >= 0; --nb)
-      if ((avail >> nb & 1u) && key[nb] == mx) {
-        ++cnt;
-        loc = 16 * nb + j;
+    if (j == 0) {
+      s_m[tl] = m;
+      s_inv[tl] = inv;
+    }
+    uint32_t avail = 0;
+  #pragma unroll
+    for (int nb = 0; nb < NB; ++nb) avail |= (16 * nb + j < E ? 1u : 0u) << nb;
+    bool exact = nan_row;
+    float s_sel = 0.0f;
+    int d_sel = 0;
+    for (int r = 0; r < k; ++r) {
+      float c = -INFINITY;
+  #pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+        if (avail >> nb & 1u) c = fmaxf(c, key[nb]);
+      const float mx = row16(c, fmax_);
+      int cnt = 0, loc = 1 << 20;
+  #pragma unroll
+      for (int nb = NB - 1; nb >= 0; --nb)
+        if ((avail >> nb & 1u) && key[nb] == mx) {
+          ++cnt;
+          loc = 16 * nb + j;
+        }
+      exact |= row16_sum_i(cnt) != 1;
+      const int id = row16_min_i(loc);
+      if ((id & 15) == j && id < (1 << 20)) avail &= ~(1u << (id >> 4));
+      if (j == r) {
+        s_sel = mx;
+        d_sel = id;
       }
-    exact |= row16_sum_i(cnt) != 1;
-    const int id = row16_min_i(loc);
-    if ((id & 15) == j && id < (1 << 20)) avail &= ~(1u << (id >> 4));
-    if (j == r) {
-      s_sel = mx;
-      d_sel = id;
     }
-  }
-  {
-    const bool o = j < k;
-    const float s = o ? s_sel : 0.0f;
-    float wgt = s;
-    if (train) {
-      if (normalize && k > 1) wgt = s / row16(s, fadd_);
-    } else if (normalize) {
-      const float mk = row16(o ? s : -INFINITY, fmax_);
-      const float e = o ? expf(s - mk) : 0.0f;
-      wgt = e * (1.0f / row16(e, fadd_));
-    } else {
-      wgt = expf(s - m) * inv;
+    {
+      const bool o = j < k;
+      const float s = o ? s_sel : 0.0f;
+      float wgt = s;
+      if (train) {
+        if (normalize && k > 1) wgt = s / row16(s, fadd_);
+      } else if (normalize) {
+        const float mk = row16(o ? s : -INFINITY, fmax_);
+        const float e = o ? expf(s - mk) : 0.0f;
+        wgt = e * (1.0f / row16(e, fadd_));
+      } else {
+        wgt = expf(s - m) * inv;
+      }
+      if (live && !exact && o) {
+        a.topk_idx[t * k + j] = d_sel;
+        ((ET*)a.topk_w)[t * k + j] = Elem<DT>::from_f(wgt);
+        atomicAdd(&s_hist[d_sel], 1);
+      }
+      if (live && exact && j == 0) s_tie[atomicAdd(&s_ntie, 1)] = tl;
     }
-    if (live && !exact && o) {
-      a.topk_idx[t * k + j] = d_sel;
-      ((ET*)a.topk_w)[t * k + j] = Elem<DT>::from_f(wgt);
-      atomicAdd(&s_hist[d_sel], 1);
-    }
-    if (live && exact && j == 0) s_tie[atomicAdd(&s_ntie, 1)] = tl;
-  }
+  }  // the selection waves
   __syncthreads();
 
   // ---- the exact pass for the undecided tokens: one wave per token -------------------
