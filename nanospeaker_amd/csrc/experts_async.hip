@@ -1443,6 +1443,126 @@ __global__ void __launch_bounds__(NT, D > 2 || MB == 6 ? 3 : 2) expert_dx_reg_ke
   wait_vmcnt<0>();
 }
 
+// expert_dx_res: the same dX rows for 96-row tiles, with the tile's dA1 rows (all 2H
+// columns: at most 8 k-steps of 32, 48 KiB) copied into LDS once and kept there for the
+// whole tile.  The ring kernel above copies each k-step again for every pass over the
+// output columns (3 passes at d = 576), and at 3 workgroups per CU those re-reads miss the
+// XCD's L2 (a tile's 48 KiB times 96 workgroups per XCD is past its 4 MiB): measured
+// FETCH_SIZE 2.4x the kernel's algorithmic reads.  With the tile resident, dA1 is read
+// once; the k-loop streams only the weight fragments, D steps ahead, and holds no
+// barrier (nothing is written to LDS after the copies land).
+template <int DT, int D>
+__global__ void __launch_bounds__(NT, 3) expert_dx_res_kernel(ExpParams p) {
+  using G = Geo<DT>;
+  using T = typename G::T;
+  using M = Mma<DT>;
+  using Frag = typename M::Frag;
+  static_assert(G::ES == 2, "16-bit types only");
+  static_assert(D >= 2 && D <= 4, "prefetch distance");
+  constexpr int MB = 6, TM = MB * 16;
+  constexpr int KMAX = 8;                 // resident k-steps: 2H <= 256
+  constexpr int A_BYTES = TM * G::ROWB;   // one k-step of the tile
+  constexpr int NBF = 3;                  // weight fragments per wave per step
+  __shared__ __attribute__((aligned(1024))) char s_tile[KMAX][A_BYTES];
+  __shared__ int s_loc[3];
+
+  const int tile = tile_of_block(p);
+  Located loc;
+  if (!locate(tile, p.E + p.S, [&](int g) { return (rows_of(p, g) + TM - 1) / TM; },
+              [](int) { return 0; }, s_loc, loc))
+    return;
+  const int g = loc.g, m0 = loc.local * TM;
+  const int rows = min(TM, rows_of(p, g) - m0);
+  const int64_t slot0 = row_start(p, g) + m0;
+  const int tid = threadIdx.x, lane = tid & 63, lc = lane & 15, lg = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int d = p.d, twoH = 2 * p.H;
+  const char* zero = (const char*)g_zero_kib + lane * 16;
+  const T* Win = per_group<T>(p.w_in, p.w_sh_in, g, p.E, (int64_t)d * twoH);
+  const int wk = (lane >> 4) * 8;
+  const int nkk = twoH / G::KC;  // <= KMAX (the launcher checks)
+  const int npass = (d + NP2 - 1) / NP2;
+  const int nsteps = npass * nkk;
+
+  // The tile's dA1 rows, every k-step, in the ring kernel's swizzled stage layout: slot c
+  // of stage kk holds chunk (c % 4) ^ swz(r) of row r = c / 4, k-step kk.  Copy one of
+  // wave w fills slots 64 w .. 64 w + 63 (rows 16 w .. 16 w + 15); copy two (lanes < 32)
+  // rows 64 + 8 w + lane / 4.  Rows past the tile read the zero page.
+  {
+    const int ar = tid >> 2, ac = (tid & 3) ^ swz<DT>(ar);
+    const T* arow = ar < rows ? (const T*)p.da1 + (slot0 + ar) * twoH + ac * G::VE : nullptr;
+    const int r2 = 64 + wave * 8 + (lane >> 2);
+    const int ac2 = (lane & 3) ^ swz<DT>(r2);
+    const T* arow2 =
+        lane < 32 && r2 < rows ? (const T*)p.da1 + (slot0 + r2) * twoH + ac2 * G::VE : nullptr;
+    for (int kk = 0; kk < nkk; ++kk) {  // uniform
+      const int k0 = kk * G::KC;
+      async_copy16(arow ? (const void*)(arow + k0) : (const void*)zero,
+                   s_tile[kk] + wave * 1024);
+      if (lane < 32)
+        async_copy16(arow2 ? (const void*)(arow2 + k0) : (const void*)zero,
+                     s_tile[kk] + 4096 + wave * 512);
+    }
+  }
+
+  struct WSet {
+    Frag f[NBF];
+  };
+  auto load_w = [&](int s) __attribute__((always_inline)) -> WSet {
+    const int pass = s / nkk, k0 = (s - pass * nkk) * G::KC;
+    WSet w;
+#pragma unroll
+    for (int j = 0; j < NBF; ++j) {
+      const int c = (pass * (NP2 / 16) + wave * 3 + j) * 16 + lc;
+      w.f[j] = M::load(c < d ? (const char*)(Win + (int64_t)c * twoH + k0 + wk) : zero);
+    }
+    return w;
+  };
+  WSet wset[D];
+#pragma unroll
+  for (int j = 0; j < D; ++j) wset[j] = load_w(j);
+  // The copies were issued before the D weight sets: once at most D * NBF operations are
+  // outstanding, every copy of this wave has landed; the barrier publishes all waves'.
+  wait_vmcnt<D * NBF>();
+  barrier_dma();
+
+  T* DX = (T*)p.dxrow + slot0 * d;
+  f32x4 acc[MB][3];
+  auto step = [&](int s, const WSet& w) __attribute__((always_inline)) {
+    const int pass = s / nkk, kk = s - pass * nkk;
+    if (kk == 0) {
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    const char* st = s_tile[kk];
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+      const Frag af = frag_sw<DT>(st, i * 16);
+#pragma unroll
+      for (int j = 0; j < 3; ++j) M::run(acc[i][j], w.f[j], af);
+    }
+    if (kk == nkk - 1)
+      store_rows_direct<DT, MB>(acc, DX, d, rows, pass * NP2 + wave * 48, lc, lg);
+  };
+  int s = 0;
+  for (; s + D < nsteps; s += D) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      wait_vmcnt<(D - 1) * NBF>();  // weight set s + j has landed
+      step(s + j, wset[j]);
+      wset[j] = load_w(s + j + D);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < D; ++j) {
+    wait_vmcnt_dyn((D - 1 - j) * NBF);  // a constant once unrolled
+    step(s + j, wset[j]);
+  }
+  wait_vmcnt<0>();
+}
+
 static int device_cus();
 static int64_t tile_grid(const ExpParams& p, int bm);
 
@@ -1484,7 +1604,11 @@ static void bwd_reg_launch(const ExpParams& p, int nbw, int dist, int mb, hipStr
 template <int DT>
 static void dx_reg_launch(const ExpParams& p, int mb, int dist, hipStream_t s) {
   const unsigned g4 = (unsigned)tile_grid(p, 64), g6 = (unsigned)tile_grid(p, 96);
-  if (mb == 6) {
+  if (mb == 6 && 2 * p.H <= 256) {  // the tile's dA1 rows fit the resident 48 KiB
+    if (dist == 4) expert_dx_res_kernel<DT, 4><<<g6, NT, 0, s>>>(p);
+    else if (dist == 3) expert_dx_res_kernel<DT, 3><<<g6, NT, 0, s>>>(p);
+    else expert_dx_res_kernel<DT, 2><<<g6, NT, 0, s>>>(p);
+  } else if (mb == 6) {
     if (dist == 4) expert_dx_reg_kernel<DT, 4, 6><<<g6, NT, 0, s>>>(p);
     else if (dist == 3) expert_dx_reg_kernel<DT, 3, 6><<<g6, NT, 0, s>>>(p);
     else expert_dx_reg_kernel<DT, 2, 6><<<g6, NT, 0, s>>>(p);

@@ -7,7 +7,8 @@ Every expert kernel stages its token rows through `async_copy16` (gemm_core.h): 
 This file restates, lane by lane, the address arithmetic of the copies in
 experts_async.hip -- the forward (`expert_fwd_reg_kernel`), the GLU backward
 (`expert_bwd_reg_kernel`, with and without the saved pre-activations) and dX
-(`expert_dx_reg_kernel`) -- and checks for every tile height, wave, lane, copy and k-step:
+(`expert_dx_reg_kernel`, and `expert_dx_res_kernel`, which keeps every k-step of its tile
+resident) -- and checks for every tile height, wave, lane, copy and k-step:
 
   * the global source lies inside its tensor ([T, d] rows of x / dout, [rows, 2H] rows of
     dA1) or is the lane's 16 bytes of the 1 KiB zero buffer;
@@ -130,6 +131,28 @@ def test_copies_stay_in_bounds_and_match_the_fragment_layout(kernel, MB, d):
         per_wave.setdefault((w, b), []).append(l)
     for (w, b), lanes in per_wave.items():
         assert sorted(lanes) == list(range(len(lanes)))
+
+
+@pytest.mark.parametrize("two_h", [64, 128, 192, 256])
+def test_dx_resident_tile_fits_its_stages(two_h):
+    """expert_dx_res_kernel copies all 2H / 32 k-steps of its 96-row tile up front, k-step
+    kk into stage kk of s_tile[8][96 x 64 B]: every copy stays inside the array, no two
+    land on the same bytes, and each global chunk stays inside the tile's dA1 rows."""
+    TM, KMAX = 96, 8
+    nkk = two_h // 32
+    assert nkk <= KMAX
+    stage = TM * ROWB
+    copies = dx_copies(6)
+    seen = set()
+    for kk in range(nkk):
+        for wave, lane, base, r, c in copies:
+            off = kk * stage + base + 16 * lane
+            assert 0 <= off and off + 16 <= KMAX * stage
+            assert off not in seen
+            seen.add(off)
+            assert off - kk * stage == r * ROWB + ((c ^ swz(r)) << 4)
+            assert kk * 32 + c * VE + VE <= two_h  # inside the row's 2H elements
+    assert len(seen) == nkk * TM * 4
 
 
 def test_backward_tiles_fit_their_ring_stages():
