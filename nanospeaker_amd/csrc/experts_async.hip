@@ -306,6 +306,10 @@ expert_fwd_reg_kernel(ExpParams p) {
   const int g = loc.g, m0 = loc.local * TM;
   const int rows = min(TM, rows_of(p, g) - m0);
   const int64_t slot0 = row_start(p, g) + m0;
+  // The first saved pre-activation block of the tile, read here with the other group
+  // offsets: inside the epilogue the load of offs[g] would come after the block stores
+  // and the GEMM2 weight loads, and waiting for it would wait for all of them.
+  const int64_t a1_blk0 = p.a1_out ? act_block(p, g, m0) : 0;
   const int tid = threadIdx.x, lane = tid & 63, lc = lane & 15, lg = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int d = p.d, H = p.H, twoH = 2 * p.H;
@@ -479,7 +483,7 @@ expert_fwd_reg_kernel(ExpParams p) {
           // column block is all in or all out.
           const int jb = wave * NBW + j;
           if (i * 16 + lc < rows && jb * 16 < H) {
-            T* blk = (T*)p.a1_out + act_block(p, g, m0 + i * 16) * (twoH / 16) * 256 + lane * 4;
+            T* blk = (T*)p.a1_out + (a1_blk0 + i) * (twoH / 16) * 256 + lane * 4;
             *(uint2*)(blk + jb * 256) =
                 make_uint2(pack2<DT>(accg[i][j][0] + bg[0], accg[i][j][1] + bg[1]),
                            pack2<DT>(accg[i][j][2] + bg[2], accg[i][j][3] + bg[3]));
