@@ -182,7 +182,8 @@ KERNEL_SYMBOLS = {
                    "nsmoe::expert_fwd_kernel"),
     "expert_bwd": ("nsmoe::expert_bwd_reg_kernel", "nsmoe::expert_bwd_async_kernel",
                    "nsmoe::expert_bwd_kernel"),
-    "expert_dx": ("nsmoe::expert_dx_reg_kernel", "nsmoe::expert_dx_async_kernel"),
+    "expert_dx": ("nsmoe::expert_dx_res_kernel", "nsmoe::expert_dx_reg_kernel",
+                  "nsmoe::expert_dx_async_kernel"),
     "dw": ("nsmoe::dw_pair_kernel",),
     "dw_in": ("nsmoe::dw_async_kernel<0, 0", "nsmoe::dw_kernel<0, 0"),
     "dw_out": ("nsmoe::dw_async_kernel<0, 1", "nsmoe::dw_kernel<0, 1"),
