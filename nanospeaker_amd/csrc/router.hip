@@ -7,13 +7,14 @@
 // router_fwd_kernel: one workgroup of 16 waves per 32 tokens (one workgroup per CU at
 // T = 8192).  All 16 waves issue the W_r loads.
 //   * GEMM, on 4 of the waves (16 tokens x half the experts each): v_mfma_f32_16x16x32 with
-//     the token rows as the A operand, read straight from global memory, and W_r as the B
-//     operand.  All of x
-//     and all of W_r are requested up front, one memory round trip for both.  W_r [d, E] is
-//     stored with the expert index contiguous, so chunks of its rows are staged
-//     untransposed in LDS and read back with ds_read_b64_tr_b16, which hands each lane 4
-//     consecutive k of one expert column.  The fp32 sums are rounded to the block's dtype
-//     -- the value router.py:69's GEMM produces -- stored as the logits, and kept in LDS.
+//     the token rows as the A operand, read straight from global memory into registers,
+//     and W_r as the B operand.  W_r [d, E] (87.5 KiB at d = 576, E = 76) is copied whole
+//     into LDS, untransposed, by LDS-DMA copies spread over all 16 waves, while the rows
+//     load: one memory round trip for both and one barrier before the MFMAs.  W_r is stored
+//     with the expert index contiguous, so its fragments are read with ds_read_b64_tr_b16,
+//     which hands each lane 4 consecutive k of one expert column.  The fp32 sums are
+//     rounded to the block's dtype -- the value router.py:69's GEMM produces -- stored as
+//     the logits, and kept in LDS.
 //   * Softmax and the selection, on 8 of the waves: one token per 16-lane DPP row, a lane
 //     holding E / 16 of its experts.  The selection is k rounds of arg-max; a round whose
 //     maximum is not unique among the values still in play (or a NaN in the row) leaves
@@ -25,7 +26,8 @@
 //     row unless more than 16 of the 32 tie, so the pass costs one row's latency.
 //   * With the RMSNorm in front (RouterArgs::norm_w), the GEMM waves normalise their rows
 //     in registers between the load and the first MFMA (the row's sum of squares over its
-//     4 lanes) and one of each row's two waves stores the normalised row.
+//     4 lanes) and one of each row's two waves stores the normalised row; the norm's weight
+//     arrives in LDS with W_r's copies.
 //   * Per workgroup it leaves the expert histogram of its tokens (a chunk of 32 k pairs for
 //     the dispatch's place pass) and, in training, the column sums of probs for the
 //     balance loss.
@@ -77,25 +79,21 @@ __device__ __forceinline__ int row16_min_i(int v) {
 __device__ __forceinline__ float fmax_(float a, float b) { return fmaxf(a, b); }
 __device__ __forceinline__ float fadd_(float a, float b) { return a + b; }
 
-// k-steps (32 rows of W_r) per staged chunk: the stage and the logit tile share the
-// workgroup's 64 KiB of LDS.
-template <int NB> constexpr int chunk_steps() { return 6; }
-
 template <int DT, int NB>
 __global__ void __launch_bounds__(RT_THREADS) router_fwd_kernel(RouterArgs a) {
   using ET = typename Elem<DT>::T;
   constexpr int NC = NB * 16;               // expert columns, padded to whole MFMA blocks
-  constexpr int PITCH = NC * 2 + 16;        // bytes per staged W_r row (16-byte pad)
-  constexpr int CS = chunk_steps<NB>();
-  constexpr int CK = CS * 32;               // W_r rows per staged chunk
-  constexpr int MAXC = (CK * (NC / 4) + RT_THREADS - 1) / RT_THREADS;  // pieces per thread
-  constexpr int MAXCH = (RT_MAX_STEPS + CS - 1) / CS;                    // chunks of W_r
+  // W_r whole in LDS, row-major as in memory ([d, E], E * 2 bytes a row), plus slack: the
+  // last row's padding columns [E, NC) read past its end (their logits are dropped).
+  constexpr int WR_BYTES = RT_MAX_STEPS * 32 * RT_MAX_E * 2 + 64;
   constexpr int LGP = NC + 1;               // logit-tile pitch (floats)
   constexpr int POS = RT_WAVES * 256 * (int)sizeof(int2);
-  constexpr int STAGE = CK * PITCH > POS ? CK * PITCH : POS;
-  // The W_r stage during the GEMM; the exact pass's swap slots afterwards.
-  __shared__ __align__(16) char s_stage[STAGE];
+  constexpr int STAGE = WR_BYTES > POS ? WR_BYTES : POS;
+  // W_r during the GEMM; the exact pass's swap slots afterwards.
+  __shared__ __align__(1024) char s_stage[STAGE];
+  __shared__ __align__(1024) char s_nw[(RT_MAX_STEPS * 64 + 1023) / 1024 * 1024];  // norm w
   __shared__ float s_lg[RT_TOK * LGP];      // per token: the logits, then its keys
+  __shared__ float s_bias[RT_MAX_E];
   __shared__ float s_m[RT_TOK], s_inv[RT_TOK];
   __shared__ int32_t s_hist[128];
   __shared__ int32_t s_tie[RT_TOK];
@@ -110,11 +108,33 @@ __global__ void __launch_bounds__(RT_THREADS) router_fwd_kernel(RouterArgs a) {
   const int64_t tok0 = (int64_t)blockIdx.x * RT_TOK;
   const bool mma_wave = wave < RT_MMA_WAVES;  // uniform
   const int nks = d >> 5;
+  const char* zero = (const char*)g_zero_kib + lane * 16;
 
-  // ---- GEMM ------------------------------------------------------------------------------
-  // A GEMM wave's 16 token rows, whole (d <= 32 RT_MAX_STEPS), requested first: one HBM
-  // round trip for all of them.  Lane (g, j) holds row tok + j, elements 32 ks + 8 g .. + 7
-  // (the A operand of k-step ks).
+  // ---- operands ----------------------------------------------------------------------------
+  // W_r (and the norm's weight) go global -> LDS by LDS-DMA copies, 1 KiB per wave
+  // instruction spread over all 16 waves, with no registers in flight and no staging
+  // pass; d E 2 is a multiple of 256 (d % 32 == 0, E % 4 == 0), so only the last copy of
+  // each is partial, its surplus lanes reading the zero page.
+  {
+    const int nw16 = (d * E * 2) >> 4;  // 16-byte chunks of W_r
+    const char* wsrc = (const char*)a.w;
+    for (int i = wave; i * 64 < nw16; i += RT_WAVES) {  // uniform
+      const int c = i * 64 + lane;
+      async_copy16(c < nw16 ? (const void*)(wsrc + c * 16) : (const void*)zero,
+                   s_stage + i * 1024);
+    }
+    if (a.norm_w) {
+      const int nn16 = (d * 2) >> 4;
+      const char* nsrc = (const char*)a.norm_w;
+      for (int i = wave; i * 64 < nn16; i += RT_WAVES) {
+        const int c = i * 64 + lane;
+        async_copy16(c < nn16 ? (const void*)(nsrc + c * 16) : (const void*)zero,
+                     s_nw + i * 1024);
+      }
+    }
+  }
+  // A GEMM wave's 16 token rows, whole (d <= 32 RT_MAX_STEPS), requested at once.  Lane
+  // (g, j) holds row tok + j, elements 32 ks + 8 g .. + 7 (the A operand of k-step ks).
   constexpr int NBH = (NB + RT_MMA_SPLIT - 1) / RT_MMA_SPLIT;  // column blocks per GEMM wave
   const int tile = wave / RT_MMA_SPLIT, cb0 = (wave % RT_MMA_SPLIT) * NBH;
   u32x4 xr[RT_MAX_STEPS];
@@ -125,6 +145,12 @@ __global__ void __launch_bounds__(RT_THREADS) router_fwd_kernel(RouterArgs a) {
     for (int ks = 0; ks < RT_MAX_STEPS; ++ks)
       if (ks < nks) xr[ks] = *(const u32x4*)(xp + ks * 32);
   }
+  for (int e = tid; e < 128; e += RT_THREADS) s_hist[e] = 0;
+  if (tid == 0) s_ntie = 0;
+  for (int e = tid; e < E; e += RT_THREADS) s_bias[e] = a.bias ? a.bias[e] : 0.0f;
+  wait_vmcnt<0>();  // this wave's copies (and loads) have landed
+  __syncthreads();  // every wave's copies and the LDS fills are visible
+
   if (a.norm_w && mma_wave) {  // uniform: RMSNorm of the rows in place (RouterArgs)
     // The row's sum of squares: this lane's 8 nks elements, then its 4 lanes (g = 0..3).
     const int64_t trow = tok0 + tile * 16 + j;
@@ -142,13 +168,13 @@ __global__ void __launch_bounds__(RT_THREADS) router_fwd_kernel(RouterArgs a) {
     ss += __shfl_xor(ss, 16, 64);
     ss += __shfl_xor(ss, 32, 64);
     const float rstd = 1.0f / sqrtf(ss / (float)d + a.norm_eps);
-    const ET* wn = (const ET*)a.norm_w + 8 * g;
+    const char* wn = s_nw + 16 * g;
     ET* xo = (ET*)a.xn + trow * d + 8 * g;
     const bool writer = cb0 == 0 && trow < T;  // one of the row's two GEMM waves
 #pragma unroll
     for (int ks = 0; ks < RT_MAX_STEPS; ++ks) {
       if (ks < nks) {
-        const u32x4 w = *(const u32x4*)(wn + ks * 32);
+        const u32x4 w = *(const u32x4*)(wn + ks * 64);
         u32x4 o;
 #pragma unroll
         for (int e = 0; e < 4; ++e)
@@ -160,79 +186,29 @@ __global__ void __launch_bounds__(RT_THREADS) router_fwd_kernel(RouterArgs a) {
     }
     if (writer && g == 0) a.rstd[trow] = rstd;
   }
+
+  // ---- GEMM: 18 k-steps from the resident W_r -------------------------------------------
+  // B fragment of k-step ks, column block nb: lane (g, j) reads rows 32 ks + 8 g + 4 h +
+  // j / 4 and columns 16 nb + 4 (j % 4) .. + 3, for h = 0, 1.
 #pragma unroll
   for (int nb = 0; nb < NBH; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // Pad columns [E, NC) of the stage stay zero: the loads never write them.
-  for (int i = tid; i < CK * (PITCH / 4); i += RT_THREADS) {
-    const int c = i % (PITCH / 4);
-    if (c * 4 >= E * 2) *(int32_t*)(s_stage + (i / (PITCH / 4)) * PITCH + c * 4) = 0;
-  }
-  for (int e = tid; e < 128; e += RT_THREADS) s_hist[e] = 0;
-  if (tid == 0) s_ntie = 0;
-  // W_r in chunks of CK rows: a chunk is CK E contiguous elements in global memory, read
-  // as 8-byte pieces (E % 4 == 0); piece f lands at row f / (E / 4), column
-  // 4 (f % (E / 4)) of the stage.
-  const int cpr = E >> 2;
-  const uint2* w8 = (const uint2*)a.w;
-  const int nchunk = (nks + CS - 1) / CS;
-  // Every chunk's pieces are requested now, beside x.
-  uint2 wreg[MAXCH][MAXC];
+  if (mma_wave) {
+    const int EP = E * 2;  // bytes per W_r row
+    const char* sb0 = s_stage + (8 * g + (j >> 2)) * EP + 8 * (j & 3);
 #pragma unroll
-  for (int c = 0; c < MAXCH; ++c) {
-    if (c < nchunk) {
-      const int n8 = min(CK, d - c * CK) * cpr;
-      const uint2* src = w8 + (int64_t)c * CK * cpr;
+    for (int ks = 0; ks < RT_MAX_STEPS; ++ks) {
+      if (ks < nks) {  // uniform
+        const char* sb = sb0 + ks * 32 * EP;
 #pragma unroll
-      for (int u = 0; u < MAXC; ++u)
-        if (tid + u * RT_THREADS < n8) wreg[c][u] = src[tid + u * RT_THREADS];
-    }
-  }
-  // Stage offsets of this thread's pieces, the same for every chunk.
-  int lds_off[MAXC];
-#pragma unroll
-  for (int u = 0; u < MAXC; ++u) {
-    const int f = tid + u * RT_THREADS;
-    const int r = f / cpr;
-    lds_off[u] = r * PITCH + (f - r * cpr) * 8;
-  }
-  auto store_w = [&](int c) {
-    const int n8 = min(CK, d - c * CK) * cpr;
-#pragma unroll
-    for (int u = 0; u < MAXC; ++u)
-      if (tid + u * RT_THREADS < n8) *(uint2*)(s_stage + lds_off[u]) = wreg[c][u];
-  };
-  __syncthreads();  // the pad zeros are in place before the first stage
-  store_w(0);
-  // B fragment addresses inside a stage: lane (g, j) reads rows 8 g + 4 h + j / 4 and
-  // columns 16 nb + 4 (j % 4) .. + 3, for h = 0, 1, of the k-step's 32 rows.
-  const int boff = (8 * g + (j >> 2)) * PITCH + 8 * (j & 3);
-#pragma unroll
-  for (int c = 0; c < MAXCH; ++c) {  // unrolled, so every register index is static
-    if (c >= nchunk) break;           // uniform
-    const bool more = c + 1 < nchunk;
-    __syncthreads();                  // stage c is complete
-    if (mma_wave) {
-#pragma unroll
-      for (int s = 0; s < CS; ++s) {
-        const int ks = c * CS + s;
-        if (ks < RT_MAX_STEPS && ks < nks) {  // uniform
-          const char* sb = s_stage + s * 32 * PITCH + boff;
-#pragma unroll
-          for (int nb = 0; nb < NBH; ++nb) {
-            if (cb0 + nb < NB) {  // uniform
-              const uint2 lo = lds_read_tr16(sb + (cb0 + nb) * 32);
-              const uint2 hi = lds_read_tr16(sb + 4 * PITCH + (cb0 + nb) * 32);
-              const typename Mma<DT>::Frag b{u32x4{lo.x, lo.y, hi.x, hi.y}};
-              Mma<DT>::run(acc[nb], typename Mma<DT>::Frag{xr[ks < RT_MAX_STEPS ? ks : 0]},
-                           b);
-            }
+        for (int nb = 0; nb < NBH; ++nb) {
+          if (cb0 + nb < NB) {  // uniform
+            const uint2 lo = lds_read_tr16(sb + (cb0 + nb) * 32);
+            const uint2 hi = lds_read_tr16(sb + 4 * EP + (cb0 + nb) * 32);
+            const typename Mma<DT>::Frag b{u32x4{lo.x, lo.y, hi.x, hi.y}};
+            Mma<DT>::run(acc[nb], typename Mma<DT>::Frag{xr[ks]}, b);
           }
         }
       }
-    }
-    if (more) {
-      __syncthreads();  // every GEMM wave is done with stage c
-      store_w(c + 1);
     }
   }
 
@@ -248,7 +224,7 @@ __global__ void __launch_bounds__(RT_THREADS) router_fwd_kernel(RouterArgs a) {
         if (cb0 + nb >= NB) continue;  // uniform
         const int e = 16 * (cb0 + nb) + j;
         float l = acc[nb][i];
-        if (a.bias && e < E) l += a.bias[e];
+        if (e < E) l += s_bias[e];
         const ET lv = Elem<DT>::from_f(l);
         if (t < T && e < E) ((ET*)a.logits)[t * E + e] = lv;
         s_lg[tl * LGP + e] = e < E ? Elem<DT>::to_f(lv) : -INFINITY;
@@ -426,6 +402,8 @@ static void launch_fwd(const RouterArgs& a, unsigned grid, hipStream_t s) {
 }
 
 int router_fused_launch(const RouterArgs& a, int dtype, hipStream_t s) {
+  NSMOE_REQUIRE(((uintptr_t)a.w & 15) == 0 && ((uintptr_t)a.norm_w & 15) == 0,
+                "router: the router weight and the norm weight must be 16-byte aligned");
   NSMOE_REQUIRE(router_fused_supported(dtype, a.d, a.E, a.k),
                 "router: the fused router takes bf16/fp16, d %% 32 == 0, d <= %d, "
                 "E %% 4 == 0, E <= %d, top_k <= %d (d %d, E %d, k %d)", 32 * RT_MAX_STEPS,

@@ -19,7 +19,8 @@ resident) -- and checks for every tile height, wave, lane, copy and k-step:
     r * 64 + ((c ^ swz(r)) << 4) (gemm_core.h sw_off);
 
 and the saved pre-activations' block index (experts_common.h act_block) stays inside the
-buffer the host sizes.  A forward variant with a producer-only wave, since removed, faulted
+buffer the host sizes.  The fused router (router.hip) copies its weight whole into LDS the
+same way; its copies and its transposed fragment reads are checked against its stage.  A forward variant with a producer-only wave, since removed, faulted
 the GPU once; it used the scalar-base ("saddr") form of the copy, a 32-bit vector offset
 from a 64-bit scalar base.  The copies kept use the 64-bit vaddr form, whose addresses are
 exactly the ones checked here.
@@ -153,6 +154,55 @@ def test_dx_resident_tile_fits_its_stages(two_h):
             assert off - kk * stage == r * ROWB + ((c ^ swz(r)) << 4)
             assert kk * 32 + c * VE + VE <= two_h  # inside the row's 2H elements
     assert len(seen) == nkk * TM * 4
+
+
+RT_MAX_STEPS, RT_MAX_E, RT_WAVES = 18, 80, 16   # router_fused.h / router.hip
+
+
+@pytest.mark.parametrize("d", [32, 64, 288, 576])
+@pytest.mark.parametrize("E", [4, 12, 16, 64, 76, 80])
+def test_router_weight_copies_and_fragment_reads_stay_in_the_stage(d, E):
+    """router_fwd_kernel copies W_r [d, E] whole into s_stage (copy i of a wave: 16-byte
+    chunks 64 i .. 64 i + 63 of the weight, landing at 1024 i + 16 lane; chunks past the
+    weight read the zero page) and reads the MFMA B fragments with ds_read_b64_tr_b16 at
+    row 32 ks + 8 g + 4 h + j / 4, byte 32 nb + 8 (j % 4) of E * 2-byte rows.  Every copy
+    and every 8-byte read stays inside the stage; every byte of the weight is copied once
+    to its own offset; reads past the weight (padding columns of the last rows) land in
+    the zero-filled tail of the last copy or the stage's slack."""
+    stage = max(RT_MAX_STEPS * 32 * RT_MAX_E * 2 + 64, RT_WAVES * 256 * 8)
+    nb_blocks = (E + 15) // 16
+    wbytes = d * E * 2
+    assert wbytes % 256 == 0
+    nw16 = wbytes // 16
+    written = set()
+    for wave in range(RT_WAVES):
+        i = wave
+        while i * 64 < nw16:
+            for lane in range(64):
+                c = i * 64 + lane
+                off = i * 1024 + 16 * lane
+                assert off + 16 <= stage
+                if c < nw16:
+                    assert off == c * 16  # chunk c of the weight at its own offset
+                    written.add(c)
+            i += RT_WAVES
+    assert written == set(range(nw16))
+    filled = -(-nw16 // 64) * 1024  # bytes the copies cover, zero-filled past the weight
+    ep = E * 2
+    nbh = -(-nb_blocks // 2)
+    for cb0 in (0, nbh):
+        for nb in range(cb0, min(cb0 + nbh, nb_blocks)):
+            for ks in range(d // 32):
+                for g in range(4):
+                    for j in range(16):
+                        for h in (0, 1):
+                            off = (32 * ks + 8 * g + 4 * h + j // 4) * ep + 32 * nb + 8 * (j % 4)
+                            assert off % 8 == 0 and off + 8 <= stage
+                            col = 16 * nb + 4 * (j % 4)
+                            if col < E:  # a real column: inside the weight's row
+                                assert off + 8 <= (32 * ks + 8 * g + 4 * h + j // 4 + 1) * ep
+                            else:      # padding column: read but dropped
+                                assert off + 8 <= max(filled, wbytes + 64)
 
 
 def test_backward_tiles_fit_their_ring_stages():
