@@ -104,8 +104,8 @@ def kernel_units(name: str, T: int, k: int, S: int, d: int, H: int, E: int):
         return T * ((k + S) * d * 2 + (E + 7) // 8 * 8 * 2 + d * 2 + k * 4), "hbm", "GB/s"
     if name == "router_dw":         # x and d(logits) read once
         return T * (d * 2 + (E + 7) // 8 * 8 * 2), "hbm", "GB/s"
-    if name == "pack":              # W_in (routed + shared) read once and written once
-        return (E + S) * d * 2 * H * 2 * 2, "hbm", "GB/s"
+    if name == "pack":              # W_in and W_out (routed + shared) read and written once
+        return (E + S) * (d * 2 * H + H * d) * 2 * 2, "hbm", "GB/s"
     return None
 
 
@@ -190,7 +190,7 @@ KERNEL_SYMBOLS = {
     "route_fwd": ("nsmoe::router_fwd_kernel", "nsmoe::route_fwd_kernel"),
     "combine": ("nsmoe::combine_kernel",),
     "combine_dx": ("nsmoe::combine_dx_kernel",),
-    "pack": ("nsmoe::pack_kernel", "nsmoe::pack_ks_kernel"),
+    "pack": ("nsmoe::pack_pair_kernel", "nsmoe::pack_kernel", "nsmoe::pack_ks_kernel"),
     "dispatch": ("nsmoe::dispatch_hist_kernel", "nsmoe::dispatch_place_kernel"),
     "router_dw": ("nsmoe::router_dw_kernel", "nsmoe::router_dw_reduce_kernel"),
 }

@@ -66,16 +66,16 @@ pack_kernel(const typename Elem<DT>::T* __restrict__ routed,
 // at once) and transposes it into that k block's LDS tile; after a barrier wave w writes
 // fragment (4 nt + w, kb) of each k block.  A workgroup per k block keeps only 32 threads
 // and 4 KB of loads in flight, which leaves the pass at about half of HBM's rate.
+// The tile is (g, nt, k blocks kb0 .. kb0 + KS - 1); `tile` is KS LDS tiles.
 template <int DT, int MODE, int KS>
-__global__ void __launch_bounds__(256)
-pack_ks_kernel(const typename Elem<DT>::T* __restrict__ routed,
-               const typename Elem<DT>::T* __restrict__ shared, int E, int d, int H, int HP,
-               int n_kb, int n_nb, char* __restrict__ out, int fast) {
+__device__ __forceinline__ void pack_ks_tile(const typename Elem<DT>::T* __restrict__ routed,
+                                             const typename Elem<DT>::T* __restrict__ shared,
+                                             int E, int d, int H, int HP, int n_kb, int n_nb,
+                                             char* __restrict__ out, int fast, int g, int nt,
+                                             int kb0, char (*tile)[64 * Geo<DT>::ROWB]) {
   using G = Geo<DT>;
   using T = typename G::T;
   static_assert(G::ES == 2 && KS * 32 <= 256, "16-bit types, at most 8 k blocks");
-  __shared__ __attribute__((aligned(16))) char tile[KS][64 * G::ROWB];
-  const int g = blockIdx.z, nt = blockIdx.y, kb0 = blockIdx.x * KS;
   const int K = MODE == 0 ? d : H;
   const int ld = MODE == 0 ? 2 * H : d;
   const int64_t gstride = MODE == 0 ? (int64_t)d * 2 * H : (int64_t)H * d;
@@ -130,6 +130,52 @@ pack_ks_kernel(const typename Elem<DT>::T* __restrict__ routed,
   }
 }
 
+// Both 16-bit packs in one launch: workgroups [0, n_in) pack W_in (6 k blocks each), the
+// rest W_out (4 k blocks each), so the two stacks stream together and W_out's
+// workgroups fill the tail of W_in's.  A workgroup's (k block group, column tile, group)
+// comes from its linear index, the k block groups fastest.
+constexpr int PACK_KS_IN = 6, PACK_KS_OUT = 4;
+
+struct PackPairArgs {
+  const void *w_in, *w_sh_in, *w_out, *w_sh_out;
+  int E, G, d, H, HP, in_kb, in_nb, out_kb, out_nb, fast;
+  char *p_in, *p_out;
+  int gx_in, gy_in, gx_out, gy_out;  // k block groups and column tiles of each part
+};
+
+template <int DT>
+__global__ void __launch_bounds__(256) pack_pair_kernel(PackPairArgs a) {
+  using G = Geo<DT>;
+  using T = typename G::T;
+  __shared__ __attribute__((aligned(16))) char tile[PACK_KS_IN][64 * G::ROWB];
+  const int per_in = a.gx_in * a.gy_in, in_blocks = per_in * a.G;
+  int b = blockIdx.x;
+  if (b < in_blocks) {  // uniform
+    const int g = b / per_in, r = b - g * per_in, nt = r / a.gx_in, bx = r - nt * a.gx_in;
+    pack_ks_tile<DT, 0, PACK_KS_IN>((const T*)a.w_in, (const T*)a.w_sh_in, a.E, a.d, a.H, a.HP,
+                                    a.in_kb, a.in_nb, a.p_in, a.fast, g, nt,
+                                    bx * PACK_KS_IN, tile);
+  } else {
+    b -= in_blocks;
+    const int per_out = a.gx_out * a.gy_out;
+    const int g = b / per_out, r = b - g * per_out, nt = r / a.gx_out, bx = r - nt * a.gx_out;
+    pack_ks_tile<DT, 1, PACK_KS_OUT>((const T*)a.w_out, (const T*)a.w_sh_out, a.E, a.d, a.H,
+                                     a.HP, a.out_kb, a.out_nb, a.p_out, a.fast, g, nt,
+                                     bx * PACK_KS_OUT, tile);
+  }
+}
+
+// W_in alone.
+template <int DT, int MODE, int KS>
+__global__ void __launch_bounds__(256)
+pack_ks_kernel(const typename Elem<DT>::T* __restrict__ routed,
+               const typename Elem<DT>::T* __restrict__ shared, int E, int d, int H, int HP,
+               int n_kb, int n_nb, char* __restrict__ out, int fast) {
+  __shared__ __attribute__((aligned(16))) char tile[KS][64 * Geo<DT>::ROWB];
+  pack_ks_tile<DT, MODE, KS>(routed, shared, E, d, H, HP, n_kb, n_nb, out, fast, blockIdx.z,
+                             blockIdx.y, blockIdx.x * KS, tile);
+}
+
 PackGeom pack_geom(int dtype, int d, int H, int E, int S) {
   PackGeom pg;
   const int es = dtype == DT_F32 ? 4 : 2;
@@ -152,10 +198,25 @@ static int launch_pack(const PackGeom& pg, const void* w_in, const void* w_out,
                        void* p_in, void* p_out, bool fast, hipStream_t s) {
   using T = typename Elem<DT>::T;
   const int G = E + S;
+  if constexpr (DT != DT_F32) {
+    if (p_out) {  // both stacks: one launch
+      PackPairArgs a{w_in, w_sh_in, w_out, w_sh_out, E, G, d, H, pg.hp, pg.in_kb, pg.in_nb,
+                     pg.out_kb, pg.out_nb, fast ? 1 : 0, (char*)p_in, (char*)p_out,
+                     (int)cdiv(pg.in_kb, PACK_KS_IN), pg.in_nb / 4,
+                     (int)cdiv(pg.out_kb, PACK_KS_OUT), pg.out_nb / 4};
+      const int64_t blocks =
+          ((int64_t)a.gx_in * a.gy_in + (int64_t)a.gx_out * a.gy_out) * (int64_t)G;
+      NSMOE_REQUIRE(blocks < (int64_t)INT32_MAX, "pack: %lld workgroups", (long long)blocks);
+      KernelTimer timer("pack", s);
+      pack_pair_kernel<DT><<<(unsigned)blocks, 256, 0, s>>>(a);
+      timer.stop();
+      return check_launch("pack_pair_kernel");
+    }
+  }
   {
     KernelTimer timer("pack", s);
     if constexpr (DT != DT_F32) {
-      constexpr int KS = 6;
+      constexpr int KS = PACK_KS_IN;
       dim3 grid((unsigned)cdiv(pg.in_kb, KS), (unsigned)(pg.in_nb / 4), (unsigned)G);
       pack_ks_kernel<DT, 0, KS><<<grid, 256, 0, s>>>((const T*)w_in, (const T*)w_sh_in, E, d,
                                                      H, pg.hp, pg.in_kb, pg.in_nb, (char*)p_in,
@@ -169,20 +230,14 @@ static int launch_pack(const PackGeom& pg, const void* w_in, const void* w_out,
     timer.stop();
     NSMOE_TRY(check_launch("pack_kernel<w_in>"));
   }
-  if (p_out) {
-    if constexpr (DT != DT_F32) {
-      constexpr int KS = 4;
-      dim3 grid((unsigned)cdiv(pg.out_kb, KS), (unsigned)(pg.out_nb / 4), (unsigned)G);
-      pack_ks_kernel<DT, 1, KS><<<grid, 256, 0, s>>>((const T*)w_out, (const T*)w_sh_out, E, d,
-                                                     H, pg.hp, pg.out_kb, pg.out_nb,
-                                                     (char*)p_out, fast ? 1 : 0);
-    } else {
+  if constexpr (DT == DT_F32) {  // 16-bit types pack W_out only beside W_in (above)
+    if (p_out) {
       dim3 grid((unsigned)pg.out_kb, (unsigned)(pg.out_nb / 4), (unsigned)G);
       pack_kernel<DT, 1><<<grid, 256, 0, s>>>((const T*)w_out, (const T*)w_sh_out, E, d, H,
                                              pg.hp, pg.out_kb, pg.out_nb, (char*)p_out,
                                              fast ? 1 : 0);
+      NSMOE_TRY(check_launch("pack_kernel<w_out>"));
     }
-    NSMOE_TRY(check_launch("pack_kernel<w_out>"));
   }
   return NSMOE_OK;
 }

@@ -245,7 +245,8 @@ __device__ __forceinline__ void sort_d(RegRow& a, int n) {
 
 // ---- the same steps, wave-parallel ---------------------------------------------------
 //
-// Unguarded Hoare partition of [first, last) around pivot a[first], computed from ranks.
+// Unguarded Hoare partition of [first, last) around pivot a[first] (key pk, which the
+// caller already holds), computed from ranks.
 // On the array as move_median_to_first left it, let L be the ascending positions in
 // (first, last) where the left scan stops (!gt(a[p], pivot)) and R the descending
 // positions in [first, last) where the right scan stops (!gt(pivot, a[p])).  Iteration i
@@ -257,8 +258,8 @@ __device__ __forceinline__ void sort_d(RegRow& a, int n) {
 // positions with ballots.  The swaps go through LDS: the element at L[i] (i < i*) is
 // written to slot i and the one at R[i] to slot 128 + i; then L[i] reads slot 128 + i
 // and R[i] reads slot i.  `kv` is the wave's [256] LDS scratch of (key, id) pairs.
-__device__ __forceinline__ int partition_parallel(RegRow& a, int first, int last, int2* kv) {
-  const uint32_t pk = a.key(first);
+__device__ __forceinline__ int partition_parallel(RegRow& a, int first, int last, int2* kv,
+                                                  uint32_t pk) {
   const int lane = a.lane;
   const int p0 = lane, p1 = lane + 64;
   const uint32_t x0 = (uint32_t)a.k0, x1 = (uint32_t)a.k1;
@@ -340,8 +341,26 @@ __device__ __forceinline__ void nth_element_par(RegRow& a, int nth, int n, int2*
       return;
     }
     --depth;
-    move_median_to_first_d(a, first, first + 1, first + (last - first) / 2, last - 1);
-    const int cut = partition_parallel(a, first, last, pos);
+    // move_median_to_first(first, first + 1, mid, last - 1) from one read of the four
+    // positions: the swap's values are then known scalars, and so is the pivot's key.
+    const int x = first + 1, y = first + (last - first) / 2, z = last - 1;
+    const KV ef = a.get(first), ex = a.get(x), ey = a.get(y), ez = a.get(z);
+    int m;
+    KV em;
+    if (gt(ex, ey)) {
+      if (gt(ey, ez)) m = y, em = ey;
+      else if (gt(ex, ez)) m = z, em = ez;
+      else m = x, em = ex;
+    } else if (gt(ex, ez)) {
+      m = x, em = ex;
+    } else if (gt(ey, ez)) {
+      m = z, em = ez;
+    } else {
+      m = y, em = ey;
+    }
+    a.set(first, em);
+    a.set(m, ef);
+    const int cut = partition_parallel(a, first, last, pos, em.key);
     if (cut <= nth) first = cut;
     else last = cut;
   }
