@@ -192,7 +192,7 @@ KERNEL_SYMBOLS = {
     "combine_dx": ("nsmoe::combine_dx_kernel",),
     "pack": ("nsmoe::pack_pair_kernel", "nsmoe::pack_kernel", "nsmoe::pack_ks_kernel"),
     "dispatch": ("nsmoe::dispatch_hist_kernel", "nsmoe::dispatch_place_kernel"),
-    "router_dw": ("nsmoe::router_dw_kernel", "nsmoe::router_dw_reduce_kernel"),
+    "router_dw": ("nsmoe::router_dw_kernel",),
 }
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                             "hbm_traffic_T8192.md")

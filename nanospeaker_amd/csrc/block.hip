@@ -372,7 +372,7 @@ int block_bwd_router(const nsmoe_experts_args* a, const nsmoe_experts_args& b,
   c.S = a->n_shared;
   c.E = E;
   c.ep = ldg;
-  NSMOE_TRY(combine_dx_launch(a->dtype, c, s));
+  // The router dW's partials first; their reduce rides in the combine_dx launch.
   RouterDwArgs r;
   r.x = b.x;
   r.glogits = gl;
@@ -382,7 +382,8 @@ int block_bwd_router(const nsmoe_experts_args* a, const nsmoe_experts_args& b,
   r.d = (int)a->d_model;
   r.E = E;
   r.ep = ldg;
-  return router_dw_launch(a->dtype, r, s);
+  NSMOE_TRY(router_dw_launch(a->dtype, r, s));
+  return combine_dx_launch(a->dtype, c, &r, s);
 }
 
 }  // namespace nsmoe

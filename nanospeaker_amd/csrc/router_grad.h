@@ -18,11 +18,11 @@ struct CombineDxArgs {
   int d, k, S, E, ep;
 };
 
-// W.grad = x^T glogits  (router_dw_kernel + router_dw_reduce_kernel)
+// W.grad = x^T glogits  (router_dw_kernel, then the reduce inside combine_dx's launch)
 struct RouterDwArgs {
   const void* x;         // [T, d]
   const void* glogits;   // [T, ep]
-  float* partial;        // [cdiv(T, 256), d, ep] fp32 scratch
+  float* partial;        // [cdiv(T, RDW_RC), d, ep] fp32 scratch (router_dw_partial_bytes)
   void* dw;              // [d, E] output
   int64_t T;
   int d, E, ep;
@@ -33,7 +33,11 @@ bool router_grad_supported(int dtype, int d, int E);
 // Row pitch of d(logits) on this path: E rounded up to 8 (16-byte rows).
 int router_logits_pitch(int E);
 size_t router_dw_partial_bytes(int64_t T, int d, int E);
-int combine_dx_launch(int dtype, const CombineDxArgs& a, hipStream_t stream);
+// combine_dx; with rdw set the same launch also reduces router_dw_kernel's partials into
+// rdw->dw (router_dw_launch must have run before it on the stream).
+int combine_dx_launch(int dtype, const CombineDxArgs& a, const RouterDwArgs* rdw,
+                      hipStream_t stream);
+// The router dW's partials (router_dw_kernel) alone.
 int router_dw_launch(int dtype, const RouterDwArgs& a, hipStream_t stream);
 
 }  // namespace nsmoe

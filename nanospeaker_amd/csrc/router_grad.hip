@@ -11,7 +11,9 @@
 //     same fp32 sum, so dx is written once.
 //   router_dw_kernel    fp32 partials of x^T d(logits) over chunks of RDW_RC tokens
 //                       (split over tokens: the output is only d x E)
-//   router_dw_reduce    the partials summed in chunk order -> W.grad in the module dtype
+//   router dW reduce    the partials summed in chunk order -> W.grad in the module dtype,
+//                       as extra workgroups of the combine_dx launch that follows
+//                       router_dw_kernel
 //
 // d(logits) arrives from route_bwd with a row pitch `ep` = E rounded up to 8 (16-byte rows,
 // zero in the pad columns), which both kernels read as MFMA operands directly.
@@ -26,11 +28,58 @@ constexpr int CDX_PITCH = CDX_COLS + 4;  // fp32 LDS row pitch (4 banks of skew 
 constexpr int CDX_KMAX = 8;   // top_k and shared counts of the gather fast path
 constexpr int CDX_SMAX = 2;
 constexpr int CDX_KS = 4;    // k-steps of 32 experts in the router term (E <= 128)
-constexpr int RDW_RC = 256;   // tokens per router_dw chunk
+constexpr int RDW_RC = 160;   // tokens per router_dw chunk: 5 k-steps
 constexpr int RDW_BMT = 64;   // columns of x (rows of W) per router_dw tile
 constexpr int RDW_BNT = 128;  // experts per router_dw tile (all of them: E <= 128)
-constexpr int RDW_S = 3;      // router_dw ring stages
+// router_dw ring stages: one more than a chunk's k-steps, so every copy of the chunk is
+// requested before the first MFMA (one memory round trip per workgroup instead of one per
+// two steps); 6 stages of 12 KiB, two workgroups per CU.  At T = 8192, d = 576: 52 chunks
+// x 9 column tiles = 468 workgroups, one round on 256 CUs.  Measured against 128, 256 and
+// 320 tokens per chunk (11.1 against 13.1, 16.9 and 12.5 us launch to launch), with the
+// reduce's extra partials costing 0.6 us in the combine_dx launch.
+constexpr int RDW_S = RDW_RC / 32 + 1;
 constexpr int RDW_LOADS = 8;  // router_dw_reduce: partials in flight per lane
+
+// W.grad[m][n] = sum over the chunks of partial[c][m][n], n < E.  Four lanes per 4-wide
+// output group: lane q sums chunks q, q + 4, q + 8, ... (RDW_LOADS of them in flight at a
+// time, in that order), then the four lane sums are added as (q0 + q1) + (q2 + q3): a fixed
+// order, so the result does not vary between runs.
+// Workgroup `blk` of the reduce (NT threads); workgroups past the output do nothing.
+template <int DT>
+__device__ __forceinline__ void router_dw_reduce_block(const RouterDwArgs& a, int nchunks,
+                                                       int64_t blk) {
+  using T = typename Elem<DT>::T;
+  const int n4 = a.ep / 4;
+  const int64_t i = (blk * NT + threadIdx.x) >> 2;
+  const int q = threadIdx.x & 3;
+  const bool live = i < (int64_t)a.d * n4;
+  const int m = live ? (int)(i / n4) : 0, n = live ? (int)(i % n4) * 4 : 0;
+  const int64_t mn = (int64_t)a.d * a.ep;
+  const float* src = a.partial + (int64_t)m * a.ep + n;
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int c0 = q; c0 < nchunks; c0 += 4 * RDW_LOADS) {
+    f32x4 v[RDW_LOADS];
+#pragma unroll
+    for (int u = 0; u < RDW_LOADS; ++u) {
+      const int c = c0 + 4 * u;
+      v[u] = live && c < nchunks ? *(const f32x4*)(src + (int64_t)c * mn) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int u = 0; u < RDW_LOADS; ++u) acc += v[u];
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float x1 = __shfl_xor(acc[e], 1, 64);  // (q0 + q1), (q2 + q3), in lane order
+    const float s01 = (q & 1) ? x1 + acc[e] : acc[e] + x1;
+    const float x2 = __shfl_xor(s01, 2, 64);
+    acc[e] = (q & 2) ? x2 + s01 : s01 + x2;
+  }
+  if (live && q == 0 && n < a.E)
+    *(uint2*)((T*)a.dw + (int64_t)m * a.E + n) =
+        make_uint2(pack2<DT>(acc[0], acc[1]), pack2<DT>(acc[2], acc[3]));
+}
+
+inline int64_t router_dw_reduce_blocks(int d, int ep) { return cdiv((int64_t)d * ep, NT); }
 
 // ---- combine_dx ----------------------------------------------------------------------------
 //
@@ -42,14 +91,24 @@ constexpr int RDW_LOADS = 8;  // router_dw_reduce: partials in flight per lane
 // expert rows (two 16-byte loads per row) and stores dx with two 16-byte stores.
 // W arrives packed in fragment order (RouterWPack: one 16-byte load per lane per fragment,
 // zero past E).
+//
+// With `rdw` set, workgroups past the token tiles (blockIdx.x >= tx) are the router dW's
+// reduce instead: its fp32 partials summed in chunk order into W.grad, streaming beside
+// the combine rather than as a launch of its own.
 template <int DT, int KM>
-__global__ void __launch_bounds__(NT, KM <= 6 ? 4 : 3) combine_dx_kernel(CombineDxArgs a) {
+__global__ void __launch_bounds__(NT, KM <= 6 ? 4 : 3)
+combine_dx_kernel(CombineDxArgs a, RouterDwArgs rdw, int rchunks, int tx) {
   using G = Geo<DT>;
   using T = typename G::T;
   using M = Mma<DT>;
   using Frag = typename M::Frag;
   __shared__ __attribute__((aligned(16))) float s_acc[4][16][CDX_PITCH];
   __shared__ __attribute__((aligned(1024))) char s_w[4 * CDX_KS][1024];  // the W tile
+  if ((int)blockIdx.x >= tx) {  // uniform: a router dW reduce workgroup
+    router_dw_reduce_block<DT>(rdw, rchunks,
+                               (int64_t)(blockIdx.x - tx) * gridDim.y + blockIdx.y);
+    return;
+  }
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t t0 = (int64_t)blockIdx.x * CDX_TOK + 16 * wave;
@@ -184,7 +243,7 @@ __device__ __forceinline__ int rdw_swz(int r) {
 }
 
 template <int DT>
-__global__ void __launch_bounds__(NT, 2) router_dw_kernel(RouterDwArgs a) {
+__global__ void __launch_bounds__(NT) router_dw_kernel(RouterDwArgs a) {
   using G = Geo<DT>;
   using T = typename G::T;
   using M = Mma<DT>;
@@ -289,43 +348,6 @@ __global__ void __launch_bounds__(NT, 2) router_dw_kernel(RouterDwArgs a) {
   }
 }
 
-// W.grad[m][n] = sum over the chunks of partial[c][m][n], n < E.  Four lanes per 4-wide
-// output group: lane q sums chunks q, q + 4, q + 8, ... (RDW_LOADS of them in flight at a
-// time, in that order), then the four lane sums are added as (q0 + q1) + (q2 + q3): a fixed
-// order, so the result does not vary between runs.
-template <int DT>
-__global__ void __launch_bounds__(NT) router_dw_reduce_kernel(RouterDwArgs a, int nchunks) {
-  using T = typename Elem<DT>::T;
-  const int n4 = a.ep / 4;
-  const int64_t i = ((int64_t)blockIdx.x * NT + threadIdx.x) >> 2;
-  const int q = threadIdx.x & 3;
-  const bool live = i < (int64_t)a.d * n4;
-  const int m = live ? (int)(i / n4) : 0, n = live ? (int)(i % n4) * 4 : 0;
-  const int64_t mn = (int64_t)a.d * a.ep;
-  const float* src = a.partial + (int64_t)m * a.ep + n;
-  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int c0 = q; c0 < nchunks; c0 += 4 * RDW_LOADS) {
-    f32x4 v[RDW_LOADS];
-#pragma unroll
-    for (int u = 0; u < RDW_LOADS; ++u) {
-      const int c = c0 + 4 * u;
-      v[u] = live && c < nchunks ? *(const f32x4*)(src + (int64_t)c * mn) : f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-#pragma unroll
-    for (int u = 0; u < RDW_LOADS; ++u) acc += v[u];
-  }
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const float x1 = __shfl_xor(acc[e], 1, 64);  // (q0 + q1), (q2 + q3), in lane order
-    const float s01 = (q & 1) ? x1 + acc[e] : acc[e] + x1;
-    const float x2 = __shfl_xor(s01, 2, 64);
-    acc[e] = (q & 2) ? x2 + s01 : s01 + x2;
-  }
-  if (live && q == 0 && n < a.E)
-    *(uint2*)((T*)a.dw + (int64_t)m * a.E + n) =
-        make_uint2(pack2<DT>(acc[0], acc[1]), pack2<DT>(acc[2], acc[3]));
-}
-
 // ---- launchers ------------------------------------------------------------------------------
 
 bool router_grad_supported(int dtype, int d, int E) {
@@ -339,20 +361,31 @@ size_t router_dw_partial_bytes(int64_t T, int d, int E) {
   return (size_t)cdiv(T, RDW_RC) * (size_t)d * (size_t)router_logits_pitch(E) * sizeof(float);
 }
 
-int combine_dx_launch(int dtype, const CombineDxArgs& a, hipStream_t s) {
+int combine_dx_launch(int dtype, const CombineDxArgs& a, const RouterDwArgs* rdw,
+                      hipStream_t s) {
   NSMOE_REQUIRE(router_grad_supported(dtype, a.d, a.E) && a.ep == router_logits_pitch(a.E),
                 "combine_dx: unsupported shape (d %d, E %d, pitch %d)", a.d, a.E, a.ep);
+  NSMOE_REQUIRE(!rdw || (rdw->d == a.d && rdw->ep == a.ep && rdw->T == a.T && rdw->partial &&
+                         rdw->dw),
+                "combine_dx: the folded router dW reduce takes the same shape");
   if (a.T == 0) return NSMOE_OK;
   NSMOE_REQUIRE(a.l_cap + (int64_t)a.S * a.T < INT32_MAX, "combine_dx: %lld rows exceed 2^31",
                 (long long)(a.l_cap + (int64_t)a.S * a.T));
-  const dim3 grid((unsigned)cdiv(a.T, CDX_TOK), (unsigned)cdiv(a.d, CDX_COLS));
+  const int64_t tx = cdiv(a.T, CDX_TOK), ty = cdiv(a.d, CDX_COLS);
+  const int64_t rx = rdw ? cdiv(router_dw_reduce_blocks(a.d, a.ep), ty) : 0;
+  NSMOE_REQUIRE(tx + rx < INT32_MAX, "combine_dx: %lld tokens", (long long)a.T);
+  const dim3 grid((unsigned)(tx + rx), (unsigned)ty);
+  const RouterDwArgs r = rdw ? *rdw : RouterDwArgs{};
+  const int rchunks = rdw ? (int)cdiv(a.T, RDW_RC) : 0;
   KernelTimer timer("combine_dx", s);
   if (a.k <= 6) {
-    if (dtype == DT_BF16) combine_dx_kernel<DT_BF16, 6><<<grid, NT, 0, s>>>(a);
-    else combine_dx_kernel<DT_F16, 6><<<grid, NT, 0, s>>>(a);
+    if (dtype == DT_BF16)
+      combine_dx_kernel<DT_BF16, 6><<<grid, NT, 0, s>>>(a, r, rchunks, (int)tx);
+    else combine_dx_kernel<DT_F16, 6><<<grid, NT, 0, s>>>(a, r, rchunks, (int)tx);
   } else {
-    if (dtype == DT_BF16) combine_dx_kernel<DT_BF16, CDX_KMAX><<<grid, NT, 0, s>>>(a);
-    else combine_dx_kernel<DT_F16, CDX_KMAX><<<grid, NT, 0, s>>>(a);
+    if (dtype == DT_BF16)
+      combine_dx_kernel<DT_BF16, CDX_KMAX><<<grid, NT, 0, s>>>(a, r, rchunks, (int)tx);
+    else combine_dx_kernel<DT_F16, CDX_KMAX><<<grid, NT, 0, s>>>(a, r, rchunks, (int)tx);
   }
   timer.stop();
   return check_launch("combine_dx_kernel");
@@ -363,17 +396,13 @@ int router_dw_launch(int dtype, const RouterDwArgs& a, hipStream_t s) {
                 "router_dw: unsupported shape (d %d, E %d, pitch %d)", a.d, a.E, a.ep);
   if (a.T == 0) return NSMOE_OK;
   const int64_t nchunks = cdiv(a.T, RDW_RC);
+  NSMOE_REQUIRE(nchunks < 65536, "router_dw: %lld tokens", (long long)a.T);
   const dim3 grid((unsigned)cdiv(a.d, RDW_BMT), (unsigned)nchunks);
   KernelTimer timer("router_dw", s);
   if (dtype == DT_BF16) router_dw_kernel<DT_BF16><<<grid, NT, 0, s>>>(a);
   else router_dw_kernel<DT_F16><<<grid, NT, 0, s>>>(a);
-  NSMOE_TRY(check_launch("router_dw_kernel"));
-  const int64_t nthreads = (int64_t)a.d * (a.ep / 4) * 4;
-  const unsigned rblocks = (unsigned)cdiv(nthreads, NT);
-  if (dtype == DT_BF16) router_dw_reduce_kernel<DT_BF16><<<rblocks, NT, 0, s>>>(a, (int)nchunks);
-  else router_dw_reduce_kernel<DT_F16><<<rblocks, NT, 0, s>>>(a, (int)nchunks);
   timer.stop();
-  return check_launch("router_dw_reduce_kernel");
+  return check_launch("router_dw_kernel");
 }
 
 }  // namespace nsmoe
