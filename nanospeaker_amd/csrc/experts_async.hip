@@ -21,6 +21,41 @@
 
 namespace nsmoe {
 
+// One 16-row block of a wave's 48-column slice of a 192-column pass, from the packed MFMA
+// accumulators: lo[j] / hi[j] hold columns cw + 16 j + 4 lg .. + 1 / + 2 .. + 3 of row
+// row0 + lc (lane 16 lg + lc).  Blocks 0 and 1 are regrouped across lanes (two permlane
+// swaps per dword) so that lane (lc, lg) holds columns cw + 8 lg .. + 7 of its row;
+// permlane32_swap(b0, b1) gives rows (b0.r0, b0.r1, b1.r0, b1.r1) and (b0.r2, b0.r3, b1.r2,
+// b1.r3), permlane16_swap of those (b0.r0, b0.r2, b1.r0, b1.r2) and (b0.r1, b0.r3, b1.r1,
+// b1.r3).  That 64-byte row segment and block 2's 32 bytes (columns cw + 32 + 4 lg ..) are
+// then moved to the quad-major lane order (bperm_to_quads), so each quad of lanes writes
+// one row's contiguous bytes: a 16-byte store and an 8-byte store per lane.  cw is
+// wave-uniform; rows at or past `rows` and columns at or past d are not written.
+template <int DT>
+__device__ __forceinline__ void store_block48(const uint32_t (&lo)[3], const uint32_t (&hi)[3],
+                                              typename Elem<DT>::T* Y, int d, int row0,
+                                              int rows, int cw, int lane) {
+  using T = typename Elem<DT>::T;
+  if (cw + 32 <= d) {
+    const auto l32 = __builtin_amdgcn_permlane32_swap(lo[0], lo[1], false, false);
+    const auto h32 = __builtin_amdgcn_permlane32_swap(hi[0], hi[1], false, false);
+    const auto l16 = __builtin_amdgcn_permlane16_swap(l32[0], l32[1], false, false);
+    const auto h16 = __builtin_amdgcn_permlane16_swap(h32[0], h32[1], false, false);
+    const int qa = bperm_to_quads(lane);
+    const u32x4 v = bperm4(qa, u32x4{l16[0], h16[0], l16[1], h16[1]});
+    const uint32_t b2lo = bperm(qa, lo[2]), b2hi = bperm(qa, hi[2]);
+    const int m = row0 + (lane >> 2), c = lane & 3;
+    if (m < rows) {
+      T* yrow = Y + (int64_t)m * d;
+      *(u32x4*)(yrow + cw + c * 8) = v;
+      if (cw + 32 < d) *(uint2*)(yrow + cw + 32 + c * 4) = make_uint2(b2lo, b2hi);
+    }
+  } else if (cw < d) {
+    const int m = row0 + (lane & 15);
+    if (m < rows) *(uint2*)(Y + (int64_t)m * d + cw + (lane >> 4) * 4) = make_uint2(lo[0], hi[0]);
+  }
+}
+
 // ============================ forward ====================================================
 //
 // One workgroup = 4 waves = one 64-row tile of one group.
@@ -582,11 +617,9 @@ expert_fwd_reg_kernel(ExpParams p) {
         // + b_out, * gate.  The wave's 48 columns of this pass are blocks 0..2; blocks 0
         // and 1 are regrouped across lanes (two permlane swaps per dword) so that lane
         // (lc, lg) holds columns cw + 8 lg .. + 7 of its row and stores them in one 16-byte
-        // store (16 rows x 64 contiguous bytes per instruction); block 2 leaves in 8-byte
-        // stores.  Lanes hold 4 consecutive columns per block: row r = lg of a 16-lane
-        // group holds columns 4 r .. 4 r + 3.  permlane32_swap(b0, b1) gives rows
-        // (b0.r0, b0.r1, b1.r0, b1.r1) and (b0.r2, b0.r3, b1.r2, b1.r3); permlane16_swap of
-        // those gives (b0.r0, b0.r2, b1.r0, b1.r2) and (b0.r1, b0.r3, b1.r1, b1.r3).
+        // store; block 2 leaves in 8-byte stores (the permlane steps are store_block48's).
+        // The stores stay in the MFMA lane order: the quad-major order of store_block48
+        // costs this kernel more registers than it has (measured slower with the spills).
         const int cw = pass * NP2 + wave * 48;  // wave-uniform
         float bo[3][4];
 #pragma unroll
@@ -604,7 +637,6 @@ expert_fwd_reg_kernel(ExpParams p) {
         }
 #pragma unroll
         for (int i = 0; i < MB; ++i) {
-          const int m = i * 16 + lc;
           const float wt = wrow[i];
           uint32_t lo[3], hi[3];
 #pragma unroll
@@ -612,6 +644,7 @@ expert_fwd_reg_kernel(ExpParams p) {
             lo[j] = pack2<DT>((acc[i][j][0] + bo[j][0]) * wt, (acc[i][j][1] + bo[j][1]) * wt);
             hi[j] = pack2<DT>((acc[i][j][2] + bo[j][2]) * wt, (acc[i][j][3] + bo[j][3]) * wt);
           }
+          const int m = i * 16 + lc;
           T* yrow = Y + (int64_t)m * d;
           if (cw + 32 <= d) {
             const auto l32 = __builtin_amdgcn_permlane32_swap(lo[0], lo[1], false, false);
@@ -1007,6 +1040,7 @@ __global__ void __launch_bounds__(NT, SA && MB <= 4 ? 3 : 2) expert_bwd_reg_kern
   const char* zero = (const char*)g_zero_kib + lane * 16;
   const char* P1 = p.p_in + (int64_t)g * p.in_nb * p.in_kb * G::PKB + lane * G::FRAGB;
   // W_out fragment rows: lane l reads row (jb * 16 + l % 16), k elements 8 * (l / 16) ..
+  // (the MFMA lane order; the quad-major order with ds_bpermute measured no faster here)
   const T* Wout = per_group<T>(p.w_out, p.w_sh_out, g, p.E, (int64_t)H * d);
   const int wk = (lane >> 4) * 8;
   const int nk = p.in_kb;
@@ -1260,44 +1294,20 @@ __global__ void __launch_bounds__(NT, SA && MB <= 4 ? 3 : 2) expert_bwd_reg_kern
 
 // Rows of a wave's 48-column slice of one 192-column pass, straight from the MFMA
 // accumulators (acc[i][j]: row block i, column block j; lane (lc, lg) holds columns
-// 4 lg .. 4 lg + 3 of row lc in each).  Blocks 0 and 1 are regrouped across lanes (two
-// permlane swaps per dword) so that lane (lc, lg) holds columns cw + 8 lg .. + 7 of its
-// row and stores them with one 16-byte store; block 2 leaves in 8-byte stores.
-// permlane32_swap(b0, b1) gives rows (b0.r0, b0.r1, b1.r0, b1.r1) and (b0.r2, b0.r3, b1.r2,
-// b1.r3); permlane16_swap of those gives (b0.r0, b0.r2, b1.r0, b1.r2) and (b0.r1, b0.r3,
-// b1.r1, b1.r3).  cw is wave-uniform; columns at or past d are not written.
+// 4 lg .. 4 lg + 3 of row lc in each), rounded to the element type (store_block48).
 template <int DT, int MB>
 __device__ __forceinline__ void store_rows_direct(const f32x4 (&acc)[MB][3],
                                                   typename Elem<DT>::T* Y, int d, int rows,
-                                                  int cw, int lc, int lg) {
-  using T = typename Elem<DT>::T;
+                                                  int cw, int lane) {
 #pragma unroll
   for (int i = 0; i < MB; ++i) {
-    const int m = i * 16 + lc;
     uint32_t lo[3], hi[3];
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
       lo[j] = pack2<DT>(acc[i][j][0], acc[i][j][1]);
       hi[j] = pack2<DT>(acc[i][j][2], acc[i][j][3]);
     }
-    T* yrow = Y + (int64_t)m * d;
-    if (cw + 32 <= d) {
-      const auto l32 = __builtin_amdgcn_permlane32_swap(lo[0], lo[1], false, false);
-      const auto h32 = __builtin_amdgcn_permlane32_swap(hi[0], hi[1], false, false);
-      const auto l16 = __builtin_amdgcn_permlane16_swap(l32[0], l32[1], false, false);
-      const auto h16 = __builtin_amdgcn_permlane16_swap(h32[0], h32[1], false, false);
-      if (m < rows) {
-        u32x4 v;
-        v[0] = l16[0];
-        v[1] = h16[0];
-        v[2] = l16[1];
-        v[3] = h16[1];
-        *(u32x4*)(yrow + cw + lg * 8) = v;
-        if (cw + 32 < d) *(uint2*)(yrow + cw + 32 + lg * 4) = make_uint2(lo[2], hi[2]);
-      }
-    } else if (cw < d && m < rows) {
-      *(uint2*)(yrow + cw + lg * 4) = make_uint2(lo[0], hi[0]);
-    }
+    store_block48<DT>(lo, hi, Y, d, i * 16, rows, cw, lane);
   }
 }
 
@@ -1335,21 +1345,24 @@ __global__ void __launch_bounds__(NT, D > 2 || MB == 6 ? 3 : 2) expert_dx_reg_ke
   const int d = p.d, twoH = 2 * p.H;
   const char* zero = (const char*)g_zero_kib + lane * 16;
   const T* Win = per_group<T>(p.w_in, p.w_sh_in, g, p.E, (int64_t)d * twoH);
-  const int wk = (lane >> 4) * 8;
-  const int nkk = twoH / G::KC;
+  const int wq = (lane & 3) * 8;  // this lane's k offset in a quad-major fragment
+  const int fq = bperm_from_quads(lane);
+  const int nkk = twoH / G::KC;  // <= KMAX in the resident-tile kernel (the launcher checks)
   const int npass = (d + NP2 - 1) / NP2;
   const int nsteps = npass * nkk;
 
   struct WSet {
     Frag f[NBF];
   };
+  // W_in fragments in the quad-major lane order (lane 4 r + q: row 16 block + r, 16-byte
+  // chunk q of the k-step), moved to the MFMA order with ds_bpermute when the step runs.
   auto load_w = [&](int s) __attribute__((always_inline)) -> WSet {
     const int pass = s / nkk, k0 = (s - pass * nkk) * G::KC;
     WSet w;
 #pragma unroll
     for (int j = 0; j < NBF; ++j) {
-      const int c = (pass * (NP2 / 16) + wave * 3 + j) * 16 + lc;
-      w.f[j] = M::load(c < d ? (const char*)(Win + (int64_t)c * twoH + k0 + wk) : zero);
+      const int c = (pass * (NP2 / 16) + wave * 3 + j) * 16 + (lane >> 2);
+      w.f[j] = M::load(c < d ? (const char*)(Win + (int64_t)c * twoH + k0 + wq) : zero);
     }
     return w;
   };
@@ -1391,17 +1404,20 @@ __global__ void __launch_bounds__(NT, D > 2 || MB == 6 ? 3 : 2) expert_dx_reg_ke
 #pragma unroll
         for (int j = 0; j < 3; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
+    Frag wf[NBF];
+#pragma unroll
+    for (int j = 0; j < NBF; ++j) wf[j].v = bperm4(fq, w.f[j].v);
     barrier_dma();
     const char* st = s_ring[s % S];
 #pragma unroll
     for (int i = 0; i < MB; ++i) {
       const Frag af = frag_sw<DT>(st, i * 16);
 #pragma unroll
-      for (int j = 0; j < 3; ++j) M::run(acc[i][j], w.f[j], af);
+      for (int j = 0; j < 3; ++j) M::run(acc[i][j], wf[j], af);
     }
     if constexpr (!STAGE_Y) {
       if (kk == nkk - 1) store_rows_direct<DT, MB>(acc, DX, d, rows, pass * NP2 + wave * 48,
-                                                    lc, lg);
+                                                    lane);
     } else if (kk == nkk - 1) {  // the pass's 192 columns: staged, then whole row segments out
 #pragma unroll
       for (int j = 0; j < 3; ++j) {
@@ -1483,8 +1499,9 @@ __global__ void __launch_bounds__(NT, 3) expert_dx_res_kernel(ExpParams p) {
   const int d = p.d, twoH = 2 * p.H;
   const char* zero = (const char*)g_zero_kib + lane * 16;
   const T* Win = per_group<T>(p.w_in, p.w_sh_in, g, p.E, (int64_t)d * twoH);
-  const int wk = (lane >> 4) * 8;
-  const int nkk = twoH / G::KC;  // <= KMAX (the launcher checks)
+  const int wq = (lane & 3) * 8;  // this lane's k offset in a quad-major fragment
+  const int fq = bperm_from_quads(lane);
+  const int nkk = twoH / G::KC;  // <= KMAX in the resident-tile kernel (the launcher checks)
   const int npass = (d + NP2 - 1) / NP2;
   const int nsteps = npass * nkk;
 
@@ -1512,13 +1529,15 @@ __global__ void __launch_bounds__(NT, 3) expert_dx_res_kernel(ExpParams p) {
   struct WSet {
     Frag f[NBF];
   };
+  // W_in fragments in the quad-major lane order (lane 4 r + q: row 16 block + r, 16-byte
+  // chunk q of the k-step), moved to the MFMA order with ds_bpermute when the step runs.
   auto load_w = [&](int s) __attribute__((always_inline)) -> WSet {
     const int pass = s / nkk, k0 = (s - pass * nkk) * G::KC;
     WSet w;
 #pragma unroll
     for (int j = 0; j < NBF; ++j) {
-      const int c = (pass * (NP2 / 16) + wave * 3 + j) * 16 + lc;
-      w.f[j] = M::load(c < d ? (const char*)(Win + (int64_t)c * twoH + k0 + wk) : zero);
+      const int c = (pass * (NP2 / 16) + wave * 3 + j) * 16 + (lane >> 2);
+      w.f[j] = M::load(c < d ? (const char*)(Win + (int64_t)c * twoH + k0 + wq) : zero);
     }
     return w;
   };
@@ -1540,15 +1559,18 @@ __global__ void __launch_bounds__(NT, 3) expert_dx_res_kernel(ExpParams p) {
 #pragma unroll
         for (int j = 0; j < 3; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
+    Frag wf[NBF];
+#pragma unroll
+    for (int j = 0; j < NBF; ++j) wf[j].v = bperm4(fq, w.f[j].v);
     const char* st = s_tile[kk];
 #pragma unroll
     for (int i = 0; i < MB; ++i) {
       const Frag af = frag_sw<DT>(st, i * 16);
 #pragma unroll
-      for (int j = 0; j < 3; ++j) M::run(acc[i][j], w.f[j], af);
+      for (int j = 0; j < 3; ++j) M::run(acc[i][j], wf[j], af);
     }
     if (kk == nkk - 1)
-      store_rows_direct<DT, MB>(acc, DX, d, rows, pass * NP2 + wave * 48, lc, lg);
+      store_rows_direct<DT, MB>(acc, DX, d, rows, pass * NP2 + wave * 48, lane);
   };
   int s = 0;
   for (; s + D < nsteps; s += D) {

@@ -238,6 +238,34 @@ __device__ __forceinline__ uint2 lds_read_tr16(const char* p) {
   return u;
 }
 
+// ---- 16 x 4 lane transposes (ds_bpermute) ------------------------------------------------
+//
+// The L1's address unit takes a wave's 16-byte accesses a lane quad (lanes 4 q .. 4 q + 3)
+// at a time, and a quad whose four addresses lie in one 64-byte segment costs about a
+// quarter of the cycles of a quad that touches four rows (rocprofv3 TA_TA_BUSY: ~16 against
+// ~64 cycles per wave access on gfx950).  The MFMA operand and accumulator layouts put the
+// 16 rows of a fragment on consecutive lanes -- lane 16 c + r holds row r, 16-byte chunk c
+// -- so a row-major operand read, or a row-major output written, in that order makes every
+// quad touch four rows.  Such accesses are issued in the quad-major order instead -- lane
+// 4 r + c holds row r, chunk c, each quad one row's 64 contiguous bytes -- and the data is
+// moved between the two orders across lanes with ds_bpermute (no LDS memory involved).
+//
+// bperm_from_quads(): the ds_bpermute byte address that gives lane l of the MFMA order the
+// value of quad-order lane 4 (l % 16) + l / 16; bperm_to_quads(): lane l of the quad order
+// takes MFMA-order lane 16 (l % 4) + l / 4.
+__device__ __forceinline__ int bperm_from_quads(int lane) {
+  return (4 * (lane & 15) + (lane >> 4)) << 2;
+}
+__device__ __forceinline__ int bperm_to_quads(int lane) {
+  return (16 * (lane & 3) + (lane >> 2)) << 2;
+}
+__device__ __forceinline__ uint32_t bperm(int addr, uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_ds_bpermute(addr, (int)v);
+}
+__device__ __forceinline__ u32x4 bperm4(int addr, const u32x4& v) {
+  return u32x4{bperm(addr, v[0]), bperm(addr, v[1]), bperm(addr, v[2]), bperm(addr, v[3])};
+}
+
 // Workgroup barrier for data that reached LDS by LDS-DMA copies the caller has already
 // waited for (vmcnt) and that no wave writes with ds_* stores in between: a bare
 // s_barrier plus a compiler barrier.  Unlike barrier_lds, no fence is involved, so loads

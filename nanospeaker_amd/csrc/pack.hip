@@ -94,10 +94,11 @@ __device__ __forceinline__ void pack_ks_tile(const typename Elem<DT>::T* __restr
     n0 = nt * 64;
     nlim = d;
   }
-  // This thread's 8 x 8 block: rows kb * 32 + kbl * 8 + r, columns n0 + nbl * 8 .. + 7 (the
-  // block numbering of TransStage: k block blk % 4, n block blk / 4).
+  // This thread's 8 x 8 block: rows kb * 32 + kbl * 8 + r, columns n0 + nbl * 8 .. + 7.  The
+  // column block is the fastest index, so each lane quad loads 64 contiguous bytes of one
+  // row (a quad over four rows costs the L1's address unit about three times as much).
   const int step = threadIdx.x >> 5, blk = threadIdx.x & 31;
-  const int kbl = blk & 3, nbl = blk >> 2;
+  const int kbl = blk >> 3, nbl = blk & 7;
   const int kb = kb0 + step;
   const bool on = step < KS && kb < n_kb;
   const int col = n0 + nbl * G::VE;
@@ -131,9 +132,11 @@ __device__ __forceinline__ void pack_ks_tile(const typename Elem<DT>::T* __restr
 }
 
 // Both 16-bit packs in one launch: workgroups [0, n_in) pack W_in (6 k blocks each), the
-// rest W_out (4 k blocks each), so the two stacks stream together and W_out's
-// workgroups fill the tail of W_in's.  A workgroup's (k block group, column tile, group)
-// comes from its linear index, the k block groups fastest.
+// rest W_out (4 k blocks each, two column tiles one after the other), so the two stacks
+// stream together in one round of resident workgroups (24 KiB of LDS each: 6 per CU; at
+// nanoSpeaker's shape 936 + 390 workgroups, where one W_out tile per workgroup made 1638).
+// A workgroup's (k block group, column tile, group) comes from its linear index, the k
+// block groups fastest.
 constexpr int PACK_KS_IN = 6, PACK_KS_OUT = 4;
 
 struct PackPairArgs {
@@ -157,11 +160,17 @@ __global__ void __launch_bounds__(256) pack_pair_kernel(PackPairArgs a) {
                                     bx * PACK_KS_IN, tile);
   } else {
     b -= in_blocks;
-    const int per_out = a.gx_out * a.gy_out;
-    const int g = b / per_out, r = b - g * per_out, nt = r / a.gx_out, bx = r - nt * a.gx_out;
-    pack_ks_tile<DT, 1, PACK_KS_OUT>((const T*)a.w_out, (const T*)a.w_sh_out, a.E, a.d, a.H,
-                                     a.HP, a.out_kb, a.out_nb, a.p_out, a.fast, g, nt,
-                                     bx * PACK_KS_OUT, tile);
+    const int gy2 = (a.gy_out + 1) / 2;
+    const int per_out = a.gx_out * gy2;
+    const int g = b / per_out, r = b - g * per_out, nt2 = r / a.gx_out, bx = r - nt2 * a.gx_out;
+    for (int u = 0; u < 2; ++u) {
+      const int nt = 2 * nt2 + u;
+      if (nt >= a.gy_out) break;  // uniform
+      if (u) __syncthreads();     // every wave is done reading the first tile's LDS
+      pack_ks_tile<DT, 1, PACK_KS_OUT>((const T*)a.w_out, (const T*)a.w_sh_out, a.E, a.d,
+                                       a.H, a.HP, a.out_kb, a.out_nb, a.p_out, a.fast, g, nt,
+                                       bx * PACK_KS_OUT, tile);
+    }
   }
 }
 
@@ -205,7 +214,7 @@ static int launch_pack(const PackGeom& pg, const void* w_in, const void* w_out,
                      (int)cdiv(pg.in_kb, PACK_KS_IN), pg.in_nb / 4,
                      (int)cdiv(pg.out_kb, PACK_KS_OUT), pg.out_nb / 4};
       const int64_t blocks =
-          ((int64_t)a.gx_in * a.gy_in + (int64_t)a.gx_out * a.gy_out) * (int64_t)G;
+          ((int64_t)a.gx_in * a.gy_in + (int64_t)a.gx_out * ((a.gy_out + 1) / 2)) * (int64_t)G;
       NSMOE_REQUIRE(blocks < (int64_t)INT32_MAX, "pack: %lld workgroups", (long long)blocks);
       KernelTimer timer("pack", s);
       pack_pair_kernel<DT><<<(unsigned)blocks, 256, 0, s>>>(a);
