@@ -105,11 +105,19 @@ int main() {
     return 1;
   }
   const int grid = 768, iters = 256;
-  hipEvent_t a, b; hipEventCreate(&a); hipEventCreate(&b);
+  hipEvent_t a, b;
+  (void)hipEventCreate(&a);
+  (void)hipEventCreate(&b);
   auto timeit = [&](const char* name, auto launch, double instrs_per_wave) {
-    launch(); hipDeviceSynchronize();
-    hipEventRecord(a); for (int r = 0; r < 5; ++r) launch(); hipEventRecord(b); hipEventSynchronize(b);
-    float ms; hipEventElapsedTime(&ms, a, b); ms /= 5;
+    launch();
+    (void)hipDeviceSynchronize();
+    (void)hipEventRecord(a);
+    for (int r = 0; r < 5; ++r) launch();
+    (void)hipEventRecord(b);
+    (void)hipEventSynchronize(b);
+    float ms = 0.0f;
+    (void)hipEventElapsedTime(&ms, a, b);
+    ms /= 5;
     const double waves_per_cu = grid * 4 / 256.0;
     const double cyc = ms * 1e-3 * 2.4e9;
     printf("%-22s %8.2f us  %7.1f cycles per wave-instr per CU (at 2.4 GHz)\n", name, ms * 1e3, cyc / (waves_per_cu * instrs_per_wave));
