@@ -982,10 +982,10 @@ __global__ void __launch_bounds__(NT, 2) expert_dx_async_kernel(ExpParams p) {
 }
 
 // expert_bwd_reg / expert_dx_reg: expert_bwd_async / expert_dx_async with the schedule of
-// expert_fwd_reg -- each wave's private weight fragments loaded from L2 into registers two
-// k-steps ahead, only the shared token tiles (x and dout; dA1 rows) copied through the
-// LDS ring, and every row output assembled in LDS and written as whole row segments with
-// 16-byte stores.  Step s waits until only what slot s - 1 issued is in flight; all loads
+// expert_fwd_reg -- the packed W_in fragments (when a1 is recomputed) and dX's W_in
+// fragments loaded into registers D k-steps ahead, the token tiles (x and dout; dA1 rows)
+// and the GLU backward's W_out fragments copied through LDS rings, and the GLU backward's
+// row outputs assembled in LDS and written as whole row segments with 16-byte stores.  Step s waits until only what slot s - 1 issued is in flight; all loads
 // of a steady step are unconditional (zero page for fragments past the edge).
 // Shapes: an even number of k-steps.
 
@@ -1014,8 +1014,12 @@ __global__ void __launch_bounds__(NT, SA && MB <= 4 ? 3 : 2) expert_bwd_reg_kern
   constexpr int DA_PITCH = 2 * HPMAX * G::ES + 16;  // staged dA1 rows
   constexpr int HB_PITCH = HPMAX * G::ES + 16;      // staged w h rows
   constexpr int RING = S * NA * A_BYTES;
+  // W_out fragments of the 4 waves for one k-step (NBW 16-row x 32-k fragments a wave),
+  // copied with the token tiles into an S-stage ring of their own after the token ring.
+  constexpr int WB = 4 * NBW * 1024;
+  constexpr int WRING = S * WB;
   constexpr int STAGE_BYTES = TM * (DA_PITCH + HB_PITCH);
-  constexpr int LDS_BYTES = RING > STAGE_BYTES ? RING : STAGE_BYTES;
+  constexpr int LDS_BYTES = RING + WRING > STAGE_BYTES ? RING + WRING : STAGE_BYTES;
   __shared__ __attribute__((aligned(1024))) char s_lds[LDS_BYTES];
   __shared__ int s_tok[TM];
   __shared__ int s_pair[TM];
@@ -1025,6 +1029,7 @@ __global__ void __launch_bounds__(NT, SA && MB <= 4 ? 3 : 2) expert_bwd_reg_kern
   char* s_da = s_lds;                   // epilogue staging, over the ring
   char* s_hb = s_lds + TM * DA_PITCH;
   auto ring = [&](int s) __attribute__((always_inline)) { return s_lds + (s % S) * NA * A_BYTES; };
+  auto wring = [&](int s) __attribute__((always_inline)) { return s_lds + RING + (s % S) * WB; };
 
   const int tile = tile_of_block(p);
   Located loc;
@@ -1039,14 +1044,17 @@ __global__ void __launch_bounds__(NT, SA && MB <= 4 ? 3 : 2) expert_bwd_reg_kern
   const int d = p.d, H = p.H, twoH = 2 * p.H;
   const char* zero = (const char*)g_zero_kib + lane * 16;
   const char* P1 = p.p_in + (int64_t)g * p.in_nb * p.in_kb * G::PKB + lane * G::FRAGB;
-  // W_out fragment rows: lane l reads row (jb * 16 + l % 16), k elements 8 * (l / 16) ..
-  // (the MFMA lane order; the quad-major order with ds_bpermute measured no faster here)
+  // W_out fragments reach LDS by LDS-DMA copies in the token tiles' swizzled row layout:
+  // copy slot l of fragment jb holds chunk (l % 4) ^ swz(l / 4) of W_out row jb * 16 + l / 4,
+  // so each lane quad reads one row's 64 contiguous bytes (a register load in the MFMA lane
+  // order makes every quad touch four rows, three times the address-unit cycles), and the
+  // step reads the fragment back with frag_sw.
   const T* Wout = per_group<T>(p.w_out, p.w_sh_out, g, p.E, (int64_t)H * d);
-  const int wk = (lane >> 4) * 8;
+  const int wo_row = lane >> 2, wo_chunk = (lane & 3) ^ swz<DT>(lane >> 2);
   const int nk = p.in_kb;
 
   struct WSet {
-    Frag f[NBF];
+    Frag f[GI > 0 ? GI : 1];  // the packed W_in gate / up fragments (recomputing a1 only)
   };
   auto load_w = [&](int s) __attribute__((always_inline)) -> WSet {
     const int k0 = s * G::KC;
@@ -1058,8 +1066,10 @@ __global__ void __launch_bounds__(NT, SA && MB <= 4 ? 3 : 2) expert_bwd_reg_kern
         w.f[j] = M::load(P1 + ((int64_t)jb * nk + s) * G::PKB);
         w.f[NBW + j] = M::load(P1 + ((int64_t)(HPMAX / 16 + jb) * nk + s) * G::PKB);
       }
-      const int n = jb * 16 + lc;
-      w.f[GI + j] = M::load(n < H ? (const char*)(Wout + (int64_t)n * d + k0 + wk) : zero);
+      const int n = jb * 16 + wo_row;
+      async_copy16(n < H ? (const void*)(Wout + (int64_t)n * d + k0 + wo_chunk * G::VE)
+                         : (const void*)zero,
+                   wring(s) + (wave * NBW + j) * 1024);
     }
     return w;
   };
@@ -1146,6 +1156,9 @@ __global__ void __launch_bounds__(NT, SA && MB <= 4 ? 3 : 2) expert_bwd_reg_kern
   auto mma = [&](int s, const WSet& w) __attribute__((always_inline)) {
     barrier_dma();
     const char* st = ring(s);
+    Frag gw[NBW];
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) gw[j] = frag_sw<DT>(wring(s) + (wave * NBW + j) * 1024, 0);
 #pragma unroll
     for (int i = 0; i < MB; ++i) {
       const Frag df = frag_sw<DT>(st + DOFF, i * 16);
@@ -1158,7 +1171,7 @@ __global__ void __launch_bounds__(NT, SA && MB <= 4 ? 3 : 2) expert_bwd_reg_kern
         }
       }
 #pragma unroll
-      for (int j = 0; j < NBW; ++j) M::run(accG[i][j], w.f[GI + j], df);
+      for (int j = 0; j < NBW; ++j) M::run(accG[i][j], gw[j], df);
     }
   };
   // Prologue order: w(0) .. w(D - 1) [row lookups] x(0) d(0) .. x(D - 1) d(D - 1), gate.
