@@ -7,10 +7,12 @@
 // router_fwd_kernel: one workgroup of 16 waves per 32 tokens (one workgroup per CU at
 // T = 8192).  All 16 waves issue the W_r loads.
 //   * GEMM, on 4 of the waves (16 tokens x half the experts each): v_mfma_f32_16x16x32 with
-//     the token rows as the A operand, read straight from global memory into registers,
-//     and W_r as the B operand.  W_r [d, E] (87.5 KiB at d = 576, E = 76) is copied whole
-//     into LDS, untransposed, by LDS-DMA copies spread over all 16 waves, while the rows
-//     load: one memory round trip for both and one barrier before the MFMAs.  W_r is stored
+//     the token rows as the A operand and W_r as the B operand.  The workgroup's 32 token
+//     rows (one contiguous 36 KiB block of x at d = 576) and W_r [d, E] (87.5 KiB at E = 76)
+//     are both copied whole into LDS, untransposed, by 1 KiB LDS-DMA copies spread over
+//     all 16 waves: one memory round trip and one barrier before the MFMAs, and every
+//     lane quad reads 64 contiguous bytes (register loads in the MFMA lane order would
+//     make each quad touch four rows).  W_r is stored
 //     with the expert index contiguous, so its fragments are read with ds_read_b64_tr_b16,
 //     which hands each lane 4 consecutive k of one expert column.  The fp32 sums are
 //     rounded to the block's dtype -- the value router.py:69's GEMM produces -- stored as
@@ -92,6 +94,9 @@ __global__ void __launch_bounds__(RT_THREADS) router_fwd_kernel(RouterArgs a) {
   // W_r during the GEMM; the exact pass's swap slots afterwards.
   __shared__ __align__(1024) char s_stage[STAGE];
   __shared__ __align__(1024) char s_nw[(RT_MAX_STEPS * 64 + 1023) / 1024 * 1024];  // norm w
+  // The workgroup's RT_TOK token rows, d * 2 bytes each, one contiguous block of x, copied
+  // whole by LDS-DMA (x_slot's chunk order inside each row).
+  __shared__ __align__(1024) char s_x[RT_TOK * RT_MAX_STEPS * 64];
   __shared__ float s_lg[RT_TOK * LGP];      // per token: the logits, then its keys
   __shared__ float s_bias[RT_MAX_E];
   __shared__ float s_m[RT_TOK], s_inv[RT_TOK];
@@ -133,23 +138,46 @@ __global__ void __launch_bounds__(RT_THREADS) router_fwd_kernel(RouterArgs a) {
       }
     }
   }
-  // A GEMM wave's 16 token rows, whole (d <= 32 RT_MAX_STEPS), requested at once.  Lane
-  // (g, j) holds row tok + j, elements 32 ks + 8 g .. + 7 (the A operand of k-step ks).
+  // The token rows: x[tok0 .. tok0 + RT_TOK) is one contiguous d * 2 * RT_TOK-byte block,
+  // copied by 1 KiB LDS-DMA copies over all 16 waves (whole 64-byte row segments per lane
+  // quad).  LDS slot (r, p) of row r holds the row's 16-byte chunk x_slot(p, r) (an
+  // involution: chunks of whole 8-chunk groups XORed with r % 8), so that the 16 rows a
+  // fragment read touches at one chunk position fall on 8 different bank groups.  Rows
+  // past T read the zero page.
+  const int cpr = d >> 3;                 // 16-byte chunks per row
+  const int cpr8 = cpr & ~7;
+  auto x_slot = [&](int c, int r) { return c < cpr8 ? c ^ (r & 7) : c; };
+  {
+    const int nslot = RT_TOK * cpr;
+    const char* xsrc = (const char*)a.x;
+    for (int i = wave; i * 64 < nslot; i += RT_WAVES) {  // uniform
+      const int s = i * 64 + lane;
+      const int r = s / cpr, p = s - r * cpr;
+      const bool ok = s < nslot && tok0 + r < T;
+      async_copy16(ok ? (const void*)(xsrc + ((tok0 + r) * d + x_slot(p, r) * 8) * 2)
+                      : (const void*)zero,
+                   s_x + i * 1024);
+    }
+  }
+  // A GEMM wave's 16 token rows, whole (d <= 32 RT_MAX_STEPS), read from LDS once the
+  // copies have landed.  Lane (g, j) holds row tok + j, elements 32 ks + 8 g .. + 7 (the A
+  // operand of k-step ks).
   constexpr int NBH = (NB + RT_MMA_SPLIT - 1) / RT_MMA_SPLIT;  // column blocks per GEMM wave
   const int tile = wave / RT_MMA_SPLIT, cb0 = (wave % RT_MMA_SPLIT) * NBH;
   u32x4 xr[RT_MAX_STEPS];
   f32x4 acc[NBH];
-  if (mma_wave) {
-    const ET* xp = (const ET*)a.x + min(tok0 + tile * 16 + j, T - 1) * d + 8 * g;
-#pragma unroll
-    for (int ks = 0; ks < RT_MAX_STEPS; ++ks)
-      if (ks < nks) xr[ks] = *(const u32x4*)(xp + ks * 32);
-  }
   for (int e = tid; e < 128; e += RT_THREADS) s_hist[e] = 0;
   if (tid == 0) s_ntie = 0;
   for (int e = tid; e < E; e += RT_THREADS) s_bias[e] = a.bias ? a.bias[e] : 0.0f;
-  wait_vmcnt<0>();  // this wave's copies (and loads) have landed
+  wait_vmcnt<0>();  // this wave's copies have landed
   __syncthreads();  // every wave's copies and the LDS fills are visible
+  if (mma_wave) {
+    const int r = tile * 16 + j;
+    const char* xl = s_x + r * cpr * 16;
+#pragma unroll
+    for (int ks = 0; ks < RT_MAX_STEPS; ++ks)
+      if (ks < nks) xr[ks] = *(const u32x4*)(xl + x_slot(ks * 4 + g, r) * 16);
+  }
 
   if (a.norm_w && mma_wave) {  // uniform: RMSNorm of the rows in place (RouterArgs)
     // The row's sum of squares: this lane's 8 nks elements, then its 4 lanes (g = 0..3).
