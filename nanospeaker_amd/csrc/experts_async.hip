@@ -614,12 +614,8 @@ expert_fwd_reg_kernel(ExpParams p) {
           }
         }
       } else {
-        // + b_out, * gate.  The wave's 48 columns of this pass are blocks 0..2; blocks 0
-        // and 1 are regrouped across lanes (two permlane swaps per dword) so that lane
-        // (lc, lg) holds columns cw + 8 lg .. + 7 of its row and stores them in one 16-byte
-        // store; block 2 leaves in 8-byte stores (the permlane steps are store_block48's).
-        // The stores stay in the MFMA lane order: the quad-major order of store_block48
-        // costs this kernel more registers than it has (measured slower with the spills).
+        // + b_out, * gate, then the wave's 48 columns of this pass (blocks 0..2) leave as
+        // whole row segments in the quad-major lane order (store_block48).
         const int cw = pass * NP2 + wave * 48;  // wave-uniform
         float bo[3][4];
 #pragma unroll
@@ -644,25 +640,12 @@ expert_fwd_reg_kernel(ExpParams p) {
             lo[j] = pack2<DT>((acc[i][j][0] + bo[j][0]) * wt, (acc[i][j][1] + bo[j][1]) * wt);
             hi[j] = pack2<DT>((acc[i][j][2] + bo[j][2]) * wt, (acc[i][j][3] + bo[j][3]) * wt);
           }
-          const int m = i * 16 + lc;
-          T* yrow = Y + (int64_t)m * d;
-          if (cw + 32 <= d) {
-            const auto l32 = __builtin_amdgcn_permlane32_swap(lo[0], lo[1], false, false);
-            const auto h32 = __builtin_amdgcn_permlane32_swap(hi[0], hi[1], false, false);
-            const auto l16 = __builtin_amdgcn_permlane16_swap(l32[0], l32[1], false, false);
-            const auto h16 = __builtin_amdgcn_permlane16_swap(h32[0], h32[1], false, false);
-            if (m < rows) {
-              u32x4 v;
-              v[0] = l16[0];
-              v[1] = h16[0];
-              v[2] = l16[1];
-              v[3] = h16[1];
-              *(u32x4*)(yrow + cw + lg * 8) = v;
-              if (cw + 32 < d) *(uint2*)(yrow + cw + 32 + lg * 4) = make_uint2(lo[2], hi[2]);
-            }
-          } else if (cw < d && m < rows) {
-            *(uint2*)(yrow + cw + lg * 4) = make_uint2(lo[0], hi[0]);
-          }
+          // The lane id passes an empty asm first, so the store's lane arithmetic is
+          // computed here rather than hoisted to the kernel's start, where it would stay
+          // live through GEMM1 (the kernel is at its register cap).
+          int sl = lane;
+          asm volatile("" : "+v"(sl));
+          store_block48<DT>(lo, hi, Y, d, i * 16, rows, cw, sl);
         }
       }
     }
