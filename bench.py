@@ -154,8 +154,9 @@ def time_gpu(m, x, g, steps: int, warmup: int):
             step()
         torch.cuda.synchronize()
         kernels = {}
-        for name in ("route_fwd", "dispatch", "pack", "expert_fwd", "combine", "expert_bwd",
-                     "expert_dx", "dw_in", "dw_out", "dw", "combine_dx", "router_dw"):
+        for name in ("route_fwd", "dispatch", "place_pack", "pack", "expert_fwd", "combine",
+                     "expert_bwd", "expert_dx", "dw_in", "dw_out", "dw", "combine_dx",
+                     "router_dw"):
             tot, n = nat.timing_read(name)
             if n:
                 kernels[name] = (tot / n, n // steps)
@@ -192,6 +193,7 @@ KERNEL_SYMBOLS = {
     "combine_dx": ("nsmoe::combine_dx_kernel",),
     "pack": ("nsmoe::pack_pair_kernel", "nsmoe::pack_kernel", "nsmoe::pack_ks_kernel"),
     "dispatch": ("nsmoe::dispatch_hist_kernel", "nsmoe::dispatch_place_kernel"),
+    "place_pack": ("nsmoe::dispatch_place_pack_kernel",),
     "router_dw": ("nsmoe::router_dw_kernel",),
 }
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",

@@ -19,6 +19,7 @@
 #include "experts_common.h"
 #include "norm.h"
 #include "pack.h"
+#include "pack_tile.h"
 #include "router_fused.h"
 #include "router_grad.h"
 #include "../../include/nsmoe.h"
@@ -166,9 +167,24 @@ extern "C" int nsmoe_block_fwd(const nsmoe_experts_args* a, const nsmoe_block_no
   // side stream while the latency-bound routing and dispatch kernels run on the caller's.
   hipStream_t s = (hipStream_t)stream;
   const bool pack = route_flags & NSMOE_BLOCK_PACK;
-  hipStream_t s_pack = pack ? side_fork(s, kSideSlotPack) : s;
-  int rc = pack ? nsmoe_pack_weights(&b, (void*)b.w_in_packed, (void*)b.w_out_packed, s_pack)
-                : NSMOE_OK;
+  // On the fused-router path the 16-bit packs run inside the dispatch's place launch, in
+  // workgroups of their own beside the placing ones (dispatch_place_launch), unless the
+  // side stream is asked for.
+  PackPairArgs pk{};
+  const bool pack_in_place =
+      pack && w_router && !option(OPT_SIDE_STREAM) &&
+      pack_pair_args(a->dtype, b.w_in, b.w_out, b.w_sh_in, b.w_sh_out, (int)b.n_experts,
+                     (int)b.n_shared, (int)b.d_model, (int)b.d_hidden, (void*)b.w_in_packed,
+                     (void*)b.w_out_packed, &pk);
+  hipStream_t s_pack = pack && !pack_in_place ? side_fork(s, kSideSlotPack) : s;
+  int rc = pack && !pack_in_place
+               ? nsmoe_pack_weights(&b, (void*)b.w_in_packed, (void*)b.w_out_packed, s_pack)
+               : NSMOE_OK;
+  if (pack_in_place) {  // nsmoe_pack_weights' own checks
+    NSMOE_REQUIRE(b.w_in && b.w_out, "block_fwd: NULL expert weights");
+    NSMOE_REQUIRE(b.n_shared == 0 || (b.w_sh_in && b.w_sh_out),
+                  "block_fwd: shared weights missing");
+  }
   if (w_router) {
     // Router GEMM + tail + the dispatch's histograms in the router's two launches; the
     // dispatch is then its place pass alone, with the balance loss in one more workgroup.
@@ -197,7 +213,8 @@ extern "C" int nsmoe_block_fwd(const nsmoe_experts_args* a, const nsmoe_block_no
     if (rc == NSMOE_OK)
       rc = dispatch_place_launch(topk_idx, m, E, r.hist, router_fused_chunks(T), RT_TOK * k,
                                  (int32_t*)b.sorted_ids, eids, (int32_t*)b.pad_offsets, counts,
-                                 npp, inv, probs ? &fold : nullptr, s);
+                                 npp, inv, probs ? &fold : nullptr, s,
+                                 pack_in_place ? &pk : nullptr, a->dtype);
   } else {
     // In training the route kernel also leaves the balance loss's per-workgroup column
     // sums of probs in the workspace, so probs is not read back for the loss.

@@ -29,6 +29,7 @@
 #include "balance.h"
 #include "nsmoe_capi_internal.h"
 #include "nsmoe_common.h"
+#include "pack_tile.h"
 
 namespace nsmoe {
 
@@ -62,25 +63,56 @@ dispatch_hist_kernel(const int64_t* __restrict__ topk_idx, int64_t M, int E,
 // fill are split over the workgroups; workgroup 0 also writes counts, offsets and the
 // padded total.  Column sums: thread (e, seg) owns a segment of expert e's column and
 // issues its loads together; the segment sums are added in LDS.
-__global__ void __launch_bounds__(1024)
-dispatch_place_kernel(const int64_t* __restrict__ topk_idx, int64_t M, int E,
-                      const int32_t* __restrict__ hist, int64_t n_chunks, int hist_group,
-                      int chunk_pairs, int64_t l_cap,
-                      int32_t* __restrict__ sorted_ids, int32_t* __restrict__ expert_ids,
-                      int32_t* __restrict__ offs, int32_t* __restrict__ counts,
-                      int32_t* __restrict__ npp, int32_t* __restrict__ inv,
-                      const float* __restrict__ bal_partial, int64_t bal_nblk, int64_t bal_T,
-                      float bal_coef, float* __restrict__ bal_aux) {
-  extern __shared__ unsigned long long s_mask[];  // [waves][E]
-  __shared__ int32_t s_base[DISPATCH_MAX_EXPERTS];
-  __shared__ int32_t s_tot[DISPATCH_MAX_EXPERTS];
-  __shared__ int32_t s_off[DISPATCH_MAX_EXPERTS + 1];
-  __shared__ int32_t s_seg_b[1024], s_seg_t[1024];
-  __shared__ int32_t s_wave[16];
-  __shared__ BalanceLds s_bal;
+struct PlaceParams {
+  const int64_t* topk_idx;
+  int64_t M;
+  int E;
+  const int32_t* hist;
+  int64_t n_chunks;
+  int hist_group, chunk_pairs;
+  int64_t l_cap;
+  int32_t *sorted_ids, *expert_ids, *offs, *counts, *npp, *inv;
+  const float* bal_partial;  // the folded balance loss (or NULL): one more workgroup
+  int64_t bal_nblk, bal_T;
+  float bal_coef;
+  float* bal_aux;
+};
+
+struct PlaceLds {
+  int32_t base[DISPATCH_MAX_EXPERTS];
+  int32_t tot[DISPATCH_MAX_EXPERTS];
+  int32_t off[DISPATCH_MAX_EXPERTS + 1];
+  int32_t seg_b[1024], seg_t[1024];
+  int32_t wave[16];
+  BalanceLds bal;
+};
+
+// The place pass of workgroup `chunk` (1024 threads); s_mask holds waves x E 64-bit masks.
+// UNR: histogram loads per thread in flight together.
+template <int UNR>
+__device__ __forceinline__ void place_body(const PlaceParams& P, int64_t chunk, PlaceLds& Ls,
+                                           unsigned long long* __restrict__ s_mask) {
+  const int64_t* __restrict__ topk_idx = P.topk_idx;
+  const int64_t M = P.M;
+  const int E = P.E;
+  const int32_t* __restrict__ hist = P.hist;
+  const int64_t n_chunks = P.n_chunks;
+  const int hist_group = P.hist_group, chunk_pairs = P.chunk_pairs;
+  const int64_t l_cap = P.l_cap;
+  int32_t* __restrict__ sorted_ids = P.sorted_ids;
+  int32_t* __restrict__ expert_ids = P.expert_ids;
+  int32_t* __restrict__ offs = P.offs;
+  int32_t* __restrict__ counts = P.counts;
+  int32_t* __restrict__ npp = P.npp;
+  int32_t* __restrict__ inv = P.inv;
+  int32_t* s_base = Ls.base;
+  int32_t* s_tot = Ls.tot;
+  int32_t* s_off = Ls.off;
+  int32_t* s_seg_b = Ls.seg_b;
+  int32_t* s_seg_t = Ls.seg_t;
+  int32_t* s_wave = Ls.wave;
   const int tid = threadIdx.x, nt = blockDim.x;
   const int lane = tid & 63, wave = tid >> 6, waves = nt >> 6;
-  const int64_t chunk = blockIdx.x;
 
   // This workgroup's pairs (the loads go out first) and the rank masks.  A workgroup
   // places chunk_pairs <= blockDim.x pairs, one per thread from thread 0: hist_group
@@ -102,7 +134,6 @@ dispatch_place_kernel(const int64_t* __restrict__ topk_idx, int64_t M, int E,
   // chunk rows (256 chunks over 13 segments at T = 8192, E = 76).  The loads take 32-bit
   // byte offsets from the uniform base (the launchers keep hist under 1 GiB), so each
   // costs one VGPR.
-  constexpr int UNR = 24;
   const char* hb = (const char*)hist;
   const int nseg = E <= nt ? nt / E : 1;
   const int span = nseg > 1 ? E : nt;
@@ -142,7 +173,8 @@ dispatch_place_kernel(const int64_t* __restrict__ topk_idx, int64_t M, int E,
   }
   const int64_t G = (n_chunks + hist_group - 1) / hist_group;  // the placing workgroups
   if (chunk == G) {  // the balance-loss workgroup (uniform): totals -> loss
-    balance_loss_block(bal_partial, bal_nblk, s_tot, bal_T, E, bal_coef, bal_aux, s_bal);
+    balance_loss_block(P.bal_partial, P.bal_nblk, s_tot, P.bal_T, E, P.bal_coef, P.bal_aux,
+                       Ls.bal);
     return;
   }
 
@@ -219,6 +251,68 @@ dispatch_place_kernel(const int64_t* __restrict__ topk_idx, int64_t M, int E,
   for (int64_t q = total + chunk * nt + tid; q < l_cap; q += G * nt) sorted_ids[q] = (int32_t)M;
 }
 
+
+__global__ void __launch_bounds__(1024) dispatch_place_kernel(PlaceParams P) {
+  extern __shared__ unsigned long long s_mask[];  // [waves][E]
+  __shared__ PlaceLds L;
+  place_body<24>(P, blockIdx.x, L, s_mask);
+}
+
+// The place pass with the 16-bit weight pack beside it, in one launch: workgroups
+// [0, n_place) place (as dispatch_place_kernel, E <= 128), the rest pack.  The pack does
+// not depend on the routing, and the place pass's few latency-bound workgroups leave most
+// CUs idle, so the packing runs in that time instead of in a launch of its own.
+// A packing workgroup is four groups of 256 threads, each packing one tile per round --
+// a W_in tile of PACK_FUSED_KS_IN k blocks or a W_out tile of PACK_KS_OUT -- from an
+// enumeration of all the tiles dealt round-robin over the groups; every group runs the
+// same number of rounds (rounds past the last tile move nothing), because each round
+// holds two workgroup barriers.  LDS: one 64 KiB area, either the place pass's arrays and
+// masks or the four groups' transpose tiles.
+constexpr int PACK_FUSED_KS_IN = 3;
+constexpr int PACK_GROUP_LDS = PACK_KS_OUT * 64 * 64;  // bytes per group (16-bit types)
+constexpr int PLACE_PACK_LDS = 4 * PACK_GROUP_LDS;
+static_assert(sizeof(PlaceLds) + 16 * 128 * 8 <= PLACE_PACK_LDS, "the place pass fits the area");
+
+template <int DT>
+__global__ void __launch_bounds__(1024)
+dispatch_place_pack_kernel(PlaceParams P, PackPairArgs K, int n_place, int rounds) {
+  __shared__ __attribute__((aligned(16))) char s_raw[PLACE_PACK_LDS];
+  if ((int)blockIdx.x < n_place) {  // uniform
+    place_body<24>(P, blockIdx.x, *(PlaceLds*)s_raw,
+               (unsigned long long*)(s_raw + (sizeof(PlaceLds) + 7) / 8 * 8));
+    return;
+  }
+  using T = typename Elem<DT>::T;
+  constexpr int TB = 64 * Geo<DT>::ROWB;  // one k block's transpose tile
+  const int grp = threadIdx.x >> 8, tid = threadIdx.x & 255;
+  char (*tile)[TB] = (char (*)[TB])(s_raw + grp * PACK_GROUP_LDS);
+  const int gx_in = (K.in_kb + PACK_FUSED_KS_IN - 1) / PACK_FUSED_KS_IN;
+  const int per_in = gx_in * K.gy_in, per_out = K.gx_out * K.gy_out;
+  const int64_t n_in = (int64_t)per_in * K.G, n_all = n_in + (int64_t)per_out * K.G;
+  const int64_t ngroups = (int64_t)(gridDim.x - n_place) * 4;
+  const int64_t g0 = (int64_t)(blockIdx.x - n_place) * 4 + grp;
+  for (int it = 0; it < rounds; ++it) {
+    if (it) __syncthreads();  // every group is done reading the previous round's tiles
+    const int64_t u = g0 + it * ngroups;
+    if (u < n_in) {  // uniform per group (whole waves)
+      const int g = (int)(u / per_in), r = (int)(u - (int64_t)g * per_in);
+      const int nt = r / gx_in, bx = r - nt * gx_in;
+      pack_ks_tile<DT, 0, PACK_FUSED_KS_IN>((const T*)K.w_in, (const T*)K.w_sh_in, K.E, K.d,
+                                            K.H, K.HP, K.in_kb, K.in_nb, K.p_in, K.fast, g, nt,
+                                            bx * PACK_FUSED_KS_IN, tile, tid);
+    } else {
+      // A W_out tile, or past the last tile: kb0 = out_kb moves nothing but still takes
+      // the routine's barrier.
+      const bool live = u < n_all;
+      const int64_t v = live ? u - n_in : 0;
+      const int g = (int)(v / per_out), r = (int)(v - (int64_t)g * per_out);
+      const int nt = r / K.gx_out, bx = r - nt * K.gx_out;
+      pack_ks_tile<DT, 1, PACK_KS_OUT>((const T*)K.w_out, (const T*)K.w_sh_out, K.E, K.d, K.H,
+                                       K.HP, K.out_kb, K.out_nb, K.p_out, K.fast, g, nt,
+                                       live ? bx * PACK_KS_OUT : K.out_kb, tile, tid);
+    }
+  }
+}
 }  // namespace nsmoe
 
 using namespace nsmoe;
@@ -283,11 +377,12 @@ int dispatch_launch(const int64_t* topk_idx, int64_t n_pairs, int32_t n_experts,
       topk_idx, n_pairs, n_experts, hist);
   NSMOE_TRY(check_launch("dispatch_hist_kernel"));
   const bool fold = bal != nullptr;
+  const PlaceParams P{topk_idx, n_pairs, n_experts, hist, n_chunks, 1, chunk, l_cap,
+                      sorted_ids, expert_ids, pad_offsets, counts, n_post_pad, inv,
+                      fold ? bal->partial : nullptr, fold ? bal->nblk : 0, fold ? bal->T : 1,
+                      fold ? bal->coef : 0.0f, fold ? bal->aux : nullptr};
   dispatch_place_kernel<<<(unsigned)(n_chunks + (fold ? 1 : 0)), chunk,
-                          (chunk / 64) * n_experts * sizeof(unsigned long long), s>>>(
-      topk_idx, n_pairs, n_experts, hist, n_chunks, 1, chunk, l_cap, sorted_ids, expert_ids, pad_offsets,
-      counts, n_post_pad, inv, fold ? bal->partial : nullptr, fold ? bal->nblk : 0,
-      fold ? bal->T : 1, fold ? bal->coef : 0.0f, fold ? bal->aux : nullptr);
+                          (chunk / 64) * n_experts * sizeof(unsigned long long), s>>>(P);
   timer.stop();
   return check_launch("dispatch_place_kernel");
 }
@@ -299,7 +394,8 @@ int dispatch_place_launch(const int64_t* topk_idx, int64_t n_pairs, int32_t n_ex
                           const int32_t* hist, int64_t n_chunks, int chunk_pairs,
                           int32_t* sorted_ids, int32_t* expert_ids, int32_t* pad_offsets,
                           int32_t* counts, int32_t* n_post_pad, int32_t* inv,
-                          const BalanceArgs* bal, hipStream_t s) {
+                          const BalanceArgs* bal, hipStream_t s, const PackPairArgs* pack,
+                          int pack_dtype) {
   NSMOE_REQUIRE(n_pairs > 0 && n_pairs < (int64_t)INT32_MAX / 2,
                 "dispatch_place: n_pairs %lld out of range", (long long)n_pairs);
   NSMOE_REQUIRE(n_experts >= 1 && n_experts <= 128 && chunk_pairs >= 1 &&
@@ -314,14 +410,46 @@ int dispatch_place_launch(const int64_t* topk_idx, int64_t n_pairs, int32_t n_ex
   const bool fold = bal != nullptr;
   const int group = 1024 / chunk_pairs;
   const int64_t n_place = (n_chunks + group - 1) / group;
+  const PlaceParams P{topk_idx, n_pairs, n_experts, hist, n_chunks, group,
+                      group * chunk_pairs, l_cap, sorted_ids, expert_ids, pad_offsets, counts,
+                      n_post_pad, inv, fold ? bal->partial : nullptr, fold ? bal->nblk : 0,
+                      fold ? bal->T : 1, fold ? bal->coef : 0.0f, fold ? bal->aux : nullptr};
+  const int np = (int)(n_place + (fold ? 1 : 0));
+  if (pack && (pack_dtype == DT_BF16 || pack_dtype == DT_F16)) {
+    // Packing workgroups: enough for one round of resident workgroups beside the placing
+    // ones (the kernel's occupancy per CU, from the runtime), each group then packing
+    // ceil(tiles / groups) tiles.
+    const int64_t gx_in = cdiv(pack->in_kb, PACK_FUSED_KS_IN);
+    const int64_t tiles = (gx_in * pack->gy_in + (int64_t)pack->gx_out * pack->gy_out) * pack->G;
+    int cus = 0, dev = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    const void* kfn = pack_dtype == DT_BF16 ? (const void*)dispatch_place_pack_kernel<DT_BF16>
+                                            : (const void*)dispatch_place_pack_kernel<DT_F16>;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kfn, 1024, 0) != hipSuccess ||
+        per_cu <= 0)
+      per_cu = 1;
+    (void)hipGetLastError();
+    int64_t npack = (int64_t)per_cu * cus - np;
+    if (npack < 8) npack = 8;
+    if (npack > cdiv(tiles, 4)) npack = cdiv(tiles, 4);
+    const int rounds = (int)cdiv(tiles, 4 * npack);
+    NSMOE_REQUIRE(np + npack < (int64_t)INT32_MAX, "place+pack: grid");
+    KernelTimer timer("place_pack", s);
+    if (pack_dtype == DT_BF16)
+      dispatch_place_pack_kernel<DT_BF16><<<(unsigned)(np + npack), 1024, 0, s>>>(P, *pack, np,
+                                                                                 rounds);
+    else
+      dispatch_place_pack_kernel<DT_F16><<<(unsigned)(np + npack), 1024, 0, s>>>(P, *pack, np,
+                                                                                rounds);
+    timer.stop();
+    return check_launch("dispatch_place_pack_kernel");
+  }
   KernelTimer timer("dispatch", s);
-  dispatch_place_kernel<<<(unsigned)(n_place + (fold ? 1 : 0)), 1024,
-                          16 * n_experts * sizeof(unsigned long long), s>>>(
-      topk_idx, n_pairs, n_experts, hist, n_chunks, group, group * chunk_pairs, l_cap,
-      sorted_ids,
-      expert_ids, pad_offsets, counts, n_post_pad, inv, fold ? bal->partial : nullptr,
-      fold ? bal->nblk : 0, fold ? bal->T : 1, fold ? bal->coef : 0.0f,
-      fold ? bal->aux : nullptr);
+  dispatch_place_kernel<<<(unsigned)np, 1024, 16 * n_experts * sizeof(unsigned long long), s>>>(
+      P);
   timer.stop();
   return check_launch("dispatch_place_kernel");
 }

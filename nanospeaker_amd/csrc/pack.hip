@@ -15,6 +15,7 @@
 #include "gemm_core.h"
 #include "nsmoe_capi_internal.h"
 #include "pack.h"
+#include "pack_tile.h"
 
 namespace nsmoe {
 
@@ -61,90 +62,12 @@ pack_kernel(const typename Elem<DT>::T* __restrict__ routed,
   __builtin_memcpy(dst, &f, sizeof(f));
 }
 
-// 16-bit types: one workgroup packs KS k blocks of one 64-column tile.  Thread t < 32 KS
-// loads the 8 x 8 block (t % 32) of k block t / 32 (every load of the workgroup in flight
-// at once) and transposes it into that k block's LDS tile; after a barrier wave w writes
-// fragment (4 nt + w, kb) of each k block.  A workgroup per k block keeps only 32 threads
-// and 4 KB of loads in flight, which leaves the pass at about half of HBM's rate.
-// The tile is (g, nt, k blocks kb0 .. kb0 + KS - 1); `tile` is KS LDS tiles.
-template <int DT, int MODE, int KS>
-__device__ __forceinline__ void pack_ks_tile(const typename Elem<DT>::T* __restrict__ routed,
-                                             const typename Elem<DT>::T* __restrict__ shared,
-                                             int E, int d, int H, int HP, int n_kb, int n_nb,
-                                             char* __restrict__ out, int fast, int g, int nt,
-                                             int kb0, char (*tile)[64 * Geo<DT>::ROWB]) {
-  using G = Geo<DT>;
-  using T = typename G::T;
-  static_assert(G::ES == 2 && KS * 32 <= 256, "16-bit types, at most 8 k blocks");
-  const int K = MODE == 0 ? d : H;
-  const int ld = MODE == 0 ? 2 * H : d;
-  const int64_t gstride = MODE == 0 ? (int64_t)d * 2 * H : (int64_t)H * d;
-  const T* W = g < E ? routed + (int64_t)g * gstride : shared + (int64_t)(g - E) * gstride;
-  int n0, nlim;
-  if (MODE == 0) {
-    const int c0 = nt * 64;  // packed column of the tile
-    if (c0 < HP) {
-      n0 = c0;
-      nlim = H;
-    } else {
-      n0 = H + (c0 - HP);
-      nlim = 2 * H;
-    }
-  } else {
-    n0 = nt * 64;
-    nlim = d;
-  }
-  // This thread's 8 x 8 block: rows kb * 32 + kbl * 8 + r, columns n0 + nbl * 8 .. + 7.  The
-  // column block is the fastest index, so each lane quad loads 64 contiguous bytes of one
-  // row (a quad over four rows costs the L1's address unit about three times as much).
-  const int step = threadIdx.x >> 5, blk = threadIdx.x & 31;
-  const int kbl = blk >> 3, nbl = blk & 7;
-  const int kb = kb0 + step;
-  const bool on = step < KS && kb < n_kb;
-  const int col = n0 + nbl * G::VE;
-  u32x4 v[G::VE];
-#pragma unroll
-  for (int r = 0; r < G::VE; ++r) {
-    v[r] = u32x4{0u, 0u, 0u, 0u};
-    const int k = kb * G::KC + kbl * G::VE + r;
-    if (!on || k >= K) continue;
-    const T* src = W + (int64_t)k * ld;
-    if (fast) {
-      if (col < nlim) v[r] = *(const u32x4*)(src + col);
-    } else {
-      T tmp[G::VE];
-#pragma unroll
-      for (int e = 0; e < G::VE; ++e) tmp[e] = (col + e < nlim) ? src[col + e] : T(0);
-      __builtin_memcpy(&v[r], tmp, 16);
-    }
-  }
-  if (on) store_trans8<DT>(v, tile[step], nbl, kbl);
-  __syncthreads();
-  const int wave = threadIdx.x >> 6;
-  const int nb = nt * 4 + wave;
-#pragma unroll
-  for (int st = 0; st < KS; ++st) {
-    if (kb0 + st >= n_kb) break;
-    const typename Mma<DT>::Frag f = frag_sw<DT>(tile[st], wave * 16);
-    char* dst = out + (((int64_t)g * n_nb + nb) * n_kb + kb0 + st) * G::PKB + lane_id() * G::FRAGB;
-    __builtin_memcpy(dst, &f, sizeof(f));
-  }
-}
-
 // Both 16-bit packs in one launch: workgroups [0, n_in) pack W_in (6 k blocks each), the
 // rest W_out (4 k blocks each, two column tiles one after the other), so the two stacks
 // stream together in one round of resident workgroups (24 KiB of LDS each: 6 per CU; at
 // nanoSpeaker's shape 936 + 390 workgroups, where one W_out tile per workgroup made 1638).
 // A workgroup's (k block group, column tile, group) comes from its linear index, the k
 // block groups fastest.
-constexpr int PACK_KS_IN = 6, PACK_KS_OUT = 4;
-
-struct PackPairArgs {
-  const void *w_in, *w_sh_in, *w_out, *w_sh_out;
-  int E, G, d, H, HP, in_kb, in_nb, out_kb, out_nb, fast;
-  char *p_in, *p_out;
-  int gx_in, gy_in, gx_out, gy_out;  // k block groups and column tiles of each part
-};
 
 template <int DT>
 __global__ void __launch_bounds__(256) pack_pair_kernel(PackPairArgs a) {
@@ -157,7 +80,7 @@ __global__ void __launch_bounds__(256) pack_pair_kernel(PackPairArgs a) {
     const int g = b / per_in, r = b - g * per_in, nt = r / a.gx_in, bx = r - nt * a.gx_in;
     pack_ks_tile<DT, 0, PACK_KS_IN>((const T*)a.w_in, (const T*)a.w_sh_in, a.E, a.d, a.H, a.HP,
                                     a.in_kb, a.in_nb, a.p_in, a.fast, g, nt,
-                                    bx * PACK_KS_IN, tile);
+                                    bx * PACK_KS_IN, tile, threadIdx.x);
   } else {
     b -= in_blocks;
     const int gy2 = (a.gy_out + 1) / 2;
@@ -169,7 +92,7 @@ __global__ void __launch_bounds__(256) pack_pair_kernel(PackPairArgs a) {
       if (u) __syncthreads();     // every wave is done reading the first tile's LDS
       pack_ks_tile<DT, 1, PACK_KS_OUT>((const T*)a.w_out, (const T*)a.w_sh_out, a.E, a.d,
                                        a.H, a.HP, a.out_kb, a.out_nb, a.p_out, a.fast, g, nt,
-                                       bx * PACK_KS_OUT, tile);
+                                       bx * PACK_KS_OUT, tile, threadIdx.x);
     }
   }
 }
@@ -182,7 +105,7 @@ pack_ks_kernel(const typename Elem<DT>::T* __restrict__ routed,
                int n_kb, int n_nb, char* __restrict__ out, int fast) {
   __shared__ __attribute__((aligned(16))) char tile[KS][64 * Geo<DT>::ROWB];
   pack_ks_tile<DT, MODE, KS>(routed, shared, E, d, H, HP, n_kb, n_nb, out, fast, blockIdx.z,
-                             blockIdx.y, blockIdx.x * KS, tile);
+                             blockIdx.y, blockIdx.x * KS, tile, threadIdx.x);
 }
 
 PackGeom pack_geom(int dtype, int d, int H, int E, int S) {
@@ -249,6 +172,21 @@ static int launch_pack(const PackGeom& pg, const void* w_in, const void* w_out,
     }
   }
   return NSMOE_OK;
+}
+
+bool pack_pair_args(int dtype, const void* w_in, const void* w_out, const void* w_sh_in,
+                    const void* w_sh_out, int E, int S, int d, int H, void* p_in, void* p_out,
+                    PackPairArgs* out) {
+  if (dtype == DT_F32 || !p_in || !p_out) return false;
+  const PackGeom pg = pack_geom(dtype, d, H, E, S);
+  auto al = [](const void* q) { return q == nullptr || ((uintptr_t)q & 15u) == 0; };
+  const bool fast = d % 8 == 0 && H % 8 == 0 && al(w_in) && al(w_out) && al(w_sh_in) &&
+                    al(w_sh_out);
+  *out = PackPairArgs{w_in, w_sh_in, w_out, w_sh_out, E, E + S, d, H, pg.hp, pg.in_kb,
+                      pg.in_nb, pg.out_kb, pg.out_nb, fast ? 1 : 0, (char*)p_in, (char*)p_out,
+                      (int)cdiv(pg.in_kb, PACK_KS_IN), pg.in_nb / 4,
+                      (int)cdiv(pg.out_kb, PACK_KS_OUT), pg.out_nb / 4};
+  return true;
 }
 
 int pack_weights(int dtype, const void* w_in, const void* w_out, const void* w_sh_in,
