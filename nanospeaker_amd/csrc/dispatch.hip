@@ -262,56 +262,26 @@ __global__ void __launch_bounds__(1024) dispatch_place_kernel(PlaceParams P) {
 // [0, n_place) place (as dispatch_place_kernel, E <= 128), the rest pack.  The pack does
 // not depend on the routing, and the place pass's few latency-bound workgroups leave most
 // CUs idle, so the packing runs in that time instead of in a launch of its own.
-// A packing workgroup is four groups of 256 threads, each packing one tile per round --
-// a W_in tile of PACK_FUSED_KS_IN k blocks or a W_out tile of PACK_KS_OUT -- from an
-// enumeration of all the tiles dealt round-robin over the groups; every group runs the
-// same number of rounds (rounds past the last tile move nothing), because each round
-// holds two workgroup barriers.  LDS: one 64 KiB area, either the place pass's arrays and
-// masks or the four groups' transpose tiles.
-constexpr int PACK_FUSED_KS_IN = 3;
-constexpr int PACK_GROUP_LDS = PACK_KS_OUT * 64 * 64;  // bytes per group (16-bit types)
-constexpr int PLACE_PACK_LDS = 4 * PACK_GROUP_LDS;
-static_assert(sizeof(PlaceLds) + 16 * 128 * 8 <= PLACE_PACK_LDS, "the place pass fits the area");
+// A packing workgroup's 16 waves take the pack's wave items (pack_tile.h) grid-stride,
+// each on its own with its own 8 KiB of LDS (no workgroup barrier).  LDS: one area, either
+// the place pass's arrays and masks or the 16 waves' regions.
+constexpr int PLACE_LDS = ((int)sizeof(PlaceLds) + 7) / 8 * 8 + 16 * 128 * 8;
+constexpr int PLACE_PACK_LDS = PLACE_LDS > 16 * PACK_WAVE_LDS ? PLACE_LDS : 16 * PACK_WAVE_LDS;
 
 template <int DT>
 __global__ void __launch_bounds__(1024)
-dispatch_place_pack_kernel(PlaceParams P, PackPairArgs K, int n_place, int rounds) {
+dispatch_place_pack_kernel(PlaceParams P, PackPairArgs K, int n_place) {
   __shared__ __attribute__((aligned(16))) char s_raw[PLACE_PACK_LDS];
   if ((int)blockIdx.x < n_place) {  // uniform
     place_body<24>(P, blockIdx.x, *(PlaceLds*)s_raw,
-               (unsigned long long*)(s_raw + (sizeof(PlaceLds) + 7) / 8 * 8));
+                   (unsigned long long*)(s_raw + (sizeof(PlaceLds) + 7) / 8 * 8));
     return;
   }
-  using T = typename Elem<DT>::T;
-  constexpr int TB = 64 * Geo<DT>::ROWB;  // one k block's transpose tile
-  const int grp = threadIdx.x >> 8, tid = threadIdx.x & 255;
-  char (*tile)[TB] = (char (*)[TB])(s_raw + grp * PACK_GROUP_LDS);
-  const int gx_in = (K.in_kb + PACK_FUSED_KS_IN - 1) / PACK_FUSED_KS_IN;
-  const int per_in = gx_in * K.gy_in, per_out = K.gx_out * K.gy_out;
-  const int64_t n_in = (int64_t)per_in * K.G, n_all = n_in + (int64_t)per_out * K.G;
-  const int64_t ngroups = (int64_t)(gridDim.x - n_place) * 4;
-  const int64_t g0 = (int64_t)(blockIdx.x - n_place) * 4 + grp;
-  for (int it = 0; it < rounds; ++it) {
-    if (it) __syncthreads();  // every group is done reading the previous round's tiles
-    const int64_t u = g0 + it * ngroups;
-    if (u < n_in) {  // uniform per group (whole waves)
-      const int g = (int)(u / per_in), r = (int)(u - (int64_t)g * per_in);
-      const int nt = r / gx_in, bx = r - nt * gx_in;
-      pack_ks_tile<DT, 0, PACK_FUSED_KS_IN>((const T*)K.w_in, (const T*)K.w_sh_in, K.E, K.d,
-                                            K.H, K.HP, K.in_kb, K.in_nb, K.p_in, K.fast, g, nt,
-                                            bx * PACK_FUSED_KS_IN, tile, tid);
-    } else {
-      // A W_out tile, or past the last tile: kb0 = out_kb moves nothing but still takes
-      // the routine's barrier.
-      const bool live = u < n_all;
-      const int64_t v = live ? u - n_in : 0;
-      const int g = (int)(v / per_out), r = (int)(v - (int64_t)g * per_out);
-      const int nt = r / K.gx_out, bx = r - nt * K.gx_out;
-      pack_ks_tile<DT, 1, PACK_KS_OUT>((const T*)K.w_out, (const T*)K.w_sh_out, K.E, K.d, K.H,
-                                       K.HP, K.out_kb, K.out_nb, K.p_out, K.fast, g, nt,
-                                       live ? bx * PACK_KS_OUT : K.out_kb, tile, tid);
-    }
-  }
+  const int64_t waves = (int64_t)(gridDim.x - n_place) * 16;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  char* wl = s_raw + wave * PACK_WAVE_LDS;
+  for (int64_t u = (int64_t)(blockIdx.x - n_place) * 16 + wave;; u += waves)
+    if (!pack_pair_item<DT>(K, u, lane, wl)) break;  // uniform per wave
 }
 }  // namespace nsmoe
 
@@ -416,11 +386,13 @@ int dispatch_place_launch(const int64_t* topk_idx, int64_t n_pairs, int32_t n_ex
                       fold ? bal->T : 1, fold ? bal->coef : 0.0f, fold ? bal->aux : nullptr};
   const int np = (int)(n_place + (fold ? 1 : 0));
   if (pack && (pack_dtype == DT_BF16 || pack_dtype == DT_F16)) {
-    // Packing workgroups: enough for one round of resident workgroups beside the placing
-    // ones (the kernel's occupancy per CU, from the runtime), each group then packing
-    // ceil(tiles / groups) tiles.
-    const int64_t gx_in = cdiv(pack->in_kb, PACK_FUSED_KS_IN);
-    const int64_t tiles = (gx_in * pack->gy_in + (int64_t)pack->gx_out * pack->gy_out) * pack->G;
+    // Packing workgroups: as many as are resident beside the placing ones (the kernel's
+    // occupancy per CU, from the runtime), and no more than two wave items per wave
+    // need.  With one item per wave every read would come first and every write last,
+    // leaving the L2s full of dirty lines that the end of the launch must write back
+    // before the next kernel starts (measured: ~6 us more between the launches); two
+    // items per wave interleave the second item's reads with the first one's writes.
+    const int64_t items = pack->items_in + pack->items_out;
     int cus = 0, dev = 0, per_cu = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
@@ -434,16 +406,14 @@ int dispatch_place_launch(const int64_t* topk_idx, int64_t n_pairs, int32_t n_ex
     (void)hipGetLastError();
     int64_t npack = (int64_t)per_cu * cus - np;
     if (npack < 8) npack = 8;
-    if (npack > cdiv(tiles, 4)) npack = cdiv(tiles, 4);
-    const int rounds = (int)cdiv(tiles, 4 * npack);
+    if (npack > cdiv(items, 32)) npack = cdiv(items, 32);
+    if (npack < 1) npack = 1;
     NSMOE_REQUIRE(np + npack < (int64_t)INT32_MAX, "place+pack: grid");
     KernelTimer timer("place_pack", s);
     if (pack_dtype == DT_BF16)
-      dispatch_place_pack_kernel<DT_BF16><<<(unsigned)(np + npack), 1024, 0, s>>>(P, *pack, np,
-                                                                                 rounds);
+      dispatch_place_pack_kernel<DT_BF16><<<(unsigned)(np + npack), 1024, 0, s>>>(P, *pack, np);
     else
-      dispatch_place_pack_kernel<DT_F16><<<(unsigned)(np + npack), 1024, 0, s>>>(P, *pack, np,
-                                                                                rounds);
+      dispatch_place_pack_kernel<DT_F16><<<(unsigned)(np + npack), 1024, 0, s>>>(P, *pack, np);
     timer.stop();
     return check_launch("dispatch_place_pack_kernel");
   }

@@ -19,8 +19,8 @@
 
 namespace nsmoe {
 
-// One workgroup: group g, 64 packed columns [nt * 64, +64), k block kb.  The columns
-// are staged transposed into a swizzled LDS tile (k-major rows), then each wave writes
+// fp32: one workgroup per group g, 64 packed columns [nt * 64, +64), k block kb.  The
+// columns are staged transposed into a swizzled LDS tile (k-major rows), then each wave writes
 // one 16-column fragment.
 template <int DT, int MODE>
 __global__ void __launch_bounds__(256)
@@ -62,50 +62,20 @@ pack_kernel(const typename Elem<DT>::T* __restrict__ routed,
   __builtin_memcpy(dst, &f, sizeof(f));
 }
 
-// Both 16-bit packs in one launch: workgroups [0, n_in) pack W_in (6 k blocks each), the
-// rest W_out (4 k blocks each, two column tiles one after the other), so the two stacks
-// stream together in one round of resident workgroups (24 KiB of LDS each: 6 per CU; at
-// nanoSpeaker's shape 936 + 390 workgroups, where one W_out tile per workgroup made 1638).
-// A workgroup's (k block group, column tile, group) comes from its linear index, the k
-// block groups fastest.
-
+// Both 16-bit packs in one launch (W_in alone when items_out is 0): every wave packs
+// two wave items (pack_tile.h; two k blocks of a 64-column tile each) grid-stride, W_in's
+// items first, then W_out's.  Waves share nothing, so there is no workgroup barrier, and
+// every thread's eight 16-byte loads are in flight at once.  Two items per wave let the
+// second item's reads overlap the first one's writes instead of all reads preceding all
+// writes (which leaves the L2s full of dirty lines for the end of the launch to write
+// back).
 template <int DT>
 __global__ void __launch_bounds__(256) pack_pair_kernel(PackPairArgs a) {
-  using G = Geo<DT>;
-  using T = typename G::T;
-  __shared__ __attribute__((aligned(16))) char tile[PACK_KS_IN][64 * G::ROWB];
-  const int per_in = a.gx_in * a.gy_in, in_blocks = per_in * a.G;
-  int b = blockIdx.x;
-  if (b < in_blocks) {  // uniform
-    const int g = b / per_in, r = b - g * per_in, nt = r / a.gx_in, bx = r - nt * a.gx_in;
-    pack_ks_tile<DT, 0, PACK_KS_IN>((const T*)a.w_in, (const T*)a.w_sh_in, a.E, a.d, a.H, a.HP,
-                                    a.in_kb, a.in_nb, a.p_in, a.fast, g, nt,
-                                    bx * PACK_KS_IN, tile, threadIdx.x);
-  } else {
-    b -= in_blocks;
-    const int gy2 = (a.gy_out + 1) / 2;
-    const int per_out = a.gx_out * gy2;
-    const int g = b / per_out, r = b - g * per_out, nt2 = r / a.gx_out, bx = r - nt2 * a.gx_out;
-    for (int u = 0; u < 2; ++u) {
-      const int nt = 2 * nt2 + u;
-      if (nt >= a.gy_out) break;  // uniform
-      if (u) __syncthreads();     // every wave is done reading the first tile's LDS
-      pack_ks_tile<DT, 1, PACK_KS_OUT>((const T*)a.w_out, (const T*)a.w_sh_out, a.E, a.d,
-                                       a.H, a.HP, a.out_kb, a.out_nb, a.p_out, a.fast, g, nt,
-                                       bx * PACK_KS_OUT, tile, threadIdx.x);
-    }
-  }
-}
-
-// W_in alone.
-template <int DT, int MODE, int KS>
-__global__ void __launch_bounds__(256)
-pack_ks_kernel(const typename Elem<DT>::T* __restrict__ routed,
-               const typename Elem<DT>::T* __restrict__ shared, int E, int d, int H, int HP,
-               int n_kb, int n_nb, char* __restrict__ out, int fast) {
-  __shared__ __attribute__((aligned(16))) char tile[KS][64 * Geo<DT>::ROWB];
-  pack_ks_tile<DT, MODE, KS>(routed, shared, E, d, H, HP, n_kb, n_nb, out, fast, blockIdx.z,
-                             blockIdx.y, blockIdx.x * KS, tile, threadIdx.x);
+  __shared__ __attribute__((aligned(16))) char s_w[4][PACK_WAVE_LDS];
+  const int wave = threadIdx.x >> 6;
+  const int64_t stride = (int64_t)gridDim.x * 4;
+  for (int64_t u = (int64_t)blockIdx.x * 4 + wave;; u += stride)
+    if (!pack_pair_item<DT>(a, u, threadIdx.x & 63, s_w[wave])) break;  // uniform per wave
 }
 
 PackGeom pack_geom(int dtype, int d, int H, int E, int S) {
@@ -131,38 +101,25 @@ static int launch_pack(const PackGeom& pg, const void* w_in, const void* w_out,
   using T = typename Elem<DT>::T;
   const int G = E + S;
   if constexpr (DT != DT_F32) {
-    if (p_out) {  // both stacks: one launch
-      PackPairArgs a{w_in, w_sh_in, w_out, w_sh_out, E, G, d, H, pg.hp, pg.in_kb, pg.in_nb,
-                     pg.out_kb, pg.out_nb, fast ? 1 : 0, (char*)p_in, (char*)p_out,
-                     (int)cdiv(pg.in_kb, PACK_KS_IN), pg.in_nb / 4,
-                     (int)cdiv(pg.out_kb, PACK_KS_OUT), pg.out_nb / 4};
-      const int64_t blocks =
-          ((int64_t)a.gx_in * a.gy_in + (int64_t)a.gx_out * ((a.gy_out + 1) / 2)) * (int64_t)G;
-      NSMOE_REQUIRE(blocks < (int64_t)INT32_MAX, "pack: %lld workgroups", (long long)blocks);
-      KernelTimer timer("pack", s);
-      pack_pair_kernel<DT><<<(unsigned)blocks, 256, 0, s>>>(a);
-      timer.stop();
-      return check_launch("pack_pair_kernel");
-    }
-  }
-  {
+    PackPairArgs a{w_in, w_sh_in, w_out, w_sh_out, E, G, d, H, pg.hp, pg.in_kb, pg.in_nb,
+                   pg.out_kb, pg.out_nb, fast ? 1 : 0, (char*)p_in, (char*)p_out,
+                   pack_items(G, pg.in_kb, pg.in_nb),
+                   p_out ? pack_items(G, pg.out_kb, pg.out_nb) : 0};
+    const int64_t blocks = cdiv(a.items_in + a.items_out, 8);
+    NSMOE_REQUIRE(blocks < (int64_t)INT32_MAX, "pack: %lld workgroups", (long long)blocks);
     KernelTimer timer("pack", s);
-    if constexpr (DT != DT_F32) {
-      constexpr int KS = PACK_KS_IN;
-      dim3 grid((unsigned)cdiv(pg.in_kb, KS), (unsigned)(pg.in_nb / 4), (unsigned)G);
-      pack_ks_kernel<DT, 0, KS><<<grid, 256, 0, s>>>((const T*)w_in, (const T*)w_sh_in, E, d,
-                                                     H, pg.hp, pg.in_kb, pg.in_nb, (char*)p_in,
-                                                     fast ? 1 : 0);
-    } else {
-      dim3 grid((unsigned)pg.in_kb, (unsigned)(pg.in_nb / 4), (unsigned)G);
-      pack_kernel<DT, 0><<<grid, 256, 0, s>>>((const T*)w_in, (const T*)w_sh_in, E, d, H,
-                                             pg.hp, pg.in_kb, pg.in_nb, (char*)p_in,
-                                             fast ? 1 : 0);
-    }
+    pack_pair_kernel<DT><<<(unsigned)blocks, 256, 0, s>>>(a);
+    timer.stop();
+    return check_launch("pack_pair_kernel");
+  } else {
+    KernelTimer timer("pack", s);
+    dim3 grid((unsigned)pg.in_kb, (unsigned)(pg.in_nb / 4), (unsigned)G);
+    pack_kernel<DT, 0><<<grid, 256, 0, s>>>((const T*)w_in, (const T*)w_sh_in, E, d, H, pg.hp,
+                                           pg.in_kb, pg.in_nb, (char*)p_in, fast ? 1 : 0);
     timer.stop();
     NSMOE_TRY(check_launch("pack_kernel<w_in>"));
   }
-  if constexpr (DT == DT_F32) {  // 16-bit types pack W_out only beside W_in (above)
+  if constexpr (DT == DT_F32) {
     if (p_out) {
       dim3 grid((unsigned)pg.out_kb, (unsigned)(pg.out_nb / 4), (unsigned)G);
       pack_kernel<DT, 1><<<grid, 256, 0, s>>>((const T*)w_out, (const T*)w_sh_out, E, d, H,
@@ -184,8 +141,8 @@ bool pack_pair_args(int dtype, const void* w_in, const void* w_out, const void* 
                     al(w_sh_out);
   *out = PackPairArgs{w_in, w_sh_in, w_out, w_sh_out, E, E + S, d, H, pg.hp, pg.in_kb,
                       pg.in_nb, pg.out_kb, pg.out_nb, fast ? 1 : 0, (char*)p_in, (char*)p_out,
-                      (int)cdiv(pg.in_kb, PACK_KS_IN), pg.in_nb / 4,
-                      (int)cdiv(pg.out_kb, PACK_KS_OUT), pg.out_nb / 4};
+                      pack_items(E + S, pg.in_kb, pg.in_nb),
+                      pack_items(E + S, pg.out_kb, pg.out_nb)};
   return true;
 }
 

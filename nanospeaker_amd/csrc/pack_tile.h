@@ -1,30 +1,51 @@
-// The 16-bit weight pack's tile routine (pack.hip), shared with the dispatch's place launch
-// (dispatch.hip), which packs beside its placement workgroups.
+// The 16-bit weight pack's block routine (pack.hip), shared with the dispatch's place
+// launch (dispatch.hip), which packs beside its placement workgroups.
 #pragma once
 
 #include "gemm_core.h"
 
 namespace nsmoe {
 
-// 16-bit types: 256 threads (tid 0 .. 255, four whole waves) pack KS k blocks of one
-// 64-column tile; the caller's workgroup barrier (__syncthreads) separates the LDS writes
-// from the reads, so every group of a workgroup must call this the same number of times
-// (a call with kb0 >= n_kb moves nothing and only takes the barrier).  Thread t < 32 KS
-// loads the 8 x 8 block (t % 32) of k block t / 32 (every load of the workgroup in flight
-// at once) and transposes it into that k block's LDS tile; after a barrier wave w writes
-// fragment (4 nt + w, kb) of each k block.  A workgroup per k block keeps only 32 threads
-// and 4 KB of loads in flight, which leaves the pass at about half of HBM's rate.
-// The tile is (g, nt, k blocks kb0 .. kb0 + KS - 1); `tile` is KS LDS tiles.
-template <int DT, int MODE, int KS>
-__device__ __forceinline__ void pack_ks_tile(const typename Elem<DT>::T* __restrict__ routed,
-                                             const typename Elem<DT>::T* __restrict__ shared,
-                                             int E, int d, int H, int HP, int n_kb, int n_nb,
-                                             char* __restrict__ out, int fast, int g, int nt,
-                                             int kb0, char (*tile)[64 * Geo<DT>::ROWB],
-                                             int tid) {
+// The pack in wave items: a wave packs two k blocks of one 64-column tile -- eight 1 KiB
+// fragments (f = 4 (k block % 2) + column block) -- and nothing is shared between waves,
+// so there is no workgroup barrier.  Lane l of the wave loads and transposes one 8 x 8
+// block in its registers: k block 2 kp + l / 32, rows kbl * 8 + r (r < 8) with
+// kbl = (l % 32) / 8, columns 8 nbl .. 8 nbl + 7 of the tile with nbl = l % 8 (eight lanes
+// read one row's 128 contiguous bytes).  Column c of the block is exactly one lane's
+// 16-byte share of fragment (l / 32, nbl / 2): share 16 kbl + 8 (nbl % 2) + c, whose
+// elements are the block's rows in order.  The shares go to the wave's 8 KiB of LDS in
+// fragment order, and each fragment leaves as one 1 KiB store (lane l, share l): stores of
+// 16 scattered bytes per lane would cost the L2 one request per lane.  Out-of-range rows
+// and columns pack as zeros.
+//
+// LDS: share i of the region (16 bytes, i = 64 f + s) sits at
+// i ^ 2 ((i / 64) % 4) ^ ((i / 16) % 2): any 16 consecutive lanes of one transposed write,
+// and of one fragment read, then cover all 64 banks once.
+constexpr int PACK_WAVE_LDS = 8 * 1024;
+
+__device__ __forceinline__ int pack_share_off(int i) {
+  return (i ^ (((i >> 6) & 3) << 1) ^ ((i >> 4) & 1)) << 4;
+}
+
+__host__ __device__ inline int64_t pack_items(int groups, int n_kb, int n_nb) {
+  return (int64_t)groups * (n_nb / 4) * ((n_kb + 1) / 2);
+}
+
+// Items run tiles fastest, so consecutive waves read the same rows' neighbouring 128-byte
+// segments, then k-block pairs, then groups.
+template <int DT, int MODE>
+__device__ __forceinline__ void pack_wave_item(const typename Elem<DT>::T* __restrict__ routed,
+                                               const typename Elem<DT>::T* __restrict__ shared,
+                                               int E, int d, int H, int HP, int n_kb, int n_nb,
+                                               char* __restrict__ out, int fast, int64_t item,
+                                               int lane, char* __restrict__ wl) {
   using G = Geo<DT>;
   using T = typename G::T;
-  static_assert(G::ES == 2 && KS * 32 <= 256, "16-bit types, at most 8 k blocks");
+  static_assert(G::ES == 2 && G::VE == 8 && G::KC == 32 && G::PKB == 1024, "16-bit types");
+  const int nts = n_nb / 4, kps = (n_kb + 1) / 2;
+  const int per_g = nts * kps;
+  const int g = (int)(item / per_g), r0 = (int)(item - (int64_t)g * per_g);
+  const int kp = r0 / nts, nt = r0 - kp * nts;
   const int K = MODE == 0 ? d : H;
   const int ld = MODE == 0 ? 2 * H : d;
   const int64_t gstride = MODE == 0 ? (int64_t)d * 2 * H : (int64_t)H * d;
@@ -43,20 +64,15 @@ __device__ __forceinline__ void pack_ks_tile(const typename Elem<DT>::T* __restr
     n0 = nt * 64;
     nlim = d;
   }
-  // This thread's 8 x 8 block: rows kb * 32 + kbl * 8 + r, columns n0 + nbl * 8 .. + 7.  The
-  // column block is the fastest index, so each lane quad loads 64 contiguous bytes of one
-  // row (a quad over four rows costs the L1's address unit about three times as much).
-  const int step = tid >> 5, blk = tid & 31;
-  const int kbl = blk >> 3, nbl = blk & 7;
-  const int kb = kb0 + step;
-  const bool on = step < KS && kb < n_kb;
+  const int half = lane >> 5, kbl = (lane >> 3) & 3, nbl = lane & 7;
+  const int kb = 2 * kp + half;
   const int col = n0 + nbl * G::VE;
   u32x4 v[G::VE];
 #pragma unroll
   for (int r = 0; r < G::VE; ++r) {
     v[r] = u32x4{0u, 0u, 0u, 0u};
     const int k = kb * G::KC + kbl * G::VE + r;
-    if (!on || k >= K) continue;
+    if (k >= K) continue;  // also every row of a k block past n_kb
     const T* src = W + (int64_t)k * ld;
     if (fast) {
       if (col < nlim) v[r] = *(const u32x4*)(src + col);
@@ -67,28 +83,58 @@ __device__ __forceinline__ void pack_ks_tile(const typename Elem<DT>::T* __restr
       __builtin_memcpy(&v[r], tmp, 16);
     }
   }
-  if (on) store_trans8<DT>(v, tile[step], nbl, kbl);
-  __syncthreads();
-  const int wave = tid >> 6;
-  const int nb = nt * 4 + wave;
+  const int share0 = 64 * (4 * half + (nbl >> 1)) + 16 * kbl + 8 * (nbl & 1);
+  constexpr uint32_t kLow = 0x05040100u, kHigh = 0x07060302u;  // low / high halves
 #pragma unroll
-  for (int st = 0; st < KS; ++st) {
-    if (kb0 + st >= n_kb) break;
-    const typename Mma<DT>::Frag f = frag_sw<DT>(tile[st], wave * 16);
-    char* dst = out + (((int64_t)g * n_nb + nb) * n_kb + kb0 + st) * G::PKB + lane_id() * G::FRAGB;
-    __builtin_memcpy(dst, &f, sizeof(f));
+  for (int c = 0; c < G::VE; ++c) {
+    u32x4 o;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      o[q] = __builtin_amdgcn_perm(v[2 * q + 1][c >> 1], v[2 * q][c >> 1],
+                                   (c & 1) ? kHigh : kLow);
+    *(u32x4*)(wl + pack_share_off(share0 + c)) = o;
   }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  char* dst = out + (((int64_t)g * n_nb + nt * 4) * n_kb + 2 * kp) * G::PKB + lane * G::FRAGB;
+#pragma unroll
+  for (int f = 0; f < 8; ++f) {
+    if (2 * kp + (f >> 2) >= n_kb) break;  // uniform: the odd k block past the last
+    const u32x4 o = *(const u32x4*)(wl + pack_share_off(64 * f + lane));
+    *(u32x4*)(dst + ((int64_t)(f & 3) * n_kb + (f >> 2)) * G::PKB) = o;
+  }
+  // the wave's next item must not overwrite the region before these reads
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-constexpr int PACK_KS_IN = 6, PACK_KS_OUT = 4;
-
-// Both packs' operands and geometry (pack_pair_kernel, and the place launch's pack groups).
+// Both packs' operands and geometry (pack_pair_kernel, and the place launch's pack waves).
 struct PackPairArgs {
   const void *w_in, *w_sh_in, *w_out, *w_sh_out;
   int E, G, d, H, HP, in_kb, in_nb, out_kb, out_nb, fast;
   char *p_in, *p_out;
-  int gx_in, gy_in, gx_out, gy_out;  // k block groups and column tiles of each part
+  int64_t items_in, items_out;  // wave items of each stack (items_out 0: W_in alone)
 };
+
+// Wave item u of the pair: W_in's items first, then W_out's; false past the last.  wl is
+// the wave's PACK_WAVE_LDS bytes of LDS (16-byte aligned).
+template <int DT>
+__device__ __forceinline__ bool pack_pair_item(const PackPairArgs& a, int64_t u, int lane,
+                                               char* __restrict__ wl) {
+  using T = typename Elem<DT>::T;
+  if (u < a.items_in) {
+    pack_wave_item<DT, 0>((const T*)a.w_in, (const T*)a.w_sh_in, a.E, a.d, a.H, a.HP,
+                          a.in_kb, a.in_nb, a.p_in, a.fast, u, lane, wl);
+    return true;
+  }
+  u -= a.items_in;
+  if (u >= a.items_out) return false;
+  pack_wave_item<DT, 1>((const T*)a.w_out, (const T*)a.w_sh_out, a.E, a.d, a.H, a.HP,
+                        a.out_kb, a.out_nb, a.p_out, a.fast, u, lane, wl);
+  return true;
+}
 
 // The arguments of the 16-bit pack pair for these weights (pack_pair_kernel's geometry);
 // false where the pair path does not apply (fp32).
