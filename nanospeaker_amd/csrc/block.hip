@@ -16,6 +16,7 @@
 // calls while the weights do not change.  `workspace` is scratch for one call.
 #include <string.h>
 
+#include "dw_reduce.h"
 #include "experts_common.h"
 #include "norm.h"
 #include "pack.h"
@@ -277,7 +278,8 @@ int block_bwd_router(const nsmoe_experts_args* a, const nsmoe_experts_args& b,
                      const void* logits, int32_t route_flags, float aux_coef,
                      const float* grad_aux, const nsmoe_experts_grads* grads,
                      const void* w_router, void* grad_w_router, void* grad_logits, char* ws,
-                     const BwdWs& W, const int32_t* inv, bool fuse, void* dx, hipStream_t s);
+                     const BwdWs& W, const int32_t* inv, bool fuse, void* dx, hipStream_t s,
+                     const DwReduceArgs* dwr);
 }  // namespace nsmoe
 
 extern "C" size_t nsmoe_block_bwd_workspace_size(const nsmoe_experts_args* a,
@@ -326,14 +328,16 @@ extern "C" int nsmoe_block_bwd(const nsmoe_experts_args* a, const nsmoe_block_no
   g.dtopk_w = ws + W.tw;  // the gate gradient stays internal: it feeds the router backward
   // dW runs on the side stream beside everything below; joined before returning.
   hipStream_t s_dw = s;
+  // On the fused-router path the experts' dW split-K reduce rides in combine_dx's launch.
+  DwReduceArgs dwr{};
   NSMOE_TRY(experts_bwd_launch(&b, inv, grad_out, &g, ws + W.exp, W.gl - W.exp, !fuse, s, &s_dw,
-                               act_part(L, sv, route_flags)));
+                               act_part(L, sv, route_flags), fuse ? &dwr : nullptr));
   // With the norm the combine's dx is the normalised input's gradient: it goes to the
   // workspace, and the norm's backward turns it into grads->dx.
   void* dxn = norm ? (void*)(ws + W.dxn) : grads->dx;
   int rc = block_bwd_router(a, b, L, sv, topk_idx, logits, route_flags, aux_coef, grad_aux,
                             grads, w_router, grad_w_router, grad_logits, ws, W, inv, fuse, dxn,
-                            s);
+                            s, &dwr);
   if (rc == NSMOE_OK && norm) {
     NormBwdArgs n;
     n.x = a->x;
@@ -362,7 +366,8 @@ int block_bwd_router(const nsmoe_experts_args* a, const nsmoe_experts_args& b,
                      const void* logits, int32_t route_flags, float aux_coef,
                      const float* grad_aux, const nsmoe_experts_grads* grads,
                      const void* w_router, void* grad_w_router, void* grad_logits, char* ws,
-                     const BwdWs& W, const int32_t* inv, bool fuse, void* dx, hipStream_t s) {
+                     const BwdWs& W, const int32_t* inv, bool fuse, void* dx, hipStream_t s,
+                     const DwReduceArgs* dwr) {
   const bool probs = route_flags & NSMOE_ROUTE_PROBS;
   const void* src = probs ? (const void*)(sv + L.off[NSMOE_SAVED_PROBS]) : logits;
   NSMOE_REQUIRE(src, "block_bwd: NULL logits (eval branch)");
@@ -400,7 +405,7 @@ int block_bwd_router(const nsmoe_experts_args* a, const nsmoe_experts_args& b,
   r.E = E;
   r.ep = ldg;
   NSMOE_TRY(router_dw_launch(a->dtype, r, s));
-  return combine_dx_launch(a->dtype, c, &r, s);
+  return combine_dx_launch(a->dtype, c, &r, s, dwr);
 }
 
 }  // namespace nsmoe

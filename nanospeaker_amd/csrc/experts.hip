@@ -20,6 +20,7 @@
 //   bias_grad    per-group column sums for the optional biases.
 #include <algorithm>
 
+#include "dw_reduce.h"
 #include "experts_common.h"
 #include "pack.h"
 #include "../../include/nsmoe.h"
@@ -789,99 +790,16 @@ __global__ void __launch_bounds__(NT) dw_kernel(ExpParams p) {
       }
 }
 
-// Sums the fp32 partials of multi-chunk groups in chunk order.  grid = (dwr_blocks, group).
-// Each thread sums 4 consecutive elements (one 16-byte vector per chunk, every chunk's
-// load in flight at once), so the pass streams the partials at full width; the order of
-// the additions is the chunk order for every element, whatever the launch shape.
-
-template <int DT, int MODE>
-__device__ __forceinline__ void dw_reduce_group(const ExpParams& p, int g) {
-  using T = typename Elem<DT>::T;
-  const int nch = dw_chunks(rows_of(p, g));
-  if (nch <= 1) return;
-  // First partial of group g: the chunk counts of the multi-chunk groups before it,
-  // counted by all threads at once (integer sum: the order does not matter).
-  __shared__ int s_base;
-  if (threadIdx.x == 0) s_base = 0;
-  __syncthreads();
-  int part = 0;
-  for (int q = threadIdx.x; q < g; q += NT) {
-    const int c = dw_chunks(rows_of(p, q));
-    if (c > 1) part += c;
-  }
-  if (part) atomicAdd(&s_base, part);
-  __syncthreads();
-  const int d = p.d, H = p.H;
-  const int64_t mn = MODE == 0 ? (int64_t)d * 2 * H : (int64_t)H * d;
-  T* dst = g < p.E ? (T*)p.dw_a + (int64_t)g * mn : (T*)p.dw_sh + (int64_t)(g - p.E) * mn;
-  const float* src = p.partial + (int64_t)s_base * mn;
-  const int64_t n4 = (mn % 4 == 0) ? mn / 4 : 0;  // 16-byte vectors (every partial is 16-B aligned)
-  for (int64_t i = (int64_t)blockIdx.x * NT + threadIdx.x; i < n4; i += (int64_t)gridDim.x * NT) {
-    // Up to DEPTH chunks' loads in flight at once, added in chunk order.
-    constexpr int DEPTH = 16;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int c0 = 0; c0 < nch; c0 += DEPTH) {
-      f32x4 a[DEPTH];
-#pragma unroll
-      for (int u = 0; u < DEPTH; ++u)
-        if (c0 + u < nch) a[u] = ((const f32x4*)(src + (int64_t)(c0 + u) * mn))[i];
-#pragma unroll
-      for (int u = 0; u < DEPTH; ++u)
-        if (c0 + u < nch) acc += a[u];
-    }
-    if (DT != DT_F32 && ((uintptr_t)dst & 7) == 0) {  // one 8-byte store (mn % 4 == 0)
-      *(uint2*)(dst + i * 4) = make_uint2(pack2<DT>(acc[0], acc[1]), pack2<DT>(acc[2], acc[3]));
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) dst[i * 4 + e] = Elem<DT>::from_f(acc[e]);
-    }
-  }
-  for (int64_t i = n4 * 4 + (int64_t)blockIdx.x * NT + threadIdx.x; i < mn;
-       i += (int64_t)gridDim.x * NT) {
-    float acc = 0.0f;
-    for (int c = 0; c < nch; ++c) acc += src[(int64_t)c * mn + i];
-    dst[i] = Elem<DT>::from_f(acc);
-  }
-}
-
+// The dW split-K reduce (dw_reduce.h): one group per grid row, or both modes over the
+// multi-chunk groups in one launch.  grid = (dwr_blocks, rows).
 template <int DT, int MODE>
 __global__ void __launch_bounds__(NT) dw_reduce_kernel(ExpParams p) {
-  dw_reduce_group<DT, MODE>(p, blockIdx.y);
+  dw_reduce_group<DT, MODE>(p, blockIdx.y, blockIdx.x, gridDim.x);
 }
 
-// Both modes in one launch, over the groups that can have several chunks.  grid.y in
-// [0, 2 NY), NY = S + routed_rows: mode = y / NY, row j = y % NY.  Rows j < S take shared
-// group E + j.  With routed_rows = E, row S + r takes routed group r; with routed_rows = 1
-// the one row S finds the routed groups of several chunks (usually none or a few: routed
-// groups average fewer rows than a chunk) and takes them in turn.  A launch over all
-// 2 (E + S) groups spends most of its time on workgroups that only find one chunk.
 template <int DT>
-__global__ void __launch_bounds__(NT) dw_reduce_pair_kernel(ExpParams p_in, ExpParams p_out,
-                                                            int routed_rows) {
-  const int E = p_in.E, S = p_in.S, ny = S + routed_rows;
-  const int mode = (int)blockIdx.y >= ny ? 1 : 0, j = (int)blockIdx.y - mode * ny;
-  auto run = [&](int g) {
-    if (mode == 0) dw_reduce_group<DT, 0>(p_in, g);
-    else dw_reduce_group<DT, 1>(p_out, g);
-  };
-  if (j < S) {
-    run(E + j);
-  } else if (routed_rows == E) {
-    run(j - S);
-  } else {
-    __shared__ int s_list[NT];
-    __shared__ int s_n;
-    for (int g0 = 0; g0 < E; g0 += NT) {
-      if (threadIdx.x == 0) s_n = 0;
-      __syncthreads();
-      const int g = g0 + (int)threadIdx.x;
-      if (g < E && dw_chunks(rows_of(p_in, g)) > 1) s_list[atomicAdd(&s_n, 1)] = g;
-      __syncthreads();
-      const int n = s_n;
-      for (int i = 0; i < n; ++i) run(s_list[i]);
-      __syncthreads();  // the list is read before the next round rewrites it
-    }
-  }
+__global__ void __launch_bounds__(NT) dw_reduce_pair_kernel(DwReduceArgs r) {
+  dw_reduce_pair_row<DT>(r, blockIdx.x, blockIdx.y);
 }
 
 // Rows of routed groups in dw_reduce_pair_kernel's grid: one per routed group when an
@@ -1110,7 +1028,7 @@ static BwdLayout bwd_layout(const nsmoe_experts_args* a) {
 template <int DT>
 static int experts_dw(const nsmoe_experts_args* a, const ExpParams& p,
                       const nsmoe_experts_grads* gr, char* ws, const BwdLayout& L,
-                      hipStream_t s) {
+                      hipStream_t s, DwReduceArgs* defer) {
   const int G = a->n_experts + a->n_shared;
   const int d = a->d_model, H = a->d_hidden;
   const int64_t gc = dw_groups_chunks(a);
@@ -1125,9 +1043,13 @@ static int experts_dw(const nsmoe_experts_args* a, const ExpParams& p,
   if (prc != -1) {
     NSMOE_TRY(prc);
     const int rr = dw_reduce_routed_rows(a);
-    dim3 rg(dwr_blocks(a), (unsigned)(2 * (a->n_shared + rr)));
-    dw_reduce_pair_kernel<DT><<<rg, NT, 0, s>>>(q_in, q_out, rr);
-    NSMOE_TRY(check_launch("dw_reduce_pair_kernel"));
+    const DwReduceArgs r{q_in, q_out, rr, (int)dwr_blocks(a), 2 * (a->n_shared + rr)};
+    if (defer) {  // the caller's later launch runs it
+      *defer = r;
+    } else {
+      dw_reduce_pair_kernel<DT><<<dim3((unsigned)r.nbx, (unsigned)r.rows), NT, 0, s>>>(r);
+      NSMOE_TRY(check_launch("dw_reduce_pair_kernel"));
+    }
   } else {
     {  // dW_in
       const ExpParams& q = q_in;
@@ -1189,7 +1111,8 @@ static int experts_dw(const nsmoe_experts_args* a, const ExpParams& p,
 template <int DT>
 static int experts_bwd_impl(const nsmoe_experts_args* a, const int32_t* inv, const void* dout,
                             const nsmoe_experts_grads* gr, char* ws, bool combine,
-                            hipStream_t s, hipStream_t* side_out, const void* act_in) {
+                            hipStream_t s, hipStream_t* side_out, const void* act_in,
+                            DwReduceArgs* defer) {
   const BwdLayout L = bwd_layout(a);
   ExpParams p = make_params(a);
   // The forward wrote them under the same condition (p.fast here before dout's alignment
@@ -1215,7 +1138,10 @@ static int experts_bwd_impl(const nsmoe_experts_args* a, const int32_t* inv, con
     NSMOE_TRY(check_launch("expert_bwd_kernel"));
   }
   hipStream_t s2 = side_fork(s, kSideSlotDw);
-  int rc = experts_dw<DT>(a, p, gr, ws, L, s2);
+  // The reduce is handed to the caller only while dW runs on s itself (its partials are
+  // then complete before any later launch on s).
+  if (defer) defer->nbx = 0;
+  int rc = experts_dw<DT>(a, p, gr, ws, L, s2, s2 == s ? defer : nullptr);
   if (rc == NSMOE_OK && arc != -1) rc = launch_bwd_async(DT, p, nbw, grid, 1, s);
   if (rc == NSMOE_OK && combine)
     rc = launch_combine<DT>(ws + L.dxrow, inv, a->n_tokens, a->d_model, a->top_k, a->n_shared,
@@ -1287,7 +1213,7 @@ namespace nsmoe {
 int experts_bwd_launch(const nsmoe_experts_args* a, const int32_t* inv, const void* grad_out,
                        const nsmoe_experts_grads* grads, void* workspace,
                        size_t workspace_bytes, bool combine, hipStream_t s,
-                       hipStream_t* side_out, const void* act_in) {
+                       hipStream_t* side_out, const void* act_in, DwReduceArgs* defer) {
   NSMOE_TRY(validate(a));
   NSMOE_REQUIRE(grads, "experts_bwd: NULL grads");
   if (a->n_tokens == 0) return NSMOE_OK;
@@ -1306,13 +1232,13 @@ int experts_bwd_launch(const nsmoe_experts_args* a, const int32_t* inv, const vo
   switch (a->dtype) {
     case DT_BF16:
       return experts_bwd_impl<DT_BF16>(a, inv, grad_out, grads, (char*)workspace, combine, s,
-                                       side_out, act_in);
+                                       side_out, act_in, defer);
     case DT_F16:
       return experts_bwd_impl<DT_F16>(a, inv, grad_out, grads, (char*)workspace, combine, s,
-                                       side_out, act_in);
+                                       side_out, act_in, defer);
     default:
       return experts_bwd_impl<DT_F32>(a, inv, grad_out, grads, (char*)workspace, combine, s,
-                                       side_out, act_in);
+                                       side_out, act_in, defer);
   }
 }
 

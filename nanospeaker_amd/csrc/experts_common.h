@@ -156,6 +156,7 @@ struct nsmoe_experts_args;
 struct nsmoe_experts_grads;
 
 namespace nsmoe {
+struct DwReduceArgs;  // dw_reduce.h
 // nsmoe_experts_bwd; with combine = false the per-row dX stay in the workspace at
 // experts_bwd_dxrows_offset(a) (rows as the forward's row space) and grads->dx is unused.
 // The dW stage runs on the side stream (side_fork slot kSideSlotDw); with side_out != NULL
@@ -163,10 +164,14 @@ namespace nsmoe {
 // side_join(stream, *side_out, kSideSlotDw), otherwise it is joined before returning.
 // act_in: the forward's saved pre-activations (experts_fwd_launch's act_out), or NULL to
 // recompute them.
+// defer_reduce: when set and dW runs on `stream`, the dW split-K reduce is not launched
+// but described there (nbx > 0) for a later launch on the stream to run (combine_dx's);
+// nbx = 0 when it ran here.
 int experts_bwd_launch(const ::nsmoe_experts_args* a, const int32_t* inv, const void* grad_out,
                        const ::nsmoe_experts_grads* grads, void* workspace,
                        size_t workspace_bytes, bool combine, hipStream_t stream,
-                       hipStream_t* side_out, const void* act_in = nullptr);
+                       hipStream_t* side_out, const void* act_in = nullptr,
+                       DwReduceArgs* defer_reduce = nullptr);
 size_t experts_bwd_dxrows_offset(const ::nsmoe_experts_args* a);
 // nsmoe_experts_fwd that also writes the pre-activations a1 = x W_in + b_in (act_block's
 // layout) to act_out when experts_save_act_bytes(a) > 0 -- the backward then reads them

@@ -34,9 +34,12 @@ bool router_grad_supported(int dtype, int d, int E);
 int router_logits_pitch(int E);
 size_t router_dw_partial_bytes(int64_t T, int d, int E);
 // combine_dx; with rdw set the same launch also reduces router_dw_kernel's partials into
-// rdw->dw (router_dw_launch must have run before it on the stream).
+// rdw->dw (router_dw_launch must have run before it on the stream), and with dwr set
+// (nbx > 0) the experts' dW split-K reduce (experts_bwd_launch's defer_reduce; the dW
+// launch must have run before it on the stream).
+struct DwReduceArgs;
 int combine_dx_launch(int dtype, const CombineDxArgs& a, const RouterDwArgs* rdw,
-                      hipStream_t stream);
+                      hipStream_t stream, const DwReduceArgs* dwr = nullptr);
 // The router dW's partials (router_dw_kernel) alone.
 int router_dw_launch(int dtype, const RouterDwArgs& a, hipStream_t stream);
 

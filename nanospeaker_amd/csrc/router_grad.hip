@@ -17,6 +17,7 @@
 //
 // d(logits) arrives from route_bwd with a row pitch `ep` = E rounded up to 8 (16-byte rows,
 // zero in the pad columns), which both kernels read as MFMA operands directly.
+#include "dw_reduce.h"
 #include "experts_common.h"
 #include "router_grad.h"
 
@@ -94,16 +95,25 @@ inline int64_t router_dw_reduce_blocks(int d, int ep) { return cdiv((int64_t)d *
 //
 // With `rdw` set, workgroups past the token tiles (blockIdx.x >= tx) are the router dW's
 // reduce instead: its fp32 partials summed in chunk order into W.grad, streaming beside
-// the combine rather than as a launch of its own.
+// the combine rather than as a launch of its own.  Workgroups from wx on are the experts'
+// dW split-K reduce (dw_reduce.h) when dwr.nbx > 0: the token tiles cover about half of
+// the CUs, and the reduce streams on the others instead of in a launch of its own.
 template <int DT, int KM>
 __global__ void __launch_bounds__(NT, KM <= 6 ? 4 : 3)
-combine_dx_kernel(CombineDxArgs a, RouterDwArgs rdw, int rchunks, int tx) {
+combine_dx_kernel(CombineDxArgs a, RouterDwArgs rdw, int rchunks, int tx, DwReduceArgs dwr,
+                  int wx) {
   using G = Geo<DT>;
   using T = typename G::T;
   using M = Mma<DT>;
   using Frag = typename M::Frag;
   __shared__ __attribute__((aligned(16))) float s_acc[4][16][CDX_PITCH];
   __shared__ __attribute__((aligned(1024))) char s_w[4 * CDX_KS][1024];  // the W tile
+  if ((int)blockIdx.x >= wx) {  // uniform: an experts' dW reduce workgroup
+    const int64_t f = (int64_t)(blockIdx.x - wx) * gridDim.y + blockIdx.y;
+    const int y = (int)(f / dwr.nbx), bx = (int)(f - (int64_t)y * dwr.nbx);
+    if (y < dwr.rows) dw_reduce_pair_row<DT>(dwr, bx, y);
+    return;
+  }
   if ((int)blockIdx.x >= tx) {  // uniform: a router dW reduce workgroup
     router_dw_reduce_block<DT>(rdw, rchunks,
                                (int64_t)(blockIdx.x - tx) * gridDim.y + blockIdx.y);
@@ -362,7 +372,7 @@ size_t router_dw_partial_bytes(int64_t T, int d, int E) {
 }
 
 int combine_dx_launch(int dtype, const CombineDxArgs& a, const RouterDwArgs* rdw,
-                      hipStream_t s) {
+                      hipStream_t s, const DwReduceArgs* dwr) {
   NSMOE_REQUIRE(router_grad_supported(dtype, a.d, a.E) && a.ep == router_logits_pitch(a.E),
                 "combine_dx: unsupported shape (d %d, E %d, pitch %d)", a.d, a.E, a.ep);
   NSMOE_REQUIRE(!rdw || (rdw->d == a.d && rdw->ep == a.ep && rdw->T == a.T && rdw->partial &&
@@ -373,19 +383,29 @@ int combine_dx_launch(int dtype, const CombineDxArgs& a, const RouterDwArgs* rdw
                 (long long)(a.l_cap + (int64_t)a.S * a.T));
   const int64_t tx = cdiv(a.T, CDX_TOK), ty = cdiv(a.d, CDX_COLS);
   const int64_t rx = rdw ? cdiv(router_dw_reduce_blocks(a.d, a.ep), ty) : 0;
-  NSMOE_REQUIRE(tx + rx < INT32_MAX, "combine_dx: %lld tokens", (long long)a.T);
-  const dim3 grid((unsigned)(tx + rx), (unsigned)ty);
+  // The experts' dW reduce workgroups, flattened over the grid's columns.
+  const bool red = dwr && dwr->nbx > 0 && dwr->rows > 0;
+  const int64_t wx = tx + rx;
+  const int64_t dx_extra = red ? cdiv((int64_t)dwr->nbx * dwr->rows, ty) : 0;
+  NSMOE_REQUIRE(wx + dx_extra < INT32_MAX, "combine_dx: %lld tokens", (long long)a.T);
+  const dim3 grid((unsigned)(wx + dx_extra), (unsigned)ty);
+  DwReduceArgs dr{};
+  if (red) dr = *dwr;
   const RouterDwArgs r = rdw ? *rdw : RouterDwArgs{};
   const int rchunks = rdw ? (int)cdiv(a.T, RDW_RC) : 0;
   KernelTimer timer("combine_dx", s);
   if (a.k <= 6) {
     if (dtype == DT_BF16)
-      combine_dx_kernel<DT_BF16, 6><<<grid, NT, 0, s>>>(a, r, rchunks, (int)tx);
-    else combine_dx_kernel<DT_F16, 6><<<grid, NT, 0, s>>>(a, r, rchunks, (int)tx);
+      combine_dx_kernel<DT_BF16, 6><<<grid, NT, 0, s>>>(a, r, rchunks, (int)tx, dr,
+                                                               (int)wx);
+    else combine_dx_kernel<DT_F16, 6><<<grid, NT, 0, s>>>(a, r, rchunks, (int)tx, dr,
+                                                               (int)wx);
   } else {
     if (dtype == DT_BF16)
-      combine_dx_kernel<DT_BF16, CDX_KMAX><<<grid, NT, 0, s>>>(a, r, rchunks, (int)tx);
-    else combine_dx_kernel<DT_F16, CDX_KMAX><<<grid, NT, 0, s>>>(a, r, rchunks, (int)tx);
+      combine_dx_kernel<DT_BF16, CDX_KMAX><<<grid, NT, 0, s>>>(a, r, rchunks, (int)tx, dr,
+                                                               (int)wx);
+    else combine_dx_kernel<DT_F16, CDX_KMAX><<<grid, NT, 0, s>>>(a, r, rchunks, (int)tx, dr,
+                                                               (int)wx);
   }
   timer.stop();
   return check_launch("combine_dx_kernel");
