@@ -156,7 +156,9 @@ int nsmoe_dispatch(const int64_t* topk_idx, int64_t n_pairs, int32_t n_experts,
  * until the process ends), so it takes calls whose nsmoe_dispatch_workspace_size is at
  * most 4 MiB -- up to 14,128,128 pairs at 76 experts, 262,144 at 1024 -- and rejects
  * larger ones with error 1.  It allocates nothing.  Every call on a device shares that
- * device's array: calls that overlap on one device (two streams, two threads) race. */
+ * device's array: calls that overlap on one device (two streams, two threads) race.
+ * The first call on each device resolves the array's address and must not be made under
+ * HIP graph capture (error 1 if it is); later calls, captured or not, reuse it. */
 int nsmoe_dispatch_noalloc(const int64_t* topk_idx, int64_t n_pairs, int32_t n_experts,
                            int32_t* sorted_ids, int32_t* expert_ids, int32_t* pad_offsets,
                            int32_t* counts, int32_t* n_post_pad, int32_t* inv, void* stream);

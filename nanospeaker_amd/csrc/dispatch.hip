@@ -453,7 +453,10 @@ constexpr int kScratchDevices = 64;
 static void* g_scratch[kScratchDevices];
 static std::mutex g_scratch_mu;
 
-static int dispatch_scratch(void** out) {
+// The symbol lookup is not a stream operation and may load the code object, which a
+// graph capture must not see: a device's first call under capture is refused (one call
+// outside capture, of any size, resolves the address for every later one).
+static int dispatch_scratch(void** out, hipStream_t stream) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess || dev < 0 || dev >= kScratchDevices) {
@@ -462,6 +465,14 @@ static int dispatch_scratch(void** out) {
   }
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch[dev]) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(stream, &cs);
+    if (e != hipSuccess || cs != hipStreamCaptureStatusNone) {
+      set_error("dispatch_noalloc: the first call on device %d is under graph capture; "
+                "make one call outside capture first (it resolves the scratch address)",
+                dev);
+      return NSMOE_EINVAL;
+    }
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || !p) {
@@ -491,7 +502,7 @@ extern "C" int nsmoe_dispatch_noalloc(const int64_t* topk_idx, int64_t n_pairs,
                 "its %zu B maximum (use nsmoe_dispatch with a workspace)",
                 (long long)n_pairs, n_experts, need, kDispatchScratchBytes);
   void* ws = nullptr;
-  if (need > 0) NSMOE_TRY(dispatch_scratch(&ws));
+  if (need > 0) NSMOE_TRY(dispatch_scratch(&ws, (hipStream_t)stream));
   return dispatch_launch(topk_idx, n_pairs, n_experts, sorted_ids, expert_ids, pad_offsets,
                          counts, n_post_pad, inv, ws, kDispatchScratchBytes, nullptr, stream);
 }

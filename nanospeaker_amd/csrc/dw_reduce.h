@@ -18,8 +18,12 @@ __device__ __forceinline__ void dw_reduce_group(const ExpParams& p, int g, int b
   const int nch = dw_chunks(rows_of(p, g));
   if (nch <= 1) return;
   // First partial of group g: the chunk counts of the multi-chunk groups before it,
-  // counted by all threads at once (integer sum: the order does not matter).
+  // counted by all threads at once (integer sum: the order does not matter).  A caller
+  // may run several groups in turn (dw_reduce_pair_row): the barrier before the reset
+  // keeps thread 0 from clearing s_base while a slower wave still reads the previous
+  // group's value.
   __shared__ int s_base;
+  __syncthreads();
   if (threadIdx.x == 0) s_base = 0;
   __syncthreads();
   int part = 0;

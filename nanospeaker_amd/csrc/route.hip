@@ -491,6 +491,7 @@ int route_bwd_launch(const void* src, const int64_t* topk_idx, const void* grad_
   const RouterWPack pk = pack ? *pack : RouterWPack{nullptr, nullptr, 0, 0, 1};
   dim3 grid((unsigned)(row_blocks + pack_blocks)), block(ROUTE_THREADS);
   size_t lds = (size_t)n_experts * ROUTE_WAVES * sizeof(float) * 2;
+  KernelTimer timer("route_bwd", s);
   switch (w_dtype) {
     case DT_BF16:
       route_bwd_kernel<DT_BF16><<<grid, block, lds, s>>>(src, topk_idx, (const uint16_t*)grad_w,
@@ -510,6 +511,7 @@ int route_bwd_launch(const void* src, const int64_t* topk_idx, const void* grad_
     default:
       NSMOE_REQUIRE(false, "route_bwd: unknown dtype %d", w_dtype);
   }
+  timer.stop();
   return check_launch("route_bwd_kernel");
 }
 

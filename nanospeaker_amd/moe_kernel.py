@@ -24,6 +24,7 @@ import ctypes
 import threading
 import weakref
 from collections import OrderedDict
+from contextlib import contextmanager, nullcontext
 from typing import Optional
 
 import torch
@@ -48,6 +49,7 @@ DISPATCH_MAX_EXPERTS = 1024
 MAX_GROUPS = 1024
 
 _DT = {torch.bfloat16: nat.BF16, torch.float16: nat.F16, torch.float32: nat.F32}
+_DT_TORCH = {v: k for k, v in _DT.items()}
 
 
 def kernel_supported(t: Tensor) -> bool:
@@ -242,6 +244,18 @@ def _c(t: Optional[Tensor]) -> Optional[Tensor]:
     return None if t is None else t.contiguous()
 
 
+class _PackEntry:
+    """One cached pack: weak references to the key tensors and their states, the two
+    buffers, the stream they were packed on, what refresh() needs to pack them again, and
+    whether a captured graph reads them (then LRU eviction skips the entry)."""
+
+    __slots__ = ("refs", "states", "p_in", "p_out", "stream", "spec", "pinned")
+
+    def __init__(self, refs, states, p_in, p_out, stream, spec):
+        self.refs, self.states, self.p_in, self.p_out = refs, states, p_in, p_out
+        self.stream, self.spec, self.pinned = stream, spec, False
+
+
 class PackCache:
     """
     The expert weights' fragment-order packs (nsmoe_pack_weights), kept while the weights
@@ -255,18 +269,37 @@ class PackCache:
     the tensor or a view of it (an optimizer step, load_state_dict, `copy_`) bumps the
     version, and the next call packs into a fresh buffer; an autograd graph that still
     holds the old pack keeps it.  Writes through `.data` bypass the version counter: call
-    `clear()` after them.  While the current stream is being captured into a HIP graph
-    the cache is bypassed, so the graph packs on every replay.  At most `capacity`
-    weight sets are kept (least recently used out); an entry goes as soon as one of its
-    weights is freed.
+    `clear()` (or `refresh()`) after them.  At most `capacity` weight sets are kept (least
+    recently used out); an entry goes as soon as one of its weights is freed.
+
+    * **Casts.** A caller whose parameters are in another dtype than x (an autocast-style
+      fp32 master copy with bf16 activations) hands the op cast temporaries that die with
+      the call.  `sources({id(temp): param})` names the parameter each temporary was cast
+      from for the calls made inside it; the entry is then keyed on the parameters (and
+      the packed dtype), so the next call and the checkpoint's recompute hit.
+    * **Streams.** A pack is enqueued on the stream current at the miss.  A hit from
+      another stream makes that stream wait for the packing stream and marks the buffers
+      as used there (`record_stream`), so neither a half-written pack nor a freed one is
+      read.
+    * **Graphs.** While the current stream is being captured into a HIP graph the cache
+      is bypassed by default and the graph packs on every replay.  With
+      `share_with_graphs = True` a capture that finds a valid entry reads its buffers
+      directly (no pack in the graph: a decode step's replay then moves only the routed
+      rows and the weights once), and the entry is pinned: it is no longer evicted, and
+      keeps its buffers, until `clear()`.  Such a graph reads whatever the buffers hold
+      at replay: after an in-place weight update, call `refresh()` (it repacks every
+      live entry into its own buffers, on the current stream) before replaying.  A
+      capture that misses still packs inside the graph and files nothing.
     """
 
     def __init__(self, capacity: int = 64):
         self.capacity = capacity
         self.hits = 0
         self.misses = 0
+        self.share_with_graphs = False
         self._lock = threading.RLock()
-        self._entries: "OrderedDict[tuple, tuple]" = OrderedDict()
+        self._entries: "OrderedDict[tuple, _PackEntry]" = OrderedDict()
+        self._local = threading.local()
 
     @staticmethod
     def _state(t: Tensor) -> tuple:
@@ -283,46 +316,108 @@ class PackCache:
     def __len__(self) -> int:
         return len(self._entries)
 
-    def lookup(self, nbytes: "tuple[int, int]", device, *weights):
+    @contextmanager
+    def sources(self, mapping: "dict[int, Tensor]"):
+        """Within the block, a weight w handed to lookup() with id(w) in `mapping` is keyed
+        on mapping[id(w)], the tensor it was cast from."""
+        prev = getattr(self._local, "src", None)
+        self._local.src = mapping
+        try:
+            yield
+        finally:
+            self._local.src = prev
+
+    def _key_tensor(self, w: Tensor) -> Tensor:
+        src = getattr(self._local, "src", None)
+        return src.get(id(w), w) if src else w
+
+    def lookup(self, nbytes: "tuple[int, int]", device, *weights, spec=None):
         """
         (packed W_in, packed W_out, pending) for these weights (W_in, W_out, W_sh_in,
         W_sh_out; the shared ones may be None).  pending is None on a hit; otherwise the
         buffers are new and still to be packed, and `store(pending, ...)` files them once
-        the pack is enqueued.
+        the pack is enqueued.  `spec` = (dtype, d_model, d_hidden, n_experts, n_shared)
+        lets refresh() pack the entry again.
         """
         present = tuple(w for w in weights if w is not None)
-        if torch.device(device).type == "cuda" and torch.cuda.is_current_stream_capturing():
-            pending = None, ()
-        else:
-            key = tuple(w.data_ptr() for w in present) + (len(present),)
+        cuda = torch.device(device).type == "cuda"
+        capturing = cuda and torch.cuda.is_current_stream_capturing()
+        pending = None, ()
+        if not capturing or self.share_with_graphs:
+            keys = tuple(self._key_tensor(w) for w in present)
+            key = (tuple(k.data_ptr() for k in keys) + (len(keys),)
+                   + tuple(w.dtype for w in present))
             with self._lock:
                 entry = self._entries.get(key)
                 if entry is not None:
-                    refs, states, p_in, p_out = entry
-                    if all(r() is w for r, w in zip(refs, present)) and all(
-                            s == self._state(w) for s, w in zip(states, present)):
+                    if all(r() is k for r, k in zip(entry.refs, keys)) and all(
+                            s == self._state(k) for s, k in zip(entry.states, keys)):
                         self._entries.move_to_end(key)
                         self.hits += 1
-                        return p_in, p_out, None
-                    del self._entries[key]
-            pending = key, present
+                        if capturing:
+                            entry.pinned = True
+                        elif cuda:
+                            cur = torch.cuda.current_stream(device)
+                            if entry.stream is not None and cur != entry.stream:
+                                cur.wait_stream(entry.stream)
+                                entry.p_in.record_stream(cur)
+                                entry.p_out.record_stream(cur)
+                        return entry.p_in, entry.p_out, None
+                    if not entry.pinned:
+                        del self._entries[key]
+            if not capturing:
+                pending = key, keys, spec
         self.misses += 1
         p_in = torch.empty(nbytes[0], dtype=torch.uint8, device=device)
         p_out = torch.empty(nbytes[1], dtype=torch.uint8, device=device)
         return p_in, p_out, pending
 
     def store(self, pending, p_in: Tensor, p_out: Tensor) -> None:
-        key, present = pending
-        if not present:
+        key, keys = pending[0], pending[1]
+        if not keys:
             return
+        spec = pending[2] if len(pending) > 2 else None
         cb = lambda _ref, key=key: self._drop(key)
-        entry = (tuple(weakref.ref(w, cb) for w in present),
-                 tuple(self._state(w) for w in present), p_in, p_out)
+        stream = torch.cuda.current_stream(p_in.device) if p_in.is_cuda else None
+        entry = _PackEntry(tuple(weakref.ref(k, cb) for k in keys),
+                           tuple(self._state(k) for k in keys), p_in, p_out, stream, spec)
         with self._lock:
+            old = self._entries.get(key)
+            if old is not None and old.pinned:
+                return  # a graph reads the pinned buffers; refresh() updates them
             self._entries[key] = entry
             self._entries.move_to_end(key)
-            while len(self._entries) > self.capacity:
-                self._entries.popitem(last=False)
+            over = len(self._entries) - self.capacity
+            for k in [k for k, e in self._entries.items() if not e.pinned][:max(over, 0)]:
+                del self._entries[k]
+
+    def refresh(self) -> int:
+        """Pack every live entry again from its weights' current values, into its own
+        buffers, on the current stream, and record the new versions.  For graphs captured
+        with `share_with_graphs` after an in-place weight update (they hold the buffers'
+        addresses).  Returns the number of entries repacked."""
+        n = 0
+        with self._lock:
+            for entry in list(self._entries.values()):
+                keys = [r() for r in entry.refs]
+                if any(k is None for k in keys) or entry.spec is None:
+                    continue
+                dt, d, h, e, s = entry.spec
+                ws = [k if k.dtype == dt else k.detach().to(dt) for k in keys]
+                ws = [w.contiguous() for w in ws]
+                a = nat.ExpertsArgs(dtype=_DT[dt], activation=0, n_tokens=0, d_model=d,
+                                    d_hidden=h, n_experts=e, n_shared=s, top_k=1,
+                                    reserved0=0, l_cap=0, w_in=ws[0].data_ptr(),
+                                    w_out=ws[1].data_ptr(),
+                                    w_sh_in=ws[2].data_ptr() if s else None,
+                                    w_sh_out=ws[3].data_ptr() if s else None)
+                nat.check(nat.lib().nsmoe_pack_weights(a, entry.p_in.data_ptr(),
+                                                       entry.p_out.data_ptr(), _stream()),
+                          "nsmoe_pack_weights")
+                entry.states = tuple(self._state(k) for k in keys)
+                entry.stream = torch.cuda.current_stream(entry.p_in.device)
+                n += 1
+        return n
 
 
 PACKS = PackCache()
@@ -343,13 +438,38 @@ def _pack_sizes(args: nat.ExpertsArgs) -> "tuple[int, int]":
 
 def _pack(args: nat.ExpertsArgs, device, weights):
     """Weights in MFMA fragment order, from the pack cache or packed now: (W_in, W_out)."""
-    p_in, p_out, pending = PACKS.lookup(_pack_sizes(args), device, *weights)
+    spec = (_DT_TORCH[args.dtype], args.d_model, args.d_hidden, args.n_experts, args.n_shared)
+    p_in, p_out, pending = PACKS.lookup(_pack_sizes(args), device, *weights, spec=spec)
     if pending is not None:
         nat.check(nat.lib().nsmoe_pack_weights(args, p_in.data_ptr(), p_out.data_ptr(),
                                                _stream()), "nsmoe_pack_weights")
         PACKS.store(pending, p_in, p_out)
     args.w_in_packed, args.w_out_packed = p_in.data_ptr(), p_out.data_ptr()
     return p_in, p_out
+
+
+def _cast_params(dtype: torch.dtype, *params, contiguous: bool = False):
+    """(each param cast to dtype -- itself when it already is, and contiguous if asked --,
+    {id(cast): param} for the ones that became new tensors): the pack cache keys those on
+    the parameters (PackCache.sources), so a cast temporary's pack is found again on the
+    next call."""
+    out, srcs = [], {}
+    for t in params:
+        c = None if t is None else t.to(dtype)
+        if c is not None and contiguous:
+            c = c.contiguous()
+        if c is not None and c is not t:
+            srcs[id(c)] = t
+        out.append(c)
+    return out, srcs
+
+
+def _sources(srcs):
+    """PackCache.sources(srcs) for an eager call that cast parameters, else a no-op (a
+    traced call's casts are made at run time by the compiled graph)."""
+    if srcs and not torch.compiler.is_compiling():
+        return PACKS.sources(srcs)
+    return nullcontext()
 
 
 def _check_activation(activation: str) -> None:
@@ -616,9 +736,10 @@ def fused_moe_forward(x, w_in, w_out, topk_w, topk_idx, b_in, b_out, activation)
     """
     _check_activation(activation)
     sids, eids, offs, counts, npp, inv = moe_dispatch(topk_idx, w_in.shape[0])
-    cast = lambda t: None if t is None else t.to(x.dtype)
-    out = moe_experts(x, cast(w_in), cast(w_out), topk_w.to(x.dtype), cast(b_in),
-                      cast(b_out), sids, eids, offs, counts, npp, inv, activation)
+    (w_in, w_out, b_in, b_out), srcs = _cast_params(x.dtype, w_in, w_out, b_in, b_out)
+    with _sources(srcs):
+        out = moe_experts(x, w_in, w_out, topk_w.to(x.dtype), b_in, b_out, sids, eids, offs,
+                          counts, npp, inv, activation)
     return out, counts
 
 
@@ -627,10 +748,10 @@ def fused_moe_block_forward(x, w_in, w_out, topk_w, topk_idx, b_in, b_out, w_sh_
     """fused_moe_forward with the shared experts folded into the same grouped launch."""
     _check_activation(activation)
     sids, eids, offs, counts, npp, inv = moe_dispatch(topk_idx, w_in.shape[0])
-    cast = lambda t: None if t is None else t.to(x.dtype)
-    out, _ = moe_block(x, cast(w_in), cast(w_out), cast(w_sh_in), cast(w_sh_out), cast(b_in),
-                       cast(b_out), cast(b_sh_in), cast(b_sh_out), topk_w.to(x.dtype), sids,
-                       offs, counts, inv, activation)
+    params, srcs = _cast_params(x.dtype, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in,
+                                b_sh_out)
+    with _sources(srcs):
+        out, _ = moe_block(x, *params, topk_w.to(x.dtype), sids, offs, counts, inv, activation)
     return out, counts
 
 
@@ -815,7 +936,7 @@ def _block_fwd_impl(x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in
     a = plan.bind(x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out)
     if n:
         p_in, p_out, pending = PACKS.lookup(plan.pack_bytes, dev, w_in, w_out, w_sh_in,
-                                            w_sh_out)
+                                            w_sh_out, spec=(dt, d, h2 // 2, e, s))
         a.w_in_packed, a.w_out_packed = p_in.data_ptr(), p_out.data_ptr()
         ws = torch.empty(plan.fwd_ws, dtype=torch.uint8, device=dev)
         nrm = None
@@ -1075,17 +1196,16 @@ def block_forward_state(x, router_W, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out
             xn, router_W, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out,
             top_k, want_probs, normalize, activation, aux_coef, logit_bias)
         return x + out, aux, counts, topk_idx, logits, saved, flags
-    cast = lambda t: None if t is None else t.to(x.dtype)
     op = block_fwd if torch.compiler.is_compiling() else _BlockEager.apply
     # The pre-activations are saved only for a forward that autograd will run backward
     # through (a checkpointed block's first, gradient-free forward does not save them).
     params = (router_W, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out, norm_w)
     save_act = SAVE_ACT and torch.is_grad_enabled() and (
         x.requires_grad or any(t is not None and t.requires_grad for t in params))
-    out, aux, counts, topk_idx, logits, saved, _ = op(
-        x.contiguous(), cast(router_W).contiguous(), cast(w_in).contiguous(),
-        cast(w_out).contiguous(), _c(cast(w_sh_in)), _c(cast(w_sh_out)), _c(cast(b_in)),
-        _c(cast(b_out)), _c(cast(b_sh_in)), _c(cast(b_sh_out)), top_k, want_probs, normalize,
-        activation, float(aux_coef), logit_bias, save_act, _c(cast(norm_w)), float(norm_eps))
+    cast, srcs = _cast_params(x.dtype, *params, contiguous=True)
+    with _sources(srcs):
+        out, aux, counts, topk_idx, logits, saved, _ = op(
+            x.contiguous(), *cast[:9], top_k, want_probs, normalize, activation,
+            float(aux_coef), logit_bias, save_act, cast[9], float(norm_eps))
     flags = _route_bits(x.dtype, want_probs, normalize, save_act, norm_w is not None)
     return out, aux, counts, topk_idx, logits, saved, flags

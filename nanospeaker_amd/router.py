@@ -12,9 +12,13 @@ class TopKRouter(nn.Module):
     Softmax router sending each token to its top_k experts; same constructor, parameter
     (`W` [d_model, n_experts]) and outputs as the reference TopKRouter.
 
-    The logits GEMM `(x @ W).float()` and the optional exploration noise run in torch.
-    On a GPU the rest -- softmax, top-k with CPU torch.topk's tie order, renormalisation
-    and the cast -- is one HIP kernel (`moe_kernel.route`), and its backward another.
+    MoEBlock's kernel path does not call this forward: there the logits GEMM x @ W, the
+    softmax, top-k with CPU torch.topk's tie order, renormalisation, the cast and the
+    dispatch histograms are one HIP kernel (`router_fwd_kernel`, through
+    `moe_kernel.block_forward`), and the GEMM's backward runs in the block's backward
+    kernels.  Called on its own (the reference's standalone router), the logits GEMM
+    `(x @ W).float()` and the optional exploration noise run in torch, and on a GPU the
+    tail is one HIP kernel (`moe_kernel.route`), its backward another.
     """
 
     def __init__(self, d_model: int, n_experts: int, top_k: int = 2,

@@ -3,7 +3,6 @@
 from typing import Callable
 
 import torch
-from torch import nn
 
 Activation = Callable[[torch.Tensor], torch.Tensor]
 
@@ -17,11 +16,6 @@ ACTIVATIONS: "dict[str, Activation]" = {
     "sigmoid": torch.sigmoid,
     "tanh": torch.tanh,
 }
-
-
-def initialize_normal_torch_weights(M, N, std=0.02) -> nn.Parameter:
-    """An [M, N] parameter drawn from N(0, std^2) (reference: utils.py:22-24)."""
-    return nn.Parameter(torch.randn(M, N) * std)
 
 
 def resolve_activation(activation: "str | Activation") -> "tuple[str, Activation]":

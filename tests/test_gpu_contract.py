@@ -225,3 +225,37 @@ def test_pack_cache_reuse_and_invalidation():
     assert torch.equal(m._routing.cpu(), ref.topk_idx)
     assert_close_bf16("out after the update", out3.float().cpu(), ref.out)
     assert not torch.equal(out3, out1)
+
+
+def test_pack_cache_hits_for_cast_parameters():
+    """fp32 parameters with bf16 activations (an autocast-style caller): every call hands
+    the op fresh bf16 casts, and the cache, keyed on the parameters, packs once -- the
+    second call and the reentrant checkpoint's forward and recompute all hit -- while
+    the output still matches the oracle run on the cast weights."""
+    print("[contract] pack cache with cast parameters", flush=True)
+    torch.manual_seed(0)
+    m = MoEBlock(576, 76, d_ff=192, top_k=6, n_shared=2, capacity_factor=None, fused=False)
+    m = m.to(DEV).eval()  # fp32 parameters
+    x = torch.randn(512, 576).to(torch.bfloat16)
+    xd = x.to(DEV)
+    mk.PACKS.clear()
+    h0, m0 = mk.PACKS.hits, mk.PACKS.misses
+    with torch.no_grad():
+        out1 = m(xd)
+        out2 = m(xd)
+    assert (mk.PACKS.misses - m0, mk.PACKS.hits - h0) == (1, 1)
+    assert torch.equal(out1, out2)
+    fields = ("W_in", "W_out", "W_sh_in", "W_sh_out")
+    p = R.Params(m.router.W.detach().cpu().to(torch.bfloat16),
+                 *(getattr(m, f).detach().cpu().to(torch.bfloat16) for f in fields))
+    ref = R.block(x, p, 6, train=False, fp32=True, logits=m._logits.float().cpu())
+    assert torch.equal(m._routing.cpu(), ref.topk_idx)
+    assert_close_bf16("out, cast parameters", out1.float().cpu(), ref.out)
+    m.train()
+    xg = xd.clone().requires_grad_(True)
+    out, aux = checkpoint(lambda t: (m(t), m.aux_loss), xg, use_reentrant=True)
+    ((out.float() ** 2).mean() + aux).backward()
+    torch.cuda.synchronize()
+    assert (mk.PACKS.misses - m0, mk.PACKS.hits - h0) == (1, 3), \
+        (mk.PACKS.misses - m0, mk.PACKS.hits - h0)
+    assert all(t.grad is not None and t.grad.dtype == torch.float32 for t in m.parameters())

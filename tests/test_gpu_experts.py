@@ -144,17 +144,22 @@ def test_backward_tile_heights_and_prefetch(mb, dist, bwd_dist, bwd_mb, shape, T
 
 def test_dw_reduce_skewed_routing():
     """Routed experts average far fewer rows than a dW chunk (768), so the dW reduce takes
-    them in its one looping row; expert 0 still gets 900 rows (two chunks) and must be
-    summed there, beside the shared experts."""
+    them in its one looping row; experts 0, 1 and 2 still get 900+ rows (two chunks each)
+    and are summed there one after another, beside the shared experts.  Three groups in
+    turn exercise the reduce's reuse of its shared base between groups."""
     d, E, d_ff = SHAPES["ns_h128"]
-    T = 1100
+    T = 2000
     p, x, gout, tw, _ = make_case(d, E, d_ff, 2, 2, False, T, torch.bfloat16, seed=11)
     t = torch.arange(T)
-    first = torch.where(t < 900, torch.zeros_like(t), 1 + t % (E - 1))
-    second = 1 + (t * 7 + 3) % (E - 1)
-    second = torch.where(second == first, 1 + (second % (E - 1)), second)
+    first = torch.where(t < 900, torch.zeros_like(t),
+                        torch.where(t < 1800, torch.ones_like(t), 3 + t % (E - 3)))
+    second = torch.where(t < 900, torch.full_like(t, 2), 3 + (t * 7 + 3) % (E - 3))
+    second = torch.where(second == first, 3 + (second - 2) % (E - 3), second)
     ti = torch.stack([first, second], 1).to(torch.int64)
-    assert (ti[:, 0] != ti[:, 1]).all() and (ti == 0).sum() == 900
+    counts = torch.bincount(ti.flatten(), minlength=E)
+    assert (ti[:, 0] != ti[:, 1]).all()
+    assert (counts[:3] > 768).all() and (counts[3:] <= 768).all()
+    assert T * 2 < E * 691  # the reduce's single looping row for routed groups
     ref_out, ref_g = oracle_fwd_bwd(p, x, gout, tw, ti, "silu")
     out, g = gpu_fwd_bwd(p, x, gout, tw, ti, "silu")
     check("out", out, ref_out, torch.bfloat16)

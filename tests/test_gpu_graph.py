@@ -149,3 +149,76 @@ def test_replay_repacks_weights_updated_in_place():
             torch.cuda.synchronize()
             ref = m(x)
             assert torch.equal(out, ref), f"replay {r} used stale packed weights"
+
+
+def _decode_oracle(m, x):
+    """The oracle's eval forward of block m on x [T, d] (the block's own logits)."""
+    from oracle import moe_ref as R
+    fields = ("W_in", "W_out", "W_sh_in", "W_sh_out")
+    p = R.Params(m.router.W.detach().cpu(), *(getattr(m, f).detach().cpu() for f in fields))
+    return R.block(x.cpu(), p, m.top_k, train=False, fp32=True,
+                   logits=m._logits.float().cpu())
+
+
+def test_decode_graph_reads_shared_packs_and_refresh():
+    """A decode step (T = 64, eval) captured with PackCache.share_with_graphs reads the
+    cached packs instead of packing in the graph.  Replays match the oracle (routing
+    bit-exact, output within the bf16 bar); after an in-place weight update they keep
+    the frozen packs until PackCache.refresh(), after which a replay matches the oracle
+    of the updated weights."""
+    from tests.helpers import assert_close_bf16
+    m, _, _ = _block(64, seed=4)
+    m.eval()
+    x = torch.randn(64, 576, device=DEV).to(torch.bfloat16)
+    mk.PACKS.clear()
+    mk.PACKS.share_with_graphs = True
+    try:
+        with torch.no_grad():
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                for _ in range(2):
+                    m(x)  # the first call packs and files the pack
+            torch.cuda.current_stream().wait_stream(side)
+            torch.cuda.synchronize()
+            h0, m0 = mk.PACKS.hits, mk.PACKS.misses
+            graph = torch.cuda.CUDAGraph()
+            print("[graph] decode capture with shared packs", flush=True)
+            with torch.cuda.graph(graph):
+                out = m(x)
+            assert (mk.PACKS.hits - h0, mk.PACKS.misses - m0) == (1, 0), \
+                "the capture did not read the cached packs"
+            for r in range(3):
+                m(torch.randn_like(x))  # eager work between replays
+                torch.cuda.synchronize()
+                graph.replay()
+                torch.cuda.synchronize()
+                if r == 0:
+                    first = out.clone()
+                assert torch.equal(out, first), f"replay {r}"
+            eager = m(x)
+            assert torch.equal(first, eager)
+            ref = _decode_oracle(m, x)
+            assert torch.equal(m._routing.cpu(), ref.topk_idx), "routing differs"
+            assert_close_bf16("decode replay", first.float().cpu(), ref.out)
+            # an in-place update: the replay keeps the frozen packs ...
+            m.W_in.mul_(0.5)
+            m.W_sh_out.add_(0.02)
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            stale = out.clone()
+            # ... until refresh() repacks into the same buffers
+            assert mk.PACKS.refresh() >= 1
+            graph.replay()
+            torch.cuda.synchronize()
+            fresh = out.clone()
+            eager2 = m(x)
+            assert torch.equal(fresh, eager2), "refreshed replay != eager"
+            assert not torch.equal(stale, fresh)
+            ref2 = _decode_oracle(m, x)
+            assert torch.equal(m._routing.cpu(), ref2.topk_idx), "routing differs"
+            assert_close_bf16("decode replay after refresh", fresh.float().cpu(), ref2.out)
+    finally:
+        mk.PACKS.share_with_graphs = False
+        mk.PACKS.clear()

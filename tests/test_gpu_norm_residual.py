@@ -15,6 +15,9 @@ gradient in one kernel (MoEBlock.forward_residual, nsmoe.h NSMOE_BLOCK_NORM):
     (rms_norm_backward) to the bf16 bar;
   * the unfused path (fp32 blocks, or norm modules it does not take) is exactly
     x + block(norm(x)).
+
+Sizes: T = 8192 train forward + backward, T = 2048 train forward, T = 32768 eval forward
+(the prefill's per-layer call), T = 512 fp16, and ragged / other shapes.
 """
 
 import pytest
@@ -115,6 +118,14 @@ def test_forward_backward_T8192_train():
 
 def test_forward_T2048_train():
     run(2048, True, False)
+
+
+def test_prefill_sublayer_T32768_eval():
+    """The FFN sublayer exactly as the 20-layer prefill runs it in every layer (batch 4 x
+    8192 = 32768 tokens, eval): the norm in the router kernel, the residual in the combine,
+    196,608 routed pairs."""
+    ref = run(32768, False, False)
+    assert int(ref.counts.sum()) == 32768 * 6
 
 
 def test_eval_forward_backward_T512_fp16():

@@ -77,3 +77,49 @@ def test_shared_weights_are_part_of_the_key():
     fill(cache, ws[:2] + sh)
     assert cache.lookup((16, 8), "cpu", *ws)[2] is not None
     assert cache.lookup((16, 8), "cpu", *(ws[:2] + sh))[2] is None
+
+
+def test_cast_temporaries_are_keyed_on_their_parameters():
+    """An autocast-style caller hands the op a fresh cast of its fp32 parameters on every
+    call; under PackCache.sources the entry belongs to the parameters, so the next
+    call's new temporaries hit, and an update of a parameter invalidates it."""
+    cache, params = PackCache(), weights()
+    present = params[:2]
+
+    def call():
+        temps = [t.to(torch.bfloat16) for t in present]
+        with cache.sources({id(c): t for c, t in zip(temps, present)}):
+            p_in, p_out, pending = cache.lookup((16, 8), "cpu", *temps, None, None)
+            if pending is not None:
+                cache.store(pending, p_in, p_out)
+        return pending is None
+
+    assert not call()           # first call packs
+    assert call() and call()    # new temporaries, same parameters: hits
+    assert len(cache) == 1
+    with torch.no_grad():
+        present[0].add_(1.0)
+    assert not call()           # the parameter moved on
+
+
+def test_packed_dtype_is_part_of_the_key():
+    cache, params = PackCache(), weights()
+    for dt in (torch.bfloat16, torch.float16):
+        temps = [t.to(dt) for t in params[:2]]
+        with cache.sources({id(c): t for c, t in zip(temps, params)}):
+            p_in, p_out, pending = cache.lookup((16, 8), "cpu", *temps)
+            assert pending is not None, dt   # a bf16 pack is no fp16 pack
+            cache.store(pending, p_in, p_out)
+    assert len(cache) == 2
+
+
+def test_pinned_entries_outlive_eviction():
+    """Entries a captured graph reads are pinned: LRU eviction passes over them."""
+    cache = PackCache(capacity=1)
+    sets = [weights(i) for i in range(3)]
+    fill(cache, sets[0])
+    next(iter(cache._entries.values())).pinned = True
+    fill(cache, sets[1])
+    fill(cache, sets[2])
+    assert cache.lookup((16, 8), "cpu", *sets[0])[2] is None   # pinned: kept
+    assert cache.lookup((16, 8), "cpu", *sets[1])[2] is not None

@@ -69,3 +69,38 @@ def test_noalloc_dispatch_rejects_sizes_past_its_scratch():
 def test_noalloc_dispatch_of_no_pairs():
     out = run(torch.zeros(0, 2, dtype=torch.int64, device=DEV), 8, noalloc=True)
     assert int(out[4]) == 0 and int(out[3].sum()) == 0 and int(out[2].abs().sum()) == 0
+
+
+def test_noalloc_dispatch_under_graph_capture():
+    """Captured into a HIP graph (after one uncaptured call resolved the scratch address)
+    and replayed three times with new routing written into the captured input between
+    replays, each replay equals nsmoe_dispatch on that routing."""
+    lib = nat.lib()
+    E, T, k = 76, 1024, 6
+    g = torch.Generator(device="cpu").manual_seed(5)
+    draw = lambda: torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)]).to(DEV)
+    idx = draw()
+    run(idx, E, noalloc=True)  # resolves the address outside capture
+    flat = idx.reshape(-1).contiguous()
+    m = flat.numel()
+    out = buffers(m, E)
+    ptrs = [t.data_ptr() for t in out]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    print("[noalloc] capture", flush=True)
+    with torch.cuda.graph(graph, stream=side):
+        rc = lib.nsmoe_dispatch_noalloc(flat.data_ptr(), m, E, *ptrs,
+                                        torch.cuda.current_stream().cuda_stream)
+    nat.check(rc, "dispatch_noalloc (captured)")
+    for rep in range(3):
+        new = draw()
+        flat.copy_(new.reshape(-1))
+        for t in out:
+            t.fill_(-7)
+        graph.replay()
+        torch.cuda.synchronize()
+        want = run(new, E, noalloc=False)
+        for name, a, b in zip(("sorted_ids", "expert_ids", "pad_offsets", "counts",
+                               "n_post_pad", "inv"), out, want):
+            assert torch.equal(a, b), f"{name} differs on replay {rep}"
