@@ -511,47 +511,74 @@ def build_decoder(n_layers=20, seed=0):
 
 
 def config5(steps, warmup):
-    """The 20-layer prefill (batch 4 x 8192, eval, bf16; attention on SDPA, window 512 with
-    every fourth layer global): tokens/s, and the MoE calls' share of the forward from
-    HIP events around each call."""
+    """The 20-layer prefill (batch 4 x 8192, eval, bf16; window 512 with every fourth layer
+    global): tokens/s with the HIP attention (nsmoe_attn_prefill) and the HIP MoE in every
+    layer, the shares of the attention sublayers and of the MoE sublayers from HIP events
+    around each call, and the same prefill with the attention on torch SDPA (the reference's
+    path) for comparison."""
     model, idx = build_decoder()
     model, idx = model.cuda(), idx.cuda()
-    pairs = []
+    pairs = {"attn": [], "moe": []}
+
+    def timed(kind, fn):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        y = fn()
+        b.record()
+        pairs[kind].append((a, b))
+        return y
 
     def hook(blk, h):
         # The FFN half: x + moe(norm_ffn(x)), norm and residual inside the MoE kernels.
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        y = blk.ffn.forward_residual(h, blk.norm_ffn)
-        b.record()
-        pairs.append((a, b))
-        return y
+        return timed("moe", lambda: blk.ffn.forward_residual(h, blk.norm_ffn))
 
+    originals = [blk.attn.forward for blk in model.blocks]
     reps = max(2, min(steps, 3))
-    with torch.no_grad():
-        for _ in range(max(1, min(warmup, 2))):
-            model(idx)
+
+    def run_timed(n):
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        for _ in range(reps):
+        for _ in range(n):
             model(idx)
         torch.cuda.synchronize()
-        ms = (time.perf_counter() - t0) * 1e3 / reps
+        return (time.perf_counter() - t0) * 1e3 / n
+
+    with torch.no_grad():
+        assert model.blocks[1].attn.use_kernel(model.embed(idx[:, :1]))
+        for _ in range(max(1, min(warmup, 2))):
+            model(idx)
+        ms = run_timed(reps)
+        for blk, fwd in zip(model.blocks, originals):
+            blk.attn.forward = (lambda z, fwd=fwd: timed("attn", lambda: fwd(z)))
         model(idx, ffn_hook=hook)
         torch.cuda.synchronize()
-        pairs.clear()
+        for v in pairs.values():
+            v.clear()
         t0 = time.perf_counter()
         model(idx, ffn_hook=hook)
         torch.cuda.synchronize()
         hooked_ms = (time.perf_counter() - t0) * 1e3
-        moe_ms = sum(a.elapsed_time(b) for a, b in pairs)
+        moe_ms = sum(a.elapsed_time(b) for a, b in pairs["moe"])
+        attn_ms = sum(a.elapsed_time(b) for a, b in pairs["attn"])
+        for blk, fwd in zip(model.blocks, originals):
+            blk.attn.forward = fwd
+        # the same prefill with the attention on torch SDPA
+        for blk in model.blocks:
+            blk.attn.kernel = False
+        model(idx)
+        sdpa_ms = run_timed(max(1, reps - 1))
+        for blk in model.blocks:
+            blk.attn.kernel = True
     n = idx.numel()
-    return {"workload": "20-layer decoder prefill, batch 4 x 8192, eval, bf16; SDPA attention "
-                        "(window 512, global_every 4), HIP MoE with its RMSNorm and "
-                        "residual in every layer",
+    return {"workload": "20-layer decoder prefill, batch 4 x 8192, eval, bf16; HIP attention "
+                        "(QK-norm, RoPE, window 512, global_every 4) and HIP MoE with its "
+                        "RMSNorm and residual in every layer",
             "tokens_per_s": round(n / (ms / 1e3), 1), "ms": round(ms, 3),
+            "attn_ms": round(attn_ms, 3), "attn_share": round(attn_ms / hooked_ms, 4),
             "moe_ms": round(moe_ms, 3), "moe_share": round(moe_ms / hooked_ms, 4),
-            "moe_calls": len(pairs), "moe_tokens_per_call": n}
+            "moe_calls": len(pairs["moe"]), "moe_tokens_per_call": n,
+            "sdpa_attention_ms": round(sdpa_ms, 3),
+            "sdpa_attention_tokens_per_s": round(n / (sdpa_ms / 1e3), 1)}
 
 
 def cpu_info():

@@ -47,7 +47,7 @@ int32_t nsmoe_abi_version(void);
  * the library records a HIP event pair on the launch stream around each launch of its
  * main kernels ("pack", "route_fwd", "dispatch", "expert_fwd", "combine",
  * "expert_bwd", "expert_dx", "dw" (or "dw_in" and "dw_out" where they run apart),
- * "combine_dx", "router_dw", "norm_bwd") until
+ * "combine_dx", "router_dw", "route_bwd", "norm_bwd", "attn_k_prep", "attn_fwd") until
  * `capacity` pairs are used.
  * nsmoe_timing_read waits for the recorded events of one kernel and returns their
  * summed duration.  capacity 0 disables timing and frees the events. */
@@ -354,6 +354,44 @@ int nsmoe_block_bwd(const nsmoe_experts_args* args, const nsmoe_block_norm* norm
                     const nsmoe_experts_grads* grads, const void* w_router,
                     void* grad_w_router, void* grad_logits, void* workspace,
                     size_t workspace_bytes, void* stream);
+
+/* ---- prefill attention (the decoder around the block) --------------------------------
+ * Replaces the middle of OptimizedMultiHeadAttention.forward on its SDPA path
+ * (src/model/mha.py:258-287, masks mha.py:49-66): the per-head RMSNorm of Q and K
+ * (qk_norm=True; F.rms_norm, src/model/ln.py:30-36), the rotary embedding
+ * (src/model/rope.py, rotate-half over the whole head, p = 1; the rotation in the dtype
+ * from fp32 tables cast to it) at positions 0 .. seq_len - 1, and causal attention with an
+ * optional sliding window over grouped-query heads (query head h reads key/value head
+ * h / (n_heads / n_kv_heads)), scale 1 / sqrt(64).
+ *   qkv  [batch * seq_len, ld]: each token's n_heads query heads, then n_kv_heads key
+ *        heads, then n_kv_heads value heads, 64 elements each (the projection
+ *        Z [W_q | W_k | W_v]).  The key heads are normalised and rotated IN PLACE.
+ *   out  [batch * seq_len, n_heads * 64]: the attention output, ready for W_O.
+ *   cos, sin [seq_len, 32] fp32: cos / sin(pos * base^(-2 j / 64)) (rope.py's table).
+ *   q_gamma, k_gamma [64]: the two RMSNorm gains, args dtype.
+ * 16-bit types; head_dim 64; n_heads / n_kv_heads in 1..4.  window = keys a query sees,
+ * itself included (mha.py:63); 0 or >= seq_len is full causal attention.
+ */
+typedef struct nsmoe_attn_args {
+  int32_t dtype;       /* NSMOE_BF16 or NSMOE_F16 */
+  int32_t n_heads;     /* Hq */
+  int32_t n_kv_heads;  /* Hkv */
+  int32_t head_dim;    /* 64 */
+  int64_t batch;
+  int64_t seq_len;
+  int32_t ld;          /* qkv row pitch in elements (a multiple of 8) */
+  int32_t window;
+  float eps;           /* the RMSNorms' epsilon */
+  int32_t reserved;
+  void* qkv;
+  const void* q_gamma;
+  const void* k_gamma;
+  const float* cos;
+  const float* sin;
+  void* out;
+} nsmoe_attn_args;
+
+int nsmoe_attn_prefill(const nsmoe_attn_args* args, void* stream);
 
 #ifdef __cplusplus
 }

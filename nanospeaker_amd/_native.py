@@ -15,7 +15,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libnsmoe.so"
 BF16, F16, F32 = 0, 1, 2
 ROUTE_PROBS, ROUTE_NORMALIZE, ROUTE_LOGITS16 = 1, 2, 4
 BLOCK_PACK, BLOCK_SAVE_ACT, BLOCK_NORM = 8, 16, 32
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 # Every symbol include/nsmoe.h declares, with (restype, argtypes).
 _vp, _i32, _i64, _sz = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t
@@ -41,6 +41,18 @@ class ExpertsGrads(ctypes.Structure):
     _fields_ = [(n, _vp) for n in (
         "dx", "dw_in", "dw_out", "dw_sh_in", "dw_sh_out", "dtopk_w",
         "db_in", "db_out", "db_sh_in", "db_sh_out")]
+
+
+class AttnArgs(ctypes.Structure):
+    """Mirror of `nsmoe_attn_args`."""
+
+    _fields_ = [
+        ("dtype", _i32), ("n_heads", _i32), ("n_kv_heads", _i32), ("head_dim", _i32),
+        ("batch", _i64), ("seq_len", _i64), ("ld", _i32), ("window", _i32),
+        ("eps", ctypes.c_float), ("reserved", _i32),
+        ("qkv", _vp), ("q_gamma", _vp), ("k_gamma", _vp), ("cos", _vp), ("sin", _vp),
+        ("out", _vp),
+    ]
 
 
 class BlockNorm(ctypes.Structure):
@@ -90,6 +102,7 @@ SIGNATURES = {
                                        _vp, _i32, ctypes.c_float, _vp, _vp, _vp, _vp, _vp,
                                        ctypes.POINTER(ExpertsGrads), _vp, _vp, _vp, _vp, _sz,
                                        _vp]),
+    "nsmoe_attn_prefill": (ctypes.c_int, [ctypes.POINTER(AttnArgs), _vp]),
 }
 
 # Parts of the block's `saved` buffer (NSMOE_SAVED_* in nsmoe.h).

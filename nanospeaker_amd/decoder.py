@@ -4,11 +4,15 @@ src/model/nanospeaker.py:133-269 -- embedding, 20 pre-norm blocks of attention a
 final norm, tied unembedding; src/model/mha.py:245-287 for the attention, ln.py:30-36
 for RMSNorm, rope.py for the rotary embedding).
 
-Only the MoE block and its FFN half is this build's HIP code: x + moe(norm_ffn(x)) runs
-through MoEBlock.forward_residual, which takes the RMSNorm and the residual add into the
-block's kernels.  The rest is plain PyTorch: the attention's RMSNorm is `F.rms_norm`, the
-attention is `scaled_dot_product_attention` (the reference's SDPA path, `flex=False`),
-the projections are torch matmuls.  The stack runs the prefill of the
+The FFN half of each block, x + moe(norm_ffn(x)), runs through MoEBlock.forward_residual,
+which takes the RMSNorm and the residual add into the block's HIP kernels.  The attention
+of a gradient-free 16-bit forward on the GPU (the prefill) runs through `attn_prefill`,
+the library's HIP kernels (nsmoe_attn_prefill: QK-norm, RoPE, windowed or full causal
+grouped-query flash attention) between two torch GEMMs, the fused Q/K/V projection and
+W_O.  Everywhere else (CPU, fp32 / fp64, a forward that autograd differentiates, or
+`kernel=False`) the attention is plain PyTorch: `F.rms_norm`, the rotation in the dtype
+and `scaled_dot_product_attention` (the reference's SDPA path, `flex=False`); that path is
+also the GPU kernel's reference in the tests.  The stack runs the prefill of the
 benchmark's fifth workload (batch 4 x 8192 tokens, eval, bf16) with the MoE kernels in
 situ, so the block's share of a real forward can be measured.
 
@@ -31,6 +35,7 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
+from . import _native as nat
 from .moe import MoEBlock
 
 
@@ -94,11 +99,48 @@ class Rotary:
             hit = self._tables[key] = (ang.cos().to(dtype), ang.sin().to(dtype))
         return hit
 
+    def tables_f32(self, n: int, device):
+        """The fp32 cos / sin tables [n, d_head / 2] (what `tables` casts)."""
+        return self.tables(n, device, torch.float32)
+
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
         cos, sin = self.tables(x.shape[-2], x.device, x.dtype)
         half = self.d_head // 2
         a, b = x[..., :half], x[..., half:]
         return torch.cat((a * cos - b * sin, b * cos + a * sin), dim=-1)
+
+
+_ATTN_DT = {torch.bfloat16: nat.BF16, torch.float16: nat.F16}
+
+
+def attn_prefill(qkv: torch.Tensor, B: int, T: int, n_heads: int, n_kv_heads: int,
+                 q_gamma: torch.Tensor, k_gamma: torch.Tensor, cos: torch.Tensor,
+                 sin: torch.Tensor, window: "int | None", eps: float) -> torch.Tensor:
+    """
+    The attention of a prefill (positions 0 .. T - 1) on the library's HIP kernels
+    (nsmoe_attn_prefill): qkv [B * T, (n_heads + 2 n_kv_heads) * 64] is the fused
+    projection Z [W_q | W_k | W_v]; its key heads are normalised and rotated in place.
+    Returns [B * T, n_heads * 64], the input of W_O.  q_gamma / k_gamma are the two
+    RMSNorm gains, cos / sin the fp32 rotary tables [T, 32]; window None is full causal
+    attention.  Forward only (no autograd).
+    """
+    if qkv.dtype not in _ATTN_DT:
+        raise ValueError(f"attn_prefill: 16-bit types only, got {qkv.dtype}")
+    dt = qkv.dtype
+    qkv = qkv.contiguous()
+    out = torch.empty((B * T, n_heads * 64), dtype=dt, device=qkv.device)
+    qg = q_gamma.detach().to(dt).contiguous()
+    kg = k_gamma.detach().to(dt).contiguous()
+    cos, sin = cos.float().contiguous(), sin.float().contiguous()
+    a = nat.AttnArgs(dtype=_ATTN_DT[dt], n_heads=n_heads, n_kv_heads=n_kv_heads,
+                     head_dim=64, batch=B, seq_len=T, ld=qkv.shape[1],
+                     window=0 if window is None else int(window), eps=float(eps),
+                     reserved=0, qkv=qkv.data_ptr(), q_gamma=qg.data_ptr(),
+                     k_gamma=kg.data_ptr(), cos=cos.data_ptr(), sin=sin.data_ptr(),
+                     out=out.data_ptr())
+    nat.check(nat.lib().nsmoe_attn_prefill(a, torch.cuda.current_stream().cuda_stream),
+              "nsmoe_attn_prefill")
+    return out
 
 
 def band_attention(q, k, v, window: int) -> torch.Tensor:
@@ -151,10 +193,12 @@ class Attention(nn.Module):
     """Grouped-query self-attention with QK-norm, rotary embeddings and an optional window
     (reference: OptimizedMultiHeadAttention, mha.py:245-287, on its SDPA path)."""
 
-    def __init__(self, cfg: DecoderConfig, rotary: Rotary, window: "int | None"):
+    def __init__(self, cfg: DecoderConfig, rotary: Rotary, window: "int | None",
+                 kernel: bool = True):
         super().__init__()
         d, h, hk, dh = cfg.d_model, cfg.n_heads, cfg.n_kv_heads, cfg.d_head
         self.h, self.hk, self.dh, self.window, self.rotary = h, hk, dh, window, rotary
+        self.kernel = kernel
         self.W_q = nn.Parameter(torch.randn(d, h * dh) * cfg.std)
         self.W_k = nn.Parameter(torch.randn(d, hk * dh) * cfg.std)
         self.W_v = nn.Parameter(torch.randn(d, hk * dh) * cfg.std)
@@ -163,8 +207,23 @@ class Attention(nn.Module):
         self.q_norm = RMSNorm(dh, cfg.norm_eps)
         self.k_norm = RMSNorm(dh, cfg.norm_eps)
 
+    def use_kernel(self, z: torch.Tensor) -> bool:
+        """The HIP prefill kernels take a gradient-free 16-bit forward on the GPU with
+        64-wide heads and 1-4 query heads per key/value head."""
+        return (self.kernel and z.is_cuda and z.dtype in _ATTN_DT and self.dh == 64
+                and self.h % self.hk == 0 and self.h // self.hk <= 4
+                and not (torch.is_grad_enabled() and any(
+                    t.requires_grad for t in (z, self.W_q, self.W_k, self.W_v, self.W_O))))
+
     def forward(self, z: torch.Tensor) -> torch.Tensor:
         B, T, _ = z.shape
+        if self.use_kernel(z):
+            w = torch.cat((self.W_q, self.W_k, self.W_v), dim=1).to(z.dtype)
+            qkv = z.reshape(B * T, -1) @ w
+            cos, sin = self.rotary.tables_f32(T, z.device)
+            o = attn_prefill(qkv, B, T, self.h, self.hk, self.q_norm.gamma, self.k_norm.gamma,
+                             cos, sin, self.window, self.q_norm.eps)
+            return o.view(B, T, self.h * self.dh) @ self.W_O
         q = (z @ self.W_q).view(B, T, self.h, self.dh).transpose(1, 2)
         k = (z @ self.W_k).view(B, T, self.hk, self.dh).transpose(1, 2)
         v = (z @ self.W_v).view(B, T, self.hk, self.dh).transpose(1, 2)
@@ -186,7 +245,7 @@ class DecoderBlock(nn.Module):
     def __init__(self, cfg: DecoderConfig, rotary: Rotary, layer: int, kernel: bool = True):
         super().__init__()
         self.norm_attn = RMSNorm(cfg.d_model, cfg.norm_eps)
-        self.attn = Attention(cfg, rotary, cfg.layer_window(layer))
+        self.attn = Attention(cfg, rotary, cfg.layer_window(layer), kernel)
         self.norm_ffn = RMSNorm(cfg.d_model, cfg.norm_eps)
         self.ffn = MoEBlock(cfg.d_model, cfg.n_experts, 3 * cfg.d_expert // 2,
                             top_k=cfg.top_k, n_shared=cfg.n_shared, capacity_factor=None,

@@ -42,8 +42,46 @@ def test_struct_layouts_match_the_header():
     assert fields == [f for f, _ in nat.ExpertsArgs._fields_]
 
 
+def test_attn_args_layout_matches_the_header():
+    # nsmoe_attn_args: 4 x i32, 2 x i64, 2 x i32, f32, i32, then 6 pointers
+    assert ctypes.sizeof(nat.AttnArgs) == 4 * 4 + 8 * 2 + 4 * 4 + 8 * 6
+    assert nat.AttnArgs.qkv.offset == 48
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    body = text[text.index("typedef struct nsmoe_attn_args"):text.index("} nsmoe_attn_args")]
+    assert re.findall(r"\b(\w+);", body) == [f for f, _ in nat.AttnArgs._fields_]
+
+
+def _attn(**kw):
+    base = dict(dtype=0, n_heads=9, n_kv_heads=3, head_dim=64, batch=1, seq_len=16,
+                ld=960, window=0, eps=1e-6, reserved=0, qkv=16, q_gamma=16, k_gamma=16,
+                cos=16, sin=16, out=16)
+    base.update(kw)
+    return nat.AttnArgs(**base)
+
+
+@pytest.mark.parametrize("kw,needle", [
+    (dict(dtype=2), "16-bit"),
+    (dict(head_dim=128), "head_dim"),
+    (dict(n_heads=9, n_kv_heads=2), "n_heads"),
+    (dict(n_heads=10, n_kv_heads=2), "n_heads"),
+    (dict(ld=900), "pitch"),
+    (dict(window=-1), "window"),
+    (dict(qkv=None), "NULL"),
+    (dict(qkv=8), "misaligned"),
+])
+def test_attn_prefill_rejects_bad_arguments(kw, needle):
+    lib = nat.lib()
+    assert lib.nsmoe_attn_prefill(_attn(**kw), None) == 1
+    assert needle in lib.nsmoe_last_error().decode()
+
+
+def test_attn_prefill_of_nothing_is_a_no_op():
+    assert nat.lib().nsmoe_attn_prefill(_attn(batch=0, qkv=None), None) == 0
+    assert nat.lib().nsmoe_attn_prefill(_attn(seq_len=0, qkv=None), None) == 0
+
+
 def test_abi_version_and_alignment():
-    assert nat.lib().nsmoe_abi_version() == nat.ABI_VERSION == 6
+    assert nat.lib().nsmoe_abi_version() == nat.ABI_VERSION == 7
     assert nat.lib().nsmoe_align_m() == mk.ALIGN_M
 
 
