@@ -581,6 +581,42 @@ def config5(steps, warmup):
             "sdpa_attention_tokens_per_s": round(n / (sdpa_ms / 1e3), 1)}
 
 
+def config5_head(steps, warmup):
+    """The tied head with the next-token cross-entropy at the prefill batch (4 x 8192
+    tokens: 32764 rows, vocabulary 32768, d 576), loss and both gradients (the training
+    form, nanospeaker.py:241-250): milliseconds per call, and the HIP cross-entropy
+    kernel's own time and HBM rate (each logit read once and its gradient written once)."""
+    from nanospeaker_amd import _native as nat
+    from nanospeaker_amd.head import linear_cross_entropy
+
+    g = torch.Generator().manual_seed(0)
+    n, V, d = 4 * 8191, 32768, 576
+    h = torch.randn(n, d, generator=g).to(torch.bfloat16).cuda().requires_grad_(True)
+    W = (torch.randn(V, d, generator=g) * 0.02).to(torch.bfloat16).cuda().requires_grad_(True)
+    y = torch.randint(0, V, (n,), generator=g).cuda()
+
+    def call():
+        h.grad = W.grad = None
+        linear_cross_entropy(h, W, y).backward()
+
+    reps = max(3, min(steps, 10))
+    ms = eager_time(call, reps, max(1, min(warmup, 3)))
+    nat.timing_enable(16)
+    call()
+    torch.cuda.synchronize()
+    ce_ms, nce = nat.timing_read("ce_rows")
+    nat.timing_enable(0)
+    ce_us = ce_ms * 1e3 / max(nce, 1)
+    gbs = n * V * 4 / (ce_us * 1e-6) / 1e9
+    gemm_tflop = 3 * 2 * n * V * d / 1e12
+    return {"workload": "tied head + next-token cross-entropy, loss and dh, dW, 4 x 8191 "
+                        "rows, vocab 32768, d 576, bf16 (logits in one chunk)",
+            "ms": round(ms, 3), "tokens_per_s": round(n / (ms / 1e3), 1),
+            "ce_rows_us": round(ce_us, 2), "ce_rows_hbm_gbs": round(gbs, 1),
+            "ce_rows_hbm_frac": round(gbs / PEAK_HBM_GBS, 4),
+            "gemm_tflop_per_call": round(gemm_tflop, 3)}
+
+
 def cpu_info():
     model, flags = "unknown", set()
     try:
@@ -771,7 +807,8 @@ def main():
         torch.cuda.empty_cache()
         confs = {}
         for name, fn in (("c1_T2048_fwd", config1), ("c3_T64_eval", config3),
-                         ("c4_T16384_skew_fwd_bwd", config4), ("c5_prefill", config5)):
+                         ("c4_T16384_skew_fwd_bwd", config4), ("c5_prefill", config5),
+                         ("c5_head_cross_entropy", config5_head)):
             print(f"[bench] {name}", file=sys.stderr, flush=True)
             confs[name] = fn(a.steps, a.warmup)
             torch.cuda.empty_cache()

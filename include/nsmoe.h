@@ -47,7 +47,7 @@ int32_t nsmoe_abi_version(void);
  * the library records a HIP event pair on the launch stream around each launch of its
  * main kernels ("pack", "route_fwd", "dispatch", "expert_fwd", "combine",
  * "expert_bwd", "expert_dx", "dw" (or "dw_in" and "dw_out" where they run apart),
- * "combine_dx", "router_dw", "route_bwd", "norm_bwd", "attn_k_prep", "attn_fwd") until
+ * "combine_dx", "router_dw", "route_bwd", "norm_bwd", "attn_k_prep", "attn_fwd", "ce_rows") until
  * `capacity` pairs are used.
  * nsmoe_timing_read waits for the recorded events of one kernel and returns their
  * summed duration.  capacity 0 disables timing and frees the events. */
@@ -392,6 +392,23 @@ typedef struct nsmoe_attn_args {
 } nsmoe_attn_args;
 
 int nsmoe_attn_prefill(const nsmoe_attn_args* args, void* stream);
+
+/* ---- cross-entropy over the tied head's logits ----------------------------------------
+ * The loss part of NanoSpeaker.forward with targets (src/model/nanospeaker.py:236-250:
+ * F.cross_entropy((h @ embed.weight.T).float(), y), mean over the targets that are not
+ * ignore_index; the reference fuses it with the head GEMM through
+ * LigerFusedLinearCrossEntropyLoss).  The GEMMs around it stay library GEMMs.
+ *   logits [n_rows, ld] (vocab columns used), 16-bit; target [n_rows] int64.
+ *   loss [n_rows] fp32: logsumexp(row) - row[target] in fp32 (0 for ignore_index, NaN for a
+ *        target outside [0, vocab)).
+ *   grad NULL, or [n_rows, ld] (may be `logits` itself): (softmax(row) - onehot(target)) / n
+ *        rounded to the dtype, n = *n_valid (int64, device memory: the number of targets
+ *        that are not ignore_index); zero rows for ignored targets.
+ * vocab a multiple of 8, at most 65536; ld a multiple of 8; 16-byte aligned rows.
+ */
+int nsmoe_cross_entropy_rows(int32_t dtype, const void* logits, int64_t ld, int64_t n_rows,
+                             int32_t vocab, const int64_t* target, int64_t ignore_index,
+                             const int64_t* n_valid, float* loss, void* grad, void* stream);
 
 #ifdef __cplusplus
 }

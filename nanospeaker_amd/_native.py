@@ -103,6 +103,8 @@ SIGNATURES = {
                                        ctypes.POINTER(ExpertsGrads), _vp, _vp, _vp, _vp, _sz,
                                        _vp]),
     "nsmoe_attn_prefill": (ctypes.c_int, [ctypes.POINTER(AttnArgs), _vp]),
+    "nsmoe_cross_entropy_rows": (ctypes.c_int, [_i32, _vp, _i64, _i64, _i32, _vp, _i64, _vp,
+                                                _vp, _vp, _vp]),
 }
 
 # Parts of the block's `saved` buffer (NSMOE_SAVED_* in nsmoe.h).

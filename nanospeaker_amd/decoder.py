@@ -36,6 +36,7 @@ import torch.nn.functional as F
 from torch import nn
 
 from . import _native as nat
+from .head import linear_cross_entropy
 from .moe import MoEBlock
 
 
@@ -288,6 +289,16 @@ class Decoder(nn.Module):
             aux = aux + a
         return self.norm_out(x), aux
 
-    def forward(self, idx: torch.Tensor, ffn_hook=None) -> torch.Tensor:
-        x, _ = self.trunk(idx, ffn_hook)
-        return x @ self.embed.weight.t()
+    def forward(self, idx: torch.Tensor, targets: "torch.Tensor | None" = None,
+                ffn_hook=None):
+        """Logits [B, T, vocab] (the tied unembedding), or with `targets` [B, T] the
+        next-token loss and the summed balance loss (nanospeaker.py:236-250): position t
+        predicts token t + 1, through head.linear_cross_entropy (the HIP cross-entropy
+        between library GEMMs on the GPU; F.cross_entropy of the materialised fp32 logits
+        elsewhere), never materialising more logits than one chunk."""
+        x, aux = self.trunk(idx, ffn_hook)
+        if targets is None:
+            return x @ self.embed.weight.t()
+        h = x[:, :-1].reshape(-1, self.cfg.d_model)
+        y = targets[:, 1:].reshape(-1)
+        return linear_cross_entropy(h, self.embed.weight, y), aux

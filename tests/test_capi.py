@@ -80,6 +80,21 @@ def test_attn_prefill_of_nothing_is_a_no_op():
     assert nat.lib().nsmoe_attn_prefill(_attn(seq_len=0, qkv=None), None) == 0
 
 
+@pytest.mark.parametrize("args,needle", [
+    ((2, 16, 64, 4, 64, 16, -100, 16, 16, None), "16-bit"),
+    ((0, 16, 64, 4, 60, 16, -100, 16, 16, None), "multiple of 8"),
+    ((0, 16, 64, 4, 65544, 16, -100, 16, 16, None), "at most"),
+    ((0, 16, 32, 4, 64, 16, -100, 16, 16, None), "pitch"),
+    ((0, 16, 64, 4, 64, None, -100, 16, 16, None), "NULL"),
+    ((0, 16, 64, 4, 64, 16, -100, None, 16, 16), "NULL"),
+    ((0, 8, 64, 4, 64, 16, -100, 16, 16, None), "aligned"),
+])
+def test_cross_entropy_rows_rejects_bad_arguments(args, needle):
+    lib = nat.lib()
+    assert lib.nsmoe_cross_entropy_rows(*args, None) == 1
+    assert needle in lib.nsmoe_last_error().decode()
+
+
 def test_abi_version_and_alignment():
     assert nat.lib().nsmoe_abi_version() == nat.ABI_VERSION == 7
     assert nat.lib().nsmoe_align_m() == mk.ALIGN_M

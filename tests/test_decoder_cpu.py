@@ -76,3 +76,20 @@ def test_small_decoder_runs_on_the_eager_block_path():
         logits2 = m(idx2)
     torch.testing.assert_close(logits2[:, :15], logits[:, :15], rtol=0, atol=0)
     assert not torch.equal(logits2[:, 15:], logits[:, 15:])
+
+
+def test_decoder_loss_is_the_reference_next_token_cross_entropy():
+    """forward(idx, targets) (nanospeaker.py:241-250): position t predicts token t + 1,
+    mean cross-entropy of the tied head's logits; on the CPU head.linear_cross_entropy is
+    F.cross_entropy of the materialised fp32 logits, exactly."""
+    torch.manual_seed(0)
+    cfg = DecoderConfig(n_layers=1, vocab_size=64, window=None, global_every=None)
+    model = Decoder(cfg, kernel=False).eval()
+    idx = torch.randint(0, 64, (2, 10))
+    loss, aux = model(idx, targets=idx)
+    with torch.no_grad():
+        x, _ = model.trunk(idx)
+        ref = F.cross_entropy((x[:, :-1].reshape(-1, 576) @ model.embed.weight.t()).float(),
+                              idx[:, 1:].reshape(-1))
+    torch.testing.assert_close(loss, ref, rtol=0, atol=0)
+    assert aux.shape == ()
