@@ -50,6 +50,10 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-configs", action="store_true",
                     help="time only the headline workload (T=8192 fwd+bwd)")
+    ap.add_argument("--only", metavar="NAMES",
+                    help="run only these comma-separated configurations (c1_T2048_fwd, "
+                         "c3_T64_eval, c4_T16384_skew_fwd_bwd, c5_prefill, "
+                         "c5_head_cross_entropy) and print their JSON, no headline line")
     ap.add_argument("--single-stream", action="store_true",
                     help="keep every kernel on one stream (the library's default: the "
                          "side_stream option off), so that profiled kernels never overlap")
@@ -510,6 +514,17 @@ def build_decoder(n_layers=20, seed=0):
     return model, idx
 
 
+def attention_flops(B: int, T: int, H: int, window, dh: int = 64) -> float:
+    """Useful FLOPs of one attention layer over a prefill: per (head, query), the keys it
+    sees (min(q + 1, window) under a window, q + 1 without) times 2 dh for Q K^T and 2 dh
+    for P V; masked scores count nothing."""
+    if window is None or window >= T:
+        keys = T * (T + 1) // 2
+    else:
+        keys = window * (window + 1) // 2 + (T - window) * window
+    return float(B * H * keys * 4 * dh)
+
+
 def config5(steps, warmup):
     """The 20-layer prefill (batch 4 x 8192, eval, bf16; window 512 with every fourth layer
     global): tokens/s with the HIP attention (nsmoe_attn_prefill) and the HIP MoE in every
@@ -562,6 +577,16 @@ def config5(steps, warmup):
         attn_ms = sum(a.elapsed_time(b) for a, b in pairs["attn"])
         for blk, fwd in zip(model.blocks, originals):
             blk.attn.forward = fwd
+        # the attention kernels alone, from the library's event pairs (one prefill)
+        from nanospeaker_amd import _native as nat
+        nat.timing_enable(4096)
+        model(idx)
+        torch.cuda.synchronize()
+        fwd_ms, n_fwd = nat.timing_read("attn_fwd")
+        prep_ms, _ = nat.timing_read("attn_k_prep")
+        nat.timing_enable(0)
+        B, T = idx.shape
+        flops = sum(attention_flops(B, T, blk.attn.h, blk.attn.window) for blk in model.blocks)
         # the same prefill with the attention on torch SDPA
         for blk in model.blocks:
             blk.attn.kernel = False
@@ -577,6 +602,11 @@ def config5(steps, warmup):
             "attn_ms": round(attn_ms, 3), "attn_share": round(attn_ms / hooked_ms, 4),
             "moe_ms": round(moe_ms, 3), "moe_share": round(moe_ms / hooked_ms, 4),
             "moe_calls": len(pairs["moe"]), "moe_tokens_per_call": n,
+            "attn_fwd_kernel_ms": round(fwd_ms, 3), "attn_k_prep_ms": round(prep_ms, 3),
+            "attn_fwd_launches": n_fwd,
+            "attn_fwd_tflops": round(flops / (fwd_ms * 1e-3) / 1e12, 1),
+            "attn_fwd_mfma_frac": round(flops / (fwd_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "attn_useful_tflop_per_prefill": round(flops / 1e12, 3),
             "sdpa_attention_ms": round(sdpa_ms, 3),
             "sdpa_attention_tokens_per_s": round(n / (sdpa_ms / 1e3), 1)}
 
@@ -738,6 +768,16 @@ def main():
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU visible"}))
         sys.exit(1)
+    if a.only:
+        fns = {"c1_T2048_fwd": config1, "c3_T64_eval": config3,
+               "c4_T16384_skew_fwd_bwd": config4, "c5_prefill": config5,
+               "c5_head_cross_entropy": config5_head}
+        out = {}
+        for name in a.only.split(","):
+            print(f"[bench] {name}", file=sys.stderr, flush=True)
+            out[name] = fns[name](a.steps, a.warmup)
+        print(json.dumps({"configs": out}), flush=True)
+        return
     T = a.tokens
     if a.calibrate_copy:
         calibrate_copy()

@@ -50,6 +50,7 @@ static const OptionSpec kOptions[OPT_COUNT] = {
     {"fwd_dist", 2, 6, nullptr},      {"bwd_rows", 0, 0, kBwdRows},
     {"bwd_dist", 2, 4, nullptr},      {"dx_rows", 0, 0, kDxRows},
     {"dx_dist", 2, 4, nullptr},       {"xcd_run", 1, 1024, nullptr},
+    {"dw_stages", 2, 4, nullptr},
 };
 static std::atomic<int64_t> g_options[OPT_COUNT];
 

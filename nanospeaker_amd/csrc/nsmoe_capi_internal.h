@@ -57,6 +57,7 @@ enum OptionId : int {
   OPT_DX_ROWS,
   OPT_DX_DIST,
   OPT_XCD_RUN,
+  OPT_DW_STAGES,
   OPT_COUNT
 };
 int64_t option(OptionId id);

@@ -41,7 +41,7 @@
 
 namespace nsmoe {
 
-constexpr int RT_MMA_SPLIT = 2;             // GEMM waves per 16-token tile (column halves)
+constexpr int RT_MMA_SPLIT = 5;             // GEMM waves per 16-token tile (one 16-expert block each at E <= 80)
 constexpr int RT_MMA_WAVES = RT_TOK / 16 * RT_MMA_SPLIT;  // waves that run the GEMM
 constexpr int RT_WAVES = 16;                // waves per workgroup (loads, exact pass)
 constexpr int RT_THREADS = RT_WAVES * 64;
