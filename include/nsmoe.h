@@ -47,7 +47,7 @@ int32_t nsmoe_abi_version(void);
  * the library records a HIP event pair on the launch stream around each launch of its
  * main kernels ("pack", "route_fwd", "dispatch", "expert_fwd", "combine",
  * "expert_bwd", "expert_dx", "dw" (or "dw_in" and "dw_out" where they run apart),
- * "combine_dx", "router_dw", "route_bwd", "norm_bwd", "attn_k_prep", "attn_fwd", "ce_rows") until
+ * "combine_dx", "router_dw", "route_bwd", "norm_bwd", "attn_k_prep", "attn_fwd", "ce_rows", "norm_fwd") until
  * `capacity` pairs are used.
  * nsmoe_timing_read waits for the recorded events of one kernel and returns their
  * summed duration.  capacity 0 disables timing and frees the events. */
@@ -355,6 +355,15 @@ int nsmoe_block_bwd(const nsmoe_experts_args* args, const nsmoe_block_norm* norm
                     const nsmoe_experts_grads* grads, const void* w_router,
                     void* grad_w_router, void* grad_logits, void* workspace,
                     size_t workspace_bytes, void* stream);
+
+/* ---- RMSNorm forward (the decoder around the block) -------------------------------------
+ * RMSNorm.forward (src/model/ln.py:30-36, F.rms_norm) for the norms the block's kernels do
+ * not take: the attention's pre-norm (nanospeaker.py:168) and the final norm
+ * (nanospeaker.py:231).  y [n_rows, d] = (x rstd) weight rounded once to the dtype, fp32
+ * rstd = 1 / sqrt(mean(x^2) + eps), written to rstd [n_rows] when it is not NULL.
+ * 16-bit types; d a multiple of 8, at most 1024; 16-byte aligned x, weight, y. */
+int nsmoe_rms_norm(int32_t dtype, const void* x, const void* weight, float eps,
+                   int64_t n_rows, int32_t d, void* y, float* rstd, void* stream);
 
 /* ---- prefill attention (the decoder around the block) --------------------------------
  * Replaces the middle of OptimizedMultiHeadAttention.forward on its SDPA path

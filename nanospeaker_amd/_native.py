@@ -102,6 +102,8 @@ SIGNATURES = {
                                        _vp, _i32, ctypes.c_float, _vp, _vp, _vp, _vp, _vp,
                                        ctypes.POINTER(ExpertsGrads), _vp, _vp, _vp, _vp, _sz,
                                        _vp]),
+    "nsmoe_rms_norm": (ctypes.c_int, [_i32, _vp, _vp, ctypes.c_float, _i64, _i32, _vp, _vp,
+                                      _vp]),
     "nsmoe_attn_prefill": (ctypes.c_int, [ctypes.POINTER(AttnArgs), _vp]),
     "nsmoe_cross_entropy_rows": (ctypes.c_int, [_i32, _vp, _i64, _i64, _i32, _vp, _i64, _vp,
                                                 _vp, _vp, _vp]),

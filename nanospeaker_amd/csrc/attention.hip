@@ -20,8 +20,8 @@
 //                       (head, query) columns.  Each wave loads its queries straight into
 //                       MFMA B fragments, normalising and rotating them in registers.  Key
 //                       and value tiles of 64 rows are copied global -> LDS by LDS-DMA
-//                       (two stages, one barrier per tile), with a chunk swizzle that keeps
-//                       the fragment reads free of bank conflicts.
+//                       (three stages: two tiles in flight, one barrier per tile), with a
+//                       chunk swizzle that keeps the fragment reads free of bank conflicts.
 //
 // The kernel computes S^T = K Q^T, so lane l of a wave ends with 4 consecutive keys of one
 // query column (the MFMA accumulator layout).  Everything the online softmax needs per
@@ -47,6 +47,7 @@ constexpr int AT_BQ = 64;    // queries per workgroup
 constexpr int AT_BK = 64;    // keys per tile
 constexpr int AT_NT = 256;   // threads per workgroup
 constexpr int AT_TILE = AT_BK * AT_DH * 2;  // bytes of one K or V tile (16-bit)
+constexpr int AT_STAGES = 3;                // K / V ring stages: two tiles in flight
 
 struct AttnParams {
   uint16_t* qkv;           // [B * T, ld]
@@ -136,7 +137,7 @@ __global__ void __launch_bounds__(AT_NT, 2) attn_fwd_kernel(AttnParams p) {
   using M = Mma<DT>;
   using Frag = typename M::Frag;
   constexpr int NB = G;  // column blocks of 16 (head, query) columns per wave
-  __shared__ __attribute__((aligned(1024))) char s_kv[2][2][AT_TILE];  // [stage][K, V]
+  __shared__ __attribute__((aligned(1024))) char s_kv[AT_STAGES][2][AT_TILE];  // [stage][K, V]
 
   const int lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -219,12 +220,18 @@ __global__ void __launch_bounds__(AT_NT, 2) attn_fwd_kernel(AttnParams p) {
     for (int db = 0; db < 4; ++db) o[db][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
+  // Tiles t + 1 and t + 2 are in flight while tile t is computed: tile t + 2's copies go
+  // into the stage tile t - 1 used, after the barrier that every wave reaches only once
+  // done with tile t - 1.
   issue(t_first, 0);
+  if (t_first < t_last) issue(t_first + 1, 1);
   for (int t = t_first; t <= t_last; ++t) {
-    const int st = (t - t_first) & 1;
-    wait_vmcnt<0>();  // this wave's copies of tile t
+    const int st = (t - t_first) % AT_STAGES;
+    // this wave's copies of tile t (tile t + 1's four may stay in flight)
+    if (t < t_last) wait_vmcnt<4>();
+    else wait_vmcnt<0>();
     barrier_dma();    // every wave's copies of tile t; every wave done with tile t - 1
-    if (t < t_last) issue(t + 1, st ^ 1);
+    if (t + 2 <= t_last) issue(t + 2, (st + 2) % AT_STAGES);
     const char* Kt = s_kv[st][0];
     const char* Vt = s_kv[st][1];
     const int key0 = t * AT_BK;
@@ -249,6 +256,9 @@ __global__ void __launch_bounds__(AT_NT, 2) attn_fwd_kernel(AttnParams p) {
 
     // Mask (only tiles that cross the diagonal or the window's far edge) and online softmax.
     const bool masked = key0 + AT_BK - 1 > q0 || (banded && key0 < qmax - p.window + 1);
+    // The running maximum m is kept on the raw scores; p = 2^(s c - m c) with
+    // c = log2(e) / 8 is one FMA and one exp2 per score.
+    const float c = p.scale_log2;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
       float mx = -INFINITY;
@@ -256,7 +266,7 @@ __global__ void __launch_bounds__(AT_NT, 2) attn_fwd_kernel(AttnParams p) {
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          float v = s[kb][nb][e] * p.scale_log2;
+          float v = s[kb][nb][e];
           if (masked) {
             const int key = key0 + 16 * kb + 4 * g + e, q = qpos[nb];
             if (key > q || (banded && q - key >= p.window)) v = -INFINITY;
@@ -267,8 +277,8 @@ __global__ void __launch_bounds__(AT_NT, 2) attn_fwd_kernel(AttnParams p) {
       mx = fmaxf(mx, __shfl_xor(mx, 16));
       mx = fmaxf(mx, __shfl_xor(mx, 32));
       const float mnew = fmaxf(m[nb], mx);
-      const float msub = mnew == -INFINITY ? 0.0f : mnew;  // no key seen yet: p = 0
-      const float alpha = __builtin_amdgcn_exp2f(m[nb] - msub);
+      const float msub = mnew == -INFINITY ? 0.0f : mnew * c;  // no key seen yet: p = 0
+      const float alpha = __builtin_amdgcn_exp2f(fmaf(m[nb], c, -msub));
       m[nb] = mnew;
       float ls = lsum[nb] * alpha;
 #pragma unroll
@@ -277,7 +287,7 @@ __global__ void __launch_bounds__(AT_NT, 2) attn_fwd_kernel(AttnParams p) {
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float pe = __builtin_amdgcn_exp2f(s[kb][nb][e] - msub);
+          const float pe = __builtin_amdgcn_exp2f(fmaf(s[kb][nb][e], c, -msub));
           s[kb][nb][e] = pe;
           ls += pe;
         }

@@ -13,6 +13,7 @@
 //                       plus the residual's gradient: dx = g + dx_norm (rounded again), and
 //                       this workgroup's fp32 column sums of dxn xh for the gain's gradient;
 //   norm_dw_reduce      those partial sums added in workgroup order -> dw (the dtype).
+#include "../../include/nsmoe.h"
 #include "gemm_core.h"
 #include "nsmoe_capi_internal.h"
 #include "norm.h"
@@ -141,4 +142,78 @@ int norm_bwd_launch(int dtype, const NormBwdArgs& a, hipStream_t s) {
   return check_launch("norm_bwd_kernel");
 }
 
+// ---- the forward, on its own ------------------------------------------------------------
+//
+// y = RMSNorm(x) for the norms the block's kernels do not take (the attention's pre-norm and
+// the final norm of the decoder around the block): F.rms_norm's arithmetic, fp32
+// rstd = 1 / sqrt(mean(x^2) + eps) and y = (x rstd) w rounded once, as the router kernel's
+// fused norm computes it.  One wave per row (16-byte chunks, two per lane at d <= 1024),
+// the row's sum of squares by a wave butterfly; 4 rows per workgroup, so a row is one read
+// and one write of HBM.
+template <int DT>
+__global__ void __launch_bounds__(NB_THREADS) norm_fwd_kernel(const void* __restrict__ x,
+                                                              const void* __restrict__ w,
+                                                              void* __restrict__ y,
+                                                              float* __restrict__ rstd_out,
+                                                              int64_t T, int d, float eps) {
+  using ET = typename Elem<DT>::T;
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * (NB_THREADS / 64) + (threadIdx.x >> 6);
+  if (t >= T) return;  // uniform per wave; no workgroup barrier below
+  const int nch = d / 8;
+  u32x4 xv[NB_MAXU];
+  float ss = 0.0f;
+#pragma unroll
+  for (int u = 0; u < NB_MAXU; ++u) {
+    const int c = lane + 64 * u;
+    xv[u] = c < nch ? *(const u32x4*)((const ET*)x + t * d + 8 * c) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float v = unpack2<DT>(xv[u][e / 2], e & 1);
+      ss += v * v;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  const float rstd = 1.0f / sqrtf(ss / (float)d + eps);
+  if (rstd_out && lane == 0) rstd_out[t] = rstd;
+#pragma unroll
+  for (int u = 0; u < NB_MAXU; ++u) {
+    const int c = lane + 64 * u;
+    if (c >= nch) continue;
+    const u32x4 wv = *(const u32x4*)((const ET*)w + 8 * c);
+    u32x4 o;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      o[q] = pack2<DT>(unpack2<DT>(xv[u][q], 0) * rstd * unpack2<DT>(wv[q], 0),
+                       unpack2<DT>(xv[u][q], 1) * rstd * unpack2<DT>(wv[q], 1));
+    *(u32x4*)((ET*)y + t * d + 8 * c) = o;
+  }
+}
+
 }  // namespace nsmoe
+
+using namespace nsmoe;
+
+extern "C" int nsmoe_rms_norm(int32_t dtype, const void* x, const void* weight, float eps,
+                              int64_t n_rows, int32_t d, void* y, float* rstd, void* stream) {
+  NSMOE_REQUIRE(dtype == DT_BF16 || dtype == DT_F16, "rms_norm: 16-bit types only");
+  NSMOE_REQUIRE(d >= 8 && d % 8 == 0 && d <= NORM_MAX_D,
+                "rms_norm: d %% 8 == 0 and d <= %d (d %d)", NORM_MAX_D, d);
+  NSMOE_REQUIRE(n_rows >= 0, "rms_norm: n_rows %lld < 0", (long long)n_rows);
+  if (n_rows == 0) return NSMOE_OK;
+  NSMOE_REQUIRE(x && weight && y, "rms_norm: NULL pointer");
+  NSMOE_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)weight & 15) == 0 &&
+                    ((uintptr_t)y & 15) == 0,
+                "rms_norm: x, weight and y must be 16-byte aligned");
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t grid = (n_rows + NB_THREADS / 64 - 1) / (NB_THREADS / 64);
+  NSMOE_REQUIRE(grid < INT32_MAX, "rms_norm: too many rows");
+  KernelTimer timer("norm_fwd", s);
+  if (dtype == DT_BF16)
+    norm_fwd_kernel<DT_BF16><<<(unsigned)grid, NB_THREADS, 0, s>>>(x, weight, y, rstd, n_rows, d, eps);
+  else
+    norm_fwd_kernel<DT_F16><<<(unsigned)grid, NB_THREADS, 0, s>>>(x, weight, y, rstd, n_rows, d, eps);
+  timer.stop();
+  return check_launch("norm_fwd_kernel");
+}

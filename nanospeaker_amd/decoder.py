@@ -69,14 +69,24 @@ class DecoderConfig:
 
 
 class RMSNorm(nn.Module):
-    """x / rms(x) * gamma over the last dim, computed by F.rms_norm (ln.py:30-36)."""
+    """x / rms(x) * gamma over the last dim (ln.py:30-36, F.rms_norm's arithmetic).  A
+    gradient-free 16-bit forward of contiguous rows on the GPU runs the library's kernel
+    (nsmoe_rms_norm: one HBM read and write of the rows); everything else is F.rms_norm."""
 
-    def __init__(self, d: int, eps: float = 1e-6):
+    def __init__(self, d: int, eps: float = 1e-6, kernel: bool = True):
         super().__init__()
-        self.d, self.eps = d, eps
+        self.d, self.eps, self.kernel = d, eps, kernel
         self.gamma = nn.Parameter(torch.ones(d))
 
+    def use_kernel(self, x: torch.Tensor) -> bool:
+        return (self.kernel and x.is_cuda and x.dtype in _ATTN_DT
+                and self.gamma.dtype == x.dtype and x.is_contiguous() and self.d % 8 == 0
+                and self.d <= 1024
+                and not (torch.is_grad_enabled() and (x.requires_grad or self.gamma.requires_grad)))
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.use_kernel(x):
+            return rms_norm(x, self.gamma, self.eps)
         return F.rms_norm(x, (self.d,), self.gamma, self.eps)
 
 
@@ -112,6 +122,19 @@ class Rotary:
 
 
 _ATTN_DT = {torch.bfloat16: nat.BF16, torch.float16: nat.F16}
+
+
+def rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    """F.rms_norm(x, (d,), w, eps) of a contiguous 16-bit GPU tensor on the library's kernel
+    (nsmoe_rms_norm).  Forward only."""
+    d = x.shape[-1]
+    y = torch.empty_like(x)
+    wc = w.detach().contiguous()
+    nat.check(nat.lib().nsmoe_rms_norm(_ATTN_DT[x.dtype], x.data_ptr(), wc.data_ptr(),
+                                       float(eps), x.numel() // d, d, y.data_ptr(), None,
+                                       torch.cuda.current_stream().cuda_stream),
+              "nsmoe_rms_norm")
+    return y
 
 
 def attn_prefill(qkv: torch.Tensor, B: int, T: int, n_heads: int, n_kv_heads: int,
@@ -216,14 +239,39 @@ class Attention(nn.Module):
                 and not (torch.is_grad_enabled() and any(
                     t.requires_grad for t in (z, self.W_q, self.W_k, self.W_v, self.W_O))))
 
+    def _w_qkv(self, dtype) -> torch.Tensor:
+        """[W_q | W_k | W_v] in `dtype`, kept while the three weights are unchanged (their
+        identity, storage and autograd versions)."""
+        key = tuple((t.data_ptr(), t._version) for t in (self.W_q, self.W_k, self.W_v))
+        key += (dtype,)
+        hit = getattr(self, "_qkv_cache", None)
+        if hit is None or hit[0] != key:
+            w = torch.cat((self.W_q, self.W_k, self.W_v), dim=1).to(dtype).detach()
+            hit = self._qkv_cache = (key, w)
+        return hit[1]
+
+    def _kernel_attention(self, z: torch.Tensor) -> torch.Tensor:
+        """[B T, h dh]: the attention output before W_O, on the HIP prefill kernels."""
+        B, T, _ = z.shape
+        qkv = z.reshape(B * T, -1) @ self._w_qkv(z.dtype)
+        cos, sin = self.rotary.tables_f32(T, z.device)
+        return attn_prefill(qkv, B, T, self.h, self.hk, self.q_norm.gamma, self.k_norm.gamma,
+                            cos, sin, self.window, self.q_norm.eps)
+
+    def forward_residual(self, x: torch.Tensor, z: torch.Tensor) -> torch.Tensor:
+        """x + self(z): on the kernel path the residual enters the W_O GEMM as its addend
+        (one rounding of x + o W_O instead of two); elsewhere exactly x + self(z)."""
+        if self.use_kernel(z) and x.dtype == z.dtype and not (
+                torch.is_grad_enabled() and x.requires_grad):
+            B, T, d = x.shape
+            o = self._kernel_attention(z)
+            return torch.addmm(x.reshape(B * T, d), o, self.W_O.to(z.dtype)).view(B, T, d)
+        return x + self(z)
+
     def forward(self, z: torch.Tensor) -> torch.Tensor:
         B, T, _ = z.shape
         if self.use_kernel(z):
-            w = torch.cat((self.W_q, self.W_k, self.W_v), dim=1).to(z.dtype)
-            qkv = z.reshape(B * T, -1) @ w
-            cos, sin = self.rotary.tables_f32(T, z.device)
-            o = attn_prefill(qkv, B, T, self.h, self.hk, self.q_norm.gamma, self.k_norm.gamma,
-                             cos, sin, self.window, self.q_norm.eps)
+            o = self._kernel_attention(z)
             return o.view(B, T, self.h * self.dh) @ self.W_O
         q = (z @ self.W_q).view(B, T, self.h, self.dh).transpose(1, 2)
         k = (z @ self.W_k).view(B, T, self.hk, self.dh).transpose(1, 2)
@@ -254,7 +302,7 @@ class DecoderBlock(nn.Module):
                             std=cfg.std, fused=False, kernel=kernel)
 
     def forward(self, x: torch.Tensor):
-        x = x + self.attn(self.norm_attn(x))
+        x = self.attn.forward_residual(x, self.norm_attn(x))
         return self.ffn.forward_residual(x, self.norm_ffn), self.ffn.aux_loss
 
 
@@ -283,7 +331,7 @@ class Decoder(nn.Module):
             if ffn_hook is None:
                 x, a = blk(x)
             else:
-                x = x + blk.attn(blk.norm_attn(x))
+                x = blk.attn.forward_residual(x, blk.norm_attn(x))
                 x = ffn_hook(blk, x)
                 a = blk.ffn.aux_loss
             aux = aux + a

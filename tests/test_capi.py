@@ -95,6 +95,20 @@ def test_cross_entropy_rows_rejects_bad_arguments(args, needle):
     assert needle in lib.nsmoe_last_error().decode()
 
 
+@pytest.mark.parametrize("args,needle", [
+    ((2, 16, 16, 1e-6, 4, 64, 16, None), "16-bit"),
+    ((0, 16, 16, 1e-6, 4, 60, 16, None), "d %"),
+    ((0, 16, 16, 1e-6, 4, 2048, 16, None), "d %"),
+    ((0, 16, 16, 1e-6, -1, 64, 16, None), "n_rows"),
+    ((0, None, 16, 1e-6, 4, 64, 16, None), "NULL"),
+    ((0, 8, 16, 1e-6, 4, 64, 16, None), "aligned"),
+])
+def test_rms_norm_rejects_bad_arguments(args, needle):
+    lib = nat.lib()
+    assert lib.nsmoe_rms_norm(*args, None) == 1
+    assert needle in lib.nsmoe_last_error().decode()
+
+
 def test_abi_version_and_alignment():
     assert nat.lib().nsmoe_abi_version() == nat.ABI_VERSION == 7
     assert nat.lib().nsmoe_align_m() == mk.ALIGN_M

@@ -148,3 +148,29 @@ def test_module_falls_back_to_torch_when_differentiated():
     assert not att.use_kernel(z)
     att(z).float().sum().backward()
     assert z.grad is not None
+
+
+@pytest.mark.parametrize("shape,dt", [((8192, 576), torch.bfloat16), ((3, 7, 64), torch.float16),
+                                      ((1, 1024), torch.bfloat16)])
+def test_rms_norm_kernel_matches_the_oracle(shape, dt):
+    """nsmoe_rms_norm (the attention's pre-norm and the final norm on the kernel path)
+    against the oracle's restatement of F.rms_norm (pinned bit for bit to torch's CPU
+    F.rms_norm): equal up to one rounding step where the fp32 rstd's last bit differs
+    (summation order), and the module takes the kernel for a gradient-free 16-bit call."""
+    from oracle import moe_ref as R
+    from nanospeaker_amd.decoder import RMSNorm, rms_norm
+    g = torch.Generator().manual_seed(shape[-1])
+    x = (torch.randn(*shape, generator=g) * 3).to(dt)
+    w = (1 + 0.2 * torch.randn(shape[-1], generator=g)).to(dt)
+    ref, _ = R.rms_norm(x, w, 1e-6)
+    got = rms_norm(x.to(DEV), w.to(DEV), 1e-6).cpu()
+    ulp = {torch.bfloat16: 2.0 ** -7, torch.float16: 2.0 ** -10}[dt]
+    diff = (got.float() - ref.float()).abs()
+    assert bool((diff <= ulp * ref.float().abs() * 1.001 + 1e-30).all())
+    print(f"  rms_norm {shape}: {float((diff > 0).float().mean()):.2e} of elements one step off",
+          flush=True)
+    norm = RMSNorm(shape[-1], 1e-6).to(dt).to(DEV)
+    with torch.no_grad():
+        norm.gamma.copy_(w)
+        assert norm.use_kernel(x.to(DEV))
+        assert torch.equal(norm(x.to(DEV)).cpu(), got)
