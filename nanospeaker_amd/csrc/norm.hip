@@ -147,9 +147,12 @@ int norm_bwd_launch(int dtype, const NormBwdArgs& a, hipStream_t s) {
 // y = RMSNorm(x) for the norms the block's kernels do not take (the attention's pre-norm and
 // the final norm of the decoder around the block): F.rms_norm's arithmetic, fp32
 // rstd = 1 / sqrt(mean(x^2) + eps) and y = (x rstd) w rounded once, as the router kernel's
-// fused norm computes it.  One wave per row (16-byte chunks, two per lane at d <= 1024),
-// the row's sum of squares by a wave butterfly; 4 rows per workgroup, so a row is one read
-// and one write of HBM.
+// fused norm computes it.  A wave takes NF_ROWS rows (16-byte chunks, two per lane at
+// d <= 1024) and issues all their loads before the first sum of squares, so each wave keeps
+// NF_ROWS rows in flight; each row's sum is a wave butterfly.  A row is one read and one
+// write of HBM.
+constexpr int NF_ROWS = 4;
+
 template <int DT>
 __global__ void __launch_bounds__(NB_THREADS) norm_fwd_kernel(const void* __restrict__ x,
                                                               const void* __restrict__ w,
@@ -158,36 +161,51 @@ __global__ void __launch_bounds__(NB_THREADS) norm_fwd_kernel(const void* __rest
                                                               int64_t T, int d, float eps) {
   using ET = typename Elem<DT>::T;
   const int lane = threadIdx.x & 63;
-  const int64_t t = (int64_t)blockIdx.x * (NB_THREADS / 64) + (threadIdx.x >> 6);
-  if (t >= T) return;  // uniform per wave; no workgroup barrier below
+  const int64_t t0 = ((int64_t)blockIdx.x * (NB_THREADS / 64) + (threadIdx.x >> 6)) * NF_ROWS;
+  if (t0 >= T) return;  // uniform per wave; no workgroup barrier below
   const int nch = d / 8;
-  u32x4 xv[NB_MAXU];
-  float ss = 0.0f;
+  u32x4 xv[NF_ROWS][NB_MAXU];
+#pragma unroll
+  for (int r = 0; r < NF_ROWS; ++r)
+#pragma unroll
+    for (int u = 0; u < NB_MAXU; ++u) {
+      const int c = lane + 64 * u;
+      xv[r][u] = c < nch && t0 + r < T ? *(const u32x4*)((const ET*)x + (t0 + r) * d + 8 * c)
+                                       : u32x4{0u, 0u, 0u, 0u};
+    }
+  u32x4 wv[NB_MAXU];
 #pragma unroll
   for (int u = 0; u < NB_MAXU; ++u) {
     const int c = lane + 64 * u;
-    xv[u] = c < nch ? *(const u32x4*)((const ET*)x + t * d + 8 * c) : u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float v = unpack2<DT>(xv[u][e / 2], e & 1);
-      ss += v * v;
-    }
+    wv[u] = c < nch ? *(const u32x4*)((const ET*)w + 8 * c) : u32x4{0u, 0u, 0u, 0u};
   }
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
-  const float rstd = 1.0f / sqrtf(ss / (float)d + eps);
-  if (rstd_out && lane == 0) rstd_out[t] = rstd;
+  for (int r = 0; r < NF_ROWS; ++r) {
+    const int64_t t = t0 + r;
+    if (t >= T) break;  // uniform
+    float ss = 0.0f;
 #pragma unroll
-  for (int u = 0; u < NB_MAXU; ++u) {
-    const int c = lane + 64 * u;
-    if (c >= nch) continue;
-    const u32x4 wv = *(const u32x4*)((const ET*)w + 8 * c);
-    u32x4 o;
+    for (int u = 0; u < NB_MAXU; ++u)
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      o[q] = pack2<DT>(unpack2<DT>(xv[u][q], 0) * rstd * unpack2<DT>(wv[q], 0),
-                       unpack2<DT>(xv[u][q], 1) * rstd * unpack2<DT>(wv[q], 1));
-    *(u32x4*)((ET*)y + t * d + 8 * c) = o;
+      for (int e = 0; e < 8; ++e) {
+        const float v = unpack2<DT>(xv[r][u][e / 2], e & 1);
+        ss += v * v;
+      }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    const float rstd = 1.0f / sqrtf(ss / (float)d + eps);
+    if (rstd_out && lane == 0) rstd_out[t] = rstd;
+#pragma unroll
+    for (int u = 0; u < NB_MAXU; ++u) {
+      const int c = lane + 64 * u;
+      if (c >= nch) continue;
+      u32x4 o;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        o[q] = pack2<DT>(unpack2<DT>(xv[r][u][q], 0) * rstd * unpack2<DT>(wv[u][q], 0),
+                         unpack2<DT>(xv[r][u][q], 1) * rstd * unpack2<DT>(wv[u][q], 1));
+      *(u32x4*)((ET*)y + t * d + 8 * c) = o;
+    }
   }
 }
 
@@ -207,7 +225,8 @@ extern "C" int nsmoe_rms_norm(int32_t dtype, const void* x, const void* weight, 
                     ((uintptr_t)y & 15) == 0,
                 "rms_norm: x, weight and y must be 16-byte aligned");
   hipStream_t s = (hipStream_t)stream;
-  const int64_t grid = (n_rows + NB_THREADS / 64 - 1) / (NB_THREADS / 64);
+  const int64_t rows_per_wg = (int64_t)(NB_THREADS / 64) * NF_ROWS;
+  const int64_t grid = (n_rows + rows_per_wg - 1) / rows_per_wg;
   NSMOE_REQUIRE(grid < INT32_MAX, "rms_norm: too many rows");
   KernelTimer timer("norm_fwd", s);
   if (dtype == DT_BF16)

@@ -272,8 +272,14 @@ __global__ void __launch_bounds__(NT) router_dw_kernel(RouterDwArgs a) {
   constexpr int S = RDW_S;
   __shared__ __attribute__((aligned(1024))) char s_ring[S][STAGE];
 
-  const int m0 = blockIdx.x * RDW_BMT;
-  const int64_t r0 = (int64_t)blockIdx.y * RDW_RC;
+  // A 1-D grid: the column tiles of one token chunk are consecutive items, dealt to one XCD
+  // together (xcd_deal), so the chunk's d(logits) rows, which every tile of the chunk reads,
+  // come into that XCD's L2 once.
+  const int ntx = (a.d + RDW_BMT - 1) / RDW_BMT;
+  const int item = xcd_deal((int)blockIdx.x, (int)gridDim.x, ntx);
+  const int chunk = item / ntx;
+  const int m0 = (item - chunk * ntx) * RDW_BMT;
+  const int64_t r0 = (int64_t)chunk * RDW_RC;
   const int nr = (int)min<int64_t>(RDW_RC, a.T - r0);
   const int lane = threadIdx.x & 63, lc = lane & 15, lg = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -345,7 +351,7 @@ __global__ void __launch_bounds__(NT) router_dw_kernel(RouterDwArgs a) {
   }
   wait_vmcnt<0>();
 
-  float* part = a.partial + (int64_t)blockIdx.y * a.d * a.ep;
+  float* part = a.partial + (int64_t)chunk * a.d * a.ep;
 #pragma unroll
   for (int j = 0; j < TNB; ++j) {
     const int n = (wn * TNB + j) * 16 + lg * 4;
@@ -417,7 +423,7 @@ int router_dw_launch(int dtype, const RouterDwArgs& a, hipStream_t s) {
   if (a.T == 0) return NSMOE_OK;
   const int64_t nchunks = cdiv(a.T, RDW_RC);
   NSMOE_REQUIRE(nchunks < 65536, "router_dw: %lld tokens", (long long)a.T);
-  const dim3 grid((unsigned)cdiv(a.d, RDW_BMT), (unsigned)nchunks);
+  const unsigned grid = (unsigned)(cdiv(a.d, RDW_BMT) * nchunks);
   KernelTimer timer("router_dw", s);
   if (dtype == DT_BF16) router_dw_kernel<DT_BF16><<<grid, NT, 0, s>>>(a);
   else router_dw_kernel<DT_F16><<<grid, NT, 0, s>>>(a);
