@@ -20,6 +20,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
        python bench.py --calibrate-copy ...      (under rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)
        python bench.py --pmc-summary FETCH_CSV WRITE_CSV   (-> profiles/hbm_traffic_T8192.md)
        python bench.py --stats-summary KERNEL_STATS_CSV    (-> profiles/*_kernel_stats.md)
+       python bench.py --prefill-legs KERNEL_TRACE_CSV     (-> profiles/prefill_B4x8192_kernel_stats.md)
 """
 
 from __future__ import annotations
@@ -72,6 +73,9 @@ def parse():
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="print the HBM-traffic table from two rocprofv3 --pmc runs "
                          "(FETCH_SIZE, WRITE_SIZE) of `bench.py --calibrate-copy`, and exit")
+    ap.add_argument("--prefill-legs", metavar="KERNEL_TRACE_CSV",
+                    help="print per-leg kernel tables of a rocprofv3 --kernel-trace run of "
+                         "`bench.py --only c5_prefill,c5_head_cross_entropy`, and exit")
     return ap.parse_args()
 
 
@@ -251,6 +255,51 @@ def pmc_summary(fetch_csv, write_csv):
                 tb = fv * 1024 * ff + wv * 1024 * fw
                 lines.append(f"| {bname} | `{sym}` | {n} | {fv:.1f} | {wv:.1f} | {tb:.0f} |")
     return "\n".join(lines)
+
+
+def prefill_legs(path, top=14):
+    """Markdown tables of a --kernel-trace run of the prefill configurations, one per leg
+    in the order bench.py runs them: the prefills with the HIP attention (up to the first
+    dispatch of torch SDPA's `attn_fwd`), the prefills with torch attention (up to the last
+    MoE-library or SDPA kernel before the first `ce_rows_kernel`), then the head's
+    cross-entropy calls; with the hip leg's `attn_fwd_kernel` launches split into global
+    (> 300 us) and windowed layers."""
+    import csv
+    from collections import defaultdict
+
+    with open(path) as f:
+        rows = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
+    names = [r["Kernel_Name"] for r in rows]
+    first_sdpa = names.index("attn_fwd")
+    first_ce = next(i for i, n in enumerate(names) if n.startswith("void nsmoe::ce_rows"))
+    last_body = max(i for i in range(first_ce) if "nsmoe::" in names[i] or names[i] == "attn_fwd")
+    legs = {"hip": rows[:first_sdpa], "sdpa": rows[first_sdpa:last_body + 1],
+            "head": rows[last_body + 1:]}
+
+    def us(r):
+        return (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+
+    out = []
+    for leg, rs in legs.items():
+        agg = defaultdict(list)
+        for r in rs:
+            agg[r["Kernel_Name"]].append(us(r))
+        tot = sum(sum(v) for v in agg.values())
+        wall = (int(rs[-1]["End_Timestamp"]) - int(rs[0]["Start_Timestamp"])) / 1e6
+        out += [f"\n## {leg}: {len(rs)} dispatches, {tot / 1e3:.2f} ms of kernel time "
+                f"({wall:.2f} ms from first start to last end)",
+                "| kernel | calls | avg us | total ms | % |", "|---|---|---|---|---|"]
+        for n, v in sorted(agg.items(), key=lambda kv: -sum(kv[1]))[:top]:
+            out.append(f"| {n[:80]} | {len(v)} | {sum(v) / len(v):.2f} | {sum(v) / 1e3:.2f} | "
+                       f"{100 * sum(v) / tot:.1f} |")
+    att = [us(r) for r in legs["hip"] if r["Kernel_Name"].startswith("void nsmoe::attn_fwd_kernel")]
+    glob = [t for t in att if t > 300.0]
+    win = [t for t in att if t <= 300.0]
+    if glob and win:
+        out.append(f"\nhip leg `attn_fwd_kernel`: {len(glob)} global launches, avg "
+                   f"{sum(glob) / len(glob):.1f} us; {len(win)} windowed, avg "
+                   f"{sum(win) / len(win):.1f} us")
+    return "\n".join(out)
 
 
 def stats_summary(path, top=30):
@@ -756,6 +805,9 @@ def main():
         return
     if a.stats_summary:
         print(stats_summary(a.stats_summary))
+        return
+    if a.prefill_legs:
+        print(prefill_legs(a.prefill_legs))
         return
     if a.mfma_summary:
         print(mfma_summary(*a.mfma_summary, a.stats_csv))

@@ -334,7 +334,10 @@ class Decoder(nn.Module):
                 x = blk.attn.forward_residual(x, blk.norm_attn(x))
                 x = ffn_hook(blk, x)
                 a = blk.ffn.aux_loss
-            aux = aux + a
+            # The same fp32 sum as aux + a under type promotion (a widened exactly): a
+            # 16-bit loss (the block's zero in eval) is widened first, because torch's
+            # mixed-dtype add kernel takes ~45 us for a 0-dim tensor on this stack.
+            aux = aux + (a if a.dtype == aux.dtype else a.float())
         return self.norm_out(x), aux
 
     def forward(self, idx: torch.Tensor, targets: "torch.Tensor | None" = None,

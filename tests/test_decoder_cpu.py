@@ -93,3 +93,23 @@ def test_decoder_loss_is_the_reference_next_token_cross_entropy():
                               idx[:, 1:].reshape(-1))
     torch.testing.assert_close(loss, ref, rtol=0, atol=0)
     assert aux.shape == ()
+
+
+def test_trunk_balance_loss_is_the_promoted_sum_of_the_blocks():
+    """trunk's aux equals the reference's fp32 accumulation aux + a (nanospeaker.py:220-230)
+    of each block's balance loss under type promotion, for a 16-bit model in training (a
+    16-bit loss per block) and in eval (the blocks' zeros)."""
+    torch.manual_seed(1)
+    cfg = DecoderConfig(n_layers=3, vocab_size=64, window=None, global_every=None)
+    model = Decoder(cfg, kernel=False).to(torch.bfloat16)
+    idx = torch.randint(0, 64, (2, 12))
+    for train in (True, False):
+        model.train(train)
+        with torch.no_grad():
+            _, aux = model.trunk(idx)
+        ref = torch.zeros((), dtype=torch.float32)
+        for blk in model.blocks:
+            ref = ref + blk.ffn.aux_loss
+        assert aux.dtype == torch.float32
+        assert torch.equal(aux, ref), (train, aux, ref)
+        assert (float(aux) != 0.0) == train
