@@ -66,6 +66,19 @@ struct AttnParams {
 // per 32 lanes) both land on distinct banks.
 __device__ __forceinline__ int at_swz(int r) { return (((r >> 1) & 3) << 1) | ((r >> 3) & 1); }
 
+// Maximum over lanes l, l ^ 16, l ^ 32, l ^ 48, in every lane.  v_permlane16_swap applied
+// to two copies of v leaves v[l] in one result and v[l ^ 16] in the other (it exchanges
+// the odd 16-lane rows of the first operand with the even rows of the second);
+// v_permlane32_swap does the same for l ^ 32 with the two 32-lane halves.
+__device__ __forceinline__ float max_xor16_32(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v),
+                                                  false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                  false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 // RMSNorm (F.rms_norm: fp32 rstd = 1 / sqrt(mean(x^2) + eps), x rstd gamma rounded once)
 // and the rotation (in the dtype, as the reference's bf16 tensor ops: every product, the
 // difference and the sum rounded) of one 64-element head row spread over 4 lanes: this
@@ -254,35 +267,48 @@ __global__ void __launch_bounds__(AT_NT, 2) attn_fwd_kernel(AttnParams p) {
       }
     }
 
-    // Mask (only tiles that cross the diagonal or the window's far edge) and online softmax.
+    // Mask, only on tiles that cross the diagonal or the window's far edge: one uniform
+    // branch, then a select per score (no per-score control flow).
     const bool masked = key0 + AT_BK - 1 > q0 || (banded && key0 < qmax - p.window + 1);
-    // The running maximum m is kept on the raw scores; p = 2^(s c - m c) with
-    // c = log2(e) / 8 is one FMA and one exp2 per score.
+    if (masked) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const int q = qpos[nb];
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int key = key0 + 16 * kb + 4 * g + e;
+            const bool dead = (key > q) | (banded & (q - key >= p.window));
+            s[kb][nb][e] = dead ? -INFINITY : s[kb][nb][e];
+          }
+      }
+    }
+    // Online softmax.  The running maximum m is kept on the raw scores; p = 2^(s c - m c)
+    // with c = log2(e) / 8 is one FMA and one exp2 per score.  A query's 16 scores of the
+    // tile sit in lanes l, l ^ 16, l ^ 32, l ^ 48: their maximum takes two lane swaps
+    // (v_permlane16_swap / v_permlane32_swap, VALU, no LDS round trip).
     const float c = p.scale_log2;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
-      float mx = -INFINITY;
+      float mx = s[0][nb][0];
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float v = s[kb][nb][e];
-          if (masked) {
-            const int key = key0 + 16 * kb + 4 * g + e, q = qpos[nb];
-            if (key > q || (banded && q - key >= p.window)) v = -INFINITY;
-          }
-          s[kb][nb][e] = v;
-          mx = fmaxf(mx, v);
-        }
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
+        for (int e = 0; e < 4; ++e) mx = fmaxf(mx, s[kb][nb][e]);
+      mx = max_xor16_32(mx);
       const float mnew = fmaxf(m[nb], mx);
       const float msub = mnew == -INFINITY ? 0.0f : mnew * c;  // no key seen yet: p = 0
-      const float alpha = __builtin_amdgcn_exp2f(fmaf(m[nb], c, -msub));
-      m[nb] = mnew;
-      float ls = lsum[nb] * alpha;
+      // The accumulators are rescaled only when some query's maximum moved (wave-uniform
+      // branch); with m unchanged, msub is the value the earlier tiles' p used.
+      if (__ballot(mnew != m[nb])) {
+        const float alpha = __builtin_amdgcn_exp2f(fmaf(m[nb], c, -msub));
+        lsum[nb] *= alpha;
 #pragma unroll
-      for (int db = 0; db < 4; ++db) o[db][nb] *= alpha;
+        for (int db = 0; db < 4; ++db) o[db][nb] *= alpha;
+      }
+      m[nb] = mnew;
+      float ls = lsum[nb];
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
