@@ -123,6 +123,33 @@ def kernel_units(name: str, T: int, k: int, S: int, d: int, H: int, E: int):
     return None
 
 
+def kernel_bytes(name: str, T: int, k: int, S: int, d: int, H: int, E: int):
+    """Algorithmic HBM bytes per launch of the grouped-GEMM kernels (each input read once,
+    each output written once; gathered token rows counted once), or None."""
+    rows = T * k + S * T
+    w_in, w_out = (E + S) * d * 2 * H * 2, (E + S) * H * d * 2
+    if name == "expert_fwd":        # x, both weights in; rows out, saved a1 out
+        return T * d * 2 + w_in + w_out + rows * d * 2 + rows * 2 * H * 2
+    if name == "expert_bwd":        # dout, a1, W_out in; dA1, w h out
+        return T * d * 2 + rows * 2 * H * 2 + w_out + rows * 2 * H * 2 + rows * H * 2
+    if name == "expert_dx":         # dA1, W_in in; dX rows out
+        return rows * 2 * H * 2 + w_in + rows * d * 2
+    if name == "dw":                # x, dout, dA1, w h in; dW_in, dW_out out
+        return 2 * T * d * 2 + rows * 2 * H * 2 + rows * H * 2 + w_in + w_out
+    return None
+
+
+def roofline_of(name: str, T: int, k: int, S: int, d: int, H: int, E: int):
+    """(units, bound, unit, extra) for kernel `name`: the grouped GEMMs are rated against
+    the MFMA peak, the dense-contraction roof the measurement plan names for them; `extra`
+    adds their algorithmic bytes, which at these shapes sit below the ridge point
+    (2.5 PFLOP/s / 8 TB/s = 312 FLOP/B), so the HBM roof is reported beside it."""
+    units, bound, unit = kernel_units(name, T, k, S, d, H, E)
+    nbytes = kernel_bytes(name, T, k, S, d, H, E)
+    extra = {"bytes_per_launch": nbytes} if bound == "mfma" and nbytes is not None else {}
+    return units, bound, unit, extra
+
+
 def time_gpu(m, x, g, steps: int, warmup: int):
     """Eager fwd+bwd step time, its host enqueue time, per-kernel launch times and the
     eager forward (no_grad, weights unchanged, so the forward reuses the cached packs)."""
@@ -860,7 +887,7 @@ def main():
     dom = max(kernels, key=lambda n: kernels[n][0] * kernels[n][1]) if kernels else None
     roofline = None
     if dom:
-        units, bound, unit = kernel_units(dom, T, k, S, d, H, E)
+        units, bound, unit, extra = roofline_of(dom, T, k, S, d, H, E)
         avg_s = kernels[dom][0] / 1e3
         if bound == "mfma":
             achieved, peak = units / avg_s / 1e12, PEAK_BF16_TFLOPS
@@ -872,6 +899,11 @@ def main():
                     "traffic_source": "profiles/" + os.path.basename(TRAFFIC_FILE),
                     "avg_launch_us": round(kernels[dom][0] * 1e3, 2),
                     "algorithmic_per_launch": units}
+        if extra:  # the same launch against the HBM roof, from its algorithmic bytes
+            gbs = extra["bytes_per_launch"] / avg_s / 1e9
+            roofline.update(algorithmic_bytes_per_launch=extra["bytes_per_launch"],
+                            hbm_algorithmic_gbs=round(gbs, 1),
+                            hbm_frac=round(gbs / PEAK_HBM_GBS, 4))
     rec = {
         "metric": "MoE-block tokens/s fwd & fwd+bwd at T=8192 bf16; % of MFMA / HBM peak",
         "value": round(T / (ms / 1e3), 1),
