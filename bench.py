@@ -643,7 +643,7 @@ def config5(steps, warmup):
         ms = run_timed(reps)
         for blk, fwd in zip(model.blocks, originals):
             blk.attn.forward_residual = (
-                lambda x, z, fwd=fwd: timed("attn", lambda: fwd(x, z)))
+                lambda x, z, fwd=fwd, **kw: timed("attn", lambda: fwd(x, z, **kw)))
         model(idx, ffn_hook=hook)
         torch.cuda.synchronize()
         for v in pairs.values():

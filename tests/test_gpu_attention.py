@@ -174,3 +174,35 @@ def test_rms_norm_kernel_matches_the_oracle(shape, dt):
         norm.gamma.copy_(w)
         assert norm.use_kernel(x.to(DEV))
         assert torch.equal(norm(x.to(DEV)).cpu(), got)
+
+
+def test_residual_in_place_equals_the_copying_add():
+    """forward_residual(inplace=True) accumulates x + o W_O into x's own memory (no copy
+    of the addend) and gives the same bits as the copying form."""
+    att = make_attention(9, 3, 512)
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(2, 300, 576, generator=g).to(torch.bfloat16).to(DEV)
+    z = torch.randn(2, 300, 576, generator=g).to(torch.bfloat16).to(DEV)
+    with torch.no_grad():
+        ref = att.forward_residual(x.clone(), z)
+        xi = x.clone()
+        got = att.forward_residual(xi, z, inplace=True)
+    assert got.data_ptr() == xi.data_ptr()
+    assert torch.equal(got, ref)
+
+
+def test_decoder_trunk_matches_its_blocks_run_one_by_one():
+    """The trunk (which lets each block's attention add its residual in place) against
+    the blocks called one at a time with copying adds."""
+    from nanospeaker_amd.decoder import Decoder
+    torch.manual_seed(0)
+    model = Decoder(DecoderConfig(n_layers=2, vocab_size=512)).to(torch.bfloat16)
+    model = model.to(DEV).eval()
+    idx = torch.randint(0, 512, (1, 200), device=DEV)
+    with torch.no_grad():
+        h, _ = model.trunk(idx)
+        x = model.embed(idx)
+        for blk in model.blocks:
+            x, _ = blk(x)
+        ref = model.norm_out(x)
+    assert torch.equal(h, ref)
