@@ -26,16 +26,17 @@
 // The kernel computes S^T = K Q^T, so lane l of a wave ends with 4 consecutive keys of one
 // query column (the MFMA accumulator layout).  Everything the online softmax needs per
 // query is then in one lane or across the 4 lanes l, l ^ 16, l ^ 32, l ^ 48: the running
-// maximum takes two shuffles per tile, and the running sum is kept per lane and reduced
-// once at the end.  The probabilities are already the B operand of O^T = V^T P^T: for the
-// 32 keys of a P V step, k slot 8 g + e (lane group g) is key 4 g + e of the first 16-key
-// block and slot 8 g + 4 + e key 4 g + e of the second -- the keys the lane holds -- and
+// maximum takes two lane swaps per tile, and the running sum comes from one more MFMA per
+// P V step (a block of ones against P^T).  The probabilities are already the B operand of
+// O^T = V^T P^T: for the 32 keys of a P V step, k slot 8 g + e (lane group g) is key
+// 4 g + e of the first 16-key block and slot 8 g + 4 + e key 4 g + e of the second -- the
+// keys the lane holds -- and
 // the value rows are read in the same order with ds_read_b64_tr_b16.  No LDS round trip
 // and no lane shuffles between the two GEMMs.
 //
 // Scores are scaled by log2(e) / sqrt(64) in fp32 and exponentiated with exp2; the
-// probabilities enter the P V MFMA rounded to the dtype, the running sums stay fp32, and
-// the output is divided by the sum and rounded once.
+// probabilities enter the P V MFMA rounded to the dtype, their sums are accumulated in fp32
+// over the same rounded values, and the output is divided by the sum and rounded once.
 #include "../../include/nsmoe.h"
 #include "gemm_core.h"
 #include "nsmoe_capi_internal.h"
@@ -223,15 +224,20 @@ __global__ void __launch_bounds__(AT_NT, 2) attn_fwd_kernel(AttnParams p) {
     }
   };
 
-  f32x4 o[4][NB];
-  float m[NB], lsum[NB];
+  // o[0..3]: O^T's four 16-dim blocks of each column block; o[4]: the row sums of the
+  // probabilities, from one more MFMA per P V step against a block of ones (every lane
+  // then holds its query's sum of the same rounded p the P V MFMAs used; no VALU adds
+  // and no cross-lane reduction).
+  f32x4 o[5][NB];
+  float m[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
     m[nb] = -INFINITY;
-    lsum[nb] = 0.0f;
 #pragma unroll
-    for (int db = 0; db < 4; ++db) o[db][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int db = 0; db < 5; ++db) o[db][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
+  constexpr uint32_t one2 = DT == DT_BF16 ? 0x3F803F80u : 0x3C003C00u;  // two 1.0s
+  const Frag ones{u32x4{one2, one2, one2, one2}};
 
   // Tiles t + 1 and t + 2 are in flight while tile t is computed: tile t + 2's copies go
   // into the stage tile t - 1 used, after the barrier that every wave reaches only once
@@ -303,21 +309,15 @@ __global__ void __launch_bounds__(AT_NT, 2) attn_fwd_kernel(AttnParams p) {
       // branch); with m unchanged, msub is the value the earlier tiles' p used.
       if (__ballot(mnew != m[nb])) {
         const float alpha = __builtin_amdgcn_exp2f(fmaf(m[nb], c, -msub));
-        lsum[nb] *= alpha;
 #pragma unroll
-        for (int db = 0; db < 4; ++db) o[db][nb] *= alpha;
+        for (int db = 0; db < 5; ++db) o[db][nb] *= alpha;
       }
       m[nb] = mnew;
-      float ls = lsum[nb];
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float pe = __builtin_amdgcn_exp2f(fmaf(s[kb][nb][e], c, -msub));
-          s[kb][nb][e] = pe;
-          ls += pe;
-        }
-      lsum[nb] = ls;
+        for (int e = 0; e < 4; ++e)
+          s[kb][nb][e] = __builtin_amdgcn_exp2f(fmaf(s[kb][nb][e], c, -msub));
     }
 
     // O^T += V^T P^T over the 64 keys, 32 at a time (key blocks 2 ks and 2 ks + 1).
@@ -342,15 +342,15 @@ __global__ void __launch_bounds__(AT_NT, 2) attn_fwd_kernel(AttnParams p) {
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) M::run(o[db][nb], vf, pf[nb]);
       }
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) M::run(o[4][nb], ones, pf[nb]);
     }
   }
 
   // O / sum, rounded once: lane holds dims 16 db + 4 g .. + 3 of its query column.
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
-    float l = lsum[nb];
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
+    const float l = o[4][nb][0];
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
     const int qp = qpos[nb];
     if (qp >= T) continue;
