@@ -208,19 +208,31 @@ __global__ void __launch_bounds__(AT_NT, 2) attn_fwd_kernel(AttnParams p) {
   // the global chunk (i % 8) ^ at_swz(row).
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)&s_kv[0][0][0];
   const uint16_t* zero = (const uint16_t*)((const char*)g_zero_kib + lane * 16);
+  // Each copy's source for tile 0 is fixed per lane; tile t adds t * 64 rows (a
+  // wave-uniform byte offset), and only a tile that runs past T checks its rows.
+  const uint16_t* csrc[4];
+  int crow[4];
+  uint32_t cdst[4];
+#pragma unroll
+  for (int u4 = 0; u4 < 4; ++u4) {
+    const int u = wave * 4 + u4;
+    const int which = u >> 3, rb = u & 7;
+    const int r = rb * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ at_swz(r);
+    crow[u4] = r;
+    csrc[u4] = p.qkv + (row0 + r) * ld + (int64_t)(p.Hq + which * p.Hkv + hk) * AT_DH + c * 8;
+    cdst[u4] = lds0 + (uint32_t)(which * AT_TILE + rb * 1024);
+  }
+  const int64_t tile_step = (int64_t)AT_BK * ld;  // elements between tiles
   auto issue = [&](int t, int stage) {
     const int key0 = t * AT_BK;
+    const int64_t off = (int64_t)t * tile_step;
+    const bool whole = key0 + AT_BK <= T;  // uniform
 #pragma unroll
     for (int u4 = 0; u4 < 4; ++u4) {
-      const int u = wave * 4 + u4;
-      const int which = u >> 3, rb = u & 7;
-      const int r = rb * 8 + (lane >> 3);
-      const int c = (lane & 7) ^ at_swz(r);
-      const int key = key0 + r;
-      const uint16_t* src =
-          key < T ? p.qkv + (row0 + key) * ld + (int64_t)(p.Hq + which * p.Hkv + hk) * AT_DH + c * 8
-                  : zero;
-      async_copy16_to(src, lds0 + (uint32_t)(stage * 2 * AT_TILE + which * AT_TILE + rb * 1024));
+      const uint16_t* src = csrc[u4] + off;
+      if (!whole && key0 + crow[u4] >= T) src = zero;
+      async_copy16_to(src, cdst[u4] + (uint32_t)(stage * 2 * AT_TILE));
     }
   };
 
@@ -297,22 +309,30 @@ __global__ void __launch_bounds__(AT_NT, 2) attn_fwd_kernel(AttnParams p) {
     const float c = p.scale_log2;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
-      float mx = s[0][nb][0];
+      // The tile's maximum (m[nb] enters the max3 chain: it is equal in the query's 4
+      // lanes).
+      float mx = m[nb];
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
         for (int e = 0; e < 4; ++e) mx = fmaxf(mx, s[kb][nb][e]);
       mx = max_xor16_32(mx);
-      const float mnew = fmaxf(m[nb], mx);
-      const float msub = mnew == -INFINITY ? 0.0f : mnew * c;  // no key seen yet: p = 0
-      // The accumulators are rescaled only when some query's maximum moved (wave-uniform
-      // branch); with m unchanged, msub is the value the earlier tiles' p used.
-      if (__ballot(mnew != m[nb])) {
-        const float alpha = __builtin_amdgcn_exp2f(fmaf(m[nb], c, -msub));
+      // Lazy rescaling: m[nb] is the reference the exponents are taken against, moved
+      // (with the accumulators rescaled by 2^((m_old - m_new) c)) only when some query's
+      // scores would exceed it by more than 2^8 -- or on its first finite score.  p stays
+      // <= 256, well inside the 16-bit and fp32 ranges, and the output is the same ratio
+      // sum p v / sum p whatever the reference; the wave-uniform branch is rarely taken
+      // once the first tiles have set the scale.
+      const bool move = m[nb] == -INFINITY ? mx != -INFINITY : (mx - m[nb]) * c > 8.0f;
+      if (__ballot(move)) {
+        const float mnew = move ? mx : m[nb];
+        const float alpha = m[nb] == -INFINITY ? 0.0f
+                                               : __builtin_amdgcn_exp2f((m[nb] - mnew) * c);
 #pragma unroll
         for (int db = 0; db < 5; ++db) o[db][nb] *= alpha;
+        m[nb] = mnew;
       }
-      m[nb] = mnew;
+      const float msub = m[nb] == -INFINITY ? 0.0f : m[nb] * c;  // no key seen yet: p = 0
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
