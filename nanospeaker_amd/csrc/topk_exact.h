@@ -52,14 +52,18 @@ struct RegRow {
   // Value selects only: `c ? k0 : k1` on the members would be an lvalue (a select of
   // member addresses), which keeps the struct in memory -- the compiler then places it
   // in LDS, and every access becomes an LDS round trip.
-  // i is wave-uniform, so the half it lies in is a scalar branch: one readlane per field.
+  // i is wave-uniform: both halves are read at lane i % 64 and a scalar select keeps the
+  // one i lies in (no branch between the dependent scalar steps).
   __device__ __forceinline__ KV get(int i) const {
-    if (i < 64) return KV{(uint32_t)rl(k0, i), rl(i0, i)};
-    return KV{(uint32_t)rl(k1, i - 64), rl(i1, i - 64)};
+    const int l = i & 63;
+    const uint32_t ka = (uint32_t)rl(k0, l), kb = (uint32_t)rl(k1, l);
+    const int ia = rl(i0, l), ib = rl(i1, l);
+    return i < 64 ? KV{ka, ia} : KV{kb, ib};
   }
   __device__ __forceinline__ uint32_t key(int i) const {
-    if (i < 64) return (uint32_t)rl(k0, i);
-    return (uint32_t)rl(k1, i - 64);
+    const int l = i & 63;
+    const uint32_t ka = (uint32_t)rl(k0, l), kb = (uint32_t)rl(k1, l);
+    return i < 64 ? ka : kb;
   }
   // Both halves are written through selects (lane -1 matches no lane), so the compiler
   // keeps the four registers as registers instead of an indexed private array.
@@ -244,7 +248,24 @@ __device__ __forceinline__ void sort_d(RegRow& a, int n) {
 }
 
 // ---- the same steps, wave-parallel ---------------------------------------------------
-//
+
+// Bits [a, b) of one 64-position half (a and b clamped to [0, 64]).
+__device__ __forceinline__ uint64_t span_mask(int a, int b) {
+  a = a < 0 ? 0 : (a > 64 ? 64 : a);
+  b = b < a ? a : (b > 64 ? 64 : b);
+  const uint64_t below_b = b >= 64 ? ~0ull : ((1ull << b) - 1ull);
+  const uint64_t below_a = a >= 64 ? ~0ull : ((1ull << a) - 1ull);
+  return below_b & ~below_a;
+}
+
+// Set bits of the wave-uniform mask m in the lanes below this one.
+__device__ __forceinline__ int mbcnt64(uint64_t m) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                        __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+__device__ __forceinline__ int ff1_64(uint64_t m) { return __builtin_ctzll(m); }
+
 // Unguarded Hoare partition of [first, last) around pivot a[first] (key pk, which the
 // caller already holds), computed from ranks.
 // On the array as move_median_to_first left it, let L be the ascending positions in
@@ -257,23 +278,29 @@ __device__ __forceinline__ void sort_d(RegRow& a, int n) {
 // L[i] < R[i] <=> more than i right stoppers lie above L[i]: each lane tests its own
 // positions with ballots.  The swaps go through LDS: the element at L[i] (i < i*) is
 // written to slot i and the one at R[i] to slot 128 + i; then L[i] reads slot 128 + i
-// and R[i] reads slot i.  `kv` is the wave's [256] LDS scratch of (key, id) pairs.
+// and R[i] reads slot i.  `kv` is the wave's [256] LDS scratch of (key, id) pairs.  The
+// stopper sets are wave masks (one compare per half, the position range a scalar mask)
+// and the ranks their bit counts below each lane (v_mbcnt).
 __device__ __forceinline__ int partition_parallel(RegRow& a, int first, int last, int2* kv,
                                                   uint32_t pk) {
   const int lane = a.lane;
-  const int p0 = lane, p1 = lane + 64;
   const uint32_t x0 = (uint32_t)a.k0, x1 = (uint32_t)a.k1;
-  const bool isL0 = p0 > first && p0 < last && !gt(x0, pk);
-  const bool isL1 = p1 > first && p1 < last && !gt(x1, pk);
-  const bool isR0 = p0 >= first && p0 < last && !gt(pk, x0);
-  const bool isR1 = p1 >= first && p1 < last && !gt(pk, x1);
-  const uint64_t bl0 = __ballot(isL0), bl1 = __ballot(isL1);
-  const uint64_t br0 = __ballot(isR0), br1 = __ballot(isR1);
-  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-  const uint64_t above = lane == 63 ? 0ull : (~0ull << (lane + 1));
-  const int rl0 = __popcll(bl0 & below), rl1 = __popcll(bl0) + __popcll(bl1 & below);
-  const int ar0 = __popcll(br0 & above) + __popcll(br1), ar1 = __popcll(br1 & above);
-  const int istar = __popcll(__ballot(isL0 && ar0 > rl0)) + __popcll(__ballot(isL1 && ar1 > rl1));
+  // Stopper sets as wave masks: one compare per half, the position ranges as scalar masks.
+  const uint64_t bl0 = __builtin_amdgcn_ballot_w64(x0 <= pk) & span_mask(first + 1, last);
+  const uint64_t bl1 = __builtin_amdgcn_ballot_w64(x1 <= pk) & span_mask(first - 63, last - 64);
+  const uint64_t br0 = __builtin_amdgcn_ballot_w64(x0 >= pk) & span_mask(first, last);
+  const uint64_t br1 = __builtin_amdgcn_ballot_w64(x1 >= pk) & span_mask(first - 64, last - 64);
+  const int nl0 = __builtin_popcountll(bl0);
+  const int nr0 = __builtin_popcountll(br0), nr1 = __builtin_popcountll(br1);
+  const bool isL0 = (bl0 >> lane) & 1ull, isL1 = (bl1 >> lane) & 1ull;
+  const bool isR0 = (br0 >> lane) & 1ull, isR1 = (br1 >> lane) & 1ull;
+  // rl: an L stopper's rank from the left; ar: the right stoppers strictly above the
+  // position (an R stopper's rank from the right).
+  const int rl0 = mbcnt64(bl0), rl1 = nl0 + mbcnt64(bl1);
+  const int ar1 = nr1 - mbcnt64(br1) - (isR1 ? 1 : 0);
+  const int ar0 = nr0 - mbcnt64(br0) - (isR0 ? 1 : 0) + nr1;
+  const int istar = __builtin_popcountll(bl0 & __builtin_amdgcn_ballot_w64(ar0 > rl0)) +
+                    __builtin_popcountll(bl1 & __builtin_amdgcn_ballot_w64(ar1 > rl1));
   const bool sl0 = isL0 && rl0 < istar, sl1 = isL1 && rl1 < istar;
   const bool sr0 = isR0 && ar0 < istar, sr1 = isR1 && ar1 < istar;
   if (sl0) kv[rl0] = make_int2(a.k0, a.i0);
@@ -297,11 +324,13 @@ __device__ __forceinline__ int partition_parallel(RegRow& a, int first, int last
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  if (istar == 0) return bl0 ? __ffsll((long long)bl0) - 1 : 63 + __ffsll((long long)bl1);
-  const uint64_t n0 = __ballot(isL0 && rl0 == istar), n1 = __ballot(isL1 && rl1 == istar);
-  const uint64_t m0 = __ballot(isR0 && ar0 == istar - 1), m1 = __ballot(isR1 && ar1 == istar - 1);
-  const int lnext = n0 ? __ffsll((long long)n0) - 1 : n1 ? 63 + __ffsll((long long)n1) : 1 << 20;
-  const int rprev = m0 ? __ffsll((long long)m0) - 1 : 63 + __ffsll((long long)m1);
+  if (istar == 0) return bl0 ? ff1_64(bl0) : (bl1 ? 64 + ff1_64(bl1) : 63);
+  const uint64_t n0 = bl0 & __builtin_amdgcn_ballot_w64(rl0 == istar);
+  const uint64_t n1 = bl1 & __builtin_amdgcn_ballot_w64(rl1 == istar);
+  const uint64_t m0 = br0 & __builtin_amdgcn_ballot_w64(ar0 == istar - 1);
+  const uint64_t m1 = br1 & __builtin_amdgcn_ballot_w64(ar1 == istar - 1);
+  const int lnext = n0 ? ff1_64(n0) : n1 ? 64 + ff1_64(n1) : 1 << 20;
+  const int rprev = m0 ? ff1_64(m0) : (m1 ? 64 + ff1_64(m1) : 63);
   return lnext < rprev ? lnext : rprev;
 }
 
