@@ -58,7 +58,7 @@ route_fwd_kernel(const void* __restrict__ logits, int64_t T, int E, int k, int f
                  typename Elem<DT>::T* __restrict__ topk_w, int64_t* __restrict__ topk_idx,
                  float* __restrict__ probs, float* __restrict__ prob_colsum) {
   __shared__ float s_col[RF_WAVES][ROUTE_MAX_EXPERTS];
-  __shared__ int2 s_pos[RF_WAVES][2 * ROUTE_MAX_EXPERTS];  // exact path: swap slots
+  __shared__ int2 s_pos[RF_WAVES][TOPK_SWAP_SLOTS];  // exact path: swap slots
   using OutT = typename Elem<DT>::T;
   // readfirstlane: the compiler then knows the wave index, and every row condition
   // below, is wave-uniform (scalar branches, not exec masks).

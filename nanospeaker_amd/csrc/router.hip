@@ -89,7 +89,7 @@ __global__ void __launch_bounds__(RT_THREADS) router_fwd_kernel(RouterArgs a) {
   // last row's padding columns [E, NC) read past its end (their logits are dropped).
   constexpr int WR_BYTES = RT_MAX_STEPS * 32 * RT_MAX_E * 2 + 64;
   constexpr int LGP = NC + 1;               // logit-tile pitch (floats)
-  constexpr int POS = RT_WAVES * 256 * (int)sizeof(int2);
+  constexpr int POS = RT_WAVES * TOPK_SWAP_SLOTS * (int)sizeof(int2);
   constexpr int STAGE = WR_BYTES > POS ? WR_BYTES : POS;
   // W_r during the GEMM; the exact pass's swap slots afterwards.
   __shared__ __align__(1024) char s_stage[STAGE];
@@ -358,7 +358,7 @@ __global__ void __launch_bounds__(RT_THREADS) router_fwd_kernel(RouterArgs a) {
   // The keys come from LDS as the selection saw them; the stage holds the partitions'
   // swap slots now.
   const int nt = s_ntie;
-  int2* pos = (int2*)s_stage + wave * 256;
+  int2* pos = (int2*)s_stage + wave * TOPK_SWAP_SLOTS;
   const bool has0 = lane < E, has1 = lane + 64 < E;
   for (int q = wave; q < nt; q += RT_WAVES) {  // uniform
     const int rt = s_tie[q];

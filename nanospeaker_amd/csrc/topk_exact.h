@@ -18,6 +18,9 @@
 
 namespace nsmoe {
 
+// (key, id) swap slots a wave's partitions need in LDS (partition_parallel).
+constexpr int TOPK_SWAP_SLOTS = 128;
+
 // ---- the row in registers --------------------------------------------------------------
 
 // The exact path compares keys as order-preserving unsigned integers: x ranks before y
@@ -277,10 +280,11 @@ __device__ __forceinline__ int ff1_64(uint64_t m) { return __builtin_ctzll(m); }
 // swaps, all disjoint, and returns min(L[i*], R[i*-1]) (L[0] when i* = 0).
 // L[i] < R[i] <=> more than i right stoppers lie above L[i]: each lane tests its own
 // positions with ballots.  The swaps go through LDS: the element at L[i] (i < i*) is
-// written to slot i and the one at R[i] to slot 128 + i; then L[i] reads slot 128 + i
-// and R[i] reads slot i.  `kv` is the wave's [256] LDS scratch of (key, id) pairs.  The
-// stopper sets are wave masks (one compare per half, the position range a scalar mask)
-// and the ranks their bit counts below each lane (v_mbcnt).
+// written to slot i and the one at R[i] to slot 64 + i; then L[i] reads slot 64 + i and
+// R[i] reads slot i.  The 2 i* swapped positions are distinct, so i* <= n / 2 <= 64 and
+// `kv`, the wave's LDS scratch of (key, id) pairs, needs TOPK_SWAP_SLOTS = 128 of them.
+// The stopper sets are wave masks (one compare per half, the position range a scalar
+// mask) and the ranks their bit counts below each lane (v_mbcnt).
 __device__ __forceinline__ int partition_parallel(RegRow& a, int first, int last, int2* kv,
                                                   uint32_t pk) {
   const int lane = a.lane;
@@ -305,18 +309,18 @@ __device__ __forceinline__ int partition_parallel(RegRow& a, int first, int last
   const bool sr0 = isR0 && ar0 < istar, sr1 = isR1 && ar1 < istar;
   if (sl0) kv[rl0] = make_int2(a.k0, a.i0);
   if (sl1) kv[rl1] = make_int2(a.k1, a.i1);
-  if (sr0) kv[128 + ar0] = make_int2(a.k0, a.i0);
-  if (sr1) kv[128 + ar1] = make_int2(a.k1, a.i1);
+  if (sr0) kv[64 + ar0] = make_int2(a.k0, a.i0);
+  if (sr1) kv[64 + ar1] = make_int2(a.k1, a.i1);
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   if (sl0 || sr0) {
-    const int2 v = kv[sl0 ? 128 + rl0 : ar0];
+    const int2 v = kv[sl0 ? 64 + rl0 : ar0];
     a.k0 = v.x;
     a.i0 = v.y;
   }
   if (sl1 || sr1) {
-    const int2 v = kv[sl1 ? 128 + rl1 : ar1];
+    const int2 v = kv[sl1 ? 64 + rl1 : ar1];
     a.k1 = v.x;
     a.i1 = v.y;
   }
