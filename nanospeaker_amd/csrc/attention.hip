@@ -109,20 +109,44 @@ __device__ __forceinline__ void norm_rope_row(u32x4& lo, u32x4& hi, int j, int p
   const float4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
   const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
   const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-  auto rd = [](float v) { return Elem<DT>::to_f(Elem<DT>::from_f(v)); };
-  float o1[8], o2[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float x1 = rd(a[e] * rstd * unpack2<DT>(ga[e >> 1], e & 1));
-    const float x2 = rd(b[e] * rstd * unpack2<DT>(gb[e >> 1], e & 1));
-    const float c = rd(cs[e]), s = rd(sn[e]);
-    o1[e] = rd(rd(x1 * c) - rd(x2 * s));
-    o2[e] = rd(rd(x2 * c) + rd(x1 * s));
-  }
+  // Every rounding to the dtype: bf16 goes two values at a time through the hardware's
+  // packed round-to-nearest-even conversion (pack2) and back (the scalar software rounding
+  // made this prologue a third of a windowed layer's time); fp16 rounds one value per
+  // conversion instruction.  The last rounding of each output is the pack itself.
+  auto rd2 = [](float& x, float& y) {
+    if constexpr (DT == DT_BF16) {
+      const uint32_t u = pack2<DT>(x, y);
+      x = unpack2<DT>(u, 0);
+      y = unpack2<DT>(u, 1);
+    } else {
+      x = Elem<DT>::to_f(Elem<DT>::from_f(x));
+      y = Elem<DT>::to_f(Elem<DT>::from_f(y));
+    }
+  };
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    lo[q] = pack2<DT>(o1[2 * q], o1[2 * q + 1]);
-    hi[q] = pack2<DT>(o2[2 * q], o2[2 * q + 1]);
+    const int e = 2 * q;
+    float x1a = a[e] * rstd * unpack2<DT>(ga[q], 0), x1b = a[e + 1] * rstd * unpack2<DT>(ga[q], 1);
+    float x2a = b[e] * rstd * unpack2<DT>(gb[q], 0), x2b = b[e + 1] * rstd * unpack2<DT>(gb[q], 1);
+    float ca = cs[e], cb = cs[e + 1], sa = sn[e], sb = sn[e + 1];
+    rd2(x1a, x1b);
+    rd2(x2a, x2b);
+    rd2(ca, cb);
+    rd2(sa, sb);
+    float p1a = x1a * ca, p1b = x1b * cb, p2a = x2a * sa, p2b = x2b * sb;  // x1 c, x2 s
+    float p3a = x2a * ca, p3b = x2b * cb, p4a = x1a * sa, p4b = x1b * sb;  // x2 c, x1 s
+    rd2(p1a, p1b);
+    rd2(p2a, p2b);
+    rd2(p3a, p3b);
+    rd2(p4a, p4b);
+    const float d1a = p1a - p2a, d1b = p1b - p2b, d2a = p3a + p4a, d2b = p3b + p4b;
+    if constexpr (DT == DT_BF16) {
+      lo[q] = pack2<DT>(d1a, d1b);
+      hi[q] = pack2<DT>(d2a, d2b);
+    } else {
+      lo[q] = (uint32_t)Elem<DT>::from_f(d1a) | ((uint32_t)Elem<DT>::from_f(d1b) << 16);
+      hi[q] = (uint32_t)Elem<DT>::from_f(d2a) | ((uint32_t)Elem<DT>::from_f(d2b) << 16);
+    }
   }
 }
 
