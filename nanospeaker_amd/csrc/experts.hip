@@ -219,9 +219,10 @@ combine_kernel(const typename Elem<DT>::T* __restrict__ rows, const int32_t* __r
     u32x4 rv = *(const u32x4*)(resid + off);
     TT r[G::VE];
     __builtin_memcpy(r, &rv, 16);
+    float sum[G::VE];
 #pragma unroll
-    for (int e = 0; e < G::VE; ++e)
-      o[e] = Elem<DT>::from_f(Elem<DT>::to_f(r[e]) + Elem<DT>::to_f(o[e]));
+    for (int e = 0; e < G::VE; ++e) sum[e] = Elem<DT>::to_f(r[e]) + Elem<DT>::to_f(o[e]);
+    round_to<DT>(sum, o);
   };
   if (fast && k <= COMBINE_KMAX && S <= COMBINE_SMAX && ntok * (d / G::VE) < INT32_MAX) {
     // Every slot index is loaded first, then every row chunk: all of a thread's loads
@@ -256,8 +257,7 @@ combine_kernel(const typename Elem<DT>::T* __restrict__ rows, const int32_t* __r
         for (int e = 0; e < G::VE; ++e) acc[e] += Elem<DT>::to_f(tmp[e]);
       }
       TT o[G::VE];
-#pragma unroll
-      for (int e = 0; e < G::VE; ++e) o[e] = Elem<DT>::from_f(acc[e]);
+      round_to<DT>(acc, o);
       plus_resid(o, (int64_t)t * d + c);
       u32x4 ov;
       __builtin_memcpy(&ov, o, 16);
@@ -289,8 +289,7 @@ combine_kernel(const typename Elem<DT>::T* __restrict__ rows, const int32_t* __r
         for (int e = 0; e < G::VE; ++e) acc[e] += Elem<DT>::to_f(tmp[e]);
       }
       TT o[G::VE];
-#pragma unroll
-      for (int e = 0; e < G::VE; ++e) o[e] = Elem<DT>::from_f(acc[e]);
+      round_to<DT>(acc, o);
       plus_resid(o, t * d + c);
       u32x4 ov;
       __builtin_memcpy(&ov, o, 16);

@@ -190,6 +190,23 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
   return u;
 }
 
+// N fp32 values rounded to DT: bf16 two at a time through the packed hardware conversion
+// (round-to-nearest-even, as f_to_bf16, on every value but NaN, which stays a NaN), the
+// other types one at a time.
+template <int DT, int N>
+__device__ __forceinline__ void round_to(const float (&v)[N], typename Elem<DT>::T (&o)[N]) {
+  if constexpr (DT == DT_BF16 && N % 2 == 0) {
+#pragma unroll
+    for (int q = 0; q < N / 2; ++q) {
+      const uint32_t u = pack2<DT>(v[2 * q], v[2 * q + 1]);
+      __builtin_memcpy(&o[2 * q], &u, 4);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < N; ++e) o[e] = Elem<DT>::from_f(v[e]);
+  }
+}
+
 // Element e (0 or 1) of a dword holding two 16-bit elements, as fp32.
 template <int DT>
 __device__ __forceinline__ float unpack2(uint32_t u, int e) {
