@@ -336,6 +336,7 @@ class Decoder(nn.Module):
         it)."""
         x = self.embed(idx)
         aux = torch.zeros((), dtype=torch.float32, device=x.device)
+        zeros16 = []
         # The residual stream is the trunk's own: the embedding's output, then each block's
         # fresh output, so the attention's residual add may accumulate in place.
         for blk in self.blocks:
@@ -345,10 +346,18 @@ class Decoder(nn.Module):
                 x = blk.attn.forward_residual(x, blk.norm_attn(x), inplace=True)
                 x = ffn_hook(blk, x)
                 a = blk.ffn.aux_loss
-            # The same fp32 sum as aux + a under type promotion (a widened exactly): a
-            # 16-bit loss (the block's zero in eval) is widened first, because torch's
-            # mixed-dtype add kernel takes ~45 us for a 0-dim tensor on this stack.
-            aux = aux + (a if a.dtype == aux.dtype else a.float())
+            # The fp32 sum aux + a of the reference's trunk, a widened exactly (torch's
+            # mixed-dtype add takes ~45 us for a 0-dim tensor on this stack).  A block
+            # that computed no balance loss (eval, or a zero coefficient) returns a zero of
+            # its dtype: those are summed once at the end, in one widening reduction,
+            # instead of a conversion and an add per layer; a sum of zeros is zero in any
+            # order.
+            if not blk.ffn.router.wants_probs() and a.dtype != aux.dtype:
+                zeros16.append(a)
+            else:
+                aux = aux + (a if a.dtype == aux.dtype else a.float())
+        if zeros16:
+            aux = aux + torch.stack(zeros16).sum(dtype=torch.float32)
         return self.norm_out(x), aux
 
     def forward(self, idx: torch.Tensor, targets: "torch.Tensor | None" = None,
