@@ -291,7 +291,9 @@ int nsmoe_experts_bwd(const nsmoe_experts_args* args, const int32_t* inv,
  * (MoEBlock keeps both after the step), written by the forward and read by the backward.
  *
  * Forward: out [T, d]; aux [1] fp32 = the balance loss (train branch, route_flags has
- * NSMOE_ROUTE_PROBS; otherwise untouched).  Backward: grads as nsmoe_experts_bwd
+ * NSMOE_ROUTE_PROBS).  In the eval branch a non-NULL aux receives four zero bytes (the
+ * branch's zero loss in any dtype up to 4 bytes wide, written by the dispatch's launch so
+ * the caller needs no fill of its own); NULL leaves it to the caller.  Backward: grads as nsmoe_experts_bwd
  * (dtopk_w is ignored: the gate gradient goes straight into the router backward);
  * grad_aux (device fp32 scalar) may be NULL.  `logits` is needed again by the backward in
  * the eval branch.

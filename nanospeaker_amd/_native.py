@@ -15,7 +15,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libnsmoe.so"
 BF16, F16, F32 = 0, 1, 2
 ROUTE_PROBS, ROUTE_NORMALIZE, ROUTE_LOGITS16 = 1, 2, 4
 BLOCK_PACK, BLOCK_SAVE_ACT, BLOCK_NORM = 8, 16, 32
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 # Every symbol include/nsmoe.h declares, with (restype, argtypes).
 _vp, _i32, _i64, _sz = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t

@@ -215,7 +215,8 @@ extern "C" int nsmoe_block_fwd(const nsmoe_experts_args* a, const nsmoe_block_no
       rc = dispatch_place_launch(topk_idx, m, E, r.hist, router_fused_chunks(T), RT_TOK * k,
                                  (int32_t*)b.sorted_ids, eids, (int32_t*)b.pad_offsets, counts,
                                  npp, inv, probs ? &fold : nullptr, s,
-                                 pack_in_place ? &pk : nullptr, a->dtype);
+                                 pack_in_place ? &pk : nullptr, a->dtype,
+                                 probs ? nullptr : aux);
   } else {
     // In training the route kernel also leaves the balance loss's per-workgroup column
     // sums of probs in the workspace, so probs is not read back for the loss.
@@ -228,7 +229,7 @@ extern "C" int nsmoe_block_fwd(const nsmoe_experts_args* a, const nsmoe_block_no
     if (rc == NSMOE_OK)
       rc = dispatch_launch(topk_idx, m, E, (int32_t*)b.sorted_ids, eids,
                            (int32_t*)b.pad_offsets, counts, npp, inv, ws, dsp,
-                           probs ? &fold : nullptr, s);
+                           probs ? &fold : nullptr, s, probs ? nullptr : aux);
   }
   const int jrc = side_join(s, s_pack, kSideSlotPack);  // joined on every path
   NSMOE_TRY(rc);

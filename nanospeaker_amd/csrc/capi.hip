@@ -225,7 +225,7 @@ extern "C" uint64_t nsmoe_launch_count(void) {
   return nsmoe::g_launches.load(std::memory_order_relaxed);
 }
 
-extern "C" int32_t nsmoe_abi_version(void) { return 7; }
+extern "C" int32_t nsmoe_abi_version(void) { return 8; }
 
 extern "C" int nsmoe_set_option(const char* name, int64_t value) {
   const int i = nsmoe::option_index(name);

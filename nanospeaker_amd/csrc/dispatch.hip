@@ -76,6 +76,7 @@ struct PlaceParams {
   int64_t bal_nblk, bal_T;
   float bal_coef;
   float* bal_aux;
+  float* zero_out;  // or NULL: 4 bytes the launch sets to zero (the eval branch's loss)
 };
 
 struct PlaceLds {
@@ -113,6 +114,7 @@ __device__ __forceinline__ void place_body(const PlaceParams& P, int64_t chunk, 
   int32_t* s_wave = Ls.wave;
   const int tid = threadIdx.x, nt = blockDim.x;
   const int lane = tid & 63, wave = tid >> 6, waves = nt >> 6;
+  if (chunk == 0 && tid == 0 && P.zero_out) *P.zero_out = 0.0f;
 
   // This workgroup's pairs (the loads go out first) and the rank masks.  A workgroup
   // places chunk_pairs <= blockDim.x pairs, one per thread from thread 0: hist_group
@@ -307,7 +309,8 @@ namespace nsmoe {
 int dispatch_launch(const int64_t* topk_idx, int64_t n_pairs, int32_t n_experts,
                     int32_t* sorted_ids, int32_t* expert_ids, int32_t* pad_offsets,
                     int32_t* counts, int32_t* n_post_pad, int32_t* inv, void* workspace,
-                    size_t workspace_bytes, const BalanceArgs* bal, void* stream) {
+                    size_t workspace_bytes, const BalanceArgs* bal, void* stream,
+                    float* zero_out) {
   NSMOE_REQUIRE(n_pairs >= 0 && n_pairs < (int64_t)INT32_MAX / 2,
                 "dispatch: n_pairs %lld out of range", (long long)n_pairs);
   NSMOE_REQUIRE(n_experts >= 1 && n_experts <= DISPATCH_MAX_EXPERTS,
@@ -321,6 +324,7 @@ int dispatch_launch(const int64_t* topk_idx, int64_t n_pairs, int32_t n_experts,
     NSMOE_TRY(fill_i32(pad_offsets, n_experts + 1, 0, s));
     NSMOE_TRY(fill_i32(counts, n_experts, 0, s));
     NSMOE_TRY(fill_i32(n_post_pad, 1, 0, s));
+    if (zero_out) NSMOE_TRY(fill_i32((int32_t*)zero_out, 1, 0, s));
     return bal ? balance_final_launch(bal->partial, bal->T, n_experts, counts, bal->coef,
                                       bal->aux, s)
                : NSMOE_OK;
@@ -350,7 +354,7 @@ int dispatch_launch(const int64_t* topk_idx, int64_t n_pairs, int32_t n_experts,
   const PlaceParams P{topk_idx, n_pairs, n_experts, hist, n_chunks, 1, chunk, l_cap,
                       sorted_ids, expert_ids, pad_offsets, counts, n_post_pad, inv,
                       fold ? bal->partial : nullptr, fold ? bal->nblk : 0, fold ? bal->T : 1,
-                      fold ? bal->coef : 0.0f, fold ? bal->aux : nullptr};
+                      fold ? bal->coef : 0.0f, fold ? bal->aux : nullptr, zero_out};
   dispatch_place_kernel<<<(unsigned)(n_chunks + (fold ? 1 : 0)), chunk,
                           (chunk / 64) * n_experts * sizeof(unsigned long long), s>>>(P);
   timer.stop();
@@ -365,7 +369,7 @@ int dispatch_place_launch(const int64_t* topk_idx, int64_t n_pairs, int32_t n_ex
                           int32_t* sorted_ids, int32_t* expert_ids, int32_t* pad_offsets,
                           int32_t* counts, int32_t* n_post_pad, int32_t* inv,
                           const BalanceArgs* bal, hipStream_t s, const PackPairArgs* pack,
-                          int pack_dtype) {
+                          int pack_dtype, float* zero_out) {
   NSMOE_REQUIRE(n_pairs > 0 && n_pairs < (int64_t)INT32_MAX / 2,
                 "dispatch_place: n_pairs %lld out of range", (long long)n_pairs);
   NSMOE_REQUIRE(n_experts >= 1 && n_experts <= 128 && chunk_pairs >= 1 &&
@@ -383,7 +387,8 @@ int dispatch_place_launch(const int64_t* topk_idx, int64_t n_pairs, int32_t n_ex
   const PlaceParams P{topk_idx, n_pairs, n_experts, hist, n_chunks, group,
                       group * chunk_pairs, l_cap, sorted_ids, expert_ids, pad_offsets, counts,
                       n_post_pad, inv, fold ? bal->partial : nullptr, fold ? bal->nblk : 0,
-                      fold ? bal->T : 1, fold ? bal->coef : 0.0f, fold ? bal->aux : nullptr};
+                      fold ? bal->T : 1, fold ? bal->coef : 0.0f, fold ? bal->aux : nullptr,
+                      zero_out};
   const int np = (int)(n_place + (fold ? 1 : 0));
   if (pack && (pack_dtype == DT_BF16 || pack_dtype == DT_F16)) {
     // Packing workgroups: as many as are resident beside the placing ones (the kernel's

@@ -132,7 +132,8 @@ struct BalanceArgs {
 int dispatch_launch(const int64_t* topk_idx, int64_t n_pairs, int32_t n_experts,
                     int32_t* sorted_ids, int32_t* expert_ids, int32_t* pad_offsets,
                     int32_t* counts, int32_t* n_post_pad, int32_t* inv, void* workspace,
-                    size_t workspace_bytes, const BalanceArgs* bal, void* stream);
+                    size_t workspace_bytes, const BalanceArgs* bal, void* stream,
+                    float* zero_out = nullptr);
 // The place pass of the dispatch from per-chunk histograms [n_chunks, E] made elsewhere
 // (chunk c = pairs [c chunk_pairs, (c + 1) chunk_pairs)); E <= 128, chunk_pairs <= 1024.
 struct PackPairArgs;
@@ -143,7 +144,8 @@ int dispatch_place_launch(const int64_t* topk_idx, int64_t n_pairs, int32_t n_ex
                           int32_t* sorted_ids, int32_t* expert_ids, int32_t* pad_offsets,
                           int32_t* counts, int32_t* n_post_pad, int32_t* inv,
                           const BalanceArgs* bal, hipStream_t stream,
-                          const PackPairArgs* pack = nullptr, int pack_dtype = 0);
+                          const PackPairArgs* pack = nullptr, int pack_dtype = 0,
+                          float* zero_out = nullptr);
 int balance_final_launch(const float* partial, int64_t n_tokens, int32_t n_experts,
                          const int32_t* counts, float coef, float* aux, hipStream_t stream);
 }  // namespace nsmoe

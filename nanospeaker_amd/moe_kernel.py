@@ -931,8 +931,14 @@ def _block_fwd_impl(x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in
     out = torch.empty((n, d), dtype=dt, device=dev)
     counts = torch.empty(e, dtype=torch.int32, device=dev)
     topk_idx = torch.empty((n, top_k), dtype=torch.int64, device=dev)
-    aux = (torch.empty((), dtype=torch.float32, device=dev) if want_probs
-           else torch.zeros((), dtype=dt, device=dev))
+    # The eval branch's loss is a zero of the dtype, written by the library's dispatch
+    # launch into the 4 bytes under it (no fill kernel of its own).
+    if want_probs:
+        aux_buf = torch.empty((), dtype=torch.float32, device=dev)
+        aux = aux_buf
+    else:
+        aux_buf = torch.empty(4 // dt.itemsize, dtype=dt, device=dev)
+        aux = aux_buf[0]
     a = plan.bind(x, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in, b_sh_out)
     if n:
         p_in, p_out, pending = PACKS.lookup(plan.pack_bytes, dev, w_in, w_out, w_sh_in,
@@ -947,15 +953,14 @@ def _block_fwd_impl(x, W_r, w_in, w_out, w_sh_in, w_sh_out, b_in, b_out, b_sh_in
             a, nrm, W_r.data_ptr() if plan.fuse_route else None, _p(bias), logits.data_ptr(),
             flags | (nat.BLOCK_PACK if pending is not None else 0), aux_coef,
             saved.data_ptr(), topk_idx.data_ptr(), counts.data_ptr(), out.data_ptr(),
-            aux.data_ptr() if want_probs else None, ws.data_ptr(), plan.fwd_ws, _stream()),
+            aux_buf.data_ptr(), ws.data_ptr(), plan.fwd_ws, _stream()),
             "nsmoe_block_fwd")
         if pending is not None:
             PACKS.store(pending, p_in, p_out)
     else:
         p_in = torch.empty(plan.pack_bytes[0], dtype=torch.uint8, device=dev)
         counts.zero_()
-        if want_probs:
-            aux.zero_()
+        aux.zero_()
     return out, aux, counts, topk_idx, logits, saved, p_in
 
 

@@ -110,7 +110,7 @@ def test_rms_norm_rejects_bad_arguments(args, needle):
 
 
 def test_abi_version_and_alignment():
-    assert nat.lib().nsmoe_abi_version() == nat.ABI_VERSION == 7
+    assert nat.lib().nsmoe_abi_version() == nat.ABI_VERSION == 8
     assert nat.lib().nsmoe_align_m() == mk.ALIGN_M
 
 

@@ -22,6 +22,7 @@ dtypes, biases, shared-expert counts and shapes that take the block's other code
 experts).
 """
 
+import math
 from pathlib import Path
 
 import numpy as np
@@ -277,3 +278,22 @@ def test_block_dtype_bias_shared_matrix(dtype, bias, S):
 @pytest.mark.parametrize("train", [True, False])
 def test_block_other_shapes(cfg, train):
     run_case(257, train=train, backward=True, **cfg)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_eval_loss_is_a_zero_the_library_writes(dtype):
+    """In eval the block's loss is a zero of its dtype (moe.py's eval branch); the library's
+    dispatch launch writes it into memory the op leaves uninitialised.  Each call below
+    takes its small buffers from blocks just freed from NaN-filled tensors of the same
+    size class, so a zero that was not written would show."""
+    m, _, x, _ = build(256, dtype=dtype)
+    m = m.to(DEV).eval()
+    x = x.to(DEV)
+    with torch.no_grad():
+        for _ in range(3):
+            junk = [torch.full((128,), float("nan"), device=DEV) for _ in range(16)]
+            del junk
+            m(x)
+            aux = m.aux_loss
+            assert aux.dtype == dtype and aux.shape == ()
+            assert float(aux) == 0.0 and not math.copysign(1.0, float(aux)) < 0
