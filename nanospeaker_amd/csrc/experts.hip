@@ -1052,32 +1052,22 @@ static int experts_dw(const nsmoe_experts_args* a, const ExpParams& p,
   } else {
     {  // dW_in
       const ExpParams& q = q_in;
-      const int rc = launch_dw_async(DT, 0, q, gc, s);
-      if (rc != -1) {
-        NSMOE_TRY(rc);
-      } else {
-        const int64_t ntiles = cdiv(d, 64) * cdiv(2 * H, 128);
-        KernelTimer timer("dw_in", s);
-        dw_kernel<DT, 0><<<(unsigned)(gc * ntiles), NT, 0, s>>>(q);
-        timer.stop();
-        NSMOE_TRY(check_launch("dw_kernel<in>"));
-      }
+      const int64_t ntiles = cdiv(d, 64) * cdiv(2 * H, 128);
+      KernelTimer timer("dw_in", s);
+      dw_kernel<DT, 0><<<(unsigned)(gc * ntiles), NT, 0, s>>>(q);
+      timer.stop();
+      NSMOE_TRY(check_launch("dw_kernel<in>"));
       dim3 rg(dwr_blocks(a), (unsigned)G);
       dw_reduce_kernel<DT, 0><<<rg, NT, 0, s>>>(q);
       NSMOE_TRY(check_launch("dw_reduce_kernel<in>"));
     }
     {  // dW_out
       const ExpParams& q = q_out;
-      const int rc = launch_dw_async(DT, 1, q, gc, s);
-      if (rc != -1) {
-        NSMOE_TRY(rc);
-      } else {
-        const int64_t ntiles = cdiv(H, 128) * cdiv(d, 64);
-        KernelTimer timer("dw_out", s);
-        dw_kernel<DT, 1><<<(unsigned)(gc * ntiles), NT, 0, s>>>(q);
-        timer.stop();
-        NSMOE_TRY(check_launch("dw_kernel<out>"));
-      }
+      const int64_t ntiles = cdiv(H, 128) * cdiv(d, 64);
+      KernelTimer timer("dw_out", s);
+      dw_kernel<DT, 1><<<(unsigned)(gc * ntiles), NT, 0, s>>>(q);
+      timer.stop();
+      NSMOE_TRY(check_launch("dw_kernel<out>"));
       dim3 rg(dwr_blocks(a), (unsigned)G);
       dw_reduce_kernel<DT, 1><<<rg, NT, 0, s>>>(q);
       NSMOE_TRY(check_launch("dw_reduce_kernel<out>"));

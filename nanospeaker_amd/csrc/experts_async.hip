@@ -1943,12 +1943,6 @@ __device__ __forceinline__ int dw_run(const ExpParams& p) {
   return ((Md + Tl::BMT - 1) / Tl::BMT) * ((Nd + Tl::BNT - 1) / Tl::BNT);
 }
 
-template <int DT, int MODE, int S>
-__global__ void __launch_bounds__(NT, 2) dw_async_kernel(ExpParams p) {
-  __shared__ __attribute__((aligned(1024))) DwLds<DT, S> lds;
-  dw_item<DT, MODE, S>(p, xcd_deal(blockIdx.x, gridDim.x, dw_run<MODE>(p)), lds);
-}
-
 // dW_in and dW_out items in one launch: blocks [0, grid_in) take dW_in items, the rest
 // dW_out items (each part dealt over the XCDs on its own; grid_in is a multiple of 8 so
 // that block b - grid_in sits on the same XCD as b).  One launch fills the machine's
@@ -1962,30 +1956,6 @@ __global__ void __launch_bounds__(NT, 2) dw_pair_kernel(ExpParams p_in, ExpParam
   else
     dw_item<DT, 1, S>(p_out, xcd_deal(b - grid_in, (int)gridDim.x - grid_in, dw_run<1>(p_out)),
                       lds);
-}
-
-int launch_dw_async(int dtype, int mode, const ExpParams& q, int64_t groups_chunks,
-                    hipStream_t s) {
-  if (!q.fast || (dtype != DT_BF16 && dtype != DT_F16)) return -1;
-  if (q.T * q.d >= (int64_t(1) << 31)) return -1;  // token offsets are int32
-  const int d = q.d, H = q.H;
-  const int Md = mode == 0 ? d : H, Nd = mode == 0 ? 2 * H : d;
-  const int BMT = mode == 0 ? DwTile<0>::BMT : DwTile<1>::BMT;
-  const int BNT = mode == 0 ? DwTile<0>::BNT : DwTile<1>::BNT;
-  const int64_t ntiles = cdiv(Md, BMT) * cdiv(Nd, BNT);
-  const int64_t grid = groups_chunks * ntiles;
-  if (grid <= 0) return NSMOE_OK;
-  constexpr int S = 3;
-  KernelTimer timer(mode == 0 ? "dw_in" : "dw_out", s);
-  if (dtype == DT_BF16) {
-    if (mode == 0) dw_async_kernel<DT_BF16, 0, S><<<(unsigned)grid, NT, 0, s>>>(q);
-    else dw_async_kernel<DT_BF16, 1, S><<<(unsigned)grid, NT, 0, s>>>(q);
-  } else {
-    if (mode == 0) dw_async_kernel<DT_F16, 0, S><<<(unsigned)grid, NT, 0, s>>>(q);
-    else dw_async_kernel<DT_F16, 1, S><<<(unsigned)grid, NT, 0, s>>>(q);
-  }
-  timer.stop();
-  return check_launch("dw_async_kernel");
 }
 
 int launch_dw_pair_async(int dtype, const ExpParams& q_in, const ExpParams& q_out,

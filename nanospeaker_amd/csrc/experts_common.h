@@ -140,8 +140,6 @@ __device__ __forceinline__ int dw_chunks(int rows) {
 // Async (direct-to-LDS) variants for 16-bit types and d_hidden <= 128; each returns
 // NSMOE_OK after launching, or -1 when the shape is not one they take.
 int launch_fwd_async(int dtype, const ExpParams& p, int nbw, int64_t grid, hipStream_t s);
-// dW of every (group, row chunk, tile): mode 0 dW_in, 1 dW_out (partials as dw_reduce expects).
-int launch_dw_async(int dtype, int mode, const ExpParams& q, int64_t groups_chunks, hipStream_t s);
 // Both dW modes in one launch (q_in: dW_in, q_out: dW_out pointers and partials).
 int launch_dw_pair_async(int dtype, const ExpParams& q_in, const ExpParams& q_out,
                          int64_t groups_chunks, hipStream_t s);
