@@ -1307,6 +1307,7 @@ __device__ __forceinline__ void store_rows_direct(const f32x4 (&acc)[MB][3],
   }
 }
 
+// Launched with 64-row tiles (MB = 4); 96-row tiles take expert_dx_res_kernel.
 template <int DT, int D, int MB>
 __global__ void __launch_bounds__(NT, D > 2 || MB == 6 ? 3 : 2) expert_dx_reg_kernel(ExpParams p) {
   using G = Geo<DT>;
@@ -1626,14 +1627,12 @@ static void bwd_reg_launch(const ExpParams& p, int nbw, int dist, int mb, hipStr
 template <int DT>
 static void dx_reg_launch(const ExpParams& p, int mb, int dist, hipStream_t s) {
   const unsigned g4 = (unsigned)tile_grid(p, 64), g6 = (unsigned)tile_grid(p, 96);
-  if (mb == 6 && 2 * p.H <= 256) {  // the tile's dA1 rows fit the resident 48 KiB
+  // The register-tiled path takes H <= 128, so a 96-row tile's dA1 rows (2H <= 256
+  // columns) always fit the resident 48 KiB.
+  if (mb == 6) {
     if (dist == 4) expert_dx_res_kernel<DT, 4><<<g6, NT, 0, s>>>(p);
     else if (dist == 3) expert_dx_res_kernel<DT, 3><<<g6, NT, 0, s>>>(p);
     else expert_dx_res_kernel<DT, 2><<<g6, NT, 0, s>>>(p);
-  } else if (mb == 6) {
-    if (dist == 4) expert_dx_reg_kernel<DT, 4, 6><<<g6, NT, 0, s>>>(p);
-    else if (dist == 3) expert_dx_reg_kernel<DT, 3, 6><<<g6, NT, 0, s>>>(p);
-    else expert_dx_reg_kernel<DT, 2, 6><<<g6, NT, 0, s>>>(p);
   } else {
     if (dist == 4) expert_dx_reg_kernel<DT, 4, 4><<<g4, NT, 0, s>>>(p);
     else if (dist == 3) expert_dx_reg_kernel<DT, 3, 4><<<g4, NT, 0, s>>>(p);
