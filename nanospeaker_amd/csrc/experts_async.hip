@@ -973,7 +973,7 @@ __global__ void __launch_bounds__(NT, 2) expert_dx_async_kernel(ExpParams p) {
 // Shapes: an even number of k-steps.
 
 template <int DT, int NBW, int D, int MB, bool SA>
-__global__ void __launch_bounds__(NT, SA && MB <= 4 ? 3 : 2) expert_bwd_reg_kernel(ExpParams p) {
+__global__ void __launch_bounds__(NT, SA && MB != 5 ? 3 : 2) expert_bwd_reg_kernel(ExpParams p) {
   using G = Geo<DT>;
   using T = typename G::T;
   using M = Mma<DT>;
@@ -1001,7 +1001,10 @@ __global__ void __launch_bounds__(NT, SA && MB <= 4 ? 3 : 2) expert_bwd_reg_kern
   // copied with the token tiles into an S-stage ring of their own after the token ring.
   constexpr int WB = 4 * NBW * 1024;
   constexpr int WRING = S * WB;
-  constexpr int STAGE_BYTES = TM * (DA_PITCH + HB_PITCH);
+  // The epilogue stages its rows in two passes of MBH row blocks (half the LDS of one pass:
+  // 96-row tiles then fit three workgroups per CU).
+  constexpr int MBH = (MB + 1) / 2;
+  constexpr int STAGE_BYTES = MBH * 16 * (DA_PITCH + HB_PITCH);
   constexpr int LDS_BYTES = RING + WRING > STAGE_BYTES ? RING + WRING : STAGE_BYTES;
   __shared__ __attribute__((aligned(1024))) char s_lds[LDS_BYTES];
   __shared__ int s_tok[TM];
@@ -1010,7 +1013,7 @@ __global__ void __launch_bounds__(NT, SA && MB <= 4 ? 3 : 2) expert_bwd_reg_kern
   __shared__ float s_dtw[5][TM];
   __shared__ int s_loc[3];
   char* s_da = s_lds;                   // epilogue staging, over the ring
-  char* s_hb = s_lds + TM * DA_PITCH;
+  char* s_hb = s_lds + MBH * 16 * DA_PITCH;
   auto ring = [&](int s) __attribute__((always_inline)) { return s_lds + (s % S) * NA * A_BYTES; };
   auto wring = [&](int s) __attribute__((always_inline)) { return s_lds + RING + (s % S) * WB; };
 
@@ -1194,51 +1197,79 @@ __global__ void __launch_bounds__(NT, SA && MB <= 4 ? 3 : 2) expert_bwd_reg_kern
     wrow[i] = s_w[i * 16 + lc];
     part[i] = 0.0f;
   }
+  T* DA = (T*)p.da1 + slot0 * twoH;
+  T* HB = (T*)p.hbuf + slot0 * H;
+  const int da_cpr = twoH / G::VE, hb_cpr = H / G::VE;
   with_act(p.act, [&]<int ACT>() {
 #pragma unroll
-    for (int j = 0; j < NBW; ++j) {
-      const int n0 = (wave * NBW + j) * 16 + lg * 4;
-      if (n0 >= H) continue;  // H % 4 == 0: a group of 4 columns is all in or all out
-      float bg[4] = {0.f, 0.f, 0.f, 0.f}, bu[4] = {0.f, 0.f, 0.f, 0.f};
-      if (bin) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          bg[r] = Elem<DT>::to_f(bin[n0 + r]);
-          bu[r] = Elem<DT>::to_f(bin[H + n0 + r]);
-        }
+    for (int pass = 0; pass < 2; ++pass) {
+      const int ib = pass * MBH, ie = pass ? MB : MBH;  // row blocks [ib, ie) of this pass
+      if (pass) {
+        __syncthreads();  // the first pass's stores have read the staging
       }
 #pragma unroll
-      for (int i = 0; i < MB; ++i) {
-        const int m = i * 16 + lc;
-        const float w = wrow[i];
-        float dg[4], du[4], wh[4];
+      for (int j = 0; j < NBW; ++j) {
+        const int n0 = (wave * NBW + j) * 16 + lg * 4;
+        if (n0 >= H) continue;  // H % 4 == 0: a group of 4 columns is all in or all out
+        float bg[4] = {0.f, 0.f, 0.f, 0.f}, bu[4] = {0.f, 0.f, 0.f, 0.f};
+        if (bin) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float gg, uu;
-          if constexpr (SA) {
-            gg = unpack2<DT>(r < 2 ? a1g[i][j].x : a1g[i][j].y, r & 1);
-            uu = unpack2<DT>(r < 2 ? a1u[i][j].x : a1u[i][j].y, r & 1);
-          } else {
-            gg = accg[i][j][r] + bg[r];
-            uu = accu[i][j][r] + bu[r];
+          for (int r = 0; r < 4; ++r) {
+            bg[r] = Elem<DT>::to_f(bin[n0 + r]);
+            bu[r] = Elem<DT>::to_f(bin[H + n0 + r]);
           }
-          const float Gv = accG[i][j][r];
-          float a, da;
-          act_both_t<ACT>(gg, a, da);
-          const float hv = a * uu;
-          part[i] += Gv * hv;
-          const float dh = w * Gv;
-          dg[r] = dh * uu * da;
-          du[r] = dh * a;
-          wh[r] = w * hv;
         }
-        char* da_row = s_da + m * DA_PITCH;
-        *(uint2*)(da_row + n0 * G::ES) =
-            make_uint2(pack2<DT>(dg[0], dg[1]), pack2<DT>(dg[2], dg[3]));
-        *(uint2*)(da_row + (H + n0) * G::ES) =
-            make_uint2(pack2<DT>(du[0], du[1]), pack2<DT>(du[2], du[3]));
-        *(uint2*)(s_hb + m * HB_PITCH + n0 * G::ES) =
-            make_uint2(pack2<DT>(wh[0], wh[1]), pack2<DT>(wh[2], wh[3]));
+#pragma unroll
+        for (int i = 0; i < MB; ++i) {
+          if (i < ib || i >= ie) continue;  // resolved at compile time once unrolled
+          const int m = (i - ib) * 16 + lc;  // the row's place in the staging
+          const float w = wrow[i];
+          float dg[4], du[4], wh[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float gg, uu;
+            if constexpr (SA) {
+              gg = unpack2<DT>(r < 2 ? a1g[i][j].x : a1g[i][j].y, r & 1);
+              uu = unpack2<DT>(r < 2 ? a1u[i][j].x : a1u[i][j].y, r & 1);
+            } else {
+              gg = accg[i][j][r] + bg[r];
+              uu = accu[i][j][r] + bu[r];
+            }
+            const float Gv = accG[i][j][r];
+            float a, da;
+            act_both_t<ACT>(gg, a, da);
+            const float hv = a * uu;
+            part[i] += Gv * hv;
+            const float dh = w * Gv;
+            dg[r] = dh * uu * da;
+            du[r] = dh * a;
+            wh[r] = w * hv;
+          }
+          char* da_row = s_da + m * DA_PITCH;
+          *(uint2*)(da_row + n0 * G::ES) =
+              make_uint2(pack2<DT>(dg[0], dg[1]), pack2<DT>(dg[2], dg[3]));
+          *(uint2*)(da_row + (H + n0) * G::ES) =
+              make_uint2(pack2<DT>(du[0], du[1]), pack2<DT>(du[2], du[3]));
+          *(uint2*)(s_hb + m * HB_PITCH + n0 * G::ES) =
+              make_uint2(pack2<DT>(wh[0], wh[1]), pack2<DT>(wh[2], wh[3]));
+        }
+      }
+      __syncthreads();
+      // Whole rows out: dA1 rows of 2H elements, w h rows of H elements, 16-byte chunks.
+      const int r0 = ib * 16, nr = (ie - ib) * 16;
+      for (int c = tid; c < nr * da_cpr; c += NT) {
+        const int ml = c / da_cpr, cc = c - ml * da_cpr;
+        if (r0 + ml < rows) {
+          const int col = cc * G::VE;  // the staged row has the final layout: [gate H | up H]
+          *(u32x4*)(DA + (int64_t)(r0 + ml) * twoH + col) =
+              *(const u32x4*)(s_da + ml * DA_PITCH + col * G::ES);
+        }
+      }
+      for (int c = tid; c < nr * hb_cpr; c += NT) {
+        const int ml = c / hb_cpr, cc = c - ml * hb_cpr;
+        if (r0 + ml < rows)
+          *(u32x4*)(HB + (int64_t)(r0 + ml) * H + cc * G::VE) =
+              *(const u32x4*)(s_hb + ml * HB_PITCH + cc * 16);
       }
     }
   });
@@ -1266,22 +1297,6 @@ __global__ void __launch_bounds__(NT, SA && MB <= 4 ? 3 : 2) expert_bwd_reg_kern
     }
   }
   __syncthreads();
-  // Whole rows out: dA1 rows of 2H elements, w h rows of H elements, 16-byte chunks.
-  T* DA = (T*)p.da1 + slot0 * twoH;
-  T* HB = (T*)p.hbuf + slot0 * H;
-  const int da_cpr = twoH / G::VE, hb_cpr = H / G::VE;
-  for (int c = tid; c < TM * da_cpr; c += NT) {
-    const int m = c / da_cpr, cc = c - m * da_cpr;
-    if (m < rows) {
-      const int col = cc * G::VE;  // the staged row has the final layout: [gate H | up H]
-      *(u32x4*)(DA + (int64_t)m * twoH + col) = *(const u32x4*)(s_da + m * DA_PITCH + col * G::ES);
-    }
-  }
-  for (int c = tid; c < TM * hb_cpr; c += NT) {
-    const int m = c / hb_cpr, cc = c - m * hb_cpr;
-    if (m < rows)
-      *(u32x4*)(HB + (int64_t)m * H + cc * G::VE) = *(const u32x4*)(s_hb + m * HB_PITCH + cc * 16);
-  }
   if (g < p.E && tid < rows) {
     const float v = s_dtw[0][tid] + s_dtw[1][tid] + s_dtw[2][tid] + s_dtw[3][tid] + s_dtw[4][tid];
     ((T*)p.dtw)[s_pair[tid]] = Elem<DT>::from_f(v);
@@ -1658,15 +1673,21 @@ int launch_bwd_async(int dtype, const ExpParams& p, int nbw, int64_t grid, int p
       // distance 4 where the step count divides by 4.
       // The tile heights and distances measured fastest at T = 8192 (nanoSpeaker's
       // shape): without the saved pre-activations 48-row tiles at distance 2 once 64-row
-      // tiles overflow two workgroups per CU; with them 64-row tiles at distance 3 (three
-      // workgroups per CU).
-      int mb = !p.a1_in && tile_grid(p, 64) > 2 * (int64_t)device_cus() ? 3 : 4;
+      // tiles overflow two workgroups per CU; with them 96-row tiles at distance 2 once
+      // 64-row tiles overflow three workgroups per CU (the epilogue's two staging passes
+      // let 96-row tiles keep three per CU: at T = 8192 ~760 tiles in one round of the
+      // 768 slots instead of ~1060 over two), else 64-row tiles at distance 3.  96-row
+      // tiles take distance 2 only (a third stage would cost the third workgroup).
+      const int64_t slots3 = 3 * (int64_t)device_cus();
+      int mb = p.a1_in ? (tile_grid(p, 64) > slots3 ? 6 : 4)
+                       : (tile_grid(p, 64) > 2 * (int64_t)device_cus() ? 3 : 4);
       if (const int64_t v = option(OPT_BWD_ROWS)) mb = (int)(v / 16);
       if (mb < 3 || mb > (p.a1_in ? 6 : 5)) mb = 4;
       int dist = mb != 3 && p.in_kb % 3 == 0 ? 3 : 2;
       if (const int64_t v = option(OPT_BWD_DIST))
         if ((v == 2 || v == 3 || (v == 4 && p.a1_in)) && p.in_kb % v == 0) dist = (int)v;
       if (mb >= 5 && !p.a1_in) dist = 2;
+      if (mb == 6) dist = 2;
       KernelTimer timer("expert_bwd", s);
       if (dtype == DT_BF16) bwd_reg_launch<DT_BF16>(p, nbw, dist, mb, s);
       else bwd_reg_launch<DT_F16>(p, nbw, dist, mb, s);
