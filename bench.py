@@ -225,8 +225,8 @@ KERNEL_SYMBOLS = {
     "expert_dx": ("nsmoe::expert_dx_res_kernel", "nsmoe::expert_dx_reg_kernel",
                   "nsmoe::expert_dx_async_kernel"),
     "dw": ("nsmoe::dw_pair_kernel",),
-    "dw_in": ("nsmoe::dw_async_kernel<0, 0", "nsmoe::dw_kernel<0, 0"),
-    "dw_out": ("nsmoe::dw_async_kernel<0, 1", "nsmoe::dw_kernel<0, 1"),
+    "dw_in": ("nsmoe::dw_kernel<0, 0",),
+    "dw_out": ("nsmoe::dw_kernel<0, 1",),
     "route_fwd": ("nsmoe::router_fwd_kernel", "nsmoe::route_fwd_kernel"),
     "combine": ("nsmoe::combine_kernel",),
     "combine_dx": ("nsmoe::combine_dx_kernel",),
