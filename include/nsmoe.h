@@ -72,6 +72,9 @@ int nsmoe_timing_read(const char* kernel_name, double* total_ms, int64_t* launch
  *   "dx_dist"        its prefetch distance: 2, 3 or 4
  *   "xcd_run"        tiles of one group dealt to one XCD in a row: 1 .. 1024
  *   "dw_stages"      LDS ring stages of the dW kernel: 2, 3 or 4 (default 2)
+ *   "router_waves"   waves per workgroup of the fused router: 16 (one workgroup per CU,
+ *                    the router weight copied whole) or 8 (two per CU, the weight in parts);
+ *                    default 8 once the grid has more workgroups than the device has CUs
  * A value that does not fit a shape falls back to the library's choice for that call.
  * nsmoe_set_option returns 1 for an unknown name or a value out of range (0 always
  * restores the default); nsmoe_get_option returns -1 for an unknown name. */

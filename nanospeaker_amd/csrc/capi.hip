@@ -45,12 +45,13 @@ struct OptionSpec {
 static const int64_t kFwdRows[] = {32, 64, 96, 0};
 static const int64_t kBwdRows[] = {48, 64, 80, 96, 0};
 static const int64_t kDxRows[] = {64, 96, 0};
+static const int64_t kRouterWaves[] = {8, 16, 0};
 static const OptionSpec kOptions[OPT_COUNT] = {
     {"side_stream", 1, 1, nullptr},   {"fwd_rows", 0, 0, kFwdRows},
     {"fwd_dist", 2, 6, nullptr},      {"bwd_rows", 0, 0, kBwdRows},
     {"bwd_dist", 2, 4, nullptr},      {"dx_rows", 0, 0, kDxRows},
     {"dx_dist", 2, 4, nullptr},       {"xcd_run", 1, 1024, nullptr},
-    {"dw_stages", 2, 4, nullptr},
+    {"dw_stages", 2, 4, nullptr},     {"router_waves", 0, 0, kRouterWaves},
 };
 static std::atomic<int64_t> g_options[OPT_COUNT];
 

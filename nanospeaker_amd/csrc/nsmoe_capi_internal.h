@@ -58,6 +58,7 @@ enum OptionId : int {
   OPT_DX_DIST,
   OPT_XCD_RUN,
   OPT_DW_STAGES,
+  OPT_ROUTER_WAVES,
   OPT_COUNT
 };
 int64_t option(OptionId id);

@@ -41,11 +41,26 @@
 
 namespace nsmoe {
 
-constexpr int RT_MMA_SPLIT = 5;             // GEMM waves per 16-token tile (one 16-expert block each at E <= 80)
-constexpr int RT_MMA_WAVES = RT_TOK / 16 * RT_MMA_SPLIT;  // waves that run the GEMM
-constexpr int RT_WAVES = 16;                // waves per workgroup (loads, exact pass)
-constexpr int RT_THREADS = RT_WAVES * 64;
 constexpr int RT_SEL_WAVES = RT_TOK / 4;    // waves of the selection: 4 tokens per wave
+constexpr int RT_PART_STEPS = 6;            // k-steps of W_r per part in the 8-wave form
+
+// The two workgroup shapes (W waves, one workgroup of RT_TOK tokens either way):
+//   W = 16: one workgroup per CU; W_r whole in LDS (87.5 KiB at d = 576, E = 76).
+//   W = 8:  two workgroups per CU (under 80 KiB of LDS and 128 registers each), so that
+//           one workgroup's selection and exact pass overlap the other's copies and
+//           GEMM once the grid is more than one workgroup per CU.  W_r arrives in parts
+//           of RT_PART_STEPS k-steps, double-buffered between the stage and the token
+//           rows' area (free once the GEMM waves hold their rows in registers): part
+//           p + 1 is copied while part p's MFMAs run.
+template <int W>
+struct RtShape {
+  static_assert(W == 16 || W == 8, "workgroup shapes");
+  static constexpr int THREADS = W * 64;
+  static constexpr int SPLIT = W == 16 ? 5 : 4;  // GEMM waves per 16-token tile
+  static constexpr int MMA_WAVES = RT_TOK / 16 * SPLIT;
+  static constexpr int WR_STEPS = W == 16 ? RT_MAX_STEPS : RT_PART_STEPS;  // W_r in the stage
+  static constexpr int PER_CU = W == 16 ? 1 : 2;
+};
 
 // 16-lane DPP butterflies: every lane of each row of 16 ends with the row's reduction.
 template <class Op>
@@ -81,13 +96,16 @@ __device__ __forceinline__ int row16_min_i(int v) {
 __device__ __forceinline__ float fmax_(float a, float b) { return fmaxf(a, b); }
 __device__ __forceinline__ float fadd_(float a, float b) { return a + b; }
 
-template <int DT, int NB>
-__global__ void __launch_bounds__(RT_THREADS) router_fwd_kernel(RouterArgs a) {
+template <int DT, int NB, int W>
+__global__ void __launch_bounds__(W * 64, RtShape<W>::PER_CU) router_fwd_kernel(RouterArgs a) {
   using ET = typename Elem<DT>::T;
+  using Sh = RtShape<W>;
+  constexpr int RT_WAVES = W, RT_THREADS = Sh::THREADS;
   constexpr int NC = NB * 16;               // expert columns, padded to whole MFMA blocks
-  // W_r whole in LDS, row-major as in memory ([d, E], E * 2 bytes a row), plus slack: the
-  // last row's padding columns [E, NC) read past its end (their logits are dropped).
-  constexpr int WR_BYTES = RT_MAX_STEPS * 32 * RT_MAX_E * 2 + 64;
+  // W_r in LDS (whole, or one part of it), row-major as in memory ([d, E], E * 2 bytes a
+  // row), plus slack: the last row's padding columns [E, NC) read past its end (their
+  // logits are dropped).
+  constexpr int WR_BYTES = Sh::WR_STEPS * 32 * RT_MAX_E * 2 + 64;
   constexpr int LGP = NC + 1;               // logit-tile pitch (floats)
   constexpr int POS = RT_WAVES * TOPK_SWAP_SLOTS * (int)sizeof(int2);
   constexpr int STAGE = WR_BYTES > POS ? WR_BYTES : POS;
@@ -97,6 +115,7 @@ __global__ void __launch_bounds__(RT_THREADS) router_fwd_kernel(RouterArgs a) {
   // The workgroup's RT_TOK token rows, d * 2 bytes each, one contiguous block of x, copied
   // whole by LDS-DMA (x_slot's chunk order inside each row).
   __shared__ __align__(1024) char s_x[RT_TOK * RT_MAX_STEPS * 64];
+  static_assert(W == 16 || (int)sizeof(s_x) >= WR_BYTES, "a W_r part fits the rows' area");
   __shared__ float s_lg[RT_TOK * LGP];      // per token: the logits, then its keys
   __shared__ float s_bias[RT_MAX_E];
   __shared__ float s_m[RT_TOK], s_inv[RT_TOK];
@@ -111,7 +130,7 @@ __global__ void __launch_bounds__(RT_THREADS) router_fwd_kernel(RouterArgs a) {
   const int d = a.d, E = a.E, k = a.k;
   const bool train = a.flags & 1, normalize = a.flags & 2;
   const int64_t tok0 = (int64_t)blockIdx.x * RT_TOK;
-  const bool mma_wave = wave < RT_MMA_WAVES;  // uniform
+  const bool mma_wave = wave < Sh::MMA_WAVES;  // uniform
   const int nks = d >> 5;
   const char* zero = (const char*)g_zero_kib + lane * 16;
 
@@ -120,14 +139,22 @@ __global__ void __launch_bounds__(RT_THREADS) router_fwd_kernel(RouterArgs a) {
   // instruction spread over all 16 waves, with no registers in flight and no staging
   // pass; d E 2 is a multiple of 256 (d % 32 == 0, E % 4 == 0), so only the last copy of
   // each is partial, its surplus lanes reading the zero page.
-  {
-    const int nw16 = (d * E * 2) >> 4;  // 16-byte chunks of W_r
+  // The 8-wave form copies W_r's chunks [c0, c1) (part p: k-steps 6 p .. 6 p + 5) into a
+  // region that holds them from its start.
+  const int nw16 = (d * E * 2) >> 4;  // 16-byte chunks of W_r
+  const int part16 = (RT_PART_STEPS * 32 * E * 2) >> 4;
+  const int nparts = (nks + RT_PART_STEPS - 1) / RT_PART_STEPS;
+  auto copy_w = [&](int c0, int c1, char* dst) {
     const char* wsrc = (const char*)a.w;
-    for (int i = wave; i * 64 < nw16; i += RT_WAVES) {  // uniform
-      const int c = i * 64 + lane;
-      async_copy16(c < nw16 ? (const void*)(wsrc + c * 16) : (const void*)zero,
-                   s_stage + i * 1024);
+    for (int i = wave; i * 64 < c1 - c0; i += RT_WAVES) {  // uniform
+      const int c = c0 + i * 64 + lane;
+      async_copy16(c < c1 ? (const void*)(wsrc + c * 16) : (const void*)zero,
+                   dst + i * 1024);
     }
+  };
+  {
+    if constexpr (W == 16) copy_w(0, nw16, s_stage);
+    else copy_w(0, min(part16, nw16), s_stage);
     if (a.norm_w) {
       const int nn16 = (d * 2) >> 4;
       const char* nsrc = (const char*)a.norm_w;
@@ -162,8 +189,10 @@ __global__ void __launch_bounds__(RT_THREADS) router_fwd_kernel(RouterArgs a) {
   // A GEMM wave's 16 token rows, whole (d <= 32 RT_MAX_STEPS), read from LDS once the
   // copies have landed.  Lane (g, j) holds row tok + j, elements 32 ks + 8 g .. + 7 (the A
   // operand of k-step ks).
-  constexpr int NBH = (NB + RT_MMA_SPLIT - 1) / RT_MMA_SPLIT;  // column blocks per GEMM wave
-  const int tile = wave / RT_MMA_SPLIT, cb0 = (wave % RT_MMA_SPLIT) * NBH;
+  // A GEMM wave's column blocks: wave % SPLIT + SPLIT nb, nb < NBH.
+  constexpr int NBH = (NB + Sh::SPLIT - 1) / Sh::SPLIT;  // column blocks per GEMM wave
+  const int tile = wave / Sh::SPLIT, cw = wave % Sh::SPLIT;
+  auto cblk = [&](int nb) { return cw + Sh::SPLIT * nb; };
   u32x4 xr[RT_MAX_STEPS];
   f32x4 acc[NBH];
   for (int e = tid; e < 128; e += RT_THREADS) s_hist[e] = 0;
@@ -198,7 +227,7 @@ __global__ void __launch_bounds__(RT_THREADS) router_fwd_kernel(RouterArgs a) {
     const float rstd = 1.0f / sqrtf(ss / (float)d + a.norm_eps);
     const char* wn = s_nw + 16 * g;
     ET* xo = (ET*)a.xn + trow * d + 8 * g;
-    const bool writer = cb0 == 0 && trow < T;  // one of the row's two GEMM waves
+    const bool writer = cw == 0 && trow < T;  // one of the row's GEMM waves
 #pragma unroll
     for (int ks = 0; ks < RT_MAX_STEPS; ++ks) {
       if (ks < nks) {
@@ -215,33 +244,62 @@ __global__ void __launch_bounds__(RT_THREADS) router_fwd_kernel(RouterArgs a) {
     if (writer && g == 0) a.rstd[trow] = rstd;
   }
 
-  // ---- GEMM: 18 k-steps from the resident W_r -------------------------------------------
+  // ---- GEMM: 18 k-steps from W_r in LDS ------------------------------------------------
   // B fragment of k-step ks, column block nb: lane (g, j) reads rows 32 ks + 8 g + 4 h +
-  // j / 4 and columns 16 nb + 4 (j % 4) .. + 3, for h = 0, 1.
+  // j / 4 and columns 16 nb + 4 (j % 4) .. + 3, for h = 0, 1 (ks counted from the first
+  // k-step the region holds).
 #pragma unroll
   for (int nb = 0; nb < NBH; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (mma_wave) {
-    const int EP = E * 2;  // bytes per W_r row
-    const char* sb0 = s_stage + (8 * g + (j >> 2)) * EP + 8 * (j & 3);
+  const int EP = E * 2;  // bytes per W_r row
+  const int lofs = (8 * g + (j >> 2)) * EP + 8 * (j & 3);
+  // k-steps [KS0, KS0 + NKS) of the GEMM from `region`, which holds k-step KS0 first.
+  auto gemm_steps = [&](const char* region, auto ks0_tag, auto nks_tag) {
+    constexpr int KS0 = decltype(ks0_tag)::value, NKS = decltype(nks_tag)::value;
+    if (!mma_wave) return;
 #pragma unroll
-    for (int ks = 0; ks < RT_MAX_STEPS; ++ks) {
+    for (int ks = KS0; ks < KS0 + NKS; ++ks) {
       if (ks < nks) {  // uniform
-        const char* sb = sb0 + ks * 32 * EP;
+        const char* sb = region + lofs + (ks - KS0) * 32 * EP;
 #pragma unroll
         for (int nb = 0; nb < NBH; ++nb) {
-          if (cb0 + nb < NB) {  // uniform
-            const uint2 lo = lds_read_tr16(sb + (cb0 + nb) * 32);
-            const uint2 hi = lds_read_tr16(sb + 4 * EP + (cb0 + nb) * 32);
+          if (cblk(nb) < NB) {  // uniform
+            const uint2 lo = lds_read_tr16(sb + cblk(nb) * 32);
+            const uint2 hi = lds_read_tr16(sb + 4 * EP + cblk(nb) * 32);
             const typename Mma<DT>::Frag b{u32x4{lo.x, lo.y, hi.x, hi.y}};
             Mma<DT>::run(acc[nb], typename Mma<DT>::Frag{xr[ks]}, b);
           }
         }
       }
     }
+  };
+  using IC0 = std::integral_constant<int, 0>;
+  if constexpr (W == 16) {
+    gemm_steps(s_stage, IC0{}, std::integral_constant<int, RT_MAX_STEPS>{});
+  } else {
+    static_assert(RT_MAX_STEPS == 3 * RT_PART_STEPS, "three parts");
+    using ICP = std::integral_constant<int, RT_PART_STEPS>;
+    // Part 0 sits in the stage; the token rows' area is free once every GEMM wave holds
+    // its rows, so part 1 goes there under part 0's MFMAs, and part 2 into the stage under
+    // part 1's.  Each wait + barrier: the next part has landed (every wave's copies) and
+    // no wave still reads the region the part after it overwrites.
+    __syncthreads();
+    if (nparts > 1) copy_w(part16, min(2 * part16, nw16), s_x);
+    gemm_steps(s_stage, IC0{}, ICP{});
+    if (nparts > 1) {  // uniform
+      wait_vmcnt<0>();
+      __syncthreads();
+      if (nparts > 2) copy_w(2 * part16, nw16, s_stage);
+      gemm_steps(s_x, ICP{}, ICP{});
+      if (nparts > 2) {
+        wait_vmcnt<0>();
+        __syncthreads();
+        gemm_steps(s_stage, std::integral_constant<int, 2 * RT_PART_STEPS>{}, ICP{});
+      }
+    }
   }
 
   // ---- logits: rounded to the dtype, stored, and kept in LDS as fp32 -----------------
-  // acc[nb][i] holds the logit of token 16 tile + 4 g + i, expert 16 (cb0 + nb) + j.
+  // acc[nb][i] holds the logit of token 16 tile + 4 g + i, expert 16 cblk(nb) + j.
   if (mma_wave) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -249,8 +307,8 @@ __global__ void __launch_bounds__(RT_THREADS) router_fwd_kernel(RouterArgs a) {
       const int64_t t = tok0 + tl;
 #pragma unroll
       for (int nb = 0; nb < NBH; ++nb) {
-        if (cb0 + nb >= NB) continue;  // uniform
-        const int e = 16 * (cb0 + nb) + j;
+        if (cblk(nb) >= NB) continue;  // uniform
+        const int e = 16 * cblk(nb) + j;
         float l = acc[nb][i];
         if (e < E) l += s_bias[e];
         const ET lv = Elem<DT>::from_f(l);
@@ -414,19 +472,35 @@ RouterArgs router_fused_args(void* ws, int64_t T, int E) {
 }
 
 template <int DT, int NB>
-static void launch_nb(const RouterArgs& a, unsigned grid, hipStream_t s) {
-  router_fwd_kernel<DT, NB><<<grid, RT_THREADS, 0, s>>>(a);
+static void launch_nb(const RouterArgs& a, unsigned grid, int waves, hipStream_t s) {
+  if (waves == 8) router_fwd_kernel<DT, NB, 8><<<grid, 8 * 64, 0, s>>>(a);
+  else router_fwd_kernel<DT, NB, 16><<<grid, 16 * 64, 0, s>>>(a);
 }
 
 template <int DT>
-static void launch_fwd(const RouterArgs& a, unsigned grid, hipStream_t s) {
+static void launch_fwd(const RouterArgs& a, unsigned grid, int waves, hipStream_t s) {
   switch ((a.E + 15) / 16) {
-    case 1: launch_nb<DT, 1>(a, grid, s); break;
-    case 2: launch_nb<DT, 2>(a, grid, s); break;
-    case 3: launch_nb<DT, 3>(a, grid, s); break;
-    case 4: launch_nb<DT, 4>(a, grid, s); break;
-    default: launch_nb<DT, 5>(a, grid, s); break;
+    case 1: launch_nb<DT, 1>(a, grid, waves, s); break;
+    case 2: launch_nb<DT, 2>(a, grid, waves, s); break;
+    case 3: launch_nb<DT, 3>(a, grid, waves, s); break;
+    case 4: launch_nb<DT, 4>(a, grid, waves, s); break;
+    default: launch_nb<DT, 5>(a, grid, waves, s); break;
   }
+}
+
+// Compute units of the current device (cached per device).
+static int router_device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
 }
 
 int router_fused_launch(const RouterArgs& a, int dtype, hipStream_t s) {
@@ -441,9 +515,13 @@ int router_fused_launch(const RouterArgs& a, int dtype, hipStream_t s) {
                 "router: NULL pointer");
   if (a.T == 0) return NSMOE_OK;
   const unsigned grid = (unsigned)router_fused_chunks(a.T);
+  // 8-wave workgroups (two per CU) once the grid has more workgroups than CUs, else 16
+  // (one per CU, W_r copied whole); the "router_waves" option forces either.
+  int waves = (int64_t)grid > router_device_cus() ? 8 : 16;
+  if (const int64_t v = option(OPT_ROUTER_WAVES)) waves = (int)v;
   KernelTimer timer("route_fwd", s);
-  if (dtype == DT_BF16) launch_fwd<DT_BF16>(a, grid, s);
-  else launch_fwd<DT_F16>(a, grid, s);
+  if (dtype == DT_BF16) launch_fwd<DT_BF16>(a, grid, waves, s);
+  else launch_fwd<DT_F16>(a, grid, waves, s);
   timer.stop();
   return check_launch("router_fwd_kernel");
 }

@@ -233,6 +233,20 @@ def test_prefill_layer_T32768_eval():
     assert int(ref.counts.sum()) == 32768 * 6
 
 
+@pytest.mark.parametrize("T", [300, 1024])
+def test_glu_backward_96_row_tiles_forced(T):
+    """The GLU backward's 96-row tiles (taken by default only once 64-row tiles overflow
+    three workgroups per CU, T = 8192 here) forced at small T: their epilogue stages the
+    tile in two passes of 48 rows, and the ragged last tiles of the groups leave the
+    second pass partly or wholly empty.  Checked against the oracle through dx and every
+    gradient, with the forward's saved pre-activations (the block's default)."""
+    from tests.helpers import lib_options
+
+    assert mk.SAVE_ACT
+    with lib_options(bwd_rows=96):
+        run_case(T, train=True, backward=True)
+
+
 def test_zero_router_sends_every_token_to_the_same_experts():
     ref = run_case(2048, train=True, backward=True, zero_router=True)
     assert int((ref.counts > 0).sum()) == 6 and int(ref.counts.max()) == 2048

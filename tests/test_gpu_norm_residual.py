@@ -138,6 +138,18 @@ def test_other_shapes(cfg):
     run(300, True, True, **cfg)
 
 
+@pytest.mark.parametrize("waves", [8, 16])
+def test_router_workgroup_shapes_with_the_norm(waves):
+    """The norm inside the router kernel under both of its workgroup shapes (forced): 8
+    waves, the default once the grid has more workgroups than CUs (the prefill's
+    T = 32768 above), and 16."""
+    from tests.helpers import lib_options
+
+    with lib_options(router_waves=waves):
+        run(300, True, True)
+        run(1000, False, False)
+
+
 def test_ragged_and_single_token():
     run(1, True, True)
     run(33, True, True)

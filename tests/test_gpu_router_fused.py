@@ -23,7 +23,8 @@ mk = pytest.importorskip("nanospeaker_amd.moe_kernel")
 DEV = "cuda"
 
 
-def run(T, E, k, train, normalize, dtype=torch.bfloat16, d=64, mode="rand", bias=None, seed=0):
+def run(T, E, k, train, normalize, dtype=torch.bfloat16, d=64, mode="rand", bias=None, seed=0,
+        with_logits=False):
     g = torch.Generator().manual_seed(seed)
     W = (torch.randn(d, E, generator=g) * 0.3).to(dtype)
     if mode == "pairs":
@@ -60,7 +61,7 @@ def run(T, E, k, train, normalize, dtype=torch.bfloat16, d=64, mode="rand", bias
     if train and not torch.isnan(ref_probs).any():
         ref_aux = R.balance_loss(ref_probs, rc, 1e-2, E)
         torch.testing.assert_close(aux.float().cpu(), ref_aux.float(), rtol=1e-5, atol=1e-7)
-    return ref_idx
+    return (ref_idx, logits.cpu()) if with_logits else ref_idx
 
 
 def _gates(x, W, w_in, w_out, k, train, normalize, bias):
@@ -100,3 +101,27 @@ def test_fused_router_offsets_including_minus_inf():
     bias[3] = 2.0
     idx = run(500, 76, 6, True, True, bias=bias, seed=5)
     assert not torch.isin(idx, torch.arange(0, 76, 7)).any()
+
+
+@pytest.mark.parametrize("T,E,k,d,mode", [(300, 76, 6, 576, "pairs"), (1000, 76, 6, 224, "rand"),
+                                          (65, 80, 16, 576, "zeros"), (777, 12, 12, 160, "nan"),
+                                          (40, 76, 6, 64, "pairs")])
+def test_fused_router_both_workgroup_shapes(T, E, k, d, mode):
+    """Both workgroup shapes of the router kernel, forced: 16 waves with W_r whole in LDS,
+    and 8 waves (two workgroups per CU, the default past one workgroup per CU) with W_r
+    in parts of 6 k-steps double-buffered through LDS -- d = 576 takes three parts, 224
+    two (the second partial), 160 and 64 one.  Each shape's routing is bit-exact against
+    the oracle on its own logits, and the two shapes' logits are bit-identical (every
+    logit is the same MFMA chain over the same k-steps in the same order)."""
+    from tests.helpers import lib_options
+
+    got = {}
+    for waves in (16, 8):
+        with lib_options(router_waves=waves):
+            for train in (True, False):
+                got[waves, train] = run(T, E, k, train, True, d=d, mode=mode, seed=T + d,
+                                        with_logits=True)
+    for train in (True, False):
+        (i16, l16), (i8, l8) = got[16, train], got[8, train]
+        assert torch.equal(l8.view(torch.int16), l16.view(torch.int16)), "logits differ"
+        assert torch.equal(i8, i16)
