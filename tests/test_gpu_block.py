@@ -288,6 +288,8 @@ def test_block_dtype_bias_shared_matrix(dtype, bias, S):
     dict(d=64, E=16, d_ff=96, k=10, S=2),   # k > 8: the general dx combine
     dict(d=64, E=8, d_ff=96, k=2, S=3),     # more than two shared experts
     dict(d=128, E=12, d_ff=192, k=4, S=0, bias=True),
+    dict(d=96, E=12, d_ff=96, k=3, S=1),    # d % 64 != 0: combine_dx's last column tile
+    dict(d=80, E=8, d_ff=96, k=2, S=1),     # ragged in halves; d % 32 != 0: router fwd in torch
 ])
 @pytest.mark.parametrize("train", [True, False])
 def test_block_other_shapes(cfg, train):
