@@ -103,10 +103,11 @@ def test_fused_router_offsets_including_minus_inf():
     assert not torch.isin(idx, torch.arange(0, 76, 7)).any()
 
 
-@pytest.mark.parametrize("T,E,k,d,mode", [(300, 76, 6, 576, "pairs"), (1000, 76, 6, 224, "rand"),
-                                          (65, 80, 16, 576, "zeros"), (777, 12, 12, 160, "nan"),
-                                          (40, 76, 6, 64, "pairs")])
-def test_fused_router_both_workgroup_shapes(T, E, k, d, mode):
+@pytest.mark.parametrize("T,E,k,d,mode,dtype", [
+    (300, 76, 6, 576, "pairs", torch.bfloat16), (1000, 76, 6, 224, "rand", torch.bfloat16),
+    (65, 80, 16, 576, "zeros", torch.bfloat16), (777, 12, 12, 160, "nan", torch.bfloat16),
+    (40, 76, 6, 64, "pairs", torch.bfloat16), (513, 76, 6, 576, "rand", torch.float16)])
+def test_fused_router_both_workgroup_shapes(T, E, k, d, mode, dtype):
     """Both workgroup shapes of the router kernel, forced: 16 waves with W_r whole in LDS,
     and 8 waves (two workgroups per CU, the default past one workgroup per CU) with W_r
     in parts of 6 k-steps double-buffered through LDS -- d = 576 takes three parts, 224
@@ -119,8 +120,8 @@ def test_fused_router_both_workgroup_shapes(T, E, k, d, mode):
     for waves in (16, 8):
         with lib_options(router_waves=waves):
             for train in (True, False):
-                got[waves, train] = run(T, E, k, train, True, d=d, mode=mode, seed=T + d,
-                                        with_logits=True)
+                got[waves, train] = run(T, E, k, train, True, dtype=dtype, d=d, mode=mode,
+                                        seed=T + d, with_logits=True)
     for train in (True, False):
         (i16, l16), (i8, l8) = got[16, train], got[8, train]
         assert torch.equal(l8.view(torch.int16), l16.view(torch.int16)), "logits differ"
