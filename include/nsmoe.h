@@ -75,6 +75,9 @@ int nsmoe_timing_read(const char* kernel_name, double* total_ms, int64_t* launch
  *   "router_waves"   waves per workgroup of the fused router: 16 (one workgroup per CU,
  *                    the router weight copied whole) or 8 (two per CU, the weight in parts);
  *                    default 8 once the grid has more workgroups than the device has CUs
+ *   "pack_in_place"  1: a training block call packs the expert weights in the dispatch's
+ *                    place launch (default: in the router's launch where its 16-wave form
+ *                    runs with enough workgroups, else in the place launch)
  * A value that does not fit a shape falls back to the library's choice for that call.
  * nsmoe_set_option returns 1 for an unknown name or a value out of range (0 always
  * restores the default); nsmoe_get_option returns -1 for an unknown name. */

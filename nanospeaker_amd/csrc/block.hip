@@ -203,6 +203,14 @@ extern "C" int nsmoe_block_fwd(const nsmoe_experts_args* a, const nsmoe_block_no
     r.topk_w = (void*)b.topk_w;
     r.topk_idx = topk_idx;
     if (!probs) r.colsum = nullptr;
+    // The pack rides in the router's launch where that launch can take it, else in the
+    // place launch.
+    const bool pack_in_router =
+        pack_in_place && router_fused_can_pack(T, pk.items_in + pk.items_out);
+    if (pack_in_router) {
+      r.pack = pk;
+      r.pack_on = 1;
+    }
     if (norm) {
       r.norm_w = norm->weight;
       r.norm_eps = norm->eps;
@@ -215,7 +223,7 @@ extern "C" int nsmoe_block_fwd(const nsmoe_experts_args* a, const nsmoe_block_no
       rc = dispatch_place_launch(topk_idx, m, E, r.hist, router_fused_chunks(T), RT_TOK * k,
                                  (int32_t*)b.sorted_ids, eids, (int32_t*)b.pad_offsets, counts,
                                  npp, inv, probs ? &fold : nullptr, s,
-                                 pack_in_place ? &pk : nullptr, a->dtype,
+                                 pack_in_place && !pack_in_router ? &pk : nullptr, a->dtype,
                                  probs ? nullptr : aux);
   } else {
     // In training the route kernel also leaves the balance loss's per-workgroup column

@@ -52,6 +52,7 @@ static const OptionSpec kOptions[OPT_COUNT] = {
     {"bwd_dist", 2, 4, nullptr},      {"dx_rows", 0, 0, kDxRows},
     {"dx_dist", 2, 4, nullptr},       {"xcd_run", 1, 1024, nullptr},
     {"dw_stages", 2, 4, nullptr},     {"router_waves", 0, 0, kRouterWaves},
+    {"pack_in_place", 1, 1, nullptr},
 };
 static std::atomic<int64_t> g_options[OPT_COUNT];
 

@@ -59,6 +59,7 @@ enum OptionId : int {
   OPT_XCD_RUN,
   OPT_DW_STAGES,
   OPT_ROUTER_WAVES,
+  OPT_PACK_IN_PLACE,
   OPT_COUNT
 };
 int64_t option(OptionId id);

@@ -410,6 +410,34 @@ __global__ void __launch_bounds__(W * 64, RtShape<W>::PER_CU) router_fwd_kernel(
       if (live && exact && j == 0) s_tie[atomicAdd(&s_ntie, 1)] = tl;
     }
   }  // the selection waves
+  // The packing waves (the 16-wave form's last RT_PACK_WAVES, 12 .. 15, which the
+  // selection leaves idle and the exact pass needs only for its thirteenth tie row on)
+  // take the weight pack's wave items, grid-strided: one item now, two beside the exact
+  // pass (after any tie rows of their own), the rest after it.  Each has 8 KiB of LDS:
+  // half of them in the token rows' area (free since the GEMM waves hold their rows), half
+  // in the stage past the exact pass's swap slots (free since the GEMM read W_r).  Eight
+  // packing waves (8 .. 15, one item at each phase) measured slower: the router launch
+  // 31 -> 34.5 us against the 12.6 us the place launch saves.
+  constexpr int PW = RT_PACK_WAVES;
+  constexpr int POSR = (POS + 1023) / 1024 * 1024;
+  const bool packer = W == 16 && a.pack_on && wave >= RT_WAVES - PW;  // uniform
+  const int pw = wave - (RT_WAVES - PW);
+  int64_t pu = (int64_t)blockIdx.x * PW + pw;
+  const int64_t pstride = (int64_t)gridDim.x * PW;
+  bool pdone = !packer;
+  char* pwl = pw >= PW / 2 ? s_x + (pw - PW / 2) * PACK_WAVE_LDS
+                           : s_stage + POSR + pw * PACK_WAVE_LDS;
+  auto pack_some = [&](int n) {
+    for (int i = 0; i < n && !pdone; ++i, pu += pstride)  // uniform
+      pdone = !pack_pair_item<DT>(a.pack, pu, lane, pwl);
+  };
+  if constexpr (W == 16) {
+    static_assert(RT_SEL_WAVES <= RT_WAVES - PW, "packing waves select nothing");
+    static_assert(PW / 2 * PACK_WAVE_LDS <= (int)sizeof(s_x) &&
+                      POSR + PW / 2 * PACK_WAVE_LDS <= STAGE,
+                  "packing regions fit the rows' area and the stage");
+    pack_some(1);
+  }
   __syncthreads();
 
   // ---- the exact pass for the undecided tokens: one wave per token -------------------
@@ -435,6 +463,7 @@ __global__ void __launch_bounds__(W * 64, RtShape<W>::PER_CU) router_fwd_kernel(
     if (lane < k) atomicAdd(&s_hist[rr.i0], 1);
     if (lane + 64 < k) atomicAdd(&s_hist[rr.i1], 1);
   }
+  if constexpr (W == 16) pack_some(2);
   __syncthreads();
 
   // ---- this chunk's histogram and, in training, its column sums of probs -------------
@@ -448,6 +477,7 @@ __global__ void __launch_bounds__(W * 64, RtShape<W>::PER_CU) router_fwd_kernel(
       a.colsum[wg * E + e] = s;
     }
   }
+  if constexpr (W == 16) pack_some(1 << 30);
 }
 
 bool router_fused_supported(int dtype, int d, int E, int k) {
@@ -488,6 +518,23 @@ static void launch_fwd(const RouterArgs& a, unsigned grid, int waves, hipStream_
   }
 }
 
+static int router_device_cus();
+
+// 8-wave workgroups (two per CU) once the grid has more workgroups than CUs, else 16
+// (one per CU, W_r copied whole); the "router_waves" option forces either.
+static int router_waves_for(int64_t grid) {
+  if (const int64_t v = option(OPT_ROUTER_WAVES)) return (int)v;
+  return grid > router_device_cus() ? 8 : 16;
+}
+
+// At most 8 pack items per packing wave: about the length of the selection and the exact
+// pass (an item is one 8 KiB load, a transpose and 8 KiB of stores).
+bool router_fused_can_pack(int64_t T, int64_t items) {
+  const int64_t grid = router_fused_chunks(T);
+  return T > 0 && router_waves_for(grid) == 16 && items <= grid * RT_PACK_WAVES * 8 &&
+         !option(OPT_PACK_IN_PLACE);
+}
+
 // Compute units of the current device (cached per device).
 static int router_device_cus() {
   static int cached[64] = {0};
@@ -515,10 +562,9 @@ int router_fused_launch(const RouterArgs& a, int dtype, hipStream_t s) {
                 "router: NULL pointer");
   if (a.T == 0) return NSMOE_OK;
   const unsigned grid = (unsigned)router_fused_chunks(a.T);
-  // 8-wave workgroups (two per CU) once the grid has more workgroups than CUs, else 16
-  // (one per CU, W_r copied whole); the "router_waves" option forces either.
-  int waves = (int64_t)grid > router_device_cus() ? 8 : 16;
-  if (const int64_t v = option(OPT_ROUTER_WAVES)) waves = (int)v;
+  const int waves = router_waves_for(grid);
+  NSMOE_REQUIRE(!a.pack_on || router_fused_can_pack(a.T, a.pack.items_in + a.pack.items_out),
+                "router: the weight pack needs the 16-wave form and enough workgroups");
   KernelTimer timer("route_fwd", s);
   if (dtype == DT_BF16) launch_fwd<DT_BF16>(a, grid, waves, s);
   else launch_fwd<DT_F16>(a, grid, waves, s);

@@ -6,6 +6,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "pack_tile.h"
+
 namespace nsmoe {
 
 constexpr int RT_TOK = 32;              // tokens per router workgroup (= dispatch chunk / k)
@@ -34,7 +36,14 @@ struct RouterArgs {
   float norm_eps;
   void* xn;
   float* rstd;
+  // With pack_on, the 16-bit expert-weight pack (PackPairArgs' wave items) runs in the
+  // 16-wave form's last RT_PACK_WAVES waves of every workgroup (the ones the selection
+  // leaves idle), beside the selection and the exact pass, instead of in a launch of its
+  // own (router_fused_can_pack).
+  PackPairArgs pack;
+  int pack_on;
 };
+constexpr int RT_PACK_WAVES = 4;
 
 inline int64_t router_fused_chunks(int64_t T) { return (T + RT_TOK - 1) / RT_TOK; }
 
@@ -46,5 +55,8 @@ size_t router_fused_ws_bytes(int64_t T, int E);
 RouterArgs router_fused_args(void* ws, int64_t T, int E);
 // The router's launch (router_fwd_kernel) on stream s.
 int router_fused_launch(const RouterArgs& a, int dtype, hipStream_t s);
+// Whether the router launch for T tokens can take a weight pack of `items` wave items
+// (RouterArgs::pack_on): its 16-wave form, with few enough items per packing wave.
+bool router_fused_can_pack(int64_t T, int64_t items);
 
 }  // namespace nsmoe

@@ -313,3 +313,39 @@ def test_eval_loss_is_a_zero_the_library_writes(dtype):
             aux = m.aux_loss
             assert aux.dtype == dtype and aux.shape == ()
             assert float(aux) == 0.0 and not math.copysign(1.0, float(aux)) < 0
+
+
+def test_weight_pack_in_the_router_launch_matches_the_place_launch():
+    """In training at T = 8192 the expert-weight pack runs inside the router's launch (the
+    last 4 waves of each 16-wave workgroup, beside the selection and the exact pass); the
+    "pack_in_place" option moves it back into the dispatch's place launch.  Every output
+    and gradient agrees bit for bit, and the library's launch timers show where the pack
+    ran.  (test_forward_backward_T8192_train checks the default against the oracle.)"""
+    from nanospeaker_amd import _native as nat
+    from tests.helpers import lib_options
+
+    m, _, x, g = build(8192)
+    m = m.to(DEV).train()
+    xd, gd = x.to(DEV), g.to(DEV)
+    params = list(m.parameters())
+
+    def step(**opts):
+        with lib_options(**opts):
+            nat.timing_enable(256)
+            try:
+                mk.PACKS.clear()
+                xr = xd.detach().requires_grad_(True)
+                out = m(xr)
+                gs = torch.autograd.grad([out, m.aux_loss], [xr] + params,
+                                         [gd, torch.ones_like(m.aux_loss)])
+                torch.cuda.synchronize()
+                launches = (nat.timing_read("place_pack")[1], nat.timing_read("dispatch")[1])
+            finally:
+                nat.timing_enable(0)
+        return [out.detach().cpu()] + [t.cpu() for t in gs], launches
+
+    in_router, n_router = step()
+    in_place, n_place = step(pack_in_place=1)
+    assert n_router == (0, 1) and n_place == (1, 0), (n_router, n_place)
+    for i, (a, b) in enumerate(zip(in_router, in_place)):
+        assert torch.equal(a, b), i
