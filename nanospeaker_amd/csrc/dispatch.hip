@@ -24,6 +24,7 @@
 //   With the block's balance loss folded in, the place launch has one more workgroup: it
 //   forms the experts' totals the same way and reduces the router's column-sum partials
 //   to the loss (balance.h) while the others place their chunks.
+#include <atomic>
 #include <mutex>
 
 #include "balance.h"
@@ -397,18 +398,32 @@ int dispatch_place_launch(const int64_t* topk_idx, int64_t n_pairs, int32_t n_ex
     // leaving the L2s full of dirty lines that the end of the launch must write back
     // before the next kernel starts (measured: ~6 us more between the launches); two
     // items per wave interleave the second item's reads with the first one's writes.
+    // Both runtime queries are made once per device and dtype: the occupancy query costs
+    // tens of microseconds of host time, which an eager call would pay every step.
     const int64_t items = pack->items_in + pack->items_out;
-    int cus = 0, dev = 0, per_cu = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        cus <= 0)
-      cus = 256;
-    const void* kfn = pack_dtype == DT_BF16 ? (const void*)dispatch_place_pack_kernel<DT_BF16>
-                                            : (const void*)dispatch_place_pack_kernel<DT_F16>;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kfn, 1024, 0) != hipSuccess ||
-        per_cu <= 0)
-      per_cu = 1;
-    (void)hipGetLastError();
+    static std::atomic<int> s_cus[64], s_per_cu[64][2];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = -1;
+    const int di = pack_dtype == DT_BF16 ? 0 : 1;
+    int cus = dev >= 0 ? s_cus[dev].load(std::memory_order_relaxed) : 0;
+    int per_cu = dev >= 0 ? s_per_cu[dev][di].load(std::memory_order_relaxed) : 0;
+    if (cus <= 0 || per_cu <= 0) {
+      if (dev < 0 ||
+          hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+          cus <= 0)
+        cus = 256;
+      const void* kfn = pack_dtype == DT_BF16
+                            ? (const void*)dispatch_place_pack_kernel<DT_BF16>
+                            : (const void*)dispatch_place_pack_kernel<DT_F16>;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kfn, 1024, 0) != hipSuccess ||
+          per_cu <= 0)
+        per_cu = 1;
+      (void)hipGetLastError();
+      if (dev >= 0) {
+        s_cus[dev].store(cus, std::memory_order_relaxed);
+        s_per_cu[dev][di].store(per_cu, std::memory_order_relaxed);
+      }
+    }
     int64_t npack = (int64_t)per_cu * cus - np;
     if (npack < 8) npack = 8;
     if (npack > cdiv(items, 32)) npack = cdiv(items, 32);
