@@ -315,16 +315,18 @@ def test_eval_loss_is_a_zero_the_library_writes(dtype):
             assert float(aux) == 0.0 and not math.copysign(1.0, float(aux)) < 0
 
 
-def test_weight_pack_in_the_router_launch_matches_the_place_launch():
+@pytest.mark.parametrize("cfg", [dict(), dict(dtype=torch.float16), dict(S=0, bias=True)])
+def test_weight_pack_in_the_router_launch_matches_the_place_launch(cfg):
     """In training at T = 8192 the expert-weight pack runs inside the router's launch (the
     last 4 waves of each 16-wave workgroup, beside the selection and the exact pass); the
     "pack_in_place" option moves it back into the dispatch's place launch.  Every output
-    and gradient agrees bit for bit, and the library's launch timers show where the pack
-    ran.  (test_forward_backward_T8192_train checks the default against the oracle.)"""
+    and gradient agrees bit for bit (bf16, fp16, and without shared experts), and the
+    library's launch timers show where the pack ran.  (test_forward_backward_T8192_train
+    checks the default against the oracle.)"""
     from nanospeaker_amd import _native as nat
     from tests.helpers import lib_options
 
-    m, _, x, g = build(8192)
+    m, _, x, g = build(8192, **cfg)
     m = m.to(DEV).train()
     xd, gd = x.to(DEV), g.to(DEV)
     params = list(m.parameters())
