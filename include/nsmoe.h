@@ -277,9 +277,9 @@ int nsmoe_experts_bwd(const nsmoe_experts_args* args, const int32_t* inv,
  * w_in_packed by the backward); its routing pointers (topk_w, sorted_ids, pad_offsets,
  * counts) and l_cap are ignored -- the calls place them in `saved`.  With
  * NSMOE_BLOCK_PACK in route_flags the forward first packs the weights into
- * w_in_packed / w_out_packed itself (with the router weight passed, inside the router's
- * or the place launch; else, or with the "side_stream" option, on a second stream beside
- * the routing kernels);
+ * w_in_packed / w_out_packed itself (with the router weight passed and the "side_stream"
+ * option off, inside the router's or the place launch; otherwise in a launch of its own,
+ * on a second stream beside the routing kernels when that option is set);
  * without it they must hold the current weights already, so a caller that keeps the
  * packs while the weights do not change skips that pass.
  *
