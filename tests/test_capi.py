@@ -262,7 +262,7 @@ def test_tuning_options_round_trip_and_reject_bad_values():
     for name, good, bad in (("side_stream", 1, 2), ("fwd_rows", 32, 80), ("bwd_rows", 96, 32),
                             ("dx_rows", 64, 48), ("fwd_dist", 6, 7), ("bwd_dist", 4, 5),
                             ("dx_dist", 4, 1), ("xcd_run", 8, 2048), ("dw_stages", 3, 5),
-                            ("router_waves", 8, 4)):
+                            ("router_waves", 8, 4), ("pack_in_place", 1, 2)):
         assert nat.get_option(name) == 0
         nat.set_option(name, good)
         assert nat.get_option(name) == good
