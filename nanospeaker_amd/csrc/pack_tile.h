@@ -33,19 +33,30 @@ __host__ __device__ inline int64_t pack_items(int groups, int n_kb, int n_nb) {
 
 // Items run tiles fastest, so consecutive waves read the same rows' neighbouring 128-byte
 // segments, then k-block pairs, then groups.
-template <int DT, int MODE>
-__device__ __forceinline__ void pack_wave_item(const typename Elem<DT>::T* __restrict__ routed,
-                                               const typename Elem<DT>::T* __restrict__ shared,
-                                               int E, int d, int H, int HP, int n_kb, int n_nb,
-                                               char* __restrict__ out, int fast, int64_t item,
-                                               int lane, char* __restrict__ wl) {
-  using G = Geo<DT>;
-  using T = typename G::T;
-  static_assert(G::ES == 2 && G::VE == 8 && G::KC == 32 && G::PKB == 1024, "16-bit types");
+struct PackItem {
+  int g, kp, nt;
+};
+__device__ __forceinline__ PackItem pack_item_of(int64_t item, int n_kb, int n_nb) {
   const int nts = n_nb / 4, kps = (n_kb + 1) / 2;
   const int per_g = nts * kps;
   const int g = (int)(item / per_g), r0 = (int)(item - (int64_t)g * per_g);
-  const int kp = r0 / nts, nt = r0 - kp * nts;
+  const int kp = r0 / nts;
+  return PackItem{g, kp, r0 - kp * nts};
+}
+
+// The item's loads: lane l's 8 x 8 block, row r in v[r] (zeros out of range).  A caller
+// may issue them early and finish the item later (pack_wave_store).
+template <int DT, int MODE>
+__device__ __forceinline__ void pack_wave_load(const typename Elem<DT>::T* __restrict__ routed,
+                                               const typename Elem<DT>::T* __restrict__ shared,
+                                               int E, int d, int H, int HP, int n_kb, int n_nb,
+                                               int fast, int64_t item, int lane,
+                                               u32x4 (&v)[8]) {
+  using G = Geo<DT>;
+  using T = typename G::T;
+  static_assert(G::ES == 2 && G::VE == 8 && G::KC == 32 && G::PKB == 1024, "16-bit types");
+  const PackItem it = pack_item_of(item, n_kb, n_nb);
+  const int g = it.g, kp = it.kp, nt = it.nt;
   const int K = MODE == 0 ? d : H;
   const int ld = MODE == 0 ? 2 * H : d;
   const int64_t gstride = MODE == 0 ? (int64_t)d * 2 * H : (int64_t)H * d;
@@ -67,7 +78,6 @@ __device__ __forceinline__ void pack_wave_item(const typename Elem<DT>::T* __res
   const int half = lane >> 5, kbl = (lane >> 3) & 3, nbl = lane & 7;
   const int kb = 2 * kp + half;
   const int col = n0 + nbl * G::VE;
-  u32x4 v[G::VE];
 #pragma unroll
   for (int r = 0; r < G::VE; ++r) {
     v[r] = u32x4{0u, 0u, 0u, 0u};
@@ -83,6 +93,17 @@ __device__ __forceinline__ void pack_wave_item(const typename Elem<DT>::T* __res
       __builtin_memcpy(&v[r], tmp, 16);
     }
   }
+}
+
+// The item's transpose and stores from its loaded blocks (pack_wave_load).
+template <int DT>
+__device__ __forceinline__ void pack_wave_store(int n_kb, int n_nb, char* __restrict__ out,
+                                                int64_t item, int lane, const u32x4 (&v)[8],
+                                                char* __restrict__ wl) {
+  using G = Geo<DT>;
+  const PackItem it = pack_item_of(item, n_kb, n_nb);
+  const int g = it.g, kp = it.kp, nt = it.nt;
+  const int half = lane >> 5, kbl = (lane >> 3) & 3, nbl = lane & 7;
   const int share0 = 64 * (4 * half + (nbl >> 1)) + 16 * kbl + 8 * (nbl & 1);
   constexpr uint32_t kLow = 0x05040100u, kHigh = 0x07060302u;  // low / high halves
 #pragma unroll
@@ -110,6 +131,17 @@ __device__ __forceinline__ void pack_wave_item(const typename Elem<DT>::T* __res
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+template <int DT, int MODE>
+__device__ __forceinline__ void pack_wave_item(const typename Elem<DT>::T* __restrict__ routed,
+                                               const typename Elem<DT>::T* __restrict__ shared,
+                                               int E, int d, int H, int HP, int n_kb, int n_nb,
+                                               char* __restrict__ out, int fast, int64_t item,
+                                               int lane, char* __restrict__ wl) {
+  u32x4 v[8];
+  pack_wave_load<DT, MODE>(routed, shared, E, d, H, HP, n_kb, n_nb, fast, item, lane, v);
+  pack_wave_store<DT>(n_kb, n_nb, out, item, lane, v, wl);
+}
+
 // Both packs' operands and geometry (pack_pair_kernel, and the place launch's pack waves).
 struct PackPairArgs {
   const void *w_in, *w_sh_in, *w_out, *w_sh_out;
@@ -134,6 +166,30 @@ __device__ __forceinline__ bool pack_pair_item(const PackPairArgs& a, int64_t u,
   pack_wave_item<DT, 1>((const T*)a.w_out, (const T*)a.w_sh_out, a.E, a.d, a.H, a.HP,
                         a.out_kb, a.out_nb, a.p_out, a.fast, u, lane, wl);
   return true;
+}
+
+// Wave item u of the pair in two halves: its loads (false past the last item, nothing
+// loaded), then, later, its transpose and stores from those registers.
+template <int DT>
+__device__ __forceinline__ bool pack_pair_load(const PackPairArgs& a, int64_t u, int lane,
+                                               u32x4 (&v)[8]) {
+  using T = typename Elem<DT>::T;
+  if (u < a.items_in) {
+    pack_wave_load<DT, 0>((const T*)a.w_in, (const T*)a.w_sh_in, a.E, a.d, a.H, a.HP, a.in_kb,
+                          a.in_nb, a.fast, u, lane, v);
+    return true;
+  }
+  u -= a.items_in;
+  if (u >= a.items_out) return false;
+  pack_wave_load<DT, 1>((const T*)a.w_out, (const T*)a.w_sh_out, a.E, a.d, a.H, a.HP,
+                        a.out_kb, a.out_nb, a.fast, u, lane, v);
+  return true;
+}
+template <int DT>
+__device__ __forceinline__ void pack_pair_store(const PackPairArgs& a, int64_t u, int lane,
+                                                const u32x4 (&v)[8], char* __restrict__ wl) {
+  if (u < a.items_in) pack_wave_store<DT>(a.in_kb, a.in_nb, a.p_in, u, lane, v, wl);
+  else pack_wave_store<DT>(a.out_kb, a.out_nb, a.p_out, u - a.items_in, lane, v, wl);
 }
 
 // The arguments of the 16-bit pack pair for these weights (pack_pair_kernel's geometry);

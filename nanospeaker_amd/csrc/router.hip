@@ -200,6 +200,36 @@ __global__ void __launch_bounds__(W * 64, RtShape<W>::PER_CU) router_fwd_kernel(
   for (int e = tid; e < E; e += RT_THREADS) s_bias[e] = a.bias ? a.bias[e] : 0.0f;
   wait_vmcnt<0>();  // this wave's copies have landed
   __syncthreads();  // every wave's copies and the LDS fills are visible
+  // The packing waves (the 16-wave form's last RT_PACK_WAVES, 12 .. 15, which the GEMM and
+  // the selection leave idle and the exact pass needs only for its thirteenth tie row on)
+  // take the weight pack's wave items, grid-strided: the first item's loads now, under the
+  // GEMM, its transpose and stores during the selection, two items beside the exact pass
+  // (after any tie rows of their own), the rest after it.  Each has 8 KiB of LDS:
+  // half of them in the token rows' area (free since the GEMM waves hold their rows), half
+  // in the stage past the exact pass's swap slots (free since the GEMM read W_r).  Eight
+  // packing waves (8 .. 15, one item at each phase) measured slower: the router launch
+  // 31 -> 34.5 us against the 12.6 us the place launch saves.
+  constexpr int PW = RT_PACK_WAVES;
+  constexpr int POSR = (POS + 1023) / 1024 * 1024;
+  const bool packer = W == 16 && a.pack_on && wave >= RT_WAVES - PW;  // uniform
+  const int pw = wave - (RT_WAVES - PW);
+  int64_t pu = (int64_t)blockIdx.x * PW + pw;
+  const int64_t pstride = (int64_t)gridDim.x * PW;
+  bool pdone = !packer;
+  char* pwl = pw >= PW / 2 ? s_x + (pw - PW / 2) * PACK_WAVE_LDS
+                           : s_stage + POSR + pw * PACK_WAVE_LDS;
+  auto pack_some = [&](int n) {
+    for (int i = 0; i < n && !pdone; ++i, pu += pstride)  // uniform
+      pdone = !pack_pair_item<DT>(a.pack, pu, lane, pwl);
+  };
+  u32x4 pv[8];
+  bool pfirst = false;
+  if constexpr (W == 16) {
+    if (packer) {
+      pfirst = pack_pair_load<DT>(a.pack, pu, lane, pv);
+      pdone = !pfirst;
+    }
+  }
   if (mma_wave) {
     const int r = tile * 16 + j;
     const char* xl = s_x + r * cpr * 16;
@@ -410,33 +440,15 @@ __global__ void __launch_bounds__(W * 64, RtShape<W>::PER_CU) router_fwd_kernel(
       if (live && exact && j == 0) s_tie[atomicAdd(&s_ntie, 1)] = tl;
     }
   }  // the selection waves
-  // The packing waves (the 16-wave form's last RT_PACK_WAVES, 12 .. 15, which the
-  // selection leaves idle and the exact pass needs only for its thirteenth tie row on)
-  // take the weight pack's wave items, grid-strided: one item now, two beside the exact
-  // pass (after any tie rows of their own), the rest after it.  Each has 8 KiB of LDS:
-  // half of them in the token rows' area (free since the GEMM waves hold their rows), half
-  // in the stage past the exact pass's swap slots (free since the GEMM read W_r).  Eight
-  // packing waves (8 .. 15, one item at each phase) measured slower: the router launch
-  // 31 -> 34.5 us against the 12.6 us the place launch saves.
-  constexpr int PW = RT_PACK_WAVES;
-  constexpr int POSR = (POS + 1023) / 1024 * 1024;
-  const bool packer = W == 16 && a.pack_on && wave >= RT_WAVES - PW;  // uniform
-  const int pw = wave - (RT_WAVES - PW);
-  int64_t pu = (int64_t)blockIdx.x * PW + pw;
-  const int64_t pstride = (int64_t)gridDim.x * PW;
-  bool pdone = !packer;
-  char* pwl = pw >= PW / 2 ? s_x + (pw - PW / 2) * PACK_WAVE_LDS
-                           : s_stage + POSR + pw * PACK_WAVE_LDS;
-  auto pack_some = [&](int n) {
-    for (int i = 0; i < n && !pdone; ++i, pu += pstride)  // uniform
-      pdone = !pack_pair_item<DT>(a.pack, pu, lane, pwl);
-  };
   if constexpr (W == 16) {
     static_assert(RT_SEL_WAVES <= RT_WAVES - PW, "packing waves select nothing");
     static_assert(PW / 2 * PACK_WAVE_LDS <= (int)sizeof(s_x) &&
                       POSR + PW / 2 * PACK_WAVE_LDS <= STAGE,
                   "packing regions fit the rows' area and the stage");
-    pack_some(1);
+    if (pfirst) {  // the item loaded under the GEMM
+      pack_pair_store<DT>(a.pack, pu, lane, pv, pwl);
+      pu += pstride;
+    }
   }
   __syncthreads();
 
