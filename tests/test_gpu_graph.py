@@ -125,11 +125,13 @@ def test_side_stream_matches_single_stream():
             assert torch.equal(a, b), f"step {r}: tensor {i}"
 
 
-def test_replay_repacks_weights_updated_in_place():
+@pytest.mark.parametrize("T", [1024, 8192])
+def test_replay_repacks_weights_updated_in_place(T):
     """The pack cache is bypassed while a graph is captured, so the captured forward packs
     the weights on every replay: an in-place update between replays (an optimizer step
-    outside the graph) is seen by the next replay."""
-    m, x, _ = _block(1024, seed=3)
+    outside the graph) is seen by the next replay -- with the pack in the place launch
+    (T = 1024) and in the router's launch (T = 8192)."""
+    m, x, _ = _block(T, seed=3)
     with torch.no_grad():
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
